@@ -1,0 +1,163 @@
+/*
+ * ultima_hsamp -- C ABI of the MI355X (gfx950) token sampler.
+ *
+ * This is the boundary a foreign caller binds (ctypes, cgo, JNI, N-API). It
+ * replaces the reference's C++ entry points, which have no C ABI of their own:
+ *   - ultima::sampler::sample(std::span<float>, const SamplerParams&, SamplerContext&)
+ *       /root/reference/include/ultima/sampler/sampler.hpp:83-85,
+ *       /root/reference/src/sampler/sampler.cpp:230-277
+ *     -> ultima_hsamp_run() for [B, V] batches resident in device memory, and
+ *        ultima_hsamp_sample_host() for one row in host memory (B = 1).
+ *   - ultima::sampler::argmax(std::span<const float>)
+ *       sampler.hpp:88, sampler.cpp:220-228
+ *     -> ultima_hsamp_sample_host() with temperature <= 0 and identity knobs.
+ *   - SamplerParams and SamplerParams::identity()
+ *       sampler.hpp:16-52, sampler.cpp:192-205
+ *     -> ultima_hsamp_params, ultima_hsamp_params_default(), ultima_hsamp_params_identity().
+ *
+ * Semantics per row are the reference's transform ladder, in its order:
+ * allowed-token mask (extension) -> logit bias -> repetition penalty -> DRY ->
+ * frequency/presence -> (temperature <= 0: argmax, no uniform used) ->
+ * temperature -> top-k -> top-p -> min-p -> softmax -> categorical draw.
+ * Ties in top-k go to the lower index; ties in top-p go to the lower index.
+ * The draw takes a caller-supplied uniform u in [0, 1): the token is the first
+ * index whose double-precision running sum of normalised probabilities
+ * (index order) is >= u, which is what std::discrete_distribution does with
+ * the u it draws from SamplerContext::rng().
+ *
+ * Errors are returned as negative status codes; nothing throws, nothing aborts.
+ * All entry points are thread-safe across handles; one handle must not be used
+ * by two threads at once.
+ */
+#ifndef ULTIMA_HSAMP_H
+#define ULTIMA_HSAMP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ULTIMA_HSAMP_VERSION 1
+
+/* Status codes. */
+#define ULTIMA_HSAMP_OK 0
+#define ULTIMA_HSAMP_ERR_INVALID (-1)     /* bad argument (NULL, size, alignment, NaN knob) */
+#define ULTIMA_HSAMP_ERR_HIP (-2)         /* a HIP runtime call failed */
+#define ULTIMA_HSAMP_ERR_UNSUPPORTED (-3) /* valid request this build does not implement */
+#define ULTIMA_HSAMP_ERR_NOMEM (-4)       /* device or pinned allocation failed */
+#define ULTIMA_HSAMP_ERR_CAPACITY (-5)    /* exceeds the limits the handle was created with */
+#define ULTIMA_HSAMP_ERR_NO_DEVICE (-6)   /* no usable gfx950 device */
+
+/* Logit element types. */
+#define ULTIMA_HSAMP_F32 0
+#define ULTIMA_HSAMP_BF16 1
+
+/* ultima_hsamp_batch.flags */
+#define ULTIMA_HSAMP_WRITEBACK 1u /* leave logits in the state sample() leaves them (F32 only) */
+
+/* Per-row outcome bits written to row_flags (when given). */
+#define ULTIMA_HSAMP_ROW_GREEDY 1u        /* temperature <= 0: argmax, u unused */
+#define ULTIMA_HSAMP_ROW_U_USED 2u        /* the draw read u (T > 0 and V >= 2) */
+#define ULTIMA_HSAMP_ROW_CDF_NEAR 4u      /* |cp - u| <= 1e-6 at the chosen boundary */
+#define ULTIMA_HSAMP_ROW_NAN 8u           /* a NaN logit was seen (outside the contract) */
+#define ULTIMA_HSAMP_ROW_UNIFORM 16u      /* nothing finite was left: uniform draw over V */
+#define ULTIMA_HSAMP_ROW_TOPP_NEAR 32u    /* top-p cumulative within 1e-6 of top_p at the cutoff */
+
+/* Hard limits of this build. */
+#define ULTIMA_HSAMP_MAX_VOCAB (1 << 24)      /* token ids and V below 2^24 */
+#define ULTIMA_HSAMP_MAX_WINDOW 32767         /* effective penalty window per row */
+#define ULTIMA_HSAMP_MAX_BIAS 4096            /* logit-bias entries per row */
+
+/* One row's knobs: ultima::sampler::SamplerParams (sampler.hpp:16-52) with the
+ * logit_bias map given as a slice of the batch's bias arrays and the
+ * context's history length given explicitly. size_t knobs are uint64_t. */
+typedef struct ultima_hsamp_params {
+    float rep_penalty;          /* sampler.hpp:22 */
+    float dry_multiplier;       /* sampler.hpp:26 */
+    float dry_base;             /* sampler.hpp:27 */
+    float frequency_penalty;    /* sampler.hpp:32 */
+    float presence_penalty;     /* sampler.hpp:33 */
+    float temperature;          /* sampler.hpp:36 */
+    float top_p;                /* sampler.hpp:42 */
+    float min_p;                /* sampler.hpp:45 */
+    uint64_t repeat_last_n;     /* sampler.hpp:23 */
+    uint64_t dry_allowed_len;   /* sampler.hpp:28 */
+    uint64_t dry_last_n;        /* sampler.hpp:29 */
+    uint64_t top_k;             /* sampler.hpp:39 */
+    int64_t hist_len;           /* ids in this row's history (SamplerContext::recent()) */
+    int64_t bias_offset;        /* first entry of this row in bias_ids/bias_vals */
+    int64_t bias_count;         /* entries (unique ids) for this row; 0 = no bias */
+} ultima_hsamp_params;
+
+/* One batch. Device pointers are caller-owned device memory on the handle's
+ * device; host pointers are read during ultima_hsamp_run() only. */
+typedef struct ultima_hsamp_batch {
+    int32_t rows;               /* B >= 1 */
+    int32_t vocab;              /* V >= 1 */
+    int32_t dtype;              /* ULTIMA_HSAMP_F32 or ULTIMA_HSAMP_BF16 */
+    uint32_t flags;             /* ULTIMA_HSAMP_WRITEBACK */
+    void* logits;               /* device [rows, logits_stride] elements of dtype */
+    int64_t logits_stride;      /* elements between rows, >= vocab */
+    const int32_t* hist;        /* device [rows, hist_stride] ids, oldest first; NULL if unused */
+    int64_t hist_stride;        /* >= max hist_len */
+    const uint32_t* mask;       /* device [rows, mask_stride] words or NULL: bit t of word t>>5 */
+    int64_t mask_stride;        /* >= ceil(vocab / 32) */
+    const double* u;            /* device [rows] uniforms in [0, 1) */
+    const ultima_hsamp_params* params; /* HOST [rows] */
+    const int32_t* bias_ids;    /* HOST, indexed by params[r].bias_offset; NULL if no bias */
+    const float* bias_vals;     /* HOST, same indexing */
+    int32_t* token;             /* device [rows] out: sampled id */
+    uint32_t* row_flags;        /* device [rows] out or NULL: ULTIMA_HSAMP_ROW_* bits */
+    int32_t* topk_idx;          /* device [rows, set_cap] out or NULL: finite top-k members, index order */
+    int32_t* topk_count;        /* device [rows] out or NULL (-1 when top-k is off) */
+    int32_t* kept_idx;          /* device [rows, set_cap] out or NULL: ids left before the draw */
+    float* kept_prob;           /* device [rows, set_cap] out or NULL: their final probabilities */
+    int32_t* kept_count;        /* device [rows] out or NULL */
+    int32_t set_cap;            /* capacity of the set outputs per row */
+} ultima_hsamp_batch;
+
+typedef struct ultima_hsamp ultima_hsamp;
+
+/* Create a handle on `device` able to run batches of up to max_rows rows of
+ * up to max_vocab logits. Allocates the device workspace and pinned staging. */
+int ultima_hsamp_create(int device, int32_t max_rows, int32_t max_vocab, ultima_hsamp** out);
+
+/* Release a handle (waits for its outstanding work). NULL is a no-op. */
+int ultima_hsamp_destroy(ultima_hsamp* h);
+
+/* Sample every row of `batch`, asynchronously on `hip_stream` (a hipStream_t,
+ * NULL = the null stream). Inputs must stay valid and unchanged until the work
+ * completes; outputs are valid once it has. */
+int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* batch, void* hip_stream);
+
+/* One row in HOST memory, synchronously -- sample() of sampler.cpp:230-277 with
+ * an explicit uniform. logits (V floats) are staged to the device; with
+ * writeback != 0 they are copied back in the state sample() leaves them in.
+ * hist: hist_len ids; bias_ids/bias_vals: params->bias_count entries from
+ * params->bias_offset (may be NULL when bias_count == 0). */
+int ultima_hsamp_sample_host(ultima_hsamp* h, float* logits, int32_t vocab,
+                             const ultima_hsamp_params* params, const int32_t* hist,
+                             const int32_t* bias_ids, const float* bias_vals, double u,
+                             int writeback, int32_t* token_out);
+
+/* SamplerParams{} defaults (sampler.hpp:16-52) and SamplerParams::identity()
+ * (sampler.cpp:192-205); history and bias fields are zeroed. */
+void ultima_hsamp_params_default(ultima_hsamp_params* p);
+void ultima_hsamp_params_identity(ultima_hsamp_params* p);
+
+/* The uniform std::discrete_distribution derives from one mt19937_64 output x:
+ * generate_canonical<double, 53> = double(x) / 2^64, clamped below 1. */
+double ultima_hsamp_uniform_from_u64(uint64_t x);
+
+/* Text for a status code. */
+const char* ultima_hsamp_status_str(int status);
+
+/* ULTIMA_HSAMP_VERSION of the loaded library. */
+int ultima_hsamp_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

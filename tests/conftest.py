@@ -1,0 +1,47 @@
+"""pytest setup: the `gpu` marker, import paths and shared fixtures.
+
+CPU tests (-m "not gpu") pin the oracle and check the library's host side;
+GPU tests (-m gpu) are the parity tests proper and call the HIP sampler
+through its C ABI.
+"""
+from __future__ import annotations
+
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+for p in (ROOT, ROOT / "oracle", ROOT / "tests"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) and the built HIP library")
+
+
+@pytest.fixture(scope="session")
+def orc():
+    import oracle
+    return oracle
+
+
+@pytest.fixture(scope="session")
+def pkg():
+    import __graft_entry__
+    return __graft_entry__.load_package()
+
+
+@pytest.fixture(scope="session")
+def wl(pkg):
+    return pkg.workloads
+
+
+@pytest.fixture(scope="session")
+def hs(pkg):
+    """The C ABI binding with a handle on cuda:0 (GPU tests only)."""
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need an MI355X: torch.cuda.is_available() is False")
+    return pkg.hsamp

@@ -90,13 +90,16 @@ void set_inplace_writeback(bool on) noexcept;
 // True when a gfx950 device and libultima_hsamp are usable.
 bool gpu_available() noexcept;
 
-// Device-resident batch: `rows` rows of `vocab` fp32 logits (row stride
-// `stride`) on the sampler's device, one SamplerParams and one history per row,
-// one uniform per row in u_dev (device). Token ids land in tokens_dev (device).
-// Asynchronous on `hip_stream`; returns 0 or a negative ultima_hsamp status.
+// Device-resident batch on the sampler's device: `rows` rows of `vocab` fp32
+// logits (row stride `stride` elements), one SamplerParams per row, row r's
+// history in hist_dev[r * hist_stride ..] (hist_len[r] ids, oldest first),
+// one uniform per row in u_dev. Token ids land in tokens_dev. Asynchronous on
+// `hip_stream` (a hipStream_t); the device buffers must stay valid until the
+// work completes. Returns 0 or a negative ultima_hsamp status.
 int sample_batch(const float* logits_dev, std::int32_t rows, std::int32_t vocab,
                  std::int64_t stride, std::span<const SamplerParams> params,
-                 std::span<const std::span<const TokenId>> histories,
-                 const double* u_dev, TokenId* tokens_dev, void* hip_stream);
+                 const TokenId* hist_dev, std::int64_t hist_stride,
+                 std::span<const std::int64_t> hist_len, const double* u_dev,
+                 TokenId* tokens_dev, void* hip_stream);
 
 } // namespace ultima::sampler

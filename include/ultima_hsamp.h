@@ -129,7 +129,11 @@ int ultima_hsamp_destroy(ultima_hsamp* h);
 
 /* Sample every row of `batch`, asynchronously on `hip_stream` (a hipStream_t,
  * NULL = the null stream). Inputs must stay valid and unchanged until the work
- * completes; outputs are valid once it has. */
+ * completes; outputs are valid once it has. Work from one handle must not
+ * overlap on two streams. The call may be captured into a HIP graph once the
+ * same batch (same knobs, rows and vocab) has run uncaptured on the handle;
+ * under capture it allocates and uploads nothing and returns
+ * ULTIMA_HSAMP_ERR_UNSUPPORTED if it would have to. */
 int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* batch, void* hip_stream);
 
 /* One row in HOST memory, synchronously -- sample() of sampler.cpp:230-277 with

@@ -1,0 +1,94 @@
+"""The C ABI boundary without a GPU: the libraries load, export every symbol
+the headers declare, and the host-only entry points behave as specified."""
+import ctypes
+import subprocess
+
+import numpy as np
+import pytest
+
+
+def test_hsamp_exports_every_declared_symbol(pkg):
+    hs = pkg.hsamp
+    L = hs.lib()
+    names = hs.declared_symbols()
+    assert len(names) >= 9
+    for n in names:
+        assert hasattr(L, n), f"{n} declared in include/ultima_hsamp.h but not exported"
+
+
+def test_version_and_status_strings(pkg):
+    L = pkg.hsamp.lib()
+    assert L.ultima_hsamp_version() == 1
+    for st in (0, -1, -2, -3, -4, -5, -6):
+        assert L.ultima_hsamp_status_str(st).decode() not in ("", "unknown status")
+    assert L.ultima_hsamp_status_str(-99).decode() == "unknown status"
+
+
+def test_params_default_and_identity_match_reference(pkg, orc):
+    hs = pkg.hsamp
+    L = hs.lib()
+    for fn, ref in ((L.ultima_hsamp_params_default, orc.default_params()),
+                    (L.ultima_hsamp_params_identity, orc.identity_params())):
+        p = hs.Params()
+        fn(ctypes.byref(p))
+        for k, v in ref.items():
+            assert getattr(p, k) == pytest.approx(np.float32(v)) if isinstance(v, float) else getattr(p, k) == v, k
+        assert p.hist_len == 0 and p.bias_count == 0
+
+
+@pytest.mark.parametrize("seed", [0, 1, 42, 5489, 123456])
+def test_uniform_from_u64_is_generate_canonical(pkg, orc, seed):
+    L = pkg.hsamp.lib()
+    x = orc.mt19937_64_nth(seed, 1)
+    assert L.ultima_hsamp_uniform_from_u64(x) == orc.u_from_seed(seed)
+
+
+def test_uniform_from_u64_clamps_below_one(pkg):
+    L = pkg.hsamp.lib()
+    assert L.ultima_hsamp_uniform_from_u64(2**64 - 1) == np.nextafter(1.0, 0.0)
+    assert L.ultima_hsamp_uniform_from_u64(0) == 0.0
+
+
+def test_create_rejects_bad_arguments(pkg):
+    L = pkg.hsamp.lib()
+    h = ctypes.c_void_p()
+    assert L.ultima_hsamp_create(0, 0, 100, ctypes.byref(h)) == -1
+    assert L.ultima_hsamp_create(0, 10, 0, ctypes.byref(h)) == -1
+    assert L.ultima_hsamp_create(0, 10, 1 << 25, ctypes.byref(h)) == -5
+    assert L.ultima_hsamp_create(0, 10, 100, None) == -1
+    assert L.ultima_hsamp_destroy(None) == 0
+    assert L.ultima_hsamp_run(None, None, None) == -1
+
+
+def test_create_without_gfx950_reports_no_device(pkg):
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    L = pkg.hsamp.lib()
+    h = ctypes.c_void_p()
+    assert L.ultima_hsamp_create(0, 10, 100, ctypes.byref(h)) == -6
+    assert not h.value
+
+
+def test_cpp_dropin_exports_reference_interface(pkg):
+    so = pkg.hsamp.PKG / "libultima_sampler.so"
+    out = subprocess.run(["nm", "-DC", "--defined-only", str(so)], capture_output=True, text=True,
+                         check=True).stdout
+    for sym in ("ultima::sampler::sample(std::span<float, 18446744073709551615ul>, "
+                "ultima::sampler::SamplerParams const&, ultima::sampler::SamplerContext&)",
+                "ultima::sampler::argmax(std::span<float const, 18446744073709551615ul>)",
+                "ultima::sampler::SamplerParams::identity()",
+                "ultima::sampler::SamplerContext::SamplerContext(unsigned long)",
+                "ultima::sampler::SamplerContext::SamplerContext()",
+                "ultima::sampler::SamplerContext::push_recent(int)",
+                "ultima::sampler::SamplerContext::set_recent(std::span<int const, 18446744073709551615ul>)"):
+        assert sym in out, sym
+
+
+def test_product_does_not_link_the_oracle(pkg):
+    for so in ("libultima_hsamp.so", "libultima_sampler.so"):
+        out = subprocess.run(["ldd", str(pkg.hsamp.PKG / so)], capture_output=True, text=True).stdout
+        assert "orc_sampler" not in out and "ref_sampler" not in out
+        syms = subprocess.run(["nm", "-D", str(pkg.hsamp.PKG / so)], capture_output=True,
+                              text=True).stdout
+        assert "orc_" not in syms and "ref_sample" not in syms

@@ -1,0 +1,83 @@
+"""Build the native libraries of the package in-tree.
+
+    libultima_hsamp.so   -- HIP kernels for gfx950 + the C ABI (include/ultima_hsamp.h)
+    libultima_sampler.so -- the ultima::sampler C++ drop-in (include/ultima/sampler/sampler.hpp)
+    dropin_driver        -- tests/cpp/dropin_driver.cpp linked against the drop-in
+    tests/cpp/libdevice_expf.so -- test kit evaluating the device expf
+
+Every call compiles from scratch (no staleness checks): the outputs are small
+and the compile takes well under a minute.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+INC = ROOT / "include"
+BUILD = PKG / "_build"
+
+HSAMP_SO = PKG / "libultima_hsamp.so"
+SAMPLER_SO = PKG / "libultima_sampler.so"
+CPP_TEST = PKG / "dropin_driver"
+
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+HIPCC = str(ROCM / "bin" / "hipcc")
+
+# Device code: gfx950 only, IEEE float semantics (no contraction, correctly
+# rounded f32 division), no packed-FP32 instructions.
+HIP_FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++20", "-fPIC",
+    "-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-fno-gpu-rdc", "-Wall", "-Wno-unused-function",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{INC}", f"-I{CSRC}",
+]
+
+
+def _run(cmd: list[str]) -> None:
+    print("+", " ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError(f"build step failed: {cmd[0]} ... {cmd[-1]}")
+    noise = [ln for ln in (r.stdout + r.stderr).splitlines()
+             if ln.strip() and "packed-fp32-ops" not in ln and "not a recognized feature" not in ln]
+    if noise:
+        sys.stderr.write("\n".join(noise) + "\n")
+
+
+def build_all() -> None:
+    if shutil.which(HIPCC) is None and not Path(HIPCC).exists():
+        raise RuntimeError(f"hipcc not found at {HIPCC}")
+    BUILD.mkdir(exist_ok=True)
+    objs = {
+        "hsamp_kernels.o": CSRC / "hsamp_kernels.hip",
+        "hsamp_api.o": CSRC / "hsamp_api.cpp",
+    }
+    with ThreadPoolExecutor(max_workers=2) as ex:
+        futs = [ex.submit(_run, [HIPCC, *HIP_FLAGS, "-x", "hip", "-c", str(src), "-o", str(BUILD / o)])
+                for o, src in objs.items()]
+        for f in futs:
+            f.result()
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-fno-gpu-rdc",
+          *[str(BUILD / o) for o in objs], "-o", str(HSAMP_SO)])
+    # The C++ drop-in: host code only, reference-compatible flags.
+    cxx = ["g++", "-std=c++20", "-O2", "-fPIC", "-fno-rtti", "-fno-exceptions", "-Wall", "-Wextra",
+           f"-I{INC}"]
+    _run([*cxx, "-shared", str(CSRC / "sampler.cpp"), "-o", str(SAMPLER_SO),
+          f"-L{PKG}", "-lultima_hsamp", "-Wl,-rpath,$ORIGIN"])
+    _run([HIPCC, *HIP_FLAGS, "-shared", "-x", "hip", str(ROOT / "tests" / "cpp" / "device_expf.hip"),
+          "-o", str(ROOT / "tests" / "cpp" / "libdevice_expf.so")])
+    _run([*cxx, str(ROOT / "tests" / "cpp" / "dropin_driver.cpp"), "-o", str(CPP_TEST),
+          f"-L{PKG}", "-lultima_sampler", "-lultima_hsamp", "-Wl,-rpath,$ORIGIN"])
+
+
+if __name__ == "__main__":
+    build_all()

@@ -1,0 +1,604 @@
+// Host side of the C ABI in include/ultima_hsamp.h.
+//
+// Each run() turns the per-row knobs into RowPlans with the reference's own
+// stage predicates (src/sampler/sampler.cpp:230-277), packs them with the DRY
+// penalty tables and the sorted logit-bias entries into one blob, uploads the
+// blob through a small ring of pinned staging buffers (skipped when the same
+// blob is already resident), picks the slicing of the vocabulary and launches
+// the stream kernel on the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <tuple>
+#include <vector>
+
+#include "hsamp_plan.h"
+#include "ultima_hsamp.h"
+
+namespace hsamp {
+hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, int grid, hipStream_t stream);
+hipError_t launch_writeback(const StreamArgs& a, int grid, uint32_t lds, hipStream_t stream);
+hipError_t set_kernel_attrs();
+}  // namespace hsamp
+
+using namespace hsamp;
+
+namespace {
+
+constexpr int kSlots = 4;
+constexpr int kTile = kBlock * 32;      // elements one block streams per tile
+constexpr int kTargetBlocks = 2048;     // blocks a launch aims for (8 per CU)
+
+struct Slot {
+    char* host = nullptr;   // pinned
+    char* dev = nullptr;
+    size_t cap = 0;
+    size_t size = 0;
+    hipEvent_t ev = nullptr;
+    bool used = false;
+    bool pinned = false;    // referenced by a captured graph: never rewritten
+};
+
+int next_pow2(int x) {
+    int p = 1;
+    while (p < x) p <<= 1;
+    return p;
+}
+size_t align16(size_t x) { return (x + 15) & ~size_t(15); }
+
+}  // namespace
+
+struct ultima_hsamp {
+    int device = 0;
+    int32_t max_rows = 0;
+    int32_t max_vocab = 0;
+    hipStream_t own_stream = nullptr;
+    Slot slots[kSlots];
+    int next_slot = 0;
+    std::vector<char> blob;
+    std::vector<RowPlan> plans;
+    // scratch sized for the worst case at creation
+    unsigned long long* cand = nullptr;
+    size_t cand_elems = 0;
+    int32_t* cand_n = nullptr;
+    uint32_t* counters = nullptr;
+    int32_t* fin_idx = nullptr;
+    int32_t* fin_n = nullptr;
+    unsigned long long* ovf = nullptr;   // per-block overflow of the LDS candidate buffer
+    size_t ovf_elems = 0;
+    // sample_host staging
+    float* d_row = nullptr;
+    float* h_row = nullptr;       // pinned
+    int32_t* d_hist = nullptr;
+    int32_t* h_hist = nullptr;    // pinned
+    size_t hist_cap = 0;
+    double* d_u = nullptr;
+    int32_t* d_tok = nullptr;
+    double* h_u = nullptr;        // pinned
+    int32_t* h_tok = nullptr;     // pinned
+};
+
+namespace {
+
+int hip_fail(hipError_t e) {
+    (void)hipGetLastError();
+    return e == hipErrorOutOfMemory ? ULTIMA_HSAMP_ERR_NOMEM : ULTIMA_HSAMP_ERR_HIP;
+}
+#define HIP_TRY(x)                              \
+    do {                                        \
+        hipError_t e_ = (x);                    \
+        if (e_ != hipSuccess) return hip_fail(e_); \
+    } while (0)
+
+bool isnan_f(float x) { return x != x; }
+
+// DRY table key: (multiplier bits, base bits, allowed, window).
+using DryKey = std::tuple<uint32_t, uint32_t, int32_t, int32_t>;
+
+uint32_t fbits(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    return u;
+}
+
+struct Built {
+    size_t off_dry = 0, off_bias_ids = 0, off_bias_vals = 0, total = 0;
+    int kmax = 0;              // max top_k over rows that select
+    int max_pen = 0;           // max over penalty rows of (scan_len + bias entries)
+    bool any_pen = false;
+    bool any_full = false;     // a sampling row without top-k (not handled here)
+    bool any_big_k = false;    // top_k above kLimitK
+};
+
+// RowPlans + DRY tables + bias into h->blob; the reference's predicates in [].
+int build_blob(ultima_hsamp* h, const ultima_hsamp_batch* b, Built& out) {
+    const int B = b->rows, V = b->vocab;
+    h->plans.assign(B, RowPlan{});
+    std::vector<float> dry;
+    std::map<DryKey, int32_t> dry_seen;
+    std::vector<int32_t> bids;
+    std::vector<float> bvals;
+    std::vector<std::pair<int32_t, float>> tmp;
+    for (int r = 0; r < B; ++r) {
+        const ultima_hsamp_params& q = b->params[r];
+        RowPlan& P = h->plans[r];
+        if (isnan_f(q.rep_penalty) || isnan_f(q.dry_multiplier) || isnan_f(q.dry_base) ||
+            isnan_f(q.frequency_penalty) || isnan_f(q.presence_penalty) ||
+            isnan_f(q.temperature) || isnan_f(q.top_p) || isnan_f(q.min_p))
+            return ULTIMA_HSAMP_ERR_INVALID;
+        if (q.hist_len < 0 || q.hist_len > b->hist_stride || (q.hist_len > 0 && b->hist == nullptr))
+            return ULTIMA_HSAMP_ERR_INVALID;
+        if (q.bias_count < 0 || q.bias_count > ULTIMA_HSAMP_MAX_BIAS ||
+            (q.bias_count > 0 && (b->bias_ids == nullptr || b->bias_vals == nullptr || q.bias_offset < 0)))
+            return ULTIMA_HSAMP_ERR_INVALID;
+        const int64_t L = q.hist_len;
+        auto win = [&](uint64_t n) -> int64_t { return (int64_t)std::min<uint64_t>(n, (uint64_t)L); };
+        uint32_t fl = 0;
+        const bool greedy = q.temperature <= 0.0f;                             // [261]
+        if (greedy) fl |= RF_GREEDY;
+        int64_t rep_w = 0, dry_w = 0, fp_w = 0;
+        if (q.rep_penalty != 1.0f && q.repeat_last_n > 0 && win(q.repeat_last_n) > 0) {  // [239, 44]
+            fl |= RF_REP;
+            rep_w = win(q.repeat_last_n);
+        }
+        if (q.dry_multiplier > 0.0f && q.dry_last_n > 0 && win(q.dry_last_n) >= 2) {     // [246, 69]
+            fl |= RF_DRY;
+            dry_w = win(q.dry_last_n);
+        }
+        if ((q.frequency_penalty != 0.0f || q.presence_penalty != 0.0f) &&             // [254-256, 89]
+            win(std::max(q.repeat_last_n, q.dry_last_n)) > 0) {
+            fl |= RF_FP;
+            fp_w = win(std::max(q.repeat_last_n, q.dry_last_n));
+        }
+        const int64_t scan = std::max({rep_w, dry_w, fp_w});
+        if (scan > ULTIMA_HSAMP_MAX_WINDOW) return ULTIMA_HSAMP_ERR_CAPACITY;
+        P.rep = q.rep_penalty;
+        P.freq = q.frequency_penalty;
+        P.pres = q.presence_penalty;
+        P.hist_len = (int32_t)L;
+        P.rep_win = (int32_t)rep_w;
+        P.dry_win = (int32_t)dry_w;
+        P.fp_win = (int32_t)fp_w;
+        P.scan_len = (int32_t)scan;
+        P.dry_allowed = (int32_t)std::min<uint64_t>(q.dry_allowed_len, 0x7fff);
+        if (fl & RF_DRY) {
+            // sampler.cpp:79-81: pen = multiplier * powf(base, float(n - allowed_len))
+            const DryKey key{fbits(q.dry_multiplier), fbits(q.dry_base), P.dry_allowed, (int32_t)dry_w};
+            auto it = dry_seen.find(key);
+            if (it == dry_seen.end()) {
+                const int32_t off = (int32_t)dry.size();
+                for (int64_t c = 0; c <= dry_w; ++c) {
+                    const bool on = (uint64_t)c > q.dry_allowed_len;
+                    dry.push_back(on ? q.dry_multiplier *
+                                           std::pow(q.dry_base, static_cast<float>((uint64_t)c - q.dry_allowed_len))
+                                     : 0.0f);
+                }
+                it = dry_seen.emplace(key, off).first;
+            }
+            P.dry_tab = it->second;
+        }
+        if (q.bias_count > 0) {
+            tmp.clear();
+            for (int64_t j = 0; j < q.bias_count; ++j) {
+                const int32_t id = b->bias_ids[q.bias_offset + j];
+                if (id < 0 || id >= V) continue;                                  // [32]
+                tmp.emplace_back(id, b->bias_vals[q.bias_offset + j]);
+            }
+            std::sort(tmp.begin(), tmp.end(),
+                      [](const auto& x, const auto& y) { return x.first < y.first; });
+            for (size_t j = 1; j < tmp.size(); ++j)
+                if (tmp[j].first == tmp[j - 1].first) return ULTIMA_HSAMP_ERR_INVALID;
+            if (!tmp.empty()) {
+                fl |= RF_BIAS;
+                P.bias_off = (int32_t)bids.size();
+                P.bias_cnt = (int32_t)tmp.size();
+                for (auto& [id, v] : tmp) {
+                    bids.push_back(id);
+                    bvals.push_back(v);
+                }
+            }
+        }
+        if (b->mask != nullptr) fl |= RF_MASK;
+        if (!greedy) {
+            if (q.temperature != 1.0f) {                                          // [102]
+                fl |= RF_TEMP;
+                P.inv_temp = 1.0f / q.temperature;                                // [104]
+            }
+            if (V == 1) {
+                fl |= RF_SINGLE | RF_TOPK;
+                P.top_k = 1;
+            } else if (q.top_k > 0 && q.top_k < (uint64_t)V) {                   // [267, 110]
+                fl |= RF_TOPK;
+                P.top_k = (int32_t)q.top_k;
+                if (P.top_k > kLimitK) out.any_big_k = true;
+            } else {
+                out.any_full = true;
+            }
+            if (q.top_p < 1.0f && !(q.top_p <= 0.0f)) fl |= RF_TOPP;             // [270, 147]
+            if (q.min_p > 0.0f) fl |= RF_MINP;                                    // [273, 168]
+            P.top_p = q.top_p;
+            P.min_p = q.min_p;
+            out.kmax = std::max(out.kmax, P.top_k);
+        }
+        P.flags = fl;
+        if (fl & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) {
+            out.any_pen = true;
+            out.max_pen = std::max(out.max_pen, (int)scan + P.bias_cnt);
+        }
+    }
+    out.off_dry = align16(sizeof(RowPlan) * B);
+    out.off_bias_ids = align16(out.off_dry + sizeof(float) * dry.size());
+    out.off_bias_vals = align16(out.off_bias_ids + sizeof(int32_t) * bids.size());
+    out.total = align16(out.off_bias_vals + sizeof(float) * bvals.size());
+    h->blob.assign(out.total, 0);
+    std::memcpy(h->blob.data(), h->plans.data(), sizeof(RowPlan) * B);
+    if (!dry.empty()) std::memcpy(h->blob.data() + out.off_dry, dry.data(), sizeof(float) * dry.size());
+    if (!bids.empty()) {
+        std::memcpy(h->blob.data() + out.off_bias_ids, bids.data(), sizeof(int32_t) * bids.size());
+        std::memcpy(h->blob.data() + out.off_bias_vals, bvals.data(), sizeof(float) * bvals.size());
+    }
+    return ULTIMA_HSAMP_OK;
+}
+
+// A device copy of h->blob, reusing a slot that already holds the same bytes.
+// Under stream capture nothing is uploaded: the blob must already be resident
+// (run the same batch once before capturing), and its slot is pinned so later
+// calls never rewrite what the graph reads.
+int upload_blob(ultima_hsamp* h, hipStream_t stream, bool capturing, Slot*& used) {
+    const size_t n = h->blob.size();
+    for (auto& s : h->slots) {
+        if (s.used && s.size == n && std::memcmp(s.host, h->blob.data(), n) == 0) {
+            if (capturing) s.pinned = true;
+            used = &s;
+            return ULTIMA_HSAMP_OK;
+        }
+    }
+    if (capturing) return ULTIMA_HSAMP_ERR_UNSUPPORTED;
+    Slot* pick = nullptr;
+    for (int i = 0; i < kSlots && pick == nullptr; ++i) {
+        Slot& c = h->slots[(h->next_slot + i) % kSlots];
+        if (!c.pinned) {
+            pick = &c;
+            h->next_slot = (h->next_slot + i + 1) % kSlots;
+        }
+    }
+    if (pick == nullptr) return ULTIMA_HSAMP_ERR_CAPACITY;
+    Slot& s = *pick;
+    if (s.used) HIP_TRY(hipEventSynchronize(s.ev));   // its last kernel is done with it
+    if (s.cap < n) {
+        if (s.host) HIP_TRY(hipHostFree(s.host));
+        if (s.dev) HIP_TRY(hipFree(s.dev));
+        s.host = nullptr;
+        s.dev = nullptr;
+        const size_t cap = std::max<size_t>(n * 2, 64 * 1024);
+        HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&s.host), cap, hipHostMallocDefault));
+        HIP_TRY(hipMalloc(reinterpret_cast<void**>(&s.dev), cap));
+        s.cap = cap;
+    }
+    std::memcpy(s.host, h->blob.data(), n);
+    s.size = n;
+    s.used = true;
+    HIP_TRY(hipMemcpyAsync(s.dev, s.host, n, hipMemcpyHostToDevice, stream));
+    used = &s;
+    return ULTIMA_HSAMP_OK;
+}
+
+int validate_batch(const ultima_hsamp* h, const ultima_hsamp_batch* b) {
+    if (b == nullptr || b->params == nullptr) return ULTIMA_HSAMP_ERR_INVALID;
+    if (b->rows < 1 || b->vocab < 1) return ULTIMA_HSAMP_ERR_INVALID;
+    if (b->rows > h->max_rows || b->vocab > h->max_vocab) return ULTIMA_HSAMP_ERR_CAPACITY;
+    if (b->dtype != ULTIMA_HSAMP_F32 && b->dtype != ULTIMA_HSAMP_BF16) return ULTIMA_HSAMP_ERR_INVALID;
+    if (b->logits == nullptr || b->u == nullptr || b->token == nullptr) return ULTIMA_HSAMP_ERR_INVALID;
+    if (b->logits_stride < b->vocab) return ULTIMA_HSAMP_ERR_INVALID;
+    if (b->hist != nullptr && b->hist_stride < 0) return ULTIMA_HSAMP_ERR_INVALID;
+    if (b->mask != nullptr && b->mask_stride < (b->vocab + 31) / 32) return ULTIMA_HSAMP_ERR_INVALID;
+    if ((b->flags & ~ULTIMA_HSAMP_WRITEBACK) != 0) return ULTIMA_HSAMP_ERR_INVALID;
+    if ((b->flags & ULTIMA_HSAMP_WRITEBACK) && b->dtype != ULTIMA_HSAMP_F32)
+        return ULTIMA_HSAMP_ERR_UNSUPPORTED;
+    const bool sets = b->topk_idx || b->kept_idx || b->kept_prob;
+    if (sets && b->set_cap < 1) return ULTIMA_HSAMP_ERR_INVALID;
+    if ((b->kept_idx == nullptr) != (b->kept_prob == nullptr)) return ULTIMA_HSAMP_ERR_INVALID;
+    return ULTIMA_HSAMP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ultima_hsamp_version(void) { return ULTIMA_HSAMP_VERSION; }
+
+const char* ultima_hsamp_status_str(int s) {
+    switch (s) {
+        case ULTIMA_HSAMP_OK: return "ok";
+        case ULTIMA_HSAMP_ERR_INVALID: return "invalid argument";
+        case ULTIMA_HSAMP_ERR_HIP: return "HIP runtime error";
+        case ULTIMA_HSAMP_ERR_UNSUPPORTED: return "unsupported by this build";
+        case ULTIMA_HSAMP_ERR_NOMEM: return "out of memory";
+        case ULTIMA_HSAMP_ERR_CAPACITY: return "exceeds handle or build limits";
+        case ULTIMA_HSAMP_ERR_NO_DEVICE: return "no usable gfx950 device";
+        default: return "unknown status";
+    }
+}
+
+void ultima_hsamp_params_default(ultima_hsamp_params* p) {
+    if (p == nullptr) return;
+    *p = ultima_hsamp_params{};
+    p->rep_penalty = 1.1f;
+    p->repeat_last_n = 64;
+    p->dry_multiplier = 0.8f;
+    p->dry_base = 1.75f;
+    p->dry_allowed_len = 2;
+    p->dry_last_n = 512;
+    p->frequency_penalty = 0.0f;
+    p->presence_penalty = 0.0f;
+    p->temperature = 0.2f;
+    p->top_k = 40;
+    p->top_p = 0.95f;
+    p->min_p = 0.05f;
+}
+
+void ultima_hsamp_params_identity(ultima_hsamp_params* p) {
+    if (p == nullptr) return;
+    ultima_hsamp_params_default(p);
+    p->rep_penalty = 1.0f;
+    p->repeat_last_n = 0;
+    p->dry_multiplier = 0.0f;
+    p->dry_last_n = 0;
+    p->frequency_penalty = 0.0f;
+    p->presence_penalty = 0.0f;
+    p->temperature = 1.0f;
+    p->top_k = 0;
+    p->top_p = 1.0f;
+    p->min_p = 0.0f;
+}
+
+double ultima_hsamp_uniform_from_u64(uint64_t x) {
+    const double r = static_cast<double>(x) / 18446744073709551616.0;
+    return r >= 1.0 ? std::nextafter(1.0, 0.0) : r;
+}
+
+int ultima_hsamp_create(int device, int32_t max_rows, int32_t max_vocab, ultima_hsamp** out) {
+    if (out == nullptr) return ULTIMA_HSAMP_ERR_INVALID;
+    *out = nullptr;
+    if (max_rows < 1 || max_vocab < 1) return ULTIMA_HSAMP_ERR_INVALID;
+    if (max_vocab > ULTIMA_HSAMP_MAX_VOCAB) return ULTIMA_HSAMP_ERR_CAPACITY;
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev) {
+        (void)hipGetLastError();
+        return ULTIMA_HSAMP_ERR_NO_DEVICE;
+    }
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) return ULTIMA_HSAMP_ERR_NO_DEVICE;
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return ULTIMA_HSAMP_ERR_NO_DEVICE;
+    HIP_TRY(hipSetDevice(device));
+    static std::once_flag attrs_once;
+    static hipError_t attrs_err = hipSuccess;
+    std::call_once(attrs_once, [] { attrs_err = set_kernel_attrs(); });
+    HIP_TRY(attrs_err);
+
+    auto* h = new ultima_hsamp();
+    h->device = device;
+    h->max_rows = max_rows;
+    h->max_vocab = max_vocab;
+    auto fail = [&](int st) {
+        ultima_hsamp_destroy(h);
+        return st;
+    };
+#define CREATE_TRY(x)                                   \
+    do {                                                \
+        hipError_t e_ = (x);                            \
+        if (e_ != hipSuccess) return fail(hip_fail(e_)); \
+    } while (0)
+    CREATE_TRY(hipStreamCreateWithFlags(&h->own_stream, hipStreamNonBlocking));
+    for (auto& s : h->slots) CREATE_TRY(hipEventCreateWithFlags(&s.ev, hipEventDisableTiming));
+    // Candidates: rows * slices <= max(kTargetBlocks, max_rows) blocks, each
+    // leaving at most 2 * kLimitK entries.
+    const size_t blocks = std::max<size_t>(kTargetBlocks + 8, (size_t)max_rows);
+    h->cand_elems = blocks * 2 * kLimitK;
+    CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->cand), h->cand_elems * 8));
+    CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->cand_n), blocks * 4));
+    CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->counters), (size_t)max_rows * 4));
+    CREATE_TRY(hipMemset(h->counters, 0, (size_t)max_rows * 4));
+    CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->fin_idx), (size_t)max_rows * kLimitK * 4));
+    CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->fin_n), (size_t)max_rows * 4));
+    CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_row), (size_t)max_vocab * 4 + 64));
+    CREATE_TRY(hipHostMalloc(reinterpret_cast<void**>(&h->h_row), (size_t)max_vocab * 4 + 64,
+                             hipHostMallocDefault));
+    CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_u), 64));
+    CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_tok), 64));
+    CREATE_TRY(hipHostMalloc(reinterpret_cast<void**>(&h->h_u), 64, hipHostMallocDefault));
+    CREATE_TRY(hipHostMalloc(reinterpret_cast<void**>(&h->h_tok), 64, hipHostMallocDefault));
+    CREATE_TRY(hipDeviceSynchronize());
+#undef CREATE_TRY
+    *out = h;
+    return ULTIMA_HSAMP_OK;
+}
+
+int ultima_hsamp_destroy(ultima_hsamp* h) {
+    if (h == nullptr) return ULTIMA_HSAMP_OK;
+    (void)hipSetDevice(h->device);
+    (void)hipDeviceSynchronize();
+    for (auto& s : h->slots) {
+        if (s.host) (void)hipHostFree(s.host);
+        if (s.dev) (void)hipFree(s.dev);
+        if (s.ev) (void)hipEventDestroy(s.ev);
+    }
+    for (void* p : {(void*)h->ovf, (void*)h->cand, (void*)h->cand_n, (void*)h->counters, (void*)h->fin_idx,
+                    (void*)h->fin_n, (void*)h->d_row, (void*)h->d_hist, (void*)h->d_u, (void*)h->d_tok})
+        if (p) (void)hipFree(p);
+    for (void* p : {(void*)h->h_row, (void*)h->h_hist, (void*)h->h_u, (void*)h->h_tok})
+        if (p) (void)hipHostFree(p);
+    if (h->own_stream) (void)hipStreamDestroy(h->own_stream);
+    (void)hipGetLastError();
+    delete h;
+    return ULTIMA_HSAMP_OK;
+}
+
+int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_stream) {
+    if (h == nullptr) return ULTIMA_HSAMP_ERR_INVALID;
+    int st = validate_batch(h, b);
+    if (st != ULTIMA_HSAMP_OK) return st;
+    HIP_TRY(hipSetDevice(h->device));
+    hipStream_t stream = static_cast<hipStream_t>(hip_stream);
+    Built bl;
+    st = build_blob(h, b, bl);
+    if (st != ULTIMA_HSAMP_OK) return st;
+    if (bl.any_full || bl.any_big_k) return ULTIMA_HSAMP_ERR_UNSUPPORTED;
+
+    const int B = b->rows, V = b->vocab;
+    const int es = b->dtype == ULTIMA_HSAMP_F32 ? 4 : 2;
+    // Slicing: enough blocks to fill 256 CUs, slices of at most one tile.
+    const int tiles = (V + kTile - 1) / kTile;
+    int S = std::max(1, std::min({kTargetBlocks / B, tiles, kBlock}));
+    int slice_len = ((V + S - 1) / S + 31) & ~31;
+    S = (V + slice_len - 1) / slice_len;
+    const int kmax = std::max(1, bl.kmax);
+    const int buf_cap = std::max(512, next_pow2(2 * kmax));
+    const int cand_cap = std::max(2, std::min(buf_cap, 4 * kmax));
+    int hash_slots = 0;
+    if (bl.any_pen) hash_slots = std::max(16, next_pow2(std::min(bl.max_pen, slice_len)));
+    const int bitmap_words = slice_len / 32;
+    const size_t regionA = 4 * (size_t)((bitmap_words + 3) & ~3) + 8 * (size_t)hash_slots;
+    const size_t regionF = 8 * (size_t)next_pow2(kmax) + 20 * (size_t)kmax;
+    const size_t lds = align16(std::max(regionA, regionF)) + 8 * (size_t)buf_cap;
+    if (lds > 160 * 1024) return ULTIMA_HSAMP_ERR_CAPACITY;
+    if ((size_t)B * S * cand_cap > h->cand_elems) return ULTIMA_HSAMP_ERR_CAPACITY;
+    const int nblocks = B * S;
+    const int grid = (nblocks + kXcds - 1) / kXcds * kXcds;
+
+    hipStreamCaptureStatus cap_status = hipStreamCaptureStatusNone;
+    HIP_TRY(hipStreamIsCapturing(stream, &cap_status));
+    const bool capturing = cap_status != hipStreamCaptureStatusNone;
+    const size_t ovf_need = (size_t)grid * kTile;
+    if (ovf_need > h->ovf_elems) {
+        if (capturing) return ULTIMA_HSAMP_ERR_UNSUPPORTED;   // run once before capturing
+        // grow-only; the device must be idle before the old area goes away
+        HIP_TRY(hipDeviceSynchronize());
+        if (h->ovf) HIP_TRY(hipFree(h->ovf));
+        h->ovf = nullptr;
+        h->ovf_elems = 0;
+        HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->ovf), ovf_need * 8));
+        h->ovf_elems = ovf_need;
+    }
+
+    Slot* slot = nullptr;
+    st = upload_blob(h, stream, capturing, slot);
+    if (st != ULTIMA_HSAMP_OK) return st;
+
+    StreamArgs a{};
+    a.logits = b->logits;
+    a.logits_stride = b->logits_stride;
+    a.hist = b->hist;
+    a.hist_stride = b->hist_stride;
+    a.mask = b->mask;
+    a.mask_stride = b->mask_stride;
+    a.u = b->u;
+    a.plans = reinterpret_cast<const RowPlan*>(slot->dev);
+    a.dry_tab = reinterpret_cast<const float*>(slot->dev + bl.off_dry);
+    a.bias_ids = reinterpret_cast<const int32_t*>(slot->dev + bl.off_bias_ids);
+    a.bias_vals = reinterpret_cast<const float*>(slot->dev + bl.off_bias_vals);
+    a.token = b->token;
+    a.row_flags = b->row_flags;
+    a.topk_idx = b->topk_idx;
+    a.topk_count = b->topk_count;
+    a.kept_idx = b->kept_idx;
+    a.kept_prob = b->kept_prob;
+    a.kept_count = b->kept_count;
+    a.set_cap = b->set_cap;
+    a.rows = B;
+    a.vocab = V;
+    a.nslices = S;
+    a.slice_len = slice_len;
+    a.kmax = kmax;
+    a.cand_cap = cand_cap;
+    a.buf_cap = buf_cap;
+    a.hash_slots = hash_slots;
+    a.bitmap_words = bitmap_words;
+    a.blocks_per_xcd = grid / kXcds;
+    a.fin_cap = kLimitK;
+    a.ovf = h->ovf;
+    a.ovf_cap = kTile;
+    a.cand = h->cand;
+    a.cand_n = h->cand_n;
+    a.counters = h->counters;
+    const bool wb = (b->flags & ULTIMA_HSAMP_WRITEBACK) != 0;
+    a.fin_idx = wb ? h->fin_idx : nullptr;
+    a.fin_n = wb ? h->fin_n : nullptr;
+    a.lds_bytes = (uint32_t)lds;
+    const bool vec = (reinterpret_cast<uintptr_t>(b->logits) % 16 == 0) &&
+                     ((b->logits_stride * es) % 16 == 0);
+    HIP_TRY(launch_stream(a, b->dtype, vec, grid, stream));
+    if (wb) {
+        const uint32_t wlds = (uint32_t)(regionA + 4 * (size_t)bitmap_words + 16);
+        HIP_TRY(launch_writeback(a, grid, wlds, stream));
+    }
+    if (!capturing) HIP_TRY(hipEventRecord(slot->ev, stream));
+    return ULTIMA_HSAMP_OK;
+}
+
+int ultima_hsamp_sample_host(ultima_hsamp* h, float* logits, int32_t vocab,
+                             const ultima_hsamp_params* params, const int32_t* hist,
+                             const int32_t* bias_ids, const float* bias_vals, double u,
+                             int writeback, int32_t* token_out) {
+    if (h == nullptr || logits == nullptr || params == nullptr || token_out == nullptr)
+        return ULTIMA_HSAMP_ERR_INVALID;
+    if (vocab < 1) return ULTIMA_HSAMP_ERR_INVALID;
+    if (vocab > h->max_vocab) return ULTIMA_HSAMP_ERR_CAPACITY;
+    if (params->hist_len < 0 || (params->hist_len > 0 && hist == nullptr)) return ULTIMA_HSAMP_ERR_INVALID;
+    HIP_TRY(hipSetDevice(h->device));
+    hipStream_t s = h->own_stream;
+    const size_t L = (size_t)params->hist_len;
+    if (L > h->hist_cap) {
+        if (h->d_hist) HIP_TRY(hipFree(h->d_hist));
+        if (h->h_hist) HIP_TRY(hipHostFree(h->h_hist));
+        h->d_hist = nullptr;
+        h->h_hist = nullptr;
+        h->hist_cap = 0;
+        const size_t cap = std::max<size_t>(L, 1024);
+        HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_hist), cap * 4));
+        HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&h->h_hist), cap * 4, hipHostMallocDefault));
+        h->hist_cap = cap;
+    }
+    std::memcpy(h->h_row, logits, (size_t)vocab * 4);
+    HIP_TRY(hipMemcpyAsync(h->d_row, h->h_row, (size_t)vocab * 4, hipMemcpyHostToDevice, s));
+    if (L > 0) {
+        std::memcpy(h->h_hist, hist, L * 4);
+        HIP_TRY(hipMemcpyAsync(h->d_hist, h->h_hist, L * 4, hipMemcpyHostToDevice, s));
+    }
+    *h->h_u = u;
+    HIP_TRY(hipMemcpyAsync(h->d_u, h->h_u, 8, hipMemcpyHostToDevice, s));
+    ultima_hsamp_params p = *params;
+    p.bias_offset = 0;
+    ultima_hsamp_batch b{};
+    b.rows = 1;
+    b.vocab = vocab;
+    b.dtype = ULTIMA_HSAMP_F32;
+    b.flags = writeback ? ULTIMA_HSAMP_WRITEBACK : 0u;
+    b.logits = h->d_row;
+    b.logits_stride = ((int64_t)vocab + 3) & ~int64_t(3);
+    b.hist = L > 0 ? h->d_hist : nullptr;
+    b.hist_stride = (int64_t)L;
+    b.u = h->d_u;
+    b.params = &p;
+    b.bias_ids = params->bias_count > 0 ? bias_ids + params->bias_offset : nullptr;
+    b.bias_vals = params->bias_count > 0 ? bias_vals + params->bias_offset : nullptr;
+    b.token = h->d_tok;
+    int st = ultima_hsamp_run(h, &b, s);
+    if (st != ULTIMA_HSAMP_OK) {
+        (void)hipStreamSynchronize(s);
+        return st;
+    }
+    HIP_TRY(hipMemcpyAsync(h->h_tok, h->d_tok, 4, hipMemcpyDeviceToHost, s));
+    if (writeback) HIP_TRY(hipMemcpyAsync(h->h_row, h->d_row, (size_t)vocab * 4, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    if (writeback) std::memcpy(logits, h->h_row, (size_t)vocab * 4);
+    *token_out = *h->h_tok;
+    return ULTIMA_HSAMP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,111 @@
+// Per-row plan and launch arguments shared by the host API and the kernels.
+#pragma once
+
+#include <stdint.h>
+
+#include "ultima_hsamp.h"
+
+namespace hsamp {
+
+// Row outcome bits (ultima_hsamp.h).
+constexpr uint32_t ROWF_GREEDY = ULTIMA_HSAMP_ROW_GREEDY;
+constexpr uint32_t ROWF_U_USED = ULTIMA_HSAMP_ROW_U_USED;
+constexpr uint32_t ROWF_CDF_NEAR = ULTIMA_HSAMP_ROW_CDF_NEAR;
+constexpr uint32_t ROWF_NAN = ULTIMA_HSAMP_ROW_NAN;
+constexpr uint32_t ROWF_UNIFORM = ULTIMA_HSAMP_ROW_UNIFORM;
+constexpr uint32_t ROWF_TOPP_NEAR = ULTIMA_HSAMP_ROW_TOPP_NEAR;
+
+// RowPlan::flags -- which stages run for the row. Each follows the reference's
+// own predicate (src/sampler/sampler.cpp line in brackets), evaluated on the host.
+enum : uint32_t {
+    RF_GREEDY = 1u << 0,  // temperature <= 0: argmax after penalties       [261]
+    RF_TEMP = 1u << 1,    // temperature != 1: multiply by fl(1/T)          [101-106]
+    RF_REP = 1u << 2,     // rep != 1, repeat_last_n > 0, window non-empty  [44, 239]
+    RF_DRY = 1u << 3,     // mult > 0, dry_last_n > 0, window >= 2 ids       [69, 246]
+    RF_FP = 1u << 4,      // freq != 0 or presence != 0, window non-empty   [89, 254]
+    RF_TOPK = 1u << 5,    // 0 < top_k < V                                  [110, 267]
+    RF_TOPP = 1u << 6,    // top_p < 1 and not top_p <= 0                   [147, 270]
+    RF_MINP = 1u << 7,    // min_p > 0                                      [168, 273]
+    RF_MASK = 1u << 8,    // allowed-token mask given for the batch
+    RF_BIAS = 1u << 9,    // logit bias entries present                     [30]
+    RF_SINGLE = 1u << 10, // V == 1: one id, top-k off, no uniform drawn   [110, random.tcc:2660]
+};
+
+// Hash-table value bits for one token of a slice (penalty bookkeeping).
+enum : uint32_t {
+    HV_FP_MASK = 0x7fffu,    // occurrences in the frequency/presence window
+    HV_DRY_SHIFT = 15,       // occurrences in the DRY window, bits 15..29
+    HV_DRY_MASK = 0x7fffu,
+    HV_BIAS = 1u << 30,      // a logit-bias entry exists
+    HV_REP = 1u << 31,       // id is in the repetition window
+};
+
+struct alignas(16) RowPlan {
+    float inv_temp;     // fl(1.0f / T) when RF_TEMP
+    float rep;          // repetition penalty
+    float freq;         // frequency penalty
+    float pres;         // presence penalty
+    float top_p;
+    float min_p;
+    int32_t top_k;      // 0 < k < V when RF_TOPK
+    int32_t hist_len;   // L: ids in the row's history
+    int32_t rep_win;    // effective windows (suffix lengths), 0 when the stage is off
+    int32_t dry_win;
+    int32_t fp_win;
+    int32_t scan_len;   // max of the three: history suffix each block scans
+    int32_t dry_allowed;
+    int32_t dry_tab;    // offset of this row's DRY penalty table (dry_win + 1 floats)
+    int32_t bias_off;   // offset of this row's sorted bias ids/values in the plan blob
+    int32_t bias_cnt;
+    uint32_t flags;
+    uint32_t pad_[3];
+};
+static_assert(sizeof(RowPlan) == 80, "RowPlan layout");
+
+// Everything one launch of the stream kernel needs, passed by value.
+struct StreamArgs {
+    const void* logits;
+    int64_t logits_stride;      // elements
+    const int32_t* hist;
+    int64_t hist_stride;
+    const uint32_t* mask;
+    int64_t mask_stride;        // words
+    const double* u;
+    const RowPlan* plans;
+    const float* dry_tab;
+    const int32_t* bias_ids;
+    const float* bias_vals;
+    int32_t* token;
+    uint32_t* row_flags;
+    int32_t* topk_idx;
+    int32_t* topk_count;
+    int32_t* kept_idx;
+    float* kept_prob;
+    int32_t* kept_count;
+    int32_t set_cap;
+    int32_t rows;
+    int32_t vocab;
+    int32_t nslices;            // S slices per row
+    int32_t slice_len;          // elements per slice (multiple of 32)
+    int32_t kmax;               // max top_k over sampling rows (<= K_LIMIT)
+    int32_t cand_cap;           // candidates one slice may leave in global scratch
+    int32_t buf_cap;            // LDS candidate buffer entries
+    int32_t hash_slots;         // power of two, 0 when no row has penalties
+    int32_t bitmap_words;       // slice_len / 32
+    int32_t blocks_per_xcd;     // grid / 8
+    int32_t fin_cap;            // entries per row in fin_idx
+    unsigned long long* cand;   // [rows * S * cand_cap]
+    int32_t* cand_n;            // [rows * S]
+    uint32_t* counters;         // [rows], zero between launches
+    int32_t* fin_idx;           // [rows * fin_cap] final kept ids (for writeback)
+    int32_t* fin_n;             // [rows]
+    unsigned long long* ovf;    // [blocks * ovf_cap] per-block overflow of the LDS buffer
+    int32_t ovf_cap;            // one tile of candidates
+    uint32_t lds_bytes;         // dynamic LDS size of the launch
+};
+
+constexpr int kBlock = 256;        // threads per block (4 wave64)
+constexpr int kLimitK = 1024;      // largest top_k the fused kernel takes
+constexpr int kXcds = 8;           // MI355X: workgroups round-robin over 8 XCDs
+
+}  // namespace hsamp

@@ -1,0 +1,235 @@
+"""ctypes binding of libultima_hsamp (include/ultima_hsamp.h).
+
+PyTorch is used only to own device memory and streams; every sampling
+decision is made by the library's HIP kernels. Loading fails loudly when the
+library is not built.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "libultima_hsamp.so"
+HEADER = PKG.parent / "include" / "ultima_hsamp.h"
+
+OK, ERR_INVALID, ERR_HIP, ERR_UNSUPPORTED, ERR_NOMEM, ERR_CAPACITY, ERR_NO_DEVICE = 0, -1, -2, -3, -4, -5, -6
+F32, BF16 = 0, 1
+WRITEBACK = 1
+ROW_GREEDY, ROW_U_USED, ROW_CDF_NEAR, ROW_NAN, ROW_UNIFORM, ROW_TOPP_NEAR = 1, 2, 4, 8, 16, 32
+
+PARAM_KEYS = ("rep_penalty", "dry_multiplier", "dry_base", "frequency_penalty", "presence_penalty",
+              "temperature", "top_p", "min_p", "repeat_last_n", "dry_allowed_len", "dry_last_n",
+              "top_k")
+
+
+class Params(ctypes.Structure):
+    _fields_ = [
+        ("rep_penalty", ctypes.c_float),
+        ("dry_multiplier", ctypes.c_float),
+        ("dry_base", ctypes.c_float),
+        ("frequency_penalty", ctypes.c_float),
+        ("presence_penalty", ctypes.c_float),
+        ("temperature", ctypes.c_float),
+        ("top_p", ctypes.c_float),
+        ("min_p", ctypes.c_float),
+        ("repeat_last_n", ctypes.c_uint64),
+        ("dry_allowed_len", ctypes.c_uint64),
+        ("dry_last_n", ctypes.c_uint64),
+        ("top_k", ctypes.c_uint64),
+        ("hist_len", ctypes.c_int64),
+        ("bias_offset", ctypes.c_int64),
+        ("bias_count", ctypes.c_int64),
+    ]
+
+
+class Batch(ctypes.Structure):
+    _fields_ = [
+        ("rows", ctypes.c_int32),
+        ("vocab", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("flags", ctypes.c_uint32),
+        ("logits", ctypes.c_void_p),
+        ("logits_stride", ctypes.c_int64),
+        ("hist", ctypes.c_void_p),
+        ("hist_stride", ctypes.c_int64),
+        ("mask", ctypes.c_void_p),
+        ("mask_stride", ctypes.c_int64),
+        ("u", ctypes.c_void_p),
+        ("params", ctypes.POINTER(Params)),
+        ("bias_ids", ctypes.c_void_p),
+        ("bias_vals", ctypes.c_void_p),
+        ("token", ctypes.c_void_p),
+        ("row_flags", ctypes.c_void_p),
+        ("topk_idx", ctypes.c_void_p),
+        ("topk_count", ctypes.c_void_p),
+        ("kept_idx", ctypes.c_void_p),
+        ("kept_prob", ctypes.c_void_p),
+        ("kept_count", ctypes.c_void_p),
+        ("set_cap", ctypes.c_int32),
+    ]
+
+
+def declared_symbols() -> list[str]:
+    """Function names declared in include/ultima_hsamp.h."""
+    import re
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(ultima_hsamp_[a-z_0-9]+)\s*\(", text)))
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is not built: run __graft_entry__.build()")
+        L = ctypes.CDLL(str(LIB_PATH))
+        vp, i32, i64, f64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_double
+        L.ultima_hsamp_create.restype = ctypes.c_int
+        L.ultima_hsamp_create.argtypes = [ctypes.c_int, i32, i32, ctypes.POINTER(vp)]
+        L.ultima_hsamp_destroy.restype = ctypes.c_int
+        L.ultima_hsamp_destroy.argtypes = [vp]
+        L.ultima_hsamp_run.restype = ctypes.c_int
+        L.ultima_hsamp_run.argtypes = [vp, ctypes.POINTER(Batch), vp]
+        L.ultima_hsamp_sample_host.restype = ctypes.c_int
+        L.ultima_hsamp_sample_host.argtypes = [vp, vp, i32, ctypes.POINTER(Params), vp, vp, vp, f64,
+                                               ctypes.c_int, ctypes.POINTER(i32)]
+        L.ultima_hsamp_params_default.restype = None
+        L.ultima_hsamp_params_default.argtypes = [ctypes.POINTER(Params)]
+        L.ultima_hsamp_params_identity.restype = None
+        L.ultima_hsamp_params_identity.argtypes = [ctypes.POINTER(Params)]
+        L.ultima_hsamp_uniform_from_u64.restype = f64
+        L.ultima_hsamp_uniform_from_u64.argtypes = [ctypes.c_uint64]
+        L.ultima_hsamp_status_str.restype = ctypes.c_char_p
+        L.ultima_hsamp_status_str.argtypes = [ctypes.c_int]
+        L.ultima_hsamp_version.restype = ctypes.c_int
+        L.ultima_hsamp_version.argtypes = []
+        _lib = L
+    return _lib
+
+
+class HsampError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        self.status = status
+        super().__init__(f"{what}: {status} ({lib().ultima_hsamp_status_str(status).decode()})")
+
+
+def check(status: int, what: str) -> None:
+    if status != OK:
+        raise HsampError(status, what)
+
+
+def make_params(plist, hist_len=None, bias=None):
+    """(ctypes array of Params, bias ids array, bias values array) for a list of
+    knob dicts. bias: list (per row) of {id: value} or None."""
+    B = len(plist)
+    arr = (Params * B)()
+    ids, vals = [], []
+    for r, p in enumerate(plist):
+        q = arr[r]
+        for k in PARAM_KEYS:
+            setattr(q, k, p[k])
+        q.hist_len = 0 if hist_len is None else int(hist_len[r])
+        q.bias_offset = len(ids)
+        b = bias[r] if bias is not None else None
+        q.bias_count = 0 if not b else len(b)
+        if b:
+            for t, v in b.items():
+                ids.append(int(t))
+                vals.append(float(v))
+    bids = np.array(ids, np.int32) if ids else None
+    bvals = np.array(vals, np.float32) if vals else None
+    return arr, bids, bvals
+
+
+class Sampler:
+    """A handle on one device (create/destroy of the C ABI)."""
+
+    def __init__(self, device: int = 0, max_rows: int = 1024, max_vocab: int = 1 << 18):
+        self.device = device
+        h = ctypes.c_void_p()
+        check(lib().ultima_hsamp_create(device, max_rows, max_vocab, ctypes.byref(h)), "create")
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().ultima_hsamp_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def run(self, logits, params, u, hist=None, hist_len=None, mask=None, bias=None,
+            writeback=False, want_sets=False, set_cap=None, stream=None, outputs=None):
+        """Sample every row. logits: cuda tensor [B, >=V] float32 or bfloat16
+        (row stride = logits.stride(0)); u: cuda float64 [B]; hist: cuda int32
+        [B, H]; mask: cuda int32/uint32 [B, W]. Returns a dict of cuda tensors.
+        `outputs` may carry preallocated tensors (token, row_flags, ...)."""
+        import torch
+        B, V = logits.shape[0], logits.shape[1]
+        dev = logits.device
+        out = outputs if outputs is not None else {}
+        if "token" not in out:
+            out["token"] = torch.empty(B, dtype=torch.int32, device=dev)
+        if "row_flags" not in out:
+            out["row_flags"] = torch.empty(B, dtype=torch.int32, device=dev)
+        cap = 0
+        if want_sets:
+            cap = set_cap or V
+            for k, dt in (("topk_idx", torch.int32), ("kept_idx", torch.int32),
+                          ("kept_prob", torch.float32)):
+                if k not in out:
+                    out[k] = torch.empty((B, cap), dtype=dt, device=dev)
+            for k in ("topk_count", "kept_count"):
+                if k not in out:
+                    out[k] = torch.empty(B, dtype=torch.int32, device=dev)
+        parr, bids, bvals = make_params(params, hist_len, bias)
+        b = Batch()
+        b.rows, b.vocab = B, V
+        b.dtype = F32 if logits.dtype == torch.float32 else BF16
+        b.flags = WRITEBACK if writeback else 0
+        b.logits = logits.data_ptr()
+        b.logits_stride = logits.stride(0)
+        if hist is not None:
+            b.hist = hist.data_ptr()
+            b.hist_stride = hist.stride(0)
+        if mask is not None:
+            b.mask = mask.data_ptr()
+            b.mask_stride = mask.stride(0)
+        b.u = u.data_ptr()
+        b.params = ctypes.cast(parr, ctypes.POINTER(Params))
+        if bids is not None:
+            b.bias_ids = bids.ctypes.data
+            b.bias_vals = bvals.ctypes.data
+        b.token = out["token"].data_ptr()
+        b.row_flags = out["row_flags"].data_ptr()
+        if want_sets:
+            b.topk_idx = out["topk_idx"].data_ptr()
+            b.topk_count = out["topk_count"].data_ptr()
+            b.kept_idx = out["kept_idx"].data_ptr()
+            b.kept_prob = out["kept_prob"].data_ptr()
+            b.kept_count = out["kept_count"].data_ptr()
+            b.set_cap = cap
+        s = torch.cuda.current_stream(dev) if stream is None else stream
+        check(lib().ultima_hsamp_run(self.h, ctypes.byref(b), ctypes.c_void_p(s.cuda_stream)), "run")
+        return out
+
+    def sample_host(self, logits: np.ndarray, params: dict, hist=None, bias=None, u: float = 0.5,
+                    writeback: bool = False):
+        """One host row (sample() with an explicit uniform). Returns (token, logits)."""
+        x = np.array(logits, dtype=np.float32, copy=True)
+        h = None if hist is None else np.ascontiguousarray(hist, dtype=np.int32)
+        parr, bids, bvals = make_params([params], [0 if h is None else h.size], [bias] if bias else None)
+        tok = ctypes.c_int32(-1)
+        check(lib().ultima_hsamp_sample_host(
+            self.h, x.ctypes.data, x.size, parr, None if h is None else h.ctypes.data,
+            None if bids is None else bids.ctypes.data, None if bvals is None else bvals.ctypes.data,
+            float(u), 1 if writeback else 0, ctypes.byref(tok)), "sample_host")
+        return int(tok.value), x

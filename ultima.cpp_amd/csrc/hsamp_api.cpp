@@ -11,6 +11,8 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -23,7 +25,6 @@
 namespace hsamp {
 hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, int grid, hipStream_t stream);
 hipError_t launch_writeback(const StreamArgs& a, int grid, uint32_t lds, hipStream_t stream);
-hipError_t set_kernel_attrs();
 }  // namespace hsamp
 
 using namespace hsamp;
@@ -57,6 +58,7 @@ struct ultima_hsamp {
     int device = 0;
     int32_t max_rows = 0;
     int32_t max_vocab = 0;
+    size_t lds_limit = 0;         // LDS bytes one block may use on this device
     hipStream_t own_stream = nullptr;
     Slot slots[kSlots];
     int next_slot = 0;
@@ -85,14 +87,21 @@ struct ultima_hsamp {
 
 namespace {
 
-int hip_fail(hipError_t e) {
+// ULTIMA_HSAMP_DEBUG=1 prints each failing HIP call to stderr.
+int hip_fail(hipError_t e, const char* what, int line) {
+    static const bool debug = [] {
+        const char* v = std::getenv("ULTIMA_HSAMP_DEBUG");
+        return v != nullptr && v[0] == '1';
+    }();
+    if (debug) std::fprintf(stderr, "ultima_hsamp: %s failed (%s) at hsamp_api.cpp:%d\n", what,
+                            hipGetErrorString(e), line);
     (void)hipGetLastError();
     return e == hipErrorOutOfMemory ? ULTIMA_HSAMP_ERR_NOMEM : ULTIMA_HSAMP_ERR_HIP;
 }
-#define HIP_TRY(x)                              \
-    do {                                        \
-        hipError_t e_ = (x);                    \
-        if (e_ != hipSuccess) return hip_fail(e_); \
+#define HIP_TRY(x)                                                   \
+    do {                                                             \
+        hipError_t e_ = (x);                                         \
+        if (e_ != hipSuccess) return hip_fail(e_, #x, __LINE__);     \
     } while (0)
 
 bool isnan_f(float x) { return x != x; }
@@ -368,23 +377,28 @@ int ultima_hsamp_create(int device, int32_t max_rows, int32_t max_vocab, ultima_
     if (max_rows < 1 || max_vocab < 1) return ULTIMA_HSAMP_ERR_INVALID;
     if (max_vocab > ULTIMA_HSAMP_MAX_VOCAB) return ULTIMA_HSAMP_ERR_CAPACITY;
     int ndev = 0;
-    if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev) {
-        (void)hipGetLastError();
+    const hipError_t ce = hipGetDeviceCount(&ndev);
+    if (ce != hipSuccess || device < 0 || device >= ndev) {
+        hip_fail(ce, "hipGetDeviceCount / device index", __LINE__);
         return ULTIMA_HSAMP_ERR_NO_DEVICE;
     }
     hipDeviceProp_t prop;
-    if (hipGetDeviceProperties(&prop, device) != hipSuccess) return ULTIMA_HSAMP_ERR_NO_DEVICE;
-    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return ULTIMA_HSAMP_ERR_NO_DEVICE;
+    const hipError_t pe = hipGetDeviceProperties(&prop, device);
+    if (pe != hipSuccess) {
+        hip_fail(pe, "hipGetDeviceProperties", __LINE__);
+        return ULTIMA_HSAMP_ERR_NO_DEVICE;
+    }
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        hip_fail(hipErrorInvalidDevice, prop.gcnArchName, __LINE__);
+        return ULTIMA_HSAMP_ERR_NO_DEVICE;
+    }
     HIP_TRY(hipSetDevice(device));
-    static std::once_flag attrs_once;
-    static hipError_t attrs_err = hipSuccess;
-    std::call_once(attrs_once, [] { attrs_err = set_kernel_attrs(); });
-    HIP_TRY(attrs_err);
 
     auto* h = new ultima_hsamp();
     h->device = device;
     h->max_rows = max_rows;
     h->max_vocab = max_vocab;
+    h->lds_limit = prop.sharedMemPerBlock;
     auto fail = [&](int st) {
         ultima_hsamp_destroy(h);
         return st;
@@ -392,7 +406,7 @@ int ultima_hsamp_create(int device, int32_t max_rows, int32_t max_vocab, ultima_
 #define CREATE_TRY(x)                                   \
     do {                                                \
         hipError_t e_ = (x);                            \
-        if (e_ != hipSuccess) return fail(hip_fail(e_)); \
+        if (e_ != hipSuccess) return fail(hip_fail(e_, #x, __LINE__)); \
     } while (0)
     CREATE_TRY(hipStreamCreateWithFlags(&h->own_stream, hipStreamNonBlocking));
     for (auto& s : h->slots) CREATE_TRY(hipEventCreateWithFlags(&s.ev, hipEventDisableTiming));
@@ -466,7 +480,7 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     const size_t regionA = 4 * (size_t)((bitmap_words + 3) & ~3) + 8 * (size_t)hash_slots;
     const size_t regionF = 8 * (size_t)next_pow2(kmax) + 20 * (size_t)kmax;
     const size_t lds = align16(std::max(regionA, regionF)) + 8 * (size_t)buf_cap;
-    if (lds > 160 * 1024) return ULTIMA_HSAMP_ERR_CAPACITY;
+    if (lds + 4096 > h->lds_limit) return ULTIMA_HSAMP_ERR_CAPACITY;   // + static LDS
     if ((size_t)B * S * cand_cap > h->cand_elems) return ULTIMA_HSAMP_ERR_CAPACITY;
     const int nblocks = B * S;
     const int grid = (nblocks + kXcds - 1) / kXcds * kXcds;

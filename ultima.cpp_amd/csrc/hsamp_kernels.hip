@@ -1005,23 +1005,4 @@ hipError_t launch_writeback(const StreamArgs& a, int grid, uint32_t lds, hipStre
     return hipGetLastError();
 }
 
-hipError_t set_kernel_attrs() {
-    hipError_t e = hipSuccess;
-    const int maxlds = 160 * 1024;
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_stream<0, true>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, maxlds);
-    if (e != hipSuccess) return e;
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_stream<0, false>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, maxlds);
-    if (e != hipSuccess) return e;
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_stream<1, true>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, maxlds);
-    if (e != hipSuccess) return e;
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_stream<1, false>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, maxlds);
-    if (e != hipSuccess) return e;
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(&k_writeback<true>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, maxlds);
-}
-
 }  // namespace hsamp

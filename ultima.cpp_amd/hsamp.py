@@ -83,10 +83,17 @@ _lib = None
 
 
 def lib() -> ctypes.CDLL:
+    """Load libultima_hsamp.so. PyTorch-ROCm ships its own HIP runtime with the
+    same SONAME as ROCm's; importing torch first makes the library bind to that
+    one instance, since one process cannot hold two HSA runtimes."""
     global _lib
     if _lib is None:
         if not LIB_PATH.exists():
             raise RuntimeError(f"{LIB_PATH} is not built: run __graft_entry__.build()")
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = ctypes.CDLL(str(LIB_PATH))
         vp, i32, i64, f64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_double
         L.ultima_hsamp_create.restype = ctypes.c_int

@@ -5,7 +5,8 @@
 // penalty tables and the sorted logit-bias entries into one blob, uploads the
 // blob through a small ring of pinned staging buffers (skipped when the same
 // blob is already resident), picks the slicing of the vocabulary and launches
-// the stream kernel on the caller's stream.
+// the stream kernel (one block per row slice) and the merge kernel (one block
+// per row) on the caller's stream.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -25,6 +26,7 @@
 namespace hsamp {
 hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, int grid, hipStream_t stream);
 hipError_t launch_writeback(const StreamArgs& a, int grid, uint32_t lds, hipStream_t stream);
+hipError_t launch_merge(const StreamArgs& a, hipStream_t stream);
 }  // namespace hsamp
 
 using namespace hsamp;
@@ -33,7 +35,8 @@ namespace {
 
 constexpr int kSlots = 4;
 constexpr int kTile = kBlock * 32;      // elements one block streams per tile
-constexpr int kTargetBlocks = 2048;     // blocks a launch aims for (8 per CU)
+constexpr int kTargetBlocks = 4096;     // most blocks a launch spreads rows over
+constexpr int kMergeRound = kBlock * 8; // candidates k_merge offers per round
 
 struct Slot {
     char* host = nullptr;   // pinned
@@ -68,7 +71,11 @@ struct ultima_hsamp {
     unsigned long long* cand = nullptr;
     size_t cand_elems = 0;
     int32_t* cand_n = nullptr;
-    uint32_t* counters = nullptr;
+    int32_t* pend_n = nullptr;
+    unsigned long long* pend = nullptr;  // per-block raw logits of penalised ids
+    size_t pend_elems = 0;
+    uint32_t* gtab = nullptr;            // per-row penalty tables too large for LDS
+    size_t gtab_words = 0;
     int32_t* fin_idx = nullptr;
     int32_t* fin_n = nullptr;
     unsigned long long* ovf = nullptr;   // per-block overflow of the LDS candidate buffer
@@ -410,14 +417,10 @@ int ultima_hsamp_create(int device, int32_t max_rows, int32_t max_vocab, ultima_
     } while (0)
     CREATE_TRY(hipStreamCreateWithFlags(&h->own_stream, hipStreamNonBlocking));
     for (auto& s : h->slots) CREATE_TRY(hipEventCreateWithFlags(&s.ev, hipEventDisableTiming));
-    // Candidates: rows * slices <= max(kTargetBlocks, max_rows) blocks, each
-    // leaving at most 2 * kLimitK entries.
+    // Per-slice counts: rows * slices <= max(kTargetBlocks, max_rows) blocks.
     const size_t blocks = std::max<size_t>(kTargetBlocks + 8, (size_t)max_rows);
-    h->cand_elems = blocks * 2 * kLimitK;
-    CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->cand), h->cand_elems * 8));
     CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->cand_n), blocks * 4));
-    CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->counters), (size_t)max_rows * 4));
-    CREATE_TRY(hipMemset(h->counters, 0, (size_t)max_rows * 4));
+    CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->pend_n), blocks * 4));
     CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->fin_idx), (size_t)max_rows * kLimitK * 4));
     CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->fin_n), (size_t)max_rows * 4));
     CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_row), (size_t)max_vocab * 4 + 64));
@@ -442,7 +445,8 @@ int ultima_hsamp_destroy(ultima_hsamp* h) {
         if (s.dev) (void)hipFree(s.dev);
         if (s.ev) (void)hipEventDestroy(s.ev);
     }
-    for (void* p : {(void*)h->ovf, (void*)h->cand, (void*)h->cand_n, (void*)h->counters, (void*)h->fin_idx,
+    for (void* p : {(void*)h->ovf, (void*)h->cand, (void*)h->cand_n, (void*)h->pend_n, (void*)h->pend,
+                    (void*)h->gtab, (void*)h->fin_idx,
                     (void*)h->fin_n, (void*)h->d_row, (void*)h->d_hist, (void*)h->d_u, (void*)h->d_tok})
         if (p) (void)hipFree(p);
     for (void* p : {(void*)h->h_row, (void*)h->h_hist, (void*)h->h_u, (void*)h->h_tok})
@@ -469,36 +473,55 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     // Slicing: enough blocks to fill 256 CUs, slices of at most one tile.
     const int tiles = (V + kTile - 1) / kTile;
     int S = std::max(1, std::min({kTargetBlocks / B, tiles, kBlock}));
+    if (const char* fs = std::getenv("ULTIMA_HSAMP_SLICES")) S = std::max(1, std::min(std::atoi(fs), kBlock));
     int slice_len = ((V + S - 1) / S + 31) & ~31;
     S = (V + slice_len - 1) / slice_len;
     const int kmax = std::max(1, bl.kmax);
     const int buf_cap = std::max(512, next_pow2(2 * kmax));
-    const int cand_cap = std::max(2, std::min(buf_cap, 4 * kmax));
-    int hash_slots = 0;
-    if (bl.any_pen) hash_slots = std::max(16, next_pow2(std::min(bl.max_pen, slice_len)));
+    const int cand_cap = slice_len;                 // a slice's list holds all its ids
     const int bitmap_words = slice_len / 32;
-    const size_t regionA = 4 * (size_t)((bitmap_words + 3) & ~3) + 8 * (size_t)hash_slots;
+    const size_t statik = 4096;                     // static LDS of the kernels, rounded up
+    // k_stream: [penalised-id bitmap] [allowed-id mask words]
+    const size_t lds = align16(8 * (size_t)bitmap_words);
+    if (lds + statik > h->lds_limit) return ULTIMA_HSAMP_ERR_CAPACITY;
+    // k_merge: [penalty table | finalize scratch] [candidate buffer]; the
+    // table (load factor <= 1/2) moves to global memory when it does not fit.
     const size_t regionF = 8 * (size_t)next_pow2(kmax) + 20 * (size_t)kmax;
-    const size_t lds = align16(std::max(regionA, regionF)) + 8 * (size_t)buf_cap;
-    if (lds + 4096 > h->lds_limit) return ULTIMA_HSAMP_ERR_CAPACITY;   // + static LDS
-    if ((size_t)B * S * cand_cap > h->cand_elems) return ULTIMA_HSAMP_ERR_CAPACITY;
+    const int mhash = bl.any_pen ? std::max(16, next_pow2(2 * bl.max_pen)) : 16;
+    const size_t lds_budget = std::min<size_t>(h->lds_limit, 64 * 1024) - statik;
+    const bool gtab = 8 * (size_t)mhash + 8 * (size_t)buf_cap > lds_budget ||
+                      8 * (size_t)mhash + 4 * (size_t)bitmap_words > lds_budget;
+    const size_t merge_lds = align16(std::max(gtab ? 0 : 8 * (size_t)mhash, regionF)) + 8 * (size_t)buf_cap;
+    const size_t wb_lds = (gtab ? 0 : 8 * (size_t)mhash) + 4 * (size_t)bitmap_words;
+    if (merge_lds + statik > h->lds_limit || wb_lds + statik > h->lds_limit) return ULTIMA_HSAMP_ERR_CAPACITY;
     const int nblocks = B * S;
     const int grid = (nblocks + kXcds - 1) / kXcds * kXcds;
+    const int pend_cap = bl.any_pen ? std::min(slice_len, bl.max_pen) : 0;
 
     hipStreamCaptureStatus cap_status = hipStreamCaptureStatusNone;
     HIP_TRY(hipStreamIsCapturing(stream, &cap_status));
     const bool capturing = cap_status != hipStreamCaptureStatusNone;
-    const size_t ovf_need = (size_t)grid * kTile;
-    if (ovf_need > h->ovf_elems) {
+    // grow-only scratch; the device must be idle before an old area goes away
+    auto grow = [&](auto*& ptr, size_t& have, size_t need, size_t elem) -> int {
+        if (need <= have) return ULTIMA_HSAMP_OK;
         if (capturing) return ULTIMA_HSAMP_ERR_UNSUPPORTED;   // run once before capturing
-        // grow-only; the device must be idle before the old area goes away
         HIP_TRY(hipDeviceSynchronize());
-        if (h->ovf) HIP_TRY(hipFree(h->ovf));
-        h->ovf = nullptr;
-        h->ovf_elems = 0;
-        HIP_TRY(hipMalloc(reinterpret_cast<void**>(&h->ovf), ovf_need * 8));
-        h->ovf_elems = ovf_need;
-    }
+        if (ptr) HIP_TRY(hipFree(ptr));
+        ptr = nullptr;
+        have = 0;
+        if (hipMalloc(reinterpret_cast<void**>(&ptr), need * elem) != hipSuccess) {
+            (void)hipGetLastError();
+            ptr = nullptr;
+            return ULTIMA_HSAMP_ERR_NOMEM;
+        }
+        have = need;
+        return ULTIMA_HSAMP_OK;
+    };
+    st = grow(h->ovf, h->ovf_elems, (size_t)B * kMergeRound, 8);
+    if (st == ULTIMA_HSAMP_OK) st = grow(h->cand, h->cand_elems, (size_t)B * S * cand_cap, 8);
+    if (st == ULTIMA_HSAMP_OK) st = grow(h->pend, h->pend_elems, std::max<size_t>(1, (size_t)grid * pend_cap), 8);
+    if (st == ULTIMA_HSAMP_OK && gtab) st = grow(h->gtab, h->gtab_words, (size_t)B * 2 * mhash, 4);
+    if (st != ULTIMA_HSAMP_OK) return st;
 
     Slot* slot = nullptr;
     st = upload_blob(h, stream, capturing, slot);
@@ -531,15 +554,19 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     a.kmax = kmax;
     a.cand_cap = cand_cap;
     a.buf_cap = buf_cap;
-    a.hash_slots = hash_slots;
+    a.mhash_slots = mhash;
     a.bitmap_words = bitmap_words;
     a.blocks_per_xcd = grid / kXcds;
     a.fin_cap = kLimitK;
     a.ovf = h->ovf;
-    a.ovf_cap = kTile;
+    a.ovf_cap = kMergeRound;
     a.cand = h->cand;
     a.cand_n = h->cand_n;
-    a.counters = h->counters;
+    a.pend = h->pend;
+    a.pend_n = h->pend_n;
+    a.pend_cap = pend_cap;
+    a.gtab = gtab ? h->gtab : nullptr;
+    a.merge_lds = (uint32_t)merge_lds;
     const bool wb = (b->flags & ULTIMA_HSAMP_WRITEBACK) != 0;
     a.fin_idx = wb ? h->fin_idx : nullptr;
     a.fin_n = wb ? h->fin_n : nullptr;
@@ -547,10 +574,8 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     const bool vec = (reinterpret_cast<uintptr_t>(b->logits) % 16 == 0) &&
                      ((b->logits_stride * es) % 16 == 0);
     HIP_TRY(launch_stream(a, b->dtype, vec, grid, stream));
-    if (wb) {
-        const uint32_t wlds = (uint32_t)(regionA + 4 * (size_t)bitmap_words + 16);
-        HIP_TRY(launch_writeback(a, grid, wlds, stream));
-    }
+    HIP_TRY(launch_merge(a, stream));
+    if (wb) HIP_TRY(launch_writeback(a, grid, (uint32_t)wb_lds, stream));
     if (!capturing) HIP_TRY(hipEventRecord(slot->ev, stream));
     return ULTIMA_HSAMP_OK;
 }

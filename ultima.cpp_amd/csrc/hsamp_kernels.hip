@@ -67,10 +67,13 @@ struct Shared {
     float fred[4];
     int ired[4];
     u64 ured[4];
+    u64 minv_w[4];
     uint32_t hist[256];
     int soff[257];      // slice offsets during the merge
     int flags;
     int nan0;
+    int npend;          // penalised ids set aside in the stream
+    alignas(16) u64 wv[64];  // the finishing wave's cross-lane scratch
     float sm_m, sm_inv;
     int cutoff;
     double dS;
@@ -149,91 +152,122 @@ __device__ __forceinline__ uint32_t wave_kth_largest(const uint32_t (&g)[4], int
     return prefix;
 }
 
-// k-th largest (1 <= k <= n) of n distinct composites in buf, by 8-bit radix
-// passes from the top with early exit.
-__device__ __attribute__((noinline)) u64 block_select_kth(const u64* buf, int n, int k, Shared& st) {
-    u64 prefix = 0, pmask = 0;
-    int need = k;
-    const int tid = threadIdx.x;
-    for (int shift = 56; shift >= 0; shift -= 8) {
-        st.hist[tid] = 0u;
-        if (tid == 0) st.minv = ~0ull;
-        __syncthreads();
-        for (int i = tid; i < n; i += kBlock) {
-            const u64 v = buf[i];
-            if ((v & pmask) == prefix) atomicAdd(&st.hist[(uint32_t)(v >> shift) & 255u], 1u);
+__device__ __forceinline__ u64 shfl_xor_u64(u64 v, int m) {
+    return (u64)__shfl_xor((long long)v, m, 64);
+}
+
+// Keep the k largest of the buffer's n = st.n distinct composites (exactly
+// k), and raise the threshold to the k-th. The entries are held in registers
+// (n <= 16 * 256); the k-th is found by 8-bit radix passes that start below
+// the bits all entries share, and stop as soon as the digit's bucket is
+// exactly what is still needed.
+__device__ __attribute__((noinline)) void buf_compact(u64* buf, int k, Shared& st) {
+    const int n = st.n;
+    if (n <= k) return;
+    constexpr int MAXE = 16;
+    const int tid = threadIdx.x, lane = lane_id();
+    u64 v[MAXE];
+    u64 lo = ~0ull, hi = 0ull;
+#pragma unroll
+    for (int m = 0; m < MAXE; ++m) {
+        const int i = tid + m * kBlock;
+        v[m] = (i < n) ? buf[i] : 0ull;
+        if (i < n) {
+            lo = v[m] < lo ? v[m] : lo;
+            hi = v[m] > hi ? v[m] : hi;
         }
+    }
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) {
+        const u64 a2 = shfl_xor_u64(lo, d), b2 = shfl_xor_u64(hi, d);
+        lo = a2 < lo ? a2 : lo;
+        hi = b2 > hi ? b2 : hi;
+    }
+    if (lane == 0) {
+        st.ured[wave_id()] = lo;
+        st.minv_w[wave_id()] = hi;
+    }
+    __syncthreads();
+    lo = st.ured[0];
+    hi = st.minv_w[0];
+#pragma unroll
+    for (int i = 1; i < kBlock / 64; ++i) {
+        lo = st.ured[i] < lo ? st.ured[i] : lo;
+        hi = st.minv_w[i] > hi ? st.minv_w[i] : hi;
+    }
+    const int hb = 63 - __clzll((long long)(lo ^ hi));   // highest differing bit (n >= 2)
+    u64 pmask = (hb >= 63) ? 0ull : ~((2ull << hb) - 1ull);
+    u64 prefix = hi & pmask;
+    int need = k;
+    u64 kth = 0ull;
+    bool done = false;
+    for (int shift = hb >= 7 ? hb - 7 : 0;; ) {
+        st.hist[tid] = 0u;
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < MAXE; ++m)
+            if (tid + m * kBlock < n && (v[m] & pmask) == prefix)
+                atomicAdd(&st.hist[(uint32_t)(v[m] >> shift) & 255u], 1u);
         __syncthreads();
         if (tid < 64) {
-            const int l = tid;
-            const int c0 = st.hist[255 - 4 * l], c1 = st.hist[254 - 4 * l];
-            const int c2 = st.hist[253 - 4 * l], c3 = st.hist[252 - 4 * l];
+            const int c0 = st.hist[255 - 4 * lane], c1 = st.hist[254 - 4 * lane];
+            const int c2 = st.hist[253 - 4 * lane], c3 = st.hist[252 - 4 * lane];
             const int s4 = c0 + c1 + c2 + c3;
             int incl = s4;
 #pragma unroll
             for (int d = 1; d < 64; d <<= 1) {
                 const int y = __shfl_up(incl, d, 64);
-                if (l >= d) incl += y;
+                if (lane >= d) incl += y;
             }
             const int excl = incl - s4;
             const bool mine = excl < need && need <= incl;
             const u64 bal = __ballot(mine);
-            if (mine && (int)(__ffsll((long long)bal) - 1) == l) {
-                int cum = excl;
-                const int cs[4] = {c0, c1, c2, c3};
-                for (int q = 0; q < 4; ++q) {
-                    if (cum + cs[q] >= need) {
-                        st.sel_d = 255 - 4 * l - q;
-                        st.sel_need = need - cum;
-                        st.sel_cnt = cs[q];
-                        break;
-                    }
-                    cum += cs[q];
-                }
+            if (mine && (int)(__ffsll((long long)bal) - 1) == lane) {
+                int q, cnt, before;
+                if (excl + c0 >= need) { q = 0; cnt = c0; before = excl; }
+                else if (excl + c0 + c1 >= need) { q = 1; cnt = c1; before = excl + c0; }
+                else if (excl + c0 + c1 + c2 >= need) { q = 2; cnt = c2; before = excl + c0 + c1; }
+                else { q = 3; cnt = c3; before = excl + c0 + c1 + c2; }
+                st.sel_d = 255 - 4 * lane - q;
+                st.sel_need = need - before;
+                st.sel_cnt = cnt;
             }
         }
         __syncthreads();
-        const int d = st.sel_d, cnt = st.sel_cnt;
+        const int dgt = st.sel_d, cnt = st.sel_cnt;
         need = st.sel_need;
-        prefix |= (u64)d << shift;
+        prefix = (prefix & ~((u64)0xFF << shift)) | ((u64)dgt << shift);
         pmask |= (u64)0xFF << shift;
-        if (cnt == need) {
-            for (int i = tid; i < n; i += kBlock) {
-                const u64 v = buf[i];
-                if ((v & pmask) == prefix) atomicMin(&st.minv, v);
+        if (cnt == need || shift == 0) {
+            // every entry under this prefix is in: the k-th is their minimum
+            u64 mn = ~0ull;
+#pragma unroll
+            for (int m = 0; m < MAXE; ++m)
+                if (tid + m * kBlock < n && (v[m] & pmask) == prefix && v[m] < mn) mn = v[m];
+#pragma unroll
+            for (int d = 32; d > 0; d >>= 1) {
+                const u64 o = shfl_xor_u64(mn, d);
+                mn = o < mn ? o : mn;
             }
+            if (lane == 0) st.ured[wave_id()] = mn;
             __syncthreads();
-            const u64 r = st.minv;
-            __syncthreads();
-            return r;
+            kth = st.ured[0];
+#pragma unroll
+            for (int i = 1; i < kBlock / 64; ++i) kth = st.ured[i] < kth ? st.ured[i] : kth;
+            done = true;
         }
         __syncthreads();
+        if (done) break;
+        shift = shift >= 8 ? shift - 8 : 0;
     }
-    return prefix;
-}
-
-// Keep the k largest of the buffer's entries (exactly k; they are distinct).
-__device__ __attribute__((noinline)) void buf_compact(u64* buf, int k, Shared& st) {
-    const int n = st.n;
-    if (n <= k) return;
-    const u64 kth = block_select_kth(buf, n, k, st);
-    constexpr int MAXE = 16;  // buf_cap <= 4096
-    u64 v[MAXE];
     int cnt = 0;
-    const int tid = threadIdx.x;
 #pragma unroll
-    for (int m = 0; m < MAXE; ++m) {
-        const int i = tid + m * kBlock;
-        v[m] = (i < n) ? buf[i] : 0ull;
-        cnt += (i < n && v[m] >= kth) ? 1 : 0;
-    }
+    for (int m = 0; m < MAXE; ++m) cnt += (tid + m * kBlock < n && v[m] >= kth) ? 1 : 0;
     int total;
-    int pos = block_excl_scan(cnt, &total, st);  // syncs: every read above is done
+    int pos = block_excl_scan(cnt, &total, st);
 #pragma unroll
-    for (int m = 0; m < MAXE; ++m) {
-        const int i = tid + m * kBlock;
-        if (i < n && v[m] >= kth) buf[pos++] = v[m];
-    }
+    for (int m = 0; m < MAXE; ++m)
+        if (tid + m * kBlock < n && v[m] >= kth) buf[pos++] = v[m];
     __syncthreads();
     if (tid == 0) {
         st.n = total;
@@ -244,31 +278,45 @@ __device__ __attribute__((noinline)) void buf_compact(u64* buf, int k, Shared& s
 
 // Offer register-held candidates to the LDS buffer. Slot i of every thread
 // holds an order key kv[i] (0 = empty) of id idx(i); it survives when its
-// composite is >= the threshold. Survivors reserve entries with one LDS atomic
-// per wave and slot; entries past the buffer's capacity go to the block's
-// global overflow area `ovf` (drained by drain_overflow).
+// composite is >= the threshold. Each lane counts its survivors, the wave
+// reserves one contiguous range with a single LDS atomic, and each lane writes
+// its survivors in slot order; entries past the buffer's capacity go to the
+// block's global overflow area `ovf` (drained by drain_overflow).
 template <int NE, typename Idx>
 __device__ __forceinline__ void append_regs(u64* buf, int cap, const uint32_t (&kv)[NE], Idx idx,
                                             u64* ovf, Shared& st) {
+    static_assert(NE <= 32, "survivor mask is 32 bits");
     const int lane = lane_id();
     const u64 th = st.theta;
     const uint32_t thk = (uint32_t)(th >> 32);
     const uint32_t thi = ~(uint32_t)th;   // largest index that survives a tie on thk
+    uint32_t sv = 0u;
 #pragma unroll
     for (int i = 0; i < NE; ++i) {
         const uint32_t key = kv[i];
-        const bool sv = key > thk || (key == thk && (uint32_t)idx(i) <= thi);
-        const u64 bal = __ballot(sv);
-        if (bal == 0ull) continue;
-        const int leader = __ffsll((long long)bal) - 1;
-        int base = 0;
-        if (lane == leader) base = atomicAdd(&st.n, __popcll(bal));
-        base = __shfl(base, leader, 64);
-        if (sv) {
-            const int pos = base + __popcll(bal & ((1ull << lane) - 1ull));
-            const u64 c = comp(key, idx(i));
+        const bool ok = key > thk || (key == thk && (uint32_t)idx(i) <= thi);
+        sv |= ok ? (1u << i) : 0u;
+    }
+    const int cnt = __popc(sv);
+    int incl = cnt;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += y;
+    }
+    const int wtot = __shfl(incl, 63, 64);
+    if (wtot == 0) return;
+    int base = 0;
+    if (lane == 63) base = atomicAdd(&st.n, wtot);
+    base = __shfl(base, 63, 64);
+    int pos = base + incl - cnt;
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+        if ((sv >> i) & 1u) {
+            const u64 c = comp(kv[i], idx(i));
             if (pos < cap) buf[pos] = c;
             else ovf[pos - cap] = c;
+            ++pos;
         }
     }
 }
@@ -342,19 +390,35 @@ __device__ __forceinline__ int next_pow2(int x) {
 
 // ---- penalty bookkeeping -----------------------------------------------------
 
+// The row's penalty table, open addressing over mhash_slots keys and values,
+// in LDS or (for windows too large for LDS) in the row's global area. Reads go
+// through agent-scope atomic loads, which are plain LDS reads for LDS and bypass
+// the vector L1 for global memory, where the table was filled by atomics.
 struct PenaltyLds {
-    uint32_t* bitmap;   // bit (t - lo): t has an entry in the table
     uint32_t* hkey;
     uint32_t* hval;
     uint32_t hmask;
     uint32_t hshift;
 };
 
-__device__ __forceinline__ uint32_t hslot(int32_t t, const PenaltyLds& pl) {
+__device__ __forceinline__ uint32_t tab_ld(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ PenaltyLds pen_table(const StreamArgs& a, int r, unsigned char* smem) {
+    PenaltyLds pl;
+    pl.hkey = (a.gtab != nullptr) ? a.gtab + (int64_t)r * 2 * a.mhash_slots : reinterpret_cast<uint32_t*>(smem);
+    pl.hval = pl.hkey + a.mhash_slots;
+    pl.hmask = (uint32_t)a.mhash_slots - 1u;
+    pl.hshift = 32u - (uint32_t)__popc(pl.hmask);
+    return pl;
+}
+
+__device__ __forceinline__ uint32_t hslot(int32_t t, PenaltyLds pl) {
     return ((uint32_t)t * 0x9E3779B1u) >> pl.hshift;
 }
 
-__device__ uint32_t pen_insert(int32_t t, const PenaltyLds& pl) {
+__device__ uint32_t pen_insert(int32_t t, PenaltyLds pl) {
     uint32_t s = hslot(t, pl);
     for (;;) {
         const uint32_t old = atomicCAS(&pl.hkey[s], kEmpty, (uint32_t)t);
@@ -363,48 +427,12 @@ __device__ uint32_t pen_insert(int32_t t, const PenaltyLds& pl) {
     }
 }
 
-// Build the table for ids in [lo, hi) from the row's history suffix and bias.
-__device__ __attribute__((noinline)) void pen_build(const StreamArgs& a, const RowPlan& P, int r, int lo, int hi,
-                          const PenaltyLds& pl) {
-    const int tid = threadIdx.x;
-    for (int i = tid; i < a.bitmap_words; i += kBlock) pl.bitmap[i] = 0u;
-    for (int i = tid; i < a.hash_slots; i += kBlock) {
-        pl.hkey[i] = kEmpty;
-        pl.hval[i] = 0u;
-    }
-    __syncthreads();
-    const int L = P.hist_len;
-    const int32_t* h = a.hist + (int64_t)r * a.hist_stride;
-    for (int p = L - P.scan_len + tid; p < L; p += kBlock) {
-        const int32_t t = h[p];
-        if (t < lo || t >= hi) continue;
-        uint32_t add = 0u, orv = 0u;
-        if (p >= L - P.rep_win) orv |= HV_REP;
-        if (p >= L - P.dry_win) add += 1u << HV_DRY_SHIFT;
-        if (p >= L - P.fp_win) add += 1u;
-        const uint32_t s = pen_insert(t, pl);
-        if (add) atomicAdd(&pl.hval[s], add);
-        if (orv) atomicOr(&pl.hval[s], orv);
-        atomicOr(&pl.bitmap[(t - lo) >> 5], 1u << ((t - lo) & 31));
-    }
-    if (P.flags & RF_BIAS) {
-        for (int j = tid; j < P.bias_cnt; j += kBlock) {
-            const int32_t t = a.bias_ids[P.bias_off + j];
-            if (t < lo || t >= hi) continue;
-            const uint32_t s = pen_insert(t, pl);
-            atomicOr(&pl.hval[s], HV_BIAS);
-            atomicOr(&pl.bitmap[(t - lo) >> 5], 1u << ((t - lo) & 31));
-        }
-    }
-    __syncthreads();
-}
-
 // Stages 1-4 of the ladder for one id with a table entry (sampler.cpp:28-99).
-__device__ __attribute__((noinline)) float pen_apply(float x, int32_t t, const StreamArgs& a,
-                                           const RowPlan& P, const PenaltyLds& pl) {
+__device__ __forceinline__ float pen_apply(float x, int32_t t, const StreamArgs& a, const RowPlan& P,
+                                           PenaltyLds pl) {
     uint32_t s = hslot(t, pl);
-    while (pl.hkey[s] != (uint32_t)t) s = (s + 1) & pl.hmask;
-    const uint32_t v = pl.hval[s];
+    while (tab_ld(&pl.hkey[s]) != (uint32_t)t) s = (s + 1) & pl.hmask;
+    const uint32_t v = tab_ld(&pl.hval[s]);
     if (v & HV_BIAS) {
         int lo = 0, hi = P.bias_cnt;
         const int32_t* ids = a.bias_ids + P.bias_off;
@@ -438,9 +466,7 @@ struct Tile {
 };
 
 template <int DT, bool VEC>
-__device__ __forceinline__ void load_tile(const char* rowp, const uint32_t* mrow, int tb, int hi,
-                                          uint4 (&raw)[Tile<DT>::NCH],
-                                          uint32_t (&mw)[Tile<DT>::NCH]) {
+__device__ __forceinline__ void load_tile(const char* rowp, int tb, int hi, uint4 (&raw)[Tile<DT>::NCH]) {
     using T = Tile<DT>;
 #pragma unroll
     for (int j = 0; j < T::NCH; ++j) {
@@ -448,6 +474,8 @@ __device__ __forceinline__ void load_tile(const char* rowp, const uint32_t* mrow
         if (VEC && e0 + T::VW <= hi) {
             const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rowp + (size_t)e0 * T::ES));
             raw[j] = make_uint4(v.x, v.y, v.z, v.w);
+        } else if (e0 >= hi) {
+            raw[j] = make_uint4(0u, 0u, 0u, 0u);
         } else {
             uint32_t w[4] = {0u, 0u, 0u, 0u};
             for (int c = 0; c < T::VW; ++c) {
@@ -461,7 +489,6 @@ __device__ __forceinline__ void load_tile(const char* rowp, const uint32_t* mrow
             }
             raw[j] = make_uint4(w[0], w[1], w[2], w[3]);
         }
-        mw[j] = (mrow != nullptr && e0 < hi) ? mrow[e0 >> 5] : 0xFFFFFFFFu;
     }
 }
 
@@ -486,7 +513,7 @@ struct FinLds {
 
 // softmax_probs over the kept entries (sampler.cpp:124-142): m, e, float
 // index-order sum, p = e * fl(1/sum). Returns false when nothing is kept.
-__device__ __attribute__((noinline)) bool fin_softmax(const FinLds& f, int nk, Shared& st) {
+__device__ __attribute__((noinline)) bool fin_softmax(FinLds f, int nk, Shared& st) {
     const int tid = threadIdx.x;
     float m = -__builtin_inff();
     for (int j = tid; j < nk; j += kBlock)
@@ -528,8 +555,9 @@ __device__ __attribute__((noinline)) int32_t uniform_draw(int V, double u) {
 }
 
 // The ladder after top-k for one row whose top-k set is buf[0..nk).
-__device__ __attribute__((noinline)) void finalize_row(const StreamArgs& a, const RowPlan& P, int r, const u64* buf, int nk,
-                             const FinLds& f, Shared& st, uint32_t rflags) {
+__device__ __attribute__((noinline)) void finalize_row(const StreamArgs& a, const RowPlan& P, int r,
+                                                       const u64* buf, int nk, FinLds f, Shared& st,
+                                                       uint32_t rflags) {
     const int tid = threadIdx.x;
     const int V = a.vocab;
     const double u = a.u[r];
@@ -700,10 +728,420 @@ __device__ __attribute__((noinline)) void finalize_row(const StreamArgs& a, cons
     }
 }
 
-// ---- the fused stream kernel ---------------------------------------------------
 
+// ---- wave-level finalize (k <= 64) -----------------------------------------------
+// One wave finishes a row whose top-k set fits its 64 lanes. Cross-lane work
+// goes through the wave's 512-byte LDS scratch (Shared::wv): a lane writes its
+// value and every lane then reads all 64 with broadcast loads, so sorts are
+// rank placements and the reference's sequential sums are one unrolled chain
+// of adds per lane, in lane order, with no shuffles or readlanes.
+
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ double readlane_d(double v, int l) {
+    const uint64_t b = f64_to_bits(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+    return bits_to_f64(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ float wave_max_f(float v) {
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) v = fmaxf(v, __shfl_xor(v, d, 64));
+    return v;
+}
+
+// Orders the wave's LDS accesses around a cross-lane exchange. LDS operations
+// of one wave complete in program order; the fences keep the compiler from
+// moving accesses across.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Ascending sort of 64 distinct keys across the lanes (payload travels along).
+__device__ __forceinline__ void wave_sort_asc(uint32_t& key, uint32_t& pay, u64* wv) {
+    const int lane = lane_id();
+    uint32_t* w = reinterpret_cast<uint32_t*>(wv);
+    w[lane] = key;
+    wave_sync();
+    int rank = 0;
+    const uint4* w4 = reinterpret_cast<const uint4*>(w);
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        const uint4 x = w4[q];
+        rank += (x.x < key) + (x.y < key) + (x.z < key) + (x.w < key);
+    }
+    wave_sync();
+    w[rank] = key;
+    w[64 + rank] = pay;
+    wave_sync();
+    key = w[lane];
+    pay = w[64 + lane];
+    wave_sync();
+}
+
+// Descending sort of 64 distinct 64-bit keys across the lanes.
+__device__ __forceinline__ u64 wave_sort_desc(u64 key, u64* wv) {
+    const int lane = lane_id();
+    wv[lane] = key;
+    wave_sync();
+    int rank = 0;
+#pragma unroll
+    for (int q = 0; q < 64; ++q) rank += wv[q] > key;
+    wave_sync();
+    wv[rank] = key;
+    wave_sync();
+    key = wv[lane];
+    wave_sync();
+    return key;
+}
+
+// Lane-order float sum of x over the 64 lanes, starting from +0.0f. Every
+// value must be >= +0 (absent lanes pass +0.0f): the extra +0 terms then leave
+// the index-order sum of the present ones bit for bit.
+__device__ __forceinline__ float wave_seq_sum_f(float x, u64* wv) {
+    float* w = reinterpret_cast<float*>(wv);
+    w[lane_id()] = x;
+    wave_sync();
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    float s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        const float4 v = w4[q];
+        s = s + v.x;
+        s = s + v.y;
+        s = s + v.z;
+        s = s + v.w;
+    }
+    wave_sync();
+    return s;
+}
+
+// Inclusive lane-order prefix of the same sequential float sum: lane l gets
+// the running sum after adding lane l's value.
+__device__ __forceinline__ float wave_seq_prefix_f(float x, u64* wv) {
+    const int lane = lane_id();
+    float* w = reinterpret_cast<float*>(wv);
+    w[lane] = x;
+    wave_sync();
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    float s = 0.0f, mine = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        const float4 v = w4[q];
+        s = s + v.x;
+        mine = (lane == 4 * q) ? s : mine;
+        s = s + v.y;
+        mine = (lane == 4 * q + 1) ? s : mine;
+        s = s + v.z;
+        mine = (lane == 4 * q + 2) ? s : mine;
+        s = s + v.w;
+        mine = (lane == 4 * q + 3) ? s : mine;
+    }
+    wave_sync();
+    return mine;
+}
+
+// The double versions (values >= +0.0).
+__device__ __forceinline__ double wave_seq_sum_d(double x, u64* wv) {
+    double* w = reinterpret_cast<double*>(wv);
+    w[lane_id()] = x;
+    wave_sync();
+    const double2* w2 = reinterpret_cast<const double2*>(w);
+    double s = 0.0;
+#pragma unroll
+    for (int q = 0; q < 32; ++q) {
+        const double2 v = w2[q];
+        s = s + v.x;
+        s = s + v.y;
+    }
+    wave_sync();
+    return s;
+}
+
+__device__ __forceinline__ double wave_seq_prefix_d(double x, u64* wv) {
+    const int lane = lane_id();
+    double* w = reinterpret_cast<double*>(wv);
+    w[lane] = x;
+    wave_sync();
+    const double2* w2 = reinterpret_cast<const double2*>(w);
+    double s = 0.0, mine = 0.0;
+#pragma unroll
+    for (int q = 0; q < 32; ++q) {
+        const double2 v = w2[q];
+        s = s + v.x;
+        mine = (lane == 2 * q) ? s : mine;
+        s = s + v.y;
+        mine = (lane == 2 * q + 1) ? s : mine;
+    }
+    wave_sync();
+    return mine;
+}
+
+// softmax_probs (sampler.cpp:124-142) over the kept lanes of one wave; lanes
+// are in index order. The float denominator is the index-order sequential sum.
+// Returns false when nothing is kept.
+__device__ __forceinline__ bool wave_softmax(float v, bool keep, float& p, u64* wv) {
+    if (__ballot(keep) == 0ull) return false;
+    const float m = wave_max_f(keep ? v : -__builtin_inff());
+    const float e = keep ? libm_expf(v - m) : 0.0f;
+    const float s = wave_seq_sum_f(e, wv);
+    p = keep ? ((s <= 0.0f) ? e : e * (1.0f / s)) : 0.0f;
+    return true;
+}
+
+// Exact top-k (k <= 64) of the n <= 256 distinct nonzero composites buf[0..n)
+// by one wave: the k-th largest composite by an MSB-first bitwise select over
+// ballots (4 entries per lane), starting at the highest bit the entries do not
+// share and stopping once the entries under the prefix are exactly the ones
+// still needed. Lane l < min(k, n) returns one member of the set, any order.
+__device__ __forceinline__ u64 wave_topk(const u64* buf, int n, int k, u64* wv) {
+    const int lane = lane_id();
+    u64 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = (lane + 64 * i < n) ? buf[lane + 64 * i] : 0ull;
+    if (n <= k) return v[0];
+    u64 lo = ~0ull, hi = 0ull;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if (v[i] != 0ull) lo = v[i] < lo ? v[i] : lo;
+        hi = v[i] > hi ? v[i] : hi;
+    }
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) {
+        const u64 a2 = shfl_xor_u64(lo, d), b2 = shfl_xor_u64(hi, d);
+        lo = a2 < lo ? a2 : lo;
+        hi = b2 > hi ? b2 : hi;
+    }
+    const int hb = 63 - __clzll((long long)(lo ^ hi));   // n >= 2 distinct: lo != hi
+    u64 known = (hb >= 63) ? 0ull : ~((2ull << hb) - 1ull);
+    u64 prefix = hi & known;
+    int need = k, match = n;
+    u64 kth = 0ull;
+    bool found = false;
+    for (int b = hb; b >= 0; --b) {
+        const u64 bit = 1ull << b;
+        int cnt = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            cnt += __popcll(__ballot(v[i] != 0ull && (v[i] & known) == prefix && (v[i] & bit) != 0ull));
+        if (cnt >= need) {
+            prefix |= bit;
+            match = cnt;
+        } else {
+            need -= cnt;
+            match -= cnt;
+        }
+        known |= bit;
+        if (match == need) {
+            // every entry under the prefix is in: the k-th is their minimum
+            u64 mn = ~0ull;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (v[i] != 0ull && (v[i] & known) == prefix && v[i] < mn) mn = v[i];
+#pragma unroll
+            for (int d = 32; d > 0; d >>= 1) {
+                const u64 o = shfl_xor_u64(mn, d);
+                mn = o < mn ? o : mn;
+            }
+            kth = mn;
+            found = true;
+            break;
+        }
+    }
+    if (!found) kth = prefix;
+    // the k members, packed into lanes 0..k-1
+    int base = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const bool in = v[i] != 0ull && v[i] >= kth;
+        const u64 bal = __ballot(in);
+        if (in) wv[base + __popcll(bal & ((1ull << lane) - 1ull))] = v[i];
+        base += __popcll(bal);
+    }
+    wave_sync();
+    const u64 c = (lane < k) ? wv[lane] : 0ull;
+    wave_sync();
+    return c;
+}
+
+// The ladder after top-k for one row, by one wave: lane l < nk holds a
+// composite of the row's top-k set (any order), nk <= 64. Same semantics as
+// finalize_row.
+__device__ __attribute__((noinline)) void wave_finalize(const StreamArgs& a, const RowPlan& P, int r, u64 c, int nk,
+                                                        uint32_t rflags, Shared& st) {
+    const int lane = lane_id();
+    const int V = a.vocab;
+    const double u = a.u[r];
+    const bool single = (P.flags & RF_SINGLE) != 0;
+    u64* wv = st.wv;
+    if (!single) rflags |= ROWF_U_USED;
+    // index order; absent lanes carry distinct ids above every token id
+    uint32_t id = (lane < nk) ? (uint32_t)comp_idx(c) : (0x80000000u | (uint32_t)lane);
+    uint32_t vk = (lane < nk) ? (uint32_t)(c >> 32) : 0u;
+    wave_sort_asc(id, vk, wv);
+    const bool has = lane < nk;
+    const float v = key_to_float(vk);
+    if (a.topk_idx != nullptr && has && lane < a.set_cap) a.topk_idx[(int64_t)r * a.set_cap + lane] = (int32_t)id;
+    if (a.topk_count != nullptr && lane == 0) a.topk_count[r] = single ? -1 : nk;
+    bool keep = has;
+    float p = 0.0f;
+    bool have = nk > 0 && wave_softmax(v, keep, p, wv);
+    bool fresh = true;
+    if (have && (P.flags & RF_TOPP)) {
+        // sampler.cpp:146-164: order by (p desc, index asc), float running sum;
+        // absent lanes sort last with keys below 2^32
+        const u64 key = keep ? (((u64)key32(p) << 32) | (u64)(0xFFFFFFFFu - (uint32_t)lane)) : (u64)lane;
+        const u64 srt = wave_sort_desc(key, wv);
+        const bool real = srt > 0xFFFFFFFFull;
+        const float ps = real ? key_to_float((uint32_t)(srt >> 32)) : 0.0f;
+        const float cum = wave_seq_prefix_f(ps, wv);
+        const u64 hit = __ballot(real && cum >= P.top_p);
+        if (hit != 0ull) {
+            const int cutoff = __ffsll((long long)hit);   // entries kept in sorted order
+            if (fabsf(readlane_f(cum, cutoff - 1) - P.top_p) <= 1e-6f) rflags |= ROWF_TOPP_NEAR;
+            // sorted lane i tells index-order lane pos_i whether it stays
+            uint32_t* w = reinterpret_cast<uint32_t*>(wv);
+            w[lane] = 0u;
+            wave_sync();
+            if (real && lane < cutoff) w[(int)(0xFFFFFFFFu - (uint32_t)srt)] = 1u;
+            wave_sync();
+            keep = keep && w[lane] != 0u;
+            wave_sync();
+            fresh = false;
+        }
+    }
+    if (have && (P.flags & RF_MINP)) {
+        // sampler.cpp:167-176
+        if (!fresh) have = wave_softmax(v, keep, p, wv);
+        fresh = true;
+        if (have) {
+            const float mp = wave_max_f(keep ? p : 0.0f);
+            const float thr = P.min_p * mp;
+            const bool drop = keep && p < thr;
+            if (__ballot(drop) != 0ull) fresh = false;
+            keep = keep && !drop;
+        }
+    }
+    if (have && !fresh) have = wave_softmax(v, keep, p, wv);
+    int32_t tok = 0;
+    const u64 km = have ? __ballot(keep) : 0ull;
+    if (have) {
+        // sampler.cpp:178-182 / discrete_distribution: double sum, q, partial sums
+        const double pd = keep ? (double)p : 0.0;
+        const double S = wave_seq_sum_d(pd, wv);
+        const double q = keep ? pd / S : 0.0;
+        int32_t t = V - 1;
+        double near = 1.0;
+        if (single) {
+            t = 0;
+        } else if (!(u > 0.0)) {
+            t = 0;
+        } else {
+            const double cp = wave_seq_prefix_d(q, wv);
+            const double cj = (keep && (int32_t)id == V - 1) ? 1.0 : cp;
+            const u64 hit = __ballot(keep && cj >= u);
+            if (hit != 0ull) {
+                const int j = __ffsll((long long)hit) - 1;
+                t = __builtin_amdgcn_readlane((int)id, j);
+                const double prev = (j > 0) ? readlane_d(cp, j - 1) : 0.0;
+                near = fmin(fabs(readlane_d(cj, j) - u), fabs(prev - u));
+            } else {
+                near = fmin(fabs(1.0 - u), fabs(readlane_d(cp, 63) - u));
+            }
+        }
+        if (near <= 1e-6) rflags |= ROWF_CDF_NEAR;
+        tok = t;
+        const int pos = __popcll(km & ((1ull << lane) - 1ull));
+        if (keep) {
+            if (a.kept_idx != nullptr && pos < a.set_cap) {
+                a.kept_idx[(int64_t)r * a.set_cap + pos] = (int32_t)id;
+                a.kept_prob[(int64_t)r * a.set_cap + pos] = p;
+            }
+            if (a.fin_idx != nullptr && pos < a.fin_cap) a.fin_idx[(int64_t)r * a.fin_cap + pos] = (int32_t)id;
+        }
+    }
+    const int nkept = __popcll(km);
+    if (nkept == 0) {
+        rflags |= ROWF_UNIFORM;
+        if (lane == 0) tok = uniform_draw(V, u);
+    }
+    if (lane == 0) {
+        a.token[r] = tok;
+        if (a.row_flags != nullptr) a.row_flags[r] = rflags;
+        if (a.kept_count != nullptr) a.kept_count[r] = nkept;
+        if (a.fin_n != nullptr) a.fin_n[r] = nkept;
+    }
+}
+
+// The exact top-k of the buffer's n candidates, then the rest of the row.
+// For k <= 64 wave 0 selects from up to 256 candidates (more are first
+// compacted by the block) and finishes alone; larger k finish with finalize_row.
+__device__ __attribute__((noinline)) void select_and_finalize(const StreamArgs& a, const RowPlan& P, int r, u64* buf,
+                                                              FinLds f, Shared& st, uint32_t rflags) {
+    int n = st.n;
+    const int k = P.top_k;
+    if (k <= 64) {
+        if (n > 256) {
+            buf_compact(buf, k, st);
+            n = st.n;
+        }
+        if (threadIdx.x >= 64) return;
+        const u64 c = wave_topk(buf, n, k, st.wv);
+        wave_finalize(a, P, r, c, min(k, n), rflags, st);
+        return;
+    }
+    buf_compact(buf, k, st);
+    finalize_row(a, P, r, buf, st.n, f, st, rflags);
+}
+
+// ---- the stream kernel ---------------------------------------------------------
+
+// Append the register-held keys kv[i] (0 = absent) of ids idx(i) whose
+// composite is >= the threshold to the slice's list in global memory: each
+// lane counts its survivors, the wave reserves one range with a single LDS
+// atomic, and each lane writes its survivors in slot order. The list holds a
+// whole slice, so it cannot overflow.
+template <int NE, typename Idx>
+__device__ __forceinline__ void append_out(u64* out, const uint32_t (&kv)[NE], Idx idx, Shared& st) {
+    const int lane = lane_id();
+    const u64 th = st.theta;
+    const uint32_t thk = (uint32_t)(th >> 32);
+    const uint32_t thi = ~(uint32_t)th;   // largest index that survives a tie on thk
+    uint32_t sv = 0u;
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+        const uint32_t key = kv[i];
+        const bool ok = key > thk || (key == thk && (uint32_t)idx(i) <= thi);
+        sv |= ok ? (1u << i) : 0u;
+    }
+    const int cnt = __popc(sv);
+    int incl = cnt;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += y;
+    }
+    const int wtot = __shfl(incl, 63, 64);
+    if (wtot == 0) return;
+    int base = 0;
+    if (lane == 63) base = atomicAdd(&st.n, wtot);
+    int pos = __shfl(base, 63, 64) + incl - cnt;
+#pragma unroll
+    for (int i = 0; i < NE; ++i)
+        if ((sv >> i) & 1u) out[pos++] = comp(kv[i], idx(i));
+}
+
+// One block per (row, slice): stream the slice once and leave for k_merge
+//  - the ids whose key can still be among the row's top k (all of them in
+//    composite form), or the slice's argmax for a greedy row, and
+//  - the raw logits of the slice's penalised ids (history window or logit
+//    bias), whose stages 1-4 k_merge applies from the row's counts.
+// LDS: [penalised-id bitmap][allowed-id mask words], one bit per slice id.
 template <int DT, bool VEC>
-__global__ __launch_bounds__(kBlock) void k_stream(StreamArgs a) {
+__global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
     using T = Tile<DT>;
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ Shared st;
@@ -712,45 +1150,62 @@ __global__ __launch_bounds__(kBlock) void k_stream(StreamArgs a) {
     const int r = logical / a.nslices, s = logical % a.nslices;
     if (r >= a.rows) return;
     const RowPlan P = a.plans[r];
-    const int V = a.vocab;
     const int lo = s * a.slice_len;
-    const int hi = min(V, lo + a.slice_len);
+    const int hi = min(a.vocab, lo + a.slice_len);
+    const int words = a.bitmap_words;
     const bool greedy = (P.flags & RF_GREEDY) != 0;
     const bool pen = (P.flags & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) != 0;
-
-    // LDS carve: [penalty region | finalize region] aliased, then the buffer.
-    PenaltyLds pl;
-    pl.bitmap = reinterpret_cast<uint32_t*>(smem);
-    pl.hkey = pl.bitmap + ((a.bitmap_words + 3) & ~3);
-    pl.hval = pl.hkey + a.hash_slots;
-    pl.hmask = (uint32_t)a.hash_slots - 1u;
-    pl.hshift = 32u - (uint32_t)__popc(pl.hmask);
-    const int kP2 = next_pow2(max(a.kmax, 1));
-    FinLds f;
-    f.sortk = reinterpret_cast<u64*>(smem);
-    f.fidx = reinterpret_cast<int32_t*>(f.sortk + kP2);
-    f.fv = reinterpret_cast<float*>(f.fidx + a.kmax);
-    f.fe = f.fv + a.kmax;
-    f.fp = f.fe + a.kmax;
-    f.keep = reinterpret_cast<int32_t*>(f.fp + a.kmax);
-    u64* buf = reinterpret_cast<u64*>(smem + (a.lds_bytes - (uint32_t)a.buf_cap * 8u));
-    u64* ovf = a.ovf + (int64_t)logical * a.ovf_cap;
-
+    const bool masked = (P.flags & RF_MASK) != 0;
     const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * T::ES;
-    const uint32_t* mrow = (P.flags & RF_MASK) ? a.mask + (int64_t)r * a.mask_stride : nullptr;
 
+    // The first tile goes out before anything else, then the history.
+    uint4 raw[T::NCH];
+    load_tile<DT, VEC>(rowp, lo, hi, raw);
+    int32_t pre[8];
+    const int L = P.hist_len, p0 = L - P.scan_len;
+    const int32_t* hrow = a.hist + (int64_t)r * a.hist_stride;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const int p = p0 + q * kBlock + tid;
+        pre[q] = (pen && p < L) ? hrow[p] : -1;
+    }
+    uint32_t* pbm = reinterpret_cast<uint32_t*>(smem);
+    uint32_t* mbm = pbm + words;
     if (tid == 0) {
         st.theta = kThetaFloor;
         st.n = 0;
+        st.npend = 0;
         st.nan0 = 0;
         st.flags = 0;
     }
-    uint4 raw[T::NCH];
-    uint32_t mw[T::NCH];
-    load_tile<DT, VEC>(rowp, mrow, lo, hi, raw, mw);
-    if (pen) pen_build(a, P, r, lo, hi, pl);
+    for (int i = tid; i < words; i += kBlock) {
+        if (pen) pbm[i] = 0u;
+        if (masked) mbm[i] = (lo + 32 * i < hi) ? a.mask[(int64_t)r * a.mask_stride + (lo >> 5) + i] : 0u;
+    }
     __syncthreads();
+    if (pen) {
+        // the ids the penalty stages touch (sampler.cpp:236-258)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int t = pre[q];
+            if (t >= lo && t < hi) atomicOr(&pbm[(t - lo) >> 5], 1u << ((t - lo) & 31));
+        }
+        for (int p = p0 + 8 * kBlock + tid; p < L; p += kBlock) {
+            const int t = hrow[p];
+            if (t >= lo && t < hi) atomicOr(&pbm[(t - lo) >> 5], 1u << ((t - lo) & 31));
+        }
+        if (P.flags & RF_BIAS) {
+            for (int j = tid; j < P.bias_cnt; j += kBlock) {
+                const int t = a.bias_ids[P.bias_off + j];
+                if (t >= lo && t < hi) atomicOr(&pbm[(t - lo) >> 5], 1u << ((t - lo) & 31));
+            }
+        }
+        __syncthreads();
+    }
 
+    const int64_t slot = (int64_t)r * a.nslices + s;
+    u64* out = a.cand + slot * a.cand_cap;
+    u64* pend = a.pend + slot * a.pend_cap;
     const int k = P.top_k;
     const int kw = (k + 3) >> 2;
     const int G = min(4, max(1, (kw + 63) >> 6));
@@ -759,26 +1214,29 @@ __global__ __launch_bounds__(kBlock) void k_stream(StreamArgs a) {
     u64 best = 0ull;          // greedy: best composite of this thread
     int nanseen = 0;
 
-    for (int tb = lo; tb < hi; tb += T::ELEMS) {
-        // Transform each logit of the tile and keep only its order key:
-        // mask -> bias/penalties -> (temperature) -> key32; 0 marks "absent".
+    for (int tb = lo;;) {
+        // mask -> (temperature) -> order key; 0 marks "absent". Penalised ids
+        // hand their masked raw logit to k_merge instead.
         uint32_t kv[T::NE];
 #pragma unroll
         for (int j = 0; j < T::NCH; ++j) {
             const int e0 = tb + (j * kBlock + tid) * T::VW;
-            const uint32_t mbits = mw[j] >> (e0 & 31);
-            uint32_t pbits = 0u;
-            if (pen && e0 < hi) pbits = pl.bitmap[(e0 - lo) >> 5] >> ((e0 - lo) & 31);
+            const int o = e0 - lo;
+            const bool in = e0 < hi;
+            const uint32_t mb = (masked && in) ? (mbm[o >> 5] >> (o & 31)) : 0xFFFFFFFFu;
+            const uint32_t pb = (pen && in) ? (pbm[o >> 5] >> (o & 31)) : 0u;
 #pragma unroll
             for (int c = 0; c < T::VW; ++c) {
                 float x = elem<DT>(raw[j], c);
-                if (!((mbits >> c) & 1u)) x = -__builtin_inff();
-                if ((pbits >> c) & 1u) x = pen_apply(x, e0 + c, a, P, pl);
+                if (!((mb >> c) & 1u)) x = -__builtin_inff();
+                const bool penal = (pb >> c) & 1u;
+                if (penal) pend[atomicAdd(&st.npend, 1)] = ((u64)(uint32_t)(e0 + c) << 32) | __float_as_uint(x);
+                const bool here = e0 + c < hi && !penal;
                 uint32_t key;
                 if (greedy) {
                     // argmax of sampler.cpp:220-228: NaN never wins; element 0 NaN -> 0.
                     const bool nan = x != x;
-                    if (nan && e0 + c < hi) {
+                    if (nan && here) {
                         nanseen = 1;
                         if (e0 + c == 0) st.nan0 = 1;
                     }
@@ -786,39 +1244,167 @@ __global__ __launch_bounds__(kBlock) void k_stream(StreamArgs a) {
                 } else {
                     if (temp) x = x * inv_t;                    // sampler.cpp:101-106
                     if (x != x) {
-                        if (e0 + c < hi) nanseen = 1;
+                        if (here) nanseen = 1;
                         x = -__builtin_inff();
                     }
                     key = key32(x);
                 }
-                kv[j * T::VW + c] = (e0 + c < hi) ? key : 0u;
+                kv[j * T::VW + c] = here ? key : 0u;
             }
         }
-        // The raw registers are free: start the next tile's loads now.
-        if (tb + T::ELEMS < hi) load_tile<DT, VEC>(rowp, mrow, tb + T::ELEMS, hi, raw, mw);
         if (greedy) {
 #pragma unroll
             for (int j = 0; j < T::NCH; ++j) {
                 const int e0 = tb + (j * kBlock + tid) * T::VW;
 #pragma unroll
                 for (int c = 0; c < T::VW; ++c) {
-                    const u64 cc = (e0 + c < hi) ? comp(kv[j * T::VW + c], e0 + c) : 0ull;
+                    const u64 cc = kv[j * T::VW + c] != 0u ? comp(kv[j * T::VW + c], e0 + c) : 0ull;
                     best = cc > best ? cc : best;
                 }
             }
-            continue;
-        }
-        // Per-tile lower bound on the k-th largest: the kw-th largest group
-        // maximum of each wave (kw = ceil(k/4)), minimum over the 4 waves.
-        uint32_t gk[4] = {0u, 0u, 0u, 0u};
+        } else {
+            // A lower bound on the row's k-th largest from this tile: each
+            // wave's kw-th largest group maximum (kw = ceil(k/4)), minimum over
+            // the 4 waves; the block keeps the highest bound seen so far.
+            uint32_t gk[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int j = 0; j < T::NCH; ++j) {
-            const int g = (j * 4) / T::NCH;
-            const int gg = (G == 4) ? g : (G == 2 ? (g >> 1) : 0);
+            for (int j = 0; j < T::NCH; ++j) {
 #pragma unroll
-            for (int c = 0; c < T::VW; ++c) gk[gg] = max(gk[gg], kv[j * T::VW + c]);
+                for (int c = 0; c < T::VW; ++c) gk[(j * 4) / T::NCH] = max(gk[(j * 4) / T::NCH], kv[j * T::VW + c]);
+            }
+            // G groups of 32 / G keys per lane
+            if (G == 2) {
+                gk[0] = max(gk[0], gk[1]);
+                gk[1] = max(gk[2], gk[3]);
+            } else if (G == 1) {
+                gk[0] = max(max(gk[0], gk[1]), max(gk[2], gk[3]));
+            }
+            const uint32_t tw = (kw <= 64 * G) ? wave_kth_largest(gk, G, kw) : 0u;
+            if (lane_id() == 0) st.twave[wave_id()] = tw;
+            __syncthreads();
+            uint32_t tt = st.twave[0];
+#pragma unroll
+            for (int i = 1; i < kBlock / 64; ++i) tt = min(tt, st.twave[i]);
+            const u64 tl = (u64)tt << 32;
+            __syncthreads();
+            if (tid == 0 && tl > st.theta) st.theta = tl;
+            __syncthreads();
+            const int bt = tb + tid * T::VW;
+            append_out<T::NE>(out, kv, [&](int i) -> int32_t {
+                return bt + (i / T::VW) * (kBlock * T::VW) + (i % T::VW);
+            }, st);
         }
-        const uint32_t tw = (kw <= 64 * G) ? wave_kth_largest(gk, G, kw) : 0u;
+        tb += T::ELEMS;
+        if (tb >= hi) break;
+        load_tile<DT, VEC>(rowp, tb, hi, raw);
+    }
+
+    // ---- the slice's counts for k_merge ----------------------------------------
+    if (nanseen) atomicOr(&st.flags, 1);
+    if (greedy) best = block_max_u64(best, st);   // has the barrier the counts need
+    else __syncthreads();
+    if (tid == 0) {
+        const int nanf = (st.flags & 1) ? (1 << 30) : 0;
+        if (greedy) {
+            out[0] = best;
+            a.cand_n[slot] = 1 | nanf | (st.nan0 ? (1 << 29) : 0);
+        } else {
+            a.cand_n[slot] = st.n | nanf;
+        }
+        a.pend_n[slot] = st.npend;
+    }
+}
+
+// ---- the merge kernel ------------------------------------------------------------
+
+// The row's penalty table: every id of the history window with its counts
+// (repetition flag, DRY count, frequency/presence count) and its bias flag.
+// The first 8 * 256 history entries are loaded before the table is cleared.
+__device__ __forceinline__ void pen_add(const StreamArgs& a, const RowPlan& P, int L, int p, int32_t t,
+                                        PenaltyLds pl) {
+    if (t < 0 || t >= a.vocab) return;
+    uint32_t add = 0u, orv = 0u;
+    if (p >= L - P.rep_win) orv |= HV_REP;
+    if (p >= L - P.dry_win) add += 1u << HV_DRY_SHIFT;
+    if (p >= L - P.fp_win) add += 1u;
+    const uint32_t sl = pen_insert(t, pl);
+    if (add) atomicAdd(&pl.hval[sl], add);
+    if (orv) atomicOr(&pl.hval[sl], orv);
+}
+
+__device__ __forceinline__ void pen_build_row(const StreamArgs& a, const RowPlan& P, int r, PenaltyLds pl) {
+    const int tid = threadIdx.x;
+    const int L = P.hist_len;
+    const int p0 = L - P.scan_len;
+    const int32_t* h = a.hist + (int64_t)r * a.hist_stride;
+    int32_t pre[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const int p = p0 + q * kBlock + tid;
+        pre[q] = (p < L) ? h[p] : -1;
+    }
+    for (int i = tid; i < a.mhash_slots; i += kBlock) {
+        pl.hkey[i] = kEmpty;
+        pl.hval[i] = 0u;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 8; ++q) pen_add(a, P, L, p0 + q * kBlock + tid, pre[q], pl);
+    for (int p = p0 + 8 * kBlock + tid; p < L; p += kBlock) pen_add(a, P, L, p, h[p], pl);
+    if (P.flags & RF_BIAS) {
+        for (int j = tid; j < P.bias_cnt; j += kBlock) {
+            const uint32_t sl = pen_insert(a.bias_ids[P.bias_off + j], pl);
+            atomicOr(&pl.hval[sl], HV_BIAS);
+        }
+    }
+    __syncthreads();
+}
+
+// Offer the m entries of a per-slice list through the threshold filter:
+// rounds of NM entries per thread, whose loads all go out first (entry fi
+// lives in slice find_slice(fi) at fi - off[slice]); xf turns a loaded entry
+// into a composite (0 = none). Each round bounds the k-th largest from below
+// (kw-th largest lane maximum per wave, minimum over the waves) and appends
+// the survivors to the buffer.
+__device__ __forceinline__ int find_slice(const int* off, int S, int fi) {
+    // the last slice whose offset is <= fi: the one holding entry fi (off[0] = 0)
+    int sl = 0;
+#pragma unroll
+    for (int step = 128; step > 0; step >>= 1)
+        if (sl + step < S && off[sl + step] <= fi) sl += step;
+    return sl;
+}
+
+template <typename Xf>
+__device__ __forceinline__ void offer(u64* buf, u64* ovf, int cap, int k, int m, const u64* list, int64_t stride,
+                                      const int* off, int S, Xf xf, Shared& st) {
+    constexpr int NM = 8;
+    const int tid = threadIdx.x;
+    const int kw = (k + 3) >> 2;
+    for (int base = 0; base < m; base += kBlock * NM) {
+        u64 raw[NM];
+#pragma unroll
+        for (int i = 0; i < NM; ++i) {
+            const int fi = base + i * kBlock + tid;
+            raw[i] = 0ull;
+            if (fi < m) {
+                const int sl = find_slice(off, S, fi);
+                raw[i] = list[(int64_t)sl * stride + (fi - off[sl])];
+            }
+        }
+        uint32_t kv[NM];
+        int32_t id[NM];
+        uint32_t g = 0u;
+#pragma unroll
+        for (int i = 0; i < NM; ++i) {
+            const int fi = base + i * kBlock + tid;
+            const u64 c = (fi < m) ? xf(raw[i]) : 0ull;
+            kv[i] = (uint32_t)(c >> 32);
+            id[i] = comp_idx(c);
+            g = max(g, kv[i]);
+        }
+        const uint32_t gk[4] = {g, 0u, 0u, 0u};
+        const uint32_t tw = (kw <= 64) ? wave_kth_largest(gk, 1, kw) : 0u;
         if (lane_id() == 0) st.twave[wave_id()] = tw;
         __syncthreads();
         {
@@ -830,113 +1416,119 @@ __global__ __launch_bounds__(kBlock) void k_stream(StreamArgs a) {
             if (tid == 0 && tl > st.theta) st.theta = tl;
             __syncthreads();
         }
-        const int bt = tb + tid * T::VW;
-        auto idx = [&](int i) -> int32_t { return bt + (i / T::VW) * (kBlock * T::VW) + (i % T::VW); };
-        append_regs<T::NE>(buf, a.buf_cap, kv, idx, ovf, st);
-        drain_overflow(buf, a.buf_cap, k, ovf, st);
+        append_regs<NM>(buf, cap, kv, [&](int i) { return id[i]; }, ovf, st);
+        drain_overflow(buf, cap, k, ovf, st);
     }
+}
 
-    // ---- slice result -----------------------------------------------------------
-    uint32_t rflags = 0u;
-    if (nanseen) atomicOr(&st.flags, 1);
-    __syncthreads();
-    if (st.flags & 1) rflags |= ROWF_NAN;
-    if (greedy) {
-        best = block_max_u64(best, st);
-        if (a.nslices == 1) {
-            if (tid == 0) {
-                a.token[r] = st.nan0 ? 0 : comp_idx(best);
-                if (a.row_flags != nullptr) a.row_flags[r] = rflags | ROWF_GREEDY;
-                if (a.topk_count != nullptr) a.topk_count[r] = -1;
-                if (a.kept_count != nullptr) a.kept_count[r] = 0;
-            }
-            return;
-        }
-        if (tid == 0) {
-            u64* out = a.cand + ((int64_t)r * a.nslices + s) * a.cand_cap;
-            out[0] = best;
-            out[1] = (u64)(st.nan0 | (rflags ? 2 : 0));
-            a.cand_n[(int64_t)r * a.nslices + s] = 2;
-        }
-    } else if (a.nslices == 1) {
-        buf_compact(buf, k, st);
-        finalize_row(a, P, r, buf, st.n, f, st, rflags);
-        return;
-    } else {
-        if (st.n > a.cand_cap) buf_compact(buf, k, st);
-        const int n = st.n;
-        u64* out = a.cand + ((int64_t)r * a.nslices + s) * a.cand_cap;
-        for (int i = tid; i < n; i += kBlock) out[i] = buf[i];
-        if (tid == 0) a.cand_n[(int64_t)r * a.nslices + s] = n | (rflags ? (1 << 30) : 0);
-    }
-
-    // ---- last block of the row merges -----------------------------------------
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned prev = atomicAdd(&a.counters[r], 1u);
-        st.last = (prev == (unsigned)(a.nslices - 1)) ? 1 : 0;
-    }
-    __syncthreads();
-    if (!st.last) return;
-    __threadfence();
-    if (tid == 0) a.counters[r] = 0u;
-
+// One block per row: finish the penalised ids, merge everything into the
+// row's exact top-k (or argmax) and run the rest of the ladder.
+__global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ Shared st;
+    __shared__ StreamArgs sa;
+    __shared__ RowPlan sP;
+    __shared__ int poff[kBlock + 1];
+    const int tid = threadIdx.x;
+    const int r = (int)blockIdx.x;
+    if (r >= a.rows) return;
+    const RowPlan P = a.plans[r];
     const int S = a.nslices;
+    const bool greedy = (P.flags & RF_GREEDY) != 0;
+    const bool pen = (P.flags & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) != 0;
+    const int k = P.top_k;
+    if (tid == 0) {
+        sa = a;
+        sP = P;
+        st.flags = 0;
+        st.nan0 = 0;
+        st.n = 0;
+        st.theta = kThetaFloor;
+    }
+    // LDS: [row penalty table | finalize scratch] aliased, then the buffer.
+    const PenaltyLds pl = pen_table(a, r, smem);
+    const int kP2 = next_pow2(max(a.kmax, 1));
+    FinLds f;
+    f.sortk = reinterpret_cast<u64*>(smem);
+    f.fidx = reinterpret_cast<int32_t*>(f.sortk + kP2);
+    f.fv = reinterpret_cast<float*>(f.fidx + a.kmax);
+    f.fe = f.fv + a.kmax;
+    f.fp = f.fe + a.kmax;
+    f.keep = reinterpret_cast<int32_t*>(f.fp + a.kmax);
+    u64* buf = reinterpret_cast<u64*>(smem + (a.merge_lds - (uint32_t)a.buf_cap * 8u));
+    u64* ovf = a.ovf + (int64_t)r * a.ovf_cap;
     const u64* cand = a.cand + (int64_t)r * S * a.cand_cap;
-    const int32_t* cn = a.cand_n + (int64_t)r * S;
+
+    // slice counts -> offsets of the concatenated candidate and pend lists
+    int myc = 0, myp = 0, fl = 0;
+    if (tid < S) {
+        const int v = a.cand_n[(int64_t)r * S + tid];
+        myc = v & 0x1FFFFFFF;
+        fl = v >> 29;
+        myp = a.pend_n[(int64_t)r * S + tid];
+    }
+    int M, NP;
+    const int off = block_excl_scan(myc, &M, st);
+    const int offp = block_excl_scan(myp, &NP, st);
+    if (tid < S) {
+        st.soff[tid] = off;
+        poff[tid] = offp;
+    }
+    if (tid == 0) {
+        st.soff[S] = M;
+        poff[S] = NP;
+    }
+    if (fl & 2) atomicOr(&st.flags, 4);      // a NaN logit somewhere in the row
+    if (fl & 1) atomicOr(&st.nan0, 1);       // greedy: id 0 is NaN
+    if (pen) pen_build_row(a, P, r, pl);
+    else __syncthreads();
+
+    // penalised ids: stages 1-6 from the table (sampler.cpp:235-264)
+    auto pen_xf = [&](u64 e) -> u64 {
+        const int32_t t = (int32_t)(e >> 32);
+        float x = pen_apply(__uint_as_float((uint32_t)e), t, sa, sP, pl);
+        if (greedy) {
+            if (x != x) {
+                atomicOr(&st.flags, 4);
+                if (t == 0) atomicOr(&st.nan0, 1);
+                return 0ull;
+            }
+            return comp(key32(x), t);
+        }
+        if (P.flags & RF_TEMP) x = x * P.inv_temp;
+        if (x != x) {
+            atomicOr(&st.flags, 4);
+            x = -__builtin_inff();
+        }
+        return comp(key32(x), t);
+    };
+    const u64* pend = a.pend + (int64_t)r * S * a.pend_cap;
     if (greedy) {
         u64 b = 0ull;
-        int nan0 = 0, anynan = 0;
         for (int i = tid; i < S; i += kBlock) {
             const u64 c = cand[(int64_t)i * a.cand_cap];
             b = c > b ? c : b;
-            const int fl = (int)cand[(int64_t)i * a.cand_cap + 1];
-            nan0 |= fl & 1;
-            anynan |= (fl >> 1) & 1;
+        }
+        for (int fi = tid; fi < NP; fi += kBlock) {
+            const int sl = find_slice(poff, S, fi);
+            const u64 c = pen_xf(pend[(int64_t)sl * a.pend_cap + (fi - poff[sl])]);
+            b = c > b ? c : b;
         }
         b = block_max_u64(b, st);
-        if (nan0) atomicOr(&st.nan0, 1);
-        if (anynan) atomicOr(&st.flags, 2);
         __syncthreads();
         if (tid == 0) {
             a.token[r] = st.nan0 ? 0 : comp_idx(b);
-            if (a.row_flags != nullptr)
-                a.row_flags[r] = ROWF_GREEDY | ((st.flags & 2) ? ROWF_NAN : 0u);
+            if (a.row_flags != nullptr) a.row_flags[r] = ROWF_GREEDY | ((st.flags & 4) ? ROWF_NAN : 0u);
             if (a.topk_count != nullptr) a.topk_count[r] = -1;
             if (a.kept_count != nullptr) a.kept_count[r] = 0;
         }
         return;
     }
-    // slice offsets
-    int myc = 0, mynan = 0;
-    if (tid < S) {
-        const int v = cn[tid];
-        myc = v & 0x3FFFFFFF;
-        mynan = (v >> 30) & 1;
-    }
-    int M;
-    const int off = block_excl_scan(myc, &M, st);
-    if (tid < S) st.soff[tid] = off;
-    if (tid == 0) {
-        st.soff[S] = M;
-        st.n = 0;
-        st.theta = kThetaFloor;
-    }
-    if (mynan) atomicOr(&st.flags, 4);
+    offer(buf, ovf, a.buf_cap, k, NP, pend, a.pend_cap, poff, S, pen_xf, st);
+    offer(buf, ovf, a.buf_cap, k, M, cand, a.cand_cap, st.soff, S, [](u64 e) { return e; }, st);
     __syncthreads();
-    rflags = (st.flags & 4) ? ROWF_NAN : 0u;
-    append_fetch(buf, a.buf_cap, k, M, [&](int fi) {
-        int lo2 = 0, hi2 = S;  // last slice with soff <= fi
-        while (hi2 - lo2 > 1) {
-            const int mid = (lo2 + hi2) >> 1;
-            if (st.soff[mid] <= fi) lo2 = mid;
-            else hi2 = mid;
-        }
-        return cand[(int64_t)lo2 * a.cand_cap + (fi - st.soff[lo2])];
-    }, st);
-    buf_compact(buf, k, st);
-    finalize_row(a, P, r, buf, st.n, f, st, rflags);
+    const uint32_t rflags = (st.flags & 4) ? ROWF_NAN : 0u;
+    select_and_finalize(sa, sP, r, buf, f, st, rflags);
 }
 
 // ---- writeback -------------------------------------------------------------------
@@ -944,26 +1536,29 @@ __global__ __launch_bounds__(kBlock) void k_stream(StreamArgs a) {
 template <bool VEC>
 __global__ __launch_bounds__(kBlock) void k_writeback(StreamArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ StreamArgs sa;
+    __shared__ RowPlan sP;
     const int tid = threadIdx.x;
     const int logical = (int)(blockIdx.x % kXcds) * a.blocks_per_xcd + (int)(blockIdx.x / kXcds);
     const int r = logical / a.nslices, s = logical % a.nslices;
     if (r >= a.rows) return;
     const RowPlan P = a.plans[r];
+    if (tid == 0) {
+        sa = a;
+        sP = P;
+    }
     const int V = a.vocab;
     const int lo = s * a.slice_len;
     const int hi = min(V, lo + a.slice_len);
     const bool greedy = (P.flags & RF_GREEDY) != 0;
     const bool pen = (P.flags & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) != 0;
-    PenaltyLds pl;
-    pl.bitmap = reinterpret_cast<uint32_t*>(smem);
-    pl.hkey = pl.bitmap + ((a.bitmap_words + 3) & ~3);
-    pl.hval = pl.hkey + a.hash_slots;
-    pl.hmask = (uint32_t)a.hash_slots - 1u;
-    pl.hshift = 32u - (uint32_t)__popc(pl.hmask);
-    uint32_t* keepbm = pl.hval + a.hash_slots;  // kept ids of this slice
-    if (pen) pen_build(a, P, r, lo, hi, pl);
+    // LDS: [row penalty table (when not global)] [kept ids of this slice]
+    const PenaltyLds pl = pen_table(a, r, smem);
+    uint32_t* keepbm = reinterpret_cast<uint32_t*>(smem) + (a.gtab != nullptr ? 0 : 2 * a.mhash_slots);
     for (int i = tid; i < a.bitmap_words; i += kBlock) keepbm[i] = 0u;
-    __syncthreads();
+    // a global table is the one k_merge built for this row; an LDS one is rebuilt
+    if (pen && a.gtab == nullptr) pen_build_row(a, P, r, pl);
+    else __syncthreads();
     if (!greedy) {
         const int n = a.fin_n[r];
         for (int j = tid; j < n; j += kBlock) {
@@ -977,7 +1572,13 @@ __global__ __launch_bounds__(kBlock) void k_writeback(StreamArgs a) {
     for (int e = lo + tid; e < hi; e += kBlock) {
         float x = row[e];
         if (mrow != nullptr && !((mrow[e >> 5] >> (e & 31)) & 1u)) x = -__builtin_inff();
-        if (pen && ((pl.bitmap[(e - lo) >> 5] >> ((e - lo) & 31)) & 1u)) x = pen_apply(x, e, a, P, pl);
+        if (pen) {
+            // ids without a table entry pass through unchanged
+            uint32_t sl = hslot(e, pl);
+            uint32_t hk;
+            while ((hk = tab_ld(&pl.hkey[sl])) != kEmpty && hk != (uint32_t)e) sl = (sl + 1) & pl.hmask;
+            if (hk == (uint32_t)e) x = pen_apply(x, e, sa, sP, pl);
+        }
         if (!greedy) {
             if (P.flags & RF_TEMP) x = x * P.inv_temp;
             if (!((keepbm[(e - lo) >> 5] >> ((e - lo) & 31)) & 1u)) x = -__builtin_inff();
@@ -997,6 +1598,11 @@ hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, int grid, hip
         if (vec) hipLaunchKernelGGL((k_stream<1, true>), g, b, a.lds_bytes, stream, a);
         else hipLaunchKernelGGL((k_stream<1, false>), g, b, a.lds_bytes, stream, a);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_merge(const StreamArgs& a, hipStream_t stream) {
+    hipLaunchKernelGGL(k_merge, dim3(a.rows), dim3(kBlock), a.merge_lds, stream, a);
     return hipGetLastError();
 }
 

@@ -90,17 +90,21 @@ struct StreamArgs {
     int32_t kmax;               // max top_k over sampling rows (<= K_LIMIT)
     int32_t cand_cap;           // candidates one slice may leave in global scratch
     int32_t buf_cap;            // LDS candidate buffer entries
-    int32_t hash_slots;         // power of two, 0 when no row has penalties
+    int32_t mhash_slots;        // row penalty table slots in k_merge (power of two)
     int32_t bitmap_words;       // slice_len / 32
     int32_t blocks_per_xcd;     // grid / 8
     int32_t fin_cap;            // entries per row in fin_idx
     unsigned long long* cand;   // [rows * S * cand_cap]
     int32_t* cand_n;            // [rows * S]
-    uint32_t* counters;         // [rows], zero between launches
     int32_t* fin_idx;           // [rows * fin_cap] final kept ids (for writeback)
     int32_t* fin_n;             // [rows]
     unsigned long long* ovf;    // [blocks * ovf_cap] per-block overflow of the LDS buffer
     int32_t ovf_cap;            // one tile of candidates
+    unsigned long long* pend;   // [blocks * pend_cap] (id << 32 | raw logit bits) of penalised ids
+    int32_t* pend_n;            // [rows * S]
+    int32_t pend_cap;
+    uint32_t* gtab;             // [rows * 2 * mhash_slots] penalty tables, or NULL: tables in LDS
+    uint32_t merge_lds;         // dynamic LDS of k_merge
     uint32_t lds_bytes;         // dynamic LDS size of the launch
 };
 

@@ -24,7 +24,8 @@
 #include "ultima_hsamp.h"
 
 namespace hsamp {
-hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, int grid, hipStream_t stream);
+hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int grid,
+                         hipStream_t stream);
 hipError_t launch_writeback(const StreamArgs& a, int grid, uint32_t lds, hipStream_t stream);
 hipError_t launch_merge(const StreamArgs& a, hipStream_t stream);
 }  // namespace hsamp
@@ -36,7 +37,8 @@ namespace {
 constexpr int kSlots = 4;
 constexpr int kTile = kBlock * 32;      // elements one block streams per tile
 constexpr int kTargetBlocks = 4096;     // most blocks a launch spreads rows over
-constexpr int kMergeRound = kBlock * 8; // candidates k_merge offers per round
+constexpr int kMergeRound = kBlock * 16;  // candidates k_merge offers per round
+constexpr int kMergeWindow = kBlock * 16; // list entries k_merge loads up front, over all slices
 
 struct Slot {
     char* host = nullptr;   // pinned
@@ -71,9 +73,6 @@ struct ultima_hsamp {
     unsigned long long* cand = nullptr;
     size_t cand_elems = 0;
     int32_t* cand_n = nullptr;
-    int32_t* pend_n = nullptr;
-    unsigned long long* pend = nullptr;  // per-block raw logits of penalised ids
-    size_t pend_elems = 0;
     uint32_t* gtab = nullptr;            // per-row penalty tables too large for LDS
     size_t gtab_words = 0;
     int32_t* fin_idx = nullptr;
@@ -127,6 +126,9 @@ struct Built {
     int kmax = 0;              // max top_k over rows that select
     int max_pen = 0;           // max over penalty rows of (scan_len + bias entries)
     bool any_pen = false;
+    int max_scan = 0;          // max history window over penalty rows
+    int max_bias = 0;          // max logit-bias entries over rows
+    bool any_mask = false;     // the batch carries an allowed-token mask
     bool any_full = false;     // a sampling row without top-k (not handled here)
     bool any_big_k = false;    // top_k above kLimitK
 };
@@ -143,6 +145,7 @@ int build_blob(ultima_hsamp* h, const ultima_hsamp_batch* b, Built& out) {
     for (int r = 0; r < B; ++r) {
         const ultima_hsamp_params& q = b->params[r];
         RowPlan& P = h->plans[r];
+        P.inv_temp = 1.0f;   // x * 1.0f == x: rows without temperature multiply by one
         if (isnan_f(q.rep_penalty) || isnan_f(q.dry_multiplier) || isnan_f(q.dry_base) ||
             isnan_f(q.frequency_penalty) || isnan_f(q.presence_penalty) ||
             isnan_f(q.temperature) || isnan_f(q.top_p) || isnan_f(q.min_p))
@@ -219,7 +222,10 @@ int build_blob(ultima_hsamp* h, const ultima_hsamp_batch* b, Built& out) {
                 }
             }
         }
-        if (b->mask != nullptr) fl |= RF_MASK;
+        if (b->mask != nullptr) {
+            fl |= RF_MASK;
+            out.any_mask = true;
+        }
         if (!greedy) {
             if (q.temperature != 1.0f) {                                          // [102]
                 fl |= RF_TEMP;
@@ -245,6 +251,8 @@ int build_blob(ultima_hsamp* h, const ultima_hsamp_batch* b, Built& out) {
         if (fl & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) {
             out.any_pen = true;
             out.max_pen = std::max(out.max_pen, (int)scan + P.bias_cnt);
+            out.max_scan = std::max(out.max_scan, (int)scan);
+            out.max_bias = std::max(out.max_bias, (int)P.bias_cnt);
         }
     }
     out.off_dry = align16(sizeof(RowPlan) * B);
@@ -420,7 +428,6 @@ int ultima_hsamp_create(int device, int32_t max_rows, int32_t max_vocab, ultima_
     // Per-slice counts: rows * slices <= max(kTargetBlocks, max_rows) blocks.
     const size_t blocks = std::max<size_t>(kTargetBlocks + 8, (size_t)max_rows);
     CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->cand_n), blocks * 4));
-    CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->pend_n), blocks * 4));
     CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->fin_idx), (size_t)max_rows * kLimitK * 4));
     CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->fin_n), (size_t)max_rows * 4));
     CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_row), (size_t)max_vocab * 4 + 64));
@@ -445,7 +452,7 @@ int ultima_hsamp_destroy(ultima_hsamp* h) {
         if (s.dev) (void)hipFree(s.dev);
         if (s.ev) (void)hipEventDestroy(s.ev);
     }
-    for (void* p : {(void*)h->ovf, (void*)h->cand, (void*)h->cand_n, (void*)h->pend_n, (void*)h->pend,
+    for (void* p : {(void*)h->ovf, (void*)h->cand, (void*)h->cand_n,
                     (void*)h->gtab, (void*)h->fin_idx,
                     (void*)h->fin_n, (void*)h->d_row, (void*)h->d_hist, (void*)h->d_u, (void*)h->d_tok})
         if (p) (void)hipFree(p);
@@ -491,12 +498,17 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     const size_t lds_budget = std::min<size_t>(h->lds_limit, 64 * 1024) - statik;
     const bool gtab = 8 * (size_t)mhash + 8 * (size_t)buf_cap > lds_budget ||
                       8 * (size_t)mhash + 4 * (size_t)bitmap_words > lds_budget;
-    const size_t merge_lds = align16(std::max(gtab ? 0 : 8 * (size_t)mhash, regionF)) + 8 * (size_t)buf_cap;
+    size_t merge_lds = align16(std::max(gtab ? 0 : 8 * (size_t)mhash, regionF)) + 8 * (size_t)buf_cap;
+    // k_merge's fast path: [bins 8 KB][list 1 KB][table 12 B/slot | buffer]
+    const size_t fast_lds = 9216 + std::max(12 * (size_t)mhash, 8 * (size_t)buf_cap);
+    const bool fast = kmax <= 64 && !gtab && bl.max_scan <= 8 * kBlock && bl.max_bias <= kBlock &&
+                      fast_lds <= lds_budget;
+    if (fast) merge_lds = std::max(merge_lds, fast_lds);
     const size_t wb_lds = (gtab ? 0 : 8 * (size_t)mhash) + 4 * (size_t)bitmap_words;
     if (merge_lds + statik > h->lds_limit || wb_lds + statik > h->lds_limit) return ULTIMA_HSAMP_ERR_CAPACITY;
     const int nblocks = B * S;
     const int grid = (nblocks + kXcds - 1) / kXcds * kXcds;
-    const int pend_cap = bl.any_pen ? std::min(slice_len, bl.max_pen) : 0;
+    const int win = std::max(1, std::min(cand_cap, kMergeWindow / S));
 
     hipStreamCaptureStatus cap_status = hipStreamCaptureStatusNone;
     HIP_TRY(hipStreamIsCapturing(stream, &cap_status));
@@ -519,7 +531,6 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     };
     st = grow(h->ovf, h->ovf_elems, (size_t)B * kMergeRound, 8);
     if (st == ULTIMA_HSAMP_OK) st = grow(h->cand, h->cand_elems, (size_t)B * S * cand_cap, 8);
-    if (st == ULTIMA_HSAMP_OK) st = grow(h->pend, h->pend_elems, std::max<size_t>(1, (size_t)grid * pend_cap), 8);
     if (st == ULTIMA_HSAMP_OK && gtab) st = grow(h->gtab, h->gtab_words, (size_t)B * 2 * mhash, 4);
     if (st != ULTIMA_HSAMP_OK) return st;
 
@@ -562,9 +573,10 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     a.ovf_cap = kMergeRound;
     a.cand = h->cand;
     a.cand_n = h->cand_n;
-    a.pend = h->pend;
-    a.pend_n = h->pend_n;
-    a.pend_cap = pend_cap;
+    a.win = win;
+    a.win_magic = (uint32_t)((1ull << 32) / (uint64_t)win + 1);
+    a.dtype = b->dtype;
+    a.fast = fast ? 1 : 0;
     a.gtab = gtab ? h->gtab : nullptr;
     a.merge_lds = (uint32_t)merge_lds;
     const bool wb = (b->flags & ULTIMA_HSAMP_WRITEBACK) != 0;
@@ -573,7 +585,8 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     a.lds_bytes = (uint32_t)lds;
     const bool vec = (reinterpret_cast<uintptr_t>(b->logits) % 16 == 0) &&
                      ((b->logits_stride * es) % 16 == 0);
-    HIP_TRY(launch_stream(a, b->dtype, vec, grid, stream));
+    a.vec_tail = vec ? V % (16 / es) : 0;
+    HIP_TRY(launch_stream(a, b->dtype, vec, bl.any_pen, bl.any_mask, grid, stream));
     HIP_TRY(launch_merge(a, stream));
     if (wb) HIP_TRY(launch_writeback(a, grid, (uint32_t)wb_lds, stream));
     if (!capturing) HIP_TRY(hipEventRecord(slot->ev, stream));

@@ -72,8 +72,9 @@ struct Shared {
     int soff[257];      // slice offsets during the merge
     int flags;
     int nan0;
-    int npend;          // penalised ids set aside in the stream
     alignas(16) u64 wv[64];  // the finishing wave's cross-lane scratch
+    double u;           // the row's uniform
+    uint64_t expT[32];  // expf's table (libm_expf.h), copied to LDS
     float sm_m, sm_inv;
     int cutoff;
     double dS;
@@ -405,9 +406,12 @@ __device__ __forceinline__ uint32_t tab_ld(const uint32_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// GT: the table lives in the row's global area (windows too large for LDS).
+template <bool GT>
 __device__ __forceinline__ PenaltyLds pen_table(const StreamArgs& a, int r, unsigned char* smem) {
     PenaltyLds pl;
-    pl.hkey = (a.gtab != nullptr) ? a.gtab + (int64_t)r * 2 * a.mhash_slots : reinterpret_cast<uint32_t*>(smem);
+    if (GT) pl.hkey = a.gtab + (int64_t)r * 2 * a.mhash_slots;
+    else pl.hkey = reinterpret_cast<uint32_t*>(smem);
     pl.hval = pl.hkey + a.mhash_slots;
     pl.hmask = (uint32_t)a.mhash_slots - 1u;
     pl.hshift = 32u - (uint32_t)__popc(pl.hmask);
@@ -427,12 +431,8 @@ __device__ uint32_t pen_insert(int32_t t, PenaltyLds pl) {
     }
 }
 
-// Stages 1-4 of the ladder for one id with a table entry (sampler.cpp:28-99).
-__device__ __forceinline__ float pen_apply(float x, int32_t t, const StreamArgs& a, const RowPlan& P,
-                                           PenaltyLds pl) {
-    uint32_t s = hslot(t, pl);
-    while (tab_ld(&pl.hkey[s]) != (uint32_t)t) s = (s + 1) & pl.hmask;
-    const uint32_t v = tab_ld(&pl.hval[s]);
+// Stages 1-4 of the ladder for id t whose table value is v (sampler.cpp:28-99).
+__device__ __forceinline__ float pen_value(float x, int32_t t, uint32_t v, const StreamArgs& a, const RowPlan& P) {
     if (v & HV_BIAS) {
         int lo = 0, hi = P.bias_cnt;
         const int32_t* ids = a.bias_ids + P.bias_off;
@@ -454,6 +454,14 @@ __device__ __forceinline__ float pen_apply(float x, int32_t t, const StreamArgs&
     return x;
 }
 
+// The same for an id with a table entry, found by probing.
+__device__ __forceinline__ float pen_apply(float x, int32_t t, const StreamArgs& a, const RowPlan& P,
+                                           PenaltyLds pl) {
+    uint32_t s = hslot(t, pl);
+    while (tab_ld(&pl.hkey[s]) != (uint32_t)t) s = (s + 1) & pl.hmask;
+    return pen_value(x, t, tab_ld(&pl.hval[s]), a, P);
+}
+
 // ---- tile loading --------------------------------------------------------------
 
 template <int DT>
@@ -465,17 +473,20 @@ struct Tile {
     static constexpr int ELEMS = kBlock * NE;     // 8192 per tile
 };
 
+// One tile of this thread's chunks from [tb, hi). With VEC the slice ends on
+// a whole chunk (the row's last V % VW ids are left to k_merge), so every
+// chunk is one 16-byte non-temporal load or absent; without VEC (unaligned
+// rows) the elements are read one by one.
 template <int DT, bool VEC>
 __device__ __forceinline__ void load_tile(const char* rowp, int tb, int hi, uint4 (&raw)[Tile<DT>::NCH]) {
     using T = Tile<DT>;
 #pragma unroll
     for (int j = 0; j < T::NCH; ++j) {
         const int e0 = tb + (j * kBlock + (int)threadIdx.x) * T::VW;
-        if (VEC && e0 + T::VW <= hi) {
-            const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rowp + (size_t)e0 * T::ES));
+        if (VEC) {
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if (e0 < hi) v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rowp + (size_t)e0 * T::ES));
             raw[j] = make_uint4(v.x, v.y, v.z, v.w);
-        } else if (e0 >= hi) {
-            raw[j] = make_uint4(0u, 0u, 0u, 0u);
         } else {
             uint32_t w[4] = {0u, 0u, 0u, 0u};
             for (int c = 0; c < T::VW; ++c) {
@@ -520,7 +531,7 @@ __device__ __attribute__((noinline)) bool fin_softmax(FinLds f, int nk, Shared& 
         if (f.keep[j]) m = fmaxf(m, f.fv[j]);
     m = block_max_f(m, st);
     if (m == -__builtin_inff()) return false;
-    for (int j = tid; j < nk; j += kBlock) f.fe[j] = f.keep[j] ? libm_expf(f.fv[j] - m) : 0.0f;
+    for (int j = tid; j < nk; j += kBlock) f.fe[j] = f.keep[j] ? libm_expf_t(f.fv[j] - m, st.expT) : 0.0f;
     __syncthreads();
     if (tid == 0) {
         float s = 0.0f;
@@ -560,7 +571,7 @@ __device__ __attribute__((noinline)) void finalize_row(const StreamArgs& a, cons
                                                        uint32_t rflags) {
     const int tid = threadIdx.x;
     const int V = a.vocab;
-    const double u = a.u[r];
+    const double u = st.u;
     const bool single = (P.flags & RF_SINGLE) != 0;
     if (!single) rflags |= ROWF_U_USED;
     int32_t tok = 0;
@@ -768,10 +779,13 @@ __device__ __forceinline__ void wave_sort_asc(uint32_t& key, uint32_t& pay, u64*
     wave_sync();
     int rank = 0;
     const uint4* w4 = reinterpret_cast<const uint4*>(w);
+#pragma unroll 1
+    for (int q0 = 0; q0 < 16; q0 += 4) {
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-        const uint4 x = w4[q];
-        rank += (x.x < key) + (x.y < key) + (x.z < key) + (x.w < key);
+        for (int q = q0; q < q0 + 4; ++q) {
+            const uint4 x = w4[q];
+            rank += (x.x < key) + (x.y < key) + (x.z < key) + (x.w < key);
+        }
     }
     wave_sync();
     w[rank] = key;
@@ -788,8 +802,15 @@ __device__ __forceinline__ u64 wave_sort_desc(u64 key, u64* wv) {
     wv[lane] = key;
     wave_sync();
     int rank = 0;
+    const ulonglong2* w2 = reinterpret_cast<const ulonglong2*>(wv);
+#pragma unroll 1
+    for (int q0 = 0; q0 < 32; q0 += 4) {
 #pragma unroll
-    for (int q = 0; q < 64; ++q) rank += wv[q] > key;
+        for (int q = q0; q < q0 + 4; ++q) {
+            const ulonglong2 x = w2[q];
+            rank += (x.x > key) + (x.y > key);
+        }
+    }
     wave_sync();
     wv[rank] = key;
     wave_sync();
@@ -807,7 +828,7 @@ __device__ __forceinline__ float wave_seq_sum_f(float x, u64* wv) {
     wave_sync();
     const float4* w4 = reinterpret_cast<const float4*>(w);
     float s = 0.0f;
-#pragma unroll
+#pragma unroll 4
     for (int q = 0; q < 16; ++q) {
         const float4 v = w4[q];
         s = s + v.x;
@@ -828,7 +849,7 @@ __device__ __forceinline__ float wave_seq_prefix_f(float x, u64* wv) {
     wave_sync();
     const float4* w4 = reinterpret_cast<const float4*>(w);
     float s = 0.0f, mine = 0.0f;
-#pragma unroll
+#pragma unroll 4
     for (int q = 0; q < 16; ++q) {
         const float4 v = w4[q];
         s = s + v.x;
@@ -851,11 +872,14 @@ __device__ __forceinline__ double wave_seq_sum_d(double x, u64* wv) {
     wave_sync();
     const double2* w2 = reinterpret_cast<const double2*>(w);
     double s = 0.0;
+#pragma unroll 1
+    for (int q0 = 0; q0 < 32; q0 += 8) {
 #pragma unroll
-    for (int q = 0; q < 32; ++q) {
-        const double2 v = w2[q];
-        s = s + v.x;
-        s = s + v.y;
+        for (int q = q0; q < q0 + 8; ++q) {
+            const double2 v = w2[q];
+            s = s + v.x;
+            s = s + v.y;
+        }
     }
     wave_sync();
     return s;
@@ -868,13 +892,16 @@ __device__ __forceinline__ double wave_seq_prefix_d(double x, u64* wv) {
     wave_sync();
     const double2* w2 = reinterpret_cast<const double2*>(w);
     double s = 0.0, mine = 0.0;
+#pragma unroll 1
+    for (int q0 = 0; q0 < 32; q0 += 8) {
 #pragma unroll
-    for (int q = 0; q < 32; ++q) {
-        const double2 v = w2[q];
-        s = s + v.x;
-        mine = (lane == 2 * q) ? s : mine;
-        s = s + v.y;
-        mine = (lane == 2 * q + 1) ? s : mine;
+        for (int q = q0; q < q0 + 8; ++q) {
+            const double2 v = w2[q];
+            s = s + v.x;
+            mine = (lane == 2 * q) ? s : mine;
+            s = s + v.y;
+            mine = (lane == 2 * q + 1) ? s : mine;
+        }
     }
     wave_sync();
     return mine;
@@ -883,10 +910,10 @@ __device__ __forceinline__ double wave_seq_prefix_d(double x, u64* wv) {
 // softmax_probs (sampler.cpp:124-142) over the kept lanes of one wave; lanes
 // are in index order. The float denominator is the index-order sequential sum.
 // Returns false when nothing is kept.
-__device__ __forceinline__ bool wave_softmax(float v, bool keep, float& p, u64* wv) {
+__device__ __forceinline__ bool wave_softmax(float v, bool keep, float& p, u64* wv, const uint64_t* expT) {
     if (__ballot(keep) == 0ull) return false;
     const float m = wave_max_f(keep ? v : -__builtin_inff());
-    const float e = keep ? libm_expf(v - m) : 0.0f;
+    const float e = keep ? libm_expf_t(v - m, expT) : 0.0f;
     const float s = wave_seq_sum_f(e, wv);
     p = keep ? ((s <= 0.0f) ? e : e * (1.0f / s)) : 0.0f;
     return true;
@@ -974,7 +1001,7 @@ __device__ __attribute__((noinline)) void wave_finalize(const StreamArgs& a, con
                                                         uint32_t rflags, Shared& st) {
     const int lane = lane_id();
     const int V = a.vocab;
-    const double u = a.u[r];
+    const double u = st.u;
     const bool single = (P.flags & RF_SINGLE) != 0;
     u64* wv = st.wv;
     if (!single) rflags |= ROWF_U_USED;
@@ -988,7 +1015,7 @@ __device__ __attribute__((noinline)) void wave_finalize(const StreamArgs& a, con
     if (a.topk_count != nullptr && lane == 0) a.topk_count[r] = single ? -1 : nk;
     bool keep = has;
     float p = 0.0f;
-    bool have = nk > 0 && wave_softmax(v, keep, p, wv);
+    bool have = nk > 0 && wave_softmax(v, keep, p, wv, st.expT);
     bool fresh = true;
     if (have && (P.flags & RF_TOPP)) {
         // sampler.cpp:146-164: order by (p desc, index asc), float running sum;
@@ -1015,7 +1042,7 @@ __device__ __attribute__((noinline)) void wave_finalize(const StreamArgs& a, con
     }
     if (have && (P.flags & RF_MINP)) {
         // sampler.cpp:167-176
-        if (!fresh) have = wave_softmax(v, keep, p, wv);
+        if (!fresh) have = wave_softmax(v, keep, p, wv, st.expT);
         fresh = true;
         if (have) {
             const float mp = wave_max_f(keep ? p : 0.0f);
@@ -1025,7 +1052,7 @@ __device__ __attribute__((noinline)) void wave_finalize(const StreamArgs& a, con
             keep = keep && !drop;
         }
     }
-    if (have && !fresh) have = wave_softmax(v, keep, p, wv);
+    if (have && !fresh) have = wave_softmax(v, keep, p, wv, st.expT);
     int32_t tok = 0;
     const u64 km = have ? __ballot(keep) : 0ull;
     if (have) {
@@ -1076,9 +1103,29 @@ __device__ __attribute__((noinline)) void wave_finalize(const StreamArgs& a, con
     }
 }
 
+// The k largest of the n <= 256 distinct nonzero composites buf[0..n), in
+// descending order, into st.wv[0..min(k, n)) (k <= 64): entry i's rank is the
+// number of entries above it, counted against broadcast reads of the buffer.
+__device__ __forceinline__ void block_rank_topk(u64* buf, int n, int k, Shared& st) {
+    const int tid = threadIdx.x;
+    if (tid == 0) buf[n] = 0ull;   // pad to pairs; 0 is below every composite
+    __syncthreads();
+    if (tid < n) {
+        const u64 me = buf[tid];
+        const ulonglong2* b2 = reinterpret_cast<const ulonglong2*>(buf);
+        int rank = 0;
+        for (int j = 0; j < (n + 1) >> 1; ++j) {
+            const ulonglong2 x = b2[j];
+            rank += (x.x > me) + (x.y > me);
+        }
+        if (rank < k) st.wv[rank] = me;
+    }
+    __syncthreads();
+}
+
 // The exact top-k of the buffer's n candidates, then the rest of the row.
-// For k <= 64 wave 0 selects from up to 256 candidates (more are first
-// compacted by the block) and finishes alone; larger k finish with finalize_row.
+// For k <= 64 the block ranks up to 256 candidates (more are first compacted)
+// and wave 0 finishes alone; larger k finish with finalize_row.
 __device__ __attribute__((noinline)) void select_and_finalize(const StreamArgs& a, const RowPlan& P, int r, u64* buf,
                                                               FinLds f, Shared& st, uint32_t rflags) {
     int n = st.n;
@@ -1088,8 +1135,9 @@ __device__ __attribute__((noinline)) void select_and_finalize(const StreamArgs& 
             buf_compact(buf, k, st);
             n = st.n;
         }
+        block_rank_topk(buf, n, k, st);
         if (threadIdx.x >= 64) return;
-        const u64 c = wave_topk(buf, n, k, st.wv);
+        const u64 c = (lane_id() < min(k, n)) ? st.wv[lane_id()] : 0ull;
         wave_finalize(a, P, r, c, min(k, n), rflags, st);
         return;
     }
@@ -1099,24 +1147,17 @@ __device__ __attribute__((noinline)) void select_and_finalize(const StreamArgs& 
 
 // ---- the stream kernel ---------------------------------------------------------
 
-// Append the register-held keys kv[i] (0 = absent) of ids idx(i) whose
-// composite is >= the threshold to the slice's list in global memory: each
-// lane counts its survivors, the wave reserves one range with a single LDS
-// atomic, and each lane writes its survivors in slot order. The list holds a
-// whole slice, so it cannot overflow.
+// Append the register-held keys kv[i] (0 = absent) of ids idx(i) that are
+// >= the key threshold thk to the slice's list in global memory: each lane
+// counts its survivors, the wave reserves one range with a single LDS atomic,
+// and each lane writes its survivors in slot order. The list holds a whole
+// slice, so it cannot overflow.
 template <int NE, typename Idx>
-__device__ __forceinline__ void append_out(u64* out, const uint32_t (&kv)[NE], Idx idx, Shared& st) {
+__device__ __forceinline__ void append_out(u64* out, const uint32_t (&kv)[NE], Idx idx, uint32_t thk, Shared& st) {
     const int lane = lane_id();
-    const u64 th = st.theta;
-    const uint32_t thk = (uint32_t)(th >> 32);
-    const uint32_t thi = ~(uint32_t)th;   // largest index that survives a tie on thk
     uint32_t sv = 0u;
 #pragma unroll
-    for (int i = 0; i < NE; ++i) {
-        const uint32_t key = kv[i];
-        const bool ok = key > thk || (key == thk && (uint32_t)idx(i) <= thi);
-        sv |= ok ? (1u << i) : 0u;
-    }
+    for (int i = 0; i < NE; ++i) sv |= (kv[i] >= thk) ? (1u << i) : 0u;
     const int cnt = __popc(sv);
     int incl = cnt;
 #pragma unroll
@@ -1134,13 +1175,85 @@ __device__ __forceinline__ void append_out(u64* out, const uint32_t (&kv)[NE], I
         if ((sv >> i) & 1u) out[pos++] = comp(kv[i], idx(i));
 }
 
-// One block per (row, slice): stream the slice once and leave for k_merge
-//  - the ids whose key can still be among the row's top k (all of them in
-//    composite form), or the slice's argmax for a greedy row, and
-//  - the raw logits of the slice's penalised ids (history window or logit
-//    bias), whose stages 1-4 k_merge applies from the row's counts.
+// A lower bound on the kw-th largest of the 64 * G keys a wave holds (G per
+// lane): the kw-th largest with its low 16 bits cleared, by a bitwise radix
+// select of the high 16 bits over ballots. Keys of 0 stand for "no value".
+__device__ __forceinline__ uint32_t wave_kth_bound16(const uint32_t (&g)[4], int G, int kw) {
+    uint32_t prefix = 0u, known = 0u;
+    int need = kw;
+#pragma unroll
+    for (int b = 31; b >= 16; --b) {
+        const uint32_t bit = 1u << b;
+        int cnt = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (i < G) {
+                const bool m = ((g[i] & known) == prefix) && (g[i] & bit);
+                cnt += __popcll(__ballot(m));
+            }
+        }
+        if (cnt >= need) prefix |= bit;
+        else need -= cnt;
+        known |= bit;
+    }
+    return prefix;
+}
+
+// One logit of a row, by id (for the penalised ids the stream hands over).
+template <int DT>
+__device__ __forceinline__ float load_logit(const char* rowp, int t) {
+    if (DT == 0) return reinterpret_cast<const float*>(rowp)[t];
+    return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(rowp)[t] << 16);
+}
+
+// Order keys of one tile's elements held by this thread. kv[i] = 0 marks
+// "absent": past the slice end, or penalised (finished by k_merge).
+//  - greedy (GR): mask, then key32; a NaN never wins (key 0) but is noted.
+//  - sampling: mask, x * fl(1/T) (1.0f without temperature), NaN -> -inf
+//    (noted), key32.
+// x + 0.0f turns -0 into +0 and leaves every other value as it is, so ties
+// between zeros of either sign go to the lower index as in the reference.
+template <int DT, bool PEN, bool MASK, bool GR>
+__device__ __forceinline__ void tile_keys(const uint4 (&raw)[Tile<DT>::NCH], int tb, int lo, int hi,
+                                          const uint32_t* pbm, const uint32_t* mbm, float inv_t,
+                                          uint32_t (&kv)[Tile<DT>::NE], bool& nanseen) {
+    using T = Tile<DT>;
+    const int tid = threadIdx.x;
+    bool nanv = false;
+#pragma unroll
+    for (int j = 0; j < T::NCH; ++j) {
+        const int e0 = tb + (j * kBlock + tid) * T::VW;
+        const int o = e0 - lo;
+        const bool in = e0 < hi;   // whole chunks (VEC) or per element below
+        uint32_t mb = 0xFFFFFFFFu, pb = 0u;
+        if (MASK) mb = in ? (mbm[o >> 5] >> (o & 31)) : 0u;
+        if (PEN) pb = in ? (pbm[o >> 5] >> (o & 31)) : 0u;
+#pragma unroll
+        for (int c = 0; c < T::VW; ++c) {
+            float x = elem<DT>(raw[j], c);
+            if (MASK) x = ((mb >> c) & 1u) ? x : -__builtin_inff();
+            if (!GR) x = x * inv_t;                          // sampler.cpp:101-106
+            x = x + 0.0f;
+            const bool nan = x != x;
+            const uint32_t b = __float_as_uint(x);
+            uint32_t key = b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
+            key = nan ? (GR ? 0u : kKeyNegInf) : key;
+            bool here = e0 + c < hi;
+            if (PEN) here = here && !((pb >> c) & 1u);
+            nanv |= nan && here;
+            kv[j * T::VW + c] = here ? key : 0u;
+        }
+    }
+    nanseen |= nanv;
+}
+
+// One block per (row, slice): stream the slice once and leave for k_merge the
+// ids whose key can still be among the row's top k (all of them, in composite
+// form), or the slice's argmax for a greedy row. Penalised ids (history window
+// or logit bias) are left out: k_merge finishes them from the row's counts.
+// PEN / MASK: some row of the launch has penalties / an allowed-token mask.
 // LDS: [penalised-id bitmap][allowed-id mask words], one bit per slice id.
-template <int DT, bool VEC>
+template <int DT, bool VEC, bool PEN, bool MASK>
 __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
     using T = Tile<DT>;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -1151,148 +1264,114 @@ __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
     if (r >= a.rows) return;
     const RowPlan P = a.plans[r];
     const int lo = s * a.slice_len;
-    const int hi = min(a.vocab, lo + a.slice_len);
+    const int hi = min(a.vocab - (VEC ? a.vec_tail : 0), lo + a.slice_len);   // k_merge takes the ragged end
     const int words = a.bitmap_words;
     const bool greedy = (P.flags & RF_GREEDY) != 0;
-    const bool pen = (P.flags & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) != 0;
-    const bool masked = (P.flags & RF_MASK) != 0;
+    const bool pen = PEN && (P.flags & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) != 0;
+    const bool masked = MASK && (P.flags & RF_MASK) != 0;
     const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * T::ES;
 
-    // The first tile goes out before anything else, then the history.
-    uint4 raw[T::NCH];
-    load_tile<DT, VEC>(rowp, lo, hi, raw);
+    // The history goes out first (it is waited for first), then the first tile.
     int32_t pre[8];
     const int L = P.hist_len, p0 = L - P.scan_len;
     const int32_t* hrow = a.hist + (int64_t)r * a.hist_stride;
+    if (PEN) {
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-        const int p = p0 + q * kBlock + tid;
-        pre[q] = (pen && p < L) ? hrow[p] : -1;
+        for (int q = 0; q < 8; ++q) {
+            const int p = p0 + q * kBlock + tid;
+            pre[q] = (pen && p < L) ? hrow[p] : -1;
+        }
     }
+    uint4 raw[T::NCH];
+    load_tile<DT, VEC>(rowp, lo, hi, raw);
     uint32_t* pbm = reinterpret_cast<uint32_t*>(smem);
     uint32_t* mbm = pbm + words;
     if (tid == 0) {
         st.theta = kThetaFloor;
         st.n = 0;
-        st.npend = 0;
-        st.nan0 = 0;
         st.flags = 0;
     }
     for (int i = tid; i < words; i += kBlock) {
-        if (pen) pbm[i] = 0u;
+        if (PEN) pbm[i] = 0u;
         if (masked) mbm[i] = (lo + 32 * i < hi) ? a.mask[(int64_t)r * a.mask_stride + (lo >> 5) + i] : 0u;
+        else if (MASK) mbm[i] = 0xFFFFFFFFu;
     }
     __syncthreads();
-    if (pen) {
-        // the ids the penalty stages touch (sampler.cpp:236-258)
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int t = pre[q];
-            if (t >= lo && t < hi) atomicOr(&pbm[(t - lo) >> 5], 1u << ((t - lo) & 31));
-        }
-        for (int p = p0 + 8 * kBlock + tid; p < L; p += kBlock) {
-            const int t = hrow[p];
-            if (t >= lo && t < hi) atomicOr(&pbm[(t - lo) >> 5], 1u << ((t - lo) & 31));
-        }
-        if (P.flags & RF_BIAS) {
-            for (int j = tid; j < P.bias_cnt; j += kBlock) {
-                const int t = a.bias_ids[P.bias_off + j];
-                if (t >= lo && t < hi) atomicOr(&pbm[(t - lo) >> 5], 1u << ((t - lo) & 31));
-            }
-        }
-        __syncthreads();
-    }
-
     const int64_t slot = (int64_t)r * a.nslices + s;
     u64* out = a.cand + slot * a.cand_cap;
-    u64* pend = a.pend + slot * a.pend_cap;
+    if (pen) {
+        // the ids the penalty stages touch (sampler.cpp:236-258): k_merge
+        // finishes them from the row's counts
+        auto mark = [&](int t) {
+            if (t >= lo && t < hi) atomicOr(&pbm[(t - lo) >> 5], 1u << ((t - lo) & 31));
+        };
+#pragma unroll
+        for (int q = 0; q < 8; ++q) mark(pre[q]);
+        for (int p = p0 + 8 * kBlock + tid; p < L; p += kBlock) mark(hrow[p]);
+        if (P.flags & RF_BIAS)
+            for (int j = tid; j < P.bias_cnt; j += kBlock) mark(a.bias_ids[P.bias_off + j]);
+    }
+    if (PEN) __syncthreads();
+
     const int k = P.top_k;
     const int kw = (k + 3) >> 2;
     const int G = min(4, max(1, (kw + 63) >> 6));
     const float inv_t = P.inv_temp;
-    const bool temp = (P.flags & RF_TEMP) != 0;
-    u64 best = 0ull;          // greedy: best composite of this thread
-    int nanseen = 0;
+    bool nanseen = false;
+    uint32_t bk = 0u;          // greedy: best key and its first id so far
+    int32_t bi = 0x7FFFFFFF;
 
     for (int tb = lo;;) {
-        // mask -> (temperature) -> order key; 0 marks "absent". Penalised ids
-        // hand their masked raw logit to k_merge instead.
         uint32_t kv[T::NE];
-#pragma unroll
-        for (int j = 0; j < T::NCH; ++j) {
-            const int e0 = tb + (j * kBlock + tid) * T::VW;
-            const int o = e0 - lo;
-            const bool in = e0 < hi;
-            const uint32_t mb = (masked && in) ? (mbm[o >> 5] >> (o & 31)) : 0xFFFFFFFFu;
-            const uint32_t pb = (pen && in) ? (pbm[o >> 5] >> (o & 31)) : 0u;
-#pragma unroll
-            for (int c = 0; c < T::VW; ++c) {
-                float x = elem<DT>(raw[j], c);
-                if (!((mb >> c) & 1u)) x = -__builtin_inff();
-                const bool penal = (pb >> c) & 1u;
-                if (penal) pend[atomicAdd(&st.npend, 1)] = ((u64)(uint32_t)(e0 + c) << 32) | __float_as_uint(x);
-                const bool here = e0 + c < hi && !penal;
-                uint32_t key;
-                if (greedy) {
-                    // argmax of sampler.cpp:220-228: NaN never wins; element 0 NaN -> 0.
-                    const bool nan = x != x;
-                    if (nan && here) {
-                        nanseen = 1;
-                        if (e0 + c == 0) st.nan0 = 1;
-                    }
-                    key = nan ? 0u : key32(x);
-                } else {
-                    if (temp) x = x * inv_t;                    // sampler.cpp:101-106
-                    if (x != x) {
-                        if (here) nanseen = 1;
-                        x = -__builtin_inff();
-                    }
-                    key = key32(x);
-                }
-                kv[j * T::VW + c] = here ? key : 0u;
-            }
-        }
         if (greedy) {
+            // argmax of sampler.cpp:220-228; k_merge settles id 0 holding a NaN
+            tile_keys<DT, PEN, MASK, true>(raw, tb, lo, hi, pbm, mbm, inv_t, kv, nanseen);
+            uint32_t m = 0u;
 #pragma unroll
-            for (int j = 0; j < T::NCH; ++j) {
-                const int e0 = tb + (j * kBlock + tid) * T::VW;
+            for (int i = 0; i < T::NE; ++i) m = max(m, kv[i]);
+            int32_t mi = 0x7FFFFFFF;
 #pragma unroll
-                for (int c = 0; c < T::VW; ++c) {
-                    const u64 cc = kv[j * T::VW + c] != 0u ? comp(kv[j * T::VW + c], e0 + c) : 0ull;
-                    best = cc > best ? cc : best;
-                }
+            for (int i = T::NE - 1; i >= 0; --i)
+                mi = (kv[i] == m) ? (tb + tid * T::VW + (i / T::VW) * (kBlock * T::VW) + (i % T::VW)) : mi;
+            if (m > bk || (m == bk && mi < bi)) {
+                bk = m;
+                bi = mi;
             }
         } else {
+            tile_keys<DT, PEN, MASK, false>(raw, tb, lo, hi, pbm, mbm, inv_t, kv, nanseen);
             // A lower bound on the row's k-th largest from this tile: each
-            // wave's kw-th largest group maximum (kw = ceil(k/4)), minimum over
-            // the 4 waves; the block keeps the highest bound seen so far.
+            // wave's kw-th largest group maximum (kw = ceil(k/4)), low 16 bits
+            // cleared, minimum over the 4 waves; the block keeps the highest
+            // bound seen so far. Keys at or above it survive.
             uint32_t gk[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
             for (int j = 0; j < T::NCH; ++j) {
 #pragma unroll
                 for (int c = 0; c < T::VW; ++c) gk[(j * 4) / T::NCH] = max(gk[(j * 4) / T::NCH], kv[j * T::VW + c]);
             }
-            // G groups of 32 / G keys per lane
+            const uint32_t lmax = max(max(gk[0], gk[1]), max(gk[2], gk[3]));
             if (G == 2) {
                 gk[0] = max(gk[0], gk[1]);
                 gk[1] = max(gk[2], gk[3]);
             } else if (G == 1) {
-                gk[0] = max(max(gk[0], gk[1]), max(gk[2], gk[3]));
+                gk[0] = lmax;
             }
-            const uint32_t tw = (kw <= 64 * G) ? wave_kth_largest(gk, G, kw) : 0u;
+            const uint32_t tw = (kw <= 64 * G) ? wave_kth_bound16(gk, G, kw) : 0u;
             if (lane_id() == 0) st.twave[wave_id()] = tw;
             __syncthreads();
             uint32_t tt = st.twave[0];
 #pragma unroll
             for (int i = 1; i < kBlock / 64; ++i) tt = min(tt, st.twave[i]);
-            const u64 tl = (u64)tt << 32;
+            const uint32_t th0 = (uint32_t)(st.theta >> 32);
             __syncthreads();
-            if (tid == 0 && tl > st.theta) st.theta = tl;
-            __syncthreads();
-            const int bt = tb + tid * T::VW;
-            append_out<T::NE>(out, kv, [&](int i) -> int32_t {
-                return bt + (i / T::VW) * (kBlock * T::VW) + (i % T::VW);
-            }, st);
+            const uint32_t thk = max(max(tt, th0), (uint32_t)(kThetaFloor >> 32));
+            if (tid == 0) st.theta = (u64)thk << 32;
+            if (__ballot(lmax >= thk) != 0ull) {
+                const int bt = tb + tid * T::VW;
+                append_out<T::NE>(out, kv, [&](int i) -> int32_t {
+                    return bt + (i / T::VW) * (kBlock * T::VW) + (i % T::VW);
+                }, thk, st);
+            }
         }
         tb += T::ELEMS;
         if (tb >= hi) break;
@@ -1301,17 +1380,13 @@ __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
 
     // ---- the slice's counts for k_merge ----------------------------------------
     if (nanseen) atomicOr(&st.flags, 1);
-    if (greedy) best = block_max_u64(best, st);   // has the barrier the counts need
+    u64 best = 0ull;
+    if (greedy) best = block_max_u64(bk != 0u ? comp(bk, bi) : 0ull, st);   // has the barrier the flag needs
     else __syncthreads();
     if (tid == 0) {
         const int nanf = (st.flags & 1) ? (1 << 30) : 0;
-        if (greedy) {
-            out[0] = best;
-            a.cand_n[slot] = 1 | nanf | (st.nan0 ? (1 << 29) : 0);
-        } else {
-            a.cand_n[slot] = st.n | nanf;
-        }
-        a.pend_n[slot] = st.npend;
+        if (greedy) out[0] = best;
+        a.cand_n[slot] = (greedy ? 1 : st.n) | nanf;
     }
 }
 
@@ -1332,17 +1407,25 @@ __device__ __forceinline__ void pen_add(const StreamArgs& a, const RowPlan& P, i
     if (orv) atomicOr(&pl.hval[sl], orv);
 }
 
-__device__ __forceinline__ void pen_build_row(const StreamArgs& a, const RowPlan& P, int r, PenaltyLds pl) {
+// The first 8 * 256 entries of the row's history window, loaded early.
+__device__ __forceinline__ void hist_prefetch(const StreamArgs& a, const RowPlan& P, int r, bool pen,
+                                              int32_t (&pre)[8]) {
+    const int L = P.hist_len;
+    const int p0 = L - P.scan_len;
+    const int32_t* h = a.hist + (int64_t)r * a.hist_stride;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const int p = p0 + q * kBlock + (int)threadIdx.x;
+        pre[q] = (pen && p < L) ? h[p] : -1;
+    }
+}
+
+__device__ __forceinline__ void pen_build_row(const StreamArgs& a, const RowPlan& P, int r, PenaltyLds pl,
+                                              const int32_t (&pre)[8]) {
     const int tid = threadIdx.x;
     const int L = P.hist_len;
     const int p0 = L - P.scan_len;
     const int32_t* h = a.hist + (int64_t)r * a.hist_stride;
-    int32_t pre[8];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-        const int p = p0 + q * kBlock + tid;
-        pre[q] = (p < L) ? h[p] : -1;
-    }
     for (int i = tid; i < a.mhash_slots; i += kBlock) {
         pl.hkey[i] = kEmpty;
         pl.hval[i] = 0u;
@@ -1360,93 +1443,575 @@ __device__ __forceinline__ void pen_build_row(const StreamArgs& a, const RowPlan
     __syncthreads();
 }
 
-// Offer the m entries of a per-slice list through the threshold filter:
-// rounds of NM entries per thread, whose loads all go out first (entry fi
-// lives in slice find_slice(fi) at fi - off[slice]); xf turns a loaded entry
-// into a composite (0 = none). Each round bounds the k-th largest from below
-// (kw-th largest lane maximum per wave, minimum over the waves) and appends
-// the survivors to the buffer.
-__device__ __forceinline__ int find_slice(const int* off, int S, int fi) {
-    // the last slice whose offset is <= fi: the one holding entry fi (off[0] = 0)
-    int sl = 0;
-#pragma unroll
-    for (int step = 128; step > 0; step >>= 1)
-        if (sl + step < S && off[sl + step] <= fi) sl += step;
-    return sl;
-}
-
-template <typename Xf>
-__device__ __forceinline__ void offer(u64* buf, u64* ovf, int cap, int k, int m, const u64* list, int64_t stride,
-                                      const int* off, int S, Xf xf, Shared& st) {
-    constexpr int NM = 8;
+// Offer NM register-held composites c[i] (0 = none) to the buffer: the
+// batch bounds the row's k-th largest from below (each wave's kw-th largest
+// lane maximum, kw = ceil(k/4), minimum over the waves), the bound raises the
+// threshold, and the survivors are appended.
+template <int NM>
+__device__ __forceinline__ void offer_regs(u64* buf, u64* ovf, int cap, int k, const u64 (&c)[NM], Shared& st) {
     const int tid = threadIdx.x;
     const int kw = (k + 3) >> 2;
-    for (int base = 0; base < m; base += kBlock * NM) {
-        u64 raw[NM];
+    uint32_t kv[NM];
+    int32_t id[NM];
+    uint32_t g = 0u;
 #pragma unroll
-        for (int i = 0; i < NM; ++i) {
-            const int fi = base + i * kBlock + tid;
-            raw[i] = 0ull;
-            if (fi < m) {
-                const int sl = find_slice(off, S, fi);
-                raw[i] = list[(int64_t)sl * stride + (fi - off[sl])];
+    for (int i = 0; i < NM; ++i) {
+        kv[i] = (uint32_t)(c[i] >> 32);
+        id[i] = comp_idx(c[i]);
+        g = max(g, kv[i]);
+    }
+    const uint32_t gk[4] = {g, 0u, 0u, 0u};
+    const uint32_t tw = (kw <= 64) ? wave_kth_largest(gk, 1, kw) : 0u;
+    if (lane_id() == 0) st.twave[wave_id()] = tw;
+    __syncthreads();
+    {
+        uint32_t tt = st.twave[0];
+#pragma unroll
+        for (int i = 1; i < kBlock / 64; ++i) tt = min(tt, st.twave[i]);
+        const u64 tl = (u64)tt << 32;
+        __syncthreads();
+        if (tid == 0 && tl > st.theta) st.theta = tl;
+        __syncthreads();
+    }
+    append_regs<NM>(buf, cap, kv, [&](int i) { return id[i]; }, ovf, st);
+    drain_overflow(buf, cap, k, ovf, st);
+}
+
+// A row's last ids that the stream's whole-chunk loads leave out, and that
+// are not penalised: mask, (temperature), NaN handling and key as in
+// tile_keys; 0 = no candidate (greedy NaN).
+__device__ __forceinline__ u64 tail_candidate(float x, bool allowed, int32_t t, bool greedy, float inv_t,
+                                              Shared& st) {
+    if (!allowed) x = -__builtin_inff();
+    if (!greedy) x = x * inv_t;
+    if (x != x) {
+        atomicOr(&st.flags, 4);
+        if (greedy) return 0ull;
+        x = -__builtin_inff();
+    }
+    return comp(key32(x), t);
+}
+
+// The merge of one row when k <= 64, the history window holds at most 8 * 256
+// ids, at most 256 bias entries, and the penalty table fits LDS next to a
+// 2048-bin histogram. LDS: [bins 8 KB][list 1 KB][table: keys, 64-bit counts].
+//  - Penalty table: each thread inserts its (up to) 8 history ids and 1 bias
+//    id with all first probes in flight together; the thread whose insert
+//    claims a slot owns the id, reads its logit at once and, after one
+//    64-bit add per history entry (frequency/presence, DRY and repetition
+//    counts in 16-bit fields), runs stages 1-6 for it.
+//  - Selection over the 9 + NW register candidates per thread: a lower bound
+//    L on the k-th largest key (each wave's kw-th largest lane maximum, low
+//    16 bits cleared, minimum over waves) and the maximum M fix the bits all
+//    top-k keys share; a 2048-bin histogram of the next 11 bits finds the bin
+//    holding the k-th; entries at or above it (< 128) are ranked exactly by
+//    wave 0. More entries (massive ties) or list entries beyond the windows
+//    take the buffer path.
+template <int NW>
+__device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P, int r, const int32_t (&pre)[8],
+                                           int32_t bias_t, bool nan_at0, int32_t tail_t, float tail_x, bool tail_ok,
+                                           u64 (&win)[NW], unsigned char* smem, Shared& st, const StreamArgs& sa,
+                                           const RowPlan& sP) {
+    const int tid = threadIdx.x;
+    const int lane = lane_id();
+    const bool greedy = (P.flags & RF_GREEDY) != 0;
+    const bool pen = (P.flags & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) != 0;
+    const bool masked = (P.flags & RF_MASK) != 0;
+    const int k = P.top_k;
+    const int S = a.nslices, W = a.win;
+    const int fs = a.mhash_slots;
+    uint32_t* bins = reinterpret_cast<uint32_t*>(smem);
+    u64* list = reinterpret_cast<u64*>(smem + 8192);
+    uint32_t* tkey = reinterpret_cast<uint32_t*>(smem + 9216);
+    u64* tval = reinterpret_cast<u64*>(smem + 9216 + 4 * fs);
+    const uint32_t hmask = (uint32_t)fs - 1u, hshift = 32u - (uint32_t)__popc(hmask);
+    if (pen) {
+        for (int i = tid; i < fs; i += kBlock) {
+            tkey[i] = kEmpty;
+            tval[i] = 0ull;
+        }
+    }
+    for (int i = tid; i < 2048; i += kBlock) bins[i] = 0u;
+    __syncthreads();   // also publishes the slice counts
+
+    // ---- penalised ids ------------------------------------------------------------
+    u64 cp[9];
+#pragma unroll
+    for (int q = 0; q < 9; ++q) cp[q] = 0ull;
+    if (pen) {
+        const int L = P.hist_len, p0 = L - P.scan_len;
+        int32_t t[9];
+        uint32_t sl[9];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) t[q] = (pre[q] >= 0 && pre[q] < a.vocab) ? pre[q] : -1;
+        t[8] = bias_t;
+        // every thread reads the logits of its ids at once (ownership is
+        // settled below); the loads overlap the table work
+        const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * (a.dtype == 0 ? 4 : 2);
+        float x[9];
+        uint32_t mw[9];
+#pragma unroll
+        for (int q = 0; q < 9; ++q) {
+            x[q] = 0.0f;
+            mw[q] = 0xFFFFFFFFu;
+            if (t[q] >= 0) {
+                x[q] = (a.dtype == 0) ? load_logit<0>(rowp, t[q]) : load_logit<1>(rowp, t[q]);
+                if (masked) mw[q] = a.mask[(int64_t)r * a.mask_stride + (t[q] >> 5)];
             }
         }
-        uint32_t kv[NM];
-        int32_t id[NM];
-        uint32_t g = 0u;
+        uint32_t done = 0u, own = 0u;
 #pragma unroll
-        for (int i = 0; i < NM; ++i) {
-            const int fi = base + i * kBlock + tid;
-            const u64 c = (fi < m) ? xf(raw[i]) : 0ull;
-            kv[i] = (uint32_t)(c >> 32);
-            id[i] = comp_idx(c);
-            g = max(g, kv[i]);
+        for (int q = 0; q < 9; ++q) {
+            sl[q] = ((uint32_t)t[q] * 0x9E3779B1u) >> hshift;
+            if (t[q] < 0) done |= 1u << q;
         }
-        const uint32_t gk[4] = {g, 0u, 0u, 0u};
-        const uint32_t tw = (kw <= 64) ? wave_kth_largest(gk, 1, kw) : 0u;
-        if (lane_id() == 0) st.twave[wave_id()] = tw;
+        while (done != 0x1FFu) {
+#pragma unroll
+            for (int q = 0; q < 9; ++q) {
+                if ((done >> q) & 1u) continue;
+                const uint32_t old = atomicCAS(&tkey[sl[q]], kEmpty, (uint32_t)t[q]);
+                if (old == kEmpty) {
+                    own |= 1u << q;
+                    done |= 1u << q;
+                } else if (old == (uint32_t)t[q]) {
+                    done |= 1u << q;
+                } else {
+                    sl[q] = (sl[q] + 1u) & hmask;
+                }
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            if (t[q] < 0) continue;
+            const int p = p0 + q * kBlock + tid;
+            const u64 add = ((p >= L - P.fp_win) ? 1ull : 0ull) | ((p >= L - P.dry_win) ? (1ull << 16) : 0ull) |
+                            ((p >= L - P.rep_win) ? (1ull << 32) : 0ull);
+            if (add) atomicAdd(&tval[sl[q]], add);
+        }
+        if (t[8] >= 0) atomicAdd(&tval[sl[8]], 1ull << 63);
         __syncthreads();
-        {
-            uint32_t tt = st.twave[0];
 #pragma unroll
-            for (int i = 1; i < kBlock / 64; ++i) tt = min(tt, st.twave[i]);
-            const u64 tl = (u64)tt << 32;
-            __syncthreads();
-            if (tid == 0 && tl > st.theta) st.theta = tl;
-            __syncthreads();
+        for (int q = 0; q < 9; ++q) {
+            if (!((own >> q) & 1u)) continue;
+            const u64 c = tval[sl[q]];
+            const uint32_t v = ((c >> 32) & 0xFFFFull ? HV_REP : 0u) | ((c >> 63) ? HV_BIAS : 0u) |
+                               ((uint32_t)((c >> 16) & 0xFFFFull) << HV_DRY_SHIFT) | (uint32_t)(c & 0xFFFFull);
+            float y = ((mw[q] >> (t[q] & 31)) & 1u) ? x[q] : -__builtin_inff();
+            y = pen_value(y, t[q], v, sa, sP);
+            if (greedy) {
+                if (y != y) {
+                    atomicOr(&st.flags, 4);
+                    if (t[q] == 0) atomicOr(&st.nan0, 1);
+                    continue;
+                }
+            } else {
+                if (P.flags & RF_TEMP) y = y * P.inv_temp;
+                if (y != y) {
+                    atomicOr(&st.flags, 4);
+                    y = -__builtin_inff();
+                }
+            }
+            cp[q] = comp(key32(y), t[q]);
         }
-        append_regs<NM>(buf, cap, kv, [&](int i) { return id[i]; }, ovf, st);
-        drain_overflow(buf, cap, k, ovf, st);
     }
+
+    // the ragged end, unless penalised
+    auto in_table = [&](int32_t t) -> bool {
+        uint32_t s0 = ((uint32_t)t * 0x9E3779B1u) >> hshift;
+        for (;;) {
+            const uint32_t kk = tkey[s0];
+            if (kk == (uint32_t)t || kk == kEmpty) return kk == (uint32_t)t;
+            s0 = (s0 + 1u) & hmask;
+        }
+    };
+    u64 ct = 0ull;
+    if (tail_t >= 0 && !(pen && in_table(tail_t))) ct = tail_candidate(tail_x, tail_ok, tail_t, greedy, P.inv_temp, st);
+
+    // ---- the slices' lists ----------------------------------------------------------
+    int extra = 0;
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+        const int g = tid + j * kBlock;
+        const int s2 = (int)__umulhi((uint32_t)g, a.win_magic);   // g / W
+        if (s2 >= S || g - s2 * W >= st.soff[s2]) win[j] = 0ull;
+    }
+    for (int s2 = 0; s2 < S; ++s2) extra += max(0, st.soff[s2] - W);
+
+    if (greedy) {
+        u64 best = ct;
+#pragma unroll
+        for (int q = 0; q < 9; ++q) best = cp[q] > best ? cp[q] : best;
+#pragma unroll
+        for (int j = 0; j < NW; ++j) best = win[j] > best ? win[j] : best;
+        best = block_max_u64(best, st);
+        __syncthreads();
+        if (tid == 0) {
+            // argmax returns 0 when id 0 holds a NaN: a penalised id 0 was
+            // settled with the table, any other by its logit
+            const bool pen0 = pen && in_table(0);
+            const bool nan0 = pen0 ? st.nan0 != 0 : nan_at0;
+            a.token[r] = nan0 ? 0 : comp_idx(best);
+            if (a.row_flags != nullptr) a.row_flags[r] = ROWF_GREEDY | ((st.flags & 4) ? ROWF_NAN : 0u);
+            if (a.topk_count != nullptr) a.topk_count[r] = -1;
+            if (a.kept_count != nullptr) a.kept_count[r] = 0;
+        }
+        return;
+    }
+
+    // ---- exact top-k ----------------------------------------------------------------
+    constexpr int NC = 10 + NW;
+    const uint32_t floor_key = (uint32_t)(kThetaFloor >> 32);
+    uint32_t lmax = (uint32_t)(ct >> 32);
+#pragma unroll
+    for (int q = 0; q < 9; ++q) lmax = max(lmax, (uint32_t)(cp[q] >> 32));
+#pragma unroll
+    for (int j = 0; j < NW; ++j) lmax = max(lmax, (uint32_t)(win[j] >> 32));
+    const int kw = (k + 3) >> 2;
+    const uint32_t g4[4] = {lmax, 0u, 0u, 0u};
+    const uint32_t tw = wave_kth_bound16(g4, 1, kw);
+    uint32_t wm = lmax;
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) wm = max(wm, (uint32_t)__shfl_xor((int)wm, d, 64));
+    if (lane == 0) {
+        st.twave[wave_id()] = tw;
+        st.minv_w[wave_id()] = wm;
+    }
+    __syncthreads();
+    uint32_t Lk = st.twave[0], Mk = (uint32_t)st.minv_w[0];
+#pragma unroll
+    for (int i = 1; i < kBlock / 64; ++i) {
+        Lk = min(Lk, st.twave[i]);
+        Mk = max(Mk, (uint32_t)st.minv_w[i]);
+    }
+    Lk = max(Lk, floor_key);
+    const int hb = (Mk > Lk) ? 31 - __clz((int)(Lk ^ Mk)) : 0;
+    const int shift = max(0, hb - 10);
+    auto binof = [&](uint32_t key) -> uint32_t { return (key >> shift) & 2047u; };
+    const bool any = Mk >= Lk;
+    if (any) {
+        if ((uint32_t)(ct >> 32) >= Lk) atomicAdd(&bins[binof((uint32_t)(ct >> 32))], 1u);
+#pragma unroll
+        for (int q = 0; q < 9; ++q) {
+            const uint32_t key = (uint32_t)(cp[q] >> 32);
+            if (key >= Lk) atomicAdd(&bins[binof(key)], 1u);
+        }
+#pragma unroll
+        for (int j = 0; j < NW; ++j) {
+            const uint32_t key = (uint32_t)(win[j] >> 32);
+            if (key >= Lk) atomicAdd(&bins[binof(key)], 1u);
+        }
+    }
+    __syncthreads();
+    // the bin holding the k-th largest, counting down from the top bin
+    {
+        const uint4 lo4 = reinterpret_cast<const uint4*>(bins)[(2047 - 8 * tid - 7) >> 2];
+        const uint4 hi4 = reinterpret_cast<const uint4*>(bins)[(2047 - 8 * tid - 3) >> 2];
+        const uint32_t c8[8] = {hi4.w, hi4.z, hi4.y, hi4.x, lo4.w, lo4.z, lo4.y, lo4.x};   // bins 2047-8t downwards
+        int sum8 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sum8 += (int)c8[i];
+        int total;
+        const int excl = block_excl_scan(sum8, &total, st);
+        if (tid == 0) {
+            st.sel_d = -1;         // fewer than k entries: all of them
+            st.sel_need = total;
+        }
+        __syncthreads();
+        if (excl < k && excl + sum8 >= k) {
+            int cum = excl;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (cum + (int)c8[i] >= k) {
+                    st.sel_d = 2047 - 8 * tid - i;
+                    st.sel_need = cum + (int)c8[i];   // entries at or above the bin
+                    break;
+                }
+                cum += (int)c8[i];
+            }
+        }
+        __syncthreads();
+    }
+    const int bstar = st.sel_d;
+    const int nlist = st.sel_need;
+    if (nlist < 128 && extra == 0) {
+        // entries at or above the k-th's bin, then an exact rank by wave 0
+        uint32_t inm = 0u;   // which of this thread's NC candidates go to the list
+#pragma unroll
+        for (int q = 0; q < NC; ++q) {
+            const u64 c = (q < 9) ? cp[q] : (q == 9 ? ct : win[q - 10 < 0 ? 0 : q - 10]);
+            const uint32_t key = (uint32_t)(c >> 32);
+            inm |= (any && key >= Lk && (int)binof(key) >= bstar) ? (1u << q) : 0u;
+        }
+        if (__ballot(inm != 0u) != 0ull) {
+            const int cnt = __popc(inm);
+            int incl = cnt;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const int y = __shfl_up(incl, d, 64);
+                if (lane >= d) incl += y;
+            }
+            int base = 0;
+            if (lane == 63) base = atomicAdd(&st.n, incl);
+            int pos = __shfl(base, 63, 64) + incl - cnt;
+#pragma unroll
+            for (int q = 0; q < NC; ++q)
+                if ((inm >> q) & 1u) list[pos++] = (q < 9) ? cp[q] : (q == 9 ? ct : win[q - 10 < 0 ? 0 : q - 10]);
+        }
+        __syncthreads();
+        const uint32_t rflags = (st.flags & 4) ? ROWF_NAN : 0u;
+        if (tid >= 64) return;
+        const int n = st.n;
+        if (lane == 0) list[n] = 0ull;   // pad to pairs
+        wave_sync();
+        const u64 m0 = (lane < n) ? list[lane] : 0ull;
+        const u64 m1 = (lane + 64 < n) ? list[lane + 64] : 0ull;
+        int r0 = 0, r1 = 0;
+        const ulonglong2* l2 = reinterpret_cast<const ulonglong2*>(list);
+#pragma unroll 4
+        for (int j = 0; j < (n + 1) >> 1; ++j) {
+            const ulonglong2 x2 = l2[j];
+            r0 += (x2.x > m0) + (x2.y > m0);
+            r1 += (x2.x > m1) + (x2.y > m1);
+        }
+        wave_sync();
+        if (lane < n && r0 < k) st.wv[r0] = m0;
+        if (lane + 64 < n && r1 < k) st.wv[r1] = m1;
+        wave_sync();
+        const int nk = min(k, n);
+        const u64 c = (lane < nk) ? st.wv[lane] : 0ull;
+        wave_sync();
+        wave_finalize(sa, sP, r, c, nk, rflags, st);
+        return;
+    }
+    // buffer path: the table is dead, the buffer takes its place
+    u64* buf = reinterpret_cast<u64*>(smem + 9216);
+    u64* ovf = a.ovf + (int64_t)r * a.ovf_cap;
+    if (tid == 0) st.theta = (u64)Lk << 32;
+    __syncthreads();
+    offer_regs<9>(buf, ovf, a.buf_cap, k, cp, st);
+    {
+        const u64 c1[1] = {ct};
+        offer_regs<1>(buf, ovf, a.buf_cap, k, c1, st);
+    }
+    offer_regs<NW>(buf, ovf, a.buf_cap, k, win, st);
+    const u64* cand = a.cand + (int64_t)r * S * a.cand_cap;
+    if (extra > 0) {
+        for (int s2 = 0; s2 < S; ++s2) {
+            const int n = st.soff[s2];
+            for (int e0 = W; e0 < n; e0 += 8 * kBlock) {
+                u64 c[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const int e = e0 + q * kBlock + tid;
+                    c[q] = (e < n) ? cand[(int64_t)s2 * a.cand_cap + e] : 0ull;
+                }
+                offer_regs<8>(buf, ovf, a.buf_cap, k, c, st);
+            }
+        }
+    }
+    __syncthreads();
+    const uint32_t rflags = (st.flags & 4) ? ROWF_NAN : 0u;
+    FinLds f{};
+    select_and_finalize(sa, sP, r, buf, f, st, rflags);
 }
 
 // One block per row: finish the penalised ids, merge everything into the
 // row's exact top-k (or argmax) and run the rest of the ladder.
+//  - All first loads go out together: the history window, the slice counts,
+//    the first `win` entries of every slice's list (NW per thread, entry g
+//    of the window is slice g / win, position g % win) and u.
+//  - The penalty table is built from the history; every id in it is
+//    penalised: its logit is read from the row, masked, and run through
+//    stages 1-6 (sampler.cpp:235-264) with the table's counts.
+//  - Entries beyond a slice's window (rare) are offered in a second pass.
+template <bool GT, bool FAST>
 __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ Shared st;
     __shared__ StreamArgs sa;
     __shared__ RowPlan sP;
-    __shared__ int poff[kBlock + 1];
+    constexpr int NW = 16;
     const int tid = threadIdx.x;
     const int r = (int)blockIdx.x;
     if (r >= a.rows) return;
     const RowPlan P = a.plans[r];
-    const int S = a.nslices;
+    const int S = a.nslices, W = a.win;
     const bool greedy = (P.flags & RF_GREEDY) != 0;
     const bool pen = (P.flags & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) != 0;
+    const bool masked = (P.flags & RF_MASK) != 0;
     const int k = P.top_k;
+    const u64* cand = a.cand + (int64_t)r * S * a.cand_cap;
     if (tid == 0) {
-        sa = a;
-        sP = P;
         st.flags = 0;
         st.nan0 = 0;
         st.n = 0;
         st.theta = kThetaFloor;
     }
+    int32_t pre[8];
+    hist_prefetch(a, P, r, pen, pre);
+    const int32_t bias_t = (FAST && (P.flags & RF_BIAS) && tid < P.bias_cnt) ? a.bias_ids[P.bias_off + tid] : -1;
+    const int cnt_raw = (tid < S) ? a.cand_n[(int64_t)r * S + tid] : 0;
+    const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * (a.dtype == 0 ? 4 : 2);
+    bool nan_at0 = false;   // greedy: id 0 holds an allowed NaN
+    if (greedy && tid == 0) {
+        const float x0 = (a.dtype == 0) ? load_logit<0>(rowp, 0) : load_logit<1>(rowp, 0);
+        nan_at0 = x0 != x0 && (!masked || (a.mask[(int64_t)r * a.mask_stride] & 1u));
+    }
+    // the row's ragged end (ids the stream's whole-chunk loads leave out)
+    const int32_t tail_t = (tid < a.vec_tail) ? a.vocab - a.vec_tail + tid : -1;
+    float tail_x = 0.0f;
+    bool tail_ok = true;
+    if (tail_t >= 0) {
+        tail_x = (a.dtype == 0) ? load_logit<0>(rowp, tail_t) : load_logit<1>(rowp, tail_t);
+        if (masked) tail_ok = (a.mask[(int64_t)r * a.mask_stride + (tail_t >> 5)] >> (tail_t & 31)) & 1u;
+    }
+    u64 win[NW];
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+        const int g = tid + j * kBlock;
+        const int sl = (int)__umulhi((uint32_t)g, a.win_magic);   // g / W
+        win[j] = (sl < S) ? cand[(int64_t)sl * a.cand_cap + (g - sl * W)] : 0ull;
+    }
+    if (tid == 0) {
+        sa = a;
+        sP = P;
+        st.u = a.u[r];
+    }
+    if (tid < 32) st.expT[tid] = kExpT[tid];
+    __syncthreads();
+    if (tid < S) {
+        st.soff[tid] = cnt_raw & 0x1FFFFFFF;
+        if (cnt_raw & (1 << 30)) atomicOr(&st.flags, 4);   // a NaN logit in the slice
+    }
+    if (FAST) {
+        merge_fast<NW>(a, P, r, pre, bias_t, nan_at0, tail_t, tail_x, tail_ok, win, smem, st, sa, sP);
+        return;
+    }
     // LDS: [row penalty table | finalize scratch] aliased, then the buffer.
-    const PenaltyLds pl = pen_table(a, r, smem);
+    const PenaltyLds pl = pen_table<GT>(a, r, smem);
+    if (pen) pen_build_row(a, P, r, pl, pre);   // its barriers publish the counts too
+    else __syncthreads();
+    u64* buf = reinterpret_cast<u64*>(smem + (a.merge_lds - (uint32_t)a.buf_cap * 8u));
+    u64* ovf = a.ovf + (int64_t)r * a.ovf_cap;
+    u64 best = 0ull;   // greedy
+
+    if (pen) {
+        // stages 1-6 for every penalised id (sampler.cpp:235-264), 8 slots per thread per pass
+        const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * (a.dtype == 0 ? 4 : 2);
+        const uint32_t* mrow = masked ? a.mask + (int64_t)r * a.mask_stride : nullptr;
+        for (int base = 0; base < a.mhash_slots; base += 8 * kBlock) {
+            int32_t t[8];
+            float x[8];
+            uint32_t mw[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int i = base + q * kBlock + tid;
+                t[q] = (i < a.mhash_slots) ? (int32_t)tab_ld(&pl.hkey[i]) : -1;   // kEmpty reads as -1
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                x[q] = 0.0f;
+                mw[q] = 0xFFFFFFFFu;
+                if (t[q] >= 0) {
+                    x[q] = (a.dtype == 0) ? load_logit<0>(rowp, t[q]) : load_logit<1>(rowp, t[q]);
+                    if (masked) mw[q] = mrow[t[q] >> 5];
+                }
+            }
+            u64 c[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                c[q] = 0ull;
+                if (t[q] < 0) continue;
+                float y = ((mw[q] >> (t[q] & 31)) & 1u) ? x[q] : -__builtin_inff();
+                y = pen_apply(y, t[q], sa, sP, pl);
+                if (greedy) {
+                    if (y != y) {
+                        atomicOr(&st.flags, 4);
+                        if (t[q] == 0) atomicOr(&st.nan0, 1);
+                        continue;
+                    }
+                } else {
+                    if (P.flags & RF_TEMP) y = y * P.inv_temp;
+                    if (y != y) {
+                        atomicOr(&st.flags, 4);
+                        y = -__builtin_inff();
+                    }
+                }
+                c[q] = comp(key32(y), t[q]);
+            }
+            if (greedy) {
+#pragma unroll
+                for (int q = 0; q < 8; ++q) best = c[q] > best ? c[q] : best;
+            } else {
+                offer_regs<8>(buf, ovf, a.buf_cap, k, c, st);
+            }
+        }
+    }
+
+    // the ragged end, unless penalised
+    u64 ct = 0ull;
+    if (tail_t >= 0) {
+        bool pt = false;
+        if (pen) {
+            uint32_t s0 = hslot(tail_t, pl);
+            uint32_t kk;
+            while ((kk = tab_ld(&pl.hkey[s0])) != kEmpty && kk != (uint32_t)tail_t) s0 = (s0 + 1) & pl.hmask;
+            pt = kk == (uint32_t)tail_t;
+        }
+        if (!pt) ct = tail_candidate(tail_x, tail_ok, tail_t, greedy, P.inv_temp, st);
+    }
+    best = ct > best ? ct : best;
+    // the slices' lists: the window entries, then whatever lies beyond it
+    int extra = 0;
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+        const int g = tid + j * kBlock;
+        const int sl = (int)__umulhi((uint32_t)g, a.win_magic);   // g / W
+        if (sl >= S || g - sl * W >= st.soff[sl]) win[j] = 0ull;
+    }
+    for (int sl = 0; sl < S; ++sl) extra += max(0, st.soff[sl] - W);
+    if (greedy) {
+#pragma unroll
+        for (int j = 0; j < NW; ++j) best = win[j] > best ? win[j] : best;
+        best = block_max_u64(best, st);
+        __syncthreads();
+        if (tid == 0) {
+            bool pen0 = false;   // id 0 penalised: settled with the table
+            if (pen) {
+                uint32_t s0 = hslot(0, pl);
+                uint32_t kk;
+                while ((kk = tab_ld(&pl.hkey[s0])) != kEmpty && kk != 0u) s0 = (s0 + 1) & pl.hmask;
+                pen0 = kk == 0u;
+            }
+            const bool nan0 = pen0 ? st.nan0 != 0 : nan_at0;
+            a.token[r] = nan0 ? 0 : comp_idx(best);
+            if (a.row_flags != nullptr) a.row_flags[r] = ROWF_GREEDY | ((st.flags & 4) ? ROWF_NAN : 0u);
+            if (a.topk_count != nullptr) a.topk_count[r] = -1;
+            if (a.kept_count != nullptr) a.kept_count[r] = 0;
+        }
+        return;
+    }
+    {
+        const u64 c1[1] = {ct};
+        offer_regs<1>(buf, ovf, a.buf_cap, k, c1, st);
+    }
+    offer_regs<NW>(buf, ovf, a.buf_cap, k, win, st);
+    if (extra > 0) {
+        for (int sl = 0; sl < S; ++sl) {
+            const int n = st.soff[sl];
+            for (int e0 = W; e0 < n; e0 += 8 * kBlock) {
+                u64 c[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const int e = e0 + q * kBlock + tid;
+                    c[q] = (e < n) ? cand[(int64_t)sl * a.cand_cap + e] : 0ull;
+                }
+                offer_regs<8>(buf, ovf, a.buf_cap, k, c, st);
+            }
+        }
+    }
+    __syncthreads();
+    const uint32_t rflags = (st.flags & 4) ? ROWF_NAN : 0u;
     const int kP2 = next_pow2(max(a.kmax, 1));
     FinLds f;
     f.sortk = reinterpret_cast<u64*>(smem);
@@ -1455,85 +2020,12 @@ __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
     f.fe = f.fv + a.kmax;
     f.fp = f.fe + a.kmax;
     f.keep = reinterpret_cast<int32_t*>(f.fp + a.kmax);
-    u64* buf = reinterpret_cast<u64*>(smem + (a.merge_lds - (uint32_t)a.buf_cap * 8u));
-    u64* ovf = a.ovf + (int64_t)r * a.ovf_cap;
-    const u64* cand = a.cand + (int64_t)r * S * a.cand_cap;
-
-    // slice counts -> offsets of the concatenated candidate and pend lists
-    int myc = 0, myp = 0, fl = 0;
-    if (tid < S) {
-        const int v = a.cand_n[(int64_t)r * S + tid];
-        myc = v & 0x1FFFFFFF;
-        fl = v >> 29;
-        myp = a.pend_n[(int64_t)r * S + tid];
-    }
-    int M, NP;
-    const int off = block_excl_scan(myc, &M, st);
-    const int offp = block_excl_scan(myp, &NP, st);
-    if (tid < S) {
-        st.soff[tid] = off;
-        poff[tid] = offp;
-    }
-    if (tid == 0) {
-        st.soff[S] = M;
-        poff[S] = NP;
-    }
-    if (fl & 2) atomicOr(&st.flags, 4);      // a NaN logit somewhere in the row
-    if (fl & 1) atomicOr(&st.nan0, 1);       // greedy: id 0 is NaN
-    if (pen) pen_build_row(a, P, r, pl);
-    else __syncthreads();
-
-    // penalised ids: stages 1-6 from the table (sampler.cpp:235-264)
-    auto pen_xf = [&](u64 e) -> u64 {
-        const int32_t t = (int32_t)(e >> 32);
-        float x = pen_apply(__uint_as_float((uint32_t)e), t, sa, sP, pl);
-        if (greedy) {
-            if (x != x) {
-                atomicOr(&st.flags, 4);
-                if (t == 0) atomicOr(&st.nan0, 1);
-                return 0ull;
-            }
-            return comp(key32(x), t);
-        }
-        if (P.flags & RF_TEMP) x = x * P.inv_temp;
-        if (x != x) {
-            atomicOr(&st.flags, 4);
-            x = -__builtin_inff();
-        }
-        return comp(key32(x), t);
-    };
-    const u64* pend = a.pend + (int64_t)r * S * a.pend_cap;
-    if (greedy) {
-        u64 b = 0ull;
-        for (int i = tid; i < S; i += kBlock) {
-            const u64 c = cand[(int64_t)i * a.cand_cap];
-            b = c > b ? c : b;
-        }
-        for (int fi = tid; fi < NP; fi += kBlock) {
-            const int sl = find_slice(poff, S, fi);
-            const u64 c = pen_xf(pend[(int64_t)sl * a.pend_cap + (fi - poff[sl])]);
-            b = c > b ? c : b;
-        }
-        b = block_max_u64(b, st);
-        __syncthreads();
-        if (tid == 0) {
-            a.token[r] = st.nan0 ? 0 : comp_idx(b);
-            if (a.row_flags != nullptr) a.row_flags[r] = ROWF_GREEDY | ((st.flags & 4) ? ROWF_NAN : 0u);
-            if (a.topk_count != nullptr) a.topk_count[r] = -1;
-            if (a.kept_count != nullptr) a.kept_count[r] = 0;
-        }
-        return;
-    }
-    offer(buf, ovf, a.buf_cap, k, NP, pend, a.pend_cap, poff, S, pen_xf, st);
-    offer(buf, ovf, a.buf_cap, k, M, cand, a.cand_cap, st.soff, S, [](u64 e) { return e; }, st);
-    __syncthreads();
-    const uint32_t rflags = (st.flags & 4) ? ROWF_NAN : 0u;
     select_and_finalize(sa, sP, r, buf, f, st, rflags);
 }
 
 // ---- writeback -------------------------------------------------------------------
 
-template <bool VEC>
+template <bool GT>
 __global__ __launch_bounds__(kBlock) void k_writeback(StreamArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ StreamArgs sa;
@@ -1553,11 +2045,13 @@ __global__ __launch_bounds__(kBlock) void k_writeback(StreamArgs a) {
     const bool greedy = (P.flags & RF_GREEDY) != 0;
     const bool pen = (P.flags & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) != 0;
     // LDS: [row penalty table (when not global)] [kept ids of this slice]
-    const PenaltyLds pl = pen_table(a, r, smem);
-    uint32_t* keepbm = reinterpret_cast<uint32_t*>(smem) + (a.gtab != nullptr ? 0 : 2 * a.mhash_slots);
+    const PenaltyLds pl = pen_table<GT>(a, r, smem);
+    uint32_t* keepbm = reinterpret_cast<uint32_t*>(smem) + (GT ? 0 : 2 * a.mhash_slots);
+    int32_t pre[8];
+    hist_prefetch(a, P, r, pen && !GT, pre);
     for (int i = tid; i < a.bitmap_words; i += kBlock) keepbm[i] = 0u;
     // a global table is the one k_merge built for this row; an LDS one is rebuilt
-    if (pen && a.gtab == nullptr) pen_build_row(a, P, r, pl);
+    if (pen && !GT) pen_build_row(a, P, r, pl, pre);
     else __syncthreads();
     if (!greedy) {
         const int n = a.fin_n[r];
@@ -1589,25 +2083,45 @@ __global__ __launch_bounds__(kBlock) void k_writeback(StreamArgs a) {
 
 // ---- launchers -------------------------------------------------------------------
 
-hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, int grid, hipStream_t stream) {
+hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int grid,
+                         hipStream_t stream) {
     const dim3 g(grid), b(kBlock);
-    if (dtype == 0) {
-        if (vec) hipLaunchKernelGGL((k_stream<0, true>), g, b, a.lds_bytes, stream, a);
-        else hipLaunchKernelGGL((k_stream<0, false>), g, b, a.lds_bytes, stream, a);
+    const uint32_t l = a.lds_bytes;
+#define HSAMP_STREAM(DT_, V_, P_, M_) hipLaunchKernelGGL((k_stream<DT_, V_, P_, M_>), g, b, l, stream, a)
+    if (!vec) {   // unaligned rows: one general kernel per element type
+        if (dtype == 0) HSAMP_STREAM(0, false, true, true);
+        else HSAMP_STREAM(1, false, true, true);
+    } else if (dtype == 0) {
+        if (pen) {
+            if (mask) HSAMP_STREAM(0, true, true, true);
+            else HSAMP_STREAM(0, true, true, false);
+        } else {
+            if (mask) HSAMP_STREAM(0, true, false, true);
+            else HSAMP_STREAM(0, true, false, false);
+        }
     } else {
-        if (vec) hipLaunchKernelGGL((k_stream<1, true>), g, b, a.lds_bytes, stream, a);
-        else hipLaunchKernelGGL((k_stream<1, false>), g, b, a.lds_bytes, stream, a);
+        if (pen) {
+            if (mask) HSAMP_STREAM(1, true, true, true);
+            else HSAMP_STREAM(1, true, true, false);
+        } else {
+            if (mask) HSAMP_STREAM(1, true, false, true);
+            else HSAMP_STREAM(1, true, false, false);
+        }
     }
+#undef HSAMP_STREAM
     return hipGetLastError();
 }
 
 hipError_t launch_merge(const StreamArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL(k_merge, dim3(a.rows), dim3(kBlock), a.merge_lds, stream, a);
+    if (a.fast) hipLaunchKernelGGL((k_merge<false, true>), dim3(a.rows), dim3(kBlock), a.merge_lds, stream, a);
+    else if (a.gtab != nullptr) hipLaunchKernelGGL((k_merge<true, false>), dim3(a.rows), dim3(kBlock), a.merge_lds, stream, a);
+    else hipLaunchKernelGGL((k_merge<false, false>), dim3(a.rows), dim3(kBlock), a.merge_lds, stream, a);
     return hipGetLastError();
 }
 
 hipError_t launch_writeback(const StreamArgs& a, int grid, uint32_t lds, hipStream_t stream) {
-    hipLaunchKernelGGL((k_writeback<true>), dim3(grid), dim3(kBlock), lds, stream, a);
+    if (a.gtab != nullptr) hipLaunchKernelGGL((k_writeback<true>), dim3(grid), dim3(kBlock), lds, stream, a);
+    else hipLaunchKernelGGL((k_writeback<false>), dim3(grid), dim3(kBlock), lds, stream, a);
     return hipGetLastError();
 }
 

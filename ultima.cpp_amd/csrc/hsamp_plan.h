@@ -41,7 +41,7 @@ enum : uint32_t {
 };
 
 struct alignas(16) RowPlan {
-    float inv_temp;     // fl(1.0f / T) when RF_TEMP
+    float inv_temp;     // fl(1.0f / T) when RF_TEMP, else 1.0f
     float rep;          // repetition penalty
     float freq;         // frequency penalty
     float pres;         // presence penalty
@@ -100,9 +100,11 @@ struct StreamArgs {
     int32_t* fin_n;             // [rows]
     unsigned long long* ovf;    // [blocks * ovf_cap] per-block overflow of the LDS buffer
     int32_t ovf_cap;            // one tile of candidates
-    unsigned long long* pend;   // [blocks * pend_cap] (id << 32 | raw logit bits) of penalised ids
-    int32_t* pend_n;            // [rows * S]
-    int32_t pend_cap;
+    int32_t win;                // entries of each slice's list k_merge loads up front
+    uint32_t win_magic;         // floor(2^32 / win) + 1: umulhi(g, win_magic) == g / win for g < 2^16
+    int32_t dtype;              // logits element type (0 f32, 1 bf16)
+    int32_t fast;               // every row fits k_merge's fast path
+    int32_t vec_tail;           // the row's last ids k_merge reads itself (V % chunk with vector loads)
     uint32_t* gtab;             // [rows * 2 * mhash_slots] penalty tables, or NULL: tables in LDS
     uint32_t merge_lds;         // dynamic LDS of k_merge
     uint32_t lds_bytes;         // dynamic LDS size of the launch

@@ -7,7 +7,10 @@ data, resident in HBM before timing. Eight distinct input sets (315 MB, more
 than the 256 MB Infinity Cache) rotate so the kernel streams from HBM.
 
 The launches of one rotation are captured into a HIP graph (torch.cuda.CUDAGraph)
-and replayed; HIP events on the launch stream bracket the K timed steps.
+and replayed; HIP events on the launch stream bracket the K timed steps. A
+second, uncaptured pass times the two kernels of each launch apart (events
+around each launch plus one the library records between them); the roofline
+figure is the stream kernel's algorithmic bytes over its own duration.
 Prints one JSON line (see `main`). The CPU baseline is the reference's own
 sampler (oracle/_ref, compiled from its sources) or, where that was not
 built, the CPU restatement, timed on this host's cores on a bounded sample.
@@ -40,6 +43,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=1.5,
                     help="wall seconds of the CPU baseline sample (all threads)")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="also run 3 device-to-device copies of this many MiB (a known-size "
+                         "kernel that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
 
 
@@ -148,6 +154,27 @@ def main():
     ms_total = t0e.elapsed_time(t1e)
     ms_step = ms_total / steps
 
+    # Per-kernel split, live: the same launches uncaptured, each bracketed by
+    # events on the launch stream, with the library recording a third event
+    # between the stream pass (k_stream, reads the logits) and the per-row
+    # merge (k_merge).
+    n_split = max(N_SETS, min(steps, 25 * N_SETS))
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n_split)]
+    with torch.cuda.stream(stream):
+        for e in ev:
+            e[1].record(stream)           # creates the event the library records
+    stream.synchronize()
+    with torch.cuda.stream(stream):
+        for i in range(n_split):
+            ev[i][0].record(stream)
+            sampler.set_phase_event(ev[i][1])
+            launch(i % N_SETS, stream)
+            ev[i][2].record(stream)
+    stream.synchronize()
+    sampler.set_phase_event(None)
+    stream_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / n_split
+    merge_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / n_split
+
     # The replayed outputs are the real ones: spot-check them against an
     # uncaptured launch of the same inputs.
     ref_tok = [o["token"].clone() for o in outs]
@@ -160,7 +187,7 @@ def main():
             raise SystemExit("graph replay and direct launch disagree")
 
     algo_bytes = wl0.algorithmic_bytes()
-    achieved = algo_bytes / (ms_step * 1e-3) / 1e9
+    achieved = algo_bytes / (stream_ms * 1e-3) / 1e9   # k_stream: the kernel that reads the logits
     line = {
         "metric": METRIC,
         "value": B / (ms_step * 1e-3),
@@ -178,12 +205,23 @@ def main():
                                + ("hist 2048 rep 1.1 freq .5 pres .3 T .7 top-k 50"
                                   if args.config == 2 else wl0.name),
                    "rows": B, "vocab": V, "input_sets": N_SETS,
-                   "bytes_per_step": algo_bytes, "wall_s": round(wall, 4)},
+                   "bytes_per_step": algo_bytes, "wall_s": round(wall, 4),
+                   "kernel_us": {"k_stream": round(stream_ms * 1e3, 3), "k_merge": round(merge_ms * 1e3, 3),
+                                 "launches_timed": n_split},
+                   "step_hbm_gbs": round(algo_bytes / (ms_step * 1e-3) / 1e9, 1)},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_GBS, "traffic": traffic_from_profiles(args.config),
                      "kernel": "k_stream", "algorithmic_bytes_per_launch": algo_bytes},
         "cpu_baseline": None,
     }
+    if args.copy_probe_mib > 0:
+        n = args.copy_probe_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        line["config"]["copy_probe_bytes"] = n * 4
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(wl0, args.cpu_seconds)
     sampler.close()

@@ -161,6 +161,12 @@ const char* ultima_hsamp_status_str(int status);
 /* ULTIMA_HSAMP_VERSION of the loaded library. */
 int ultima_hsamp_version(void);
 
+/* Diagnostics, no counterpart in the reference: while set (non-NULL), every
+ * ultima_hsamp_run() also records this hipEvent_t on its stream between the
+ * stream pass (reads the logits) and the per-row merge, so a caller can time
+ * the two kernels apart with its own events. NULL stops it. */
+int ultima_hsamp_set_phase_event(ultima_hsamp* h, void* hip_event);
+
 #ifdef __cplusplus
 }
 #endif

@@ -65,6 +65,7 @@ struct ultima_hsamp {
     int32_t max_vocab = 0;
     size_t lds_limit = 0;         // LDS bytes one block may use on this device
     hipStream_t own_stream = nullptr;
+    hipEvent_t phase_ev = nullptr;   // recorded between the stream and merge kernels when set
     Slot slots[kSlots];
     int next_slot = 0;
     std::vector<char> blob;
@@ -336,6 +337,12 @@ extern "C" {
 
 int ultima_hsamp_version(void) { return ULTIMA_HSAMP_VERSION; }
 
+int ultima_hsamp_set_phase_event(ultima_hsamp* h, void* hip_event) {
+    if (h == nullptr) return ULTIMA_HSAMP_ERR_INVALID;
+    h->phase_ev = static_cast<hipEvent_t>(hip_event);
+    return ULTIMA_HSAMP_OK;
+}
+
 const char* ultima_hsamp_status_str(int s) {
     switch (s) {
         case ULTIMA_HSAMP_OK: return "ok";
@@ -587,6 +594,7 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
                      ((b->logits_stride * es) % 16 == 0);
     a.vec_tail = vec ? V % (16 / es) : 0;
     HIP_TRY(launch_stream(a, b->dtype, vec, bl.any_pen, bl.any_mask, grid, stream));
+    if (h->phase_ev != nullptr) HIP_TRY(hipEventRecord(h->phase_ev, stream));
     HIP_TRY(launch_merge(a, stream));
     if (wb) HIP_TRY(launch_writeback(a, grid, (uint32_t)wb_lds, stream));
     if (!capturing) HIP_TRY(hipEventRecord(slot->ev, stream));

@@ -115,6 +115,8 @@ def lib() -> ctypes.CDLL:
         L.ultima_hsamp_status_str.argtypes = [ctypes.c_int]
         L.ultima_hsamp_version.restype = ctypes.c_int
         L.ultima_hsamp_version.argtypes = []
+        L.ultima_hsamp_set_phase_event.restype = ctypes.c_int
+        L.ultima_hsamp_set_phase_event.argtypes = [vp, vp]
         _lib = L
     return _lib
 
@@ -227,6 +229,12 @@ class Sampler:
         s = torch.cuda.current_stream(dev) if stream is None else stream
         check(lib().ultima_hsamp_run(self.h, ctypes.byref(b), ctypes.c_void_p(s.cuda_stream)), "run")
         return out
+
+    def set_phase_event(self, event):
+        """Record `event` (a torch.cuda.Event already recorded once, or None)
+        between the stream and merge kernels of every later run()."""
+        ptr = None if event is None else ctypes.c_void_p(event.cuda_event)
+        check(lib().ultima_hsamp_set_phase_event(self.h, ptr), "set_phase_event")
 
     def sample_host(self, logits: np.ndarray, params: dict, hist=None, bias=None, u: float = 0.5,
                     writeback: bool = False):

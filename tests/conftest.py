@@ -45,3 +45,11 @@ def hs(pkg):
     if not torch.cuda.is_available():
         pytest.fail("GPU tests need an MI355X: torch.cuda.is_available() is False")
     return pkg.hsamp
+
+
+@pytest.fixture(scope="session")
+def sampler(hs):
+    """One library handle shared by the GPU parity tests."""
+    s = hs.Sampler(0, max_rows=1024, max_vocab=1 << 18)
+    yield s
+    s.close()

@@ -46,7 +46,13 @@ def compare_rows(wl, g, rows=None, bias=None, writeback=False, exact_probs=True)
     for r in rows:
         tr = run_oracle(wl, r, bias=bias)
         ctx = f"row {r} of {wl.name}"
-        assert int(g["token"][r]) == tr.token, f"{ctx}: token {g['token'][r]} != oracle {tr.token}"
+        flags = int(g["row_flags"][r])
+        if int(g["token"][r]) != tr.token:
+            # the one tolerated mismatch: u within 1e-6 of a CDF boundary, flagged by the GPU
+            assert (flags & 4) and tr.cdf_margin <= 1e-6, \
+                f"{ctx}: token {g['token'][r]} != oracle {tr.token} (cdf margin {tr.cdf_margin})"
+            n += 1
+            continue
         if tr.topk_idx is not None:
             cnt = int(g["topk_count"][r])
             assert cnt == tr.topk_idx.size, f"{ctx}: top-k count {cnt} != {tr.topk_idx.size}"
@@ -59,7 +65,6 @@ def compare_rows(wl, g, rows=None, bias=None, writeback=False, exact_probs=True)
         np.testing.assert_allclose(gp, op, rtol=1e-6, atol=0, err_msg=ctx)
         if exact_probs:
             np.testing.assert_array_equal(gp.view(np.uint32), op.view(np.uint32), err_msg=ctx)
-        flags = int(g["row_flags"][r])
         assert bool(flags & 1) == tr.greedy, ctx
         assert bool(flags & 2) == tr.u_consumed, ctx
         if writeback:

@@ -1,0 +1,87 @@
+"""Rows over the whole vocabulary (top-k off or above 1024): the k_full path.
+
+Every row is compared with the CPU oracle (tests/gpu_helpers.compare_rows):
+token, top-k set, kept set and probabilities bit for bit, row flags. The
+kept sets are large, so the set outputs are sized to V.
+"""
+import numpy as np
+import pytest
+
+from gpu_helpers import compare_rows, run_gpu
+
+pytestmark = pytest.mark.gpu
+
+
+def _wl(wl, V, rows, params, seed=3, sigma=2.0, dtype="f32", hist_len=0, mask=None):
+    x = wl._rows_normal(seed, rows, V, sigma)
+    hist = hl = None
+    if hist_len:
+        hist = (wl.splitmix64(seed * 7 + 1, rows * hist_len) % np.uint64(V)).astype(np.int32).reshape(rows, hist_len)
+        hl = np.full(rows, hist_len, np.int64)
+    logits = x if dtype == "f32" else wl.to_bf16_bits(x)
+    return wl.Workload("full", dtype, logits, [dict(p) for p in params], wl.uniform53(seed + 9, rows),
+                       hist, hl, mask)
+
+
+def test_config3_spike_and_flat_rows(sampler, wl):
+    w = wl.config(3, seed=5, rows=8)
+    g = run_gpu(sampler, w, set_cap=w.vocab)
+    assert compare_rows(w, g) == 8
+
+
+@pytest.mark.parametrize("knobs", [
+    dict(temperature=1.0),                                   # identity(): plain draw over V
+    dict(temperature=0.8, top_p=0.95),
+    dict(temperature=1.3, min_p=0.05),
+    dict(temperature=0.7, top_p=0.9, min_p=0.02),
+    dict(temperature=0.9, top_k=1500, top_p=0.97),            # k above the top-k path's limit
+    dict(temperature=0.9, top_k=3000),
+])
+def test_full_vocab_knobs(sampler, wl, knobs):
+    V, rows = 20011, 6
+    p = wl.identity_params(**knobs)
+    w = _wl(wl, V, rows, [p] * rows)
+    g = run_gpu(sampler, w, set_cap=V)
+    assert compare_rows(w, g) == rows
+
+
+def test_full_vocab_with_penalties_and_bf16(sampler, wl):
+    V, rows = 30000, 4
+    p = wl.identity_params(temperature=0.8, top_p=0.9, rep_penalty=1.15, repeat_last_n=256,
+                           frequency_penalty=0.4, presence_penalty=0.2)
+    for dtype in ("f32", "bf16"):
+        w = _wl(wl, V, rows, [p] * rows, dtype=dtype, hist_len=300)
+        g = run_gpu(sampler, w, set_cap=V)
+        assert compare_rows(w, g) == rows
+
+
+def test_full_vocab_mixed_with_topk_and_greedy_rows(sampler, wl):
+    V, rows = 12000, 6
+    plist = [wl.identity_params(temperature=1.0, top_p=0.9),
+             wl.identity_params(temperature=0.7, top_k=40),
+             wl.identity_params(temperature=0.0),
+             wl.identity_params(temperature=1.2),
+             wl.identity_params(temperature=0.9, top_k=2048, min_p=0.01),
+             wl.identity_params(temperature=0.6, top_k=8, top_p=0.8)]
+    w = _wl(wl, V, rows, plist, seed=8)
+    g = run_gpu(sampler, w, set_cap=V)
+    assert compare_rows(w, g) == rows
+
+
+def test_full_vocab_writeback(sampler, wl):
+    V, rows = 9000, 3
+    p = wl.identity_params(temperature=0.75, top_p=0.8, rep_penalty=1.2, repeat_last_n=64)
+    w = _wl(wl, V, rows, [p] * rows, hist_len=64)
+    g = run_gpu(sampler, w, writeback=True, set_cap=V)
+    assert compare_rows(w, g, writeback=True) == rows
+
+
+def test_full_vocab_all_masked_row_draws_uniformly(sampler, wl):
+    V, rows = 4096, 2
+    mask = np.zeros((rows, V // 32), np.uint32)
+    mask[1, 5] = 1 << 3          # row 1: one allowed id
+    p = wl.identity_params(temperature=1.0, top_p=0.9)
+    w = _wl(wl, V, rows, [p] * rows, mask=mask)
+    g = run_gpu(sampler, w, set_cap=V)
+    assert compare_rows(w, g) == rows
+    assert int(g["row_flags"][0]) & 16          # nothing finite: uniform over V

@@ -28,6 +28,7 @@ hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, bool pen, boo
                          hipStream_t stream);
 hipError_t launch_writeback(const StreamArgs& a, int grid, uint32_t lds, hipStream_t stream);
 hipError_t launch_merge(const StreamArgs& a, hipStream_t stream);
+hipError_t launch_full(const StreamArgs& a, uint32_t lds, hipStream_t stream);
 }  // namespace hsamp
 
 using namespace hsamp;
@@ -79,6 +80,12 @@ struct ultima_hsamp {
     int32_t* fin_idx = nullptr;
     int32_t* fin_n = nullptr;
     unsigned long long* ovf = nullptr;   // per-block overflow of the LDS candidate buffer
+    float* fullv = nullptr;              // full-vocabulary rows: transformed logits
+    size_t fullv_elems = 0;
+    float* fullp = nullptr;              // full-vocabulary rows: probabilities
+    size_t fullp_elems = 0;
+    uint32_t* fullk = nullptr;           // full-vocabulary rows: top-p keys
+    size_t fullk_elems = 0;
     size_t ovf_elems = 0;
     // sample_host staging
     float* d_row = nullptr;
@@ -130,8 +137,8 @@ struct Built {
     int max_scan = 0;          // max history window over penalty rows
     int max_bias = 0;          // max logit-bias entries over rows
     bool any_mask = false;     // the batch carries an allowed-token mask
-    bool any_full = false;     // a sampling row without top-k (not handled here)
-    bool any_big_k = false;    // top_k above kLimitK
+    bool any_full = false;     // a sampling row over the whole vocabulary (k_full)
+    bool any_topk = false;     // a greedy or top-k row (k_stream + k_merge)
 };
 
 // RowPlans + DRY tables + bias into h->blob; the reference's predicates in [].
@@ -238,15 +245,19 @@ int build_blob(ultima_hsamp* h, const ultima_hsamp_batch* b, Built& out) {
             } else if (q.top_k > 0 && q.top_k < (uint64_t)V) {                   // [267, 110]
                 fl |= RF_TOPK;
                 P.top_k = (int32_t)q.top_k;
-                if (P.top_k > kLimitK) out.any_big_k = true;
+                if (P.top_k > kLimitK) fl |= RF_FULL;
             } else {
-                out.any_full = true;
+                fl |= RF_FULL;                                                    // top-k off
             }
+            if (fl & RF_FULL) out.any_full = true;
+            else out.any_topk = true;
             if (q.top_p < 1.0f && !(q.top_p <= 0.0f)) fl |= RF_TOPP;             // [270, 147]
             if (q.min_p > 0.0f) fl |= RF_MINP;                                    // [273, 168]
             P.top_p = q.top_p;
             P.min_p = q.min_p;
-            out.kmax = std::max(out.kmax, P.top_k);
+            if (!(fl & RF_FULL)) out.kmax = std::max(out.kmax, P.top_k);
+        } else {
+            out.any_topk = true;
         }
         P.flags = fl;
         if (fl & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) {
@@ -460,7 +471,7 @@ int ultima_hsamp_destroy(ultima_hsamp* h) {
         if (s.ev) (void)hipEventDestroy(s.ev);
     }
     for (void* p : {(void*)h->ovf, (void*)h->cand, (void*)h->cand_n,
-                    (void*)h->gtab, (void*)h->fin_idx,
+                    (void*)h->gtab, (void*)h->fullv, (void*)h->fullp, (void*)h->fullk, (void*)h->fin_idx,
                     (void*)h->fin_n, (void*)h->d_row, (void*)h->d_hist, (void*)h->d_u, (void*)h->d_tok})
         if (p) (void)hipFree(p);
     for (void* p : {(void*)h->h_row, (void*)h->h_hist, (void*)h->h_u, (void*)h->h_tok})
@@ -480,7 +491,6 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     Built bl;
     st = build_blob(h, b, bl);
     if (st != ULTIMA_HSAMP_OK) return st;
-    if (bl.any_full || bl.any_big_k) return ULTIMA_HSAMP_ERR_UNSUPPORTED;
 
     const int B = b->rows, V = b->vocab;
     const int es = b->dtype == ULTIMA_HSAMP_F32 ? 4 : 2;
@@ -503,8 +513,11 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     const size_t regionF = 8 * (size_t)next_pow2(kmax) + 20 * (size_t)kmax;
     const int mhash = bl.any_pen ? std::max(16, next_pow2(2 * bl.max_pen)) : 16;
     const size_t lds_budget = std::min<size_t>(h->lds_limit, 64 * 1024) - statik;
+    constexpr size_t kFullWork = 24 * 1024;   // k_full: bucket counts, starts, sort batch
     const bool gtab = 8 * (size_t)mhash + 8 * (size_t)buf_cap > lds_budget ||
-                      8 * (size_t)mhash + 4 * (size_t)bitmap_words > lds_budget;
+                      8 * (size_t)mhash + 4 * (size_t)bitmap_words > lds_budget ||
+                      (bl.any_full && 8 * (size_t)mhash + kFullWork > lds_budget);
+    const size_t full_lds = (gtab ? 0 : 8 * (size_t)mhash) + kFullWork;
     size_t merge_lds = align16(std::max(gtab ? 0 : 8 * (size_t)mhash, regionF)) + 8 * (size_t)buf_cap;
     // k_merge's fast path: [bins 8 KB][list 1 KB][table 12 B/slot | buffer]
     const size_t fast_lds = 9216 + std::max(12 * (size_t)mhash, 8 * (size_t)buf_cap);
@@ -512,7 +525,9 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
                       fast_lds <= lds_budget;
     if (fast) merge_lds = std::max(merge_lds, fast_lds);
     const size_t wb_lds = (gtab ? 0 : 8 * (size_t)mhash) + 4 * (size_t)bitmap_words;
-    if (merge_lds + statik > h->lds_limit || wb_lds + statik > h->lds_limit) return ULTIMA_HSAMP_ERR_CAPACITY;
+    if (merge_lds + statik > h->lds_limit || wb_lds + statik > h->lds_limit ||
+        full_lds + statik > h->lds_limit)
+        return ULTIMA_HSAMP_ERR_CAPACITY;
     const int nblocks = B * S;
     const int grid = (nblocks + kXcds - 1) / kXcds * kXcds;
     const int win = std::max(1, std::min(cand_cap, kMergeWindow / S));
@@ -539,6 +554,12 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     st = grow(h->ovf, h->ovf_elems, (size_t)B * kMergeRound, 8);
     if (st == ULTIMA_HSAMP_OK) st = grow(h->cand, h->cand_elems, (size_t)B * S * cand_cap, 8);
     if (st == ULTIMA_HSAMP_OK && gtab) st = grow(h->gtab, h->gtab_words, (size_t)B * 2 * mhash, 4);
+    const int full_p2 = next_pow2(V);
+    if (st == ULTIMA_HSAMP_OK && bl.any_full) {
+        st = grow(h->fullv, h->fullv_elems, (size_t)B * V, 4);
+        if (st == ULTIMA_HSAMP_OK) st = grow(h->fullp, h->fullp_elems, (size_t)B * V, 4);
+        if (st == ULTIMA_HSAMP_OK) st = grow(h->fullk, h->fullk_elems, (size_t)B * 2 * full_p2, 4);
+    }
     if (st != ULTIMA_HSAMP_OK) return st;
 
     Slot* slot = nullptr;
@@ -584,6 +605,10 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     a.win_magic = (uint32_t)((1ull << 32) / (uint64_t)win + 1);
     a.dtype = b->dtype;
     a.fast = fast ? 1 : 0;
+    a.fullv = h->fullv;
+    a.fullp = h->fullp;
+    a.fullk = h->fullk;
+    a.full_p2 = full_p2;
     a.gtab = gtab ? h->gtab : nullptr;
     a.merge_lds = (uint32_t)merge_lds;
     const bool wb = (b->flags & ULTIMA_HSAMP_WRITEBACK) != 0;
@@ -593,9 +618,10 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     const bool vec = (reinterpret_cast<uintptr_t>(b->logits) % 16 == 0) &&
                      ((b->logits_stride * es) % 16 == 0);
     a.vec_tail = vec ? V % (16 / es) : 0;
-    HIP_TRY(launch_stream(a, b->dtype, vec, bl.any_pen, bl.any_mask, grid, stream));
+    if (bl.any_topk) HIP_TRY(launch_stream(a, b->dtype, vec, bl.any_pen, bl.any_mask, grid, stream));
     if (h->phase_ev != nullptr) HIP_TRY(hipEventRecord(h->phase_ev, stream));
-    HIP_TRY(launch_merge(a, stream));
+    if (bl.any_topk) HIP_TRY(launch_merge(a, stream));
+    if (bl.any_full) HIP_TRY(launch_full(a, (uint32_t)full_lds, stream));
     if (wb) HIP_TRY(launch_writeback(a, grid, (uint32_t)wb_lds, stream));
     if (!capturing) HIP_TRY(hipEventRecord(slot->ev, stream));
     return ULTIMA_HSAMP_OK;

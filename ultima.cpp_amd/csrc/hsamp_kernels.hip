@@ -78,6 +78,7 @@ struct Shared {
     float sm_m, sm_inv;
     int cutoff;
     double dS;
+    double dred[4];
     int tok;
 };
 
@@ -1263,6 +1264,7 @@ __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
     const int r = logical / a.nslices, s = logical % a.nslices;
     if (r >= a.rows) return;
     const RowPlan P = a.plans[r];
+    if (P.flags & RF_FULL) return;   // k_full's row
     const int lo = s * a.slice_len;
     const int hi = min(a.vocab - (VEC ? a.vec_tail : 0), lo + a.slice_len);   // k_merge takes the ragged end
     const int words = a.bitmap_words;
@@ -1835,6 +1837,7 @@ __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
     const int r = (int)blockIdx.x;
     if (r >= a.rows) return;
     const RowPlan P = a.plans[r];
+    if (P.flags & RF_FULL) return;   // k_full's row
     const int S = a.nslices, W = a.win;
     const bool greedy = (P.flags & RF_GREEDY) != 0;
     const bool pen = (P.flags & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) != 0;
@@ -2035,6 +2038,7 @@ __global__ __launch_bounds__(kBlock) void k_writeback(StreamArgs a) {
     const int r = logical / a.nslices, s = logical % a.nslices;
     if (r >= a.rows) return;
     const RowPlan P = a.plans[r];
+    if (P.flags & RF_FULL) return;   // k_full writes its rows back itself
     if (tid == 0) {
         sa = a;
         sP = P;
@@ -2081,6 +2085,570 @@ __global__ __launch_bounds__(kBlock) void k_writeback(StreamArgs a) {
     }
 }
 
+// ---- full-vocabulary rows ---------------------------------------------------------
+// Sampling rows whose top-k is off (top_k == 0 or >= V) or above kLimitK: the
+// whole transformed row goes through softmax, top-p, min-p and the draw. One
+// block per row; the row lives in global scratch (fullv, fullp, fullk). The
+// float sums that decide outcomes (the softmax denominator in index order,
+// the top-p cumulative in sorted order) are replayed exactly in the
+// reference's order by one wave; the double sums of the draw are accurate
+// sums whose only effect is within 1e-15 of a CDF boundary (flagged rows).
+
+// Lane-order sequential float sum of x[0..n) (values >= +0) by one wave, from
+// +0.0f, 64 values per step through the wave's LDS scratch.
+__device__ float wave_seq_sum_arr(const float* x, int n, u64* wv) {
+    const int lane = lane_id();
+    float* w = reinterpret_cast<float*>(wv);
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    float s = 0.0f;
+    float nxt = (lane < n) ? x[lane] : 0.0f;
+    for (int base = 0; base < n; base += 64) {
+        const float cur = nxt;
+        nxt = (base + 64 + lane < n) ? x[base + 64 + lane] : 0.0f;
+        w[lane] = cur;
+        wave_sync();
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const float4 v = w4[q];
+            s = s + v.x;
+            s = s + v.y;
+            s = s + v.z;
+            s = s + v.w;
+        }
+        wave_sync();
+    }
+    return s;
+}
+
+// Continue the sequential float sum `cum` over the keys k[0..n) (float bits of
+// values >= 0, in LDS or global memory): the first j whose running sum is >=
+// thr, with that sum in *at; -1 when none (cum then holds the total).
+__device__ int wave_seq_find(const uint32_t* k, int n, float thr, float& cum, float* at, u64* wv) {
+    const int lane = lane_id();
+    uint32_t* w = reinterpret_cast<uint32_t*>(wv);
+    const uint4* w4 = reinterpret_cast<const uint4*>(w);
+    float s = cum;
+    for (int base = 0; base < n; base += 64) {
+        w[lane] = (base + lane < n) ? k[base + lane] : 0u;
+        wave_sync();
+        int hit = -1;
+        float sh = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const uint4 v = w4[q];
+            const uint32_t e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                s = s + __uint_as_float(e[c]);
+                const bool h = hit < 0 && s >= thr && base + 4 * q + c < n;
+                sh = h ? s : sh;
+                hit = h ? base + 4 * q + c : hit;
+            }
+        }
+        wave_sync();
+        if (hit >= 0) {
+            *at = sh;
+            cum = sh;
+            return hit;
+        }
+    }
+    cum = s;
+    return -1;
+}
+
+// Descending bitonic sort of n <= cap keys in LDS (padded with 0 to a power
+// of two), by the whole block.
+__device__ void block_sort_desc_lds(uint32_t* a, int n) {
+    int P2 = 1;
+    while (P2 < n) P2 <<= 1;
+    for (int i = n + (int)threadIdx.x; i < P2; i += kBlock) a[i] = 0u;
+    __syncthreads();
+    for (int k = 2; k <= P2; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = threadIdx.x; i < P2; i += kBlock) {
+                const int ixj = i ^ j;
+                if (ixj > i) {
+                    const uint32_t x = a[i], y = a[ixj];
+                    const bool desc = (i & k) == 0;
+                    if (desc ? (x < y) : (x > y)) {
+                        a[i] = y;
+                        a[ixj] = x;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// The same in global memory, for a bucket too large for LDS (rare).
+__device__ void block_sort_desc_global(uint32_t* a, int n) {
+    int P2 = 1;
+    while (P2 < n) P2 <<= 1;
+    for (int i = n + (int)threadIdx.x; i < P2; i += kBlock) a[i] = 0u;
+    __syncthreads();
+    for (int k = 2; k <= P2; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = threadIdx.x; i < P2; i += kBlock) {
+                const int ixj = i ^ j;
+                if (ixj > i) {
+                    const uint32_t x = a[i], y = a[ixj];
+                    const bool desc = (i & k) == 0;
+                    if (desc ? (x < y) : (x > y)) {
+                        a[i] = y;
+                        a[ixj] = x;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+__device__ __forceinline__ double block_sum_d(double v, Shared& st) {
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
+    if (lane_id() == 0) st.dred[wave_id()] = v;
+    __syncthreads();
+    double r = 0.0;
+#pragma unroll
+    for (int i = 0; i < kBlock / 64; ++i) r += st.dred[i];
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t v, Shared& st) {
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, d, 64));
+    if (lane_id() == 0) st.ired[wave_id()] = (int)v;
+    __syncthreads();
+    uint32_t r = 0u;
+#pragma unroll
+    for (int i = 0; i < kBlock / 64; ++i) r = max(r, (uint32_t)st.ired[i]);
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ uint32_t block_min_u32(uint32_t v, Shared& st) {
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, d, 64));
+    if (lane_id() == 0) st.ired[wave_id()] = (int)v;
+    __syncthreads();
+    uint32_t r = 0xFFFFFFFFu;
+#pragma unroll
+    for (int i = 0; i < kBlock / 64; ++i) r = min(r, (uint32_t)st.ired[i]);
+    __syncthreads();
+    return r;
+}
+
+// The row's ids split into one contiguous chunk per thread (for work that
+// must run in index order).
+struct Chunk {
+    int lo, hi;
+};
+__device__ __forceinline__ Chunk my_chunk(int V) {
+    const int C = (V + kBlock - 1) / kBlock;
+    const int lo = min(V, (int)threadIdx.x * C);
+    return Chunk{lo, min(V, lo + C)};
+}
+
+template <bool GT>
+__global__ __launch_bounds__(kBlock) void k_full(StreamArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ Shared st;
+    __shared__ StreamArgs sa;
+    __shared__ RowPlan sP;
+    const int tid = threadIdx.x;
+    const int lane = lane_id();
+    const int r = (int)blockIdx.x;
+    if (r >= a.rows) return;
+    const RowPlan P = a.plans[r];
+    if (!(P.flags & RF_FULL)) return;
+    const int V = a.vocab;
+    const bool pen = (P.flags & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) != 0;
+    const bool masked = (P.flags & RF_MASK) != 0;
+    float* fv = a.fullv + (size_t)r * V;
+    float* pv = a.fullp + (size_t)r * V;
+    uint32_t* sk = a.fullk + (size_t)r * 2 * a.full_p2;   // [bucketed keys][scratch for a big bucket]
+    const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * (a.dtype == 0 ? 4 : 2);
+    int32_t pre[8];
+    hist_prefetch(a, P, r, pen, pre);
+    if (tid == 0) {
+        sa = a;
+        sP = P;
+        st.u = a.u[r];
+        st.flags = 0;
+    }
+    if (tid < 32) st.expT[tid] = kExpT[tid];
+    const PenaltyLds pl = pen_table<GT>(a, r, smem);
+    uint32_t* work = reinterpret_cast<uint32_t*>(smem + (GT ? 0 : 8 * (size_t)a.mhash_slots));   // 24 KB
+    if (pen) pen_build_row(a, P, r, pl, pre);
+    else __syncthreads();
+    uint32_t rflags = ROWF_U_USED;
+
+    // ---- stages 1-5 (sampler.cpp:235-265): mask, penalties, temperature ----------
+    bool nanv = false;
+    for (int i = tid; i < V; i += kBlock) {
+        float x = (a.dtype == 0) ? load_logit<0>(rowp, i) : load_logit<1>(rowp, i);
+        if (masked && !((a.mask[(int64_t)r * a.mask_stride + (i >> 5)] >> (i & 31)) & 1u)) x = -__builtin_inff();
+        if (pen) {
+            uint32_t s0 = hslot(i, pl);
+            uint32_t kk;
+            while ((kk = tab_ld(&pl.hkey[s0])) != kEmpty && kk != (uint32_t)i) s0 = (s0 + 1) & pl.hmask;
+            if (kk == (uint32_t)i) x = pen_value(x, i, tab_ld(&pl.hval[s0]), sa, sP);
+        }
+        x = x * P.inv_temp;
+        if (x != x) {
+            nanv = true;
+            x = -__builtin_inff();
+        }
+        fv[i] = x;
+    }
+    if (nanv) atomicOr(&st.flags, 4);
+    __syncthreads();
+
+    // ---- top-k above kLimitK (sampler.cpp:109-121): the k-th largest key by four
+    // 8-bit digit passes, ties to the lower ids ---------------------------------------
+    if (P.flags & RF_TOPK) {
+        const int k = P.top_k;
+        uint32_t prefix = 0u, kmask = 0u;
+        int need = k;
+        for (int shift = 24; shift >= 0; shift -= 8) {
+            work[tid] = 0u;
+            __syncthreads();
+            for (int i = tid; i < V; i += kBlock) {
+                const uint32_t key = key32(fv[i]);
+                if ((key & kmask) == prefix) atomicAdd(&work[(key >> shift) & 255u], 1u);
+            }
+            __syncthreads();
+            if (tid < 64) {
+                const int c0 = work[255 - 4 * lane], c1 = work[254 - 4 * lane];
+                const int c2 = work[253 - 4 * lane], c3 = work[252 - 4 * lane];
+                const int s4 = c0 + c1 + c2 + c3;
+                int incl = s4;
+#pragma unroll
+                for (int d = 1; d < 64; d <<= 1) {
+                    const int y = __shfl_up(incl, d, 64);
+                    if (lane >= d) incl += y;
+                }
+                const int excl = incl - s4;
+                const bool mine = excl < need && need <= incl;
+                if (mine) {
+                    int q, before;
+                    if (excl + c0 >= need) { q = 0; before = excl; }
+                    else if (excl + c0 + c1 >= need) { q = 1; before = excl + c0; }
+                    else if (excl + c0 + c1 + c2 >= need) { q = 2; before = excl + c0 + c1; }
+                    else { q = 3; before = excl + c0 + c1 + c2; }
+                    st.sel_d = 255 - 4 * lane - q;
+                    st.sel_need = need - before;
+                }
+            }
+            __syncthreads();
+            prefix |= (uint32_t)st.sel_d << shift;
+            kmask |= 0xFFu << shift;
+            need = st.sel_need;
+            __syncthreads();
+        }
+        // keep key > K, and the `need` lowest ids with key == K
+        const Chunk ch = my_chunk(V);
+        int eq = 0;
+        for (int i = ch.lo; i < ch.hi; ++i) eq += key32(fv[i]) == prefix;
+        int tot;
+        int before = block_excl_scan(eq, &tot, st);
+        int fin = 0;
+        for (int i = ch.lo; i < ch.hi; ++i) {
+            const uint32_t key = key32(fv[i]);
+            bool keep = key > prefix;
+            if (key == prefix) keep = before++ < need;
+            if (!keep) fv[i] = -__builtin_inff();
+            else fin += fv[i] != -__builtin_inff();
+        }
+        // the finite members, index order
+        int nfin;
+        int pos = block_excl_scan(fin, &nfin, st);
+        if (a.topk_idx != nullptr) {
+            for (int i = ch.lo; i < ch.hi; ++i) {
+                if (fv[i] == -__builtin_inff()) continue;
+                if (pos < a.set_cap) a.topk_idx[(int64_t)r * a.set_cap + pos] = i;
+                ++pos;
+            }
+        }
+        if (tid == 0 && a.topk_count != nullptr) a.topk_count[r] = nfin;
+        __syncthreads();
+    } else if (tid == 0 && a.topk_count != nullptr) {
+        a.topk_count[r] = -1;
+    }
+
+    // softmax_probs (sampler.cpp:124-142) of fv into pv; false when nothing is finite
+    auto softmax = [&]() -> bool {
+        float m = -__builtin_inff();
+        for (int i = tid; i < V; i += kBlock) m = fmaxf(m, fv[i]);
+        m = block_max_f(m, st);
+        if (m == -__builtin_inff()) {
+            const float pu = 1.0f / (float)V;
+            for (int i = tid; i < V; i += kBlock) pv[i] = pu;
+            __syncthreads();
+            return false;
+        }
+        for (int i = tid; i < V; i += kBlock)
+            pv[i] = (fv[i] == -__builtin_inff()) ? 0.0f : libm_expf_t(fv[i] - m, st.expT);
+        __syncthreads();
+        if (tid < 64) {
+            const float s = wave_seq_sum_arr(pv, V, st.wv);
+            if (lane == 0) st.sm_m = s;
+        }
+        __syncthreads();
+        const float s = st.sm_m;
+        if (s > 0.0f) {
+            const float inv = 1.0f / s;
+            for (int i = tid; i < V; i += kBlock) pv[i] = pv[i] * inv;
+        }
+        __syncthreads();
+        return true;
+    };
+
+    bool fresh = false;   // pv matches fv
+    // ---- top-p (sampler.cpp:146-164) -------------------------------------------------
+    if (P.flags & RF_TOPP) {
+        softmax();
+        fresh = true;
+        // keys of the positive probabilities (float bits order them), bucketed
+        // by the 11 bits below the bits they all share
+        uint32_t kmx = 0u, kmn = 0xFFFFFFFFu;
+        for (int i = tid; i < V; i += kBlock) {
+            const uint32_t key = __float_as_uint(pv[i]);
+            if (key != 0u) {
+                kmx = max(kmx, key);
+                kmn = min(kmn, key);
+            }
+        }
+        kmx = block_max_u32(kmx, st);
+        kmn = block_min_u32(kmn, st);
+        int cut = -1;         // sorted position of the last kept entry
+        uint32_t cut_key = 0u;
+        float cut_cum = 0.0f;
+        if (kmx != 0u) {
+            const int hb = (kmx != kmn) ? 31 - __clz((int)(kmx ^ kmn)) : 0;
+            const int shift = max(0, hb - 10);
+            uint32_t* cnt = work;           // [2048] counts, then fill positions
+            uint32_t* off = work + 2048;    // [2048] start of each bucket, descending order
+            for (int i = tid; i < 2048; i += kBlock) cnt[i] = 0u;
+            __syncthreads();
+            for (int i = tid; i < V; i += kBlock) {
+                const uint32_t key = __float_as_uint(pv[i]);
+                if (key != 0u) atomicAdd(&cnt[(key >> shift) & 2047u], 1u);
+            }
+            __syncthreads();
+            // offsets: buckets from the top; 8 per thread, thread 0 the highest
+            {
+                int c8[8], sum8 = 0;
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    c8[q] = (int)cnt[2047 - 8 * tid - q];
+                    sum8 += c8[q];
+                }
+                int tot;
+                int o = block_excl_scan(sum8, &tot, st);
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    off[2047 - 8 * tid - q] = (uint32_t)o;
+                    o += c8[q];
+                }
+            }
+            __syncthreads();
+            // scatter (order inside a bucket does not matter: it is sorted below)
+            for (int i = tid; i < 2048; i += kBlock) cnt[i] = off[i];
+            __syncthreads();
+            for (int i = tid; i < V; i += kBlock) {
+                const uint32_t key = __float_as_uint(pv[i]);
+                if (key != 0u) sk[atomicAdd(&cnt[(key >> shift) & 2047u], 1u)] = key;
+            }
+            __syncthreads();
+            // buckets from the top, in batches of at most 2048 keys sorted in LDS
+            uint32_t* batch = work + 4096;   // [2048]
+            float cum = 0.0f;                // wave 0's running sum
+            int b = 2047;
+            while (b >= 0) {
+                // bucket b's count = next bucket start - its start (cnt now holds ends)
+                int b_lo = b, n = 0;
+                const int start = (int)off[b];
+                while (b_lo >= 0 && (n == 0 || n + (int)(cnt[b_lo] - off[b_lo]) <= 2048)) {
+                    n += (int)(cnt[b_lo] - off[b_lo]);
+                    --b_lo;
+                }
+                if (n == 0) {
+                    b = b_lo;
+                    continue;
+                }
+                const uint32_t* src;
+                if (n <= 2048) {
+                    for (int i = tid; i < n; i += kBlock) batch[i] = sk[start + i];
+                    __syncthreads();
+                    block_sort_desc_lds(batch, n);
+                    src = batch;
+                } else {
+                    uint32_t* big = sk + a.full_p2;
+                    for (int i = tid; i < n; i += kBlock) big[i] = sk[start + i];
+                    __syncthreads();
+                    block_sort_desc_global(big, n);
+                    src = big;
+                }
+                if (tid < 64) {
+                    float at = 0.0f;
+                    const int j = wave_seq_find(src, n, P.top_p, cum, &at, st.wv);
+                    if (lane == 0) {
+                        st.cutoff = (j >= 0) ? start + j : -1;
+                        st.sm_inv = at;
+                        st.tok = (j >= 0) ? (int)src[j] : 0;
+                    }
+                }
+                __syncthreads();
+                if (st.cutoff >= 0) {
+                    cut = st.cutoff;
+                    cut_key = (uint32_t)st.tok;
+                    cut_cum = st.sm_inv;
+                    break;
+                }
+                b = b_lo;
+                __syncthreads();
+            }
+        }
+        if (cut >= 0) {
+            if (fabsf(cut_cum - P.top_p) <= 1e-6f) rflags |= ROWF_TOPP_NEAR;
+            // kept: key > K*, and the lowest ids with key == K* up to position cut
+            int gt = 0;
+            const Chunk ch = my_chunk(V);
+            int eq = 0;
+            for (int i = ch.lo; i < ch.hi; ++i) {
+                const uint32_t key = __float_as_uint(pv[i]);
+                gt += key > cut_key;
+                eq += key == cut_key;
+            }
+            int ngt;
+            block_excl_scan(gt, &ngt, st);
+            int tot;
+            int before = block_excl_scan(eq, &tot, st);
+            const int need = cut + 1 - ngt;
+            for (int i = ch.lo; i < ch.hi; ++i) {
+                const uint32_t key = __float_as_uint(pv[i]);
+                bool keep = key > cut_key;
+                if (key == cut_key) keep = before++ < need;
+                if (!keep) fv[i] = -__builtin_inff();
+            }
+            __syncthreads();
+            fresh = false;
+        }
+    }
+    // ---- min-p (sampler.cpp:167-176) -------------------------------------------------
+    if (P.flags & RF_MINP) {
+        if (!fresh) softmax();
+        fresh = true;
+        float mp = 0.0f;
+        for (int i = tid; i < V; i += kBlock) mp = fmaxf(mp, pv[i]);
+        mp = block_max_f(mp, st);
+        const float thr = P.min_p * mp;
+        int dropped = 0;
+        for (int i = tid; i < V; i += kBlock) {
+            if (pv[i] < thr) {
+                dropped |= fv[i] != -__builtin_inff();
+                fv[i] = -__builtin_inff();
+            }
+        }
+        int any;
+        block_excl_scan(dropped, &any, st);
+        if (any) fresh = false;
+    }
+    const bool have = fresh ? true : softmax();
+    (void)have;
+
+    // ---- the draw (sampler.cpp:178-182, discrete_distribution) ----------------------
+    const Chunk ch = my_chunk(V);
+    int nk = 0;
+    double part = 0.0;
+    for (int i = ch.lo; i < ch.hi; ++i) {
+        nk += fv[i] != -__builtin_inff();
+        part += (double)pv[i];
+    }
+    int nkept;
+    int kpos = block_excl_scan(nk, &nkept, st);
+    const double u = st.u;
+    int32_t tok = 0;
+    if (nkept == 0) {
+        rflags |= ROWF_UNIFORM;
+        if (tid == 0) tok = uniform_draw(V, u);
+    } else {
+        const double S = block_sum_d(part, st);
+        // chunk sums of q, scanned over the threads in index order
+        double cq = 0.0;
+        for (int i = ch.lo; i < ch.hi; ++i) cq += (double)pv[i] / S;
+        double incl = cq;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const double y = __shfl_up(incl, d, 64);
+            if (lane >= d) incl += y;
+        }
+        if (lane == 63) st.dred[wave_id()] = incl;
+        __syncthreads();
+        double wbase = 0.0;
+        for (int w = 0; w < wave_id(); ++w) wbase += st.dred[w];
+        double cp = wbase + incl - cq;   // before this chunk
+        if (tid == 0) {
+            st.tok = V - 1;   // no partial sum reaches u: cp[V-1] = 1 takes it
+            st.dS = -1.0;
+        }
+        __syncthreads();
+        int hit = -1;
+        double hcp = 0.0, hprev = 0.0;
+        if (u > 0.0) {
+            for (int i = ch.lo; i < ch.hi; ++i) {
+                const double prev = cp;
+                cp = cp + (double)pv[i] / S;
+                const double c = (i == V - 1) ? 1.0 : cp;
+                if (pv[i] > 0.0f && c >= u) {
+                    hit = i;
+                    hcp = c;
+                    hprev = prev;
+                    break;
+                }
+            }
+        } else if (tid == 0) {
+            hit = 0;
+        }
+        // the first hit over all threads
+        if (hit >= 0) atomicMin(&st.tok, hit);
+        __syncthreads();
+        if (hit >= 0 && hit == st.tok) st.dS = (u > 0.0) ? fmin(fabs(hcp - u), fabs(hprev - u)) : 1.0;
+        __syncthreads();
+        // no hit anywhere: the last chunk's running sum is the total
+        if (st.dS < 0.0 && ch.lo < ch.hi && ch.hi == V) st.dS = fmin(fabs(1.0 - u), fabs(cp - u));
+        __syncthreads();
+        tok = st.tok;
+        if (st.dS <= 1e-6) rflags |= ROWF_CDF_NEAR;
+        // kept ids and probabilities, index order
+        if (a.kept_idx != nullptr) {
+            int pos = kpos;
+            for (int i = ch.lo; i < ch.hi; ++i) {
+                if (fv[i] == -__builtin_inff()) continue;
+                if (pos < a.set_cap) {
+                    a.kept_idx[(int64_t)r * a.set_cap + pos] = i;
+                    a.kept_prob[(int64_t)r * a.set_cap + pos] = pv[i];
+                }
+                ++pos;
+            }
+        }
+    }
+    // the state sample() leaves the logits in (f32 only)
+    if (a.fin_idx != nullptr) {
+        float* row = static_cast<float*>(const_cast<void*>(a.logits)) + (int64_t)r * a.logits_stride;
+        for (int i = tid; i < V; i += kBlock) row[i] = fv[i];
+    }
+    if (tid == 0) {
+        a.token[r] = tok;
+        if (a.row_flags != nullptr) a.row_flags[r] = rflags | ((st.flags & 4) ? ROWF_NAN : 0u);
+        if (a.kept_count != nullptr) a.kept_count[r] = nkept;
+    }
+}
+
 // ---- launchers -------------------------------------------------------------------
 
 hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int grid,
@@ -2116,6 +2684,12 @@ hipError_t launch_merge(const StreamArgs& a, hipStream_t stream) {
     if (a.fast) hipLaunchKernelGGL((k_merge<false, true>), dim3(a.rows), dim3(kBlock), a.merge_lds, stream, a);
     else if (a.gtab != nullptr) hipLaunchKernelGGL((k_merge<true, false>), dim3(a.rows), dim3(kBlock), a.merge_lds, stream, a);
     else hipLaunchKernelGGL((k_merge<false, false>), dim3(a.rows), dim3(kBlock), a.merge_lds, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_full(const StreamArgs& a, uint32_t lds, hipStream_t stream) {
+    if (a.gtab != nullptr) hipLaunchKernelGGL((k_full<true>), dim3(a.rows), dim3(kBlock), lds, stream, a);
+    else hipLaunchKernelGGL((k_full<false>), dim3(a.rows), dim3(kBlock), lds, stream, a);
     return hipGetLastError();
 }
 

@@ -29,6 +29,7 @@ enum : uint32_t {
     RF_MASK = 1u << 8,    // allowed-token mask given for the batch
     RF_BIAS = 1u << 9,    // logit bias entries present                     [30]
     RF_SINGLE = 1u << 10, // V == 1: one id, top-k off, no uniform drawn   [110, random.tcc:2660]
+    RF_FULL = 1u << 11,   // sampling row over the whole vocabulary: top-k off or above kLimitK (k_full)
 };
 
 // Hash-table value bits for one token of a slice (penalty bookkeeping).
@@ -105,6 +106,10 @@ struct StreamArgs {
     int32_t dtype;              // logits element type (0 f32, 1 bf16)
     int32_t fast;               // every row fits k_merge's fast path
     int32_t vec_tail;           // the row's last ids k_merge reads itself (V % chunk with vector loads)
+    float* fullv;               // [rows * vocab] k_full: transformed logits (-inf once removed)
+    float* fullp;               // [rows * vocab] k_full: probabilities
+    uint32_t* fullk;            // [rows * 2 * full_p2] k_full: probability keys by bucket, sort scratch
+    int32_t full_p2;            // next power of two >= vocab
     uint32_t* gtab;             // [rows * 2 * mhash_slots] penalty tables, or NULL: tables in LDS
     uint32_t merge_lds;         // dynamic LDS of k_merge
     uint32_t lds_bytes;         // dynamic LDS size of the launch

@@ -254,3 +254,33 @@ def test_run_rejects_invalid_requests(sampler, hs, wl):
             (2, 40000), dtype=torch.int32, device=x.device), hist_len=[40000, 40000])
     assert e.value.status == hs.ERR_CAPACITY
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("greedy_rows", [0, 2])
+def test_penalised_top_tokens_flag_mode(sampler, wl, greedy_rows):
+    """Histories that hold the rows' highest logits, repeated: the penalised ids
+    compete for the top-k (and the argmax) after their penalties. All knobs
+    only lower logits, so the stream hands penalised ids over as flagged
+    candidates and the merge finds their true values."""
+    rng = np.random.default_rng(77 + greedy_rows)
+    B, V, H = 8, 40000, 600
+    x = (rng.normal(size=(B, V)) * 2.5).astype(np.float32)
+    hist = np.empty((B, H), np.int32)
+    for r in range(B):
+        top = np.argsort(-x[r])[:40]
+        pool = np.concatenate([top, top[:10], top[:5], rng.integers(0, V, H)])
+        hist[r] = rng.permutation(pool)[:H]
+    plist = []
+    for r in range(B):
+        if r < greedy_rows:
+            plist.append(wl.identity_params(temperature=0.0, rep_penalty=1.3, repeat_last_n=200,
+                                            frequency_penalty=0.4, presence_penalty=0.2))
+        else:
+            plist.append(wl.identity_params(temperature=0.8, top_k=50, top_p=0.95, rep_penalty=1.3,
+                                            repeat_last_n=200, frequency_penalty=0.4, presence_penalty=0.2,
+                                            dry_multiplier=0.8, dry_base=1.75, dry_allowed_len=2,
+                                            dry_last_n=H))
+    w = _wl_from(wl, x, plist, rng.random(B))
+    w.hist, w.hist_len = hist, np.full(B, H, np.int64)
+    g = run_gpu(sampler, w)
+    assert compare_rows(w, g) == B

@@ -136,6 +136,7 @@ struct Built {
     bool any_pen = false;
     int max_scan = 0;          // max history window over penalty rows
     int max_bias = 0;          // max logit-bias entries over rows
+    bool pen_lowers = true;    // every penalty stage can only lower a logit
     bool any_mask = false;     // the batch carries an allowed-token mask
     bool any_full = false;     // a sampling row over the whole vocabulary (k_full)
     bool any_topk = false;     // a greedy or top-k row (k_stream + k_merge)
@@ -166,6 +167,7 @@ int build_blob(ultima_hsamp* h, const ultima_hsamp_batch* b, Built& out) {
         const int64_t L = q.hist_len;
         auto win = [&](uint64_t n) -> int64_t { return (int64_t)std::min<uint64_t>(n, (uint64_t)L); };
         uint32_t fl = 0;
+        bool bias_up = false;   // a bias entry can raise a logit
         const bool greedy = q.temperature <= 0.0f;                             // [261]
         if (greedy) fl |= RF_GREEDY;
         int64_t rep_w = 0, dry_w = 0, fp_w = 0;
@@ -227,6 +229,7 @@ int build_blob(ultima_hsamp* h, const ultima_hsamp_batch* b, Built& out) {
                 for (auto& [id, v] : tmp) {
                     bids.push_back(id);
                     bvals.push_back(v);
+                    if (!(v <= 0.0f)) bias_up = true;
                 }
             }
         }
@@ -265,6 +268,11 @@ int build_blob(ultima_hsamp* h, const ultima_hsamp_batch* b, Built& out) {
             out.max_pen = std::max(out.max_pen, (int)scan + P.bias_cnt);
             out.max_scan = std::max(out.max_scan, (int)scan);
             out.max_bias = std::max(out.max_bias, (int)P.bias_cnt);
+            // x/p, x*p (p >= 1), x - n*f - pp (f, pp >= 0), x - dry term (>= 0),
+            // x + b (b <= 0) never raise x (sampler.cpp:28-99)
+            if (((fl & RF_REP) && !(P.rep >= 1.0f)) || ((fl & RF_FP) && !(P.freq >= 0.0f && P.pres >= 0.0f)) ||
+                ((fl & RF_DRY) && !(q.dry_multiplier >= 0.0f && q.dry_base >= 0.0f)) || bias_up)
+                out.pen_lowers = false;
         }
     }
     out.off_dry = align16(sizeof(RowPlan) * B);
@@ -520,9 +528,12 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     const size_t full_lds = (gtab ? 0 : 8 * (size_t)mhash) + kFullWork;
     size_t merge_lds = align16(std::max(gtab ? 0 : 8 * (size_t)mhash, regionF)) + 8 * (size_t)buf_cap;
     // k_merge's fast path: [bins 8 KB][list 1 KB][table 12 B/slot | buffer]
-    const size_t fast_lds = 9216 + std::max(12 * (size_t)mhash, 8 * (size_t)buf_cap);
-    const bool fast = kmax <= 64 && !gtab && bl.max_scan <= 8 * kBlock && bl.max_bias <= kBlock &&
-                      fast_lds <= lds_budget;
+    // (flag mode: [bins][list][ids, counts / composites of penalised candidates][buffer])
+    const bool fast0 = kmax <= 64 && !gtab && bl.max_scan <= 8 * kBlock && bl.max_bias <= kBlock;
+    const bool pen_flag = fast0 && bl.any_pen && bl.pen_lowers;
+    const size_t fast_lds = pen_flag ? 9216 + 12 * (size_t)kFlagCap + 8 * (size_t)buf_cap
+                                     : 9216 + std::max(12 * (size_t)mhash, 8 * (size_t)buf_cap);
+    const bool fast = fast0 && fast_lds <= lds_budget;
     if (fast) merge_lds = std::max(merge_lds, fast_lds);
     const size_t wb_lds = (gtab ? 0 : 8 * (size_t)mhash) + 4 * (size_t)bitmap_words;
     if (merge_lds + statik > h->lds_limit || wb_lds + statik > h->lds_limit ||
@@ -605,6 +616,7 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     a.win_magic = (uint32_t)((1ull << 32) / (uint64_t)win + 1);
     a.dtype = b->dtype;
     a.fast = fast ? 1 : 0;
+    a.pen_flag = (fast && pen_flag) ? 1 : 0;
     a.fullv = h->fullv;
     a.fullp = h->fullp;
     a.fullk = h->fullk;

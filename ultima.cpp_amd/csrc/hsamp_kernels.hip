@@ -1200,11 +1200,24 @@ __device__ __forceinline__ uint32_t wave_kth_bound16(const uint32_t (&g)[4], int
     return prefix;
 }
 
-// One logit of a row, by id (for the penalised ids the stream hands over).
+// One logit of a row, by id.
 template <int DT>
 __device__ __forceinline__ float load_logit(const char* rowp, int t) {
     if (DT == 0) return reinterpret_cast<const float*>(rowp)[t];
     return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(rowp)[t] << 16);
+}
+
+// N logits by id (t < 0: none, 0.0f), the element type chosen once for the
+// batch so that all N loads are in flight together.
+template <int N>
+__device__ __forceinline__ void load_logits(const char* rowp, int dtype, const int32_t (&t)[N], float (&x)[N]) {
+    if (dtype == 0) {
+#pragma unroll
+        for (int q = 0; q < N; ++q) x[q] = (t[q] >= 0) ? load_logit<0>(rowp, t[q]) : 0.0f;
+    } else {
+#pragma unroll
+        for (int q = 0; q < N; ++q) x[q] = (t[q] >= 0) ? load_logit<1>(rowp, t[q]) : 0.0f;
+    }
 }
 
 // Order keys of one tile's elements held by this thread. kv[i] = 0 marks
@@ -1214,13 +1227,16 @@ __device__ __forceinline__ float load_logit(const char* rowp, int t) {
 //    (noted), key32.
 // x + 0.0f turns -0 into +0 and leaves every other value as it is, so ties
 // between zeros of either sign go to the lower index as in the reference.
+// With `flag` set, penalised ids keep their (pre-penalty) key and come back
+// as bits of `pm` instead of being left out.
 template <int DT, bool PEN, bool MASK, bool GR>
 __device__ __forceinline__ void tile_keys(const uint4 (&raw)[Tile<DT>::NCH], int tb, int lo, int hi,
-                                          const uint32_t* pbm, const uint32_t* mbm, float inv_t,
-                                          uint32_t (&kv)[Tile<DT>::NE], bool& nanseen) {
+                                          const uint32_t* pbm, const uint32_t* mbm, float inv_t, bool flag,
+                                          uint32_t (&kv)[Tile<DT>::NE], uint32_t& pm, bool& nanseen) {
     using T = Tile<DT>;
     const int tid = threadIdx.x;
     bool nanv = false;
+    pm = 0u;
 #pragma unroll
     for (int j = 0; j < T::NCH; ++j) {
         const int e0 = tb + (j * kBlock + tid) * T::VW;
@@ -1240,7 +1256,11 @@ __device__ __forceinline__ void tile_keys(const uint4 (&raw)[Tile<DT>::NCH], int
             uint32_t key = b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
             key = nan ? (GR ? 0u : kKeyNegInf) : key;
             bool here = e0 + c < hi;
-            if (PEN) here = here && !((pb >> c) & 1u);
+            if (PEN) {
+                const bool pe = here && ((pb >> c) & 1u);
+                pm |= pe ? (1u << (j * T::VW + c)) : 0u;
+                here = here && (flag || !pe);
+            }
             nanv |= nan && here;
             kv[j * T::VW + c] = here ? key : 0u;
         }
@@ -1290,7 +1310,7 @@ __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
     uint32_t* mbm = pbm + words;
     if (tid == 0) {
         st.theta = kThetaFloor;
-        st.n = 0;
+        st.n = greedy ? 1 : 0;   // a greedy row's argmax goes to out[0]
         st.flags = 0;
     }
     for (int i = tid; i < words; i += kBlock) {
@@ -1319,39 +1339,59 @@ __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
     const int kw = (k + 3) >> 2;
     const int G = min(4, max(1, (kw + 63) >> 6));
     const float inv_t = P.inv_temp;
+    const bool pflag = a.pen_flag != 0;
     bool nanseen = false;
     uint32_t bk = 0u;          // greedy: best key and its first id so far
     int32_t bi = 0x7FFFFFFF;
 
     for (int tb = lo;;) {
         uint32_t kv[T::NE];
+        uint32_t pm;
+        const int bt = tb + tid * T::VW;
+        // ids of this thread's 32 elements; penalised ones (flag mode) carry bit
+        // 31, which clears bit 31 of their composite's low word for k_merge
+        auto idx = [&](int i) -> int32_t {
+            return (bt + (i / T::VW) * (kBlock * T::VW) + (i % T::VW)) | (int32_t)(((pm >> i) & 1u) << 31);
+        };
         if (greedy) {
             // argmax of sampler.cpp:220-228; k_merge settles id 0 holding a NaN
-            tile_keys<DT, PEN, MASK, true>(raw, tb, lo, hi, pbm, mbm, inv_t, kv, nanseen);
+            tile_keys<DT, PEN, MASK, true>(raw, tb, lo, hi, pbm, mbm, inv_t, pflag, kv, pm, nanseen);
             uint32_t m = 0u;
 #pragma unroll
-            for (int i = 0; i < T::NE; ++i) m = max(m, kv[i]);
+            for (int i = 0; i < T::NE; ++i) m = max(m, ((pm >> i) & 1u) ? 0u : kv[i]);
             int32_t mi = 0x7FFFFFFF;
 #pragma unroll
             for (int i = T::NE - 1; i >= 0; --i)
-                mi = (kv[i] == m) ? (tb + tid * T::VW + (i / T::VW) * (kBlock * T::VW) + (i % T::VW)) : mi;
+                mi = (kv[i] == m && !((pm >> i) & 1u)) ? (bt + (i / T::VW) * (kBlock * T::VW) + (i % T::VW)) : mi;
             if (m > bk || (m == bk && mi < bi)) {
                 bk = m;
                 bi = mi;
             }
+            if (PEN && pflag && __ballot(pm != 0u) != 0ull) {
+                // every penalised id goes to k_merge, which finds its true value
+                uint32_t pk[T::NE];
+#pragma unroll
+                for (int i = 0; i < T::NE; ++i) pk[i] = ((pm >> i) & 1u) ? kv[i] : 0u;
+                append_out<T::NE>(out, pk, idx, 1u, st);
+            }
         } else {
-            tile_keys<DT, PEN, MASK, false>(raw, tb, lo, hi, pbm, mbm, inv_t, kv, nanseen);
+            tile_keys<DT, PEN, MASK, false>(raw, tb, lo, hi, pbm, mbm, inv_t, pflag, kv, pm, nanseen);
             // A lower bound on the row's k-th largest from this tile: each
             // wave's kw-th largest group maximum (kw = ceil(k/4)), low 16 bits
             // cleared, minimum over the 4 waves; the block keeps the highest
             // bound seen so far. Keys at or above it survive.
-            uint32_t gk[4] = {0u, 0u, 0u, 0u};
+            // (penalised keys, pre-penalty upper bounds, take no part in the bound)
+            uint32_t gk[4] = {0u, 0u, 0u, 0u}, lm = 0u;
 #pragma unroll
             for (int j = 0; j < T::NCH; ++j) {
 #pragma unroll
-                for (int c = 0; c < T::VW; ++c) gk[(j * 4) / T::NCH] = max(gk[(j * 4) / T::NCH], kv[j * T::VW + c]);
+                for (int c = 0; c < T::VW; ++c) {
+                    const int i = j * T::VW + c;
+                    gk[(j * 4) / T::NCH] = max(gk[(j * 4) / T::NCH], ((pm >> i) & 1u) ? 0u : kv[i]);
+                    lm = max(lm, kv[i]);
+                }
             }
-            const uint32_t lmax = max(max(gk[0], gk[1]), max(gk[2], gk[3]));
+            const uint32_t lmax = lm;
             if (G == 2) {
                 gk[0] = max(gk[0], gk[1]);
                 gk[1] = max(gk[2], gk[3]);
@@ -1368,12 +1408,7 @@ __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
             __syncthreads();
             const uint32_t thk = max(max(tt, th0), (uint32_t)(kThetaFloor >> 32));
             if (tid == 0) st.theta = (u64)thk << 32;
-            if (__ballot(lmax >= thk) != 0ull) {
-                const int bt = tb + tid * T::VW;
-                append_out<T::NE>(out, kv, [&](int i) -> int32_t {
-                    return bt + (i / T::VW) * (kBlock * T::VW) + (i % T::VW);
-                }, thk, st);
-            }
+            if (__ballot(lmax >= thk) != 0ull) append_out<T::NE>(out, kv, idx, thk, st);
         }
         tb += T::ELEMS;
         if (tb >= hi) break;
@@ -1388,7 +1423,7 @@ __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
     if (tid == 0) {
         const int nanf = (st.flags & 1) ? (1 << 30) : 0;
         if (greedy) out[0] = best;
-        a.cand_n[slot] = (greedy ? 1 : st.n) | nanf;
+        a.cand_n[slot] = st.n | nanf;
     }
 }
 
@@ -1527,20 +1562,30 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
     uint32_t* tkey = reinterpret_cast<uint32_t*>(smem + 9216);
     u64* tval = reinterpret_cast<u64*>(smem + 9216 + 4 * fs);
     const uint32_t hmask = (uint32_t)fs - 1u, hshift = 32u - (uint32_t)__popc(hmask);
-    if (pen) {
+    // flag mode (penalties only lower logits): the stream handed penalised ids
+    // over with their pre-penalty keys; their true values are found for just
+    // those ids, from the history held in registers, without a table.
+    // LDS there: [bins][list][pid: kFlagCap ids][pv: kFlagCap counts, then composites]
+    const bool lmode = a.pen_flag != 0;
+    uint32_t* pid = reinterpret_cast<uint32_t*>(smem + 9216);
+    u64* pv = reinterpret_cast<u64*>(smem + 9216 + 4 * kFlagCap);
+    if (pen && !lmode) {
         for (int i = tid; i < fs; i += kBlock) {
             tkey[i] = kEmpty;
             tval[i] = 0ull;
         }
     }
+    if (lmode)
+        for (int i = tid; i < kFlagCap; i += kBlock) pv[i] = 0ull;
     for (int i = tid; i < 2048; i += kBlock) bins[i] = 0u;
+    if (tid == 0) st.last = 0;   // flag-mode list length
     __syncthreads();   // also publishes the slice counts
 
     // ---- penalised ids ------------------------------------------------------------
     u64 cp[9];
 #pragma unroll
     for (int q = 0; q < 9; ++q) cp[q] = 0ull;
-    if (pen) {
+    if (pen && !lmode) {
         const int L = P.hist_len, p0 = L - P.scan_len;
         int32_t t[9];
         uint32_t sl[9];
@@ -1552,34 +1597,73 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
         const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * (a.dtype == 0 ? 4 : 2);
         float x[9];
         uint32_t mw[9];
+        load_logits<9>(rowp, a.dtype, t, x);
+#pragma unroll
+        for (int q = 0; q < 9; ++q)
+            mw[q] = (masked && t[q] >= 0) ? a.mask[(int64_t)r * a.mask_stride + (t[q] >> 5)] : 0xFFFFFFFFu;
+        // Insert: probing runs over groups of 4 slots from the group the hash
+        // names; an id sits in the first group on its way that had room, so a
+        // lookup scans groups until it finds the id or an empty slot. Each
+        // round reads every pending entry's group with one 16-byte load and
+        // claims an empty slot with one CAS; both sets of operations go out
+        // together, and entries with nothing to do repeat a harmless read and
+        // a CAS that cannot succeed instead of branching.
+        uint32_t pend = 0u, own = 0u;
 #pragma unroll
         for (int q = 0; q < 9; ++q) {
-            x[q] = 0.0f;
-            mw[q] = 0xFFFFFFFFu;
-            if (t[q] >= 0) {
-                x[q] = (a.dtype == 0) ? load_logit<0>(rowp, t[q]) : load_logit<1>(rowp, t[q]);
-                if (masked) mw[q] = a.mask[(int64_t)r * a.mask_stride + (t[q] >> 5)];
-            }
+            sl[q] = (((uint32_t)t[q] * 0x9E3779B1u) >> hshift) & ~3u;
+            if (t[q] >= 0) pend |= 1u << q;
         }
-        uint32_t done = 0u, own = 0u;
+        while (pend != 0u) {
+            uint4 g[9];
 #pragma unroll
-        for (int q = 0; q < 9; ++q) {
-            sl[q] = ((uint32_t)t[q] * 0x9E3779B1u) >> hshift;
-            if (t[q] < 0) done |= 1u << q;
-        }
-        while (done != 0x1FFu) {
+            for (int q = 0; q < 9; ++q) g[q] = *reinterpret_cast<const uint4*>(&tkey[sl[q] & ~3u]);
+            uint32_t tryc = 0u, cs[9];
 #pragma unroll
             for (int q = 0; q < 9; ++q) {
-                if ((done >> q) & 1u) continue;
-                const uint32_t old = atomicCAS(&tkey[sl[q]], kEmpty, (uint32_t)t[q]);
-                if (old == kEmpty) {
-                    own |= 1u << q;
-                    done |= 1u << q;
-                } else if (old == (uint32_t)t[q]) {
-                    done |= 1u << q;
-                } else {
-                    sl[q] = (sl[q] + 1u) & hmask;
+                cs[q] = sl[q] & ~3u;
+                if (!((pend >> q) & 1u)) continue;
+                const uint32_t tk = (uint32_t)t[q];
+                const uint32_t k4[4] = {g[q].x, g[q].y, g[q].z, g[q].w};
+                // the empty slot is taken from a point that depends on the id,
+                // so that ids meeting in one group seldom race for one slot
+                const int rot = (int)((tk * 0x9E3779B1u) >> 8) & 3;
+                int hit = -1, emp = -1;
+#pragma unroll
+                for (int c = 3; c >= 0; --c) {
+                    const int cc = (c + rot) & 3;
+                    hit = (k4[c] == tk) ? c : hit;
+                    emp = (k4[cc] == kEmpty) ? cc : emp;
                 }
+                if (hit >= 0) {                  // already in: a count goes to its slot
+                    sl[q] = cs[q] + (uint32_t)hit;
+                    pend &= ~(1u << q);
+                } else if (emp >= 0) {
+                    cs[q] += (uint32_t)emp;
+                    tryc |= 1u << q;
+                } else {
+                    sl[q] = (cs[q] + 4u) & hmask;  // group full: the next one
+                }
+            }
+            // entries not trying a slot this round aim their CAS at this lane's
+            // own word of the (still unused) histogram, which never holds kEmpty
+            uint32_t old[9];
+#pragma unroll
+            for (int q = 0; q < 9; ++q) {
+                uint32_t* at = ((tryc >> q) & 1u) ? &tkey[cs[q]] : &bins[tid];
+                old[q] = atomicCAS(at, kEmpty, (uint32_t)t[q]);
+            }
+#pragma unroll
+            for (int q = 0; q < 9; ++q) {
+                if (!((tryc >> q) & 1u)) continue;
+                if (old[q] == kEmpty) {
+                    own |= 1u << q;
+                    sl[q] = cs[q];
+                    pend &= ~(1u << q);
+                } else if (old[q] == (uint32_t)t[q]) {
+                    sl[q] = cs[q];
+                    pend &= ~(1u << q);
+                }                                  // else: lost the slot, read the group again
             }
         }
 #pragma unroll
@@ -1619,7 +1703,7 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
 
     // the ragged end, unless penalised
     auto in_table = [&](int32_t t) -> bool {
-        uint32_t s0 = ((uint32_t)t * 0x9E3779B1u) >> hshift;
+        uint32_t s0 = (((uint32_t)t * 0x9E3779B1u) >> hshift) & ~3u;
         for (;;) {
             const uint32_t kk = tkey[s0];
             if (kk == (uint32_t)t || kk == kEmpty) return kk == (uint32_t)t;
@@ -1627,7 +1711,8 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
         }
     };
     u64 ct = 0ull;
-    if (tail_t >= 0 && !(pen && in_table(tail_t))) ct = tail_candidate(tail_x, tail_ok, tail_t, greedy, P.inv_temp, st);
+    if (!lmode && tail_t >= 0 && !(pen && in_table(tail_t)))
+        ct = tail_candidate(tail_x, tail_ok, tail_t, greedy, P.inv_temp, st);
 
     // ---- the slices' lists ----------------------------------------------------------
     int extra = 0;
@@ -1639,18 +1724,134 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
     }
     for (int s2 = 0; s2 < S; ++s2) extra += max(0, st.soff[s2] - W);
 
+    int nl = 0;   // flag mode: entries of pid / pv
+    if (lmode) {
+        // flagged list entries (bit 31 of the low word clear) and the ragged
+        // end leave the register set for the list
+        uint32_t fm = 0u;
+#pragma unroll
+        for (int j = 0; j < NW; ++j) fm |= (win[j] != 0ull && !((uint32_t)win[j] & 0x80000000u)) ? (1u << j) : 0u;
+        const int cnt = __popc(fm) + (tail_t >= 0 ? 1 : 0);
+        if (__ballot(cnt != 0) != 0ull) {
+            int incl = cnt;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const int y = __shfl_up(incl, d, 64);
+                if (lane >= d) incl += y;
+            }
+            int base = 0;
+            if (lane == 63) base = atomicAdd(&st.last, incl);
+            int pos = __shfl(base, 63, 64) + incl - cnt;
+#pragma unroll
+            for (int j = 0; j < NW; ++j) {
+                if ((fm >> j) & 1u) {
+                    if (pos < kFlagCap) pid[pos] = ~(uint32_t)win[j] & 0x7FFFFFFFu;
+                    ++pos;
+                    win[j] = 0ull;
+                }
+            }
+            if (tail_t >= 0) {
+                if (pos < kFlagCap) pid[pos] = (uint32_t)tail_t | 0x80000000u;   // mark: ragged end
+                ++pos;
+            }
+        }
+        __syncthreads();
+        nl = st.last;
+        if (nl > kFlagCap) {
+            // more flagged ids than the list holds (at most scan + bias + tail,
+            // so only when kFlagCap is set below that): not reached on the
+            // host's fast-path limits
+            nl = kFlagCap;
+        }
+        // raw logits of the listed ids, 4 loads in flight per thread per round
+        const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * (a.dtype == 0 ? 4 : 2);
+        constexpr int NJ = kFlagCap / kBlock;
+        float xr[NJ];
+#pragma unroll
+        for (int j0 = 0; j0 < NJ; j0 += 4) {
+            if (j0 * kBlock >= nl) break;
+            int32_t t4[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int e = tid + (j0 + q) * kBlock;
+                t4[q] = (j0 + q < NJ && e < nl) ? (int32_t)(pid[e] & 0x7FFFFFFFu) : -1;
+            }
+            float x4[4];
+            load_logits<4>(rowp, a.dtype, t4, x4);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (j0 + q < NJ) xr[j0 + q] = x4[q];
+        }
+        // counts: each thread checks its 8 history ids against every listed id
+        if (pen) {
+            const int L = P.hist_len, p0 = L - P.scan_len;
+            u64 addq[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int p = p0 + q * kBlock + tid;
+                addq[q] = ((p >= L - P.fp_win) ? 1ull : 0ull) | ((p >= L - P.dry_win) ? (1ull << 16) : 0ull) |
+                          ((p >= L - P.rep_win) ? (1ull << 32) : 0ull);
+            }
+            for (int e = 0; e < nl; ++e) {
+                const int32_t t = (int32_t)(pid[e] & 0x7FFFFFFFu);
+                u64 add = 0ull;
+#pragma unroll
+                for (int q = 0; q < 8; ++q) add += (pre[q] == t) ? addq[q] : 0ull;
+                if (add) atomicAdd(&pv[e], add);
+            }
+        }
+        __syncthreads();
+        // true values (stages 1-6, sampler.cpp:235-264), then the composite
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int e = tid + j * kBlock;
+            if (e >= nl) break;
+            const uint32_t w = pid[e];
+            const int32_t t = (int32_t)(w & 0x7FFFFFFFu);
+            const u64 c = pv[e];
+            uint32_t v = ((c >> 32) & 0xFFFFull ? HV_REP : 0u) | ((uint32_t)((c >> 16) & 0xFFFFull) << HV_DRY_SHIFT) |
+                         (uint32_t)(c & 0xFFFFull);
+            if (P.flags & RF_BIAS) {
+                int lo = 0, hi = P.bias_cnt;
+                const int32_t* ids = a.bias_ids + P.bias_off;
+                while (lo < hi) {
+                    const int mid = (lo + hi) >> 1;
+                    if (ids[mid] < t) lo = mid + 1;
+                    else hi = mid;
+                }
+                if (lo < P.bias_cnt && ids[lo] == t) v |= HV_BIAS;
+            }
+            float y = xr[j];
+            // the ragged end was not masked by the stream
+            if ((w & 0x80000000u) && masked && !((a.mask[(int64_t)r * a.mask_stride + (t >> 5)] >> (t & 31)) & 1u))
+                y = -__builtin_inff();
+            y = pen_value(y, t, v, sa, sP);
+            u64 out = 0ull;
+            if (!greedy) y = y * P.inv_temp;
+            if (y != y) {
+                atomicOr(&st.flags, 4);
+                if (!greedy) out = comp(kKeyNegInf, t);
+            } else {
+                out = comp(key32(y), t);
+            }
+            pv[e] = out;
+        }
+        __syncthreads();
+    }
+
     if (greedy) {
         u64 best = ct;
 #pragma unroll
         for (int q = 0; q < 9; ++q) best = cp[q] > best ? cp[q] : best;
 #pragma unroll
         for (int j = 0; j < NW; ++j) best = win[j] > best ? win[j] : best;
+        for (int e = tid; e < nl; e += kBlock) best = pv[e] > best ? pv[e] : best;
         best = block_max_u64(best, st);
         __syncthreads();
         if (tid == 0) {
             // argmax returns 0 when id 0 holds a NaN: a penalised id 0 was
             // settled with the table, any other by its logit
-            const bool pen0 = pen && in_table(0);
+            const bool pen0 = pen && !lmode && in_table(0);
             const bool nan0 = pen0 ? st.nan0 != 0 : nan_at0;
             a.token[r] = nan0 ? 0 : comp_idx(best);
             if (a.row_flags != nullptr) a.row_flags[r] = ROWF_GREEDY | ((st.flags & 4) ? ROWF_NAN : 0u);
@@ -1664,6 +1865,7 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
     constexpr int NC = 10 + NW;
     const uint32_t floor_key = (uint32_t)(kThetaFloor >> 32);
     uint32_t lmax = (uint32_t)(ct >> 32);
+    for (int e = tid; e < nl; e += kBlock) lmax = max(lmax, (uint32_t)(pv[e] >> 32));
 #pragma unroll
     for (int q = 0; q < 9; ++q) lmax = max(lmax, (uint32_t)(cp[q] >> 32));
 #pragma unroll
@@ -1692,6 +1894,8 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
     const bool any = Mk >= Lk;
     if (any) {
         if ((uint32_t)(ct >> 32) >= Lk) atomicAdd(&bins[binof((uint32_t)(ct >> 32))], 1u);
+        for (int e = tid; e < nl; e += kBlock)
+            if ((uint32_t)(pv[e] >> 32) >= Lk) atomicAdd(&bins[binof((uint32_t)(pv[e] >> 32))], 1u);
 #pragma unroll
         for (int q = 0; q < 9; ++q) {
             const uint32_t key = (uint32_t)(cp[q] >> 32);
@@ -1744,8 +1948,13 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
             const uint32_t key = (uint32_t)(c >> 32);
             inm |= (any && key >= Lk && (int)binof(key) >= bstar) ? (1u << q) : 0u;
         }
-        if (__ballot(inm != 0u) != 0ull) {
-            const int cnt = __popc(inm);
+        int lcnt = 0;   // flag-mode entries of this thread that go too
+        for (int e = tid; e < nl; e += kBlock) {
+            const uint32_t key = (uint32_t)(pv[e] >> 32);
+            lcnt += (any && key >= Lk && (int)binof(key) >= bstar) ? 1 : 0;
+        }
+        if (__ballot(inm != 0u || lcnt != 0) != 0ull) {
+            const int cnt = __popc(inm) + lcnt;
             int incl = cnt;
 #pragma unroll
             for (int d = 1; d < 64; d <<= 1) {
@@ -1758,6 +1967,10 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
 #pragma unroll
             for (int q = 0; q < NC; ++q)
                 if ((inm >> q) & 1u) list[pos++] = (q < 9) ? cp[q] : (q == 9 ? ct : win[q - 10 < 0 ? 0 : q - 10]);
+            for (int e = tid; e < nl; e += kBlock) {
+                const uint32_t key = (uint32_t)(pv[e] >> 32);
+                if (any && key >= Lk && (int)binof(key) >= bstar) list[pos++] = pv[e];
+            }
         }
         __syncthreads();
         const uint32_t rflags = (st.flags & 4) ? ROWF_NAN : 0u;
@@ -1785,11 +1998,17 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
         wave_finalize(sa, sP, r, c, nk, rflags, st);
         return;
     }
-    // buffer path: the table is dead, the buffer takes its place
-    u64* buf = reinterpret_cast<u64*>(smem + 9216);
+    // buffer path: the table is dead and the buffer takes its place (in flag
+    // mode it goes after the list, which is still read)
+    u64* buf = reinterpret_cast<u64*>(smem + 9216 + (lmode ? 12 * (size_t)kFlagCap : 0));
     u64* ovf = a.ovf + (int64_t)r * a.ovf_cap;
     if (tid == 0) st.theta = (u64)Lk << 32;
     __syncthreads();
+    // (flag mode: the list's entries first, in rounds every thread joins)
+    for (int e0 = 0; e0 < nl; e0 += kBlock) {
+        const u64 c1[1] = {(e0 + tid < nl) ? pv[e0 + tid] : 0ull};
+        offer_regs<1>(buf, ovf, a.buf_cap, k, c1, st);
+    }
     offer_regs<9>(buf, ovf, a.buf_cap, k, cp, st);
     {
         const u64 c1[1] = {ct};
@@ -1855,19 +2074,19 @@ __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
     const int32_t bias_t = (FAST && (P.flags & RF_BIAS) && tid < P.bias_cnt) ? a.bias_ids[P.bias_off + tid] : -1;
     const int cnt_raw = (tid < S) ? a.cand_n[(int64_t)r * S + tid] : 0;
     const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * (a.dtype == 0 ? 4 : 2);
-    bool nan_at0 = false;   // greedy: id 0 holds an allowed NaN
-    if (greedy && tid == 0) {
-        const float x0 = (a.dtype == 0) ? load_logit<0>(rowp, 0) : load_logit<1>(rowp, 0);
-        nan_at0 = x0 != x0 && (!masked || (a.mask[(int64_t)r * a.mask_stride] & 1u));
-    }
-    // the row's ragged end (ids the stream's whole-chunk loads leave out)
+    // greedy: whether id 0 holds an allowed NaN; the row's ragged end (ids the
+    // stream's whole-chunk loads leave out)
     const int32_t tail_t = (tid < a.vec_tail) ? a.vocab - a.vec_tail + tid : -1;
-    float tail_x = 0.0f;
-    bool tail_ok = true;
-    if (tail_t >= 0) {
-        tail_x = (a.dtype == 0) ? load_logit<0>(rowp, tail_t) : load_logit<1>(rowp, tail_t);
-        if (masked) tail_ok = (a.mask[(int64_t)r * a.mask_stride + (tail_t >> 5)] >> (tail_t & 31)) & 1u;
+    float x2[2];
+    {
+        const int32_t t2[2] = {(greedy && tid == 0) ? 0 : -1, tail_t};
+        load_logits<2>(rowp, a.dtype, t2, x2);
     }
+    const bool nan_at0 = greedy && tid == 0 && x2[0] != x2[0] &&
+                         (!masked || (a.mask[(int64_t)r * a.mask_stride] & 1u));
+    const float tail_x = x2[1];
+    bool tail_ok = true;
+    if (masked && tail_t >= 0) tail_ok = (a.mask[(int64_t)r * a.mask_stride + (tail_t >> 5)] >> (tail_t & 31)) & 1u;
     u64 win[NW];
 #pragma unroll
     for (int j = 0; j < NW; ++j) {
@@ -1911,15 +2130,9 @@ __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
                 const int i = base + q * kBlock + tid;
                 t[q] = (i < a.mhash_slots) ? (int32_t)tab_ld(&pl.hkey[i]) : -1;   // kEmpty reads as -1
             }
+            load_logits<8>(rowp, a.dtype, t, x);
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                x[q] = 0.0f;
-                mw[q] = 0xFFFFFFFFu;
-                if (t[q] >= 0) {
-                    x[q] = (a.dtype == 0) ? load_logit<0>(rowp, t[q]) : load_logit<1>(rowp, t[q]);
-                    if (masked) mw[q] = mrow[t[q] >> 5];
-                }
-            }
+            for (int q = 0; q < 8; ++q) mw[q] = (masked && t[q] >= 0) ? mrow[t[q] >> 5] : 0xFFFFFFFFu;
             u64 c[8];
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
@@ -2289,7 +2502,13 @@ __global__ __launch_bounds__(kBlock) void k_full(StreamArgs a) {
     // ---- stages 1-5 (sampler.cpp:235-265): mask, penalties, temperature ----------
     bool nanv = false;
     for (int i = tid; i < V; i += kBlock) {
-        float x = (a.dtype == 0) ? load_logit<0>(rowp, i) : load_logit<1>(rowp, i);
+        float x = 0.0f;
+        {
+            const int32_t t1[1] = {i};
+            float x1[1];
+            load_logits<1>(rowp, a.dtype, t1, x1);
+            x = x1[0];
+        }
         if (masked && !((a.mask[(int64_t)r * a.mask_stride + (i >> 5)] >> (i & 31)) & 1u)) x = -__builtin_inff();
         if (pen) {
             uint32_t s0 = hslot(i, pl);

@@ -105,6 +105,8 @@ struct StreamArgs {
     uint32_t win_magic;         // floor(2^32 / win) + 1: umulhi(g, win_magic) == g / win for g < 2^16
     int32_t dtype;              // logits element type (0 f32, 1 bf16)
     int32_t fast;               // every row fits k_merge's fast path
+    int32_t pen_flag;           // penalties only lower logits: k_stream hands penalised ids over as
+                                // flagged candidates (pre-penalty key) instead of leaving them out
     int32_t vec_tail;           // the row's last ids k_merge reads itself (V % chunk with vector loads)
     float* fullv;               // [rows * vocab] k_full: transformed logits (-inf once removed)
     float* fullp;               // [rows * vocab] k_full: probabilities
@@ -116,7 +118,8 @@ struct StreamArgs {
 };
 
 constexpr int kBlock = 256;        // threads per block (4 wave64)
-constexpr int kLimitK = 1024;      // largest top_k the fused kernel takes
+constexpr int kLimitK = 1024;      // largest top_k the top-k path takes
+constexpr int kFlagCap = 2560;     // k_merge flag mode: penalised candidates per row (>= 8 * 256 + 256 + 8)
 constexpr int kXcds = 8;           // MI355X: workgroups round-robin over 8 XCDs
 
 }  // namespace hsamp

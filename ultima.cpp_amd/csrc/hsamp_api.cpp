@@ -24,8 +24,8 @@
 #include "ultima_hsamp.h"
 
 namespace hsamp {
-hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int grid,
-                         hipStream_t stream);
+hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, bool greedy_rows,
+                         bool sample_rows, int grid, hipStream_t stream);
 hipError_t launch_writeback(const StreamArgs& a, int grid, uint32_t lds, hipStream_t stream);
 hipError_t launch_merge(const StreamArgs& a, hipStream_t stream);
 hipError_t launch_full(const StreamArgs& a, uint32_t lds, hipStream_t stream);
@@ -36,7 +36,7 @@ using namespace hsamp;
 namespace {
 
 constexpr int kSlots = 4;
-constexpr int kTile = kBlock * 32;      // elements one block streams per tile
+constexpr int kTile = kBlock * 32;      // most elements of one slice (two k_stream tiles)
 constexpr int kTargetBlocks = 4096;     // most blocks a launch spreads rows over
 constexpr int kMergeRound = kBlock * 16;  // candidates k_merge offers per round
 constexpr int kMergeWindow = kBlock * 16; // list entries k_merge loads up front, over all slices
@@ -140,6 +140,8 @@ struct Built {
     bool any_mask = false;     // the batch carries an allowed-token mask
     bool any_full = false;     // a sampling row over the whole vocabulary (k_full)
     bool any_topk = false;     // a greedy or top-k row (k_stream + k_merge)
+    bool any_greedy = false;   // a greedy row (k_stream's greedy kernel)
+    bool any_sample = false;   // a top-k sampling row (k_stream's sampling kernel)
 };
 
 // RowPlans + DRY tables + bias into h->blob; the reference's predicates in [].
@@ -253,14 +255,14 @@ int build_blob(ultima_hsamp* h, const ultima_hsamp_batch* b, Built& out) {
                 fl |= RF_FULL;                                                    // top-k off
             }
             if (fl & RF_FULL) out.any_full = true;
-            else out.any_topk = true;
+            else out.any_topk = out.any_sample = true;
             if (q.top_p < 1.0f && !(q.top_p <= 0.0f)) fl |= RF_TOPP;             // [270, 147]
             if (q.min_p > 0.0f) fl |= RF_MINP;                                    // [273, 168]
             P.top_p = q.top_p;
             P.min_p = q.min_p;
             if (!(fl & RF_FULL)) out.kmax = std::max(out.kmax, P.top_k);
         } else {
-            out.any_topk = true;
+            out.any_topk = out.any_greedy = true;
         }
         P.flags = fl;
         if (fl & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) {
@@ -627,10 +629,12 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     a.fin_idx = wb ? h->fin_idx : nullptr;
     a.fin_n = wb ? h->fin_n : nullptr;
     a.lds_bytes = (uint32_t)lds;
+    // 16-byte loads: aligned rows holding at least one whole chunk
     const bool vec = (reinterpret_cast<uintptr_t>(b->logits) % 16 == 0) &&
-                     ((b->logits_stride * es) % 16 == 0);
+                     ((b->logits_stride * es) % 16 == 0) && V >= 16 / es;
     a.vec_tail = vec ? V % (16 / es) : 0;
-    if (bl.any_topk) HIP_TRY(launch_stream(a, b->dtype, vec, bl.any_pen, bl.any_mask, grid, stream));
+    if (bl.any_topk)
+        HIP_TRY(launch_stream(a, b->dtype, vec, bl.any_pen, bl.any_mask, bl.any_greedy, bl.any_sample, grid, stream));
     if (h->phase_ev != nullptr) HIP_TRY(hipEventRecord(h->phase_ev, stream));
     if (bl.any_topk) HIP_TRY(launch_merge(a, stream));
     if (bl.any_full) HIP_TRY(launch_full(a, (uint32_t)full_lds, stream));

@@ -36,6 +36,10 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kKeyNegInf = 0x007FFFFFu;        // key32(-inf)
 constexpr uint32_t kEmpty = 0xFFFFFFFFu;
+// Key of a flagged candidate (a penalised id whose true value k_merge finds):
+// the key of the NaN bit pattern 0x7FFFFFFF, which no stored key can take
+// (NaNs are stored as kKeyNegInf or left out).
+constexpr uint32_t kKeyFlag = 0xFFFFFFFFu;
 constexpr u64 kThetaFloor = (u64)(kKeyNegInf + 1) << 32;  // smallest finite composite
 
 // Order-preserving key of a float: larger float -> larger key; -0 == +0.
@@ -474,30 +478,33 @@ struct Tile {
     static constexpr int ELEMS = kBlock * NE;     // 8192 per tile
 };
 
-// One tile of this thread's chunks from [tb, hi). With VEC the slice ends on
-// a whole chunk (the row's last V % VW ids are left to k_merge), so every
-// chunk is one 16-byte non-temporal load or absent; without VEC (unaligned
-// rows) the elements are read one by one.
+// Buffer resource over one row's first `elems` elements: loads past them
+// return 0 (the hardware's range check), so tile loads need no bounds.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const char* rowp, int elems, int es) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(rowp), (short)0, elems * es, 0x00020000);
+}
+
+// One tile of this thread's chunks from [tb, hi) through the row's buffer
+// resource (range hi): every chunk is one 16-byte non-temporal load (VEC:
+// aligned rows, slices ending on a whole chunk; the row's last V % VW ids are
+// left to k_merge), or its elements one by one (unaligned rows). Chunks past
+// hi read as zeros; tile_keys counts them absent.
 template <int DT, bool VEC>
-__device__ __forceinline__ void load_tile(const char* rowp, int tb, int hi, uint4 (&raw)[Tile<DT>::NCH]) {
+__device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t rs, int tb, uint4 (&raw)[Tile<DT>::NCH]) {
     using T = Tile<DT>;
+    const int e0 = tb + (int)threadIdx.x * T::VW;
 #pragma unroll
     for (int j = 0; j < T::NCH; ++j) {
-        const int e0 = tb + (j * kBlock + (int)threadIdx.x) * T::VW;
         if (VEC) {
-            u32x4 v = {0u, 0u, 0u, 0u};
-            if (e0 < hi) v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rowp + (size_t)e0 * T::ES));
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, e0 * T::ES, j * kBlock * 16, 2);
             raw[j] = make_uint4(v.x, v.y, v.z, v.w);
         } else {
             uint32_t w[4] = {0u, 0u, 0u, 0u};
+            const int ej = e0 + j * kBlock * T::VW;
+#pragma unroll
             for (int c = 0; c < T::VW; ++c) {
-                if (e0 + c < hi) {
-                    uint32_t b;
-                    if (DT == 0) b = reinterpret_cast<const uint32_t*>(rowp)[e0 + c];
-                    else b = reinterpret_cast<const uint16_t*>(rowp)[e0 + c];
-                    if (DT == 0) w[c] = b;
-                    else w[c >> 1] |= b << ((c & 1) * 16);
-                }
+                if (DT == 0) w[c] = __builtin_amdgcn_raw_buffer_load_b32(rs, (ej + c) * 4, 0, 0);
+                else w[c >> 1] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (ej + c) * 2, 0, 0) << ((c & 1) * 16);
             }
             raw[j] = make_uint4(w[0], w[1], w[2], w[3]);
         }
@@ -1148,17 +1155,13 @@ __device__ __attribute__((noinline)) void select_and_finalize(const StreamArgs& 
 
 // ---- the stream kernel ---------------------------------------------------------
 
-// Append the register-held keys kv[i] (0 = absent) of ids idx(i) that are
-// >= the key threshold thk to the slice's list in global memory: each lane
-// counts its survivors, the wave reserves one range with a single LDS atomic,
-// and each lane writes its survivors in slot order. The list holds a whole
-// slice, so it cannot overflow.
+// Append the register-held keys kv[i] of ids idx(i) selected by bit i of sv
+// to the slice's list in global memory: each lane counts its selections, the
+// wave reserves one range with a single LDS atomic, and each lane writes its
+// entries in slot order. The list holds a whole slice, so it cannot overflow.
 template <int NE, typename Idx>
-__device__ __forceinline__ void append_out(u64* out, const uint32_t (&kv)[NE], Idx idx, uint32_t thk, Shared& st) {
+__device__ __forceinline__ void append_sel(u64* out, const uint32_t (&kv)[NE], Idx idx, uint32_t sv, Shared& st) {
     const int lane = lane_id();
-    uint32_t sv = 0u;
-#pragma unroll
-    for (int i = 0; i < NE; ++i) sv |= (kv[i] >= thk) ? (1u << i) : 0u;
     const int cnt = __popc(sv);
     int incl = cnt;
 #pragma unroll
@@ -1242,9 +1245,17 @@ __device__ __forceinline__ void tile_keys(const uint4 (&raw)[Tile<DT>::NCH], int
         const int e0 = tb + (j * kBlock + tid) * T::VW;
         const int o = e0 - lo;
         const bool in = e0 < hi;   // whole chunks (VEC) or per element below
+        // branch-free: the word index is clamped into the slice's words
+        const int wi = min(o, hi - lo - 1) >> 5;
         uint32_t mb = 0xFFFFFFFFu, pb = 0u;
-        if (MASK) mb = in ? (mbm[o >> 5] >> (o & 31)) : 0u;
-        if (PEN) pb = in ? (pbm[o >> 5] >> (o & 31)) : 0u;
+        if (MASK) {
+            const uint32_t w = mbm[wi];
+            mb = in ? (w >> (o & 31)) : 0u;
+        }
+        if (PEN) {
+            const uint32_t w = pbm[wi];
+            pb = in ? (w >> (o & 31)) : 0u;
+        }
 #pragma unroll
         for (int c = 0; c < T::VW; ++c) {
             float x = elem<DT>(raw[j], c);
@@ -1264,17 +1275,190 @@ __device__ __forceinline__ void tile_keys(const uint4 (&raw)[Tile<DT>::NCH], int
             nanv |= nan && here;
             kv[j * T::VW + c] = here ? key : 0u;
         }
+        // chunks are consumed in load order, each after its own load
+        // (the loads complete in order), not all after the last
+        __builtin_amdgcn_sched_barrier(0);
     }
     nanseen |= nanv;
+}
+
+// Marks id t in the slice's penalised-id bitmap: the ids the penalty stages
+// touch (sampler.cpp:236-258), which k_merge finishes from the row's counts.
+__device__ __forceinline__ void stream_mark(int t, int lo, int hi, uint32_t* pbm) {
+    if (t >= lo && t < hi) atomicOr(&pbm[(t - lo) >> 5], 1u << ((t - lo) & 31));
+}
+
+// Per-block set-up of k_stream, before the first tiles are requested: the
+// block's counters, the slice's allowed-id mask words and the penalised-id
+// bitmap (one bit per slice id, in LDS), cleared, with the ids whose loads
+// wait here (logit-bias ids, history positions past the first 8 * kBlock)
+// already marked. Their waits thus never cover tile loads.
+template <bool PEN, bool MASK>
+__device__ __forceinline__ void stream_setup(const StreamArgs& a, const RowPlan& P, int r, int lo, int hi,
+                                             bool greedy, bool pen, bool masked, int p0, int L,
+                                             const int32_t* hrow, uint32_t* pbm, uint32_t* mbm, Shared& st) {
+    const int tid = threadIdx.x;
+    const int words = a.bitmap_words;
+    if (tid == 0) {
+        st.theta = kThetaFloor;
+        st.n = greedy ? 1 : 0;   // a greedy row's argmax goes to out[0]
+        st.flags = 0;
+    }
+    for (int i = tid; i < words; i += kBlock) {
+        if (PEN) pbm[i] = 0u;
+        if (masked) mbm[i] = (lo + 32 * i < hi) ? a.mask[(int64_t)r * a.mask_stride + (lo >> 5) + i] : 0u;
+        else if (MASK) mbm[i] = 0xFFFFFFFFu;
+    }
+    __syncthreads();
+    if (PEN && pen) {
+        for (int p = p0 + 8 * kBlock + tid; p < L; p += kBlock) stream_mark(hrow[p], lo, hi, pbm);
+        if (P.flags & RF_BIAS)
+            for (int j = tid; j < P.bias_cnt; j += kBlock) stream_mark(a.bias_ids[P.bias_off + j], lo, hi, pbm);
+    }
+}
+
+// The greedy row's slice (argmax of sampler.cpp:220-228): the first id of the
+// largest key goes to out[0]; k_merge settles id 0 holding a NaN. In flag
+// mode every penalised id is appended too (pre-penalty key, flagged), for
+// k_merge to find its true value.
+template <int DT, bool VEC, bool PEN, bool MASK>
+__device__ __forceinline__ void stream_greedy(const StreamArgs& a, const RowPlan& P, int r, int lo, int hi,
+                                              __amdgpu_buffer_rsrc_t rs, uint4 (&raw)[Tile<DT>::NCH],
+                                              u64* out, int64_t slot,
+                                              const unsigned char* smem, Shared& st) {
+    using T = Tile<DT>;
+    const int tid = threadIdx.x;
+    const uint32_t* pbm = reinterpret_cast<const uint32_t*>(smem);
+    const uint32_t* mbm = pbm + a.bitmap_words;
+    const bool pflag = a.pen_flag != 0;
+    bool nanseen = false;
+    uint32_t bk = 0u;          // best key and its first id so far
+    int32_t bi = 0x7FFFFFFF;
+    auto process = [&](const uint4 (&raw)[T::NCH], int tb) {
+        uint32_t kv[T::NE];
+        uint32_t pm;
+        tile_keys<DT, PEN, MASK, true>(raw, tb, lo, hi, pbm, mbm, 1.0f, pflag, kv, pm, nanseen);
+        const int bt = tb + tid * T::VW;
+        uint32_t m = 0u;
+#pragma unroll
+        for (int i = 0; i < T::NE; ++i) m = max(m, ((pm >> i) & 1u) ? 0u : kv[i]);
+        int32_t mi = 0x7FFFFFFF;
+#pragma unroll
+        for (int i = T::NE - 1; i >= 0; --i)
+            mi = (kv[i] == m && !((pm >> i) & 1u)) ? (bt + (i / T::VW) * (kBlock * T::VW) + (i % T::VW)) : mi;
+        if (m > bk || (m == bk && mi < bi)) {
+            bk = m;
+            bi = mi;
+        }
+        if (PEN && pflag && __ballot(pm != 0u) != 0ull) {
+            // penalised ids go with the flag key kKeyFlag
+#pragma unroll
+            for (int i = 0; i < T::NE; ++i) kv[i] = kKeyFlag;
+            auto idx = [&](int i) -> int32_t { return bt + (i / T::VW) * (kBlock * T::VW) + (i % T::VW); };
+            append_sel<T::NE>(out, kv, idx, pm, st);
+        }
+    };
+    for (int tb = lo;;) {
+        process(raw, tb);
+        tb += T::ELEMS;
+        if (tb >= hi) break;
+        load_tile<DT, VEC>(rs, tb, raw);
+    }
+    if (nanseen) atomicOr(&st.flags, 1);
+    const u64 best = block_max_u64(bk != 0u ? comp(bk, bi) : 0ull, st);   // has the barrier the flag needs
+    if (tid == 0) {
+        out[0] = best;
+        a.cand_n[slot] = st.n | ((st.flags & 1) ? (1 << 30) : 0);
+    }
+}
+
+// A sampling row's slice: every id whose key can still be among the row's top
+// k is appended (composite form). The bound: each wave's kw-th largest group
+// maximum (kw = ceil(k/4)), low 16 bits cleared, minimum over the 4 waves;
+// the block keeps the highest bound seen so far, and keys at or above it
+// survive. In flag mode penalised ids keep their pre-penalty key (an upper
+// bound of the true one), take no part in the bound and are appended flagged.
+template <int DT, bool VEC, bool PEN, bool MASK>
+__device__ __forceinline__ void stream_sample(const StreamArgs& a, const RowPlan& P, int r, int lo, int hi,
+                                              __amdgpu_buffer_rsrc_t rs, uint4 (&raw)[Tile<DT>::NCH],
+                                              u64* out, int64_t slot,
+                                              const unsigned char* smem, Shared& st) {
+    using T = Tile<DT>;
+    const int tid = threadIdx.x;
+    const uint32_t* pbm = reinterpret_cast<const uint32_t*>(smem);
+    const uint32_t* mbm = pbm + a.bitmap_words;
+    const int k = P.top_k;
+    const int kw = (k + 3) >> 2;
+    const int G = min(4, max(1, (kw + 63) >> 6));
+    const float inv_t = P.inv_temp;
+    const bool pflag = a.pen_flag != 0;
+    bool nanseen = false;
+    auto process = [&](const uint4 (&raw)[T::NCH], int tb) {
+        uint32_t kv[T::NE];
+        uint32_t pm;
+        tile_keys<DT, PEN, MASK, false>(raw, tb, lo, hi, pbm, mbm, inv_t, pflag, kv, pm, nanseen);
+        uint32_t gk[4] = {0u, 0u, 0u, 0u}, lm = 0u;
+#pragma unroll
+        for (int j = 0; j < T::NCH; ++j) {
+#pragma unroll
+            for (int c = 0; c < T::VW; ++c) {
+                const int i = j * T::VW + c;
+                gk[i / (T::NE / 4)] = max(gk[i / (T::NE / 4)], ((pm >> i) & 1u) ? 0u : kv[i]);
+                lm = max(lm, kv[i]);
+            }
+        }
+        if (G == 2) {
+            gk[0] = max(gk[0], gk[1]);
+            gk[1] = max(gk[2], gk[3]);
+        } else if (G == 1) {
+            gk[0] = max(max(gk[0], gk[1]), max(gk[2], gk[3]));
+        }
+        const uint32_t tw = (kw <= 64 * G) ? wave_kth_bound16(gk, G, kw) : 0u;
+        if (lane_id() == 0) st.twave[wave_id()] = tw;
+        __syncthreads();
+        uint32_t tt = st.twave[0];
+#pragma unroll
+        for (int i = 1; i < kBlock / 64; ++i) tt = min(tt, st.twave[i]);
+        const uint32_t th0 = (uint32_t)(st.theta >> 32);
+        __syncthreads();
+        const uint32_t thk = max(max(tt, th0), (uint32_t)(kThetaFloor >> 32));
+        if (tid == 0) st.theta = (u64)thk << 32;
+        if (__ballot(lm >= thk) != 0ull) {
+            uint32_t sv = 0u;
+#pragma unroll
+            for (int i = 0; i < T::NE; ++i) sv |= (kv[i] >= thk) ? (1u << i) : 0u;
+            // penalised survivors go with the flag key kKeyFlag
+            if (PEN) {
+#pragma unroll
+                for (int i = 0; i < T::NE; ++i) kv[i] = ((pm >> i) & 1u) ? kKeyFlag : kv[i];
+            }
+            const int bt = tb + tid * T::VW;
+            auto idx = [&](int i) -> int32_t { return bt + (i / T::VW) * (kBlock * T::VW) + (i % T::VW); };
+            append_sel<T::NE>(out, kv, idx, sv, st);
+        }
+    };
+    for (int tb = lo;;) {
+        process(raw, tb);
+        tb += T::ELEMS;
+        if (tb >= hi) break;
+        load_tile<DT, VEC>(rs, tb, raw);
+    }
+    if (nanseen) atomicOr(&st.flags, 1);
+    __syncthreads();
+    if (tid == 0) a.cand_n[slot] = st.n | ((st.flags & 1) ? (1 << 30) : 0);
 }
 
 // One block per (row, slice): stream the slice once and leave for k_merge the
 // ids whose key can still be among the row's top k (all of them, in composite
 // form), or the slice's argmax for a greedy row. Penalised ids (history window
-// or logit bias) are left out: k_merge finishes them from the row's counts.
+// or logit bias) are left out, or in flag mode appended with a flag: k_merge
+// finishes them from the row's counts.
 // PEN / MASK: some row of the launch has penalties / an allowed-token mask.
 // LDS: [penalised-id bitmap][allowed-id mask words], one bit per slice id.
-template <int DT, bool VEC, bool PEN, bool MASK>
+// GR: the launch's greedy rows (true) or sampling rows (false); a batch with
+// both takes one launch of each, so that each loop has the whole register
+// budget of five blocks per CU.
+template <int DT, bool VEC, bool PEN, bool MASK, bool GR>
 __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
     using T = Tile<DT>;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -1287,144 +1471,42 @@ __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
     if (P.flags & RF_FULL) return;   // k_full's row
     const int lo = s * a.slice_len;
     const int hi = min(a.vocab - (VEC ? a.vec_tail : 0), lo + a.slice_len);   // k_merge takes the ragged end
-    const int words = a.bitmap_words;
-    const bool greedy = (P.flags & RF_GREEDY) != 0;
+    if (((P.flags & RF_GREEDY) != 0) != GR) return;   // the other kernel's row
     const bool pen = PEN && (P.flags & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) != 0;
     const bool masked = MASK && (P.flags & RF_MASK) != 0;
     const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * T::ES;
 
-    // The history goes out first (it is waited for first), then the first tile.
+    // The history window goes out first (it is waited for first), then the
+    // first tiles. Branch-free: clamped loads (pre[q] holds position
+    // p0 + q * kBlock + tid, used only below L), so nothing here waits.
     int32_t pre[8];
     const int L = P.hist_len, p0 = L - P.scan_len;
     const int32_t* hrow = a.hist + (int64_t)r * a.hist_stride;
-    if (PEN) {
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int p = p0 + q * kBlock + tid;
-            pre[q] = (pen && p < L) ? hrow[p] : -1;
-        }
+    for (int q = 0; q < 8; ++q) pre[q] = -1;
+    if (PEN && pen && L > 0) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) pre[q] = hrow[max(0, min(p0 + q * kBlock + tid, L - 1))];
     }
-    uint4 raw[T::NCH];
-    load_tile<DT, VEC>(rowp, lo, hi, raw);
     uint32_t* pbm = reinterpret_cast<uint32_t*>(smem);
-    uint32_t* mbm = pbm + words;
-    if (tid == 0) {
-        st.theta = kThetaFloor;
-        st.n = greedy ? 1 : 0;   // a greedy row's argmax goes to out[0]
-        st.flags = 0;
+    stream_setup<PEN, MASK>(a, P, r, lo, hi, GR, pen, masked, p0, L, hrow, pbm, pbm + a.bitmap_words, st);
+    // the first tile (processed chunk by chunk as its loads complete in order)
+    const __amdgpu_buffer_rsrc_t rs = row_rsrc(rowp, hi, T::ES);
+    uint4 raw[T::NCH];
+    load_tile<DT, VEC>(rs, lo, raw);
+    if (PEN) {
+        // the history window (waits for pre[] only: the tiles were requested after)
+        if (pen) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                if (p0 + q * kBlock + tid < L) stream_mark(pre[q], lo, hi, pbm);
+        }
+        __syncthreads();
     }
-    for (int i = tid; i < words; i += kBlock) {
-        if (PEN) pbm[i] = 0u;
-        if (masked) mbm[i] = (lo + 32 * i < hi) ? a.mask[(int64_t)r * a.mask_stride + (lo >> 5) + i] : 0u;
-        else if (MASK) mbm[i] = 0xFFFFFFFFu;
-    }
-    __syncthreads();
     const int64_t slot = (int64_t)r * a.nslices + s;
     u64* out = a.cand + slot * a.cand_cap;
-    if (pen) {
-        // the ids the penalty stages touch (sampler.cpp:236-258): k_merge
-        // finishes them from the row's counts
-        auto mark = [&](int t) {
-            if (t >= lo && t < hi) atomicOr(&pbm[(t - lo) >> 5], 1u << ((t - lo) & 31));
-        };
-#pragma unroll
-        for (int q = 0; q < 8; ++q) mark(pre[q]);
-        for (int p = p0 + 8 * kBlock + tid; p < L; p += kBlock) mark(hrow[p]);
-        if (P.flags & RF_BIAS)
-            for (int j = tid; j < P.bias_cnt; j += kBlock) mark(a.bias_ids[P.bias_off + j]);
-    }
-    if (PEN) __syncthreads();
-
-    const int k = P.top_k;
-    const int kw = (k + 3) >> 2;
-    const int G = min(4, max(1, (kw + 63) >> 6));
-    const float inv_t = P.inv_temp;
-    const bool pflag = a.pen_flag != 0;
-    bool nanseen = false;
-    uint32_t bk = 0u;          // greedy: best key and its first id so far
-    int32_t bi = 0x7FFFFFFF;
-
-    for (int tb = lo;;) {
-        uint32_t kv[T::NE];
-        uint32_t pm;
-        const int bt = tb + tid * T::VW;
-        // ids of this thread's 32 elements; penalised ones (flag mode) carry bit
-        // 31, which clears bit 31 of their composite's low word for k_merge
-        auto idx = [&](int i) -> int32_t {
-            return (bt + (i / T::VW) * (kBlock * T::VW) + (i % T::VW)) | (int32_t)(((pm >> i) & 1u) << 31);
-        };
-        if (greedy) {
-            // argmax of sampler.cpp:220-228; k_merge settles id 0 holding a NaN
-            tile_keys<DT, PEN, MASK, true>(raw, tb, lo, hi, pbm, mbm, inv_t, pflag, kv, pm, nanseen);
-            uint32_t m = 0u;
-#pragma unroll
-            for (int i = 0; i < T::NE; ++i) m = max(m, ((pm >> i) & 1u) ? 0u : kv[i]);
-            int32_t mi = 0x7FFFFFFF;
-#pragma unroll
-            for (int i = T::NE - 1; i >= 0; --i)
-                mi = (kv[i] == m && !((pm >> i) & 1u)) ? (bt + (i / T::VW) * (kBlock * T::VW) + (i % T::VW)) : mi;
-            if (m > bk || (m == bk && mi < bi)) {
-                bk = m;
-                bi = mi;
-            }
-            if (PEN && pflag && __ballot(pm != 0u) != 0ull) {
-                // every penalised id goes to k_merge, which finds its true value
-                uint32_t pk[T::NE];
-#pragma unroll
-                for (int i = 0; i < T::NE; ++i) pk[i] = ((pm >> i) & 1u) ? kv[i] : 0u;
-                append_out<T::NE>(out, pk, idx, 1u, st);
-            }
-        } else {
-            tile_keys<DT, PEN, MASK, false>(raw, tb, lo, hi, pbm, mbm, inv_t, pflag, kv, pm, nanseen);
-            // A lower bound on the row's k-th largest from this tile: each
-            // wave's kw-th largest group maximum (kw = ceil(k/4)), low 16 bits
-            // cleared, minimum over the 4 waves; the block keeps the highest
-            // bound seen so far. Keys at or above it survive.
-            // (penalised keys, pre-penalty upper bounds, take no part in the bound)
-            uint32_t gk[4] = {0u, 0u, 0u, 0u}, lm = 0u;
-#pragma unroll
-            for (int j = 0; j < T::NCH; ++j) {
-#pragma unroll
-                for (int c = 0; c < T::VW; ++c) {
-                    const int i = j * T::VW + c;
-                    gk[(j * 4) / T::NCH] = max(gk[(j * 4) / T::NCH], ((pm >> i) & 1u) ? 0u : kv[i]);
-                    lm = max(lm, kv[i]);
-                }
-            }
-            const uint32_t lmax = lm;
-            if (G == 2) {
-                gk[0] = max(gk[0], gk[1]);
-                gk[1] = max(gk[2], gk[3]);
-            } else if (G == 1) {
-                gk[0] = lmax;
-            }
-            const uint32_t tw = (kw <= 64 * G) ? wave_kth_bound16(gk, G, kw) : 0u;
-            if (lane_id() == 0) st.twave[wave_id()] = tw;
-            __syncthreads();
-            uint32_t tt = st.twave[0];
-#pragma unroll
-            for (int i = 1; i < kBlock / 64; ++i) tt = min(tt, st.twave[i]);
-            const uint32_t th0 = (uint32_t)(st.theta >> 32);
-            __syncthreads();
-            const uint32_t thk = max(max(tt, th0), (uint32_t)(kThetaFloor >> 32));
-            if (tid == 0) st.theta = (u64)thk << 32;
-            if (__ballot(lmax >= thk) != 0ull) append_out<T::NE>(out, kv, idx, thk, st);
-        }
-        tb += T::ELEMS;
-        if (tb >= hi) break;
-        load_tile<DT, VEC>(rowp, tb, hi, raw);
-    }
-
-    // ---- the slice's counts for k_merge ----------------------------------------
-    if (nanseen) atomicOr(&st.flags, 1);
-    u64 best = 0ull;
-    if (greedy) best = block_max_u64(bk != 0u ? comp(bk, bi) : 0ull, st);   // has the barrier the flag needs
-    else __syncthreads();
-    if (tid == 0) {
-        const int nanf = (st.flags & 1) ? (1 << 30) : 0;
-        if (greedy) out[0] = best;
-        a.cand_n[slot] = st.n | nanf;
-    }
+    if constexpr (GR) stream_greedy<DT, VEC, PEN, MASK>(a, P, r, lo, hi, rs, raw, out, slot, smem, st);
+    else stream_sample<DT, VEC, PEN, MASK>(a, P, r, lo, hi, rs, raw, out, slot, smem, st);
 }
 
 // ---- the merge kernel ------------------------------------------------------------
@@ -1726,11 +1808,11 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
 
     int nl = 0;   // flag mode: entries of pid / pv
     if (lmode) {
-        // flagged list entries (bit 31 of the low word clear) and the ragged
-        // end leave the register set for the list
+        // flagged list entries (key kKeyFlag) and the ragged end leave the
+        // register set for the list
         uint32_t fm = 0u;
 #pragma unroll
-        for (int j = 0; j < NW; ++j) fm |= (win[j] != 0ull && !((uint32_t)win[j] & 0x80000000u)) ? (1u << j) : 0u;
+        for (int j = 0; j < NW; ++j) fm |= ((uint32_t)(win[j] >> 32) == kKeyFlag) ? (1u << j) : 0u;
         const int cnt = __popc(fm) + (tail_t >= 0 ? 1 : 0);
         if (__ballot(cnt != 0) != 0ull) {
             int incl = cnt;
@@ -1745,7 +1827,7 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
 #pragma unroll
             for (int j = 0; j < NW; ++j) {
                 if ((fm >> j) & 1u) {
-                    if (pos < kFlagCap) pid[pos] = ~(uint32_t)win[j] & 0x7FFFFFFFu;
+                    if (pos < kFlagCap) pid[pos] = ~(uint32_t)win[j];
                     ++pos;
                     win[j] = 0ull;
                 }
@@ -2870,11 +2952,12 @@ __global__ __launch_bounds__(kBlock) void k_full(StreamArgs a) {
 
 // ---- launchers -------------------------------------------------------------------
 
-hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int grid,
-                         hipStream_t stream) {
+template <bool GR>
+static void launch_stream_kind(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int grid,
+                               hipStream_t stream) {
     const dim3 g(grid), b(kBlock);
     const uint32_t l = a.lds_bytes;
-#define HSAMP_STREAM(DT_, V_, P_, M_) hipLaunchKernelGGL((k_stream<DT_, V_, P_, M_>), g, b, l, stream, a)
+#define HSAMP_STREAM(DT_, V_, P_, M_) hipLaunchKernelGGL((k_stream<DT_, V_, P_, M_, GR>), g, b, l, stream, a)
     if (!vec) {   // unaligned rows: one general kernel per element type
         if (dtype == 0) HSAMP_STREAM(0, false, true, true);
         else HSAMP_STREAM(1, false, true, true);
@@ -2896,6 +2979,12 @@ hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, bool pen, boo
         }
     }
 #undef HSAMP_STREAM
+}
+
+hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, bool greedy_rows,
+                         bool sample_rows, int grid, hipStream_t stream) {
+    if (greedy_rows) launch_stream_kind<true>(a, dtype, vec, pen, mask, grid, stream);
+    if (sample_rows) launch_stream_kind<false>(a, dtype, vec, pen, mask, grid, stream);
     return hipGetLastError();
 }
 

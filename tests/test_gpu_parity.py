@@ -256,6 +256,34 @@ def test_run_rejects_invalid_requests(sampler, hs, wl):
     torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("greedy_rows", [0, 6, 12])
+def test_long_history_of_top_tokens(sampler, wl, greedy_rows):
+    """2048-id histories drawn mostly from each row's 300 highest logits, ids
+    repeated many times over the frequency, presence and repetition windows:
+    hundreds of penalised candidates per row reach the merge (flag mode), and
+    a batch mixing greedy and sampling rows takes both stream kernels."""
+    rng = np.random.default_rng(4242 + greedy_rows)
+    B, V, H = 12, 151936, 2048
+    x = rng.normal(size=(B, V)).astype(np.float32)
+    hist = np.empty((B, H), np.int32)
+    for r in range(B):
+        top = np.argsort(-x[r])[:300]
+        pool = np.concatenate([rng.choice(top, 1600), rng.integers(0, V, 448)])
+        hist[r] = rng.permutation(pool)
+    plist = []
+    for r in range(B):
+        if r < greedy_rows:
+            plist.append(wl.identity_params(temperature=0.0, rep_penalty=1.1, repeat_last_n=2048,
+                                            frequency_penalty=0.5, presence_penalty=0.3))
+        else:
+            plist.append(wl.identity_params(temperature=0.7, top_k=50, rep_penalty=1.1, repeat_last_n=1024,
+                                            frequency_penalty=0.5, presence_penalty=0.3))
+    w = _wl_from(wl, x, plist, rng.random(B))
+    w.hist, w.hist_len = hist, np.full(B, H, np.int64)
+    g = run_gpu(sampler, w)
+    assert compare_rows(w, g) == B
+
+
 @pytest.mark.parametrize("greedy_rows", [0, 2])
 def test_penalised_top_tokens_flag_mode(sampler, wl, greedy_rows):
     """Histories that hold the rows' highest logits, repeated: the penalised ids

@@ -533,9 +533,14 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     // (flag mode: [bins][list][ids, counts / composites of penalised candidates][buffer])
     const bool fast0 = kmax <= 64 && !gtab && bl.max_scan <= 8 * kBlock && bl.max_bias <= kBlock;
     const bool pen_flag = fast0 && bl.any_pen && bl.pen_lowers;
-    const size_t fast_lds = pen_flag ? 9216 + 12 * (size_t)kFlagCap + 8 * (size_t)buf_cap
+    // flag mode: after the list, counters of the history's ids, a bitmap over
+    // the vocabulary (16 B per 128 ids) and its rank prefixes (2 B per 128
+    // ids), which the buffer replaces once the values are found; one merge
+    // block per row, so it may use the whole LDS of a CU
+    const size_t ngroups = ((size_t)V + 127) / 128;
+    const size_t fast_lds = pen_flag ? 9216 + std::max(8 * (size_t)kCntCap + align16(18 * ngroups), 8 * (size_t)buf_cap)
                                      : 9216 + std::max(12 * (size_t)mhash, 8 * (size_t)buf_cap);
-    const bool fast = fast0 && fast_lds <= lds_budget;
+    const bool fast = fast0 && fast_lds <= (pen_flag ? h->lds_limit - statik : lds_budget);
     if (fast) merge_lds = std::max(merge_lds, fast_lds);
     const size_t wb_lds = (gtab ? 0 : 8 * (size_t)mhash) + 4 * (size_t)bitmap_words;
     if (merge_lds + statik > h->lds_limit || wb_lds + statik > h->lds_limit ||

@@ -24,6 +24,8 @@
 // No MFMA: nothing here is a contraction. The stream phase is HBM-bound.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "hsamp_plan.h"
 #include "libm_expf.h"
 
@@ -780,21 +782,19 @@ __device__ __forceinline__ void wave_sync() {
 }
 
 // Ascending sort of 64 distinct keys across the lanes (payload travels along).
+// All 64 keys are read before any is compared, so the LDS latency is paid once.
 __device__ __forceinline__ void wave_sort_asc(uint32_t& key, uint32_t& pay, u64* wv) {
     const int lane = lane_id();
     uint32_t* w = reinterpret_cast<uint32_t*>(wv);
     w[lane] = key;
     wave_sync();
-    int rank = 0;
     const uint4* w4 = reinterpret_cast<const uint4*>(w);
-#pragma unroll 1
-    for (int q0 = 0; q0 < 16; q0 += 4) {
+    uint4 x[16];
 #pragma unroll
-        for (int q = q0; q < q0 + 4; ++q) {
-            const uint4 x = w4[q];
-            rank += (x.x < key) + (x.y < key) + (x.z < key) + (x.w < key);
-        }
-    }
+    for (int q = 0; q < 16; ++q) x[q] = w4[q];
+    int rank = 0;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) rank += (x[q].x < key) + (x[q].y < key) + (x[q].z < key) + (x[q].w < key);
     wave_sync();
     w[rank] = key;
     w[64 + rank] = pay;
@@ -809,16 +809,13 @@ __device__ __forceinline__ u64 wave_sort_desc(u64 key, u64* wv) {
     const int lane = lane_id();
     wv[lane] = key;
     wave_sync();
-    int rank = 0;
     const ulonglong2* w2 = reinterpret_cast<const ulonglong2*>(wv);
-#pragma unroll 1
-    for (int q0 = 0; q0 < 32; q0 += 4) {
+    ulonglong2 x[32];
 #pragma unroll
-        for (int q = q0; q < q0 + 4; ++q) {
-            const ulonglong2 x = w2[q];
-            rank += (x.x > key) + (x.y > key);
-        }
-    }
+    for (int q = 0; q < 32; ++q) x[q] = w2[q];
+    int rank = 0;
+#pragma unroll
+    for (int q = 0; q < 32; ++q) rank += (x[q].x > key) + (x[q].y > key);
     wave_sync();
     wv[rank] = key;
     wave_sync();
@@ -829,20 +826,23 @@ __device__ __forceinline__ u64 wave_sort_desc(u64 key, u64* wv) {
 
 // Lane-order float sum of x over the 64 lanes, starting from +0.0f. Every
 // value must be >= +0 (absent lanes pass +0.0f): the extra +0 terms then leave
-// the index-order sum of the present ones bit for bit.
+// the index-order sum of the present ones bit for bit. Every lane reads all 64
+// values up front and runs the same chain of adds.
 __device__ __forceinline__ float wave_seq_sum_f(float x, u64* wv) {
     float* w = reinterpret_cast<float*>(wv);
     w[lane_id()] = x;
     wave_sync();
     const float4* w4 = reinterpret_cast<const float4*>(w);
+    float4 v[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) v[q] = w4[q];
     float s = 0.0f;
-#pragma unroll 4
+#pragma unroll
     for (int q = 0; q < 16; ++q) {
-        const float4 v = w4[q];
-        s = s + v.x;
-        s = s + v.y;
-        s = s + v.z;
-        s = s + v.w;
+        s = s + v[q].x;
+        s = s + v[q].y;
+        s = s + v[q].z;
+        s = s + v[q].w;
     }
     wave_sync();
     return s;
@@ -856,17 +856,19 @@ __device__ __forceinline__ float wave_seq_prefix_f(float x, u64* wv) {
     w[lane] = x;
     wave_sync();
     const float4* w4 = reinterpret_cast<const float4*>(w);
+    float4 v[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) v[q] = w4[q];
     float s = 0.0f, mine = 0.0f;
-#pragma unroll 4
+#pragma unroll
     for (int q = 0; q < 16; ++q) {
-        const float4 v = w4[q];
-        s = s + v.x;
+        s = s + v[q].x;
         mine = (lane == 4 * q) ? s : mine;
-        s = s + v.y;
+        s = s + v[q].y;
         mine = (lane == 4 * q + 1) ? s : mine;
-        s = s + v.z;
+        s = s + v[q].z;
         mine = (lane == 4 * q + 2) ? s : mine;
-        s = s + v.w;
+        s = s + v[q].w;
         mine = (lane == 4 * q + 3) ? s : mine;
     }
     wave_sync();
@@ -879,15 +881,14 @@ __device__ __forceinline__ double wave_seq_sum_d(double x, u64* wv) {
     w[lane_id()] = x;
     wave_sync();
     const double2* w2 = reinterpret_cast<const double2*>(w);
-    double s = 0.0;
-#pragma unroll 1
-    for (int q0 = 0; q0 < 32; q0 += 8) {
+    double2 v[32];
 #pragma unroll
-        for (int q = q0; q < q0 + 8; ++q) {
-            const double2 v = w2[q];
-            s = s + v.x;
-            s = s + v.y;
-        }
+    for (int q = 0; q < 32; ++q) v[q] = w2[q];
+    double s = 0.0;
+#pragma unroll
+    for (int q = 0; q < 32; ++q) {
+        s = s + v[q].x;
+        s = s + v[q].y;
     }
     wave_sync();
     return s;
@@ -899,17 +900,16 @@ __device__ __forceinline__ double wave_seq_prefix_d(double x, u64* wv) {
     w[lane] = x;
     wave_sync();
     const double2* w2 = reinterpret_cast<const double2*>(w);
-    double s = 0.0, mine = 0.0;
-#pragma unroll 1
-    for (int q0 = 0; q0 < 32; q0 += 8) {
+    double2 v[32];
 #pragma unroll
-        for (int q = q0; q < q0 + 8; ++q) {
-            const double2 v = w2[q];
-            s = s + v.x;
-            mine = (lane == 2 * q) ? s : mine;
-            s = s + v.y;
-            mine = (lane == 2 * q + 1) ? s : mine;
-        }
+    for (int q = 0; q < 32; ++q) v[q] = w2[q];
+    double s = 0.0, mine = 0.0;
+#pragma unroll
+    for (int q = 0; q < 32; ++q) {
+        s = s + v[q].x;
+        mine = (lane == 2 * q) ? s : mine;
+        s = s + v[q].y;
+        mine = (lane == 2 * q + 1) ? s : mine;
     }
     wave_sync();
     return mine;
@@ -1005,7 +1005,7 @@ __device__ __forceinline__ u64 wave_topk(const u64* buf, int n, int k, u64* wv) 
 // The ladder after top-k for one row, by one wave: lane l < nk holds a
 // composite of the row's top-k set (any order), nk <= 64. Same semantics as
 // finalize_row.
-__device__ __attribute__((noinline)) void wave_finalize(const StreamArgs& a, const RowPlan& P, int r, u64 c, int nk,
+__device__ __forceinline__ void wave_finalize(const StreamArgs& a, const RowPlan& P, int r, u64 c, int nk,
                                                         uint32_t rflags, Shared& st) {
     const int lane = lane_id();
     const int V = a.vocab;
@@ -1319,8 +1319,8 @@ __device__ __forceinline__ void stream_setup(const StreamArgs& a, const RowPlan&
 
 // The greedy row's slice (argmax of sampler.cpp:220-228): the first id of the
 // largest key goes to out[0]; k_merge settles id 0 holding a NaN. In flag
-// mode every penalised id is appended too (pre-penalty key, flagged), for
-// k_merge to find its true value.
+// mode the penalised ids that can still win are appended too (flagged), for
+// k_merge to find their true values.
 template <int DT, bool VEC, bool PEN, bool MASK>
 __device__ __forceinline__ void stream_greedy(const StreamArgs& a, const RowPlan& P, int r, int lo, int hi,
                                               __amdgpu_buffer_rsrc_t rs, uint4 (&raw)[Tile<DT>::NCH],
@@ -1351,11 +1351,21 @@ __device__ __forceinline__ void stream_greedy(const StreamArgs& a, const RowPlan
             bi = mi;
         }
         if (PEN && pflag && __ballot(pm != 0u) != 0ull) {
-            // penalised ids go with the flag key kKeyFlag
+            // A penalised id's true value is at most its key here (penalties
+            // only lower it), so only those reaching the wave's best key so
+            // far can be the argmax; they go with the flag key kKeyFlag.
+            uint32_t wb = bk;
 #pragma unroll
-            for (int i = 0; i < T::NE; ++i) kv[i] = kKeyFlag;
-            auto idx = [&](int i) -> int32_t { return bt + (i / T::VW) * (kBlock * T::VW) + (i % T::VW); };
-            append_sel<T::NE>(out, kv, idx, pm, st);
+            for (int d = 32; d > 0; d >>= 1) wb = max(wb, (uint32_t)__shfl_xor((int)wb, d, 64));
+            uint32_t sel = 0u;
+#pragma unroll
+            for (int i = 0; i < T::NE; ++i) sel |= (((pm >> i) & 1u) && kv[i] >= wb) ? (1u << i) : 0u;
+            if (__ballot(sel != 0u) != 0ull) {
+#pragma unroll
+                for (int i = 0; i < T::NE; ++i) kv[i] = kKeyFlag;
+                auto idx = [&](int i) -> int32_t { return bt + (i / T::VW) * (kBlock * T::VW) + (i % T::VW); };
+                append_sel<T::NE>(out, kv, idx, sel, st);
+            }
         }
     };
     for (int tb = lo;;) {
@@ -1645,23 +1655,82 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
     u64* tval = reinterpret_cast<u64*>(smem + 9216 + 4 * fs);
     const uint32_t hmask = (uint32_t)fs - 1u, hshift = 32u - (uint32_t)__popc(hmask);
     // flag mode (penalties only lower logits): the stream handed penalised ids
-    // over with their pre-penalty keys; their true values are found for just
-    // those ids, from the history held in registers, without a table.
-    // LDS there: [bins][list][pid: kFlagCap ids][pv: kFlagCap counts, then composites]
+    // over flagged; their true values are found for just those ids, from
+    // counters of the history's ids, without a table.
+    // LDS there: [bins][list][counters: 64 bits per distinct history id]
+    // [vocabulary bitmap: 16 B per 128 ids][rank prefixes: 2 B per 128 ids],
+    // all after the list replaced by the buffer once the values are found
     const bool lmode = a.pen_flag != 0;
-    uint32_t* pid = reinterpret_cast<uint32_t*>(smem + 9216);
-    u64* pv = reinterpret_cast<u64*>(smem + 9216 + 4 * kFlagCap);
+    u64* cnt = reinterpret_cast<u64*>(smem + 9216);
+    uint4* vb4 = reinterpret_cast<uint4*>(smem + 9216 + 8 * kCntCap);
     if (pen && !lmode) {
         for (int i = tid; i < fs; i += kBlock) {
             tkey[i] = kEmpty;
             tval[i] = 0ull;
         }
     }
-    if (lmode)
-        for (int i = tid; i < kFlagCap; i += kBlock) pv[i] = 0ull;
+    if (lmode && pen) {
+        for (int i = tid; i < kCntCap; i += kBlock) cnt[i] = 0ull;
+        for (int i = tid; i < ((a.vocab + 127) >> 7); i += kBlock) vb4[i] = make_uint4(0u, 0u, 0u, 0u);
+    }
     for (int i = tid; i < 2048; i += kBlock) bins[i] = 0u;
-    if (tid == 0) st.last = 0;   // flag-mode list length
     __syncthreads();   // also publishes the slice counts
+
+    // Flag mode, before anything waits for the lists: counters of the
+    // history's ids. A bitmap over the vocabulary marks the ids, and an id's
+    // rank among them (prefix popcounts per 128 ids) indexes its counters.
+    const int ng = (a.vocab + 127) >> 7;
+    const uint16_t* vp = reinterpret_cast<const uint16_t*>(vb4 + ng);
+    if (lmode && pen) {
+        uint32_t* vb = reinterpret_cast<uint32_t*>(vb4);
+        uint16_t* vpw = reinterpret_cast<uint16_t*>(vb4 + ng);
+        const int L = P.hist_len, p0 = L - P.scan_len;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int p = p0 + q * kBlock + tid;
+            if (p >= 0 && p < L && pre[q] >= 0 && pre[q] < a.vocab) atomicOr(&vb[pre[q] >> 5], 1u << (pre[q] & 31));
+        }
+        __syncthreads();
+        {
+            const int per = (ng + kBlock - 1) / kBlock;
+            const int g0 = min(ng, tid * per), g1 = min(ng, g0 + per);
+            int sum = 0;
+            for (int g = g0; g < g1; ++g) {
+                const uint4 w = vb4[g];
+                sum += __popc(w.x) + __popc(w.y) + __popc(w.z) + __popc(w.w);
+            }
+            int tot;
+            int run = block_excl_scan(sum, &tot, st);
+            for (int g = g0; g < g1; ++g) {
+                const uint4 w = vb4[g];
+                vpw[g] = (uint16_t)run;
+                run += __popc(w.x) + __popc(w.y) + __popc(w.z) + __popc(w.w);
+            }
+        }
+        __syncthreads();
+    }
+    // rank of id t among the marked ids, or -1 when t is not marked
+    auto rank = [&](int t) -> int {
+        const uint4 w = vb4[t >> 7];
+        const int wi = (t >> 5) & 3;
+        const uint32_t wt = wi == 0 ? w.x : wi == 1 ? w.y : wi == 2 ? w.z : w.w;
+        const int rk = (int)vp[t >> 7] + (wi > 0 ? __popc(w.x) : 0) + (wi > 1 ? __popc(w.y) : 0) +
+                       (wi > 2 ? __popc(w.z) : 0) + __popc(wt & ((1u << (t & 31)) - 1u));
+        return ((wt >> (t & 31)) & 1u) ? rk : -1;
+    };
+    if (lmode && pen) {
+        const int L = P.hist_len, p0 = L - P.scan_len;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int p = p0 + q * kBlock + tid;
+            if (p >= 0 && p < L && pre[q] >= 0 && pre[q] < a.vocab) {
+                const u64 add = ((p >= L - P.fp_win) ? 1ull : 0ull) | ((p >= L - P.dry_win) ? (1ull << 16) : 0ull) |
+                                ((p >= L - P.rep_win) ? (1ull << 32) : 0ull);
+                atomicAdd(&cnt[rank(pre[q])], add);
+            }
+        }
+        __syncthreads();
+    }
 
     // ---- penalised ids ------------------------------------------------------------
     u64 cp[9];
@@ -1804,93 +1873,27 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
         const int s2 = (int)__umulhi((uint32_t)g, a.win_magic);   // g / W
         if (s2 >= S || g - s2 * W >= st.soff[s2]) win[j] = 0ull;
     }
-    for (int s2 = 0; s2 < S; ++s2) extra += max(0, st.soff[s2] - W);
+    extra = (st.flags & 8) ? 1 : 0;   // some slice's list runs past the window
 
-    int nl = 0;   // flag mode: entries of pid / pv
     if (lmode) {
-        // flagged list entries (key kKeyFlag) and the ragged end leave the
-        // register set for the list
-        uint32_t fm = 0u;
-#pragma unroll
-        for (int j = 0; j < NW; ++j) fm |= ((uint32_t)(win[j] >> 32) == kKeyFlag) ? (1u << j) : 0u;
-        const int cnt = __popc(fm) + (tail_t >= 0 ? 1 : 0);
-        if (__ballot(cnt != 0) != 0ull) {
-            int incl = cnt;
-#pragma unroll
-            for (int d = 1; d < 64; d <<= 1) {
-                const int y = __shfl_up(incl, d, 64);
-                if (lane >= d) incl += y;
-            }
-            int base = 0;
-            if (lane == 63) base = atomicAdd(&st.last, incl);
-            int pos = __shfl(base, 63, 64) + incl - cnt;
-#pragma unroll
-            for (int j = 0; j < NW; ++j) {
-                if ((fm >> j) & 1u) {
-                    if (pos < kFlagCap) pid[pos] = ~(uint32_t)win[j];
-                    ++pos;
-                    win[j] = 0ull;
-                }
-            }
-            if (tail_t >= 0) {
-                if (pos < kFlagCap) pid[pos] = (uint32_t)tail_t | 0x80000000u;   // mark: ragged end
-                ++pos;
-            }
-        }
-        __syncthreads();
-        nl = st.last;
-        if (nl > kFlagCap) {
-            // more flagged ids than the list holds (at most scan + bias + tail,
-            // so only when kFlagCap is set below that): not reached on the
-            // host's fast-path limits
-            nl = kFlagCap;
-        }
-        // raw logits of the listed ids, 4 loads in flight per thread per round
+        // Flag mode: the flagged window entries (key kKeyFlag) and the ragged
+        // end get their true values in place (stages 1-6, sampler.cpp:235-264),
+        // from the row's raw logits and their ids' counts in the history
+        // windows. Their logits (and mask words) are requested first; the
+        // counts are built while those loads are in flight.
         const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * (a.dtype == 0 ? 4 : 2);
-        constexpr int NJ = kFlagCap / kBlock;
-        float xr[NJ];
+        int32_t ft[NW];
 #pragma unroll
-        for (int j0 = 0; j0 < NJ; j0 += 4) {
-            if (j0 * kBlock >= nl) break;
-            int32_t t4[4];
+        for (int j = 0; j < NW; ++j) ft[j] = ((uint32_t)(win[j] >> 32) == kKeyFlag) ? (int32_t)comp_idx(win[j]) : -1;
+        float xr[NW];
+        load_logits<NW>(rowp, a.dtype, ft, xr);
+        uint32_t mwf[NW];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int e = tid + (j0 + q) * kBlock;
-                t4[q] = (j0 + q < NJ && e < nl) ? (int32_t)(pid[e] & 0x7FFFFFFFu) : -1;
-            }
-            float x4[4];
-            load_logits<4>(rowp, a.dtype, t4, x4);
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                if (j0 + q < NJ) xr[j0 + q] = x4[q];
-        }
-        // counts: each thread checks its 8 history ids against every listed id
-        if (pen) {
-            const int L = P.hist_len, p0 = L - P.scan_len;
-            u64 addq[8];
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const int p = p0 + q * kBlock + tid;
-                addq[q] = ((p >= L - P.fp_win) ? 1ull : 0ull) | ((p >= L - P.dry_win) ? (1ull << 16) : 0ull) |
-                          ((p >= L - P.rep_win) ? (1ull << 32) : 0ull);
-            }
-            for (int e = 0; e < nl; ++e) {
-                const int32_t t = (int32_t)(pid[e] & 0x7FFFFFFFu);
-                u64 add = 0ull;
-#pragma unroll
-                for (int q = 0; q < 8; ++q) add += (pre[q] == t) ? addq[q] : 0ull;
-                if (add) atomicAdd(&pv[e], add);
-            }
-        }
-        __syncthreads();
-        // true values (stages 1-6, sampler.cpp:235-264), then the composite
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            const int e = tid + j * kBlock;
-            if (e >= nl) break;
-            const uint32_t w = pid[e];
-            const int32_t t = (int32_t)(w & 0x7FFFFFFFu);
-            const u64 c = pv[e];
+        for (int j = 0; j < NW; ++j)
+            mwf[j] = (masked && ft[j] >= 0) ? a.mask[(int64_t)r * a.mask_stride + (ft[j] >> 5)] : 0xFFFFFFFFu;
+        // the true value of id t (raw logit x, allowed by the mask or not,
+        // history counters c) as a composite; 0 (absent) for a greedy row's NaN
+        auto value = [&](int32_t t, float x, bool allowed, u64 c) -> u64 {
             uint32_t v = ((c >> 32) & 0xFFFFull ? HV_REP : 0u) | ((uint32_t)((c >> 16) & 0xFFFFull) << HV_DRY_SHIFT) |
                          (uint32_t)(c & 0xFFFFull);
             if (P.flags & RF_BIAS) {
@@ -1903,22 +1906,31 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
                 }
                 if (lo < P.bias_cnt && ids[lo] == t) v |= HV_BIAS;
             }
-            float y = xr[j];
-            // the ragged end was not masked by the stream
-            if ((w & 0x80000000u) && masked && !((a.mask[(int64_t)r * a.mask_stride + (t >> 5)] >> (t & 31)) & 1u))
-                y = -__builtin_inff();
+            float y = allowed ? x : -__builtin_inff();
             y = pen_value(y, t, v, sa, sP);
-            u64 out = 0ull;
             if (!greedy) y = y * P.inv_temp;
             if (y != y) {
                 atomicOr(&st.flags, 4);
-                if (!greedy) out = comp(kKeyNegInf, t);
-            } else {
-                out = comp(key32(y), t);
+                return greedy ? 0ull : comp(kKeyNegInf, t);
             }
-            pv[e] = out;
+            return comp(key32(y), t);
+        };
+        // batched: every rank first, then every counter, then the values
+        u64 cj[NW];
+        if (pen) {
+            int rk[NW];
+#pragma unroll
+            for (int j = 0; j < NW; ++j) rk[j] = ft[j] >= 0 ? rank(ft[j]) : -1;
+#pragma unroll
+            for (int j = 0; j < NW; ++j) cj[j] = rk[j] >= 0 ? cnt[rk[j]] : 0ull;
         }
-        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < NW; ++j)
+            if (ft[j] >= 0) win[j] = value(ft[j], xr[j], (mwf[j] >> (ft[j] & 31)) & 1u, pen ? cj[j] : 0ull);
+        if (tail_t >= 0) {
+            const int rk = pen ? rank(tail_t) : -1;
+            ct = value(tail_t, tail_x, tail_ok, rk >= 0 ? cnt[rk] : 0ull);
+        }
     }
 
     if (greedy) {
@@ -1927,7 +1939,6 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
         for (int q = 0; q < 9; ++q) best = cp[q] > best ? cp[q] : best;
 #pragma unroll
         for (int j = 0; j < NW; ++j) best = win[j] > best ? win[j] : best;
-        for (int e = tid; e < nl; e += kBlock) best = pv[e] > best ? pv[e] : best;
         best = block_max_u64(best, st);
         __syncthreads();
         if (tid == 0) {
@@ -1947,7 +1958,6 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
     constexpr int NC = 10 + NW;
     const uint32_t floor_key = (uint32_t)(kThetaFloor >> 32);
     uint32_t lmax = (uint32_t)(ct >> 32);
-    for (int e = tid; e < nl; e += kBlock) lmax = max(lmax, (uint32_t)(pv[e] >> 32));
 #pragma unroll
     for (int q = 0; q < 9; ++q) lmax = max(lmax, (uint32_t)(cp[q] >> 32));
 #pragma unroll
@@ -1976,8 +1986,6 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
     const bool any = Mk >= Lk;
     if (any) {
         if ((uint32_t)(ct >> 32) >= Lk) atomicAdd(&bins[binof((uint32_t)(ct >> 32))], 1u);
-        for (int e = tid; e < nl; e += kBlock)
-            if ((uint32_t)(pv[e] >> 32) >= Lk) atomicAdd(&bins[binof((uint32_t)(pv[e] >> 32))], 1u);
 #pragma unroll
         for (int q = 0; q < 9; ++q) {
             const uint32_t key = (uint32_t)(cp[q] >> 32);
@@ -2030,13 +2038,8 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
             const uint32_t key = (uint32_t)(c >> 32);
             inm |= (any && key >= Lk && (int)binof(key) >= bstar) ? (1u << q) : 0u;
         }
-        int lcnt = 0;   // flag-mode entries of this thread that go too
-        for (int e = tid; e < nl; e += kBlock) {
-            const uint32_t key = (uint32_t)(pv[e] >> 32);
-            lcnt += (any && key >= Lk && (int)binof(key) >= bstar) ? 1 : 0;
-        }
-        if (__ballot(inm != 0u || lcnt != 0) != 0ull) {
-            const int cnt = __popc(inm) + lcnt;
+        if (__ballot(inm != 0u) != 0ull) {
+            const int cnt = __popc(inm);
             int incl = cnt;
 #pragma unroll
             for (int d = 1; d < 64; d <<= 1) {
@@ -2049,10 +2052,6 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
 #pragma unroll
             for (int q = 0; q < NC; ++q)
                 if ((inm >> q) & 1u) list[pos++] = (q < 9) ? cp[q] : (q == 9 ? ct : win[q - 10 < 0 ? 0 : q - 10]);
-            for (int e = tid; e < nl; e += kBlock) {
-                const uint32_t key = (uint32_t)(pv[e] >> 32);
-                if (any && key >= Lk && (int)binof(key) >= bstar) list[pos++] = pv[e];
-            }
         }
         __syncthreads();
         const uint32_t rflags = (st.flags & 4) ? ROWF_NAN : 0u;
@@ -2080,17 +2079,12 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
         wave_finalize(sa, sP, r, c, nk, rflags, st);
         return;
     }
-    // buffer path: the table is dead and the buffer takes its place (in flag
-    // mode it goes after the list, which is still read)
-    u64* buf = reinterpret_cast<u64*>(smem + 9216 + (lmode ? 12 * (size_t)kFlagCap : 0));
+    // buffer path: the table (or the counters) are dead and the buffer takes
+    // their place
+    u64* buf = reinterpret_cast<u64*>(smem + 9216);
     u64* ovf = a.ovf + (int64_t)r * a.ovf_cap;
     if (tid == 0) st.theta = (u64)Lk << 32;
     __syncthreads();
-    // (flag mode: the list's entries first, in rounds every thread joins)
-    for (int e0 = 0; e0 < nl; e0 += kBlock) {
-        const u64 c1[1] = {(e0 + tid < nl) ? pv[e0 + tid] : 0ull};
-        offer_regs<1>(buf, ovf, a.buf_cap, k, c1, st);
-    }
     offer_regs<9>(buf, ovf, a.buf_cap, k, cp, st);
     {
         const u64 c1[1] = {ct};
@@ -2135,47 +2129,96 @@ __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
     __shared__ RowPlan sP;
     constexpr int NW = 16;
     const int tid = threadIdx.x;
-    const int r = (int)blockIdx.x;
-    if (r >= a.rows) return;
-    const RowPlan P = a.plans[r];
-    if (P.flags & RF_FULL) return;   // k_full's row
+    // The row whose slices k_stream handed over on this block's XCD (blocks
+    // go to the XCDs round robin; row r's lists sit in the L2 of XCD
+    // r * nslices / blocks_per_xcd).
     const int S = a.nslices, W = a.win;
+    const int x = (int)(blockIdx.x % kXcds);
+    const int r0 = min(a.rows, (x * a.blocks_per_xcd + S - 1) / S);
+    const int r1 = min(a.rows, ((x + 1) * a.blocks_per_xcd + S - 1) / S);
+    const int r = r0 + (int)(blockIdx.x / kXcds);
+    if (r >= r1) return;
+    // Flag-mode launches read the plan first and request the history window
+    // ahead of the lists (loads complete in order), so that the counters are
+    // built while the lists are in flight; other launches request what needs
+    // no plan first: the slice counts, the window of the slices' lists, the
+    // ragged end and id 0's logit.
+    const bool hist_first = FAST && a.pen_flag != 0;
+    RowPlan P;
+    int32_t pre[8];
+    if (hist_first) {
+        P = a.plans[r];
+        if (P.flags & RF_FULL) return;   // k_full's row
+        // branch-free: clamped positions, used only below hist_len
+#pragma unroll
+        for (int q = 0; q < 8; ++q) pre[q] = -1;
+        const int L = P.hist_len;
+        if ((P.flags & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) && L > 0) {
+            const int32_t* h = a.hist + (int64_t)r * a.hist_stride;
+            const int p0 = L - P.scan_len;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) pre[q] = h[max(0, min(p0 + q * kBlock + tid, L - 1))];
+        }
+    }
+    const u64* cand = a.cand + (int64_t)r * S * a.cand_cap;
+    const int cnt_raw = (tid < S) ? a.cand_n[(int64_t)r * S + tid] : 0;
+    // one buffer resource over the row's lists: branch-free loads, entries
+    // past the last slice read as 0
+    u64 win[NW];
+    {
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<u64*>(cand), (short)0, S * a.cand_cap * 8, 0x00020000);
+        const uint32_t magic = a.win_magic;
+        const int cap = a.cand_cap;
+#pragma unroll
+        for (int j = 0; j < NW; ++j) {
+            const int g = tid + j * kBlock;
+            const int sl = (int)__umulhi((uint32_t)g, magic);   // g / W
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, (sl * cap + (g - sl * W)) * 8, 0, 0);
+            win[j] = ((u64)v[1] << 32) | v[0];
+        }
+    }
+    const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * (a.dtype == 0 ? 4 : 2);
+    // greedy: whether id 0 holds an allowed NaN; the row's ragged end (ids the
+    // stream's whole-chunk loads leave out)
+    const int32_t tail_t = (tid < a.vec_tail) ? a.vocab - a.vec_tail + tid : -1;
+    // raw bits, converted where used (no wait here); absent ids read past the
+    // row's buffer range and come back 0
+    uint32_t xb0, xb1;
+    {
+        const int es = a.dtype == 0 ? 4 : 2;
+        const __amdgpu_buffer_rsrc_t lr = row_rsrc(rowp, a.vocab, es);
+        const int o0 = tid == 0 ? 0 : a.vocab * es, o1 = (tail_t >= 0 ? tail_t : a.vocab) * es;
+        if (a.dtype == 0) {
+            xb0 = __builtin_amdgcn_raw_buffer_load_b32(lr, o0, 0, 0);
+            xb1 = __builtin_amdgcn_raw_buffer_load_b32(lr, o1, 0, 0);
+        } else {
+            xb0 = __builtin_amdgcn_raw_buffer_load_b16(lr, o0, 0, 0);
+            xb1 = __builtin_amdgcn_raw_buffer_load_b16(lr, o1, 0, 0);
+        }
+    }
+    if (!hist_first) {
+        P = a.plans[r];
+        if (P.flags & RF_FULL) return;   // k_full's row
+    }
     const bool greedy = (P.flags & RF_GREEDY) != 0;
     const bool pen = (P.flags & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) != 0;
     const bool masked = (P.flags & RF_MASK) != 0;
     const int k = P.top_k;
-    const u64* cand = a.cand + (int64_t)r * S * a.cand_cap;
     if (tid == 0) {
         st.flags = 0;
         st.nan0 = 0;
         st.n = 0;
         st.theta = kThetaFloor;
     }
-    int32_t pre[8];
-    hist_prefetch(a, P, r, pen, pre);
+    if (!hist_first) hist_prefetch(a, P, r, pen, pre);
     const int32_t bias_t = (FAST && (P.flags & RF_BIAS) && tid < P.bias_cnt) ? a.bias_ids[P.bias_off + tid] : -1;
-    const int cnt_raw = (tid < S) ? a.cand_n[(int64_t)r * S + tid] : 0;
-    const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * (a.dtype == 0 ? 4 : 2);
-    // greedy: whether id 0 holds an allowed NaN; the row's ragged end (ids the
-    // stream's whole-chunk loads leave out)
-    const int32_t tail_t = (tid < a.vec_tail) ? a.vocab - a.vec_tail + tid : -1;
-    float x2[2];
-    {
-        const int32_t t2[2] = {(greedy && tid == 0) ? 0 : -1, tail_t};
-        load_logits<2>(rowp, a.dtype, t2, x2);
-    }
-    const bool nan_at0 = greedy && tid == 0 && x2[0] != x2[0] &&
-                         (!masked || (a.mask[(int64_t)r * a.mask_stride] & 1u));
-    const float tail_x = x2[1];
+    auto logit_of = [&](uint32_t b) -> float { return __uint_as_float(a.dtype == 0 ? b : (b << 16)); };
+    const float x0 = logit_of(xb0);
+    const bool nan_at0 = greedy && tid == 0 && x0 != x0 && (!masked || (a.mask[(int64_t)r * a.mask_stride] & 1u));
+    const float tail_x = logit_of(xb1);
     bool tail_ok = true;
     if (masked && tail_t >= 0) tail_ok = (a.mask[(int64_t)r * a.mask_stride + (tail_t >> 5)] >> (tail_t & 31)) & 1u;
-    u64 win[NW];
-#pragma unroll
-    for (int j = 0; j < NW; ++j) {
-        const int g = tid + j * kBlock;
-        const int sl = (int)__umulhi((uint32_t)g, a.win_magic);   // g / W
-        win[j] = (sl < S) ? cand[(int64_t)sl * a.cand_cap + (g - sl * W)] : 0ull;
-    }
     if (tid == 0) {
         sa = a;
         sP = P;
@@ -2186,6 +2229,7 @@ __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
     if (tid < S) {
         st.soff[tid] = cnt_raw & 0x1FFFFFFF;
         if (cnt_raw & (1 << 30)) atomicOr(&st.flags, 4);   // a NaN logit in the slice
+        if ((cnt_raw & 0x1FFFFFFF) > W) atomicOr(&st.flags, 8);   // a list past the window
     }
     if (FAST) {
         merge_fast<NW>(a, P, r, pre, bias_t, nan_at0, tail_t, tail_x, tail_ok, win, smem, st, sa, sP);
@@ -2267,7 +2311,7 @@ __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
         const int sl = (int)__umulhi((uint32_t)g, a.win_magic);   // g / W
         if (sl >= S || g - sl * W >= st.soff[sl]) win[j] = 0ull;
     }
-    for (int sl = 0; sl < S; ++sl) extra += max(0, st.soff[sl] - W);
+    extra = (st.flags & 8) ? 1 : 0;   // some slice's list runs past the window
     if (greedy) {
 #pragma unroll
         for (int j = 0; j < NW; ++j) best = win[j] > best ? win[j] : best;
@@ -2989,9 +3033,18 @@ hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, bool pen, boo
 }
 
 hipError_t launch_merge(const StreamArgs& a, hipStream_t stream) {
-    if (a.fast) hipLaunchKernelGGL((k_merge<false, true>), dim3(a.rows), dim3(kBlock), a.merge_lds, stream, a);
-    else if (a.gtab != nullptr) hipLaunchKernelGGL((k_merge<true, false>), dim3(a.rows), dim3(kBlock), a.merge_lds, stream, a);
-    else hipLaunchKernelGGL((k_merge<false, false>), dim3(a.rows), dim3(kBlock), a.merge_lds, stream, a);
+    // kXcds times the most rows whose first slice one XCD streamed (k_merge
+    // takes each row on that XCD)
+    int most = 0;
+    for (int x = 0; x < kXcds; ++x) {
+        const int r0 = std::min(a.rows, (x * a.blocks_per_xcd + a.nslices - 1) / a.nslices);
+        const int r1 = std::min(a.rows, ((x + 1) * a.blocks_per_xcd + a.nslices - 1) / a.nslices);
+        most = std::max(most, r1 - r0);
+    }
+    const dim3 g(kXcds * most);
+    if (a.fast) hipLaunchKernelGGL((k_merge<false, true>), g, dim3(kBlock), a.merge_lds, stream, a);
+    else if (a.gtab != nullptr) hipLaunchKernelGGL((k_merge<true, false>), g, dim3(kBlock), a.merge_lds, stream, a);
+    else hipLaunchKernelGGL((k_merge<false, false>), g, dim3(kBlock), a.merge_lds, stream, a);
     return hipGetLastError();
 }
 

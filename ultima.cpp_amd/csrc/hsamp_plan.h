@@ -119,7 +119,7 @@ struct StreamArgs {
 
 constexpr int kBlock = 256;        // threads per block (4 wave64)
 constexpr int kLimitK = 1024;      // largest top_k the top-k path takes
-constexpr int kFlagCap = 2560;     // k_merge flag mode: penalised candidates per row (>= 8 * 256 + 256 + 8)
+constexpr int kCntCap = 8 * kBlock;  // k_merge flag mode: distinct history ids (the longest fast-path window)
 constexpr int kXcds = 8;           // MI355X: workgroups round-robin over 8 XCDs
 
 }  // namespace hsamp

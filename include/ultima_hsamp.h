@@ -64,6 +64,8 @@ extern "C" {
 #define ULTIMA_HSAMP_ROW_NAN 8u           /* a NaN logit was seen (outside the contract) */
 #define ULTIMA_HSAMP_ROW_UNIFORM 16u      /* nothing finite was left: uniform draw over V */
 #define ULTIMA_HSAMP_ROW_TOPP_NEAR 32u    /* top-p cumulative within 1e-6 of top_p at the cutoff */
+#define ULTIMA_HSAMP_ROW_REREAD 64u       /* diagnostics: penalties pushed the top-k below the first
+                                             pass's bounds and the row was read again in full */
 
 /* Hard limits of this build. */
 #define ULTIMA_HSAMP_MAX_VOCAB (1 << 24)      /* token ids and V below 2^24 */

@@ -27,10 +27,12 @@ def test_config_rows_match_oracle(sampler, wl, cfg, rows):
     assert compare_rows(w, g) == rows
 
 
-def test_config2_full_batch(sampler, wl):
+def test_config2_full_batch(sampler, hs, wl):
     w = wl.config(2, seed=1)
     g = run_gpu(sampler, w)
     assert compare_rows(w, g) == 64
+    # penalties on random histories never push the top-k below the stream's bounds
+    assert not np.any(g["row_flags"] & hs.ROW_REREAD)
 
 
 def test_config4_full_batch(sampler, wl):
@@ -254,6 +256,44 @@ def test_run_rejects_invalid_requests(sampler, hs, wl):
             (2, 40000), dtype=torch.int32, device=x.device), hist_len=[40000, 40000])
     assert e.value.status == hs.ERR_CAPACITY
     torch.cuda.synchronize()
+
+
+def test_penalties_below_the_stream_bounds(sampler, hs, wl):
+    """Sampling rows whose histories hold their 1500 highest logits under heavy
+    penalties: the true top-k lies far below every slice's survival bound on
+    pre-penalty keys, so the merge's bound check fails and it reads each row
+    again in full."""
+    rng = np.random.default_rng(99)
+    B, V, H = 4, 40000, 2048
+    x = rng.normal(size=(B, V)).astype(np.float32)
+    hist = np.empty((B, H), np.int32)
+    for r in range(B):
+        top = np.argsort(-x[r])[:1500]
+        hist[r] = rng.permutation(np.concatenate([top, rng.choice(top, H - 1500)]))
+    plist = [wl.identity_params(temperature=0.9, top_k=40, top_p=0.9, rep_penalty=50.0, repeat_last_n=2048,
+                                frequency_penalty=2.0, presence_penalty=1.0) for _ in range(B)]
+    w = _wl_from(wl, x, plist, rng.random(B))
+    w.hist, w.hist_len = hist, np.full(B, H, np.int64)
+    g = run_gpu(sampler, w)
+    assert compare_rows(w, g) == B
+    assert np.all(g["row_flags"] & hs.ROW_REREAD)
+
+
+def test_greedy_flagged_past_the_window(sampler, wl):
+    """Greedy rows whose 2048 penalised ids hold the largest logits of the
+    first slice: that slice hands over more flagged ids than the merge's
+    window, and the ones past it still take part in the argmax."""
+    rng = np.random.default_rng(7)
+    B, V, H = 4, 40000, 2048
+    x = rng.normal(size=(B, V)).astype(np.float32)
+    x[:, :H] += 8.0
+    hist = np.stack([rng.permutation(H) for _ in range(B)]).astype(np.int32)
+    plist = [wl.identity_params(temperature=0.0, rep_penalty=1.5, repeat_last_n=2048,
+                                frequency_penalty=0.3 * (r + 1), presence_penalty=0.5) for r in range(B)]
+    w = _wl_from(wl, x, plist, rng.random(B))
+    w.hist, w.hist_len = hist, np.full(B, H, np.int64)
+    g = run_gpu(sampler, w)
+    assert compare_rows(w, g) == B
 
 
 @pytest.mark.parametrize("greedy_rows", [0, 6, 12])

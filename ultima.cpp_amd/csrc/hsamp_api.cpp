@@ -24,8 +24,8 @@
 #include "ultima_hsamp.h"
 
 namespace hsamp {
-hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, bool greedy_rows,
-                         bool sample_rows, int grid, hipStream_t stream);
+hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, bool pen_greedy, bool pen_sample, bool mask,
+                         bool greedy_rows, bool sample_rows, int grid, hipStream_t stream);
 hipError_t launch_writeback(const StreamArgs& a, int grid, uint32_t lds, hipStream_t stream);
 hipError_t launch_merge(const StreamArgs& a, hipStream_t stream);
 hipError_t launch_full(const StreamArgs& a, uint32_t lds, hipStream_t stream);
@@ -74,7 +74,8 @@ struct ultima_hsamp {
     // scratch sized for the worst case at creation
     unsigned long long* cand = nullptr;
     size_t cand_elems = 0;
-    int32_t* cand_n = nullptr;
+    int32_t* cand_n = nullptr;    // [slots] counts, then [slots] bounds
+    size_t cand_slots = 0;
     uint32_t* gtab = nullptr;            // per-row penalty tables too large for LDS
     size_t gtab_words = 0;
     int32_t* fin_idx = nullptr;
@@ -455,7 +456,8 @@ int ultima_hsamp_create(int device, int32_t max_rows, int32_t max_vocab, ultima_
     for (auto& s : h->slots) CREATE_TRY(hipEventCreateWithFlags(&s.ev, hipEventDisableTiming));
     // Per-slice counts: rows * slices <= max(kTargetBlocks, max_rows) blocks.
     const size_t blocks = std::max<size_t>(kTargetBlocks + 8, (size_t)max_rows);
-    CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->cand_n), blocks * 4));
+    CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->cand_n), blocks * 8));
+    h->cand_slots = blocks;
     CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->fin_idx), (size_t)max_rows * kLimitK * 4));
     CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->fin_n), (size_t)max_rows * 4));
     CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->d_row), (size_t)max_vocab * 4 + 64));
@@ -533,12 +535,12 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     // (flag mode: [bins][list][ids, counts / composites of penalised candidates][buffer])
     const bool fast0 = kmax <= 64 && !gtab && bl.max_scan <= 8 * kBlock && bl.max_bias <= kBlock;
     const bool pen_flag = fast0 && bl.any_pen && bl.pen_lowers;
-    // flag mode: after the list, counters of the history's ids, a bitmap over
+    // flag mode: after the list, counters of the penalised ids, a bitmap over
     // the vocabulary (16 B per 128 ids) and its rank prefixes (2 B per 128
-    // ids), which the buffer replaces once the values are found; one merge
+    // ids), then the buffer of a row read again in full (rare); one merge
     // block per row, so it may use the whole LDS of a CU
     const size_t ngroups = ((size_t)V + 127) / 128;
-    const size_t fast_lds = pen_flag ? 9216 + std::max(8 * (size_t)kCntCap + align16(18 * ngroups), 8 * (size_t)buf_cap)
+    const size_t fast_lds = pen_flag ? 9216 + 8 * (size_t)kCntCap + align16(18 * ngroups) + 8 * (size_t)buf_cap
                                      : 9216 + std::max(12 * (size_t)mhash, 8 * (size_t)buf_cap);
     const bool fast = fast0 && fast_lds <= (pen_flag ? h->lds_limit - statik : lds_budget);
     if (fast) merge_lds = std::max(merge_lds, fast_lds);
@@ -619,6 +621,7 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     a.ovf_cap = kMergeRound;
     a.cand = h->cand;
     a.cand_n = h->cand_n;
+    a.cand_th = h->cand_n + h->cand_slots;
     a.win = win;
     a.win_magic = (uint32_t)((1ull << 32) / (uint64_t)win + 1);
     a.dtype = b->dtype;
@@ -638,8 +641,14 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     const bool vec = (reinterpret_cast<uintptr_t>(b->logits) % 16 == 0) &&
                      ((b->logits_stride * es) % 16 == 0) && V >= 16 / es;
     a.vec_tail = vec ? V % (16 / es) : 0;
+    a.uniform = (bl.any_greedy && !bl.any_sample && !bl.any_full ? 1 : 0) |
+                (bl.any_sample && !bl.any_greedy && !bl.any_full ? 2 : 0);
+    // In flag mode the sampling rows' stream needs no penalties at all: it
+    // bounds on pre-penalty keys, which penalties can only lower, and k_merge
+    // finds the penalised candidates' true values (checking the bounds).
     if (bl.any_topk)
-        HIP_TRY(launch_stream(a, b->dtype, vec, bl.any_pen, bl.any_mask, bl.any_greedy, bl.any_sample, grid, stream));
+        HIP_TRY(launch_stream(a, b->dtype, vec, bl.any_pen, bl.any_pen && !a.pen_flag, bl.any_mask, bl.any_greedy,
+                              bl.any_sample, grid, stream));
     if (h->phase_ev != nullptr) HIP_TRY(hipEventRecord(h->phase_ev, stream));
     if (bl.any_topk) HIP_TRY(launch_merge(a, stream));
     if (bl.any_full) HIP_TRY(launch_full(a, (uint32_t)full_lds, stream));

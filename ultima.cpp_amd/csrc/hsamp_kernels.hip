@@ -78,6 +78,7 @@ struct Shared {
     int soff[257];      // slice offsets during the merge
     int flags;
     int nan0;
+    uint32_t thmax;     // largest survival bound of the row's sampling slices
     alignas(16) u64 wv[64];  // the finishing wave's cross-lane scratch
     double u;           // the row's uniform
     uint64_t expT[32];  // expf's table (libm_expf.h), copied to LDS
@@ -1210,6 +1211,11 @@ __device__ __forceinline__ float load_logit(const char* rowp, int t) {
     return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(rowp)[t] << 16);
 }
 
+// One logit of a row, by id, the element type chosen at run time.
+__device__ __forceinline__ float load_logit_dt(const char* rowp, int dtype, int t) {
+    return dtype == 0 ? load_logit<0>(rowp, t) : load_logit<1>(rowp, t);
+}
+
 // N logits by id (t < 0: none, 0.0f), the element type chosen once for the
 // batch so that all N loads are in flight together.
 template <int N>
@@ -1455,7 +1461,10 @@ __device__ __forceinline__ void stream_sample(const StreamArgs& a, const RowPlan
     }
     if (nanseen) atomicOr(&st.flags, 1);
     __syncthreads();
-    if (tid == 0) a.cand_n[slot] = st.n | ((st.flags & 1) ? (1 << 30) : 0);
+    if (tid == 0) {
+        a.cand_n[slot] = st.n | ((st.flags & 1) ? (1 << 30) : 0);
+        a.cand_th[slot] = (int32_t)(uint32_t)(st.theta >> 32);   // every id left out has a key below it
+    }
 }
 
 // One block per (row, slice): stream the slice once and leave for k_merge the
@@ -1477,17 +1486,26 @@ __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
     const int logical = (int)(blockIdx.x % kXcds) * a.blocks_per_xcd + (int)(blockIdx.x / kXcds);
     const int r = logical / a.nslices, s = logical % a.nslices;
     if (r >= a.rows) return;
-    const RowPlan P = a.plans[r];
-    if (P.flags & RF_FULL) return;   // k_full's row
     const int lo = s * a.slice_len;
     const int hi = min(a.vocab - (VEC ? a.vec_tail : 0), lo + a.slice_len);   // k_merge takes the ragged end
-    if (((P.flags & RF_GREEDY) != 0) != GR) return;   // the other kernel's row
+    const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * T::ES;
+    const __amdgpu_buffer_rsrc_t rs = row_rsrc(rowp, hi, T::ES);
+    // When every row of the launch is this kernel's, the first tile goes out
+    // before the plan is read (it is processed chunk by chunk as its loads
+    // complete in order); otherwise after the plan has said the row is ours.
+    const bool early = ((a.uniform >> (GR ? 0 : 1)) & 1) != 0;
+    uint4 raw[T::NCH];
+    if (early) load_tile<DT, VEC>(rs, lo, raw);
+    const RowPlan P = a.plans[r];
+    if (!early) {
+        if (P.flags & RF_FULL) return;                     // k_full's row
+        if (((P.flags & RF_GREEDY) != 0) != GR) return;    // the other kernel's row
+    }
     const bool pen = PEN && (P.flags & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) != 0;
     const bool masked = MASK && (P.flags & RF_MASK) != 0;
-    const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * T::ES;
 
-    // The history window goes out first (it is waited for first), then the
-    // first tiles. Branch-free: clamped loads (pre[q] holds position
+    // The history window goes out next (before the first tile when that has
+    // not gone yet). Branch-free: clamped loads (pre[q] holds position
     // p0 + q * kBlock + tid, used only below L), so nothing here waits.
     int32_t pre[8];
     const int L = P.hist_len, p0 = L - P.scan_len;
@@ -1500,12 +1518,9 @@ __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
     }
     uint32_t* pbm = reinterpret_cast<uint32_t*>(smem);
     stream_setup<PEN, MASK>(a, P, r, lo, hi, GR, pen, masked, p0, L, hrow, pbm, pbm + a.bitmap_words, st);
-    // the first tile (processed chunk by chunk as its loads complete in order)
-    const __amdgpu_buffer_rsrc_t rs = row_rsrc(rowp, hi, T::ES);
-    uint4 raw[T::NCH];
-    load_tile<DT, VEC>(rs, lo, raw);
+    if (!early) load_tile<DT, VEC>(rs, lo, raw);
     if (PEN) {
-        // the history window (waits for pre[] only: the tiles were requested after)
+        // the history window (waits for pre[] only when the tile was requested after)
         if (pen) {
 #pragma unroll
             for (int q = 0; q < 8; ++q)
@@ -1638,7 +1653,8 @@ __device__ __forceinline__ u64 tail_candidate(float x, bool allowed, int32_t t, 
 //    take the buffer path.
 template <int NW>
 __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P, int r, const int32_t (&pre)[8],
-                                           int32_t bias_t, bool nan_at0, int32_t tail_t, float tail_x, bool tail_ok,
+                                           int32_t bias_t, int32_t bias_h, bool nan_at0, int32_t tail_t, float tail_x,
+                                           bool tail_ok, double ur,
                                            u64 (&win)[NW], unsigned char* smem, Shared& st, const StreamArgs& sa,
                                            const RowPlan& sP) {
     const int tid = threadIdx.x;
@@ -1690,6 +1706,7 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
             const int p = p0 + q * kBlock + tid;
             if (p >= 0 && p < L && pre[q] >= 0 && pre[q] < a.vocab) atomicOr(&vb[pre[q] >> 5], 1u << (pre[q] & 31));
         }
+        if (bias_h >= 0 && bias_h < a.vocab) atomicOr(&vb[bias_h >> 5], 1u << (bias_h & 31));   // zero counts
         __syncthreads();
         {
             const int per = (ng + kBlock - 1) / kBlock;
@@ -1875,6 +1892,30 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
     }
     extra = (st.flags & 8) ? 1 : 0;   // some slice's list runs past the window
 
+    // the true value of id t (raw logit x, allowed by the mask or not,
+    // history counters c) as a composite; 0 (absent) for a greedy row's NaN
+    auto value = [&](int32_t t, float x, bool allowed, u64 c) -> u64 {
+        uint32_t v = ((c >> 32) & 0xFFFFull ? HV_REP : 0u) | ((uint32_t)((c >> 16) & 0xFFFFull) << HV_DRY_SHIFT) |
+                     (uint32_t)(c & 0xFFFFull);
+        if (P.flags & RF_BIAS) {
+            int lo = 0, hi = P.bias_cnt;
+            const int32_t* ids = a.bias_ids + P.bias_off;
+            while (lo < hi) {
+                const int mid = (lo + hi) >> 1;
+                if (ids[mid] < t) lo = mid + 1;
+                else hi = mid;
+            }
+            if (lo < P.bias_cnt && ids[lo] == t) v |= HV_BIAS;
+        }
+        float y = allowed ? x : -__builtin_inff();
+        y = pen_value(y, t, v, sa, sP);
+        if (!greedy) y = y * P.inv_temp;
+        if (y != y) {
+            atomicOr(&st.flags, 4);
+            return greedy ? 0ull : comp(kKeyNegInf, t);
+        }
+        return comp(key32(y), t);
+    };
     if (lmode) {
         // Flag mode: the flagged window entries (key kKeyFlag) and the ragged
         // end get their true values in place (stages 1-6, sampler.cpp:235-264),
@@ -1882,39 +1923,29 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
         // windows. Their logits (and mask words) are requested first; the
         // counts are built while those loads are in flight.
         const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * (a.dtype == 0 ? 4 : 2);
+        // greedy rows: the flagged entries; sampling rows (streamed without
+        // penalties): every entry whose id is in the history or the bias list
         int32_t ft[NW];
+        if (greedy || !pen) {
 #pragma unroll
-        for (int j = 0; j < NW; ++j) ft[j] = ((uint32_t)(win[j] >> 32) == kKeyFlag) ? (int32_t)comp_idx(win[j]) : -1;
+            for (int j = 0; j < NW; ++j) ft[j] = ((uint32_t)(win[j] >> 32) == kKeyFlag) ? (int32_t)comp_idx(win[j]) : -1;
+        } else {
+            const uint32_t* vb = reinterpret_cast<const uint32_t*>(vb4);
+            uint32_t wd[NW];
+#pragma unroll
+            for (int j = 0; j < NW; ++j) wd[j] = vb[win[j] != 0ull ? (comp_idx(win[j]) >> 5) : 0];
+#pragma unroll
+            for (int j = 0; j < NW; ++j) {
+                const int32_t t = (int32_t)comp_idx(win[j]);
+                ft[j] = (win[j] != 0ull && ((wd[j] >> (t & 31)) & 1u)) ? t : -1;
+            }
+        }
         float xr[NW];
         load_logits<NW>(rowp, a.dtype, ft, xr);
         uint32_t mwf[NW];
 #pragma unroll
         for (int j = 0; j < NW; ++j)
             mwf[j] = (masked && ft[j] >= 0) ? a.mask[(int64_t)r * a.mask_stride + (ft[j] >> 5)] : 0xFFFFFFFFu;
-        // the true value of id t (raw logit x, allowed by the mask or not,
-        // history counters c) as a composite; 0 (absent) for a greedy row's NaN
-        auto value = [&](int32_t t, float x, bool allowed, u64 c) -> u64 {
-            uint32_t v = ((c >> 32) & 0xFFFFull ? HV_REP : 0u) | ((uint32_t)((c >> 16) & 0xFFFFull) << HV_DRY_SHIFT) |
-                         (uint32_t)(c & 0xFFFFull);
-            if (P.flags & RF_BIAS) {
-                int lo = 0, hi = P.bias_cnt;
-                const int32_t* ids = a.bias_ids + P.bias_off;
-                while (lo < hi) {
-                    const int mid = (lo + hi) >> 1;
-                    if (ids[mid] < t) lo = mid + 1;
-                    else hi = mid;
-                }
-                if (lo < P.bias_cnt && ids[lo] == t) v |= HV_BIAS;
-            }
-            float y = allowed ? x : -__builtin_inff();
-            y = pen_value(y, t, v, sa, sP);
-            if (!greedy) y = y * P.inv_temp;
-            if (y != y) {
-                atomicOr(&st.flags, 4);
-                return greedy ? 0ull : comp(kKeyNegInf, t);
-            }
-            return comp(key32(y), t);
-        };
         // batched: every rank first, then every counter, then the values
         u64 cj[NW];
         if (pen) {
@@ -1933,12 +1964,38 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
         }
     }
 
+    if (tid == 0) st.u = ur;
+    const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * (a.dtype == 0 ? 4 : 2);
+    // flag mode: the true value of list entry c (flagged, or any entry of a
+    // sampling row whose id is penalised), read from the row
+    auto resolve = [&](u64 c) -> u64 {
+        if (c == 0ull) return 0ull;
+        const int32_t t = (int32_t)comp_idx(c);
+        const bool flagged = (uint32_t)(c >> 32) == kKeyFlag;
+        const int rk = pen ? rank(t) : -1;
+        if (!flagged && rk < 0) return c;
+        const float x = load_logit_dt(rowp, a.dtype, t);
+        const bool allowed = !masked || ((a.mask[(int64_t)r * a.mask_stride + (t >> 5)] >> (t & 31)) & 1u);
+        return value(t, x, allowed, rk >= 0 ? cnt[rk] : 0ull);
+    };
+
     if (greedy) {
         u64 best = ct;
 #pragma unroll
         for (int q = 0; q < 9; ++q) best = cp[q] > best ? cp[q] : best;
 #pragma unroll
         for (int j = 0; j < NW; ++j) best = win[j] > best ? win[j] : best;
+        if (lmode && extra != 0) {
+            // flagged entries past a slice's window (rare)
+            const u64* cand = a.cand + (int64_t)r * S * a.cand_cap;
+            for (int s2 = 0; s2 < S; ++s2) {
+                const int n = st.soff[s2];
+                for (int e = W + tid; e < n; e += kBlock) {
+                    const u64 c = resolve(cand[(int64_t)s2 * a.cand_cap + e]);
+                    best = c > best ? c : best;
+                }
+            }
+        }
         best = block_max_u64(best, st);
         __syncthreads();
         if (tid == 0) {
@@ -2029,6 +2086,53 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
     }
     const int bstar = st.sel_d;
     const int nlist = st.sel_need;
+    if (lmode && pen) {
+        // Sampling rows streamed without penalties: every id a slice left out
+        // has a key below that slice's bound (penalties only lower keys), so
+        // the candidates hold the exact top-k when its k-th key reaches every
+        // bound (checked against the lower edge of the k-th's bin). Otherwise,
+        // or when lists ran past their windows (entries not yet resolved),
+        // the whole row is read again (rare).
+        const uint32_t th = st.thmax;
+        bool ok = th <= floor_key;
+        if (!ok && any && bstar >= 0) {
+            const uint32_t top = (shift + 11 >= 32) ? 0u : (Mk & ~((1u << (shift + 11)) - 1u));
+            ok = (top | ((uint32_t)bstar << shift)) >= th;
+        }
+        if (!ok || extra != 0) {
+            u64* rbuf = reinterpret_cast<u64*>(smem + 9216 + 8 * kCntCap + ((18 * ng + 15) & ~15));
+            u64* ovf = a.ovf + (int64_t)r * a.ovf_cap;
+            __syncthreads();
+            if (tid == 0) {
+                st.n = 0;
+                st.theta = kThetaFloor;
+            }
+            __syncthreads();
+            for (int base = 0; base < a.vocab; base += 8 * kBlock) {
+                int32_t t[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) t[q] = (base + q * kBlock + tid < a.vocab) ? base + q * kBlock + tid : -1;
+                float x[8];
+                load_logits<8>(rowp, a.dtype, t, x);
+                u64 c[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    c[q] = 0ull;
+                    if (t[q] < 0) continue;
+                    const bool allowed =
+                        !masked || ((a.mask[(int64_t)r * a.mask_stride + (t[q] >> 5)] >> (t[q] & 31)) & 1u);
+                    const int rk = rank(t[q]);
+                    c[q] = value(t[q], x[q], allowed, rk >= 0 ? cnt[rk] : 0ull);
+                }
+                offer_regs<8>(rbuf, ovf, a.buf_cap, k, c, st);
+            }
+            __syncthreads();
+            const uint32_t rflags = ((st.flags & 4) ? ROWF_NAN : 0u) | ROWF_REREAD;
+            FinLds f{};
+            select_and_finalize(sa, sP, r, rbuf, f, st, rflags);
+            return;
+        }
+    }
     if (nlist < 128 && extra == 0) {
         // entries at or above the k-th's bin, then an exact rank by wave 0
         uint32_t inm = 0u;   // which of this thread's NC candidates go to the list
@@ -2160,8 +2264,11 @@ __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
             for (int q = 0; q < 8; ++q) pre[q] = h[max(0, min(p0 + q * kBlock + tid, L - 1))];
         }
     }
+    // (flag mode: the bias ids count as penalised; read with the history)
+    const int32_t bias_h = (hist_first && (P.flags & RF_BIAS) && tid < P.bias_cnt) ? a.bias_ids[P.bias_off + tid] : -1;
     const u64* cand = a.cand + (int64_t)r * S * a.cand_cap;
     const int cnt_raw = (tid < S) ? a.cand_n[(int64_t)r * S + tid] : 0;
+    const uint32_t th_raw = (hist_first && tid < S) ? (uint32_t)a.cand_th[(int64_t)r * S + tid] : 0u;
     // one buffer resource over the row's lists: branch-free loads, entries
     // past the last slice read as 0
     u64 win[NW];
@@ -2210,6 +2317,7 @@ __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
         st.nan0 = 0;
         st.n = 0;
         st.theta = kThetaFloor;
+        st.thmax = 0u;
     }
     if (!hist_first) hist_prefetch(a, P, r, pen, pre);
     const int32_t bias_t = (FAST && (P.flags & RF_BIAS) && tid < P.bias_cnt) ? a.bias_ids[P.bias_off + tid] : -1;
@@ -2219,22 +2327,32 @@ __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
     const float tail_x = logit_of(xb1);
     bool tail_ok = true;
     if (masked && tail_t >= 0) tail_ok = (a.mask[(int64_t)r * a.mask_stride + (tail_t >> 5)] >> (tail_t & 31)) & 1u;
+    // u goes to LDS once the loads issued before it are needed anyway
+    const double ur = a.u[r];
     if (tid == 0) {
         sa = a;
         sP = P;
-        st.u = a.u[r];
     }
-    if (tid < 32) st.expT[tid] = kExpT[tid];
+    if (tid < 32) {
+        // expf's table from immediates (an indexed read would wait for every
+        // load issued so far)
+        uint64_t e = 0ull;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) e = (tid == i) ? kExpT[i] : e;
+        st.expT[tid] = e;
+    }
     __syncthreads();
     if (tid < S) {
         st.soff[tid] = cnt_raw & 0x1FFFFFFF;
         if (cnt_raw & (1 << 30)) atomicOr(&st.flags, 4);   // a NaN logit in the slice
         if ((cnt_raw & 0x1FFFFFFF) > W) atomicOr(&st.flags, 8);   // a list past the window
+        if (hist_first) atomicMax(&st.thmax, th_raw);
     }
     if (FAST) {
-        merge_fast<NW>(a, P, r, pre, bias_t, nan_at0, tail_t, tail_x, tail_ok, win, smem, st, sa, sP);
+        merge_fast<NW>(a, P, r, pre, bias_t, bias_h, nan_at0, tail_t, tail_x, tail_ok, ur, win, smem, st, sa, sP);
         return;
     }
+    if (tid == 0) st.u = ur;
     // LDS: [row penalty table | finalize scratch] aliased, then the buffer.
     const PenaltyLds pl = pen_table<GT>(a, r, smem);
     if (pen) pen_build_row(a, P, r, pl, pre);   // its barriers publish the counts too
@@ -3025,10 +3143,10 @@ static void launch_stream_kind(const StreamArgs& a, int dtype, bool vec, bool pe
 #undef HSAMP_STREAM
 }
 
-hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, bool greedy_rows,
-                         bool sample_rows, int grid, hipStream_t stream) {
-    if (greedy_rows) launch_stream_kind<true>(a, dtype, vec, pen, mask, grid, stream);
-    if (sample_rows) launch_stream_kind<false>(a, dtype, vec, pen, mask, grid, stream);
+hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, bool pen_greedy, bool pen_sample, bool mask,
+                         bool greedy_rows, bool sample_rows, int grid, hipStream_t stream) {
+    if (greedy_rows) launch_stream_kind<true>(a, dtype, vec, pen_greedy, mask, grid, stream);
+    if (sample_rows) launch_stream_kind<false>(a, dtype, vec, pen_sample, mask, grid, stream);
     return hipGetLastError();
 }
 

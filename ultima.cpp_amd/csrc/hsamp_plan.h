@@ -14,6 +14,7 @@ constexpr uint32_t ROWF_CDF_NEAR = ULTIMA_HSAMP_ROW_CDF_NEAR;
 constexpr uint32_t ROWF_NAN = ULTIMA_HSAMP_ROW_NAN;
 constexpr uint32_t ROWF_UNIFORM = ULTIMA_HSAMP_ROW_UNIFORM;
 constexpr uint32_t ROWF_TOPP_NEAR = ULTIMA_HSAMP_ROW_TOPP_NEAR;
+constexpr uint32_t ROWF_REREAD = ULTIMA_HSAMP_ROW_REREAD;
 
 // RowPlan::flags -- which stages run for the row. Each follows the reference's
 // own predicate (src/sampler/sampler.cpp line in brackets), evaluated on the host.
@@ -97,6 +98,7 @@ struct StreamArgs {
     int32_t fin_cap;            // entries per row in fin_idx
     unsigned long long* cand;   // [rows * S * cand_cap]
     int32_t* cand_n;            // [rows * S]
+    int32_t* cand_th;           // [rows * S] a sampling slice's final survival bound (key)
     int32_t* fin_idx;           // [rows * fin_cap] final kept ids (for writeback)
     int32_t* fin_n;             // [rows]
     unsigned long long* ovf;    // [blocks * ovf_cap] per-block overflow of the LDS buffer
@@ -108,6 +110,7 @@ struct StreamArgs {
     int32_t pen_flag;           // penalties only lower logits: k_stream hands penalised ids over as
                                 // flagged candidates (pre-penalty key) instead of leaving them out
     int32_t vec_tail;           // the row's last ids k_merge reads itself (V % chunk with vector loads)
+    int32_t uniform;            // bit 0: every row is greedy, bit 1: every row is top-k sampling
     float* fullv;               // [rows * vocab] k_full: transformed logits (-inf once removed)
     float* fullp;               // [rows * vocab] k_full: probabilities
     uint32_t* fullk;            // [rows * 2 * full_p2] k_full: probability keys by bucket, sort scratch
@@ -119,7 +122,7 @@ struct StreamArgs {
 
 constexpr int kBlock = 256;        // threads per block (4 wave64)
 constexpr int kLimitK = 1024;      // largest top_k the top-k path takes
-constexpr int kCntCap = 8 * kBlock;  // k_merge flag mode: distinct history ids (the longest fast-path window)
+constexpr int kCntCap = 9 * kBlock;  // k_merge flag mode: distinct penalised ids (fast-path window + bias list)
 constexpr int kXcds = 8;           // MI355X: workgroups round-robin over 8 XCDs
 
 }  // namespace hsamp

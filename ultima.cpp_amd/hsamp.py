@@ -18,7 +18,7 @@ HEADER = PKG.parent / "include" / "ultima_hsamp.h"
 OK, ERR_INVALID, ERR_HIP, ERR_UNSUPPORTED, ERR_NOMEM, ERR_CAPACITY, ERR_NO_DEVICE = 0, -1, -2, -3, -4, -5, -6
 F32, BF16 = 0, 1
 WRITEBACK = 1
-ROW_GREEDY, ROW_U_USED, ROW_CDF_NEAR, ROW_NAN, ROW_UNIFORM, ROW_TOPP_NEAR = 1, 2, 4, 8, 16, 32
+ROW_GREEDY, ROW_U_USED, ROW_CDF_NEAR, ROW_NAN, ROW_UNIFORM, ROW_TOPP_NEAR, ROW_REREAD = 1, 2, 4, 8, 16, 32, 64
 
 PARAM_KEYS = ("rep_penalty", "dry_multiplier", "dry_base", "frequency_penalty", "presence_penalty",
               "temperature", "top_p", "min_p", "repeat_last_n", "dry_allowed_len", "dry_last_n",

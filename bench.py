@@ -8,9 +8,10 @@ than the 256 MB Infinity Cache) rotate so the kernel streams from HBM.
 
 The launches of one rotation are captured into a HIP graph (torch.cuda.CUDAGraph)
 and replayed; HIP events on the launch stream bracket the K timed steps. A
-second, uncaptured pass times the two kernels of each launch apart (events
-around each launch plus one the library records between them); the roofline
-figure is the stream kernel's algorithmic bytes over its own duration.
+second graph of the same launches with only the pass over the logits (the
+library's STREAM_ONLY diagnostics flag), timed the same way, gives the stream
+kernel's own duration (the merge takes the rest of the step); the roofline
+figure is the stream kernel's algorithmic bytes over that duration.
 Prints one JSON line (see `main`). The CPU baseline is the reference's own
 sampler (oracle/_ref, compiled from its sources) or, where that was not
 built, the CPU restatement, timed on this host's cores on a bounded sample.
@@ -154,26 +155,36 @@ def main():
     ms_total = t0e.elapsed_time(t1e)
     ms_step = ms_total / steps
 
-    # Per-kernel split, live: the same launches uncaptured, each bracketed by
-    # events on the launch stream, with the library recording a third event
-    # between the stream pass (k_stream, reads the logits) and the per-row
-    # merge (k_merge).
-    n_split = max(N_SETS, min(steps, 25 * N_SETS))
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(n_split)]
-    with torch.cuda.stream(stream):
-        for e in ev:
-            e[1].record(stream)           # creates the event the library records
+    # Per-kernel split, live: a second graph holds the same launches with only
+    # the pass over the logits (k_stream; the library's STREAM_ONLY
+    # diagnostics flag), replayed between events like the full step; the
+    # merge (k_merge) takes the rest of the step.
+    def launch_stream_only(i, s):
+        x, u, h, m = to_dev[i]
+        sampler.run(x, sets[i].params, u, hist=h, hist_len=sets[i].hist_len, mask=m,
+                    outputs=outs[i], stream=s, stream_only=True)
+
+    sgraph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(sgraph, stream=stream):
+        for i in range(N_SETS):
+            launch_stream_only(i, stream)
     stream.synchronize()
     with torch.cuda.stream(stream):
-        for i in range(n_split):
-            ev[i][0].record(stream)
-            sampler.set_phase_event(ev[i][1])
-            launch(i % N_SETS, stream)
-            ev[i][2].record(stream)
+        for _ in range(reps_w):
+            sgraph.replay()
     stream.synchronize()
-    sampler.set_phase_event(None)
-    stream_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / n_split
-    merge_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / n_split
+    s0e = torch.cuda.Event(enable_timing=True)
+    s1e = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        s0e.record(stream)
+        for _ in range(reps):
+            sgraph.replay()
+        s1e.record(stream)
+    stream.synchronize()
+    n_split = reps * N_SETS
+    stream_ms = s0e.elapsed_time(s1e) / n_split
+    merge_ms = ms_step - stream_ms
+    del sgraph
 
     # The replayed outputs are the real ones: spot-check them against an
     # uncaptured launch of the same inputs.

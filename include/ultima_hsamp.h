@@ -56,6 +56,9 @@ extern "C" {
 
 /* ultima_hsamp_batch.flags */
 #define ULTIMA_HSAMP_WRITEBACK 1u /* leave logits in the state sample() leaves them (F32 only) */
+#define ULTIMA_HSAMP_STREAM_ONLY 0x100u /* diagnostics, no counterpart in the reference: run only the
+                                           pass over the logits (no token is written), so that a
+                                           caller can time that kernel apart */
 
 /* Per-row outcome bits written to row_flags (when given). */
 #define ULTIMA_HSAMP_ROW_GREEDY 1u        /* temperature <= 0: argmax, u unused */
@@ -99,7 +102,7 @@ typedef struct ultima_hsamp_batch {
     int32_t rows;               /* B >= 1 */
     int32_t vocab;              /* V >= 1 */
     int32_t dtype;              /* ULTIMA_HSAMP_F32 or ULTIMA_HSAMP_BF16 */
-    uint32_t flags;             /* ULTIMA_HSAMP_WRITEBACK */
+    uint32_t flags;             /* ULTIMA_HSAMP_WRITEBACK, ULTIMA_HSAMP_STREAM_ONLY */
     void* logits;               /* device [rows, logits_stride] elements of dtype */
     int64_t logits_stride;      /* elements between rows, >= vocab */
     const int32_t* hist;        /* device [rows, hist_stride] ids, oldest first; NULL if unused */

@@ -344,7 +344,7 @@ int validate_batch(const ultima_hsamp* h, const ultima_hsamp_batch* b) {
     if (b->logits_stride < b->vocab) return ULTIMA_HSAMP_ERR_INVALID;
     if (b->hist != nullptr && b->hist_stride < 0) return ULTIMA_HSAMP_ERR_INVALID;
     if (b->mask != nullptr && b->mask_stride < (b->vocab + 31) / 32) return ULTIMA_HSAMP_ERR_INVALID;
-    if ((b->flags & ~ULTIMA_HSAMP_WRITEBACK) != 0) return ULTIMA_HSAMP_ERR_INVALID;
+    if ((b->flags & ~(ULTIMA_HSAMP_WRITEBACK | ULTIMA_HSAMP_STREAM_ONLY)) != 0) return ULTIMA_HSAMP_ERR_INVALID;
     if ((b->flags & ULTIMA_HSAMP_WRITEBACK) && b->dtype != ULTIMA_HSAMP_F32)
         return ULTIMA_HSAMP_ERR_UNSUPPORTED;
     const bool sets = b->topk_idx || b->kept_idx || b->kept_prob;
@@ -650,9 +650,11 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
         HIP_TRY(launch_stream(a, b->dtype, vec, bl.any_pen, bl.any_pen && !a.pen_flag, bl.any_mask, bl.any_greedy,
                               bl.any_sample, grid, stream));
     if (h->phase_ev != nullptr) HIP_TRY(hipEventRecord(h->phase_ev, stream));
-    if (bl.any_topk) HIP_TRY(launch_merge(a, stream));
-    if (bl.any_full) HIP_TRY(launch_full(a, (uint32_t)full_lds, stream));
-    if (wb) HIP_TRY(launch_writeback(a, grid, (uint32_t)wb_lds, stream));
+    if (!(b->flags & ULTIMA_HSAMP_STREAM_ONLY)) {
+        if (bl.any_topk) HIP_TRY(launch_merge(a, stream));
+        if (bl.any_full) HIP_TRY(launch_full(a, (uint32_t)full_lds, stream));
+        if (wb) HIP_TRY(launch_writeback(a, grid, (uint32_t)wb_lds, stream));
+    }
     if (!capturing) HIP_TRY(hipEventRecord(slot->ev, stream));
     return ULTIMA_HSAMP_OK;
 }

@@ -17,7 +17,7 @@ HEADER = PKG.parent / "include" / "ultima_hsamp.h"
 
 OK, ERR_INVALID, ERR_HIP, ERR_UNSUPPORTED, ERR_NOMEM, ERR_CAPACITY, ERR_NO_DEVICE = 0, -1, -2, -3, -4, -5, -6
 F32, BF16 = 0, 1
-WRITEBACK = 1
+WRITEBACK, STREAM_ONLY = 1, 0x100
 ROW_GREEDY, ROW_U_USED, ROW_CDF_NEAR, ROW_NAN, ROW_UNIFORM, ROW_TOPP_NEAR, ROW_REREAD = 1, 2, 4, 8, 16, 32, 64
 
 PARAM_KEYS = ("rep_penalty", "dry_multiplier", "dry_base", "frequency_penalty", "presence_penalty",
@@ -176,11 +176,12 @@ class Sampler:
             pass
 
     def run(self, logits, params, u, hist=None, hist_len=None, mask=None, bias=None,
-            writeback=False, want_sets=False, set_cap=None, stream=None, outputs=None):
+            writeback=False, want_sets=False, set_cap=None, stream=None, outputs=None, stream_only=False):
         """Sample every row. logits: cuda tensor [B, >=V] float32 or bfloat16
         (row stride = logits.stride(0)); u: cuda float64 [B]; hist: cuda int32
         [B, H]; mask: cuda int32/uint32 [B, W]. Returns a dict of cuda tensors.
-        `outputs` may carry preallocated tensors (token, row_flags, ...)."""
+        `outputs` may carry preallocated tensors (token, row_flags, ...).
+        stream_only (diagnostics): run only the pass over the logits."""
         import torch
         B, V = logits.shape[0], logits.shape[1]
         dev = logits.device
@@ -203,7 +204,7 @@ class Sampler:
         b = Batch()
         b.rows, b.vocab = B, V
         b.dtype = F32 if logits.dtype == torch.float32 else BF16
-        b.flags = WRITEBACK if writeback else 0
+        b.flags = (WRITEBACK if writeback else 0) | (STREAM_ONLY if stream_only else 0)
         b.logits = logits.data_ptr()
         b.logits_stride = logits.stride(0)
         if hist is not None:

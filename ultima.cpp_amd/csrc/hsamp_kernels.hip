@@ -1406,8 +1406,10 @@ __device__ __forceinline__ void stream_sample(const StreamArgs& a, const RowPlan
     const int k = P.top_k;
     const int kw = (k + 3) >> 2;
     const int G = min(4, max(1, (kw + 63) >> 6));
-    const float inv_t = P.inv_temp;
+    // flag mode: keys of the raw logits (x * 1.0f is x); k_merge applies the
+    // penalties and the temperature to the candidates
     const bool pflag = a.pen_flag != 0;
+    const float inv_t = pflag ? 1.0f : P.inv_temp;
     bool nanseen = false;
     auto process = [&](const uint4 (&raw)[T::NCH], int tb) {
         uint32_t kv[T::NE];
@@ -1651,7 +1653,7 @@ __device__ __forceinline__ u64 tail_candidate(float x, bool allowed, int32_t t, 
 //    holding the k-th; entries at or above it (< 128) are ranked exactly by
 //    wave 0. More entries (massive ties) or list entries beyond the windows
 //    take the buffer path.
-template <int NW>
+template <int NW, bool LM>
 __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P, int r, const int32_t (&pre)[8],
                                            int32_t bias_t, int32_t bias_h, bool nan_at0, int32_t tail_t, float tail_x,
                                            bool tail_ok, double ur,
@@ -1676,7 +1678,7 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
     // LDS there: [bins][list][counters: 64 bits per distinct history id]
     // [vocabulary bitmap: 16 B per 128 ids][rank prefixes: 2 B per 128 ids],
     // all after the list replaced by the buffer once the values are found
-    const bool lmode = a.pen_flag != 0;
+    constexpr bool lmode = LM;   // flag mode (a launch-level choice: its own instantiation)
     u64* cnt = reinterpret_cast<u64*>(smem + 9216);
     uint4* vb4 = reinterpret_cast<uint4*>(smem + 9216 + 8 * kCntCap);
     if (pen && !lmode) {
@@ -1916,37 +1918,67 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
         }
         return comp(key32(y), t);
     };
-    if (lmode) {
-        // Flag mode: the flagged window entries (key kKeyFlag) and the ragged
-        // end get their true values in place (stages 1-6, sampler.cpp:235-264),
-        // from the row's raw logits and their ids' counts in the history
-        // windows. Their logits (and mask words) are requested first; the
-        // counts are built while those loads are in flight.
-        const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * (a.dtype == 0 ? 4 : 2);
-        // greedy rows: the flagged entries; sampling rows (streamed without
-        // penalties): every entry whose id is in the history or the bias list
-        int32_t ft[NW];
-        if (greedy || !pen) {
+    if (lmode && !greedy) {
+        // Flag mode, sampling rows: the stream handed over raw keys (key32 of
+        // the masked logit, NaN as -inf), so each candidate's logit is its
+        // key's float, exactly. Penalised ids (in the history or the bias
+        // list: rank >= 0) take stages 1-6 (sampler.cpp:235-264) with their
+        // counters, then every candidate takes the temperature (sampler.cpp:
+        // 101-106). Batched: every rank, then every counter, then the values.
+        int rk[NW];
+        u64 cj[NW];
+        if (pen) {
 #pragma unroll
-            for (int j = 0; j < NW; ++j) ft[j] = ((uint32_t)(win[j] >> 32) == kKeyFlag) ? (int32_t)comp_idx(win[j]) : -1;
-        } else {
-            const uint32_t* vb = reinterpret_cast<const uint32_t*>(vb4);
-            uint32_t wd[NW];
+            for (int j = 0; j < NW; ++j) rk[j] = win[j] != 0ull ? rank((int)comp_idx(win[j])) : -1;
 #pragma unroll
-            for (int j = 0; j < NW; ++j) wd[j] = vb[win[j] != 0ull ? (comp_idx(win[j]) >> 5) : 0];
-#pragma unroll
-            for (int j = 0; j < NW; ++j) {
-                const int32_t t = (int32_t)comp_idx(win[j]);
-                ft[j] = (win[j] != 0ull && ((wd[j] >> (t & 31)) & 1u)) ? t : -1;
-            }
+            for (int j = 0; j < NW; ++j) cj[j] = rk[j] >= 0 ? cnt[rk[j]] : 0ull;
         }
+#pragma unroll
+        for (int j = 0; j < NW; ++j) {
+            if (win[j] == 0ull) continue;
+            const int32_t t = (int32_t)comp_idx(win[j]);
+            float y = key_to_float((uint32_t)(win[j] >> 32));
+            if (pen && rk[j] >= 0) {
+                const u64 c = cj[j];
+                uint32_t v = ((c >> 32) & 0xFFFFull ? HV_REP : 0u) |
+                             ((uint32_t)((c >> 16) & 0xFFFFull) << HV_DRY_SHIFT) | (uint32_t)(c & 0xFFFFull);
+                if (P.flags & RF_BIAS) {
+                    int lo = 0, hi = P.bias_cnt;
+                    const int32_t* ids = a.bias_ids + P.bias_off;
+                    while (lo < hi) {
+                        const int mid = (lo + hi) >> 1;
+                        if (ids[mid] < t) lo = mid + 1;
+                        else hi = mid;
+                    }
+                    if (lo < P.bias_cnt && ids[lo] == t) v |= HV_BIAS;
+                }
+                y = pen_value(y, t, v, sa, sP);
+            }
+            y = y * P.inv_temp;
+            if (y != y) {
+                atomicOr(&st.flags, 4);
+                y = -__builtin_inff();
+            }
+            win[j] = comp(key32(y), t);
+        }
+        if (tail_t >= 0) {
+            const int rk0 = pen ? rank(tail_t) : -1;
+            ct = value(tail_t, tail_x, tail_ok, rk0 >= 0 ? cnt[rk0] : 0ull);
+        }
+    } else if (lmode) {
+        // Flag mode, greedy rows: the flagged entries (key kKeyFlag) and the
+        // ragged end get their true values in place, from the row's raw
+        // logits and their ids' counters.
+        const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * (a.dtype == 0 ? 4 : 2);
+        int32_t ft[NW];
+#pragma unroll
+        for (int j = 0; j < NW; ++j) ft[j] = ((uint32_t)(win[j] >> 32) == kKeyFlag) ? (int32_t)comp_idx(win[j]) : -1;
         float xr[NW];
         load_logits<NW>(rowp, a.dtype, ft, xr);
         uint32_t mwf[NW];
 #pragma unroll
         for (int j = 0; j < NW; ++j)
             mwf[j] = (masked && ft[j] >= 0) ? a.mask[(int64_t)r * a.mask_stride + (ft[j] >> 5)] : 0xFFFFFFFFu;
-        // batched: every rank first, then every counter, then the values
         u64 cj[NW];
         if (pen) {
             int rk[NW];
@@ -2086,18 +2118,21 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
     }
     const int bstar = st.sel_d;
     const int nlist = st.sel_need;
-    if (lmode && pen) {
-        // Sampling rows streamed without penalties: every id a slice left out
-        // has a key below that slice's bound (penalties only lower keys), so
-        // the candidates hold the exact top-k when its k-th key reaches every
-        // bound (checked against the lower edge of the k-th's bin). Otherwise,
-        // or when lists ran past their windows (entries not yet resolved),
-        // the whole row is read again (rare).
+    if (lmode) {
+        // Sampling rows streamed on raw keys without penalties: every id a
+        // slice left out has a raw key below that slice's bound, so its true
+        // key (penalties only lower a logit, the temperature keeps the order)
+        // is at most the bound's scaled key. The candidates hold the exact
+        // top-k when its k-th key lies above the largest scaled bound (checked
+        // against the lower edge of the k-th's bin). Otherwise, or when lists
+        // ran past their windows (entries not yet resolved), the whole row is
+        // read again (rare).
         const uint32_t th = st.thmax;
         bool ok = th <= floor_key;
         if (!ok && any && bstar >= 0) {
+            const uint32_t ths = key32(key_to_float(th) * P.inv_temp);
             const uint32_t top = (shift + 11 >= 32) ? 0u : (Mk & ~((1u << (shift + 11)) - 1u));
-            ok = (top | ((uint32_t)bstar << shift)) >= th;
+            ok = (top | ((uint32_t)bstar << shift)) > ths;
         }
         if (!ok || extra != 0) {
             u64* rbuf = reinterpret_cast<u64*>(smem + 9216 + 8 * kCntCap + ((18 * ng + 15) & ~15));
@@ -2121,7 +2156,7 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
                     if (t[q] < 0) continue;
                     const bool allowed =
                         !masked || ((a.mask[(int64_t)r * a.mask_stride + (t[q] >> 5)] >> (t[q] & 31)) & 1u);
-                    const int rk = rank(t[q]);
+                    const int rk = pen ? rank(t[q]) : -1;
                     c[q] = value(t[q], x[q], allowed, rk >= 0 ? cnt[rk] : 0ull);
                 }
                 offer_regs<8>(rbuf, ovf, a.buf_cap, k, c, st);
@@ -2225,7 +2260,7 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
 //    penalised: its logit is read from the row, masked, and run through
 //    stages 1-6 (sampler.cpp:235-264) with the table's counts.
 //  - Entries beyond a slice's window (rare) are offered in a second pass.
-template <bool GT, bool FAST>
+template <bool GT, bool FAST, bool LM>
 __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ Shared st;
@@ -2247,7 +2282,7 @@ __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
     // built while the lists are in flight; other launches request what needs
     // no plan first: the slice counts, the window of the slices' lists, the
     // ragged end and id 0's logit.
-    const bool hist_first = FAST && a.pen_flag != 0;
+    constexpr bool hist_first = FAST && LM;
     RowPlan P;
     int32_t pre[8];
     if (hist_first) {
@@ -2349,7 +2384,7 @@ __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
         if (hist_first) atomicMax(&st.thmax, th_raw);
     }
     if (FAST) {
-        merge_fast<NW>(a, P, r, pre, bias_t, bias_h, nan_at0, tail_t, tail_x, tail_ok, ur, win, smem, st, sa, sP);
+        merge_fast<NW, LM>(a, P, r, pre, bias_t, bias_h, nan_at0, tail_t, tail_x, tail_ok, ur, win, smem, st, sa, sP);
         return;
     }
     if (tid == 0) st.u = ur;
@@ -3160,9 +3195,10 @@ hipError_t launch_merge(const StreamArgs& a, hipStream_t stream) {
         most = std::max(most, r1 - r0);
     }
     const dim3 g(kXcds * most);
-    if (a.fast) hipLaunchKernelGGL((k_merge<false, true>), g, dim3(kBlock), a.merge_lds, stream, a);
-    else if (a.gtab != nullptr) hipLaunchKernelGGL((k_merge<true, false>), g, dim3(kBlock), a.merge_lds, stream, a);
-    else hipLaunchKernelGGL((k_merge<false, false>), g, dim3(kBlock), a.merge_lds, stream, a);
+    if (a.fast && a.pen_flag) hipLaunchKernelGGL((k_merge<false, true, true>), g, dim3(kBlock), a.merge_lds, stream, a);
+    else if (a.fast) hipLaunchKernelGGL((k_merge<false, true, false>), g, dim3(kBlock), a.merge_lds, stream, a);
+    else if (a.gtab != nullptr) hipLaunchKernelGGL((k_merge<true, false, false>), g, dim3(kBlock), a.merge_lds, stream, a);
+    else hipLaunchKernelGGL((k_merge<false, false, false>), g, dim3(kBlock), a.merge_lds, stream, a);
     return hipGetLastError();
 }
 

@@ -1713,40 +1713,70 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
         {
             const int per = (ng + kBlock - 1) / kBlock;
             const int g0 = min(ng, tid * per), g1 = min(ng, g0 + per);
-            int sum = 0;
-            for (int g = g0; g < g1; ++g) {
-                const uint4 w = vb4[g];
-                sum += __popc(w.x) + __popc(w.y) + __popc(w.z) + __popc(w.w);
-            }
-            int tot;
-            int run = block_excl_scan(sum, &tot, st);
-            for (int g = g0; g < g1; ++g) {
-                const uint4 w = vb4[g];
-                vpw[g] = (uint16_t)run;
-                run += __popc(w.x) + __popc(w.y) + __popc(w.z) + __popc(w.w);
+            constexpr int GM = 8;   // groups per thread read at once (V <= 262144)
+            if (per <= GM) {
+                int pc[GM], sum = 0;
+#pragma unroll
+                for (int i = 0; i < GM; ++i) {
+                    const uint4 w = vb4[min(g0 + i, ng - 1)];
+                    pc[i] = (g0 + i < g1) ? __popc(w.x) + __popc(w.y) + __popc(w.z) + __popc(w.w) : 0;
+                    sum += pc[i];
+                }
+                int tot;
+                int run = block_excl_scan(sum, &tot, st);
+#pragma unroll
+                for (int i = 0; i < GM; ++i) {
+                    if (g0 + i < g1) vpw[g0 + i] = (uint16_t)run;
+                    run += pc[i];
+                }
+            } else {
+                int sum = 0;
+                for (int g = g0; g < g1; ++g) {
+                    const uint4 w = vb4[g];
+                    sum += __popc(w.x) + __popc(w.y) + __popc(w.z) + __popc(w.w);
+                }
+                int tot;
+                int run = block_excl_scan(sum, &tot, st);
+                for (int g = g0; g < g1; ++g) {
+                    const uint4 w = vb4[g];
+                    vpw[g] = (uint16_t)run;
+                    run += __popc(w.x) + __popc(w.y) + __popc(w.z) + __popc(w.w);
+                }
             }
         }
         __syncthreads();
     }
-    // rank of id t among the marked ids, or -1 when t is not marked
+    // rank of id t among the marked ids, or -1 when t is not marked; every
+    // word of the 16-byte group enters arithmetically, so the read stays one
+    // unconditional 16-byte load
     auto rank = [&](int t) -> int {
         const uint4 w = vb4[t >> 7];
         const int wi = (t >> 5) & 3;
-        const uint32_t wt = wi == 0 ? w.x : wi == 1 ? w.y : wi == 2 ? w.z : w.w;
-        const int rk = (int)vp[t >> 7] + (wi > 0 ? __popc(w.x) : 0) + (wi > 1 ? __popc(w.y) : 0) +
-                       (wi > 2 ? __popc(w.z) : 0) + __popc(wt & ((1u << (t & 31)) - 1u));
+        const uint32_t s0 = 0u - (uint32_t)(wi == 0), s1 = 0u - (uint32_t)(wi == 1);
+        const uint32_t s2 = 0u - (uint32_t)(wi == 2), s3 = 0u - (uint32_t)(wi == 3);
+        const uint32_t wt = (w.x & s0) | (w.y & s1) | (w.z & s2) | (w.w & s3);
+        const uint32_t b1 = 0u - (uint32_t)(wi > 0), b2 = 0u - (uint32_t)(wi > 1), b3 = 0u - (uint32_t)(wi > 2);
+        const int rk = (int)vp[t >> 7] + __popc(w.x & b1) + __popc(w.y & b2) + __popc(w.z & b3) +
+                       __popc(wt & ((1u << (t & 31)) - 1u));
         return ((wt >> (t & 31)) & 1u) ? rk : -1;
     };
     if (lmode && pen) {
+        // every rank read first, then the adds (no wait inside a branch)
         const int L = P.hist_len, p0 = L - P.scan_len;
+        int rkq[8];
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
             const int p = p0 + q * kBlock + tid;
-            if (p >= 0 && p < L && pre[q] >= 0 && pre[q] < a.vocab) {
-                const u64 add = ((p >= L - P.fp_win) ? 1ull : 0ull) | ((p >= L - P.dry_win) ? (1ull << 16) : 0ull) |
-                                ((p >= L - P.rep_win) ? (1ull << 32) : 0ull);
-                atomicAdd(&cnt[rank(pre[q])], add);
-            }
+            const bool ok = p >= 0 && p < L && pre[q] >= 0 && pre[q] < a.vocab;
+            const int rk = rank(ok ? pre[q] : 0);
+            rkq[q] = ok ? rk : -1;
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int p = p0 + q * kBlock + tid;
+            const u64 add = ((p >= L - P.fp_win) ? 1ull : 0ull) | ((p >= L - P.dry_win) ? (1ull << 16) : 0ull) |
+                            ((p >= L - P.rep_win) ? (1ull << 32) : 0ull);
+            if (rkq[q] >= 0) atomicAdd(&cnt[rkq[q]], add);
         }
         __syncthreads();
     }
@@ -1853,7 +1883,7 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
             const uint32_t v = ((c >> 32) & 0xFFFFull ? HV_REP : 0u) | ((c >> 63) ? HV_BIAS : 0u) |
                                ((uint32_t)((c >> 16) & 0xFFFFull) << HV_DRY_SHIFT) | (uint32_t)(c & 0xFFFFull);
             float y = ((mw[q] >> (t[q] & 31)) & 1u) ? x[q] : -__builtin_inff();
-            y = pen_value(y, t[q], v, sa, sP);
+            y = pen_value(y, t[q], v, a, P);
             if (greedy) {
                 if (y != y) {
                     atomicOr(&st.flags, 4);
@@ -1910,7 +1940,7 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
             if (lo < P.bias_cnt && ids[lo] == t) v |= HV_BIAS;
         }
         float y = allowed ? x : -__builtin_inff();
-        y = pen_value(y, t, v, sa, sP);
+        y = pen_value(y, t, v, a, P);
         if (!greedy) y = y * P.inv_temp;
         if (y != y) {
             atomicOr(&st.flags, 4);
@@ -1929,7 +1959,10 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
         u64 cj[NW];
         if (pen) {
 #pragma unroll
-            for (int j = 0; j < NW; ++j) rk[j] = win[j] != 0ull ? rank((int)comp_idx(win[j])) : -1;
+            for (int j = 0; j < NW; ++j) {
+                const int rj = rank(win[j] != 0ull ? (int)comp_idx(win[j]) : 0);
+                rk[j] = win[j] != 0ull ? rj : -1;
+            }
 #pragma unroll
             for (int j = 0; j < NW; ++j) cj[j] = rk[j] >= 0 ? cnt[rk[j]] : 0ull;
         }
@@ -1952,7 +1985,7 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
                     }
                     if (lo < P.bias_cnt && ids[lo] == t) v |= HV_BIAS;
                 }
-                y = pen_value(y, t, v, sa, sP);
+                y = pen_value(y, t, v, a, P);
             }
             y = y * P.inv_temp;
             if (y != y) {

@@ -53,3 +53,15 @@ def sampler(hs):
     s = hs.Sampler(0, max_rows=1024, max_vocab=1 << 18)
     yield s
     s.close()
+
+
+@pytest.fixture(params=["exact", "general"])
+def kernel_mode(request, monkeypatch):
+    """Runs a test twice: with exact lists allowed (the library's default for
+    the batches that qualify) and with ULTIMA_HSAMP_EXACT=0, which sends every
+    batch to the general stream and merge kernels."""
+    if request.param == "general":
+        monkeypatch.setenv("ULTIMA_HSAMP_EXACT", "0")
+    else:
+        monkeypatch.delenv("ULTIMA_HSAMP_EXACT", raising=False)
+    return request.param

@@ -20,9 +20,17 @@ def to_device(wl):
     return x, u, h, m
 
 
-def run_gpu(sampler, wl, bias=None, writeback=False, set_cap=2048):
+def run_gpu(sampler, wl, bias=None, writeback=False, set_cap=2048, row_align=None):
+    """row_align: place the rows in a buffer whose row stride is V rounded up
+    to this many elements (a padded, 16-byte aligned stride when V is not a
+    multiple of the load width)."""
     import torch
     x, u, h, m = to_device(wl)
+    if row_align:
+        V = x.shape[1]
+        xp = torch.zeros((x.shape[0], (V + row_align - 1) // row_align * row_align), dtype=x.dtype, device=x.device)
+        xp[:, :V] = x
+        x = xp[:, :V]
     out = sampler.run(x, wl.params, u, hist=h, hist_len=wl.hist_len, mask=m, bias=bias,
                       writeback=writeback, want_sets=True, set_cap=set_cap)
     torch.cuda.synchronize()

@@ -28,6 +28,9 @@ hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, bool pen_gree
                          bool greedy_rows, bool sample_rows, int grid, hipStream_t stream);
 hipError_t launch_writeback(const StreamArgs& a, int grid, uint32_t lds, hipStream_t stream);
 hipError_t launch_merge(const StreamArgs& a, hipStream_t stream);
+hipError_t launch_stream_ex(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int grid,
+                            hipStream_t stream);
+hipError_t launch_pick(const StreamArgs& a, int nw, hipStream_t stream);
 hipError_t launch_full(const StreamArgs& a, uint32_t lds, hipStream_t stream);
 }  // namespace hsamp
 
@@ -138,6 +141,8 @@ struct Built {
     int max_scan = 0;          // max history window over penalty rows
     int max_bias = 0;          // max logit-bias entries over rows
     bool pen_lowers = true;    // every penalty stage can only lower a logit
+    bool any_dry = false;      // a row with the DRY stage
+    bool inv_ok = true;        // every sampling row has 0 < fl(1/T) < inf
     bool any_mask = false;     // the batch carries an allowed-token mask
     bool any_full = false;     // a sampling row over the whole vocabulary (k_full)
     bool any_topk = false;     // a greedy or top-k row (k_stream + k_merge)
@@ -241,9 +246,11 @@ int build_blob(ultima_hsamp* h, const ultima_hsamp_batch* b, Built& out) {
             out.any_mask = true;
         }
         if (!greedy) {
+            P.temp = q.temperature;
             if (q.temperature != 1.0f) {                                          // [102]
                 fl |= RF_TEMP;
                 P.inv_temp = 1.0f / q.temperature;                                // [104]
+                if (!(P.inv_temp > 0.0f && P.inv_temp < INFINITY)) out.inv_ok = false;
             }
             if (V == 1) {
                 fl |= RF_SINGLE | RF_TOPK;
@@ -266,6 +273,7 @@ int build_blob(ultima_hsamp* h, const ultima_hsamp_batch* b, Built& out) {
             out.any_topk = out.any_greedy = true;
         }
         P.flags = fl;
+        if (fl & RF_DRY) out.any_dry = true;
         if (fl & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) {
             out.any_pen = true;
             out.max_pen = std::max(out.max_pen, (int)scan + P.bias_cnt);
@@ -550,7 +558,37 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
         return ULTIMA_HSAMP_ERR_CAPACITY;
     const int nblocks = B * S;
     const int grid = (nblocks + kXcds - 1) / kXcds * kXcds;
-    const int win = std::max(1, std::min(cand_cap, kMergeWindow / S));
+    int win = std::max(1, std::min(cand_cap, kMergeWindow / S));
+    // Exact lists (k_stream's EX kernels + k_pick): every row samples with
+    // top-k <= 64 and penalties that can only lower a logit, from windows the
+    // stream's registers hold, without DRY or logit bias. The stream then
+    // leaves every candidate with its final key. ULTIMA_HSAMP_EXACT=0 turns it
+    // off (the general kernels take every batch).
+    const bool wb_req = (b->flags & ULTIMA_HSAMP_WRITEBACK) != 0;
+    bool exact = bl.any_sample && !bl.any_greedy && !bl.any_full && kmax <= 64 && !wb_req && bl.inv_ok &&
+                 slice_len <= kBlock * 32 &&
+                 (!bl.any_pen || (bl.pen_lowers && !bl.any_dry && bl.max_bias == 0 && bl.max_scan <= 8 * kBlock));
+    if (const char* ev = std::getenv("ULTIMA_HSAMP_EXACT")) exact = exact && ev[0] != '0';
+    // k_stream EX: [count entries, 2 B per slice id + 8 (penalties)][allowed-id mask words]
+    // [staged chunks: kBlock x 16 B data, kBlock x 4 B first ids]
+    // (the general instantiations for unaligned rows take PEN = true: their
+    // count entries are cleared and stay zero when no row has penalties)
+    const bool vec_rows = (reinterpret_cast<uintptr_t>(b->logits) % 16 == 0) && ((b->logits_stride * es) % 16 == 0) &&
+                          V >= 16 / es;
+    const size_t cnt_bytes = (bl.any_pen || !vec_rows) ? align16(2 * ((size_t)slice_len + 8)) : 0;
+    const size_t stage_off = cnt_bytes + align16(4 * (size_t)bitmap_words);
+    const size_t lds_ex = stage_off + 20 * (size_t)kBlock;
+    // k_pick: each slice's first W entries, NW per thread; W about twice k
+    int pick_nw = 16;
+    if (exact) {
+        const int w0 = std::min(cand_cap, std::max(32, (2 * kmax + 31) / 32 * 32));
+        const int need = (S * w0 + kBlock - 1) / kBlock;
+        pick_nw = need <= 4 ? 4 : need <= 8 ? 8 : need <= 12 ? 12 : 16;
+        win = std::max(1, std::min(cand_cap, pick_nw * kBlock / S));
+        const size_t pick_lds = 8 * std::max<size_t>((size_t)pick_nw * kBlock + 2, (size_t)buf_cap);
+        if (lds_ex + statik > h->lds_limit || pick_lds + statik > h->lds_limit) exact = false;
+        else merge_lds = pick_lds;
+    }
 
     hipStreamCaptureStatus cap_status = hipStreamCaptureStatusNone;
     HIP_TRY(hipStreamIsCapturing(stream, &cap_status));
@@ -636,22 +674,27 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     const bool wb = (b->flags & ULTIMA_HSAMP_WRITEBACK) != 0;
     a.fin_idx = wb ? h->fin_idx : nullptr;
     a.fin_n = wb ? h->fin_n : nullptr;
-    a.lds_bytes = (uint32_t)lds;
+    a.lds_bytes = (uint32_t)(exact ? lds_ex : lds);
+    a.exact = exact ? 1 : 0;
+    a.mbm_off = (int32_t)(cnt_bytes / 4);
+    a.stage_off = (int32_t)stage_off;
     // 16-byte loads: aligned rows holding at least one whole chunk
-    const bool vec = (reinterpret_cast<uintptr_t>(b->logits) % 16 == 0) &&
-                     ((b->logits_stride * es) % 16 == 0) && V >= 16 / es;
+    const bool vec = vec_rows;
     a.vec_tail = vec ? V % (16 / es) : 0;
     a.uniform = (bl.any_greedy && !bl.any_sample && !bl.any_full ? 1 : 0) |
                 (bl.any_sample && !bl.any_greedy && !bl.any_full ? 2 : 0);
     // In flag mode the sampling rows' stream needs no penalties at all: it
     // bounds on pre-penalty keys, which penalties can only lower, and k_merge
     // finds the penalised candidates' true values (checking the bounds).
-    if (bl.any_topk)
+    if (exact)
+        HIP_TRY(launch_stream_ex(a, b->dtype, vec, bl.any_pen, bl.any_mask, grid, stream));
+    else if (bl.any_topk)
         HIP_TRY(launch_stream(a, b->dtype, vec, bl.any_pen, bl.any_pen && !a.pen_flag, bl.any_mask, bl.any_greedy,
                               bl.any_sample, grid, stream));
     if (h->phase_ev != nullptr) HIP_TRY(hipEventRecord(h->phase_ev, stream));
     if (!(b->flags & ULTIMA_HSAMP_STREAM_ONLY)) {
-        if (bl.any_topk) HIP_TRY(launch_merge(a, stream));
+        if (exact) HIP_TRY(launch_pick(a, pick_nw, stream));
+        else if (bl.any_topk) HIP_TRY(launch_merge(a, stream));
         if (bl.any_full) HIP_TRY(launch_full(a, (uint32_t)full_lds, stream));
         if (wb) HIP_TRY(launch_writeback(a, grid, (uint32_t)wb_lds, stream));
     }

@@ -34,6 +34,21 @@
 namespace hsamp {
 
 using u64 = unsigned long long;
+
+// Diagnostics: with HSAMP_PHASE_CLOCKS defined, thread 0 of each block records
+// the 100 MHz real-time clock at numbered points of the stream and merge
+// kernels (slot = block * 16 + point; stream blocks by logical id, merge
+// blocks from 8192 + row); hsamp_phase_read copies the clocks out. Off by
+// default: the macro then expands to nothing.
+#ifdef HSAMP_PHASE_CLOCKS
+__device__ unsigned long long g_phase[16384 * 16];
+#define HSAMP_PHASE(blk, i)                                                          \
+    do {                                                                             \
+        if (threadIdx.x == 0) g_phase[(blk) * 16 + (i)] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#else
+#define HSAMP_PHASE(blk, i) ((void)0)
+#endif
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kKeyNegInf = 0x007FFFFFu;        // key32(-inf)
@@ -66,6 +81,7 @@ struct Shared {
     u64 theta;          // current survival threshold (composite)
     u64 minv;
     int n;              // entries in the candidate buffer
+    int nst;            // exact lists: staged chunks
     int last;           // this block merges its row
     int sel_d, sel_need, sel_cnt;
     int scan[8];
@@ -1469,6 +1485,280 @@ __device__ __forceinline__ void stream_sample(const StreamArgs& a, const RowPlan
     }
 }
 
+// ---- exact lists ------------------------------------------------------------------
+// Batches whose rows all sample with top-k <= 64 and whose penalties can only
+// lower a logit (rep >= 1, freq/pres >= 0, no DRY, no bias) leave lists in
+// which every candidate carries its final logit before temperature (the raw
+// key below); k_pick applies the temperature. Every instruction a stream
+// thread runs costs about 8 ns of its CU (some 19 waves share it), so the
+// pass over the tile is lean:
+//  A. as each 16-byte chunk arrives: the chunk's float maximum (v_max ignores
+//     NaN) and one NaN test per two elements; nothing per element else.
+//  B. the bound: each wave's kw-th largest lane maximum (kw = ceil((k+8)/4),
+//     low 16 bits cleared), minimum over the waves: B, with at least k + 8
+//     ids of the slice at or above it. ths = B's scaled key; every id whose
+//     final key is below ths is beaten by them (if at least k of them keep a
+//     final key >= ths, checked at the end) and left out. R = raw_edge(ths)
+//     is the smallest raw key whose scaled key reaches ths, so the kept ids
+//     are exactly those whose final raw key reaches R.
+//  C. chunks whose maximum reaches R are staged in LDS (one wave-level prefix
+//     and one LDS atomic per wave); D. one thread per staged chunk finds its
+//     elements' final raw keys (penalised ids, nonzero count entry, take
+//     stages 1-4 from the slice's history counts; a penalty only lowers the
+//     key, so only ids at or above R before it can qualify) and appends those
+//     that reach R.
+//  E. when penalties took so many of them below R that fewer than k remain,
+//     the block goes over the slice again down to the floor (rare).
+// The slice's history counts sit in LDS, one 16-bit entry per slice id (XC_*).
+
+constexpr int kStageCap = kBlock;          // staged chunks per round
+constexpr uint32_t kKeyPosInf = 0xFF800000u;  // key32(+inf)
+
+// Raw key of a logit: key32 without merging -0 into +0 (so that key_to_float
+// gives x back), NaN as -inf. Non-decreasing in x.
+__device__ __forceinline__ uint32_t raw_key(float x) {
+    const uint32_t b = __float_as_uint(x);
+    const uint32_t k = b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
+    return (x != x) ? kKeyNegInf : k;
+}
+
+// Final key of a raw key: temperature (sampler.cpp:101-106), -0 -> +0.
+// Non-decreasing in the raw key; exact lists need 0 < inv_t < inf, so no NaN
+// arises from a finite or infinite logit.
+__device__ __forceinline__ uint32_t scaled_key(uint32_t kr, float inv_t) {
+    float y = key_to_float(kr) * inv_t;
+    y = y + 0.0f;
+    return key32(y);
+}
+
+// The smallest raw key in [key(-FLT_MAX), key(+inf)] whose scaled key reaches
+// ths (scaled_key(key(+inf)) = key(+inf) >= ths): from a first guess (ths's
+// float times T) a few unit steps, else a binary search.
+__device__ uint32_t raw_edge(uint32_t ths, float inv_t, float temp) {
+    constexpr uint32_t lo0 = kKeyNegInf + 1u;
+    const float g = key_to_float(ths) * temp;
+    uint32_t r = raw_key(g);
+    r = min(max(r, lo0), kKeyPosInf);
+    for (int it = 0; it < 4 && r < kKeyPosInf && scaled_key(r, inv_t) < ths; ++it) ++r;
+    for (int it = 0; it < 4 && r > lo0 && scaled_key(r - 1u, inv_t) >= ths; ++it) --r;
+    if (scaled_key(r, inv_t) >= ths && (r == lo0 || scaled_key(r - 1u, inv_t) < ths)) return r;
+    uint32_t lo = lo0, hi = kKeyPosInf;
+    while (lo < hi) {
+        const uint32_t mid = lo + ((hi - lo) >> 1);
+        if (scaled_key(mid, inv_t) >= ths) hi = mid;
+        else lo = mid + 1u;
+    }
+    return lo;
+}
+
+// Final raw key of slice id t (raw logit x, after the mask) with count entry
+// h: stages 1-4 (sampler.cpp:28-99, those a count entry calls for), NaN ->
+// -inf (noted).
+__device__ __forceinline__ uint32_t final_raw_key(float x, int32_t t, uint32_t h, const StreamArgs& a,
+                                                  const RowPlan& P, bool& nan) {
+    if (h == 0u) return raw_key(x);
+    const uint32_t v = ((h & XC_REP) ? HV_REP : 0u) | (h & XC_FP_MASK);
+    const float y = pen_value(x, t, v, a, P);
+    if (y != y) {
+        nan = true;
+        return kKeyNegInf;
+    }
+    return raw_key(y);
+}
+
+// A sampling row's slice [lo, hi) with exact lists (single tile, raw[] holds
+// it); the row's last slice (last_slice) also takes the ragged end that
+// whole-chunk loads leave out.
+template <int DT, bool VEC, bool PEN, bool MASK>
+__device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan& P, int r, int lo, int hi,
+                                             const uint4 (&raw)[Tile<DT>::NCH], u64* out, int64_t slot,
+                                             bool last_slice, bool pen, bool mk, const int32_t (&pre)[8],
+                                             unsigned char* smem, Shared& st) {
+    using T = Tile<DT>;
+    const int tid = threadIdx.x, lane = lane_id();
+    uint16_t* cnt = reinterpret_cast<uint16_t*>(smem);
+    const uint32_t* mbm = reinterpret_cast<const uint32_t*>(smem) + a.mbm_off;
+    uint4* sdat = reinterpret_cast<uint4*>(smem + a.stage_off);
+    int32_t* sidx = reinterpret_cast<int32_t*>(sdat + kStageCap);
+    constexpr uint32_t kFloor = (uint32_t)(kThetaFloor >> 32);
+
+    // A. chunk maxima, as the chunks arrive
+    float cm[T::NCH];
+    bool nanv = false;
+#pragma unroll
+    for (int j = 0; j < T::NCH; ++j) {
+        const int e0 = lo + (j * kBlock + tid) * T::VW;
+        const bool in = e0 < hi;
+        float x[T::VW];
+#pragma unroll
+        for (int c = 0; c < T::VW; ++c) x[c] = elem<DT>(raw[j], c);
+        if (MASK) {
+            const int o = e0 - lo;
+            const uint32_t mb = mbm[max(0, min(o, hi - lo - 1)) >> 5] >> (o & 31);
+#pragma unroll
+            for (int c = 0; c < T::VW; ++c) x[c] = ((mb >> c) & 1u) ? x[c] : -__builtin_inff();
+        }
+        if (!VEC) {
+            // element loads: the slice's last chunk may end inside (past hi reads 0)
+#pragma unroll
+            for (int c = 0; c < T::VW; ++c) x[c] = (e0 + c < hi) ? x[c] : -__builtin_inff();
+        }
+        float m = x[0];
+#pragma unroll
+        for (int c = 1; c < T::VW; ++c) m = fmaxf(m, x[c]);
+#pragma unroll
+        for (int c = 0; c < T::VW; c += 2) nanv |= __builtin_isunordered(x[c], x[c + 1]);
+        cm[j] = (in && m == m) ? m : -__builtin_inff();
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    HSAMP_PHASE(slot, 3);
+
+    // B. the slice's history counts (waits for the history loads) and the bound
+    if (PEN && pen) {
+        const int L = P.hist_len, p0 = L - P.scan_len;
+        const int mhi = min(a.vocab, lo + a.slice_len);
+        uint32_t* cw = reinterpret_cast<uint32_t*>(smem);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int p = p0 + q * kBlock + tid;
+            const int32_t t = pre[q];
+            if (p < L && t >= lo && t < mhi) {
+                const int o = t - lo;
+                const uint32_t sh = (uint32_t)(o & 1) << 4;
+                if (p >= L - P.fp_win) atomicAdd(&cw[o >> 1], 1u << sh);
+                if (p >= L - P.rep_win) atomicOr(&cw[o >> 1], XC_REP << sh);
+            }
+        }
+    }
+    uint32_t ck[T::NCH], lk = 0u;
+#pragma unroll
+    for (int j = 0; j < T::NCH; ++j) {
+        const uint32_t b = __float_as_uint(cm[j]);
+        ck[j] = b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);   // cm is never NaN
+        lk = max(lk, ck[j]);
+    }
+    const int k = P.top_k;
+    const int kw = (k + 8 + 3) >> 2;   // <= 18
+    const uint32_t g4[4] = {lk, 0u, 0u, 0u};
+    const uint32_t tw = wave_kth_bound16(g4, 1, kw);
+    if (lane == 0) st.twave[wave_id()] = tw;
+    // the ragged end (the row's last slice): read while the bound settles
+    float xt = 0.0f;
+    const bool tl = VEC && last_slice && tid < a.vec_tail;
+    const int32_t tt_id = a.vocab - a.vec_tail + tid;
+    if (tl) {
+        const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * T::ES;
+        xt = load_logit<DT>(rowp, tt_id);
+        if (mk && !((a.mask[(int64_t)r * a.mask_stride + (tt_id >> 5)] >> (tt_id & 31)) & 1u)) xt = -__builtin_inff();
+    }
+    __syncthreads();   // also publishes the history counts
+    HSAMP_PHASE(slot, 4);
+    uint32_t thr = st.twave[0];
+#pragma unroll
+    for (int i = 1; i < kBlock / 64; ++i) thr = min(thr, st.twave[i]);
+    thr = max(thr, kFloor);
+    const float inv_t = P.inv_temp;
+    const uint32_t R = raw_edge(max(scaled_key(thr, inv_t), kFloor), inv_t, P.temp);
+
+    // C, D. the ids whose final raw key lies in [Rlo, Rhi)
+    auto pass = [&](uint32_t Rlo, uint32_t Rhi) {
+        uint32_t csel = 0u;
+#pragma unroll
+        for (int j = 0; j < T::NCH; ++j) csel |= (ck[j] >= Rlo) ? (1u << j) : 0u;
+        const int c0 = __popc(csel);
+        int incl = c0;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int y = __shfl_up(incl, d, 64);
+            if (lane >= d) incl += y;
+        }
+        const int wtot = __shfl(incl, 63, 64);
+        int base = 0;
+        if (lane == 63 && wtot > 0) base = atomicAdd(&st.nst, wtot);
+        const int pos0 = __shfl(base, 63, 64) + incl - c0;
+        auto stage = [&](int rb) {
+            int p = pos0;
+#pragma unroll
+            for (int j = 0; j < T::NCH; ++j) {
+                if ((csel >> j) & 1u) {
+                    if (p >= rb && p < rb + kStageCap) {
+                        sdat[p - rb] = raw[j];
+                        sidx[p - rb] = lo + (j * kBlock + tid) * T::VW;
+                    }
+                    ++p;
+                }
+            }
+        };
+        stage(0);
+        __syncthreads();
+        const int nst = st.nst;
+        bool nanp = false;
+        for (int rb = 0;;) {
+            if (tid < nst - rb) {
+                const uint4 d = sdat[tid];
+                const int e0 = sidx[tid];
+                const int o = e0 - lo;
+                uint32_t mb = 0xFFFFFFFFu;
+                if (MASK) mb = mbm[o >> 5] >> (o & 31);
+                uint32_t hc[T::VW];
+#pragma unroll
+                for (int c = 0; c < T::VW; ++c) hc[c] = 0u;
+                if (PEN) {
+                    if (DT == 0) {
+                        const uint2 w = *reinterpret_cast<const uint2*>(cnt + o);
+                        hc[0] = w.x & 0xFFFFu;
+                        hc[1] = w.x >> 16;
+                        hc[2] = w.y & 0xFFFFu;
+                        hc[3] = w.y >> 16;
+                    } else {
+                        const uint4 w = *reinterpret_cast<const uint4*>(cnt + o);
+                        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                        for (int c = 0; c < T::VW; ++c) hc[c] = (c & 1) ? (ww[c >> 1] >> 16) : (ww[c >> 1] & 0xFFFFu);
+                    }
+                }
+#pragma unroll
+                for (int c = 0; c < T::VW; ++c) {
+                    float x = elem<DT>(d, c);
+                    if (MASK && !((mb >> c) & 1u)) x = -__builtin_inff();
+                    if ((VEC || e0 + c < hi) && raw_key(x) >= Rlo) {
+                        const uint32_t kf = final_raw_key(x, e0 + c, PEN ? hc[c] : 0u, a, P, nanp);
+                        if (kf >= Rlo && kf < Rhi) out[atomicAdd(&st.n, 1)] = comp(kf, e0 + c);
+                    }
+                }
+            }
+            rb += kStageCap;
+            if (rb >= nst) break;
+            __syncthreads();
+            stage(rb);
+            __syncthreads();
+        }
+        if (tl) {
+            const uint32_t kf = final_raw_key(xt, tt_id, PEN ? (uint32_t)cnt[tt_id - lo] : 0u, a, P, nanp);
+            if (kf >= Rlo && kf < Rhi) out[atomicAdd(&st.n, 1)] = comp(kf, tt_id);
+        }
+        if (nanp) atomicOr(&st.flags, 1);
+        __syncthreads();
+    };
+    pass(R, 0xFFFFFFFFu);
+    HSAMP_PHASE(slot, 5);
+    // E. fewer than k ids kept above a raised bound (penalties took the rest
+    // below it): every id down to the floor
+    if (PEN && st.n < k) {
+        const uint32_t Rf = raw_edge(max(scaled_key(kFloor, inv_t), kFloor), inv_t, P.temp);
+        if (R > Rf) {
+            __syncthreads();
+            if (tid == 0) st.nst = 0;
+            __syncthreads();
+            pass(Rf, R);
+        }
+    }
+    if (nanv) atomicOr(&st.flags, 1);
+    __syncthreads();
+    if (tid == 0) a.cand_n[slot] = st.n | ((st.flags & 1) ? (1 << 30) : 0);
+    HSAMP_PHASE(slot, 6);
+}
+
 // One block per (row, slice): stream the slice once and leave for k_merge the
 // ids whose key can still be among the row's top k (all of them, in composite
 // form), or the slice's argmax for a greedy row. Penalised ids (history window
@@ -1479,7 +1769,9 @@ __device__ __forceinline__ void stream_sample(const StreamArgs& a, const RowPlan
 // GR: the launch's greedy rows (true) or sampling rows (false); a batch with
 // both takes one launch of each, so that each loop has the whole register
 // budget of five blocks per CU.
-template <int DT, bool VEC, bool PEN, bool MASK, bool GR>
+// EX: exact lists (sampling rows only, see stream_exact); LDS then
+// [count entries (PEN), 2 B per slice id + 8][allowed-id mask words].
+template <int DT, bool VEC, bool PEN, bool MASK, bool GR, bool EX = false>
 __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
     using T = Tile<DT>;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -1495,10 +1787,20 @@ __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
     // When every row of the launch is this kernel's, the first tile goes out
     // before the plan is read (it is processed chunk by chunk as its loads
     // complete in order); otherwise after the plan has said the row is ours.
-    const bool early = ((a.uniform >> (GR ? 0 : 1)) & 1) != 0;
+    const bool early = EX || ((a.uniform >> (GR ? 0 : 1)) & 1) != 0;
     uint4 raw[T::NCH];
+    // exact lists: the plan's scalar load and the slice's mask words go out
+    // before the tile (the mask words then wait for nothing else)
+    RowPlan P;
+    if (EX) P = a.plans[r];
+    // (MASK launches may carry no mask: the general instantiations for
+    // unaligned rows take MASK = true; the mask words are then all ones)
+    const bool mk = MASK && a.mask != nullptr;
+    uint32_t mw_pre = 0xFFFFFFFFu;
+    if (EX && mk && tid < a.bitmap_words)
+        mw_pre = (lo + 32 * tid < hi) ? a.mask[(int64_t)r * a.mask_stride + (lo >> 5) + tid] : 0u;
     if (early) load_tile<DT, VEC>(rs, lo, raw);
-    const RowPlan P = a.plans[r];
+    if (!EX) P = a.plans[r];
     if (!early) {
         if (P.flags & RF_FULL) return;                     // k_full's row
         if (((P.flags & RF_GREEDY) != 0) != GR) return;    // the other kernel's row
@@ -1519,6 +1821,25 @@ __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
         for (int q = 0; q < 8; ++q) pre[q] = hrow[max(0, min(p0 + q * kBlock + tid, L - 1))];
     }
     uint32_t* pbm = reinterpret_cast<uint32_t*>(smem);
+    if constexpr (EX) {
+        HSAMP_PHASE(logical, 0);
+        if (PEN) {
+            for (int i = tid; i < (a.mbm_off >> 2); i += kBlock) reinterpret_cast<uint4*>(smem)[i] = make_uint4(0u, 0u, 0u, 0u);
+        }
+        if (MASK && tid < a.bitmap_words) pbm[a.mbm_off + tid] = mw_pre;
+        if (tid == 0) {
+            st.n = 0;
+            st.nst = 0;
+            st.flags = 0;
+        }
+        __syncthreads();
+        HSAMP_PHASE(logical, 1);
+        const int64_t slot = (int64_t)r * a.nslices + s;
+        u64* out = a.cand + slot * a.cand_cap;
+        stream_exact<DT, VEC, PEN, MASK>(a, P, r, lo, hi, raw, out, slot, VEC && s == a.nslices - 1, pen, mk, pre,
+                                         smem, st);
+        return;
+    }
     stream_setup<PEN, MASK>(a, P, r, lo, hi, GR, pen, masked, p0, L, hrow, pbm, pbm + a.bitmap_words, st);
     if (!early) load_tile<DT, VEC>(rs, lo, raw);
     if (PEN) {
@@ -2551,6 +2872,191 @@ __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
     select_and_finalize(sa, sP, r, buf, f, st, rflags);
 }
 
+// ---- the merge of exact lists -------------------------------------------------------
+
+// One block per sampling row whose slices left exact lists (k_stream's EX
+// kernels; k <= 64): the row's exact top-k and the rest of the ladder
+// (sampler.cpp:267-277). No history work and no logit reads: every
+// candidate carries its final logit before temperature, which is applied here.
+//  - The slice counts, a window of W entries of every slice's list (NW per
+//    thread; entry g is slice g / W, position g % W), the plan and u are
+//    requested together.
+//  - Bound: the k-th largest of the 256 lane maxima with its low 16 bits
+//    cleared. Every lane maximum is a candidate of its own, so this is a
+//    lower bound of the row's k-th largest key. The candidates at or above it
+//    are ranked exactly: by wave 0 when at most 128, else by the block after a
+//    radix compaction to the k largest when more than 256.
+//  - A list longer than its window (ties, flat rows) takes the buffer path.
+template <int NW>
+__global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ Shared st;
+    __shared__ StreamArgs sa;
+    __shared__ RowPlan sP;
+    const int tid = threadIdx.x, lane = lane_id();
+    const int S = a.nslices, W = a.win;
+    // the row whose slices k_stream handed over on this block's XCD
+    const int x = (int)(blockIdx.x % kXcds);
+    const int r0 = min(a.rows, (x * a.blocks_per_xcd + S - 1) / S);
+    const int r1 = min(a.rows, ((x + 1) * a.blocks_per_xcd + S - 1) / S);
+    const int r = r0 + (int)(blockIdx.x / kXcds);
+    if (r >= r1) return;
+    HSAMP_PHASE(8192 + r, 0);
+    const u64* cand = a.cand + (int64_t)r * S * a.cand_cap;
+    const int cnt_raw = (tid < S) ? a.cand_n[(int64_t)r * S + tid] : 0;
+    u64 win[NW];
+    {
+        // one buffer resource over the row's lists: entries past the last
+        // slice read as 0
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<u64*>(cand), (short)0, S * a.cand_cap * 8, 0x00020000);
+        const uint32_t magic = a.win_magic;
+        const int cap = a.cand_cap;
+#pragma unroll
+        for (int j = 0; j < NW; ++j) {
+            const int g = tid + j * kBlock;
+            const int sl = (int)__umulhi((uint32_t)g, magic);   // g / W
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, (sl * cap + (g - sl * W)) * 8, 0, 0);
+            win[j] = ((u64)v[1] << 32) | v[0];
+        }
+    }
+    const RowPlan P = a.plans[r];
+    const double ur = a.u[r];
+    if (tid == 0) {
+        st.flags = 0;
+        st.n = 0;
+        st.theta = kThetaFloor;
+        st.u = ur;
+        sa = a;
+        sP = P;
+    }
+    if (tid < 32) {
+        // expf's table from immediates (an indexed read would wait for every
+        // load issued so far)
+        uint64_t e = 0ull;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) e = (tid == i) ? kExpT[i] : e;
+        st.expT[tid] = e;
+    }
+    __syncthreads();
+    HSAMP_PHASE(8192 + r, 1);
+    if (tid < S) {
+        st.soff[tid] = cnt_raw & 0x1FFFFFFF;
+        if (cnt_raw & (1 << 30)) atomicOr(&st.flags, 4);          // a NaN logit in the slice
+        if ((cnt_raw & 0x1FFFFFFF) > W) atomicOr(&st.flags, 8);   // a list past the window
+    }
+    __syncthreads();
+    const int k = P.top_k;
+    const float inv_t = P.inv_temp;
+    const uint32_t rflags = (st.flags & 4) ? ROWF_NAN : 0u;
+    // the lists carry final logits before temperature: composites of the
+    // scaled keys (sampler.cpp:101-106)
+    auto scaled = [&](u64 c) -> u64 {
+        return ((u64)scaled_key((uint32_t)(c >> 32), inv_t) << 32) | (c & 0xFFFFFFFFull);
+    };
+    uint32_t lm = 0u;
+#pragma unroll
+    for (int j = 0; j < NW; ++j) {
+        const int g = tid + j * kBlock;
+        const int sl = (int)__umulhi((uint32_t)g, a.win_magic);
+        win[j] = (sl >= S || g - sl * W >= st.soff[sl]) ? 0ull : scaled(win[j]);
+        lm = max(lm, (uint32_t)(win[j] >> 32));
+    }
+    u64* list = reinterpret_cast<u64*>(smem);
+    if (st.flags & 8) {
+        // buffer path: every entry offered under a rising threshold
+        u64* ovf = a.ovf + (int64_t)r * a.ovf_cap;
+        offer_regs<NW>(list, ovf, a.buf_cap, k, win, st);
+        for (int sl = 0; sl < S; ++sl) {
+            const int n = st.soff[sl];
+            for (int e0 = W; e0 < n; e0 += 8 * kBlock) {
+                u64 c[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const int e = e0 + q * kBlock + tid;
+                    c[q] = (e < n) ? scaled(cand[(int64_t)sl * a.cand_cap + e]) : 0ull;
+                }
+                offer_regs<8>(list, ovf, a.buf_cap, k, c, st);
+            }
+        }
+        __syncthreads();
+        FinLds f{};
+        select_and_finalize(sa, sP, r, list, f, st, rflags);
+        return;
+    }
+    st.hist[tid] = lm;
+    __syncthreads();
+    HSAMP_PHASE(8192 + r, 2);
+    if (tid < 64) {
+        const uint32_t g4[4] = {st.hist[lane], st.hist[lane + 64], st.hist[lane + 128], st.hist[lane + 192]};
+        const uint32_t bound = wave_kth_bound16(g4, 4, k);
+        if (lane == 0) st.twave[0] = bound;
+    }
+    __syncthreads();
+    const uint32_t Lk = max(st.twave[0], (uint32_t)(kThetaFloor >> 32));
+    {
+        // the candidates at or above the bound, packed into the list
+        uint32_t sv = 0u;
+#pragma unroll
+        for (int j = 0; j < NW; ++j) sv |= (win[j] != 0ull && (uint32_t)(win[j] >> 32) >= Lk) ? (1u << j) : 0u;
+        const int cnt = __popc(sv);
+        int incl = cnt;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int y = __shfl_up(incl, d, 64);
+            if (lane >= d) incl += y;
+        }
+        const int wtot = __shfl(incl, 63, 64);
+        if (wtot > 0) {
+            int base = 0;
+            if (lane == 63) base = atomicAdd(&st.n, wtot);
+            int pos = __shfl(base, 63, 64) + incl - cnt;
+#pragma unroll
+            for (int j = 0; j < NW; ++j)
+                if ((sv >> j) & 1u) list[pos++] = win[j];
+        }
+    }
+    __syncthreads();
+    HSAMP_PHASE(8192 + r, 3);
+    int n = st.n;
+    if (n <= 128) {
+        // wave 0 ranks the (distinct) entries exactly: rank = entries above
+        if (tid >= 64) return;
+        if (lane == 0) list[n] = 0ull;   // pad to pairs
+        wave_sync();
+        const u64 m0 = (lane < n) ? list[lane] : 0ull;
+        const u64 m1 = (lane + 64 < n) ? list[lane + 64] : 0ull;
+        int q0 = 0, q1 = 0;
+        const ulonglong2* l2 = reinterpret_cast<const ulonglong2*>(list);
+#pragma unroll 4
+        for (int j = 0; j < (n + 1) >> 1; ++j) {
+            const ulonglong2 x2 = l2[j];
+            q0 += (x2.x > m0) + (x2.y > m0);
+            q1 += (x2.x > m1) + (x2.y > m1);
+        }
+        wave_sync();
+        if (lane < n && q0 < k) st.wv[q0] = m0;
+        if (lane + 64 < n && q1 < k) st.wv[q1] = m1;
+        wave_sync();
+        const int nk = min(k, n);
+        const u64 c = (lane < nk) ? st.wv[lane] : 0ull;
+        wave_sync();
+        HSAMP_PHASE(8192 + r, 4);
+        wave_finalize(sa, sP, r, c, nk, rflags, st);
+        HSAMP_PHASE(8192 + r, 5);
+        return;
+    }
+    if (n > 256) {
+        buf_compact(list, k, st);
+        n = st.n;
+    }
+    block_rank_topk(list, n, k, st);
+    if (tid >= 64) return;
+    const int nk = min(k, n);
+    const u64 c = (lane < nk) ? st.wv[lane] : 0ull;
+    wave_finalize(sa, sP, r, c, nk, rflags, st);
+}
+
 // ---- writeback -------------------------------------------------------------------
 
 template <bool GT>
@@ -3211,6 +3717,70 @@ static void launch_stream_kind(const StreamArgs& a, int dtype, bool vec, bool pe
 #undef HSAMP_STREAM
 }
 
+// Exact lists: the sampling kernel with final keys (every row samples).
+static void launch_stream_exact(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int grid,
+                                hipStream_t stream) {
+    const dim3 g(grid), b(kBlock);
+    const uint32_t l = a.lds_bytes;
+#define HSAMP_STREAM(DT_, V_, P_, M_) hipLaunchKernelGGL((k_stream<DT_, V_, P_, M_, false, true>), g, b, l, stream, a)
+    if (!vec) {
+        if (dtype == 0) HSAMP_STREAM(0, false, true, true);
+        else HSAMP_STREAM(1, false, true, true);
+    } else if (dtype == 0) {
+        if (pen) {
+            if (mask) HSAMP_STREAM(0, true, true, true);
+            else HSAMP_STREAM(0, true, true, false);
+        } else {
+            if (mask) HSAMP_STREAM(0, true, false, true);
+            else HSAMP_STREAM(0, true, false, false);
+        }
+    } else {
+        if (pen) {
+            if (mask) HSAMP_STREAM(1, true, true, true);
+            else HSAMP_STREAM(1, true, true, false);
+        } else {
+            if (mask) HSAMP_STREAM(1, true, false, true);
+            else HSAMP_STREAM(1, true, false, false);
+        }
+    }
+#undef HSAMP_STREAM
+}
+
+hipError_t launch_stream_ex(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int grid,
+                            hipStream_t stream) {
+    launch_stream_exact(a, dtype, vec, pen, mask, grid, stream);
+    return hipGetLastError();
+}
+
+// Blocks of the per-row kernels: kXcds times the most rows whose first slice
+// one XCD streamed (each row is merged on that XCD).
+static int row_blocks(const StreamArgs& a) {
+    int most = 0;
+    for (int x = 0; x < kXcds; ++x) {
+        const int r0 = std::min(a.rows, (x * a.blocks_per_xcd + a.nslices - 1) / a.nslices);
+        const int r1 = std::min(a.rows, ((x + 1) * a.blocks_per_xcd + a.nslices - 1) / a.nslices);
+        most = std::max(most, r1 - r0);
+    }
+    return kXcds * most;
+}
+
+hipError_t launch_pick(const StreamArgs& a, int nw, hipStream_t stream) {
+    const dim3 g(row_blocks(a)), b(kBlock);
+    switch (nw) {
+        case 4: hipLaunchKernelGGL((k_pick<4>), g, b, a.merge_lds, stream, a); break;
+        case 8: hipLaunchKernelGGL((k_pick<8>), g, b, a.merge_lds, stream, a); break;
+        case 12: hipLaunchKernelGGL((k_pick<12>), g, b, a.merge_lds, stream, a); break;
+        default: hipLaunchKernelGGL((k_pick<16>), g, b, a.merge_lds, stream, a); break;
+    }
+    return hipGetLastError();
+}
+
+#ifdef HSAMP_PHASE_CLOCKS
+extern "C" int hsamp_phase_read(void* dst, size_t bytes) {
+    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_phase), bytes, 0, hipMemcpyDeviceToHost);
+}
+#endif
+
 hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, bool pen_greedy, bool pen_sample, bool mask,
                          bool greedy_rows, bool sample_rows, int grid, hipStream_t stream) {
     if (greedy_rows) launch_stream_kind<true>(a, dtype, vec, pen_greedy, mask, grid, stream);
@@ -3219,15 +3789,7 @@ hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, bool pen_gree
 }
 
 hipError_t launch_merge(const StreamArgs& a, hipStream_t stream) {
-    // kXcds times the most rows whose first slice one XCD streamed (k_merge
-    // takes each row on that XCD)
-    int most = 0;
-    for (int x = 0; x < kXcds; ++x) {
-        const int r0 = std::min(a.rows, (x * a.blocks_per_xcd + a.nslices - 1) / a.nslices);
-        const int r1 = std::min(a.rows, ((x + 1) * a.blocks_per_xcd + a.nslices - 1) / a.nslices);
-        most = std::max(most, r1 - r0);
-    }
-    const dim3 g(kXcds * most);
+    const dim3 g(row_blocks(a));
     if (a.fast && a.pen_flag) hipLaunchKernelGGL((k_merge<false, true, true>), g, dim3(kBlock), a.merge_lds, stream, a);
     else if (a.fast) hipLaunchKernelGGL((k_merge<false, true, false>), g, dim3(kBlock), a.merge_lds, stream, a);
     else if (a.gtab != nullptr) hipLaunchKernelGGL((k_merge<true, false, false>), g, dim3(kBlock), a.merge_lds, stream, a);

@@ -42,6 +42,13 @@ enum : uint32_t {
     HV_REP = 1u << 31,       // id is in the repetition window
 };
 
+// Exact lists: per-slice history counts, one 16-bit entry per slice id
+// (frequency/presence window occurrences, repetition-window bit).
+enum : uint32_t {
+    XC_FP_MASK = 0x7fffu,
+    XC_REP = 0x8000u,
+};
+
 struct alignas(16) RowPlan {
     float inv_temp;     // fl(1.0f / T) when RF_TEMP, else 1.0f
     float rep;          // repetition penalty
@@ -60,7 +67,8 @@ struct alignas(16) RowPlan {
     int32_t bias_off;   // offset of this row's sorted bias ids/values in the plan blob
     int32_t bias_cnt;
     uint32_t flags;
-    uint32_t pad_[3];
+    float temp;         // T (sampling rows): a first guess when inverting the temperature
+    uint32_t pad_[2];
 };
 static_assert(sizeof(RowPlan) == 80, "RowPlan layout");
 
@@ -111,6 +119,10 @@ struct StreamArgs {
                                 // flagged candidates (pre-penalty key) instead of leaving them out
     int32_t vec_tail;           // the row's last ids k_merge reads itself (V % chunk with vector loads)
     int32_t uniform;            // bit 0: every row is greedy, bit 1: every row is top-k sampling
+    int32_t exact;              // exact lists: k_stream leaves every candidate with its final logit
+                                // before temperature (penalties applied), k_pick merges them
+    int32_t mbm_off;            // exact lists: words from the LDS base to the slice's mask words
+    int32_t stage_off;          // exact lists: bytes from the LDS base to the staged chunks
     float* fullv;               // [rows * vocab] k_full: transformed logits (-inf once removed)
     float* fullp;               // [rows * vocab] k_full: probabilities
     uint32_t* fullk;            // [rows * 2 * full_p2] k_full: probability keys by bucket, sort scratch

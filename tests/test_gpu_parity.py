@@ -184,9 +184,6 @@ def test_sampling_penalties_ragged_end(sampler, wl, V, dtype, kernel_mode):
     of the 16-byte load width: the row's last ids, which the stream's vector
     loads leave out, hold high logits and sit in the history many times, so
     their true values decide the top-k."""
-    if kernel_mode == "general" and V <= 8192:
-        pytest.xfail("known bug: the general kernels' flag-mode merge of single-slice rows (V <= 8192) "
-                     "with penalties returns NaN-flagged uniform draws")
     rng = np.random.default_rng(V + 17)
     B, H = 4, 256
     xf = (rng.normal(size=(B, V)) * 2).astype(np.float32)

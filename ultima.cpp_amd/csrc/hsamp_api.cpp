@@ -678,6 +678,8 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     a.exact = exact ? 1 : 0;
     a.mbm_off = (int32_t)(cnt_bytes / 4);
     a.stage_off = (int32_t)stage_off;
+    a.hist_direct = (exact && bl.any_pen && b->hist != nullptr && b->hist_stride >= 1 &&
+                     b->hist_stride <= 8 * kBlock) ? 1 : 0;
     // 16-byte loads: aligned rows holding at least one whole chunk
     const bool vec = vec_rows;
     a.vec_tail = vec ? V % (16 / es) : 0;

@@ -1034,6 +1034,7 @@ __device__ __forceinline__ void wave_finalize(const StreamArgs& a, const RowPlan
     uint32_t id = (lane < nk) ? (uint32_t)comp_idx(c) : (0x80000000u | (uint32_t)lane);
     uint32_t vk = (lane < nk) ? (uint32_t)(c >> 32) : 0u;
     wave_sort_asc(id, vk, wv);
+    HSAMP_PHASE(8192 + r, 6);
     const bool has = lane < nk;
     const float v = key_to_float(vk);
     if (a.topk_idx != nullptr && has && lane < a.set_cap) a.topk_idx[(int64_t)r * a.set_cap + lane] = (int32_t)id;
@@ -1041,6 +1042,7 @@ __device__ __forceinline__ void wave_finalize(const StreamArgs& a, const RowPlan
     bool keep = has;
     float p = 0.0f;
     bool have = nk > 0 && wave_softmax(v, keep, p, wv, st.expT);
+    HSAMP_PHASE(8192 + r, 7);
     bool fresh = true;
     if (have && (P.flags & RF_TOPP)) {
         // sampler.cpp:146-164: order by (p desc, index asc), float running sum;
@@ -1082,9 +1084,11 @@ __device__ __forceinline__ void wave_finalize(const StreamArgs& a, const RowPlan
     const u64 km = have ? __ballot(keep) : 0ull;
     if (have) {
         // sampler.cpp:178-182 / discrete_distribution: double sum, q, partial sums
+        HSAMP_PHASE(8192 + r, 8);
         const double pd = keep ? (double)p : 0.0;
         const double S = wave_seq_sum_d(pd, wv);
         const double q = keep ? pd / S : 0.0;
+        HSAMP_PHASE(8192 + r, 9);
         int32_t t = V - 1;
         double near = 1.0;
         if (single) {
@@ -1105,6 +1109,7 @@ __device__ __forceinline__ void wave_finalize(const StreamArgs& a, const RowPlan
             }
         }
         if (near <= 1e-6) rflags |= ROWF_CDF_NEAR;
+        HSAMP_PHASE(8192 + r, 10);
         tok = t;
         const int pos = __popcll(km & ((1ull << lane) - 1ull));
         if (keep) {
@@ -1573,7 +1578,7 @@ template <int DT, bool VEC, bool PEN, bool MASK>
 __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan& P, int r, int lo, int hi,
                                              const uint4 (&raw)[Tile<DT>::NCH], u64* out, int64_t slot,
                                              bool last_slice, bool pen, bool mk, const int32_t (&pre)[8],
-                                             unsigned char* smem, Shared& st) {
+                                             int pbase, unsigned char* smem, Shared& st) {
     using T = Tile<DT>;
     const int tid = threadIdx.x, lane = lane_id();
     uint16_t* cnt = reinterpret_cast<uint16_t*>(smem);
@@ -1620,9 +1625,9 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
         uint32_t* cw = reinterpret_cast<uint32_t*>(smem);
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-            const int p = p0 + q * kBlock + tid;
+            const int p = pbase + q * kBlock + tid;   // pre[q]'s history position
             const int32_t t = pre[q];
-            if (p < L && t >= lo && t < mhi) {
+            if (p >= p0 && p < L && t >= lo && t < mhi) {
                 const int o = t - lo;
                 const uint32_t sh = (uint32_t)(o & 1) << 4;
                 if (p >= L - P.fp_win) atomicAdd(&cw[o >> 1], 1u << sh);
@@ -1793,6 +1798,16 @@ __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
     // before the tile (the mask words then wait for nothing else)
     RowPlan P;
     if (EX) P = a.plans[r];
+    // exact lists with short history rows: the whole row goes out first, so
+    // that it returns ahead of the tile whatever the plan's latency
+    int32_t pre[8];
+    const bool hd = EX && PEN && a.hist_direct != 0;
+    if (hd) {
+        const int32_t* h0 = a.hist + (int64_t)r * a.hist_stride;
+        const int hs1 = (int)a.hist_stride - 1;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) pre[q] = h0[min(q * kBlock + tid, hs1)];
+    }
     // (MASK launches may carry no mask: the general instantiations for
     // unaligned rows take MASK = true; the mask words are then all ones)
     const bool mk = MASK && a.mask != nullptr;
@@ -1805,18 +1820,22 @@ __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
         if (P.flags & RF_FULL) return;                     // k_full's row
         if (((P.flags & RF_GREEDY) != 0) != GR) return;    // the other kernel's row
     }
-    const bool pen = PEN && (P.flags & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) != 0;
+    // (flag mode: sampling rows stream without penalty marks -- k_merge finds
+    // their penalised ids -- also in the instantiations for unaligned rows,
+    // which take PEN = true for every batch)
+    const bool pen = PEN && (P.flags & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) != 0 && (GR || EX || !a.pen_flag);
     const bool masked = MASK && (P.flags & RF_MASK) != 0;
 
     // The history window goes out next (before the first tile when that has
     // not gone yet). Branch-free: clamped loads (pre[q] holds position
     // p0 + q * kBlock + tid, used only below L), so nothing here waits.
-    int32_t pre[8];
     const int L = P.hist_len, p0 = L - P.scan_len;
     const int32_t* hrow = a.hist + (int64_t)r * a.hist_stride;
+    if (!hd) {
 #pragma unroll
-    for (int q = 0; q < 8; ++q) pre[q] = -1;
-    if (PEN && pen && L > 0) {
+        for (int q = 0; q < 8; ++q) pre[q] = -1;
+    }
+    if (!hd && PEN && pen && L > 0) {
 #pragma unroll
         for (int q = 0; q < 8; ++q) pre[q] = hrow[max(0, min(p0 + q * kBlock + tid, L - 1))];
     }
@@ -1837,7 +1856,7 @@ __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
         const int64_t slot = (int64_t)r * a.nslices + s;
         u64* out = a.cand + slot * a.cand_cap;
         stream_exact<DT, VEC, PEN, MASK>(a, P, r, lo, hi, raw, out, slot, VEC && s == a.nslices - 1, pen, mk, pre,
-                                         smem, st);
+                                         hd ? 0 : p0, smem, st);
         return;
     }
     stream_setup<PEN, MASK>(a, P, r, lo, hi, GR, pen, masked, p0, L, hrow, pbm, pbm + a.bitmap_words, st);
@@ -2881,11 +2900,11 @@ __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
 //  - The slice counts, a window of W entries of every slice's list (NW per
 //    thread; entry g is slice g / W, position g % W), the plan and u are
 //    requested together.
-//  - Bound: the k-th largest of the 256 lane maxima with its low 16 bits
-//    cleared. Every lane maximum is a candidate of its own, so this is a
-//    lower bound of the row's k-th largest key. The candidates at or above it
-//    are ranked exactly: by wave 0 when at most 128, else by the block after a
-//    radix compaction to the k largest when more than 256.
+//  - Selection: the candidates' key range gives the bits they all share; a
+//    256-bin LDS histogram of the next 8 bits finds the bin holding the k-th
+//    largest key, and the candidates in it or above are ranked exactly: by
+//    wave 0 when at most 128, else by the block (after a radix compaction to
+//    the k largest when more than 256).
 //  - A list longer than its window (ties, flat rows) takes the buffer path.
 template <int NW>
 __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
@@ -2938,6 +2957,7 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
         for (int i = 0; i < 32; ++i) e = (tid == i) ? kExpT[i] : e;
         st.expT[tid] = e;
     }
+    st.hist[tid] = 0u;
     __syncthreads();
     HSAMP_PHASE(8192 + r, 1);
     if (tid < S) {
@@ -2984,21 +3004,64 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
         select_and_finalize(sa, sP, r, list, f, st, rflags);
         return;
     }
-    st.hist[tid] = lm;
-    __syncthreads();
-    HSAMP_PHASE(8192 + r, 2);
-    if (tid < 64) {
-        const uint32_t g4[4] = {st.hist[lane], st.hist[lane + 64], st.hist[lane + 128], st.hist[lane + 192]};
-        const uint32_t bound = wave_kth_bound16(g4, 4, k);
-        if (lane == 0) st.twave[0] = bound;
+    // The k-th largest key's 8-bit bin under the prefix every candidate
+    // shares (the block's key range), from a 256-bin LDS histogram; the
+    // candidates in that bin or above go to the list.
+    uint32_t kmn = 0xFFFFFFFFu;
+#pragma unroll
+    for (int j = 0; j < NW; ++j)
+        if (win[j] != 0ull) kmn = min(kmn, (uint32_t)(win[j] >> 32));
+    uint32_t kmx = lm;
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) {
+        kmn = min(kmn, (uint32_t)__shfl_xor((int)kmn, d, 64));
+        kmx = max(kmx, (uint32_t)__shfl_xor((int)kmx, d, 64));
+    }
+    if (lane == 0) {
+        st.twave[wave_id()] = kmn;
+        st.minv_w[wave_id()] = kmx;
     }
     __syncthreads();
-    const uint32_t Lk = max(st.twave[0], (uint32_t)(kThetaFloor >> 32));
+    HSAMP_PHASE(8192 + r, 2);
+    kmn = st.twave[0];
+    kmx = (uint32_t)st.minv_w[0];
+#pragma unroll
+    for (int i = 1; i < kBlock / 64; ++i) {
+        kmn = min(kmn, st.twave[i]);
+        kmx = max(kmx, (uint32_t)st.minv_w[i]);
+    }
+    const int hb = (kmx > kmn) ? 31 - __clz((int)(kmn ^ kmx)) : 0;
+    const int shift = max(0, hb - 7);
+#pragma unroll
+    for (int j = 0; j < NW; ++j)
+        if (win[j] != 0ull) atomicAdd(&st.hist[((uint32_t)(win[j] >> 32) >> shift) & 255u], 1u);
+    __syncthreads();
+    if (tid < 64) {
+        // bins from the top: lane l holds 255-4l .. 252-4l
+        const int c0 = st.hist[255 - 4 * lane], c1 = st.hist[254 - 4 * lane];
+        const int c2 = st.hist[253 - 4 * lane], c3 = st.hist[252 - 4 * lane];
+        const int s4 = c0 + c1 + c2 + c3;
+        int incl = s4;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int y = __shfl_up(incl, d, 64);
+            if (lane >= d) incl += y;
+        }
+        const int excl = incl - s4;
+        if (lane == 0) st.sel_d = 0;   // fewer than k candidates: all of them
+        if (excl < k && k <= incl) {
+            const int q = (excl + c0 >= k) ? 0 : (excl + c0 + c1 >= k) ? 1 : (excl + c0 + c1 + c2 >= k) ? 2 : 3;
+            st.sel_d = 255 - 4 * lane - q;
+        }
+    }
+    __syncthreads();
+    const uint32_t bstar = (uint32_t)st.sel_d;
     {
-        // the candidates at or above the bound, packed into the list
+        // the candidates in the k-th's bin or above, packed into the list
         uint32_t sv = 0u;
 #pragma unroll
-        for (int j = 0; j < NW; ++j) sv |= (win[j] != 0ull && (uint32_t)(win[j] >> 32) >= Lk) ? (1u << j) : 0u;
+        for (int j = 0; j < NW; ++j)
+            sv |= (win[j] != 0ull && (((uint32_t)(win[j] >> 32) >> shift) & 255u) >= bstar) ? (1u << j) : 0u;
         const int cnt = __popc(sv);
         int incl = cnt;
 #pragma unroll

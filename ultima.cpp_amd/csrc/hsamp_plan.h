@@ -123,6 +123,8 @@ struct StreamArgs {
                                 // before temperature (penalties applied), k_pick merges them
     int32_t mbm_off;            // exact lists: words from the LDS base to the slice's mask words
     int32_t stage_off;          // exact lists: bytes from the LDS base to the staged chunks
+    int32_t hist_direct;        // exact lists: every history row fits 8 * kBlock ids; k_stream
+                                // loads whole rows before the tile, without waiting for the plan
     float* fullv;               // [rows * vocab] k_full: transformed logits (-inf once removed)
     float* fullp;               // [rows * vocab] k_full: probabilities
     uint32_t* fullk;            // [rows * 2 * full_p2] k_full: probability keys by bucket, sort scratch

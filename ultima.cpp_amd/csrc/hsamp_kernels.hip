@@ -932,6 +932,28 @@ __device__ __forceinline__ double wave_seq_prefix_d(double x, u64* wv) {
     return mine;
 }
 
+// Tree scans across the wave. Their sums are associated differently from
+// the reference's sequential ones, so only decisions taken with a wide
+// margin come from them.
+__device__ __forceinline__ double wave_tree_prefix_d(double x) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const double y = __shfl_up(x, d, 64);
+        if (lane >= d) x = x + y;
+    }
+    return x;
+}
+__device__ __forceinline__ float wave_tree_prefix_f(float x) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const float y = __shfl_up(x, d, 64);
+        if (lane >= d) x = x + y;
+    }
+    return x;
+}
+
 // softmax_probs (sampler.cpp:124-142) over the kept lanes of one wave; lanes
 // are in index order. The float denominator is the index-order sequential sum.
 // Returns false when nothing is kept.
@@ -1051,7 +1073,20 @@ __device__ __forceinline__ void wave_finalize(const StreamArgs& a, const RowPlan
         const u64 srt = wave_sort_desc(key, wv);
         const bool real = srt > 0xFFFFFFFFull;
         const float ps = real ? key_to_float((uint32_t)(srt >> 32)) : 0.0f;
-        const float cum = wave_seq_prefix_f(ps, wv);
+        // the first sorted entry whose running float sum reaches top_p: from
+        // a tree prefix (within 5e-6 of the sequential sums of <= 64 values
+        // up to 1) when the decision and the TOPP_NEAR flag are clear of it
+        // by 1e-5 on both sides, else from the reference's sequential sums
+        float cum = wave_tree_prefix_f(ps);
+        {
+            const u64 h0 = __ballot(real && cum >= P.top_p);
+            const int c0 = (h0 != 0ull) ? __ffsll((long long)h0) - 1 : 64;
+            const float at = (c0 < 64) ? readlane_f(cum, c0) : 0.0f;
+            const float before = (c0 > 0) ? readlane_f(cum, min(c0, 64) - 1) : -1.0f;
+            const bool clear = (c0 < 64 ? fabsf(at - P.top_p) > 1e-5f : true) &&
+                               (c0 > 0 ? fabsf(before - P.top_p) > 1e-5f : true);
+            if (!clear) cum = wave_seq_prefix_f(ps, wv);
+        }
         const u64 hit = __ballot(real && cum >= P.top_p);
         if (hit != 0ull) {
             const int cutoff = __ffsll((long long)hit);   // entries kept in sorted order
@@ -1096,7 +1131,21 @@ __device__ __forceinline__ void wave_finalize(const StreamArgs& a, const RowPlan
         } else if (!(u > 0.0)) {
             t = 0;
         } else {
-            const double cp = wave_seq_prefix_d(q, wv);
+            // the partial sums from a tree prefix (within 1e-14 of the
+            // sequential ones) when every comparison that decides the token
+            // and the CDF_NEAR flag is clear of u by 2e-6, else the
+            // reference's sequential sums
+            double cp = wave_tree_prefix_d(q);
+            {
+                const double cja = (keep && (int32_t)id == V - 1) ? 1.0 : cp;
+                const u64 h0 = __ballot(keep && cja >= u);
+                const int j0 = (h0 != 0ull) ? __ffsll((long long)h0) - 1 : 64;
+                const double at = (j0 < 64) ? readlane_d(cja, j0) : readlane_d(cp, 63);
+                const double before = (j0 > 0) ? readlane_d(cp, min(j0, 64) - 1) : -1.0;
+                const bool clear = fabs(at - u) > 2e-6 && (j0 > 0 ? fabs(before - u) > 2e-6 : true) &&
+                                   (j0 < 64 ? true : fabs(1.0 - u) > 2e-6);
+                if (!clear) cp = wave_seq_prefix_d(q, wv);
+            }
             const double cj = (keep && (int32_t)id == V - 1) ? 1.0 : cp;
             const u64 hit = __ballot(keep && cj >= u);
             if (hit != 0ull) {
@@ -1663,39 +1712,44 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
     for (int i = 1; i < kBlock / 64; ++i) thr = min(thr, st.twave[i]);
     thr = max(thr, kFloor);
     const float inv_t = P.inv_temp;
-    const uint32_t R = raw_edge(max(scaled_key(thr, inv_t), kFloor), inv_t, P.temp);
+    // R: thr itself when the raw key below it scales below ths (the usual
+    // case), else the search
+    const uint32_t sthr = scaled_key(thr, inv_t);
+    uint32_t R = thr;
+    if (!(sthr >= kFloor && (thr == kFloor || scaled_key(thr - 1u, inv_t) < sthr)))
+        R = raw_edge(max(sthr, kFloor), inv_t, P.temp);
+    HSAMP_PHASE(slot, 7);
 
     // C, D. the ids whose final raw key lies in [Rlo, Rhi)
     auto pass = [&](uint32_t Rlo, uint32_t Rhi) {
-        uint32_t csel = 0u;
+        // positions in (chunk, lane) order from one ballot per chunk and a
+        // single LDS atomic per wave
+        int pj[T::NCH];
+        int wtot = 0;
 #pragma unroll
-        for (int j = 0; j < T::NCH; ++j) csel |= (ck[j] >= Rlo) ? (1u << j) : 0u;
-        const int c0 = __popc(csel);
-        int incl = c0;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const int y = __shfl_up(incl, d, 64);
-            if (lane >= d) incl += y;
+        for (int j = 0; j < T::NCH; ++j) {
+            const u64 m = __ballot(ck[j] >= Rlo);
+            pj[j] = (ck[j] >= Rlo) ? wtot + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u))
+                                   : -1;
+            wtot += __popcll(m);
         }
-        const int wtot = __shfl(incl, 63, 64);
         int base = 0;
-        if (lane == 63 && wtot > 0) base = atomicAdd(&st.nst, wtot);
-        const int pos0 = __shfl(base, 63, 64) + incl - c0;
+        if (lane == 0 && wtot > 0) base = atomicAdd(&st.nst, wtot);
+        base = __builtin_amdgcn_readfirstlane(__shfl(base, 0, 64));
         auto stage = [&](int rb) {
-            int p = pos0;
 #pragma unroll
             for (int j = 0; j < T::NCH; ++j) {
-                if ((csel >> j) & 1u) {
-                    if (p >= rb && p < rb + kStageCap) {
-                        sdat[p - rb] = raw[j];
-                        sidx[p - rb] = lo + (j * kBlock + tid) * T::VW;
-                    }
-                    ++p;
+                const int p = base + pj[j] - rb;
+                if (pj[j] >= 0 && p >= 0 && p < kStageCap) {
+                    sdat[p] = raw[j];
+                    sidx[p] = lo + (j * kBlock + tid) * T::VW;
                 }
             }
         };
         stage(0);
         __syncthreads();
+        HSAMP_PHASE(slot, 8);
         const int nst = st.nst;
         bool nanp = false;
         for (int rb = 0;;) {
@@ -1743,6 +1797,7 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
             if (kf >= Rlo && kf < Rhi) out[atomicAdd(&st.n, 1)] = comp(kf, tt_id);
         }
         if (nanp) atomicOr(&st.flags, 1);
+        HSAMP_PHASE(slot, 9);
         __syncthreads();
     };
     pass(R, 0xFFFFFFFFu);
@@ -2910,7 +2965,7 @@ template <int NW>
 __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ Shared st;
-    __shared__ StreamArgs sa;
+    __shared__ StreamArgs sa;   // the buffer path's copies for select_and_finalize (not inlined)
     __shared__ RowPlan sP;
     const int tid = threadIdx.x, lane = lane_id();
     const int S = a.nslices, W = a.win;
@@ -2941,13 +2996,11 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
     }
     const RowPlan P = a.plans[r];
     const double ur = a.u[r];
+    // (nothing here waits for a load: u goes to LDS once the lists are in)
     if (tid == 0) {
         st.flags = 0;
         st.n = 0;
         st.theta = kThetaFloor;
-        st.u = ur;
-        sa = a;
-        sP = P;
     }
     if (tid < 32) {
         // expf's table from immediates (an indexed read would wait for every
@@ -2999,6 +3052,14 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
                 offer_regs<8>(list, ovf, a.buf_cap, k, c, st);
             }
         }
+        // LDS copies of the arguments and the plan, one dword per thread
+        // (a struct copy would go through per-lane scratch)
+        static_assert(sizeof(StreamArgs) % 4 == 0 && sizeof(StreamArgs) / 4 <= kBlock, "StreamArgs copy");
+        const uint32_t* kp = (const uint32_t*)__builtin_amdgcn_kernarg_segment_ptr();
+        if (tid < (int)(sizeof(StreamArgs) / 4)) reinterpret_cast<uint32_t*>(&sa)[tid] = kp[tid];
+        if (tid < (int)(sizeof(RowPlan) / 4))
+            reinterpret_cast<uint32_t*>(&sP)[tid] = reinterpret_cast<const uint32_t*>(a.plans + r)[tid];
+        if (tid == 0) st.u = ur;
         __syncthreads();
         FinLds f{};
         select_and_finalize(sa, sP, r, list, f, st, rflags);
@@ -3057,28 +3118,29 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
     __syncthreads();
     const uint32_t bstar = (uint32_t)st.sel_d;
     {
-        // the candidates in the k-th's bin or above, packed into the list
-        uint32_t sv = 0u;
+        // the candidates in the k-th's bin or above, packed into the list in
+        // (slot, lane) order: one ballot per slot, one LDS atomic per wave
+        int pj[NW];
+        int wtot = 0;
 #pragma unroll
-        for (int j = 0; j < NW; ++j)
-            sv |= (win[j] != 0ull && (((uint32_t)(win[j] >> 32) >> shift) & 255u) >= bstar) ? (1u << j) : 0u;
-        const int cnt = __popc(sv);
-        int incl = cnt;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const int y = __shfl_up(incl, d, 64);
-            if (lane >= d) incl += y;
+        for (int j = 0; j < NW; ++j) {
+            const bool in = win[j] != 0ull && (((uint32_t)(win[j] >> 32) >> shift) & 255u) >= bstar;
+            const u64 m = __ballot(in);
+            pj[j] = in ? wtot + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                                __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u))
+                       : -1;
+            wtot += __popcll(m);
         }
-        const int wtot = __shfl(incl, 63, 64);
         if (wtot > 0) {
             int base = 0;
-            if (lane == 63) base = atomicAdd(&st.n, wtot);
-            int pos = __shfl(base, 63, 64) + incl - cnt;
+            if (lane == 0) base = atomicAdd(&st.n, wtot);
+            base = __builtin_amdgcn_readfirstlane(__shfl(base, 0, 64));
 #pragma unroll
             for (int j = 0; j < NW; ++j)
-                if ((sv >> j) & 1u) list[pos++] = win[j];
+                if (pj[j] >= 0) list[base + pj[j]] = win[j];
         }
     }
+    if (tid == 0) st.u = ur;
     __syncthreads();
     HSAMP_PHASE(8192 + r, 3);
     int n = st.n;
@@ -3105,7 +3167,7 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
         const u64 c = (lane < nk) ? st.wv[lane] : 0ull;
         wave_sync();
         HSAMP_PHASE(8192 + r, 4);
-        wave_finalize(sa, sP, r, c, nk, rflags, st);
+        wave_finalize(a, P, r, c, nk, rflags, st);
         HSAMP_PHASE(8192 + r, 5);
         return;
     }
@@ -3117,7 +3179,7 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
     if (tid >= 64) return;
     const int nk = min(k, n);
     const u64 c = (lane < nk) ? st.wv[lane] : 0ull;
-    wave_finalize(sa, sP, r, c, nk, rflags, st);
+    wave_finalize(a, P, r, c, nk, rflags, st);
 }
 
 // ---- writeback -------------------------------------------------------------------

@@ -77,6 +77,67 @@ __device__ __forceinline__ int32_t comp_idx(u64 c) { return (int32_t)(~(uint32_t
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
+// ---- wave-wide reductions and scans through DPP ---------------------------------
+// Shifts within 16-lane rows (row_shr 1, 2, 4, 8), then row_bcast:15 and
+// row_bcast:31 across rows: an inclusive scan over the 64 lanes in six VALU
+// steps, without the LDS crossbar that shuffles use. Lanes whose source lies
+// outside the row keep `id` (the operation's identity); lane 63 ends with the
+// whole wave's result.
+template <int CTRL, int ROWM>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t id, uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)id, (int)x, CTRL, ROWM, 0xF, false);
+}
+template <typename F>
+__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t x, uint32_t id, F op) {
+    x = op(x, dpp_u32<0x111, 0xF>(id, x));
+    x = op(x, dpp_u32<0x112, 0xF>(id, x));
+    x = op(x, dpp_u32<0x114, 0xF>(id, x));
+    x = op(x, dpp_u32<0x118, 0xF>(id, x));
+    x = op(x, dpp_u32<0x142, 0xA>(id, x));
+    x = op(x, dpp_u32<0x143, 0xC>(id, x));
+    return x;
+}
+__device__ __forceinline__ int wave_incl_sum_i(int x) {
+    return (int)wave_scan_u32((uint32_t)x, 0u, [](uint32_t a, uint32_t b) { return a + b; });
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+    x = wave_scan_u32(x, 0u, [](uint32_t a, uint32_t b) { return max(a, b); });
+    return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
+    x = wave_scan_u32(x, 0xFFFFFFFFu, [](uint32_t a, uint32_t b) { return min(a, b); });
+    return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+}
+template <int CTRL, int ROWM>
+__device__ __forceinline__ float dpp_f32(float id, float x) {
+    return __uint_as_float(dpp_u32<CTRL, ROWM>(__float_as_uint(id), __float_as_uint(x)));
+}
+template <int CTRL, int ROWM>
+__device__ __forceinline__ double dpp_f64(double x) {
+    const uint64_t b = (uint64_t)__double_as_longlong(x);
+    const uint32_t lo = dpp_u32<CTRL, ROWM>(0u, (uint32_t)b), hi = dpp_u32<CTRL, ROWM>(0u, (uint32_t)(b >> 32));
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+// Inclusive scans (tree association: only for decisions taken with a margin).
+__device__ __forceinline__ float wave_tree_prefix_f(float x) {
+    x = x + dpp_f32<0x111, 0xF>(0.0f, x);
+    x = x + dpp_f32<0x112, 0xF>(0.0f, x);
+    x = x + dpp_f32<0x114, 0xF>(0.0f, x);
+    x = x + dpp_f32<0x118, 0xF>(0.0f, x);
+    x = x + dpp_f32<0x142, 0xA>(0.0f, x);
+    x = x + dpp_f32<0x143, 0xC>(0.0f, x);
+    return x;
+}
+__device__ __forceinline__ double wave_tree_prefix_d(double x) {
+    x = x + dpp_f64<0x111, 0xF>(x);
+    x = x + dpp_f64<0x112, 0xF>(x);
+    x = x + dpp_f64<0x114, 0xF>(x);
+    x = x + dpp_f64<0x118, 0xF>(x);
+    x = x + dpp_f64<0x142, 0xA>(x);
+    x = x + dpp_f64<0x143, 0xC>(x);
+    return x;
+}
+
 struct Shared {
     u64 theta;          // current survival threshold (composite)
     u64 minv;
@@ -784,9 +845,14 @@ __device__ __forceinline__ double readlane_d(double v, int l) {
     return bits_to_f64(((uint64_t)hi << 32) | lo);
 }
 __device__ __forceinline__ float wave_max_f(float v) {
-#pragma unroll
-    for (int d = 32; d > 0; d >>= 1) v = fmaxf(v, __shfl_xor(v, d, 64));
-    return v;
+    // (no NaN reaches it)
+    v = fmaxf(v, dpp_f32<0x111, 0xF>(-__builtin_inff(), v));
+    v = fmaxf(v, dpp_f32<0x112, 0xF>(-__builtin_inff(), v));
+    v = fmaxf(v, dpp_f32<0x114, 0xF>(-__builtin_inff(), v));
+    v = fmaxf(v, dpp_f32<0x118, 0xF>(-__builtin_inff(), v));
+    v = fmaxf(v, dpp_f32<0x142, 0xA>(-__builtin_inff(), v));
+    v = fmaxf(v, dpp_f32<0x143, 0xC>(-__builtin_inff(), v));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 // Orders the wave's LDS accesses around a cross-lane exchange. LDS operations
@@ -932,27 +998,6 @@ __device__ __forceinline__ double wave_seq_prefix_d(double x, u64* wv) {
     return mine;
 }
 
-// Tree scans across the wave. Their sums are associated differently from
-// the reference's sequential ones, so only decisions taken with a wide
-// margin come from them.
-__device__ __forceinline__ double wave_tree_prefix_d(double x) {
-    const int lane = lane_id();
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const double y = __shfl_up(x, d, 64);
-        if (lane >= d) x = x + y;
-    }
-    return x;
-}
-__device__ __forceinline__ float wave_tree_prefix_f(float x) {
-    const int lane = lane_id();
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const float y = __shfl_up(x, d, 64);
-        if (lane >= d) x = x + y;
-    }
-    return x;
-}
 
 // softmax_probs (sampler.cpp:124-142) over the kept lanes of one wave; lanes
 // are in index order. The float denominator is the index-order sequential sum.
@@ -1736,7 +1781,7 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
         }
         int base = 0;
         if (lane == 0 && wtot > 0) base = atomicAdd(&st.nst, wtot);
-        base = __builtin_amdgcn_readfirstlane(__shfl(base, 0, 64));
+        base = __builtin_amdgcn_readfirstlane(base);
         auto stage = [&](int rb) {
 #pragma unroll
             for (int j = 0; j < T::NCH; ++j) {
@@ -3072,12 +3117,8 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
 #pragma unroll
     for (int j = 0; j < NW; ++j)
         if (win[j] != 0ull) kmn = min(kmn, (uint32_t)(win[j] >> 32));
-    uint32_t kmx = lm;
-#pragma unroll
-    for (int d = 32; d > 0; d >>= 1) {
-        kmn = min(kmn, (uint32_t)__shfl_xor((int)kmn, d, 64));
-        kmx = max(kmx, (uint32_t)__shfl_xor((int)kmx, d, 64));
-    }
+    kmn = wave_min_u32(kmn);
+    uint32_t kmx = wave_max_u32(lm);
     if (lane == 0) {
         st.twave[wave_id()] = kmn;
         st.minv_w[wave_id()] = kmx;
@@ -3102,12 +3143,7 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
         const int c0 = st.hist[255 - 4 * lane], c1 = st.hist[254 - 4 * lane];
         const int c2 = st.hist[253 - 4 * lane], c3 = st.hist[252 - 4 * lane];
         const int s4 = c0 + c1 + c2 + c3;
-        int incl = s4;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const int y = __shfl_up(incl, d, 64);
-            if (lane >= d) incl += y;
-        }
+        const int incl = wave_incl_sum_i(s4);
         const int excl = incl - s4;
         if (lane == 0) st.sel_d = 0;   // fewer than k candidates: all of them
         if (excl < k && k <= incl) {
@@ -3134,7 +3170,7 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
         if (wtot > 0) {
             int base = 0;
             if (lane == 0) base = atomicAdd(&st.n, wtot);
-            base = __builtin_amdgcn_readfirstlane(__shfl(base, 0, 64));
+            base = __builtin_amdgcn_readfirstlane(base);
 #pragma unroll
             for (int j = 0; j < NW; ++j)
                 if (pj[j] >= 0) list[base + pj[j]] = win[j];

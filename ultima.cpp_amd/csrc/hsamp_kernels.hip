@@ -1305,12 +1305,11 @@ __device__ __forceinline__ uint32_t wave_kth_bound16(const uint32_t (&g)[4], int
     for (int b = 31; b >= 16; --b) {
         const uint32_t bit = 1u << b;
         int cnt = 0;
+        // under the prefix with this bit set: one AND and one compare
+        const uint32_t kb = known | bit, pb = prefix | bit;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            if (i < G) {
-                const bool m = ((g[i] & known) == prefix) && (g[i] & bit);
-                cnt += __popcll(__ballot(m));
-            }
+            if (i < G) cnt += __popcll(__ballot((g[i] & kb) == pb));
         }
         if (cnt >= need) prefix |= bit;
         else need -= cnt;
@@ -1717,11 +1716,12 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
         const int L = P.hist_len, p0 = L - P.scan_len;
         const int mhi = min(a.vocab, lo + a.slice_len);
         uint32_t* cw = reinterpret_cast<uint32_t*>(smem);
+        const uint32_t wl = (uint32_t)(L - p0), sl = (uint32_t)(mhi - lo);
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
             const int p = pbase + q * kBlock + tid;   // pre[q]'s history position
             const int32_t t = pre[q];
-            if (p >= p0 && p < L && t >= lo && t < mhi) {
+            if ((uint32_t)(p - p0) < wl && (uint32_t)(t - lo) < sl) {
                 const int o = t - lo;
                 const uint32_t sh = (uint32_t)(o & 1) << 4;
                 if (p >= L - P.fp_win) atomicAdd(&cw[o >> 1], 1u << sh);
@@ -1798,37 +1798,19 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
         const int nst = st.nst;
         bool nanp = false;
         for (int rb = 0;;) {
-            if (tid < nst - rb) {
-                const uint4 d = sdat[tid];
-                const int e0 = sidx[tid];
-                const int o = e0 - lo;
-                uint32_t mb = 0xFFFFFFFFu;
-                if (MASK) mb = mbm[o >> 5] >> (o & 31);
-                uint32_t hc[T::VW];
-#pragma unroll
-                for (int c = 0; c < T::VW; ++c) hc[c] = 0u;
-                if (PEN) {
-                    if (DT == 0) {
-                        const uint2 w = *reinterpret_cast<const uint2*>(cnt + o);
-                        hc[0] = w.x & 0xFFFFu;
-                        hc[1] = w.x >> 16;
-                        hc[2] = w.y & 0xFFFFu;
-                        hc[3] = w.y >> 16;
-                    } else {
-                        const uint4 w = *reinterpret_cast<const uint4*>(cnt + o);
-                        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-                        for (int c = 0; c < T::VW; ++c) hc[c] = (c & 1) ? (ww[c >> 1] >> 16) : (ww[c >> 1] & 0xFFFFu);
-                    }
-                }
-#pragma unroll
-                for (int c = 0; c < T::VW; ++c) {
-                    float x = elem<DT>(d, c);
-                    if (MASK && !((mb >> c) & 1u)) x = -__builtin_inff();
-                    if ((VEC || e0 + c < hi) && raw_key(x) >= Rlo) {
-                        const uint32_t kf = final_raw_key(x, e0 + c, PEN ? hc[c] : 0u, a, P, nanp);
-                        if (kf >= Rlo && kf < Rhi) out[atomicAdd(&st.n, 1)] = comp(kf, e0 + c);
-                    }
+            // VW threads per staged chunk, one element each
+            for (int e = tid; e < min(kStageCap, nst - rb) * T::VW; e += kBlock) {
+                const int ci = e / T::VW, c = e % T::VW;
+                const int e0 = sidx[ci];
+                const int t = e0 + c;
+                const int o = t - lo;
+                const uint32_t wsel = reinterpret_cast<const uint32_t*>(&sdat[ci])[DT == 0 ? c : (c >> 1)];
+                float x = (DT == 0) ? __uint_as_float(wsel)
+                                    : __uint_as_float((c & 1) ? (wsel & 0xFFFF0000u) : (wsel << 16));
+                if (MASK && !((mbm[o >> 5] >> (o & 31)) & 1u)) x = -__builtin_inff();
+                if ((VEC || t < hi) && raw_key(x) >= Rlo) {
+                    const uint32_t kf = final_raw_key(x, t, PEN ? (uint32_t)cnt[o] : 0u, a, P, nanp);
+                    if (kf >= Rlo && kf < Rhi) out[atomicAdd(&st.n, 1)] = comp(kf, t);
                 }
             }
             rb += kStageCap;
@@ -1903,10 +1885,11 @@ __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
     int32_t pre[8];
     const bool hd = EX && PEN && a.hist_direct != 0;
     if (hd) {
-        const int32_t* h0 = a.hist + (int64_t)r * a.hist_stride;
-        const int hs1 = (int)a.hist_stride - 1;
+        // one buffer resource over the row: positions past hist_stride read 0
+        const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<int32_t*>(a.hist + (int64_t)r * a.hist_stride), (short)0, (int)a.hist_stride * 4, 0x00020000);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) pre[q] = h0[min(q * kBlock + tid, hs1)];
+        for (int q = 0; q < 8; ++q) pre[q] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(hr, tid * 4, q * kBlock * 4, 0);
     }
     // (MASK launches may carry no mask: the general instantiations for
     // unaligned rows take MASK = true; the mask words are then all ones)

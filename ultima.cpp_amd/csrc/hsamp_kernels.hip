@@ -1770,13 +1770,14 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
         // positions in (chunk, lane) order from one ballot per chunk and a
         // single LDS atomic per wave
         int pj[T::NCH];
+        uint32_t csel = 0u;
         int wtot = 0;
 #pragma unroll
         for (int j = 0; j < T::NCH; ++j) {
-            const u64 m = __ballot(ck[j] >= Rlo);
-            pj[j] = (ck[j] >= Rlo) ? wtot + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
-                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u))
-                                   : -1;
+            const bool in = ck[j] >= Rlo;
+            const u64 m = __ballot(in);
+            pj[j] = wtot + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+            csel |= (uint32_t)in << j;
             wtot += __popcll(m);
         }
         int base = 0;
@@ -1786,7 +1787,7 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
 #pragma unroll
             for (int j = 0; j < T::NCH; ++j) {
                 const int p = base + pj[j] - rb;
-                if (pj[j] >= 0 && p >= 0 && p < kStageCap) {
+                if (((csel >> j) & 1u) && (uint32_t)p < (uint32_t)kStageCap) {
                     sdat[p] = raw[j];
                     sidx[p] = lo + (j * kBlock + tid) * T::VW;
                 }
@@ -2985,9 +2986,11 @@ __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
 //    requested together.
 //  - Selection: the candidates' key range gives the bits they all share; a
 //    256-bin LDS histogram of the next 8 bits finds the bin holding the k-th
-//    largest key, and the candidates in it or above are ranked exactly: by
-//    wave 0 when at most 128, else by the block (after a radix compaction to
-//    the k largest when more than 256).
+//    largest key. The candidates above that bin are all kept; those in it (at
+//    most 64) are ranked among themselves (composite order, ties to the lower
+//    id) and the best join. A fuller bin sends every candidate in it or above
+//    to an exact rank: by wave 0 when at most 128, else by the block (after a
+//    radix compaction to the k largest when more than 256).
 //  - A list longer than its window (ties, flat rows) takes the buffer path.
 template <int NW>
 __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
@@ -3004,6 +3007,10 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
     const int r = r0 + (int)(blockIdx.x / kXcds);
     if (r >= r1) return;
     HSAMP_PHASE(8192 + r, 0);
+    // the plan and u first (scalar loads: the first barrier waits for them,
+    // so they go out ahead of the lists)
+    const RowPlan P = a.plans[r];
+    const double ur = a.u[r];
     const u64* cand = a.cand + (int64_t)r * S * a.cand_cap;
     const int cnt_raw = (tid < S) ? a.cand_n[(int64_t)r * S + tid] : 0;
     u64 win[NW];
@@ -3022,12 +3029,11 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
             win[j] = ((u64)v[1] << 32) | v[0];
         }
     }
-    const RowPlan P = a.plans[r];
-    const double ur = a.u[r];
     // (nothing here waits for a load: u goes to LDS once the lists are in)
     if (tid == 0) {
         st.flags = 0;
         st.n = 0;
+        st.nst = 0;
         st.theta = kThetaFloor;
     }
     if (tid < 32) {
@@ -3121,6 +3127,7 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
     for (int j = 0; j < NW; ++j)
         if (win[j] != 0ull) atomicAdd(&st.hist[((uint32_t)(win[j] >> 32) >> shift) & 255u], 1u);
     __syncthreads();
+    HSAMP_PHASE(8192 + r, 11);
     if (tid < 64) {
         // bins from the top: lane l holds 255-4l .. 252-4l
         const int c0 = st.hist[255 - 4 * lane], c1 = st.hist[254 - 4 * lane];
@@ -3135,41 +3142,75 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
         }
     }
     __syncthreads();
-    const uint32_t bstar = (uint32_t)st.sel_d;
+    HSAMP_PHASE(8192 + r, 12);
+    const uint32_t bstar = (uint32_t)__builtin_amdgcn_readfirstlane(st.sel_d);
     {
         // the candidates in the k-th's bin or above, packed into the list in
         // (slot, lane) order: one ballot per slot, one LDS atomic per wave
         int pj[NW];
+        uint32_t sel = 0u;
         int wtot = 0;
 #pragma unroll
         for (int j = 0; j < NW; ++j) {
-            const bool in = win[j] != 0ull && (((uint32_t)(win[j] >> 32) >> shift) & 255u) >= bstar;
+            const bool in = (win[j] != 0ull) & ((((uint32_t)(win[j] >> 32) >> shift) & 255u) >= bstar);
             const u64 m = __ballot(in);
-            pj[j] = in ? wtot + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
-                                                                __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u))
-                       : -1;
+            pj[j] = wtot + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+            sel |= (uint32_t)in << j;
             wtot += __popcll(m);
         }
-        if (wtot > 0) {
-            int base = 0;
-            if (lane == 0) base = atomicAdd(&st.n, wtot);
-            base = __builtin_amdgcn_readfirstlane(base);
+        int base = 0;
+        if (lane == 0 && wtot > 0) base = atomicAdd(&st.n, wtot);
+        base = __builtin_amdgcn_readfirstlane(base);
 #pragma unroll
-            for (int j = 0; j < NW; ++j)
-                if (pj[j] >= 0) list[base + pj[j]] = win[j];
-        }
+        for (int j = 0; j < NW; ++j)
+            if ((sel >> j) & 1u) list[base + pj[j]] = win[j];
     }
     if (tid == 0) st.u = ur;
     __syncthreads();
     HSAMP_PHASE(8192 + r, 3);
     int n = st.n;
     if (n <= 128) {
-        // wave 0 ranks the (distinct) entries exactly: rank = entries above
+        // Wave 0 holds the n entries (two per lane). Those above the k-th's
+        // bin are all in; the ones in it (bcnt) are packed aside, ranked among
+        // themselves (composite order, ties to the lower id) and the best
+        // bneed join. More than 64 in the bin: the full rank below.
         if (tid >= 64) return;
-        if (lane == 0) list[n] = 0ull;   // pad to pairs
-        wave_sync();
         const u64 m0 = (lane < n) ? list[lane] : 0ull;
         const u64 m1 = (lane + 64 < n) ? list[lane + 64] : 0ull;
+        const uint32_t b0 = ((uint32_t)(m0 >> 32) >> shift) & 255u, b1 = ((uint32_t)(m1 >> 32) >> shift) & 255u;
+        const bool a0 = (m0 != 0ull) & (b0 > bstar), a1 = (m1 != 0ull) & (b1 > bstar);
+        const bool i0 = (m0 != 0ull) & (b0 == bstar), i1 = (m1 != 0ull) & (b1 == bstar);
+        const u64 ma0 = __ballot(a0), ma1 = __ballot(a1), mi0 = __ballot(i0), mi1 = __ballot(i1);
+        const int above = __popcll(ma0) + __popcll(ma1);
+        const int bcnt = __popcll(mi0) + __popcll(mi1);
+        if (bcnt <= 64) {
+            const int bneed = k - above;
+            u64* bl = list + 128;   // the bin's entries, packed (after the n <= 128 entries)
+            auto mb = [&](u64 m) -> int {
+                return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+            };
+            if (i0) bl[mb(mi0)] = m0;
+            if (i1) bl[__popcll(mi0) + mb(mi1)] = m1;
+            wave_sync();
+            const u64 e = (lane < bcnt) ? bl[lane] : 0ull;
+            int q = 0;
+            for (int j = 0; j < bcnt; ++j) q += bl[j] > e;
+            wave_sync();
+            if (a0) st.wv[mb(ma0)] = m0;
+            if (a1) st.wv[__popcll(ma0) + mb(ma1)] = m1;
+            if (lane < bcnt && q < bneed) st.wv[above + q] = e;
+            wave_sync();
+            const int nk = min(k, above + min(bneed, bcnt));
+            const u64 c = (lane < nk) ? st.wv[lane] : 0ull;
+            wave_sync();
+            HSAMP_PHASE(8192 + r, 4);
+            wave_finalize(a, P, r, c, nk, rflags, st);
+            HSAMP_PHASE(8192 + r, 5);
+            return;
+        }
+        // wave 0 ranks the (distinct) entries exactly: rank = entries above
+        if (lane == 0) list[n] = 0ull;   // pad to pairs
+        wave_sync();
         int q0 = 0, q1 = 0;
         const ulonglong2* l2 = reinterpret_cast<const ulonglong2*>(list);
 #pragma unroll 4
@@ -3185,9 +3226,7 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
         const int nk = min(k, n);
         const u64 c = (lane < nk) ? st.wv[lane] : 0ull;
         wave_sync();
-        HSAMP_PHASE(8192 + r, 4);
         wave_finalize(a, P, r, c, nk, rflags, st);
-        HSAMP_PHASE(8192 + r, 5);
         return;
     }
     if (n > 256) {

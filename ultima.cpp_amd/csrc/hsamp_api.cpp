@@ -520,6 +520,8 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     if (const char* fs = std::getenv("ULTIMA_HSAMP_SLICES")) S = std::max(1, std::min(std::atoi(fs), kBlock));
     int slice_len = ((V + S - 1) / S + 31) & ~31;
     S = (V + slice_len - 1) / slice_len;
+    // block and row indices are divided by S with a 32-bit reciprocal (exact below 2^32 / S)
+    if ((uint64_t)(B + 2) * (uint64_t)S * (uint64_t)(S + kXcds) >= (1ull << 32)) return ULTIMA_HSAMP_ERR_CAPACITY;
     const int kmax = std::max(1, bl.kmax);
     const int buf_cap = std::max(512, next_pow2(2 * kmax));
     const int cand_cap = slice_len;                 // a slice's list holds all its ids
@@ -662,6 +664,7 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     a.cand_th = h->cand_n + h->cand_slots;
     a.win = win;
     a.win_magic = (uint32_t)((1ull << 32) / (uint64_t)win + 1);
+    a.ns_magic = S > 1 ? (uint32_t)((1ull << 32) / (uint64_t)S + 1) : 0u;   // S == 1: the kernels divide by 1 themselves
     a.dtype = b->dtype;
     a.fast = fast ? 1 : 0;
     a.pen_flag = (fast && pen_flag) ? 1 : 0;

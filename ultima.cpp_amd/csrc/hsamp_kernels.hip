@@ -1859,14 +1859,30 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
 // budget of five blocks per CU.
 // EX: exact lists (sampling rows only, see stream_exact); LDS then
 // [count entries (PEN), 2 B per slice id + 8][allowed-id mask words].
+// g / nslices for block and row indices (a 32-bit reciprocal; one slice per
+// row divides by 1, which the reciprocal cannot express)
+__device__ __forceinline__ int div_slices(int g, const StreamArgs& a) {
+    return a.nslices == 1 ? g : (int)__umulhi((uint32_t)g, a.ns_magic);
+}
+
 template <int DT, bool VEC, bool PEN, bool MASK, bool GR, bool EX = false>
 __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
     using T = Tile<DT>;
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ Shared st;
     const int tid = threadIdx.x;
-    const int logical = (int)(blockIdx.x % kXcds) * a.blocks_per_xcd + (int)(blockIdx.x / kXcds);
-    const int r = logical / a.nslices, s = logical % a.nslices;
+    uint32_t bid = blockIdx.x;
+    if constexpr (EX) {
+        // the launch arguments the first loads need, in registers together:
+        // one round of scalar loads instead of one per branch that uses them
+        // (an asm statement that reads them; it touches no memory)
+        __asm__("" : "+s"(bid)
+                : "s"(a.logits), "s"(a.logits_stride), "s"(a.hist), "s"(a.hist_stride), "s"(a.mask),
+                  "s"(a.mask_stride), "s"(a.plans), "s"(a.rows), "s"(a.vocab), "s"(a.nslices), "s"(a.slice_len),
+                  "s"(a.bitmap_words), "s"(a.blocks_per_xcd), "s"(a.ns_magic), "s"(a.vec_tail), "s"(a.hist_direct));
+    }
+    const int logical = (int)(bid % kXcds) * a.blocks_per_xcd + (int)(bid / kXcds);
+    const int r = div_slices(logical, a), s = logical - r * a.nslices;
     if (r >= a.rows) return;
     const int lo = s * a.slice_len;
     const int hi = min(a.vocab - (VEC ? a.vec_tail : 0), lo + a.slice_len);   // k_merge takes the ragged end
@@ -1877,12 +1893,12 @@ __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
     // complete in order); otherwise after the plan has said the row is ours.
     const bool early = EX || ((a.uniform >> (GR ? 0 : 1)) & 1) != 0;
     uint4 raw[T::NCH];
-    // exact lists: the plan's scalar load and the slice's mask words go out
-    // before the tile (the mask words then wait for nothing else)
+    // Exact lists: the history row, the slice's mask words and the tile go out
+    // first (their addresses come from the launch arguments alone) and the
+    // plan's scalar load after them: a wait for the plan placed ahead of the
+    // tile's loads would hold the whole slice back by one memory round trip.
     RowPlan P;
-    if (EX) P = a.plans[r];
-    // exact lists with short history rows: the whole row goes out first, so
-    // that it returns ahead of the tile whatever the plan's latency
+    // exact lists with short history rows: the whole row goes out first
     int32_t pre[8];
     const bool hd = EX && PEN && a.hist_direct != 0;
     if (hd) {
@@ -1899,7 +1915,8 @@ __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
     if (EX && mk && tid < a.bitmap_words)
         mw_pre = (lo + 32 * tid < hi) ? a.mask[(int64_t)r * a.mask_stride + (lo >> 5) + tid] : 0u;
     if (early) load_tile<DT, VEC>(rs, lo, raw);
-    if (!EX) P = a.plans[r];
+    if (EX) __builtin_amdgcn_sched_barrier(0);
+    P = a.plans[r];
     if (!early) {
         if (P.flags & RF_FULL) return;                     // k_full's row
         if (((P.flags & RF_GREEDY) != 0) != GR) return;    // the other kernel's row
@@ -2730,8 +2747,8 @@ __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
     // r * nslices / blocks_per_xcd).
     const int S = a.nslices, W = a.win;
     const int x = (int)(blockIdx.x % kXcds);
-    const int r0 = min(a.rows, (x * a.blocks_per_xcd + S - 1) / S);
-    const int r1 = min(a.rows, ((x + 1) * a.blocks_per_xcd + S - 1) / S);
+    const int r0 = min(a.rows, div_slices(x * a.blocks_per_xcd + S - 1, a));
+    const int r1 = min(a.rows, div_slices((x + 1) * a.blocks_per_xcd + S - 1, a));
     const int r = r0 + (int)(blockIdx.x / kXcds);
     if (r >= r1) return;
     // Flag-mode launches read the plan first and request the history window
@@ -2999,18 +3016,20 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
     __shared__ StreamArgs sa;   // the buffer path's copies for select_and_finalize (not inlined)
     __shared__ RowPlan sP;
     const int tid = threadIdx.x, lane = lane_id();
+    uint32_t bid = blockIdx.x;
+    // the launch arguments the first loads need, in registers together: one
+    // round of scalar loads instead of one per branch that uses them (an asm
+    // statement that reads them; it touches no memory)
+    __asm__("" : "+s"(bid)
+            : "s"(a.blocks_per_xcd), "s"(a.ns_magic), "s"(a.rows), "s"(a.nslices), "s"(a.win), "s"(a.cand),
+              "s"(a.cand_cap), "s"(a.cand_n), "s"(a.win_magic), "s"(a.plans), "s"(a.u));
     const int S = a.nslices, W = a.win;
     // the row whose slices k_stream handed over on this block's XCD
-    const int x = (int)(blockIdx.x % kXcds);
-    const int r0 = min(a.rows, (x * a.blocks_per_xcd + S - 1) / S);
-    const int r1 = min(a.rows, ((x + 1) * a.blocks_per_xcd + S - 1) / S);
-    const int r = r0 + (int)(blockIdx.x / kXcds);
+    const int x = (int)(bid % kXcds);
+    const int r0 = min(a.rows, div_slices(x * a.blocks_per_xcd + S - 1, a));
+    const int r1 = min(a.rows, div_slices((x + 1) * a.blocks_per_xcd + S - 1, a));
+    const int r = r0 + (int)(bid / kXcds);
     if (r >= r1) return;
-    HSAMP_PHASE(8192 + r, 0);
-    // the plan and u first (scalar loads: the first barrier waits for them,
-    // so they go out ahead of the lists)
-    const RowPlan P = a.plans[r];
-    const double ur = a.u[r];
     const u64* cand = a.cand + (int64_t)r * S * a.cand_cap;
     const int cnt_raw = (tid < S) ? a.cand_n[(int64_t)r * S + tid] : 0;
     u64 win[NW];
@@ -3029,6 +3048,12 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
             win[j] = ((u64)v[1] << 32) | v[0];
         }
     }
+    // the plan and u after the lists (scalar loads: a wait for them placed
+    // ahead of the lists' loads would delay those by a memory round trip)
+    __builtin_amdgcn_sched_barrier(0);
+    const RowPlan P = a.plans[r];
+    const double ur = a.u[r];
+    HSAMP_PHASE(8192 + r, 0);
     // (nothing here waits for a load: u goes to LDS once the lists are in)
     if (tid == 0) {
         st.flags = 0;
@@ -3249,7 +3274,7 @@ __global__ __launch_bounds__(kBlock) void k_writeback(StreamArgs a) {
     __shared__ RowPlan sP;
     const int tid = threadIdx.x;
     const int logical = (int)(blockIdx.x % kXcds) * a.blocks_per_xcd + (int)(blockIdx.x / kXcds);
-    const int r = logical / a.nslices, s = logical % a.nslices;
+    const int r = div_slices(logical, a), s = logical - r * a.nslices;
     if (r >= a.rows) return;
     const RowPlan P = a.plans[r];
     if (P.flags & RF_FULL) return;   // k_full writes its rows back itself

@@ -113,6 +113,8 @@ struct StreamArgs {
     int32_t ovf_cap;            // one tile of candidates
     int32_t win;                // entries of each slice's list k_merge loads up front
     uint32_t win_magic;         // floor(2^32 / win) + 1: umulhi(g, win_magic) == g / win for g < 2^16
+    uint32_t ns_magic;          // floor(2^32 / nslices) + 1: umulhi(g, ns_magic) == g / nslices
+                                // for g < 2^32 / nslices (block and row indices)
     int32_t dtype;              // logits element type (0 f32, 1 bf16)
     int32_t fast;               // every row fits k_merge's fast path
     int32_t pen_flag;           // penalties only lower logits: k_stream hands penalised ids over as

@@ -55,13 +55,16 @@ def sampler(hs):
     s.close()
 
 
-@pytest.fixture(params=["exact", "general"])
+@pytest.fixture(params=["exact", "exact2", "general"])
 def kernel_mode(request, monkeypatch):
-    """Runs a test twice: with exact lists allowed (the library's default for
-    the batches that qualify) and with ULTIMA_HSAMP_EXACT=0, which sends every
-    batch to the general stream and merge kernels."""
+    """Runs a test three times: with exact lists over slices of one tile, with
+    exact lists over slices of two tiles (ULTIMA_HSAMP_EXACT_TILES; aligned
+    rows only, others keep one tile), and with ULTIMA_HSAMP_EXACT=0, which
+    sends every batch to the general stream and merge kernels."""
+    monkeypatch.delenv("ULTIMA_HSAMP_EXACT", raising=False)
     if request.param == "general":
         monkeypatch.setenv("ULTIMA_HSAMP_EXACT", "0")
+        monkeypatch.delenv("ULTIMA_HSAMP_EXACT_TILES", raising=False)
     else:
-        monkeypatch.delenv("ULTIMA_HSAMP_EXACT", raising=False)
+        monkeypatch.setenv("ULTIMA_HSAMP_EXACT_TILES", "2" if request.param == "exact2" else "1")
     return request.param

@@ -28,7 +28,7 @@ hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, bool pen_gree
                          bool greedy_rows, bool sample_rows, int grid, hipStream_t stream);
 hipError_t launch_writeback(const StreamArgs& a, int grid, uint32_t lds, hipStream_t stream);
 hipError_t launch_merge(const StreamArgs& a, hipStream_t stream);
-hipError_t launch_stream_ex(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int grid,
+hipError_t launch_stream_ex(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int tiles, int grid,
                             hipStream_t stream);
 hipError_t launch_pick(const StreamArgs& a, int nw, hipStream_t stream);
 hipError_t launch_full(const StreamArgs& a, uint32_t lds, hipStream_t stream);
@@ -39,8 +39,9 @@ using namespace hsamp;
 namespace {
 
 constexpr int kSlots = 4;
-constexpr int kTile = kBlock * 32;      // most elements of one slice (two k_stream tiles)
+constexpr int kTile = kBlock * 32;      // elements of one k_stream tile (32 per thread)
 constexpr int kTargetBlocks = 4096;     // most blocks a launch spreads rows over
+constexpr int kTwoTileBlocks = 512;     // exact lists: two-tile slices while B * S stays at or above this
 constexpr int kMergeRound = kBlock * 16;  // candidates k_merge offers per round
 constexpr int kMergeWindow = kBlock * 16; // list entries k_merge loads up front, over all slices
 
@@ -514,15 +515,40 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
 
     const int B = b->rows, V = b->vocab;
     const int es = b->dtype == ULTIMA_HSAMP_F32 ? 4 : 2;
-    // Slicing: enough blocks to fill 256 CUs, slices of at most one tile.
+    // Exact lists (k_stream's EX kernels + k_pick): every row samples with
+    // top-k <= 64 and penalties that can only lower a logit, from windows the
+    // stream's registers hold, without DRY or logit bias. The stream then
+    // leaves every candidate with its final key. ULTIMA_HSAMP_EXACT=0 turns it
+    // off (the general kernels take every batch).
+    const int kmax = std::max(1, bl.kmax);
+    const bool wb_req = (b->flags & ULTIMA_HSAMP_WRITEBACK) != 0;
+    bool exact_ok = bl.any_sample && !bl.any_greedy && !bl.any_full && kmax <= 64 && !wb_req && bl.inv_ok &&
+                    (!bl.any_pen || (bl.pen_lowers && !bl.any_dry && bl.max_bias == 0 && bl.max_scan <= 8 * kBlock));
+    if (const char* ev = std::getenv("ULTIMA_HSAMP_EXACT")) exact_ok = exact_ok && ev[0] != '0';
+    // 16-byte loads: aligned rows holding at least one whole chunk
+    const bool vec_rows = (reinterpret_cast<uintptr_t>(b->logits) % 16 == 0) && ((b->logits_stride * es) % 16 == 0) &&
+                          V >= 16 / es;
+    // Slicing: enough blocks to fill 256 CUs, slices of at most one tile. Exact
+    // lists over aligned rows take slices of two tiles while the batch still
+    // gives two blocks per CU: each block's setup, history scan and bound then
+    // cover twice the ids, and k_pick merges half as many lists.
     const int tiles = (V + kTile - 1) / kTile;
     int S = std::max(1, std::min({kTargetBlocks / B, tiles, kBlock}));
+    int ex_tiles = 1;
+    if (exact_ok && vec_rows) {
+        const int S2 = (V + 2 * kTile - 1) / (2 * kTile);
+        int want = ((int64_t)B * S2 >= kTwoTileBlocks && S2 < S) ? 2 : 1;
+        if (const char* et = std::getenv("ULTIMA_HSAMP_EXACT_TILES")) want = std::atoi(et) == 2 ? 2 : 1;
+        if (want == 2) {
+            S = std::min(S, S2);
+            ex_tiles = 2;
+        }
+    }
     if (const char* fs = std::getenv("ULTIMA_HSAMP_SLICES")) S = std::max(1, std::min(std::atoi(fs), kBlock));
     int slice_len = ((V + S - 1) / S + 31) & ~31;
     S = (V + slice_len - 1) / slice_len;
     // block and row indices are divided by S with a 32-bit reciprocal (exact below 2^32 / S)
     if ((uint64_t)(B + 2) * (uint64_t)S * (uint64_t)(S + kXcds) >= (1ull << 32)) return ULTIMA_HSAMP_ERR_CAPACITY;
-    const int kmax = std::max(1, bl.kmax);
     const int buf_cap = std::max(512, next_pow2(2 * kmax));
     const int cand_cap = slice_len;                 // a slice's list holds all its ids
     const int bitmap_words = slice_len / 32;
@@ -561,22 +587,12 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     const int nblocks = B * S;
     const int grid = (nblocks + kXcds - 1) / kXcds * kXcds;
     int win = std::max(1, std::min(cand_cap, kMergeWindow / S));
-    // Exact lists (k_stream's EX kernels + k_pick): every row samples with
-    // top-k <= 64 and penalties that can only lower a logit, from windows the
-    // stream's registers hold, without DRY or logit bias. The stream then
-    // leaves every candidate with its final key. ULTIMA_HSAMP_EXACT=0 turns it
-    // off (the general kernels take every batch).
-    const bool wb_req = (b->flags & ULTIMA_HSAMP_WRITEBACK) != 0;
-    bool exact = bl.any_sample && !bl.any_greedy && !bl.any_full && kmax <= 64 && !wb_req && bl.inv_ok &&
-                 slice_len <= kBlock * 32 &&
-                 (!bl.any_pen || (bl.pen_lowers && !bl.any_dry && bl.max_bias == 0 && bl.max_scan <= 8 * kBlock));
-    if (const char* ev = std::getenv("ULTIMA_HSAMP_EXACT")) exact = exact && ev[0] != '0';
+    if (slice_len > kTile) ex_tiles = 2;
+    bool exact = exact_ok && slice_len <= kTile * ex_tiles && (ex_tiles == 1 || vec_rows);
     // k_stream EX: [count entries, 2 B per slice id + 8 (penalties)][allowed-id mask words]
     // [staged chunks: kBlock x 16 B data, kBlock x 4 B first ids]
     // (the general instantiations for unaligned rows take PEN = true: their
     // count entries are cleared and stay zero when no row has penalties)
-    const bool vec_rows = (reinterpret_cast<uintptr_t>(b->logits) % 16 == 0) && ((b->logits_stride * es) % 16 == 0) &&
-                          V >= 16 / es;
     const size_t cnt_bytes = (bl.any_pen || !vec_rows) ? align16(2 * ((size_t)slice_len + 8)) : 0;
     const size_t stage_off = cnt_bytes + align16(4 * (size_t)bitmap_words);
     const size_t lds_ex = stage_off + 20 * (size_t)kBlock;
@@ -692,7 +708,7 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     // bounds on pre-penalty keys, which penalties can only lower, and k_merge
     // finds the penalised candidates' true values (checking the bounds).
     if (exact)
-        HIP_TRY(launch_stream_ex(a, b->dtype, vec, bl.any_pen, bl.any_mask, grid, stream));
+        HIP_TRY(launch_stream_ex(a, b->dtype, vec, bl.any_pen, bl.any_mask, ex_tiles, grid, stream));
     else if (bl.any_topk)
         HIP_TRY(launch_stream(a, b->dtype, vec, bl.any_pen, bl.any_pen && !a.pen_flag, bl.any_mask, bl.any_greedy,
                               bl.any_sample, grid, stream));

@@ -569,12 +569,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const char* rowp, int
 // aligned rows, slices ending on a whole chunk; the row's last V % VW ids are
 // left to k_merge), or its elements one by one (unaligned rows). Chunks past
 // hi read as zeros; tile_keys counts them absent.
-template <int DT, bool VEC>
-__device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t rs, int tb, uint4 (&raw)[Tile<DT>::NCH]) {
+template <int DT, bool VEC, int NC = Tile<DT>::NCH>
+__device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t rs, int tb, uint4 (&raw)[NC]) {
     using T = Tile<DT>;
     const int e0 = tb + (int)threadIdx.x * T::VW;
 #pragma unroll
-    for (int j = 0; j < T::NCH; ++j) {
+    for (int j = 0; j < NC; ++j) {
         if (VEC) {
             const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, e0 * T::ES, j * kBlock * 16, 2);
             raw[j] = make_uint4(v.x, v.y, v.z, v.w);
@@ -1667,9 +1667,9 @@ __device__ __forceinline__ uint32_t final_raw_key(float x, int32_t t, uint32_t h
 // A sampling row's slice [lo, hi) with exact lists (single tile, raw[] holds
 // it); the row's last slice (last_slice) also takes the ragged end that
 // whole-chunk loads leave out.
-template <int DT, bool VEC, bool PEN, bool MASK>
+template <int DT, bool VEC, bool PEN, bool MASK, int NC>
 __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan& P, int r, int lo, int hi,
-                                             const uint4 (&raw)[Tile<DT>::NCH], u64* out, int64_t slot,
+                                             const uint4 (&raw)[NC], u64* out, int64_t slot,
                                              bool last_slice, bool pen, bool mk, const int32_t (&pre)[8],
                                              int pbase, unsigned char* smem, Shared& st) {
     using T = Tile<DT>;
@@ -1681,10 +1681,10 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
     constexpr uint32_t kFloor = (uint32_t)(kThetaFloor >> 32);
 
     // A. chunk maxima, as the chunks arrive
-    float cm[T::NCH];
+    float cm[NC];
     bool nanv = false;
 #pragma unroll
-    for (int j = 0; j < T::NCH; ++j) {
+    for (int j = 0; j < NC; ++j) {
         const int e0 = lo + (j * kBlock + tid) * T::VW;
         const bool in = e0 < hi;
         float x[T::VW];
@@ -1729,9 +1729,9 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
             }
         }
     }
-    uint32_t ck[T::NCH], lk = 0u;
+    uint32_t ck[NC], lk = 0u;
 #pragma unroll
-    for (int j = 0; j < T::NCH; ++j) {
+    for (int j = 0; j < NC; ++j) {
         const uint32_t b = __float_as_uint(cm[j]);
         ck[j] = b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);   // cm is never NaN
         lk = max(lk, ck[j]);
@@ -1767,26 +1767,29 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
 
     // C, D. the ids whose final raw key lies in [Rlo, Rhi)
     auto pass = [&](uint32_t Rlo, uint32_t Rhi) {
-        // positions in (chunk, lane) order from one ballot per chunk and a
-        // single LDS atomic per wave
-        int pj[T::NCH];
+        // positions in (chunk, lane) order from one ballot per chunk (kept in
+        // scalar registers) and a single LDS atomic per wave
+        u64 mj[NC];
+        int wj[NC];
         uint32_t csel = 0u;
         int wtot = 0;
 #pragma unroll
-        for (int j = 0; j < T::NCH; ++j) {
+        for (int j = 0; j < NC; ++j) {
             const bool in = ck[j] >= Rlo;
-            const u64 m = __ballot(in);
-            pj[j] = wtot + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+            mj[j] = __ballot(in);
+            wj[j] = wtot;
             csel |= (uint32_t)in << j;
-            wtot += __popcll(m);
+            wtot += __popcll(mj[j]);
         }
         int base = 0;
         if (lane == 0 && wtot > 0) base = atomicAdd(&st.nst, wtot);
         base = __builtin_amdgcn_readfirstlane(base);
         auto stage = [&](int rb) {
 #pragma unroll
-            for (int j = 0; j < T::NCH; ++j) {
-                const int p = base + pj[j] - rb;
+            for (int j = 0; j < NC; ++j) {
+                const int p = base + wj[j] - rb +
+                              (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mj[j] >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)mj[j], 0u));
                 if (((csel >> j) & 1u) && (uint32_t)p < (uint32_t)kStageCap) {
                     sdat[p] = raw[j];
                     sidx[p] = lo + (j * kBlock + tid) * T::VW;
@@ -1865,9 +1868,11 @@ __device__ __forceinline__ int div_slices(int g, const StreamArgs& a) {
     return a.nslices == 1 ? g : (int)__umulhi((uint32_t)g, a.ns_magic);
 }
 
-template <int DT, bool VEC, bool PEN, bool MASK, bool GR, bool EX = false>
-__global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
+template <int DT, bool VEC, bool PEN, bool MASK, bool GR, int EX = 0>
+__global__ __launch_bounds__(kBlock, EX == 2 ? 4 : 5) void k_stream(StreamArgs a) {
     using T = Tile<DT>;
+    constexpr int NT = EX > 1 ? EX : 1;        // tiles per slice (exact lists: 1 or 2)
+    constexpr int NC = T::NCH * NT;            // chunks per thread
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ Shared st;
     const int tid = threadIdx.x;
@@ -1892,7 +1897,7 @@ __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
     // before the plan is read (it is processed chunk by chunk as its loads
     // complete in order); otherwise after the plan has said the row is ours.
     const bool early = EX || ((a.uniform >> (GR ? 0 : 1)) & 1) != 0;
-    uint4 raw[T::NCH];
+    uint4 raw[NC];
     // Exact lists: the history row, the slice's mask words and the tile go out
     // first (their addresses come from the launch arguments alone) and the
     // plan's scalar load after them: a wait for the plan placed ahead of the
@@ -1911,10 +1916,15 @@ __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
     // (MASK launches may carry no mask: the general instantiations for
     // unaligned rows take MASK = true; the mask words are then all ones)
     const bool mk = MASK && a.mask != nullptr;
-    uint32_t mw_pre = 0xFFFFFFFFu;
-    if (EX && mk && tid < a.bitmap_words)
-        mw_pre = (lo + 32 * tid < hi) ? a.mask[(int64_t)r * a.mask_stride + (lo >> 5) + tid] : 0u;
-    if (early) load_tile<DT, VEC>(rs, lo, raw);
+    uint32_t mw_pre[NT];
+#pragma unroll
+    for (int q = 0; q < NT; ++q) {
+        const int w = tid + q * kBlock;
+        mw_pre[q] = 0xFFFFFFFFu;
+        if (EX && mk && w < a.bitmap_words)
+            mw_pre[q] = (lo + 32 * w < hi) ? a.mask[(int64_t)r * a.mask_stride + (lo >> 5) + w] : 0u;
+    }
+    if (early) load_tile<DT, VEC, NC>(rs, lo, raw);
     if (EX) __builtin_amdgcn_sched_barrier(0);
     P = a.plans[r];
     if (!early) {
@@ -1946,7 +1956,9 @@ __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
         if (PEN) {
             for (int i = tid; i < (a.mbm_off >> 2); i += kBlock) reinterpret_cast<uint4*>(smem)[i] = make_uint4(0u, 0u, 0u, 0u);
         }
-        if (MASK && tid < a.bitmap_words) pbm[a.mbm_off + tid] = mw_pre;
+#pragma unroll
+        for (int q = 0; q < NT; ++q)
+            if (MASK && tid + q * kBlock < a.bitmap_words) pbm[a.mbm_off + tid + q * kBlock] = mw_pre[q];
         if (tid == 0) {
             st.n = 0;
             st.nst = 0;
@@ -1956,25 +1968,25 @@ __global__ __launch_bounds__(kBlock, 5) void k_stream(StreamArgs a) {
         HSAMP_PHASE(logical, 1);
         const int64_t slot = (int64_t)r * a.nslices + s;
         u64* out = a.cand + slot * a.cand_cap;
-        stream_exact<DT, VEC, PEN, MASK>(a, P, r, lo, hi, raw, out, slot, VEC && s == a.nslices - 1, pen, mk, pre,
-                                         hd ? 0 : p0, smem, st);
-        return;
-    }
-    stream_setup<PEN, MASK>(a, P, r, lo, hi, GR, pen, masked, p0, L, hrow, pbm, pbm + a.bitmap_words, st);
-    if (!early) load_tile<DT, VEC>(rs, lo, raw);
-    if (PEN) {
-        // the history window (waits for pre[] only when the tile was requested after)
-        if (pen) {
+        stream_exact<DT, VEC, PEN, MASK, NC>(a, P, r, lo, hi, raw, out, slot, VEC && s == a.nslices - 1, pen, mk,
+                                             pre, hd ? 0 : p0, smem, st);
+    } else {
+        stream_setup<PEN, MASK>(a, P, r, lo, hi, GR, pen, masked, p0, L, hrow, pbm, pbm + a.bitmap_words, st);
+        if (!early) load_tile<DT, VEC>(rs, lo, raw);
+        if (PEN) {
+            // the history window (waits for pre[] only when the tile was requested after)
+            if (pen) {
 #pragma unroll
-            for (int q = 0; q < 8; ++q)
-                if (p0 + q * kBlock + tid < L) stream_mark(pre[q], lo, hi, pbm);
+                for (int q = 0; q < 8; ++q)
+                    if (p0 + q * kBlock + tid < L) stream_mark(pre[q], lo, hi, pbm);
+            }
+            __syncthreads();
         }
-        __syncthreads();
+        const int64_t slot = (int64_t)r * a.nslices + s;
+        u64* out = a.cand + slot * a.cand_cap;
+        if constexpr (GR) stream_greedy<DT, VEC, PEN, MASK>(a, P, r, lo, hi, rs, raw, out, slot, smem, st);
+        else stream_sample<DT, VEC, PEN, MASK>(a, P, r, lo, hi, rs, raw, out, slot, smem, st);
     }
-    const int64_t slot = (int64_t)r * a.nslices + s;
-    u64* out = a.cand + slot * a.cand_cap;
-    if constexpr (GR) stream_greedy<DT, VEC, PEN, MASK>(a, P, r, lo, hi, rs, raw, out, slot, smem, st);
-    else stream_sample<DT, VEC, PEN, MASK>(a, P, r, lo, hi, rs, raw, out, slot, smem, st);
 }
 
 // ---- the merge kernel ------------------------------------------------------------
@@ -3925,15 +3937,19 @@ static void launch_stream_kind(const StreamArgs& a, int dtype, bool vec, bool pe
 #undef HSAMP_STREAM
 }
 
-// Exact lists: the sampling kernel with final keys (every row samples).
+// Exact lists: the sampling kernel with final keys (every row samples), slices
+// of one tile, or of two (aligned rows).
+template <int NT>
 static void launch_stream_exact(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int grid,
                                 hipStream_t stream) {
     const dim3 g(grid), b(kBlock);
     const uint32_t l = a.lds_bytes;
-#define HSAMP_STREAM(DT_, V_, P_, M_) hipLaunchKernelGGL((k_stream<DT_, V_, P_, M_, false, true>), g, b, l, stream, a)
+#define HSAMP_STREAM(DT_, V_, P_, M_) hipLaunchKernelGGL((k_stream<DT_, V_, P_, M_, false, NT>), g, b, l, stream, a)
     if (!vec) {
-        if (dtype == 0) HSAMP_STREAM(0, false, true, true);
-        else HSAMP_STREAM(1, false, true, true);
+        if constexpr (NT == 1) {
+            if (dtype == 0) HSAMP_STREAM(0, false, true, true);
+            else HSAMP_STREAM(1, false, true, true);
+        }
     } else if (dtype == 0) {
         if (pen) {
             if (mask) HSAMP_STREAM(0, true, true, true);
@@ -3954,9 +3970,12 @@ static void launch_stream_exact(const StreamArgs& a, int dtype, bool vec, bool p
 #undef HSAMP_STREAM
 }
 
-hipError_t launch_stream_ex(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int grid,
+hipError_t launch_stream_ex(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int tiles, int grid,
                             hipStream_t stream) {
-    launch_stream_exact(a, dtype, vec, pen, mask, grid, stream);
+    // two-tile slices are for aligned rows only (the host never asks otherwise)
+    if (tiles == 2 && !vec) return hipErrorInvalidValue;
+    if (tiles == 2) launch_stream_exact<2>(a, dtype, vec, pen, mask, grid, stream);
+    else launch_stream_exact<1>(a, dtype, vec, pen, mask, grid, stream);
     return hipGetLastError();
 }
 

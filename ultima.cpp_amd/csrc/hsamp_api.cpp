@@ -69,6 +69,7 @@ struct ultima_hsamp {
     int32_t max_rows = 0;
     int32_t max_vocab = 0;
     size_t lds_limit = 0;         // LDS bytes one block may use on this device
+    int cus = 256;                // compute units of this device
     hipStream_t own_stream = nullptr;
     hipEvent_t phase_ev = nullptr;   // recorded between the stream and merge kernels when set
     Slot slots[kSlots];
@@ -452,6 +453,7 @@ int ultima_hsamp_create(int device, int32_t max_rows, int32_t max_vocab, ultima_
     h->max_rows = max_rows;
     h->max_vocab = max_vocab;
     h->lds_limit = prop.sharedMemPerBlock;
+    h->cus = std::max(1, prop.multiProcessorCount);
     auto fail = [&](int st) {
         ultima_hsamp_destroy(h);
         return st;
@@ -528,19 +530,37 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     // 16-byte loads: aligned rows holding at least one whole chunk
     const bool vec_rows = (reinterpret_cast<uintptr_t>(b->logits) % 16 == 0) && ((b->logits_stride * es) % 16 == 0) &&
                           V >= 16 / es;
-    // Slicing: enough blocks to fill 256 CUs, slices of at most one tile. Exact
-    // lists over aligned rows take slices of two tiles while the batch still
-    // gives two blocks per CU: each block's setup, history scan and bound then
-    // cover twice the ids, and k_pick merges half as many lists.
+    // Slicing: enough blocks to fill the CUs, slices of at most one tile.
+    // Exact lists over aligned rows take slices of up to two tiles while the
+    // batch still gives two blocks per CU: each block's setup, history scan
+    // and bound then cover more ids, and k_pick merges fewer lists. Among
+    // those slicings, the one whose busiest CU streams the fewest ids, with
+    // a block's fixed work counted as kFixedIds ids (blocks spread evenly).
     const int tiles = (V + kTile - 1) / kTile;
     int S = std::max(1, std::min({kTargetBlocks / B, tiles, kBlock}));
     int ex_tiles = 1;
     if (exact_ok && vec_rows) {
+        constexpr int64_t kFixedIds = 4096;
         const int S2 = (V + 2 * kTile - 1) / (2 * kTile);
         int want = ((int64_t)B * S2 >= kTwoTileBlocks && S2 < S) ? 2 : 1;
-        if (const char* et = std::getenv("ULTIMA_HSAMP_EXACT_TILES")) want = std::atoi(et) == 2 ? 2 : 1;
+        bool forced = false;
+        if (const char* et = std::getenv("ULTIMA_HSAMP_EXACT_TILES")) {
+            want = std::atoi(et) == 2 ? 2 : 1;
+            forced = true;   // two tiles asked for: the fewest slices
+        }
         if (want == 2) {
-            S = std::min(S, S2);
+            int best = std::min(S, S2);
+            int64_t best_cost = INT64_MAX;
+            for (int c = best; !forced && c <= std::min(S, 2 * S2); ++c) {
+                const int64_t len = ((V + c - 1) / c + 31) & ~31;
+                const int64_t per_cu = ((int64_t)B * c + h->cus - 1) / h->cus;
+                const int64_t cost = per_cu * (len + kFixedIds);
+                if (cost < best_cost) {
+                    best_cost = cost;
+                    best = c;
+                }
+            }
+            S = best;
             ex_tiles = 2;
         }
     }
@@ -587,7 +607,7 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     const int nblocks = B * S;
     const int grid = (nblocks + kXcds - 1) / kXcds * kXcds;
     int win = std::max(1, std::min(cand_cap, kMergeWindow / S));
-    if (slice_len > kTile) ex_tiles = 2;
+    ex_tiles = slice_len > kTile ? 2 : 1;
     bool exact = exact_ok && slice_len <= kTile * ex_tiles && (ex_tiles == 1 || vec_rows);
     // k_stream EX: [count entries, 2 B per slice id + 8 (penalties)][allowed-id mask words]
     // [staged chunks: kBlock x 16 B data, kBlock x 4 B first ids]

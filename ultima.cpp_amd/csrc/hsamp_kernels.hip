@@ -1729,6 +1729,7 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
             }
         }
     }
+    HSAMP_PHASE(slot, 10);
     uint32_t ck[NC], lk = 0u;
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
@@ -1741,6 +1742,7 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
     const uint32_t g4[4] = {lk, 0u, 0u, 0u};
     const uint32_t tw = wave_kth_bound16(g4, 1, kw);
     if (lane == 0) st.twave[wave_id()] = tw;
+    HSAMP_PHASE(slot, 11);
     // the ragged end (the row's last slice): read while the bound settles
     float xt = 0.0f;
     const bool tl = VEC && last_slice && tid < a.vec_tail;
@@ -1784,6 +1786,7 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
         int base = 0;
         if (lane == 0 && wtot > 0) base = atomicAdd(&st.nst, wtot);
         base = __builtin_amdgcn_readfirstlane(base);
+        HSAMP_PHASE(slot, 12);
         auto stage = [&](int rb) {
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
@@ -1913,6 +1916,22 @@ __global__ __launch_bounds__(kBlock, EX == 2 ? 4 : 5) void k_stream(StreamArgs a
 #pragma unroll
         for (int q = 0; q < 8; ++q) pre[q] = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(hr, tid * 4, q * kBlock * 4, 0);
     }
+    if constexpr (EX && PEN) {
+        if (!hd) {
+            // longer history rows: the window's place comes from the plan,
+            // which then goes first (the tile waits one round trip); the
+            // window still goes out ahead of the tile, as the short rows do
+            P = a.plans[r];
+            const int L = P.hist_len, p0 = L - P.scan_len;
+            const int32_t* hrow = a.hist + (int64_t)r * a.hist_stride;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) pre[q] = -1;
+            if ((P.flags & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) != 0 && L > 0) {
+#pragma unroll
+                for (int q = 0; q < 8; ++q) pre[q] = hrow[max(0, min(p0 + q * kBlock + tid, L - 1))];
+            }
+        }
+    }
     // (MASK launches may carry no mask: the general instantiations for
     // unaligned rows take MASK = true; the mask words are then all ones)
     const bool mk = MASK && a.mask != nullptr;
@@ -1926,7 +1945,7 @@ __global__ __launch_bounds__(kBlock, EX == 2 ? 4 : 5) void k_stream(StreamArgs a
     }
     if (early) load_tile<DT, VEC, NC>(rs, lo, raw);
     if (EX) __builtin_amdgcn_sched_barrier(0);
-    P = a.plans[r];
+    if (!(EX && PEN) || hd) P = a.plans[r];
     if (!early) {
         if (P.flags & RF_FULL) return;                     // k_full's row
         if (((P.flags & RF_GREEDY) != 0) != GR) return;    // the other kernel's row
@@ -1942,11 +1961,11 @@ __global__ __launch_bounds__(kBlock, EX == 2 ? 4 : 5) void k_stream(StreamArgs a
     // p0 + q * kBlock + tid, used only below L), so nothing here waits.
     const int L = P.hist_len, p0 = L - P.scan_len;
     const int32_t* hrow = a.hist + (int64_t)r * a.hist_stride;
-    if (!hd) {
+    if (!EX) {
 #pragma unroll
         for (int q = 0; q < 8; ++q) pre[q] = -1;
     }
-    if (!hd && PEN && pen && L > 0) {
+    if (!EX && PEN && pen && L > 0) {
 #pragma unroll
         for (int q = 0; q < 8; ++q) pre[q] = hrow[max(0, min(p0 + q * kBlock + tid, L - 1))];
     }

@@ -225,6 +225,33 @@ def test_top64_ties_and_zero_signs(sampler, wl, kernel_mode):
     assert compare_rows(w, g) == 6
 
 
+def test_nan_logits_flagged_and_left_out(sampler, wl, kernel_mode):
+    """NaN logits are outside the contract: the row is flagged (bit 8) and its
+    NaN ids count as -inf, so the rest of the row samples exactly as the
+    oracle does with those ids at -inf. NaNs sit next to the row's largest
+    logits (same 16-byte chunk), in a row's ragged end, and fill one row
+    except for a few ids."""
+    rng = np.random.default_rng(31)
+    V = 151936
+    x = rng.normal(0, 2, size=(5, V)).astype(np.float32)
+    top = np.argsort(-x[0])[:40]
+    x[0, top[::3] ^ 1] = np.nan              # neighbours of some top ids
+    x[1, V - 3:] = np.nan                     # the ragged end
+    x[1, 12345] = np.nan
+    x[2, :] = np.nan
+    x[2, [7, 70000, 151935]] = [1.0, 2.0, 0.5]
+    x[3, ::1000] = np.nan
+    plist = [wl.identity_params(top_k=k, temperature=t, top_p=p) for k, t, p in
+             ((50, 0.7, 1.0), (40, 1.0, 0.9), (10, 1.0, 1.0), (64, 1.3, 0.95), (20, 0.8, 1.0))]
+    w = _wl_from(wl, x, plist, rng.random(5))
+    g = run_gpu(sampler, w)
+    for r in range(4):
+        assert int(g["row_flags"][r]) & 8, f"row {r}: NaN not flagged"
+    assert not (int(g["row_flags"][4]) & 8)
+    ref = _wl_from(wl, np.where(np.isnan(x), np.float32(-np.inf), x), plist, w.u)
+    assert compare_rows(ref, g) == 5
+
+
 def test_single_token_vocab(sampler, wl):
     x = np.array([[3.0], [-np.inf]], np.float32)
     plist = [wl.identity_params(top_k=5), wl.identity_params(temperature=2.0)]

@@ -1680,14 +1680,12 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
     int32_t* sidx = reinterpret_cast<int32_t*>(sdat + kStageCap);
     constexpr uint32_t kFloor = (uint32_t)(kThetaFloor >> 32);
 
-    // A. chunk maxima, as the chunks arrive
-    float cm[NC];
-    bool nanv = false;
-#pragma unroll
-    for (int j = 0; j < NC; ++j) {
+    // A. chunk maxima, as the chunks arrive: IEEE maximum (NaN-propagating,
+    // -0 < +0 as raw keys order them), so that a NaN shows in its chunk's
+    // maximum; such chunks then take the NaN-ignoring maximum of their other
+    // ids (NaN ids count as -inf), after the loop
+    auto chunk = [&](int j, float (&x)[T::VW]) {
         const int e0 = lo + (j * kBlock + tid) * T::VW;
-        const bool in = e0 < hi;
-        float x[T::VW];
 #pragma unroll
         for (int c = 0; c < T::VW; ++c) x[c] = elem<DT>(raw[j], c);
         if (MASK) {
@@ -1701,14 +1699,36 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
 #pragma unroll
             for (int c = 0; c < T::VW; ++c) x[c] = (e0 + c < hi) ? x[c] : -__builtin_inff();
         }
+    };
+    float cm[NC];
+    bool nanv = false;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        float x[T::VW];
+        chunk(j, x);
         float m = x[0];
 #pragma unroll
-        for (int c = 1; c < T::VW; ++c) m = fmaxf(m, x[c]);
-#pragma unroll
-        for (int c = 0; c < T::VW; c += 2) nanv |= __builtin_isunordered(x[c], x[c + 1]);
-        cm[j] = (in && m == m) ? m : -__builtin_inff();
+        for (int c = 1; c < T::VW; ++c) m = __builtin_elementwise_maximum(m, x[c]);
+        nanv |= m != m;
+        cm[j] = m;
         __builtin_amdgcn_sched_barrier(0);
     }
+    if (nanv) {
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+            if (cm[j] != cm[j]) {
+                float x[T::VW];
+                chunk(j, x);
+                float m = -__builtin_inff();
+#pragma unroll
+                for (int c = 0; c < T::VW; ++c) m = (x[c] == x[c]) ? __builtin_elementwise_maximum(m, x[c]) : m;
+                cm[j] = m;
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NC; ++j)
+        if (lo + (j * kBlock + tid) * T::VW >= hi) cm[j] = -__builtin_inff();
     HSAMP_PHASE(slot, 3);
 
     // B. the slice's history counts (waits for the history loads) and the bound

@@ -360,6 +360,36 @@ def test_penalties_below_the_stream_bounds(sampler, hs, wl, kernel_mode):
         assert not np.any(g["row_flags"] & hs.ROW_REREAD)
 
 
+def test_penalty_windows_of_different_lengths(sampler, wl, kernel_mode):
+    """Exact lists keep a plain count per id when the repetition and the
+    frequency/presence windows coincide (or one stage is off) and a count
+    plus a repetition bit otherwise. Rows: repetition window shorter than the
+    frequency/presence window (DRY off but dry_last_n widening it), equal
+    windows, repetition off, frequency/presence off, and a DRY window shorter
+    than the repetition window. Histories repeat the rows' top ids so that
+    every kind of count reaches the kept set."""
+    rng = np.random.default_rng(77)
+    B, V, H = 5, 60000, 1024
+    x = rng.normal(0, 2, size=(B, V)).astype(np.float32)
+    hist = np.empty((B, H), np.int32)
+    for r in range(B):
+        top = np.argsort(-x[r])[:60]
+        hist[r] = rng.permutation(np.concatenate([rng.choice(top, 400), rng.integers(0, V, H - 400)]))
+    base = dict(temperature=0.8, top_k=50, top_p=0.95)
+    plist = [wl.identity_params(**base, rep_penalty=1.3, repeat_last_n=64, dry_last_n=700,
+                                frequency_penalty=0.4, presence_penalty=0.2),
+             wl.identity_params(**base, rep_penalty=1.3, repeat_last_n=700, frequency_penalty=0.4,
+                                presence_penalty=0.2),
+             wl.identity_params(**base, repeat_last_n=300, dry_last_n=300, frequency_penalty=0.7),
+             wl.identity_params(**base, rep_penalty=1.5, repeat_last_n=900),
+             wl.identity_params(**base, rep_penalty=1.2, repeat_last_n=500, dry_last_n=100,
+                                presence_penalty=0.6)]
+    w = _wl_from(wl, x, plist, rng.random(B))
+    w.hist, w.hist_len = hist, np.full(B, H, np.int64)
+    g = run_gpu(sampler, w)
+    assert compare_rows(w, g) == B
+
+
 def test_greedy_flagged_past_the_window(sampler, wl):
     """Greedy rows whose 2048 penalised ids hold the largest logits of the
     first slice: that slice hands over more flagged ids than the merge's

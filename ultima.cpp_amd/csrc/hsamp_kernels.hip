@@ -1651,11 +1651,14 @@ __device__ uint32_t raw_edge(uint32_t ths, float inv_t, float temp) {
 
 // Final raw key of slice id t (raw logit x, after the mask) with count entry
 // h: stages 1-4 (sampler.cpp:28-99, those a count entry calls for), NaN ->
-// -inf (noted).
-__device__ __forceinline__ uint32_t final_raw_key(float x, int32_t t, uint32_t h, const StreamArgs& a,
+// -inf (noted). one: the entry is a plain count over the whole scanned window
+// (the repetition and frequency/presence windows are equal, or one of them
+// is off): the id repeats when it counts at all.
+__device__ __forceinline__ uint32_t final_raw_key(float x, int32_t t, uint32_t h, bool one, const StreamArgs& a,
                                                   const RowPlan& P, bool& nan) {
     if (h == 0u) return raw_key(x);
-    const uint32_t v = ((h & XC_REP) ? HV_REP : 0u) | (h & XC_FP_MASK);
+    const uint32_t v = one ? ((P.rep_win > 0 ? HV_REP : 0u) | (P.fp_win > 0 ? h : 0u))
+                           : (((h & XC_REP) ? HV_REP : 0u) | (h & XC_FP_MASK));
     const float y = pen_value(x, t, v, a, P);
     if (y != y) {
         nan = true;
@@ -1731,21 +1734,35 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
         if (lo + (j * kBlock + tid) * T::VW >= hi) cm[j] = -__builtin_inff();
     HSAMP_PHASE(slot, 3);
 
-    // B. the slice's history counts (waits for the history loads) and the bound
+    // B. the slice's history counts (waits for the history loads) and the bound.
+    // Exact lists run without DRY, so the scanned window is the larger of the
+    // repetition and frequency/presence windows; when those are equal (or one
+    // is off) a count entry is a plain count over it (one atomic per id).
+    const bool one = P.rep_win == 0 || P.fp_win == 0 || P.rep_win == P.fp_win;
     if (PEN && pen) {
         const int L = P.hist_len, p0 = L - P.scan_len;
         const int mhi = min(a.vocab, lo + a.slice_len);
         uint32_t* cw = reinterpret_cast<uint32_t*>(smem);
         const uint32_t wl = (uint32_t)(L - p0), sl = (uint32_t)(mhi - lo);
+        if (one) {
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int p = pbase + q * kBlock + tid;   // pre[q]'s history position
-            const int32_t t = pre[q];
-            if ((uint32_t)(p - p0) < wl && (uint32_t)(t - lo) < sl) {
-                const int o = t - lo;
-                const uint32_t sh = (uint32_t)(o & 1) << 4;
-                if (p >= L - P.fp_win) atomicAdd(&cw[o >> 1], 1u << sh);
-                if (p >= L - P.rep_win) atomicOr(&cw[o >> 1], XC_REP << sh);
+            for (int q = 0; q < 8; ++q) {
+                const int p = pbase + q * kBlock + tid;   // pre[q]'s history position
+                const int32_t t = pre[q];
+                if ((uint32_t)(p - p0) < wl && (uint32_t)(t - lo) < sl)
+                    atomicAdd(&cw[(t - lo) >> 1], 1u << ((uint32_t)((t - lo) & 1) << 4));
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int p = pbase + q * kBlock + tid;
+                const int32_t t = pre[q];
+                if ((uint32_t)(p - p0) < wl && (uint32_t)(t - lo) < sl) {
+                    const int o = t - lo;
+                    const uint32_t sh = (uint32_t)(o & 1) << 4;
+                    if (p >= L - P.fp_win) atomicAdd(&cw[o >> 1], 1u << sh);
+                    if (p >= L - P.rep_win) atomicOr(&cw[o >> 1], XC_REP << sh);
+                }
             }
         }
     }
@@ -1836,7 +1853,7 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
                                     : __uint_as_float((c & 1) ? (wsel & 0xFFFF0000u) : (wsel << 16));
                 if (MASK && !((mbm[o >> 5] >> (o & 31)) & 1u)) x = -__builtin_inff();
                 if ((VEC || t < hi) && raw_key(x) >= Rlo) {
-                    const uint32_t kf = final_raw_key(x, t, PEN ? (uint32_t)cnt[o] : 0u, a, P, nanp);
+                    const uint32_t kf = final_raw_key(x, t, PEN ? (uint32_t)cnt[o] : 0u, one, a, P, nanp);
                     if (kf >= Rlo && kf < Rhi) out[atomicAdd(&st.n, 1)] = comp(kf, t);
                 }
             }
@@ -1847,7 +1864,7 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
             __syncthreads();
         }
         if (tl) {
-            const uint32_t kf = final_raw_key(xt, tt_id, PEN ? (uint32_t)cnt[tt_id - lo] : 0u, a, P, nanp);
+            const uint32_t kf = final_raw_key(xt, tt_id, PEN ? (uint32_t)cnt[tt_id - lo] : 0u, one, a, P, nanp);
             if (kf >= Rlo && kf < Rhi) out[atomicAdd(&st.n, 1)] = comp(kf, tt_id);
         }
         if (nanp) atomicOr(&st.flags, 1);

@@ -610,12 +610,12 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     ex_tiles = slice_len > kTile ? 2 : 1;
     bool exact = exact_ok && slice_len <= kTile * ex_tiles && (ex_tiles == 1 || vec_rows);
     // k_stream EX: [count entries, 2 B per slice id + 8 (penalties)][allowed-id mask words]
-    // [staged chunks: kBlock x 16 B data, kBlock x 4 B first ids]
+    // [staged chunks: kBlock slots of 32 B (16 B data, the chunk's first id)]
     // (the general instantiations for unaligned rows take PEN = true: their
     // count entries are cleared and stay zero when no row has penalties)
     const size_t cnt_bytes = (bl.any_pen || !vec_rows) ? align16(2 * ((size_t)slice_len + 8)) : 0;
     const size_t stage_off = cnt_bytes + align16(4 * (size_t)bitmap_words);
-    const size_t lds_ex = stage_off + 20 * (size_t)kBlock;
+    const size_t lds_ex = stage_off + 32 * (size_t)kBlock;
     // k_pick: each slice's first W entries, NW per thread; W about twice k
     int pick_nw = 16;
     if (exact) {

@@ -1679,8 +1679,8 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
     const int tid = threadIdx.x, lane = lane_id();
     uint16_t* cnt = reinterpret_cast<uint16_t*>(smem);
     const uint32_t* mbm = reinterpret_cast<const uint32_t*>(smem) + a.mbm_off;
-    uint4* sdat = reinterpret_cast<uint4*>(smem + a.stage_off);
-    int32_t* sidx = reinterpret_cast<int32_t*>(sdat + kStageCap);
+    // staged chunks: 32-byte slots, 16 bytes of logits then the chunk's first id
+    unsigned char* stg = smem + a.stage_off;
     constexpr uint32_t kFloor = (uint32_t)(kThetaFloor >> 32);
 
     // A. chunk maxima, as the chunks arrive: IEEE maximum (NaN-propagating,
@@ -1767,13 +1767,11 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
         }
     }
     HSAMP_PHASE(slot, 10);
-    uint32_t ck[NC], lk = 0u;
+    // the lane's largest chunk maximum as a raw key (cm is never NaN)
+    float lmf = cm[0];
 #pragma unroll
-    for (int j = 0; j < NC; ++j) {
-        const uint32_t b = __float_as_uint(cm[j]);
-        ck[j] = b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);   // cm is never NaN
-        lk = max(lk, ck[j]);
-    }
+    for (int j = 1; j < NC; ++j) lmf = __builtin_elementwise_maximum(lmf, cm[j]);
+    const uint32_t lk = raw_key(lmf);
     const int k = P.top_k;
     const int kw = (k + 8 + 3) >> 2;   // <= 18
     const uint32_t g4[4] = {lk, 0u, 0u, 0u};
@@ -1806,18 +1804,18 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
 
     // C, D. the ids whose final raw key lies in [Rlo, Rhi)
     auto pass = [&](uint32_t Rlo, uint32_t Rhi) {
-        // positions in (chunk, lane) order from one ballot per chunk (kept in
-        // scalar registers) and a single LDS atomic per wave
+        // The chunks whose maximum reaches Rlo (as floats: a superset of the
+        // raw-key test, which orders -0 below +0), at positions in (chunk,
+        // lane) order from one ballot per chunk (kept in scalar registers)
+        // and a single LDS atomic per wave.
+        const float Rf = key_to_float(Rlo);
         u64 mj[NC];
         int wj[NC];
-        uint32_t csel = 0u;
         int wtot = 0;
 #pragma unroll
         for (int j = 0; j < NC; ++j) {
-            const bool in = ck[j] >= Rlo;
-            mj[j] = __ballot(in);
+            mj[j] = __ballot(cm[j] >= Rf);
             wj[j] = wtot;
-            csel |= (uint32_t)in << j;
             wtot += __popcll(mj[j]);
         }
         int base = 0;
@@ -1825,14 +1823,16 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
         base = __builtin_amdgcn_readfirstlane(base);
         HSAMP_PHASE(slot, 12);
         auto stage = [&](int rb) {
+            // the wave's positions all within this round: no per-lane check
+            const bool all_in = base >= rb && base + wtot <= rb + kStageCap;
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
-                const int p = base + wj[j] - rb +
-                              (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mj[j] >> 32),
-                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)mj[j], 0u));
-                if (((csel >> j) & 1u) && (uint32_t)p < (uint32_t)kStageCap) {
-                    sdat[p] = raw[j];
-                    sidx[p] = lo + (j * kBlock + tid) * T::VW;
+                const uint32_t p = __builtin_amdgcn_mbcnt_hi(
+                    (uint32_t)(mj[j] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mj[j], (uint32_t)(base + wj[j] - rb)));
+                if (cm[j] >= Rf && (all_in || p < (uint32_t)kStageCap)) {
+                    unsigned char* sp = stg + p * 32u;
+                    *reinterpret_cast<uint4*>(sp) = raw[j];
+                    *reinterpret_cast<int32_t*>(sp + 16) = lo + (j * kBlock + tid) * T::VW;
                 }
             }
         };
@@ -1842,19 +1842,36 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
         const int nst = st.nst;
         bool nanp = false;
         for (int rb = 0;;) {
-            // VW threads per staged chunk, one element each
-            for (int e = tid; e < min(kStageCap, nst - rb) * T::VW; e += kBlock) {
+            // VW threads per staged chunk, one element each; every lane runs
+            // every step, so each step appends with one ballot and one atomic
+            const int ne = min(kStageCap, nst - rb) * T::VW;
+            for (int e1 = 0; e1 < ne; e1 += kBlock) {
+                const int e = e1 + tid;
                 const int ci = e / T::VW, c = e % T::VW;
-                const int e0 = sidx[ci];
-                const int t = e0 + c;
+                const unsigned char* sp = stg + (uint32_t)min(ci, kStageCap - 1) * 32u;
+                const int t = *reinterpret_cast<const int32_t*>(sp + 16) + c;
                 const int o = t - lo;
-                const uint32_t wsel = reinterpret_cast<const uint32_t*>(&sdat[ci])[DT == 0 ? c : (c >> 1)];
+                const uint32_t wsel = reinterpret_cast<const uint32_t*>(sp)[DT == 0 ? c : (c >> 1)];
                 float x = (DT == 0) ? __uint_as_float(wsel)
                                     : __uint_as_float((c & 1) ? (wsel & 0xFFFF0000u) : (wsel << 16));
-                if (MASK && !((mbm[o >> 5] >> (o & 31)) & 1u)) x = -__builtin_inff();
-                if ((VEC || t < hi) && raw_key(x) >= Rlo) {
-                    const uint32_t kf = final_raw_key(x, t, PEN ? (uint32_t)cnt[o] : 0u, one, a, P, nanp);
-                    if (kf >= Rlo && kf < Rhi) out[atomicAdd(&st.n, 1)] = comp(kf, t);
+                uint32_t kf = 0u;
+                bool keep = false;
+                if (e < ne) {
+                    if (MASK && !((mbm[o >> 5] >> (o & 31)) & 1u)) x = -__builtin_inff();
+                    if ((VEC || t < hi) && raw_key(x) >= Rlo) {
+                        kf = final_raw_key(x, t, PEN ? (uint32_t)cnt[o] : 0u, one, a, P, nanp);
+                        keep = kf >= Rlo && kf < Rhi;
+                    }
+                }
+                const u64 mk2 = __ballot(keep);
+                if (mk2 != 0ull) {
+                    int ob = 0;
+                    if (lane == 0) ob = atomicAdd(&st.n, __popcll(mk2));
+                    ob = __builtin_amdgcn_readfirstlane(ob);
+                    if (keep)
+                        out[ob + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mk2 >> 32),
+                                                                __builtin_amdgcn_mbcnt_lo((uint32_t)mk2, 0u))] =
+                            comp(kf, t);
                 }
             }
             rb += kStageCap;

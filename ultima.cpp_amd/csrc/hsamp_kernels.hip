@@ -151,6 +151,7 @@ struct Shared {
     int ired[4];
     u64 ured[4];
     u64 minv_w[4];
+    int fw[4];          // per-wave flags (k_pick)
     uint32_t hist[256];
     int soff[257];      // slice offsets during the merge
     int flags;
@@ -3139,9 +3140,8 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
     const RowPlan P = a.plans[r];
     const double ur = a.u[r];
     HSAMP_PHASE(8192 + r, 0);
-    // (nothing here waits for a load: u goes to LDS once the lists are in)
+    // (u goes to LDS once the lists are in)
     if (tid == 0) {
-        st.flags = 0;
         st.n = 0;
         st.nst = 0;
         st.theta = kThetaFloor;
@@ -3155,17 +3155,20 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
         st.expT[tid] = e;
     }
     st.hist[tid] = 0u;
-    __syncthreads();
-    HSAMP_PHASE(8192 + r, 1);
-    if (tid < S) {
-        st.soff[tid] = cnt_raw & 0x1FFFFFFF;
-        if (cnt_raw & (1 << 30)) atomicOr(&st.flags, 4);          // a NaN logit in the slice
-        if ((cnt_raw & 0x1FFFFFFF) > W) atomicOr(&st.flags, 8);   // a list past the window
+    // the lists' lengths, and per wave whether a slice saw a NaN logit (4) or
+    // a list runs past the window (8), all published by one barrier
+    if (tid < S) st.soff[tid] = cnt_raw & 0x1FFFFFFF;
+    {
+        const u64 bn = __ballot(tid < S && (cnt_raw & (1 << 30)) != 0);
+        const u64 bw = __ballot(tid < S && (cnt_raw & 0x1FFFFFFF) > W);
+        if (lane == 0) st.fw[wave_id()] = (bn != 0ull ? 4 : 0) | (bw != 0ull ? 8 : 0);
     }
     __syncthreads();
+    HSAMP_PHASE(8192 + r, 1);
+    const int fl0 = st.fw[0] | st.fw[1] | st.fw[2] | st.fw[3];
     const int k = P.top_k;
     const float inv_t = P.inv_temp;
-    const uint32_t rflags = (st.flags & 4) ? ROWF_NAN : 0u;
+    const uint32_t rflags = (fl0 & 4) ? ROWF_NAN : 0u;
     // the lists carry final logits before temperature: composites of the
     // scaled keys (sampler.cpp:101-106)
     auto scaled = [&](u64 c) -> u64 {
@@ -3180,8 +3183,10 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
         lm = max(lm, (uint32_t)(win[j] >> 32));
     }
     u64* list = reinterpret_cast<u64*>(smem);
-    if (st.flags & 8) {
+    if (fl0 & 8) {
         // buffer path: every entry offered under a rising threshold
+        if (tid == 0) st.flags = fl0;
+        __syncthreads();
         u64* ovf = a.ovf + (int64_t)r * a.ovf_cap;
         offer_regs<NW>(list, ovf, a.buf_cap, k, win, st);
         for (int sl = 0; sl < S; ++sl) {
@@ -3301,10 +3306,16 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
             };
             if (i0) bl[mb(mi0)] = m0;
             if (i1) bl[__popcll(mi0) + mb(mi1)] = m1;
+            if (lane == 0) bl[bcnt] = 0ull;   // pad to pairs
             wave_sync();
             const u64 e = (lane < bcnt) ? bl[lane] : 0ull;
             int q = 0;
-            for (int j = 0; j < bcnt; ++j) q += bl[j] > e;
+            const ulonglong2* b2 = reinterpret_cast<const ulonglong2*>(bl);
+#pragma unroll 4
+            for (int j = 0; j < (bcnt + 1) >> 1; ++j) {
+                const ulonglong2 x2 = b2[j];
+                q += (x2.x > e) + (x2.y > e);
+            }
             wave_sync();
             if (a0) st.wv[mb(ma0)] = m0;
             if (a1) st.wv[__popcll(ma0) + mb(ma1)] = m1;

@@ -1803,12 +1803,14 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
         R = raw_edge(max(sthr, kFloor), inv_t, P.temp);
     HSAMP_PHASE(slot, 7);
 
-    // C, D. the ids whose final raw key lies in [Rlo, Rhi)
+    // C, D. the ids whose final raw key lies in [Rlo, Rhi). Each wave stages
+    // its own chunks whose maximum reaches Rlo (as floats: a superset of the
+    // raw-key test, which orders -0 below +0) into its own LDS slots, in
+    // (chunk, lane) order from one ballot per chunk, and runs them one
+    // element per lane: no block barrier between staging and the pass.
+    constexpr int kCapW = kStageCap / (kBlock / 64);   // slots per wave and round
+    unsigned char* wst = stg + (uint32_t)wave_id() * (uint32_t)kCapW * 32u;
     auto pass = [&](uint32_t Rlo, uint32_t Rhi) {
-        // The chunks whose maximum reaches Rlo (as floats: a superset of the
-        // raw-key test, which orders -0 below +0), at positions in (chunk,
-        // lane) order from one ballot per chunk (kept in scalar registers)
-        // and a single LDS atomic per wave.
         const float Rf = key_to_float(Rlo);
         u64 mj[NC];
         int wj[NC];
@@ -1819,37 +1821,30 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
             wj[j] = wtot;
             wtot += __popcll(mj[j]);
         }
-        int base = 0;
-        if (lane == 0 && wtot > 0) base = atomicAdd(&st.nst, wtot);
-        base = __builtin_amdgcn_readfirstlane(base);
         HSAMP_PHASE(slot, 12);
-        auto stage = [&](int rb) {
-            // the wave's positions all within this round: no per-lane check
-            const bool all_in = base >= rb && base + wtot <= rb + kStageCap;
+        bool nanp = false;
+        for (int rb = 0; rb < wtot; rb += kCapW) {
+            // this round's chunks: positions [rb, rb + kCapW) of the wave's order
+            const bool all_in = rb == 0 && wtot <= kCapW;
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
                 const uint32_t p = __builtin_amdgcn_mbcnt_hi(
-                    (uint32_t)(mj[j] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mj[j], (uint32_t)(base + wj[j] - rb)));
-                if (cm[j] >= Rf && (all_in || p < (uint32_t)kStageCap)) {
-                    unsigned char* sp = stg + p * 32u;
+                    (uint32_t)(mj[j] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mj[j], (uint32_t)(wj[j] - rb)));
+                if (cm[j] >= Rf && (all_in || p < (uint32_t)kCapW)) {
+                    unsigned char* sp = wst + p * 32u;
                     *reinterpret_cast<uint4*>(sp) = raw[j];
                     *reinterpret_cast<int32_t*>(sp + 16) = lo + (j * kBlock + tid) * T::VW;
                 }
             }
-        };
-        stage(0);
-        __syncthreads();
-        HSAMP_PHASE(slot, 8);
-        const int nst = st.nst;
-        bool nanp = false;
-        for (int rb = 0;;) {
-            // VW threads per staged chunk, one element each; every lane runs
+            wave_sync();
+            HSAMP_PHASE(slot, 8);
+            // VW lanes per staged chunk, one element each; every lane runs
             // every step, so each step appends with one ballot and one atomic
-            const int ne = min(kStageCap, nst - rb) * T::VW;
-            for (int e1 = 0; e1 < ne; e1 += kBlock) {
-                const int e = e1 + tid;
+            const int ne = min(kCapW, wtot - rb) * T::VW;
+            for (int e1 = 0; e1 < ne; e1 += 64) {
+                const int e = e1 + lane;
                 const int ci = e / T::VW, c = e % T::VW;
-                const unsigned char* sp = stg + (uint32_t)min(ci, kStageCap - 1) * 32u;
+                const unsigned char* sp = wst + (uint32_t)min(ci, kCapW - 1) * 32u;
                 const int t = *reinterpret_cast<const int32_t*>(sp + 16) + c;
                 const int o = t - lo;
                 const uint32_t wsel = reinterpret_cast<const uint32_t*>(sp)[DT == 0 ? c : (c >> 1)];
@@ -1875,11 +1870,7 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
                             comp(kf, t);
                 }
             }
-            rb += kStageCap;
-            if (rb >= nst) break;
-            __syncthreads();
-            stage(rb);
-            __syncthreads();
+            wave_sync();   // the slots are read before the next round writes them
         }
         if (tl) {
             const uint32_t kf = final_raw_key(xt, tt_id, PEN ? (uint32_t)cnt[tt_id - lo] : 0u, one, a, P, nanp);
@@ -1895,12 +1886,7 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
     // below it): every id down to the floor
     if (PEN && st.n < k) {
         const uint32_t Rf = raw_edge(max(scaled_key(kFloor, inv_t), kFloor), inv_t, P.temp);
-        if (R > Rf) {
-            __syncthreads();
-            if (tid == 0) st.nst = 0;
-            __syncthreads();
-            pass(Rf, R);
-        }
+        if (R > Rf) pass(Rf, R);
     }
     if (nanv) atomicOr(&st.flags, 1);
     __syncthreads();

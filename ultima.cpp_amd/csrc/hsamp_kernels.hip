@@ -1684,7 +1684,40 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
     unsigned char* stg = smem + a.stage_off;
     constexpr uint32_t kFloor = (uint32_t)(kThetaFloor >> 32);
 
-    // A. chunk maxima, as the chunks arrive: IEEE maximum (NaN-propagating,
+    // A. the slice's history counts, while the tile is still on its way (the
+    // history row and the plan were asked for first). Exact lists run without
+    // DRY, so the scanned window is the larger of the
+    // repetition and frequency/presence windows; when those are equal (or one
+    // is off) a count entry is a plain count over it (one atomic per id).
+    const bool one = P.rep_win == 0 || P.fp_win == 0 || P.rep_win == P.fp_win;
+    if (PEN && pen) {
+        const int L = P.hist_len, p0 = L - P.scan_len;
+        const int mhi = min(a.vocab, lo + a.slice_len);
+        uint32_t* cw = reinterpret_cast<uint32_t*>(smem);
+        const uint32_t wl = (uint32_t)(L - p0), sl = (uint32_t)(mhi - lo);
+        if (one) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int p = pbase + q * kBlock + tid;   // pre[q]'s history position
+                const int32_t t = pre[q];
+                if ((uint32_t)(p - p0) < wl && (uint32_t)(t - lo) < sl)
+                    atomicAdd(&cw[(t - lo) >> 1], 1u << ((uint32_t)((t - lo) & 1) << 4));
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int p = pbase + q * kBlock + tid;
+                const int32_t t = pre[q];
+                if ((uint32_t)(p - p0) < wl && (uint32_t)(t - lo) < sl) {
+                    const int o = t - lo;
+                    const uint32_t sh = (uint32_t)(o & 1) << 4;
+                    if (p >= L - P.fp_win) atomicAdd(&cw[o >> 1], 1u << sh);
+                    if (p >= L - P.rep_win) atomicOr(&cw[o >> 1], XC_REP << sh);
+                }
+            }
+        }
+    }
+    // B. chunk maxima, as the chunks arrive: IEEE maximum (NaN-propagating,
     // -0 < +0 as raw keys order them), so that a NaN shows in its chunk's
     // maximum; such chunks then take the NaN-ignoring maximum of their other
     // ids (NaN ids count as -inf), after the loop
@@ -1735,38 +1768,6 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
         if (lo + (j * kBlock + tid) * T::VW >= hi) cm[j] = -__builtin_inff();
     HSAMP_PHASE(slot, 3);
 
-    // B. the slice's history counts (waits for the history loads) and the bound.
-    // Exact lists run without DRY, so the scanned window is the larger of the
-    // repetition and frequency/presence windows; when those are equal (or one
-    // is off) a count entry is a plain count over it (one atomic per id).
-    const bool one = P.rep_win == 0 || P.fp_win == 0 || P.rep_win == P.fp_win;
-    if (PEN && pen) {
-        const int L = P.hist_len, p0 = L - P.scan_len;
-        const int mhi = min(a.vocab, lo + a.slice_len);
-        uint32_t* cw = reinterpret_cast<uint32_t*>(smem);
-        const uint32_t wl = (uint32_t)(L - p0), sl = (uint32_t)(mhi - lo);
-        if (one) {
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const int p = pbase + q * kBlock + tid;   // pre[q]'s history position
-                const int32_t t = pre[q];
-                if ((uint32_t)(p - p0) < wl && (uint32_t)(t - lo) < sl)
-                    atomicAdd(&cw[(t - lo) >> 1], 1u << ((uint32_t)((t - lo) & 1) << 4));
-            }
-        } else {
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const int p = pbase + q * kBlock + tid;
-                const int32_t t = pre[q];
-                if ((uint32_t)(p - p0) < wl && (uint32_t)(t - lo) < sl) {
-                    const int o = t - lo;
-                    const uint32_t sh = (uint32_t)(o & 1) << 4;
-                    if (p >= L - P.fp_win) atomicAdd(&cw[o >> 1], 1u << sh);
-                    if (p >= L - P.rep_win) atomicOr(&cw[o >> 1], XC_REP << sh);
-                }
-            }
-        }
-    }
     HSAMP_PHASE(slot, 10);
     // the lane's largest chunk maximum as a raw key (cm is never NaN)
     float lmf = cm[0];

@@ -1813,30 +1813,30 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
     unsigned char* wst = stg + (uint32_t)wave_id() * (uint32_t)kCapW * 32u;
     auto pass = [&](uint32_t Rlo, uint32_t Rhi) {
         const float Rf = key_to_float(Rlo);
-        u64 mj[NC];
-        int wj[NC];
-        int wtot = 0;
-#pragma unroll
-        for (int j = 0; j < NC; ++j) {
-            mj[j] = __ballot(cm[j] >= Rf);
-            wj[j] = wtot;
-            wtot += __popcll(mj[j]);
-        }
-        HSAMP_PHASE(slot, 12);
-        bool nanp = false;
-        for (int rb = 0; rb < wtot; rb += kCapW) {
-            // this round's chunks: positions [rb, rb + kCapW) of the wave's order
-            const bool all_in = rb == 0 && wtot <= kCapW;
+        // the wave's chunks at positions [rb, rb + kCapW) of its order, the
+        // positions counted as the ballots go (nothing kept per chunk)
+        auto stage = [&](int rb) -> int {
+            int off = 0;
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
+                const bool in = cm[j] >= Rf;
+                const u64 m = __ballot(in);
                 const uint32_t p = __builtin_amdgcn_mbcnt_hi(
-                    (uint32_t)(mj[j] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mj[j], (uint32_t)(wj[j] - rb)));
-                if (cm[j] >= Rf && (all_in || p < (uint32_t)kCapW)) {
+                    (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, (uint32_t)(off - rb)));
+                if (in && p < (uint32_t)kCapW) {
                     unsigned char* sp = wst + p * 32u;
                     *reinterpret_cast<uint4*>(sp) = raw[j];
                     *reinterpret_cast<int32_t*>(sp + 16) = lo + (j * kBlock + tid) * T::VW;
                 }
+                off += __popcll(m);
             }
+            return off;
+        };
+        HSAMP_PHASE(slot, 12);
+        bool nanp = false;
+        const int wtot = stage(0);
+        for (int rb = 0; rb < wtot; rb += kCapW) {
+            if (rb > 0) stage(rb);
             wave_sync();
             HSAMP_PHASE(slot, 8);
             // VW lanes per staged chunk, one element each; every lane runs
@@ -1851,15 +1851,14 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
                 const uint32_t wsel = reinterpret_cast<const uint32_t*>(sp)[DT == 0 ? c : (c >> 1)];
                 float x = (DT == 0) ? __uint_as_float(wsel)
                                     : __uint_as_float((c & 1) ? (wsel & 0xFFFF0000u) : (wsel << 16));
-                uint32_t kf = 0u;
-                bool keep = false;
-                if (e < ne) {
-                    if (MASK && !((mbm[o >> 5] >> (o & 31)) & 1u)) x = -__builtin_inff();
-                    if ((VEC || t < hi) && raw_key(x) >= Rlo) {
-                        kf = final_raw_key(x, t, PEN ? (uint32_t)cnt[o] : 0u, one, a, P, nanp);
-                        keep = kf >= Rlo && kf < Rhi;
-                    }
-                }
+                // one branch, for the penalised ids; the rest is straight-line
+                const bool live = e < ne && (VEC || t < hi);
+                const uint32_t oc = min((uint32_t)o, (uint32_t)(a.slice_len - 1));
+                if (MASK && !((mbm[oc >> 5] >> (oc & 31)) & 1u)) x = -__builtin_inff();
+                uint32_t kf = raw_key(x);
+                const uint32_t h = PEN ? (uint32_t)cnt[oc] : 0u;
+                if (PEN && live && h != 0u && kf >= Rlo) kf = final_raw_key(x, t, h, one, a, P, nanp);
+                const bool keep = live && kf >= Rlo && kf < Rhi;
                 const u64 mk2 = __ballot(keep);
                 if (mk2 != 0ull) {
                     int ob = 0;

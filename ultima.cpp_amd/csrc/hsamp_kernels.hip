@@ -1891,6 +1891,8 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
     if (nanv) atomicOr(&st.flags, 1);
     __syncthreads();
     if (tid == 0) a.cand_n[slot] = st.n | ((st.flags & 1) ? (1 << 30) : 0);
+    // the rest of k_pick's window reads as empty (it then needs no lengths)
+    for (int i = st.n + tid; i < a.win; i += kBlock) out[i] = 0ull;
     HSAMP_PHASE(slot, 6);
 }
 
@@ -3160,12 +3162,12 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
     auto scaled = [&](u64 c) -> u64 {
         return ((u64)scaled_key((uint32_t)(c >> 32), inv_t) << 32) | (c & 0xFFFFFFFFull);
     };
+    // (k_stream leaves each window's entries past its list at 0, and the
+    // buffer resource reads 0 past the last slice)
     uint32_t lm = 0u;
 #pragma unroll
     for (int j = 0; j < NW; ++j) {
-        const int g = tid + j * kBlock;
-        const int sl = (int)__umulhi((uint32_t)g, a.win_magic);
-        win[j] = (sl >= S || g - sl * W >= st.soff[sl]) ? 0ull : scaled(win[j]);
+        win[j] = (win[j] != 0ull) ? scaled(win[j]) : 0ull;
         lm = max(lm, (uint32_t)(win[j] >> 32));
     }
     u64* list = reinterpret_cast<u64*>(smem);

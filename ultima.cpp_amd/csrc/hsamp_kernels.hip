@@ -3087,8 +3087,6 @@ template <int NW>
 __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ Shared st;
-    __shared__ StreamArgs sa;   // the buffer path's copies for select_and_finalize (not inlined)
-    __shared__ RowPlan sP;
     const int tid = threadIdx.x, lane = lane_id();
     uint32_t bid = blockIdx.x;
     // the launch arguments the first loads need, in registers together: one
@@ -3171,6 +3169,9 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
         lm = max(lm, (uint32_t)(win[j] >> 32));
     }
     u64* list = reinterpret_cast<u64*>(smem);
+    uint32_t bstar = 0u;
+    int shift = 0;
+    bool blk = false;   // the buffer path: the block ranks the buffer
     if (fl0 & 8) {
         // buffer path: every entry offered under a rising threshold
         if (tid == 0) st.flags = fl0;
@@ -3189,19 +3190,11 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
                 offer_regs<8>(list, ovf, a.buf_cap, k, c, st);
             }
         }
-        // LDS copies of the arguments and the plan, one dword per thread
-        // (a struct copy would go through per-lane scratch)
-        static_assert(sizeof(StreamArgs) % 4 == 0 && sizeof(StreamArgs) / 4 <= kBlock, "StreamArgs copy");
-        const uint32_t* kp = (const uint32_t*)__builtin_amdgcn_kernarg_segment_ptr();
-        if (tid < (int)(sizeof(StreamArgs) / 4)) reinterpret_cast<uint32_t*>(&sa)[tid] = kp[tid];
-        if (tid < (int)(sizeof(RowPlan) / 4))
-            reinterpret_cast<uint32_t*>(&sP)[tid] = reinterpret_cast<const uint32_t*>(a.plans + r)[tid];
+        // the buffer's entries are ranked by the block below
         if (tid == 0) st.u = ur;
         __syncthreads();
-        FinLds f{};
-        select_and_finalize(sa, sP, r, list, f, st, rflags);
-        return;
-    }
+        blk = true;
+    } else {
     // The k-th largest key's 8-bit bin under the prefix every candidate
     // shares (the block's key range), from a 256-bin LDS histogram; the
     // candidates in that bin or above go to the list.
@@ -3225,7 +3218,7 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
         kmx = max(kmx, (uint32_t)st.minv_w[i]);
     }
     const int hb = (kmx > kmn) ? 31 - __clz((int)(kmn ^ kmx)) : 0;
-    const int shift = max(0, hb - 7);
+    shift = max(0, hb - 7);
 #pragma unroll
     for (int j = 0; j < NW; ++j)
         if (win[j] != 0ull) atomicAdd(&st.hist[((uint32_t)(win[j] >> 32) >> shift) & 255u], 1u);
@@ -3246,7 +3239,7 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
     }
     __syncthreads();
     HSAMP_PHASE(8192 + r, 12);
-    const uint32_t bstar = (uint32_t)__builtin_amdgcn_readfirstlane(st.sel_d);
+    bstar = (uint32_t)__builtin_amdgcn_readfirstlane(st.sel_d);
     {
         // the candidates in the k-th's bin or above, packed into the list in
         // (slot, lane) order: one ballot per slot, one LDS atomic per wave
@@ -3270,13 +3263,15 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
     }
     if (tid == 0) st.u = ur;
     __syncthreads();
+    }
     HSAMP_PHASE(8192 + r, 3);
     int n = st.n;
-    if (n <= 128) {
+    int nk;   // wave 0: the row's top-k set in st.wv[0, nk), any order
+    if (!blk && n <= 128) {
         // Wave 0 holds the n entries (two per lane). Those above the k-th's
         // bin are all in; the ones in it (bcnt) are packed aside, ranked among
         // themselves (composite order, ties to the lower id) and the best
-        // bneed join. More than 64 in the bin: the full rank below.
+        // bneed join. More than 64 in the bin: every entry is ranked.
         if (tid >= 64) return;
         const u64 m0 = (lane < n) ? list[lane] : 0ull;
         const u64 m1 = (lane + 64 < n) ? list[lane + 64] : 0ull;
@@ -3308,45 +3303,40 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
             if (a0) st.wv[mb(ma0)] = m0;
             if (a1) st.wv[__popcll(ma0) + mb(ma1)] = m1;
             if (lane < bcnt && q < bneed) st.wv[above + q] = e;
+            nk = min(k, above + min(bneed, bcnt));
+        } else {
+            // rank = entries above, over the (distinct) entries
+            if (lane == 0) list[n] = 0ull;   // pad to pairs
             wave_sync();
-            const int nk = min(k, above + min(bneed, bcnt));
-            const u64 c = (lane < nk) ? st.wv[lane] : 0ull;
-            wave_sync();
-            HSAMP_PHASE(8192 + r, 4);
-            wave_finalize(a, P, r, c, nk, rflags, st);
-            HSAMP_PHASE(8192 + r, 5);
-            return;
-        }
-        // wave 0 ranks the (distinct) entries exactly: rank = entries above
-        if (lane == 0) list[n] = 0ull;   // pad to pairs
-        wave_sync();
-        int q0 = 0, q1 = 0;
-        const ulonglong2* l2 = reinterpret_cast<const ulonglong2*>(list);
+            int q0 = 0, q1 = 0;
+            const ulonglong2* l2 = reinterpret_cast<const ulonglong2*>(list);
 #pragma unroll 4
-        for (int j = 0; j < (n + 1) >> 1; ++j) {
-            const ulonglong2 x2 = l2[j];
-            q0 += (x2.x > m0) + (x2.y > m0);
-            q1 += (x2.x > m1) + (x2.y > m1);
+            for (int j = 0; j < (n + 1) >> 1; ++j) {
+                const ulonglong2 x2 = l2[j];
+                q0 += (x2.x > m0) + (x2.y > m0);
+                q1 += (x2.x > m1) + (x2.y > m1);
+            }
+            wave_sync();
+            if (lane < n && q0 < k) st.wv[q0] = m0;
+            if (lane + 64 < n && q1 < k) st.wv[q1] = m1;
+            nk = min(k, n);
         }
         wave_sync();
-        if (lane < n && q0 < k) st.wv[q0] = m0;
-        if (lane + 64 < n && q1 < k) st.wv[q1] = m1;
-        wave_sync();
-        const int nk = min(k, n);
-        const u64 c = (lane < nk) ? st.wv[lane] : 0ull;
-        wave_sync();
-        wave_finalize(a, P, r, c, nk, rflags, st);
-        return;
+    } else {
+        if (n > 256) {
+            buf_compact(list, k, st);
+            n = st.n;
+        }
+        block_rank_topk(list, n, k, st);
+        if (tid >= 64) return;
+        nk = min(k, n);
     }
-    if (n > 256) {
-        buf_compact(list, k, st);
-        n = st.n;
-    }
-    block_rank_topk(list, n, k, st);
-    if (tid >= 64) return;
-    const int nk = min(k, n);
+    // one finalize for every path
     const u64 c = (lane < nk) ? st.wv[lane] : 0ull;
+    wave_sync();
+    HSAMP_PHASE(8192 + r, 4);
     wave_finalize(a, P, r, c, nk, rflags, st);
+    HSAMP_PHASE(8192 + r, 5);
 }
 
 // ---- writeback -------------------------------------------------------------------

@@ -1164,6 +1164,15 @@ __device__ __forceinline__ void wave_finalize(const StreamArgs& a, const RowPlan
     int32_t tok = 0;
     const u64 km = have ? __ballot(keep) : 0ull;
     if (have) {
+        // the kept set and its probabilities go out ahead of the draw
+        const int pos = __popcll(km & ((1ull << lane) - 1ull));
+        if (keep) {
+            if (a.kept_idx != nullptr && pos < a.set_cap) {
+                a.kept_idx[(int64_t)r * a.set_cap + pos] = (int32_t)id;
+                a.kept_prob[(int64_t)r * a.set_cap + pos] = p;
+            }
+            if (a.fin_idx != nullptr && pos < a.fin_cap) a.fin_idx[(int64_t)r * a.fin_cap + pos] = (int32_t)id;
+        }
         // sampler.cpp:178-182 / discrete_distribution: double sum, q, partial sums
         HSAMP_PHASE(8192 + r, 8);
         const double pd = keep ? (double)p : 0.0;
@@ -1206,14 +1215,6 @@ __device__ __forceinline__ void wave_finalize(const StreamArgs& a, const RowPlan
         if (near <= 1e-6) rflags |= ROWF_CDF_NEAR;
         HSAMP_PHASE(8192 + r, 10);
         tok = t;
-        const int pos = __popcll(km & ((1ull << lane) - 1ull));
-        if (keep) {
-            if (a.kept_idx != nullptr && pos < a.set_cap) {
-                a.kept_idx[(int64_t)r * a.set_cap + pos] = (int32_t)id;
-                a.kept_prob[(int64_t)r * a.set_cap + pos] = p;
-            }
-            if (a.fin_idx != nullptr && pos < a.fin_cap) a.fin_idx[(int64_t)r * a.fin_cap + pos] = (int32_t)id;
-        }
     }
     const int nkept = __popcll(km);
     if (nkept == 0) {

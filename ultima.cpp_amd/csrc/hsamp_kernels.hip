@@ -3126,20 +3126,15 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     const RowPlan P = a.plans[r];
     const double ur = a.u[r];
+    // expf's table, loaded after the lists (its wait then costs nothing) and
+    // put in LDS once they are in
+    const uint64_t etab = kExpT[tid & 31];
     HSAMP_PHASE(8192 + r, 0);
     // (u goes to LDS once the lists are in)
     if (tid == 0) {
         st.n = 0;
         st.nst = 0;
         st.theta = kThetaFloor;
-    }
-    if (tid < 32) {
-        // expf's table from immediates (an indexed read would wait for every
-        // load issued so far)
-        uint64_t e = 0ull;
-#pragma unroll
-        for (int i = 0; i < 32; ++i) e = (tid == i) ? kExpT[i] : e;
-        st.expT[tid] = e;
     }
     st.hist[tid] = 0u;
     // the lists' lengths, and per wave whether a slice saw a NaN logit (4) or
@@ -3169,6 +3164,7 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
         win[j] = (win[j] != 0ull) ? scaled(win[j]) : 0ull;
         lm = max(lm, (uint32_t)(win[j] >> 32));
     }
+    if (tid < 32) st.expT[tid] = etab;   // read by wave 0 after later barriers
     u64* list = reinterpret_cast<u64*>(smem);
     uint32_t bstar = 0u;
     int shift = 0;

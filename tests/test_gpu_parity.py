@@ -164,6 +164,36 @@ def test_uniform_edges(sampler, wl, kernel_mode):
     compare_rows(w, g)
 
 
+def test_u_on_and_beside_cdf_boundaries(sampler, wl, kernel_mode):
+    """u placed exactly on, and 1e-12 either side of, interior partial sums
+    of the reference's CDF (double sum S of the kept p in index order,
+    q = p / S, sequential partial sums): the finalize must leave its tree
+    fast path for the reference's sequential sums there, and every token must
+    match (or be flagged CDF_NEAR within 1e-6, the one tolerated mismatch)."""
+    rng = np.random.default_rng(123)
+    V = 151936
+    base = rng.normal(0, 1.5, size=(1, V)).astype(np.float32)
+    params = wl.identity_params(top_k=20, temperature=0.9)
+    probe = _wl_from(wl, base, [params], [0.5])
+    tr = O.sample_row(probe.logits_f32()[0], params, hist=None, mask=None, bias=None, u=0.5)
+    p = tr.kept_prob.astype(np.float64)
+    S = 0.0
+    for v in p:
+        S += v
+    cp, acc = [], 0.0
+    for v in p:
+        acc += v / S
+        cp.append(acc)
+    us = []
+    for j in (0, 3, 9, 15):
+        for d in (0.0, 1e-12, -1e-12):
+            us.append(min(max(cp[j] + d, 0.0), 1.0 - 2.0**-53))
+    B = len(us)
+    w = _wl_from(wl, np.repeat(base, B, axis=0), [params] * B, us)
+    g = run_gpu(sampler, w)
+    assert compare_rows(w, g) == B
+
+
 @pytest.mark.parametrize("V", [2, 5, 31, 33, 1000, 50257])
 def test_small_and_unaligned_vocab(sampler, wl, V, kernel_mode):
     rng = np.random.default_rng(V)

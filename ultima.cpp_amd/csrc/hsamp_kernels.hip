@@ -1176,8 +1176,6 @@ __device__ __forceinline__ void wave_finalize(const StreamArgs& a, const RowPlan
         // sampler.cpp:178-182 / discrete_distribution: double sum, q, partial sums
         HSAMP_PHASE(8192 + r, 8);
         const double pd = keep ? (double)p : 0.0;
-        const double S = wave_seq_sum_d(pd, wv);
-        const double q = keep ? pd / S : 0.0;
         HSAMP_PHASE(8192 + r, 9);
         int32_t t = V - 1;
         double near = 1.0;
@@ -1186,11 +1184,13 @@ __device__ __forceinline__ void wave_finalize(const StreamArgs& a, const RowPlan
         } else if (!(u > 0.0)) {
             t = 0;
         } else {
-            // the partial sums from a tree prefix (within 1e-14 of the
-            // sequential ones) when every comparison that decides the token
+            // the partial sums as a tree prefix of p over its tree total
+            // (within 1e-13 of the reference's sequential q = p / S and
+            // partial sums of q) when every comparison that decides the token
             // and the CDF_NEAR flag is clear of u by 2e-6, else the
-            // reference's sequential sums
-            double cp = wave_tree_prefix_d(q);
+            // reference's sequential sum, quotients and partial sums
+            const double pp = wave_tree_prefix_d(pd);
+            double cp = pp / readlane_d(pp, 63);
             {
                 const double cja = (keep && (int32_t)id == V - 1) ? 1.0 : cp;
                 const u64 h0 = __ballot(keep && cja >= u);
@@ -1199,7 +1199,10 @@ __device__ __forceinline__ void wave_finalize(const StreamArgs& a, const RowPlan
                 const double before = (j0 > 0) ? readlane_d(cp, min(j0, 64) - 1) : -1.0;
                 const bool clear = fabs(at - u) > 2e-6 && (j0 > 0 ? fabs(before - u) > 2e-6 : true) &&
                                    (j0 < 64 ? true : fabs(1.0 - u) > 2e-6);
-                if (!clear) cp = wave_seq_prefix_d(q, wv);
+                if (!clear) {
+                    const double S = wave_seq_sum_d(pd, wv);
+                    cp = wave_seq_prefix_d(keep ? pd / S : 0.0, wv);
+                }
             }
             const double cj = (keep && (int32_t)id == V - 1) ? 1.0 : cp;
             const u64 hit = __ballot(keep && cj >= u);

@@ -1597,8 +1597,8 @@ __device__ __forceinline__ void stream_sample(const StreamArgs& a, const RowPlan
 // pass over the tile is lean:
 //  A. as each 16-byte chunk arrives: the chunk's float maximum (v_max ignores
 //     NaN) and one NaN test per two elements; nothing per element else.
-//  B. the bound: each wave's kw-th largest lane maximum (kw = ceil((k+8)/4),
-//     low 16 bits cleared), minimum over the waves: B, with at least k + 8
+//  B. the bound: each wave's kw-th largest lane maximum (kw = ceil((k+4)/4),
+//     low 16 bits cleared), minimum over the waves: B, with at least k + 4
 //     ids of the slice at or above it. ths = B's scaled key; every id whose
 //     final key is below ths is beaten by them (if at least k of them keep a
 //     final key >= ths, checked at the end) and left out. R = raw_edge(ths)
@@ -1779,7 +1779,7 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
     for (int j = 1; j < NC; ++j) lmf = __builtin_elementwise_maximum(lmf, cm[j]);
     const uint32_t lk = raw_key(lmf);
     const int k = P.top_k;
-    const int kw = (k + 8 + 3) >> 2;   // <= 18
+    const int kw = (k + 4 + 3) >> 2;   // <= 17
     const uint32_t g4[4] = {lk, 0u, 0u, 0u};
     const uint32_t tw = wave_kth_bound16(g4, 1, kw);
     if (lane == 0) st.twave[wave_id()] = tw;

@@ -1,26 +1,36 @@
-"""Benchmark of the MI355X token sampler.
+"""Benchmark of the MI355X token sampler on a BASELINE configuration.
 
-One step = one launch of the sampler over one [B=64, V=151936] fp32 batch:
-penalties from 2048-id histories (rep 1.1, frequency 0.5, presence 0.3),
-temperature 0.7, top-k 50, softmax and the draw. Inputs are seeded synthetic
-data, resident in HBM before timing. Eight distinct input sets (315 MB, more
-than the 256 MB Infinity Cache) rotate so the kernel streams from HBM.
+Default: configuration 2, the headline. One step = one launch of the sampler
+over one [B=64, V=151936] fp32 batch: penalties from 2048-id histories (rep
+1.1, frequency 0.5, presence 0.3), temperature 0.7, top-k 50, softmax and the
+draw. `--config N` runs configuration N (1-5) the same way. Inputs are seeded
+synthetic data, resident in HBM before timing. Eight distinct input sets
+rotate (315 MB for configuration 2, more than the 256 MB Infinity Cache) so
+that the kernels stream from HBM.
 
-The launches of one rotation are captured into a HIP graph (torch.cuda.CUDAGraph)
-and replayed; HIP events on the launch stream bracket the K timed steps. A
-second graph of the same launches with only the pass over the logits (the
-library's STREAM_ONLY diagnostics flag), timed the same way, gives the stream
-kernel's own duration (the merge takes the rest of the step); the roofline
-figure is the stream kernel's algorithmic bytes over that duration.
-Prints one JSON line (see `main`). The CPU baseline is the reference's own
-sampler (oracle/_ref, compiled from its sources) or, where that was not
-built, the CPU restatement, timed on this host's cores on a bounded sample.
+Timing: the launches of one rotation are captured into a HIP graph
+(torch.cuda.CUDAGraph), plus a graph of the first K % 8 sets, so that exactly
+`--warmup` untimed and `--steps` timed steps run; HIP events on the launch
+stream bracket the timed steps. The same is done for
+  * the stream kernel alone (the library's STREAM_ONLY diagnostics flag): its
+    own duration, over which `roofline.achieved` is the algorithmic bytes;
+  * a plain read of the same bytes with the stream kernel's launch shape
+    (ultima_hsamp_read_probe): `roofline.ceiling_gbs`, the floor for this grid;
+  * uncaptured calls of ultima_hsamp_run through the C ABI (host submission
+    included): `config.uncaptured`.
+Prints one JSON line. The CPU baseline is the reference's own sampler
+(oracle/_ref, compiled from its sources) or, where that was not built, the
+CPU restatement, timed on this host's cores on a bounded sample: median of
+repetitions on N threads and on one thread, plus a per-stage breakdown from
+the restatement's stage clock.
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -33,6 +43,9 @@ sys.path.insert(0, str(ROOT))
 METRIC = "sampled rows/sec at B=64,V=151936 fp32; achieved HBM GB/s vs peak"
 PEAK_GBS = 8000.0
 N_SETS = 8
+# the kernel that reads the logits, and the per-row kernel after it, by configuration
+STREAM_KERNEL = {1: "k_stream", 2: "k_stream", 3: "k_full", 4: "k_stream", 5: "k_stream"}
+ROW_KERNEL = {1: "k_pick", 2: "k_pick", 3: None, 4: "k_pick", 5: "k_merge"}
 
 
 def parse():
@@ -40,50 +53,133 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=40)
-    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 4, 5])
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-seconds", type=float, default=1.5,
-                    help="wall seconds of the CPU baseline sample (all threads)")
+    ap.add_argument("--cpu-reps", type=int, default=7, help="timed repetitions of each CPU leg (median)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="also run 3 device-to-device copies of this many MiB (a known-size "
                          "kernel that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
 
 
-def cpu_baseline(wl, seconds: float):
-    """The reference sampler on this host, rows split over the host's cores."""
+def host_threads() -> int:
+    """Threads the CPU baseline may use: this process's CPU share (the GPU box
+    exports it as OMP_NUM_THREADS), else the CPUs it may run on."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        return int(env)
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
+def cpu_baseline(wl, reps: int):
+    """The reference sampler on this host: rows/s on N threads (whole batch,
+    static row split) and on one thread (a sample of rows), medians of `reps`
+    timed repetitions after one untimed pass; per-stage breakdown from the
+    restatement's clock on the one-thread sample."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle as O  # the checker / baseline, never the product
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = host_threads()
     kind = "reference" if O.ref_available() else "port"
     x0 = wl.logits_f32()
     hist = wl.hist if wl.hist is not None else np.zeros((wl.rows, 1), np.int32)
     hl = wl.hist_len if wl.hist_len is not None else np.zeros(wl.rows, np.int64)
     seeds = np.arange(wl.rows, dtype=np.uint64) + 1
-    timed, rows, passes = 0.0, 0, 0
-    while timed < seconds or passes < 2:
-        x = x0.copy()
+
+    def one_pass(rows, nthreads):
+        x = x0[:rows].copy()
         t0 = time.perf_counter()
         if kind == "reference":
-            O.ref_sample_batch(x, wl.params, hist, hl, seeds, nthreads=threads)
+            O.ref_sample_batch(x, wl.params[:rows], hist[:rows], hl[:rows], seeds[:rows], nthreads=nthreads)
         else:
-            O.sample_batch(x, wl.params, hist, hl, wl.mask, wl.u, nthreads=threads)
-        timed += time.perf_counter() - t0
-        rows += wl.rows
-        passes += 1
-    return {"value": rows / timed, "unit": "rows/s", "cores": threads, "kind": kind,
-            "sample": f"{passes} passes over the {wl.rows}-row {wl.name} batch "
-                      f"({rows} rows, {timed:.2f} s wall on {threads} threads)"}
+            O.sample_batch(x, wl.params[:rows], hist[:rows], hl[:rows], None if wl.mask is None else wl.mask[:rows],
+                           wl.u[:rows], nthreads=nthreads)
+        return time.perf_counter() - t0
+
+    def median_rate(rows, nthreads):
+        one_pass(rows, nthreads)                     # warm-up
+        rates = [rows / one_pass(rows, nthreads) for _ in range(reps)]
+        return statistics.median(rates), rates
+
+    rows_n = wl.rows
+    rate_n, all_n = median_rate(rows_n, threads)
+    rows_1 = min(wl.rows, 16)
+    rate_1, all_1 = median_rate(rows_1, 1)
+    xs = x0[:rows_1].copy()
+    _, st = O.sample_batch_stages(xs, wl.params[:rows_1], hist[:rows_1], hl[:rows_1],
+                                  None if wl.mask is None else wl.mask[:rows_1], wl.u[:rows_1])
+    return {"value": rate_n, "unit": "rows/s", "cores": threads, "kind": kind,
+            "threads": threads, "hardware_concurrency": os.cpu_count(),
+            "sample": f"median of {reps} timed passes (after one untimed) over the {rows_n}-row {wl.name} "
+                      f"batch on {threads} threads (static row split); one thread: {rows_1} rows",
+            "reps_rows_per_s": [round(r, 1) for r in all_n],
+            "single_thread": {"value": rate_1, "unit": "rows/s", "rows": rows_1,
+                              "reps_rows_per_s": [round(r, 1) for r in all_1]},
+            "stages": {"kind": "port", "unit": "us/row", "rows": rows_1,
+                       **{k: round(v / rows_1 * 1e6, 2) for k, v in st.items()}}}
 
 
-def traffic_from_profiles(cfg: int):
-    f = ROOT / "profiles" / f"k_stream_cfg{cfg}_traffic.json"
+def traffic_from_profiles(kernel: str, cfg: int):
+    f = ROOT / "profiles" / f"{kernel}_cfg{cfg}_traffic.json"
     if f.exists():
         try:
-            return json.loads(f.read_text()).get("hbm_bytes_per_launch")
+            return json.loads(f.read_text()).get("hbm_bytes_per_launch"), f.name
         except (ValueError, OSError):
-            return None
-    return None
+            return None, None
+    return None, None
+
+
+class Timer:
+    """Graphs of one rotation (and of its first r launches) replayed so that
+    exactly n launches run; HIP events on the stream time them."""
+
+    def __init__(self, torch, stream, launch):
+        self.torch, self.stream, self.launch = torch, stream, launch
+        self.graphs = {}
+
+    def graph(self, n):
+        if n not in self.graphs:
+            g = self.torch.cuda.CUDAGraph()
+            with self.torch.cuda.graph(g, stream=self.stream):
+                for i in range(n):
+                    self.launch(i, self.stream)
+            self.stream.synchronize()
+            self.graphs[n] = g
+        return self.graphs[n]
+
+    def run(self, n):
+        full, rem = divmod(n, N_SETS)
+        with self.torch.cuda.stream(self.stream):
+            for _ in range(full):
+                self.graph(N_SETS).replay()
+            if rem:
+                self.graph(rem).replay()
+
+    def time(self, n, warmup):
+        torch = self.torch
+        self.graph(N_SETS)
+        if n % N_SETS:
+            self.graph(n % N_SETS)
+        if warmup % N_SETS:
+            self.graph(warmup % N_SETS)
+        self.run(warmup)
+        self.stream.synchronize()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        wall0 = time.perf_counter()
+        with torch.cuda.stream(self.stream):
+            e0.record(self.stream)
+        self.run(n)
+        with torch.cuda.stream(self.stream):
+            e1.record(self.stream)
+        self.stream.synchronize()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1), time.perf_counter() - wall0
+
+    def drop(self):
+        self.graphs.clear()
 
 
 def main():
@@ -99,8 +195,9 @@ def main():
     wlm, hs = pkg.workloads, pkg.hsamp
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    cfg = args.config
 
-    sets = [wlm.config(args.config, seed=100 + i) for i in range(N_SETS)]
+    sets = [wlm.config(cfg, seed=100 + i) for i in range(N_SETS)]
     wl0 = sets[0]
     B, V = wl0.rows, wl0.vocab
     to_dev = []
@@ -118,117 +215,135 @@ def main():
     outs = [{"token": torch.empty(B, dtype=torch.int32, device=dev),
              "row_flags": torch.empty(B, dtype=torch.int32, device=dev)} for _ in sets]
 
-    def launch(i, s):
+    def launch(i, s, stream_only=False):
         x, u, h, m = to_dev[i]
         sampler.run(x, sets[i].params, u, hist=h, hist_len=sets[i].hist_len, mask=m,
-                    outputs=outs[i], stream=s)
+                    outputs=outs[i], stream=s, stream_only=stream_only)
 
     with torch.cuda.stream(stream):
         for i in range(N_SETS):          # uncaptured first run: uploads knobs, sizes scratch
             launch(i, stream)
     stream.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        for i in range(N_SETS):
-            launch(i, stream)
-    stream.synchronize()
+    first_tok = [o["token"].clone() for o in outs]
 
-    reps_w = max(1, args.warmup // N_SETS)
-    reps = max(1, args.steps // N_SETS)
-    steps = reps * N_SETS
-    with torch.cuda.stream(stream):
-        for _ in range(reps_w):
-            graph.replay()
-    stream.synchronize()
-    torch.cuda.synchronize()
-    t0e = torch.cuda.Event(enable_timing=True)
-    t1e = torch.cuda.Event(enable_timing=True)
-    wall0 = time.perf_counter()
-    with torch.cuda.stream(stream):
-        t0e.record(stream)
-        for _ in range(reps):
-            graph.replay()
-        t1e.record(stream)
-    stream.synchronize()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    ms_total = t0e.elapsed_time(t1e)
-    ms_step = ms_total / steps
+    step = Timer(torch, stream, launch)
+    ms_total, wall = step.time(args.steps, args.warmup)
+    ms_step = ms_total / args.steps
+    step.drop()
 
-    # Per-kernel split, live: a second graph holds the same launches with only
-    # the pass over the logits (k_stream; the library's STREAM_ONLY
-    # diagnostics flag), replayed between events like the full step; the
-    # per-row merge (k_pick or k_merge) takes the rest of the step.
-    def launch_stream_only(i, s):
-        x, u, h, m = to_dev[i]
-        sampler.run(x, sets[i].params, u, hist=h, hist_len=sets[i].hist_len, mask=m,
-                    outputs=outs[i], stream=s, stream_only=True)
+    # the kernel that reads the logits, alone (the per-row kernel takes the
+    # rest of the step); configuration 3 runs one kernel, k_full
+    sk = STREAM_KERNEL[cfg]
+    if sk == "k_stream":
+        only = Timer(torch, stream, lambda i, s: launch(i, s, stream_only=True))
+        stream_ms = only.time(args.steps, args.warmup)[0] / args.steps
+        only.drop()
+    else:
+        stream_ms = ms_step
+    row_ms = ms_step - stream_ms
 
-    sgraph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(sgraph, stream=stream):
-        for i in range(N_SETS):
-            launch_stream_only(i, stream)
-    stream.synchronize()
-    with torch.cuda.stream(stream):
-        for _ in range(reps_w):
-            sgraph.replay()
-    stream.synchronize()
-    s0e = torch.cuda.Event(enable_timing=True)
-    s1e = torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(stream):
-        s0e.record(stream)
-        for _ in range(reps):
-            sgraph.replay()
-        s1e.record(stream)
-    stream.synchronize()
-    n_split = reps * N_SETS
-    stream_ms = s0e.elapsed_time(s1e) / n_split
-    merge_ms = ms_step - stream_ms
-    del sgraph
+    # the same bytes read plainly with the stream kernel's launch shape
+    ceiling_ms = None
+    if sk == "k_stream":
+        probe_out = torch.empty(B * 256, dtype=torch.float32, device=dev)
 
-    # The replayed outputs are the real ones: spot-check them against an
-    # uncaptured launch of the same inputs.
-    ref_tok = [o["token"].clone() for o in outs]
-    with torch.cuda.stream(stream):
-        for i in range(N_SETS):
-            launch(i, stream)
-    stream.synchronize()
+        def probe(i, s):
+            x, u, h, m = to_dev[i]
+            sampler.read_probe(x, sets[i].params, u, probe_out, hist=h, hist_len=sets[i].hist_len, mask=m, stream=s)
+        try:
+            pt = Timer(torch, stream, probe)
+            ceiling_ms = pt.time(args.steps, args.warmup)[0] / args.steps
+            pt.drop()
+        except hs.HsampError:
+            ceiling_ms = None
+
+    # The replayed outputs are the real ones: they equal the first, uncaptured
+    # launch of the same inputs.
     for i in range(N_SETS):
-        if not torch.equal(ref_tok[i], outs[i]["token"]):
+        if not torch.equal(first_tok[i], outs[i]["token"]):
             raise SystemExit("graph replay and direct launch disagree")
 
+    # uncaptured calls through the C ABI: prepared batches, one ctypes call each
+    L = hs.lib()
+    prepared = []
+    for i in range(N_SETS):
+        x, u, h, m = to_dev[i]
+        prepared.append(sampler.batch(x, sets[i].params, u, hist=h, hist_len=sets[i].hist_len, mask=m,
+                                      outputs=outs[i]))
+    sptr = ctypes.c_void_p(stream.cuda_stream)
+    n_unc = min(args.steps, 1000)
+    for i in range(N_SETS):
+        hs.check(L.ultima_hsamp_run(sampler.h, ctypes.byref(prepared[i][0]), sptr), "run")
+    stream.synchronize()
+    u0, u1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        u0.record(stream)
+    t0 = time.perf_counter()
+    for j in range(n_unc):
+        st = L.ultima_hsamp_run(sampler.h, ctypes.byref(prepared[j % N_SETS][0]), sptr)
+        if st != 0:
+            hs.check(st, "run")
+    host_s = time.perf_counter() - t0
+    with torch.cuda.stream(stream):
+        u1.record(stream)
+    stream.synchronize()
+    unc_ms = u0.elapsed_time(u1) / n_unc
+
+    # configuration 1 through the host-row entry (sample() of the drop-in):
+    # the row's 608 KB host-to-device copy and a synchronisation included
+    host_row_us = None
+    if cfg == 1:
+        w = sets[0]
+        hist1 = None if w.hist is None else w.hist[0][: int(w.hist_len[0])]
+        lat = []
+        for j in range(200):
+            t0 = time.perf_counter()
+            sampler.sample_host(w.logits[0], w.params[0], hist=hist1, u=float(w.u[0]))
+            lat.append(time.perf_counter() - t0)
+        host_row_us = statistics.median(lat[20:]) * 1e6
+
     algo_bytes = wl0.algorithmic_bytes()
-    # the per-row merge kernel these batches take: k_pick after exact lists
-    # (every row samples with top-k <= 64), k_merge for the general kernels
-    exact_on = os.environ.get("ULTIMA_HSAMP_EXACT", "1")[:1] != "0"
-    merge_name = "k_pick" if (exact_on and args.config in (1, 2, 4)) else "k_merge"
-    achieved = algo_bytes / (stream_ms * 1e-3) / 1e9   # k_stream: the kernel that reads the logits
+    achieved = algo_bytes / (stream_ms * 1e-3) / 1e9
+    traffic, traffic_src = traffic_from_profiles(sk, cfg)
+    rk = ROW_KERNEL[cfg]
+    kern_us = {sk: round(stream_ms * 1e3, 3)}
+    if rk:
+        kern_us[rk] = round(row_ms * 1e3, 3)
+    desc = {1: "hist 64 rep 1.1 T .8 top-k 40 top-p .95",
+            2: "hist 2048 rep 1.1 freq .5 pres .3 T .7 top-k 50",
+            3: "half N(0,1) + 16 spikes at 15, half N(0,.1); T 1 top-p .9 over V",
+            4: "1% allowed-token mask, T 1 top-k 20 top-p .8",
+            5: "per-row T U[.2,1.5] top-k 1..1000 top-p U[.5,1] rep U[1,1.3] over 512 ids"}[cfg]
     line = {
         "metric": METRIC,
         "value": B / (ms_step * 1e-3),
         "unit": "rows/s",
         "n_gpus": 1,
-        "steps": steps,
-        "warmup": reps_w * N_SETS,
+        "steps": args.steps,
+        "warmup": args.warmup,
         "ms_per_step": ms_step,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32" if wl0.dtype == "f32" else "bf16",
         "data": "synthetic (seeded SplitMix64/Box-Muller logits and histories, 8 rotating sets)",
-        "config": {"workload": f"cfg{args.config}: B={B} V={V} {wl0.dtype} "
-                               + ("hist 2048 rep 1.1 freq .5 pres .3 T .7 top-k 50"
-                                  if args.config == 2 else wl0.name),
+        "config": {"workload": f"cfg{cfg}: B={B} V={V} {wl0.dtype} {desc}",
                    "rows": B, "vocab": V, "input_sets": N_SETS,
                    "bytes_per_step": algo_bytes, "wall_s": round(wall, 4),
-                   "kernel_us": {"k_stream": round(stream_ms * 1e3, 3), merge_name: round(merge_ms * 1e3, 3),
-                                 "launches_timed": n_split},
-                   "step_hbm_gbs": round(algo_bytes / (ms_step * 1e-3) / 1e9, 1)},
+                   "kernel_us": kern_us,
+                   "step_hbm_gbs": round(algo_bytes / (ms_step * 1e-3) / 1e9, 1),
+                   "uncaptured": {"us_per_step": round(unc_ms * 1e3, 3),
+                                  "host_us_per_call": round(host_s / n_unc * 1e6, 3),
+                                  "calls": n_unc}},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / PEAK_GBS, "traffic": traffic_from_profiles(args.config),
-                     "kernel": "k_stream", "algorithmic_bytes_per_launch": algo_bytes},
+                     "frac": achieved / PEAK_GBS, "traffic": traffic, "traffic_source": traffic_src,
+                     "kernel": sk, "algorithmic_bytes_per_launch": algo_bytes,
+                     "ceiling_gbs": None if ceiling_ms is None else algo_bytes / (ceiling_ms * 1e-3) / 1e9,
+                     "ceiling_us": None if ceiling_ms is None else round(ceiling_ms * 1e3, 3)},
         "cpu_baseline": None,
     }
+    if host_row_us is not None:
+        line["config"]["host_row_us"] = round(host_row_us, 2)
     if args.copy_probe_mib > 0:
         n = args.copy_probe_mib * (1 << 20) // 4
         src = torch.ones(n, dtype=torch.float32, device=dev)
@@ -237,9 +352,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         line["config"]["copy_probe_bytes"] = n * 4
-    if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(wl0, args.cpu_seconds)
     sampler.close()
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(wl0, max(5, args.cpu_reps))
     print(json.dumps(line), flush=True)
 
 

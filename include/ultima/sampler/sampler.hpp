@@ -71,9 +71,10 @@ private:
 // Apply the transform ladder to `logits` and return the sampled id; -1 when
 // `logits` is empty or the GPU backend fails (reference sampler.hpp:83-85).
 // Draws the uniform from ctx.rng() exactly when the reference does (T > 0 and
-// at least two logits). `logits` is left unchanged unless in-place writeback
-// is enabled with set_inplace_writeback(true), in which case it ends in the
-// state the reference leaves it in.
+// at least two logits). Like the reference, `logits` is transformed in place:
+// it ends in the state the reference's sample() leaves it in (penalised and
+// scaled, ids outside the kept set at -inf). set_inplace_writeback(false)
+// leaves it unchanged instead, for callers that never read it afterwards.
 TokenId sample(std::span<float> logits,
                const SamplerParams& params,
                SamplerContext&      ctx);
@@ -84,7 +85,9 @@ TokenId argmax(std::span<const float> logits) noexcept;
 // ---- Additions of this build (no reference counterpart) --------------------
 
 // Whether sample() copies the transformed logits back into the caller's
-// buffer. Off by default: no reference caller reads them after the call.
+// buffer. On by default, as the reference's sample() works in place; no
+// reference caller reads them after the call, and turning it off saves a
+// device-to-host copy of the row and a write-back kernel per call.
 void set_inplace_writeback(bool on) noexcept;
 
 // True when a gfx950 device and libultima_hsamp are usable.

@@ -138,7 +138,11 @@ int ultima_hsamp_destroy(ultima_hsamp* h);
  * overlap on two streams. The call may be captured into a HIP graph once the
  * same batch (same knobs, rows and vocab) has run uncaptured on the handle;
  * under capture it allocates and uploads nothing and returns
- * ULTIMA_HSAMP_ERR_UNSUPPORTED if it would have to. */
+ * ULTIMA_HSAMP_ERR_UNSUPPORTED if it would have to. A captured graph holds the
+ * handle's scratch: once a graph has been captured, a later uncaptured run that
+ * needs more scratch allocates a larger area and keeps the old one until
+ * ultima_hsamp_destroy(), so earlier graphs stay valid to replay (they must not
+ * be replayed after destroy, nor overlap other work of the handle). */
 int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* batch, void* hip_stream);
 
 /* One row in HOST memory, synchronously -- sample() of sampler.cpp:230-277 with
@@ -165,6 +169,15 @@ const char* ultima_hsamp_status_str(int status);
 
 /* ULTIMA_HSAMP_VERSION of the loaded library. */
 int ultima_hsamp_version(void);
+
+/* Diagnostics, no counterpart in the reference: a plain read of the batch's
+ * logits with the launch shape ultima_hsamp_run() would use for it (same grid,
+ * slices, block order and 16-byte loads; aligned rows only, else
+ * ULTIMA_HSAMP_ERR_UNSUPPORTED). Each block writes its slice's maximum to
+ * out (device, rows * 256 floats). Its duration is the floor for a pass over
+ * these bytes with this launch shape; the benchmark times it beside the
+ * stream kernel. Asynchronous on hip_stream. */
+int ultima_hsamp_read_probe(ultima_hsamp* h, const ultima_hsamp_batch* batch, float* out, void* hip_stream);
 
 /* Diagnostics, no counterpart in the reference: while set (non-NULL), every
  * ultima_hsamp_run() also records this hipEvent_t on its stream between the

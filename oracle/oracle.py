@@ -102,6 +102,8 @@ def lib():
         L.orc_argmax.argtypes = [vp, i64]
         L.orc_sample_batch.restype = None
         L.orc_sample_batch.argtypes = [vp, i64, i64, i64, vp, vp, i64, vp, vp, i64, vp, vp, i32]
+        L.orc_sample_batch_stages.restype = None
+        L.orc_sample_batch_stages.argtypes = [vp, i64, i64, i64, vp, vp, i64, vp, vp, i64, vp, vp, vp]
         L.orc_u_from_seed.restype = f64
         L.orc_u_from_seed.argtypes = [u64]
         L.orc_mt19937_64_nth.restype = u64
@@ -238,6 +240,26 @@ def sample_batch(logits_f32: np.ndarray, plist, hist=None, hist_len=None, mask=N
                        0 if mask is None else mask.strides[0] // 4,
                        _ptr(np.ascontiguousarray(u, dtype=np.float64)), _ptr(toks), nthreads)
     return toks
+
+
+STAGES = ("penalties", "temperature", "top_k", "top_p", "min_p", "softmax", "draw")
+
+
+def sample_batch_stages(logits_f32: np.ndarray, plist, hist=None, hist_len=None, mask=None, u=None):
+    """The restatement over a [B, V] float32 batch on one thread with a clock
+    around each stage. Returns (tokens, {stage: seconds summed over rows})."""
+    L = lib()
+    B, V = logits_f32.shape
+    pa = params_array(plist)
+    toks = np.zeros(B, np.int32)
+    ns = np.zeros(7, np.float64)
+    hl = None if hist is None else np.ascontiguousarray(hist_len, dtype=np.int64)
+    L.orc_sample_batch_stages(_ptr(logits_f32), B, V, logits_f32.strides[0] // 4,
+                              ctypes.cast(pa, ctypes.c_void_p), _ptr(hist),
+                              0 if hist is None else hist.strides[0] // 4, _ptr(hl), _ptr(mask),
+                              0 if mask is None else mask.strides[0] // 4,
+                              _ptr(np.ascontiguousarray(u, dtype=np.float64)), _ptr(toks), _ptr(ns))
+    return toks, {k: float(v) * 1e-9 for k, v in zip(STAGES, ns)}
 
 
 def ref_sample_row(logits, params: dict, hist=None, bias=None, seed: int = 0):

@@ -9,6 +9,7 @@
 #include "sampler_oracle.h"
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstddef>
 #include <cstdint>
@@ -241,10 +242,33 @@ int32_t orc_argmax(const float* logits, int64_t V) {
     return static_cast<int32_t>(best);
 }
 
-// src/sampler/sampler.cpp:230-277 -- the fixed stage order.
-int32_t orc_sample_row(float* logits, int64_t V_, const orc_params* p, const int32_t* hist,
-                       int64_t hist_len, const uint32_t* mask_words, const int32_t* bias_ids,
-                       const float* bias_vals, int64_t n_bias, double u, orc_trace* tr) {
+}  // extern "C"
+
+namespace {
+
+// Stage clock for the CPU baseline's breakdown: adds the time since the last
+// mark to slot i (nothing when no accumulator is given).
+struct StageClock {
+    double* acc;
+    std::chrono::steady_clock::time_point t;
+    explicit StageClock(double* a) : acc(a) {
+        if (acc) t = std::chrono::steady_clock::now();
+    }
+    void mark(int i) {
+        if (!acc) return;
+        const auto n = std::chrono::steady_clock::now();
+        acc[i] += std::chrono::duration<double, std::nano>(n - t).count();
+        t = n;
+    }
+};
+
+// src/sampler/sampler.cpp:230-277 -- the fixed stage order. stage_ns (optional):
+// nanoseconds per stage, added to [penalties, temperature, top-k, top-p,
+// min-p, softmax, draw]; the kept-set trace is taken outside the clock.
+int32_t sample_row_impl(float* logits, int64_t V_, const orc_params* p, const int32_t* hist,
+                        int64_t hist_len, const uint32_t* mask_words, const int32_t* bias_ids,
+                        const float* bias_vals, int64_t n_bias, double u, orc_trace* tr,
+                        double* stage_ns) {
     if (tr) {
         tr->topk_count = -1;
         tr->kept_count = 0;
@@ -256,6 +280,7 @@ int32_t orc_sample_row(float* logits, int64_t V_, const orc_params* p, const int
     if (V_ <= 0) return -1;
     const std::size_t V = static_cast<std::size_t>(V_);
     const Ids recent{hist, static_cast<std::size_t>(hist_len > 0 ? hist_len : 0)};
+    StageClock clk(stage_ns);
 
     apply_mask(logits, V, mask_words);
     apply_logit_bias(logits, V, bias_ids, bias_vals, n_bias);
@@ -269,12 +294,18 @@ int32_t orc_sample_row(float* logits, int64_t V_, const orc_params* p, const int
         apply_freq_presence(logits, V, window_slice(recent, win), p->frequency_penalty,
                             p->presence_penalty);
     }
+    clk.mark(0);
     if (p->temperature <= 0.0f) {
         if (tr) tr->greedy = 1;
-        return orc_argmax(logits, V_);
+        const int32_t t = orc_argmax(logits, V_);
+        clk.mark(6);
+        return t;
     }
     apply_temperature(logits, V, p->temperature);
-    if (p->top_k > 0 && apply_top_k(logits, V, p->top_k) && tr) {
+    clk.mark(1);
+    const bool topk = p->top_k > 0 && apply_top_k(logits, V, p->top_k);
+    clk.mark(2);
+    if (topk && tr) {
         int32_t n = 0;
         for (std::size_t i = 0; i < V; ++i) {
             if (logits[i] == kNegInf) continue;
@@ -284,9 +315,41 @@ int32_t orc_sample_row(float* logits, int64_t V_, const orc_params* p, const int
         tr->topk_count = n;
     }
     if (p->top_p < 1.0f) apply_top_p(logits, V, p->top_p, tr ? &tr->topp_margin : nullptr);
+    clk.mark(3);
     if (p->min_p > 0.0f) apply_min_p(logits, V, p->min_p);
+    clk.mark(4);
     record_kept(logits, V, tr);
-    return draw(softmax_probs(logits, V), u, tr);
+    StageClock clk2(stage_ns);
+    const auto probs = softmax_probs(logits, V);
+    clk2.mark(5);
+    const int32_t t = draw(probs, u, tr);
+    clk2.mark(6);
+    return t;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t orc_sample_row(float* logits, int64_t V_, const orc_params* p, const int32_t* hist,
+                       int64_t hist_len, const uint32_t* mask_words, const int32_t* bias_ids,
+                       const float* bias_vals, int64_t n_bias, double u, orc_trace* tr) {
+    return sample_row_impl(logits, V_, p, hist, hist_len, mask_words, bias_ids, bias_vals, n_bias, u, tr,
+                           nullptr);
+}
+
+// One thread, rows in order, with the per-stage clock: stage_ns[7] gets the
+// nanoseconds of [penalties, temperature, top-k, top-p, min-p, softmax, draw]
+// summed over the rows (mask and bias count as penalties).
+void orc_sample_batch_stages(float* logits, int64_t rows, int64_t V, int64_t stride,
+                             const orc_params* params, const int32_t* hist, int64_t hist_stride,
+                             const int64_t* hist_len, const uint32_t* mask, int64_t mask_stride,
+                             const double* u, int32_t* tokens, double* stage_ns) {
+    for (int i = 0; i < 7; ++i) stage_ns[i] = 0.0;
+    for (int64_t r = 0; r < rows; ++r)
+        tokens[r] = sample_row_impl(logits + r * stride, V, &params[r], hist ? hist + r * hist_stride : nullptr,
+                                    hist ? hist_len[r] : 0, mask ? mask + r * mask_stride : nullptr, nullptr,
+                                    nullptr, 0, u[r], nullptr, stage_ns);
 }
 
 void orc_sample_batch(float* logits, int64_t rows, int64_t V, int64_t stride,

@@ -73,6 +73,15 @@ int32_t orc_sample_row(float* logits, int64_t V, const orc_params* p,
                        const int32_t* bias_ids, const float* bias_vals, int64_t n_bias,
                        double u, orc_trace* trace);
 
+/* The CPU baseline's per-stage breakdown: rows in order on the calling thread,
+ * stage_ns[7] = nanoseconds summed over the rows of [penalties (mask, bias,
+ * repetition, DRY, frequency/presence), temperature, top-k, top-p, min-p,
+ * softmax, draw]. Same arguments and results as orc_sample_batch. */
+void orc_sample_batch_stages(float* logits, int64_t rows, int64_t V, int64_t stride,
+                             const orc_params* params, const int32_t* hist, int64_t hist_stride,
+                             const int64_t* hist_len, const uint32_t* mask, int64_t mask_stride,
+                             const double* u, int32_t* tokens, double* stage_ns);
+
 /* argmax of sampler.cpp:220-228 (first maximum, -1 when empty). */
 int32_t orc_argmax(const float* logits, int64_t V);
 

@@ -55,14 +55,19 @@ def sampler(hs):
     s.close()
 
 
-@pytest.fixture(params=["exact", "exact2", "general"])
+@pytest.fixture(params=["default", "exact", "exact2", "general"])
 def kernel_mode(request, monkeypatch):
-    """Runs a test three times: with exact lists over slices of one tile, with
-    exact lists over slices of two tiles (ULTIMA_HSAMP_EXACT_TILES; aligned
-    rows only, others keep one tile), and with ULTIMA_HSAMP_EXACT=0, which
-    sends every batch to the general stream and merge kernels."""
+    """Runs a test four times: with the library's own choice of kernels and
+    slicing (no override: what every caller and bench.py get), with exact
+    lists over slices of one tile, with exact lists over slices of two tiles
+    (ULTIMA_HSAMP_EXACT_TILES, the fewest slices; aligned rows only, others
+    keep one tile), and with ULTIMA_HSAMP_EXACT=0, which sends every batch to
+    the general stream and merge kernels."""
     monkeypatch.delenv("ULTIMA_HSAMP_EXACT", raising=False)
-    if request.param == "general":
+    monkeypatch.delenv("ULTIMA_HSAMP_SLICES", raising=False)
+    if request.param == "default":
+        monkeypatch.delenv("ULTIMA_HSAMP_EXACT_TILES", raising=False)
+    elif request.param == "general":
         monkeypatch.setenv("ULTIMA_HSAMP_EXACT", "0")
         monkeypatch.delenv("ULTIMA_HSAMP_EXACT_TILES", raising=False)
     else:

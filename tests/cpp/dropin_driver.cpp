@@ -8,6 +8,15 @@
 //                                   case of IN and write token + logits to OUT
 //                                   (tests/test_gpu_dropin.py compares them with
 //                                   the CPU oracle)
+//   dropin_driver cli IN OUT        the reference CLI's generation loop
+//                                   (apps/ultima-cli/main.cpp:661-679): identity()
+//                                   + temperature, one SamplerContext pushing each
+//                                   sampled id; writes token + logits per step
+//   dropin_driver batch IN OUT      sample_batch() over device copies of a batch
+//                                   (rows, per-row knobs, histories, uniforms)
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
@@ -17,6 +26,7 @@
 
 using ultima::sampler::argmax;
 using ultima::sampler::sample;
+using ultima::sampler::sample_batch;
 using ultima::sampler::SamplerContext;
 using ultima::sampler::SamplerParams;
 using ultima::sampler::TokenId;
@@ -124,11 +134,24 @@ static int refcases() {
 template <class T>
 static bool rd(std::FILE* f, T& x) { return std::fread(&x, sizeof(T), 1, f) == 1; }
 
+// The knob record both case formats share.
+static bool read_params(std::FILE* f, SamplerParams& p, uint64_t& seed) {
+    uint64_t rep_n, dry_allowed, dry_n, top_k;
+    bool ok = rd(f, p.rep_penalty) && rd(f, rep_n) && rd(f, p.dry_multiplier) && rd(f, p.dry_base) &&
+              rd(f, dry_allowed) && rd(f, dry_n) && rd(f, p.frequency_penalty) && rd(f, p.presence_penalty) &&
+              rd(f, p.temperature) && rd(f, top_k) && rd(f, p.top_p) && rd(f, p.min_p) && rd(f, seed);
+    p.repeat_last_n = rep_n;
+    p.dry_allowed_len = dry_allowed;
+    p.dry_last_n = dry_n;
+    p.top_k = top_k;
+    return ok;
+}
+
+
 static int replay(const char* in, const char* out) {
     std::FILE* f = std::fopen(in, "rb");
     std::FILE* g = std::fopen(out, "wb");
     if (!f || !g) return 100;
-    ultima::sampler::set_inplace_writeback(true);
     int32_t n = 0;
     if (!rd(f, n)) return 101;
     for (int32_t c = 0; c < n; ++c) {
@@ -148,14 +171,8 @@ static int replay(const char* in, const char* out) {
             rd(f, v);
             p.logit_bias[id] = v;
         }
-        uint64_t rep_n, dry_allowed, dry_n, top_k, seed;
-        rd(f, p.rep_penalty); rd(f, rep_n); rd(f, p.dry_multiplier); rd(f, p.dry_base);
-        rd(f, dry_allowed); rd(f, dry_n); rd(f, p.frequency_penalty); rd(f, p.presence_penalty);
-        rd(f, p.temperature); rd(f, top_k); rd(f, p.top_p); rd(f, p.min_p); rd(f, seed);
-        p.repeat_last_n = rep_n;
-        p.dry_allowed_len = dry_allowed;
-        p.dry_last_n = dry_n;
-        p.top_k = top_k;
+        uint64_t seed;
+        if (!read_params(f, p, seed)) return 105;
         SamplerContext ctx(seed);
         ctx.set_recent(h);
         const TokenId t = sample(l, p, ctx);
@@ -167,9 +184,97 @@ static int replay(const char* in, const char* out) {
     return 0;
 }
 
+// CLI file: int32 V, int32 steps, float temperature, u64 seed, int32 P, int32 prompt[P],
+// then steps x float logits[V]. Out: per step int32 token, float logits[V] after sample().
+static int cli(const char* in, const char* out) {
+    std::FILE* f = std::fopen(in, "rb");
+    std::FILE* g = std::fopen(out, "wb");
+    if (!f || !g) return 100;
+    int32_t V, steps, P;
+    float temperature;
+    uint64_t seed;
+    if (!rd(f, V) || !rd(f, steps) || !rd(f, temperature) || !rd(f, seed) || !rd(f, P)) return 101;
+    std::vector<TokenId> prompt(static_cast<size_t>(P));
+    if (P && std::fread(prompt.data(), 4, prompt.size(), f) != prompt.size()) return 102;
+    // apps/ultima-cli/main.cpp:661-664
+    SamplerParams sp = SamplerParams::identity();
+    sp.temperature = temperature;
+    SamplerContext sctx{seed};
+    for (auto t : prompt) sctx.push_recent(t);
+    std::vector<float> logits(static_cast<size_t>(V));
+    for (int32_t i = 0; i < steps; ++i) {
+        if (std::fread(logits.data(), 4, logits.size(), f) != logits.size()) return 103;
+        // main.cpp:669-672
+        const TokenId next = (temperature <= 0.0f) ? argmax(logits) : sample(logits, sp, sctx);
+        sctx.push_recent(next);
+        std::fwrite(&next, 4, 1, g);
+        std::fwrite(logits.data(), 4, logits.size(), g);
+    }
+    std::fclose(f);
+    std::fclose(g);
+    return 0;
+}
+
+// Batch file: int32 B, int32 V, int32 H, float logits[B][V], int32 hist[B][H],
+// int64 hist_len[B], double u[B], then B knob records. Out: int32 token[B].
+static int batch(const char* in, const char* out) {
+    std::FILE* f = std::fopen(in, "rb");
+    std::FILE* g = std::fopen(out, "wb");
+    if (!f || !g) return 100;
+    int32_t B, V, H;
+    if (!rd(f, B) || !rd(f, V) || !rd(f, H)) return 101;
+    const size_t nl = static_cast<size_t>(B) * static_cast<size_t>(V), nh = static_cast<size_t>(B) * static_cast<size_t>(H);
+    std::vector<float> logits(nl);
+    std::vector<TokenId> hist(nh);
+    std::vector<int64_t> hist_len(static_cast<size_t>(B));
+    std::vector<double> u(static_cast<size_t>(B));
+    if (std::fread(logits.data(), 4, nl, f) != nl || std::fread(hist.data(), 4, nh, f) != nh ||
+        std::fread(hist_len.data(), 8, hist_len.size(), f) != hist_len.size() ||
+        std::fread(u.data(), 8, u.size(), f) != u.size())
+        return 102;
+    std::vector<SamplerParams> params(static_cast<size_t>(B));
+    for (auto& p : params) {
+        uint64_t seed;
+        p = SamplerParams::identity();
+        if (!read_params(f, p, seed)) return 103;
+    }
+    float* d_logits = nullptr;
+    TokenId* d_hist = nullptr;
+    double* d_u = nullptr;
+    TokenId* d_tok = nullptr;
+    if (hipMalloc(reinterpret_cast<void**>(&d_logits), nl * 4) != hipSuccess ||
+        hipMalloc(reinterpret_cast<void**>(&d_hist), std::max<size_t>(nh, 1) * 4) != hipSuccess ||
+        hipMalloc(reinterpret_cast<void**>(&d_u), u.size() * 8) != hipSuccess ||
+        hipMalloc(reinterpret_cast<void**>(&d_tok), static_cast<size_t>(B) * 4) != hipSuccess)
+        return 104;
+    if (hipMemcpy(d_logits, logits.data(), nl * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        (nh && hipMemcpy(d_hist, hist.data(), nh * 4, hipMemcpyHostToDevice) != hipSuccess) ||
+        hipMemcpy(d_u, u.data(), u.size() * 8, hipMemcpyHostToDevice) != hipSuccess)
+        return 105;
+    const int st = sample_batch(d_logits, B, V, V, params, d_hist, H, hist_len, d_u, d_tok, nullptr);
+    if (st != 0) {
+        std::fprintf(stderr, "sample_batch: status %d\n", st);
+        return 106;
+    }
+    std::vector<TokenId> tok(static_cast<size_t>(B));
+    if (hipDeviceSynchronize() != hipSuccess ||
+        hipMemcpy(tok.data(), d_tok, tok.size() * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return 107;
+    std::fwrite(tok.data(), 4, tok.size(), g);
+    (void)hipFree(d_logits);
+    (void)hipFree(d_hist);
+    (void)hipFree(d_u);
+    (void)hipFree(d_tok);
+    std::fclose(f);
+    std::fclose(g);
+    return 0;
+}
+
 int main(int argc, char** argv) {
     if (argc >= 2 && std::strcmp(argv[1], "refcases") == 0) return refcases();
     if (argc >= 4 && std::strcmp(argv[1], "replay") == 0) return replay(argv[2], argv[3]);
-    std::fprintf(stderr, "usage: %s refcases | replay IN OUT\n", argv[0]);
+    if (argc >= 4 && std::strcmp(argv[1], "cli") == 0) return cli(argv[2], argv[3]);
+    if (argc >= 4 && std::strcmp(argv[1], "batch") == 0) return batch(argv[2], argv[3]);
+    std::fprintf(stderr, "usage: %s refcases | replay IN OUT | cli IN OUT | batch IN OUT\n", argv[0]);
     return 2;
 }

@@ -24,9 +24,14 @@ def _wl(wl, V, rows, params, seed=3, sigma=2.0, dtype="f32", hist_len=0, mask=No
 
 
 def test_config3_spike_and_flat_rows(sampler, wl):
-    w = wl.config(3, seed=5, rows=8)
+    """BASELINE config 3 at its size, B = 256: 128 rows N(0, 1) with 16 spike
+    ids at +15 (exact ties, a nucleus of the 16), 128 near-flat rows N(0, 0.1)
+    (a nucleus of about 1e5 ids), top-p 0.9 over the full vocabulary. Every
+    row is compared with the oracle: token, kept set and probabilities."""
+    w = wl.config(3, seed=5)
+    assert w.rows == 256
     g = run_gpu(sampler, w, set_cap=w.vocab)
-    assert compare_rows(w, g) == 8
+    assert compare_rows(w, g) == 256
 
 
 @pytest.mark.parametrize("knobs", [

@@ -278,3 +278,17 @@ def test_expf_is_glibc():
     assert O.expf(-np.inf) == 0.0
     assert O.expf(-200.0) == 0.0
     assert abs(O.expf(-1.0) - math.exp(-1.0)) < 1e-7
+
+
+def test_stage_clock_leaves_results_unchanged(orc, wl):
+    """The CPU baseline's per-stage breakdown runs the same ladder: tokens equal
+    the plain batch call's, and every stage of a config-2 row is timed."""
+    w = wl.config(2, seed=4, rows=3, V=20000)
+    x1, x2 = w.logits_f32().copy(), w.logits_f32().copy()
+    t1 = orc.sample_batch(x1, w.params, w.hist, w.hist_len, None, w.u)
+    t2, st = orc.sample_batch_stages(x2, w.params, w.hist, w.hist_len, None, w.u)
+    np.testing.assert_array_equal(t1, t2)
+    np.testing.assert_array_equal(x1.view(np.uint32), x2.view(np.uint32))
+    assert set(st) == set(orc.STAGES)
+    assert all(v >= 0.0 for v in st.values())
+    assert st["penalties"] > 0 and st["top_k"] > 0 and st["draw"] > 0

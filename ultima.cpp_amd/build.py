@@ -75,8 +75,10 @@ def build_all() -> None:
           f"-L{PKG}", "-lultima_hsamp", "-Wl,-rpath,$ORIGIN"])
     _run([HIPCC, *HIP_FLAGS, "-shared", "-x", "hip", str(ROOT / "tests" / "cpp" / "device_expf.hip"),
           "-o", str(ROOT / "tests" / "cpp" / "libdevice_expf.so")])
-    _run([*cxx, str(ROOT / "tests" / "cpp" / "dropin_driver.cpp"), "-o", str(CPP_TEST),
-          f"-L{PKG}", "-lultima_sampler", "-lultima_hsamp", "-Wl,-rpath,$ORIGIN"])
+    # the test driver also allocates device memory itself (sample_batch)
+    _run([*cxx, "-D__HIP_PLATFORM_AMD__", f"-I{ROCM / 'include'}", str(ROOT / "tests" / "cpp" / "dropin_driver.cpp"),
+          "-o", str(CPP_TEST), f"-L{PKG}", "-lultima_sampler", "-lultima_hsamp", f"-L{ROCM / 'lib'}", "-lamdhip64",
+          "-Wl,-rpath,$ORIGIN"])
 
 
 if __name__ == "__main__":

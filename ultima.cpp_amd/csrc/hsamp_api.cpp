@@ -16,11 +16,11 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
-#include <mutex>
 #include <tuple>
 #include <vector>
 
 #include "hsamp_plan.h"
+#include "hsamp_run.h"
 #include "ultima_hsamp.h"
 
 namespace hsamp {
@@ -32,13 +32,14 @@ hipError_t launch_stream_ex(const StreamArgs& a, int dtype, bool vec, bool pen, 
                             hipStream_t stream);
 hipError_t launch_pick(const StreamArgs& a, int nw, hipStream_t stream);
 hipError_t launch_full(const StreamArgs& a, uint32_t lds, hipStream_t stream);
+hipError_t launch_read_probe(const StreamArgs& a, int dtype, int tiles, int grid, float* out, hipStream_t stream);
 }  // namespace hsamp
 
 using namespace hsamp;
 
 namespace {
 
-constexpr int kSlots = 4;
+constexpr int kSlots = 16;   // resident plan blobs (a graph pins the ones it reads)
 constexpr int kTile = kBlock * 32;      // elements of one k_stream tile (32 per thread)
 constexpr int kTargetBlocks = 4096;     // most blocks a launch spreads rows over
 constexpr int kTwoTileBlocks = 512;     // exact lists: two-tile slices while B * S stays at or above this
@@ -68,15 +69,13 @@ struct ultima_hsamp {
     int device = 0;
     int32_t max_rows = 0;
     int32_t max_vocab = 0;
-    size_t lds_limit = 0;         // LDS bytes one block may use on this device
-    int cus = 256;                // compute units of this device
+    DevCaps caps;
     hipStream_t own_stream = nullptr;
     hipEvent_t phase_ev = nullptr;   // recorded between the stream and merge kernels when set
     Slot slots[kSlots];
     int next_slot = 0;
-    std::vector<char> blob;
-    std::vector<RowPlan> plans;
-    // scratch sized for the worst case at creation
+    HostScratch hs;
+    // device scratch, grown on demand
     unsigned long long* cand = nullptr;
     size_t cand_elems = 0;
     int32_t* cand_n = nullptr;    // [slots] counts, then [slots] bounds
@@ -85,14 +84,19 @@ struct ultima_hsamp {
     size_t gtab_words = 0;
     int32_t* fin_idx = nullptr;
     int32_t* fin_n = nullptr;
-    unsigned long long* ovf = nullptr;   // per-block overflow of the LDS candidate buffer
+    unsigned long long* ovf = nullptr;   // per-row overflow of the LDS candidate buffer
+    size_t ovf_elems = 0;
     float* fullv = nullptr;              // full-vocabulary rows: transformed logits
     size_t fullv_elems = 0;
     float* fullp = nullptr;              // full-vocabulary rows: probabilities
     size_t fullp_elems = 0;
     uint32_t* fullk = nullptr;           // full-vocabulary rows: top-p keys
     size_t fullk_elems = 0;
-    size_t ovf_elems = 0;
+    // A graph captured from this handle holds the scratch pointers of its
+    // launches: once one has been captured, scratch that grows is kept (not
+    // freed) until destroy, so that replaying an earlier graph stays valid.
+    bool captured = false;
+    std::vector<void*> retired;
     // sample_host staging
     float* d_row = nullptr;
     float* h_row = nullptr;       // pinned
@@ -105,7 +109,7 @@ struct ultima_hsamp {
     int32_t* h_tok = nullptr;     // pinned
 };
 
-namespace {
+namespace hsamp {
 
 // ULTIMA_HSAMP_DEBUG=1 prints each failing HIP call to stderr.
 int hip_fail(hipError_t e, const char* what, int line) {
@@ -118,11 +122,16 @@ int hip_fail(hipError_t e, const char* what, int line) {
     (void)hipGetLastError();
     return e == hipErrorOutOfMemory ? ULTIMA_HSAMP_ERR_NOMEM : ULTIMA_HSAMP_ERR_HIP;
 }
+
+}  // namespace hsamp
+
 #define HIP_TRY(x)                                                   \
     do {                                                             \
         hipError_t e_ = (x);                                         \
         if (e_ != hipSuccess) return hip_fail(e_, #x, __LINE__);     \
     } while (0)
+
+namespace {
 
 bool isnan_f(float x) { return x != x; }
 
@@ -135,35 +144,25 @@ uint32_t fbits(float f) {
     return u;
 }
 
-struct Built {
-    size_t off_dry = 0, off_bias_ids = 0, off_bias_vals = 0, total = 0;
-    int kmax = 0;              // max top_k over rows that select
-    int max_pen = 0;           // max over penalty rows of (scan_len + bias entries)
-    bool any_pen = false;
-    int max_scan = 0;          // max history window over penalty rows
-    int max_bias = 0;          // max logit-bias entries over rows
-    bool pen_lowers = true;    // every penalty stage can only lower a logit
-    bool any_dry = false;      // a row with the DRY stage
-    bool inv_ok = true;        // every sampling row has 0 < fl(1/T) < inf
-    bool any_mask = false;     // the batch carries an allowed-token mask
-    bool any_full = false;     // a sampling row over the whole vocabulary (k_full)
-    bool any_topk = false;     // a greedy or top-k row (k_stream + k_merge)
-    bool any_greedy = false;   // a greedy row (k_stream's greedy kernel)
-    bool any_sample = false;   // a top-k sampling row (k_stream's sampling kernel)
-};
+}  // namespace
 
-// RowPlans + DRY tables + bias into h->blob; the reference's predicates in [].
-int build_blob(ultima_hsamp* h, const ultima_hsamp_batch* b, Built& out) {
+namespace hsamp {
+
+// RowPlans + DRY tables + bias into hs.blob; the reference's predicates in [].
+int build_blob(HostScratch& hs, const ultima_hsamp_batch* b, Built& out) {
     const int B = b->rows, V = b->vocab;
-    h->plans.assign(B, RowPlan{});
-    std::vector<float> dry;
+    hs.plans.assign(B, RowPlan{});
+    std::vector<float>& dry = hs.dry;
+    dry.clear();
     std::map<DryKey, int32_t> dry_seen;
-    std::vector<int32_t> bids;
-    std::vector<float> bvals;
-    std::vector<std::pair<int32_t, float>> tmp;
+    std::vector<int32_t>& bids = hs.bias_ids;
+    std::vector<float>& bvals = hs.bias_vals;
+    bids.clear();
+    bvals.clear();
+    std::vector<std::pair<int32_t, float>>& tmp = hs.tmp;
     for (int r = 0; r < B; ++r) {
         const ultima_hsamp_params& q = b->params[r];
-        RowPlan& P = h->plans[r];
+        RowPlan& P = hs.plans[r];
         P.inv_temp = 1.0f;   // x * 1.0f == x: rows without temperature multiply by one
         if (isnan_f(q.rep_penalty) || isnan_f(q.dry_multiplier) || isnan_f(q.dry_base) ||
             isnan_f(q.frequency_penalty) || isnan_f(q.presence_penalty) ||
@@ -292,24 +291,265 @@ int build_blob(ultima_hsamp* h, const ultima_hsamp_batch* b, Built& out) {
     out.off_bias_ids = align16(out.off_dry + sizeof(float) * dry.size());
     out.off_bias_vals = align16(out.off_bias_ids + sizeof(int32_t) * bids.size());
     out.total = align16(out.off_bias_vals + sizeof(float) * bvals.size());
-    h->blob.assign(out.total, 0);
-    std::memcpy(h->blob.data(), h->plans.data(), sizeof(RowPlan) * B);
-    if (!dry.empty()) std::memcpy(h->blob.data() + out.off_dry, dry.data(), sizeof(float) * dry.size());
+    hs.blob.assign(out.total, 0);
+    std::memcpy(hs.blob.data(), hs.plans.data(), sizeof(RowPlan) * B);
+    if (!dry.empty()) std::memcpy(hs.blob.data() + out.off_dry, dry.data(), sizeof(float) * dry.size());
     if (!bids.empty()) {
-        std::memcpy(h->blob.data() + out.off_bias_ids, bids.data(), sizeof(int32_t) * bids.size());
-        std::memcpy(h->blob.data() + out.off_bias_vals, bvals.data(), sizeof(float) * bvals.size());
+        std::memcpy(hs.blob.data() + out.off_bias_ids, bids.data(), sizeof(int32_t) * bids.size());
+        std::memcpy(hs.blob.data() + out.off_bias_vals, bvals.data(), sizeof(float) * bvals.size());
     }
     return ULTIMA_HSAMP_OK;
 }
 
-// A device copy of h->blob, reusing a slot that already holds the same bytes.
+int validate_batch(const ultima_hsamp_batch* b, int32_t max_rows, int32_t max_vocab) {
+    if (b == nullptr || b->params == nullptr) return ULTIMA_HSAMP_ERR_INVALID;
+    if (b->rows < 1 || b->vocab < 1) return ULTIMA_HSAMP_ERR_INVALID;
+    if (b->rows > max_rows || b->vocab > max_vocab) return ULTIMA_HSAMP_ERR_CAPACITY;
+    if (b->dtype != ULTIMA_HSAMP_F32 && b->dtype != ULTIMA_HSAMP_BF16) return ULTIMA_HSAMP_ERR_INVALID;
+    if (b->logits == nullptr || b->u == nullptr || b->token == nullptr) return ULTIMA_HSAMP_ERR_INVALID;
+    if (b->logits_stride < b->vocab) return ULTIMA_HSAMP_ERR_INVALID;
+    if (b->hist != nullptr && b->hist_stride < 0) return ULTIMA_HSAMP_ERR_INVALID;
+    if (b->mask != nullptr && b->mask_stride < (b->vocab + 31) / 32) return ULTIMA_HSAMP_ERR_INVALID;
+    if ((b->flags & ~(ULTIMA_HSAMP_WRITEBACK | ULTIMA_HSAMP_STREAM_ONLY)) != 0) return ULTIMA_HSAMP_ERR_INVALID;
+    if ((b->flags & ULTIMA_HSAMP_WRITEBACK) && b->dtype != ULTIMA_HSAMP_F32)
+        return ULTIMA_HSAMP_ERR_UNSUPPORTED;
+    const bool sets = b->topk_idx || b->kept_idx || b->kept_prob;
+    if (sets && b->set_cap < 1) return ULTIMA_HSAMP_ERR_INVALID;
+    if ((b->kept_idx == nullptr) != (b->kept_prob == nullptr)) return ULTIMA_HSAMP_ERR_INVALID;
+    return ULTIMA_HSAMP_OK;
+}
+
+int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, RunPlan& rp) {
+    const int B = b->rows, V = b->vocab;
+    const int es = b->dtype == ULTIMA_HSAMP_F32 ? 4 : 2;
+    rp = RunPlan{};
+    rp.B = B;
+    rp.V = V;
+    // Exact lists (k_stream's EX kernels + k_pick): every row samples with
+    // top-k <= 64 and penalties that can only lower a logit, from windows the
+    // stream's registers hold, without DRY or logit bias. The stream then
+    // leaves every candidate with its final key. ULTIMA_HSAMP_EXACT=0 turns it
+    // off (the general kernels take every batch).
+    const int kmax = std::max(1, bl.kmax);
+    rp.kmax = kmax;
+    rp.wb = (b->flags & ULTIMA_HSAMP_WRITEBACK) != 0;
+    bool exact_ok = bl.any_sample && !bl.any_greedy && !bl.any_full && kmax <= 64 && !rp.wb && bl.inv_ok &&
+                    (!bl.any_pen || (bl.pen_lowers && !bl.any_dry && bl.max_bias == 0 && bl.max_scan <= 8 * kBlock));
+    if (const char* ev = std::getenv("ULTIMA_HSAMP_EXACT")) exact_ok = exact_ok && ev[0] != '0';
+    // 16-byte loads: aligned rows holding at least one whole chunk
+    const bool vec_rows = (reinterpret_cast<uintptr_t>(b->logits) % 16 == 0) && ((b->logits_stride * es) % 16 == 0) &&
+                          V >= 16 / es;
+    rp.vec = vec_rows;
+    // Slicing: enough blocks to fill the CUs, slices of at most one tile.
+    // Exact lists over aligned rows take slices of up to two tiles while the
+    // batch still gives two blocks per CU: each block's setup, history scan
+    // and bound then cover more ids, and k_pick merges fewer lists. Among
+    // those slicings, the one whose busiest CU streams the fewest ids, with
+    // a block's fixed work counted as kFixedIds ids (blocks spread evenly).
+    const int tiles = (V + kTile - 1) / kTile;
+    int S = std::max(1, std::min({kTargetBlocks / B, tiles, kBlock}));
+    if (exact_ok && vec_rows) {
+        constexpr int64_t kFixedIds = 4096;
+        const int S2 = (V + 2 * kTile - 1) / (2 * kTile);
+        int want = ((int64_t)B * S2 >= kTwoTileBlocks && S2 < S) ? 2 : 1;
+        bool forced = false;
+        if (const char* et = std::getenv("ULTIMA_HSAMP_EXACT_TILES")) {
+            want = std::atoi(et) == 2 ? 2 : 1;
+            forced = true;   // two tiles asked for: the fewest slices
+        }
+        if (want == 2) {
+            int best = std::min(S, S2);
+            int64_t best_cost = INT64_MAX;
+            for (int c = best; !forced && c <= std::min(S, 2 * S2); ++c) {
+                const int64_t len = ((V + c - 1) / c + 31) & ~31;
+                const int64_t per_cu = ((int64_t)B * c + dc.cus - 1) / dc.cus;
+                const int64_t cost = per_cu * (len + kFixedIds);
+                if (cost < best_cost) {
+                    best_cost = cost;
+                    best = c;
+                }
+            }
+            S = best;
+        }
+    }
+    // diagnostics: a forced slice count (as many slices as the kernels allow)
+    if (const char* fs = std::getenv("ULTIMA_HSAMP_SLICES")) S = std::max(1, std::min(std::atoi(fs), kBlock));
+    const int slice_len = ((V + S - 1) / S + 31) & ~31;
+    S = (V + slice_len - 1) / slice_len;
+    // block and row indices are divided by S with a 32-bit reciprocal (exact below 2^32 / S)
+    if ((uint64_t)(B + 2) * (uint64_t)S * (uint64_t)(S + kXcds) >= (1ull << 32)) return ULTIMA_HSAMP_ERR_CAPACITY;
+    rp.S = S;
+    rp.slice_len = slice_len;
+    const int buf_cap = std::max(512, next_pow2(2 * kmax));
+    const int cand_cap = slice_len;                 // a slice's list holds all its ids
+    const int bitmap_words = slice_len / 32;
+    rp.buf_cap = buf_cap;
+    rp.cand_cap = cand_cap;
+    rp.bitmap_words = bitmap_words;
+    const size_t statik = 4096;                     // static LDS of the kernels, rounded up
+    // k_stream: [penalised-id bitmap] [allowed-id mask words]
+    rp.lds = align16(8 * (size_t)bitmap_words);
+    if (rp.lds + statik > dc.lds_limit) return ULTIMA_HSAMP_ERR_CAPACITY;
+    // k_merge: [penalty table | finalize scratch] [candidate buffer]; the
+    // table (load factor <= 1/2) moves to global memory when it does not fit.
+    const size_t regionF = 8 * (size_t)next_pow2(kmax) + 20 * (size_t)kmax;
+    const int mhash = bl.any_pen ? std::max(16, next_pow2(2 * bl.max_pen)) : 16;
+    rp.mhash = mhash;
+    const size_t lds_budget = std::min<size_t>(dc.lds_limit, 64 * 1024) - statik;
+    constexpr size_t kFullWork = 24 * 1024;   // k_full: bucket counts, starts, sort batch
+    const bool gtab = 8 * (size_t)mhash + 8 * (size_t)buf_cap > lds_budget ||
+                      8 * (size_t)mhash + 4 * (size_t)bitmap_words > lds_budget ||
+                      (bl.any_full && 8 * (size_t)mhash + kFullWork > lds_budget);
+    rp.gtab = gtab;
+    rp.full_lds = (gtab ? 0 : 8 * (size_t)mhash) + kFullWork;
+    size_t merge_lds = align16(std::max(gtab ? 0 : 8 * (size_t)mhash, regionF)) + 8 * (size_t)buf_cap;
+    // k_merge's fast path: [bins 8 KB][list 1 KB][table 12 B/slot | buffer]
+    // (flag mode: [bins][list][ids, counts / composites of penalised candidates][buffer])
+    const bool fast0 = kmax <= 64 && !gtab && bl.max_scan <= 8 * kBlock && bl.max_bias <= kBlock;
+    const bool pen_flag = fast0 && bl.any_pen && bl.pen_lowers;
+    // flag mode: after the list, counters of the penalised ids, a bitmap over
+    // the vocabulary (16 B per 128 ids) and its rank prefixes (2 B per 128
+    // ids), then the buffer of a row read again in full (rare); one merge
+    // block per row, so it may use the whole LDS of a CU
+    const size_t ngroups = ((size_t)V + 127) / 128;
+    const size_t fast_lds = pen_flag ? 9216 + 8 * (size_t)kCntCap + align16(18 * ngroups) + 8 * (size_t)buf_cap
+                                     : 9216 + std::max(12 * (size_t)mhash, 8 * (size_t)buf_cap);
+    const bool fast = fast0 && fast_lds <= (pen_flag ? dc.lds_limit - statik : lds_budget);
+    if (fast) merge_lds = std::max(merge_lds, fast_lds);
+    rp.fast = fast;
+    rp.pen_flag = fast && pen_flag;
+    rp.wb_lds = (gtab ? 0 : 8 * (size_t)mhash) + 4 * (size_t)bitmap_words;
+    if (merge_lds + statik > dc.lds_limit || rp.wb_lds + statik > dc.lds_limit ||
+        rp.full_lds + statik > dc.lds_limit)
+        return ULTIMA_HSAMP_ERR_CAPACITY;
+    const int nblocks = B * S;
+    rp.grid = (nblocks + kXcds - 1) / kXcds * kXcds;
+    rp.win = std::max(1, std::min(cand_cap, kMergeWindow / S));
+    rp.ex_tiles = slice_len > kTile ? 2 : 1;
+    bool exact = exact_ok && slice_len <= kTile * rp.ex_tiles && (rp.ex_tiles == 1 || vec_rows);
+    // k_stream EX: [count entries, 2 B per slice id + 8 (penalties)][allowed-id mask words]
+    // [staged chunks: kBlock slots of 32 B (16 B data, the chunk's first id)]
+    // (the general instantiations for unaligned rows take PEN = true: their
+    // count entries are cleared and stay zero when no row has penalties)
+    rp.cnt_bytes = (bl.any_pen || !vec_rows) ? align16(2 * ((size_t)slice_len + 8)) : 0;
+    rp.stage_off = rp.cnt_bytes + align16(4 * (size_t)bitmap_words);
+    rp.lds_ex = rp.stage_off + 32 * (size_t)kBlock;
+    // k_pick: each slice's first W entries, NW per thread; W about twice k
+    if (exact) {
+        const int w0 = std::min(cand_cap, std::max(32, (2 * kmax + 31) / 32 * 32));
+        const int need = (S * w0 + kBlock - 1) / kBlock;
+        rp.pick_nw = need <= 4 ? 4 : need <= 8 ? 8 : need <= 12 ? 12 : 16;
+        rp.win = std::max(1, std::min(cand_cap, rp.pick_nw * kBlock / S));
+        const size_t pick_lds = 8 * std::max<size_t>((size_t)rp.pick_nw * kBlock + 2, (size_t)buf_cap);
+        if (rp.lds_ex + statik > dc.lds_limit || pick_lds + statik > dc.lds_limit) exact = false;
+        else merge_lds = pick_lds;
+    }
+    rp.exact = exact;
+    rp.merge_lds = merge_lds;
+    rp.full_p2 = next_pow2(V);
+    // scratch
+    rp.cand_slots = (size_t)nblocks;
+    rp.cand_elems = (size_t)nblocks * (size_t)cand_cap;
+    rp.ovf_elems = (size_t)B * kMergeRound;
+    rp.gtab_words = gtab ? (size_t)B * 2 * mhash : 0;
+    rp.full_elems = bl.any_full ? (size_t)B * V : 0;
+    rp.fullk_elems = bl.any_full ? (size_t)B * 2 * rp.full_p2 : 0;
+    rp.fin_elems = rp.wb ? (size_t)B * kLimitK : 0;
+    return ULTIMA_HSAMP_OK;
+}
+
+int launch_run(const RunPlan& rp, const Built& bl, const ultima_hsamp_batch* b, const RunBuffers& buf,
+               hipStream_t stream, hipEvent_t phase_ev) {
+    StreamArgs a{};
+    a.logits = b->logits;
+    a.logits_stride = b->logits_stride;
+    a.hist = b->hist;
+    a.hist_stride = b->hist_stride;
+    a.mask = b->mask;
+    a.mask_stride = b->mask_stride;
+    a.u = b->u;
+    a.plans = reinterpret_cast<const RowPlan*>(buf.blob);
+    a.dry_tab = reinterpret_cast<const float*>(buf.blob + bl.off_dry);
+    a.bias_ids = reinterpret_cast<const int32_t*>(buf.blob + bl.off_bias_ids);
+    a.bias_vals = reinterpret_cast<const float*>(buf.blob + bl.off_bias_vals);
+    a.token = b->token;
+    a.row_flags = b->row_flags;
+    a.topk_idx = b->topk_idx;
+    a.topk_count = b->topk_count;
+    a.kept_idx = b->kept_idx;
+    a.kept_prob = b->kept_prob;
+    a.kept_count = b->kept_count;
+    a.set_cap = b->set_cap;
+    a.rows = rp.B;
+    a.vocab = rp.V;
+    a.nslices = rp.S;
+    a.slice_len = rp.slice_len;
+    a.kmax = rp.kmax;
+    a.cand_cap = rp.cand_cap;
+    a.buf_cap = rp.buf_cap;
+    a.mhash_slots = rp.mhash;
+    a.bitmap_words = rp.bitmap_words;
+    a.blocks_per_xcd = rp.grid / kXcds;
+    a.fin_cap = kLimitK;
+    a.ovf = buf.ovf;
+    a.ovf_cap = kMergeRound;
+    a.cand = buf.cand;
+    a.cand_n = buf.cand_n;
+    a.cand_th = buf.cand_n + buf.cand_slots;
+    a.win = rp.win;
+    a.win_magic = (uint32_t)((1ull << 32) / (uint64_t)rp.win + 1);
+    a.ns_magic = rp.S > 1 ? (uint32_t)((1ull << 32) / (uint64_t)rp.S + 1) : 0u;   // S == 1: the kernels divide by 1 themselves
+    a.dtype = b->dtype;
+    a.fast = rp.fast ? 1 : 0;
+    a.pen_flag = rp.pen_flag ? 1 : 0;
+    a.fullv = buf.fullv;
+    a.fullp = buf.fullp;
+    a.fullk = buf.fullk;
+    a.full_p2 = rp.full_p2;
+    a.gtab = rp.gtab ? buf.gtab : nullptr;
+    a.merge_lds = (uint32_t)rp.merge_lds;
+    a.fin_idx = rp.wb ? buf.fin_idx : nullptr;
+    a.fin_n = rp.wb ? buf.fin_n : nullptr;
+    a.lds_bytes = (uint32_t)(rp.exact ? rp.lds_ex : rp.lds);
+    a.exact = rp.exact ? 1 : 0;
+    a.mbm_off = (int32_t)(rp.cnt_bytes / 4);
+    a.stage_off = (int32_t)rp.stage_off;
+    a.hist_direct = (rp.exact && bl.any_pen && b->hist != nullptr && b->hist_stride >= 1 &&
+                     b->hist_stride <= 8 * kBlock) ? 1 : 0;
+    a.vec_tail = rp.vec ? rp.V % (16 / (b->dtype == ULTIMA_HSAMP_F32 ? 4 : 2)) : 0;
+    a.uniform = (bl.any_greedy && !bl.any_sample && !bl.any_full ? 1 : 0) |
+                (bl.any_sample && !bl.any_greedy && !bl.any_full ? 2 : 0);
+    // In flag mode the sampling rows' stream needs no penalties at all: it
+    // bounds on pre-penalty keys, which penalties can only lower, and k_merge
+    // finds the penalised candidates' true values (checking the bounds).
+    if (rp.exact)
+        HIP_TRY(launch_stream_ex(a, b->dtype, rp.vec, bl.any_pen, bl.any_mask, rp.ex_tiles, rp.grid, stream));
+    else if (bl.any_topk)
+        HIP_TRY(launch_stream(a, b->dtype, rp.vec, bl.any_pen, bl.any_pen && !a.pen_flag, bl.any_mask,
+                              bl.any_greedy, bl.any_sample, rp.grid, stream));
+    if (phase_ev != nullptr) HIP_TRY(hipEventRecord(phase_ev, stream));
+    if (!(b->flags & ULTIMA_HSAMP_STREAM_ONLY)) {
+        if (rp.exact) HIP_TRY(launch_pick(a, rp.pick_nw, stream));
+        else if (bl.any_topk) HIP_TRY(launch_merge(a, stream));
+        if (bl.any_full) HIP_TRY(launch_full(a, (uint32_t)rp.full_lds, stream));
+        if (rp.wb) HIP_TRY(launch_writeback(a, rp.grid, (uint32_t)rp.wb_lds, stream));
+    }
+    return ULTIMA_HSAMP_OK;
+}
+
+}  // namespace hsamp
+
+namespace {
+
+// A device copy of hs.blob, reusing a slot that already holds the same bytes.
 // Under stream capture nothing is uploaded: the blob must already be resident
 // (run the same batch once before capturing), and its slot is pinned so later
 // calls never rewrite what the graph reads.
 int upload_blob(ultima_hsamp* h, hipStream_t stream, bool capturing, Slot*& used) {
-    const size_t n = h->blob.size();
+    const std::vector<char>& blob = h->hs.blob;
+    const size_t n = blob.size();
     for (auto& s : h->slots) {
-        if (s.used && s.size == n && std::memcmp(s.host, h->blob.data(), n) == 0) {
+        if (s.used && s.size == n && std::memcmp(s.host, blob.data(), n) == 0) {
             if (capturing) s.pinned = true;
             used = &s;
             return ULTIMA_HSAMP_OK;
@@ -337,7 +577,7 @@ int upload_blob(ultima_hsamp* h, hipStream_t stream, bool capturing, Slot*& used
         HIP_TRY(hipMalloc(reinterpret_cast<void**>(&s.dev), cap));
         s.cap = cap;
     }
-    std::memcpy(s.host, h->blob.data(), n);
+    std::memcpy(s.host, blob.data(), n);
     s.size = n;
     s.used = true;
     HIP_TRY(hipMemcpyAsync(s.dev, s.host, n, hipMemcpyHostToDevice, stream));
@@ -345,21 +585,25 @@ int upload_blob(ultima_hsamp* h, hipStream_t stream, bool capturing, Slot*& used
     return ULTIMA_HSAMP_OK;
 }
 
-int validate_batch(const ultima_hsamp* h, const ultima_hsamp_batch* b) {
-    if (b == nullptr || b->params == nullptr) return ULTIMA_HSAMP_ERR_INVALID;
-    if (b->rows < 1 || b->vocab < 1) return ULTIMA_HSAMP_ERR_INVALID;
-    if (b->rows > h->max_rows || b->vocab > h->max_vocab) return ULTIMA_HSAMP_ERR_CAPACITY;
-    if (b->dtype != ULTIMA_HSAMP_F32 && b->dtype != ULTIMA_HSAMP_BF16) return ULTIMA_HSAMP_ERR_INVALID;
-    if (b->logits == nullptr || b->u == nullptr || b->token == nullptr) return ULTIMA_HSAMP_ERR_INVALID;
-    if (b->logits_stride < b->vocab) return ULTIMA_HSAMP_ERR_INVALID;
-    if (b->hist != nullptr && b->hist_stride < 0) return ULTIMA_HSAMP_ERR_INVALID;
-    if (b->mask != nullptr && b->mask_stride < (b->vocab + 31) / 32) return ULTIMA_HSAMP_ERR_INVALID;
-    if ((b->flags & ~(ULTIMA_HSAMP_WRITEBACK | ULTIMA_HSAMP_STREAM_ONLY)) != 0) return ULTIMA_HSAMP_ERR_INVALID;
-    if ((b->flags & ULTIMA_HSAMP_WRITEBACK) && b->dtype != ULTIMA_HSAMP_F32)
-        return ULTIMA_HSAMP_ERR_UNSUPPORTED;
-    const bool sets = b->topk_idx || b->kept_idx || b->kept_prob;
-    if (sets && b->set_cap < 1) return ULTIMA_HSAMP_ERR_INVALID;
-    if ((b->kept_idx == nullptr) != (b->kept_prob == nullptr)) return ULTIMA_HSAMP_ERR_INVALID;
+// Grow-only device scratch. Growing waits for the device to be idle; once a
+// graph has been captured from the handle the old area is kept until destroy.
+template <typename T>
+int grow(ultima_hsamp* h, bool capturing, T*& ptr, size_t& have, size_t need) {
+    if (need <= have) return ULTIMA_HSAMP_OK;
+    if (capturing) return ULTIMA_HSAMP_ERR_UNSUPPORTED;   // run once before capturing
+    HIP_TRY(hipDeviceSynchronize());
+    if (ptr != nullptr) {
+        if (h->captured) h->retired.push_back(ptr);
+        else HIP_TRY(hipFree(ptr));
+    }
+    ptr = nullptr;
+    have = 0;
+    if (hipMalloc(reinterpret_cast<void**>(&ptr), need * sizeof(T)) != hipSuccess) {
+        (void)hipGetLastError();
+        ptr = nullptr;
+        return ULTIMA_HSAMP_ERR_NOMEM;
+    }
+    have = need;
     return ULTIMA_HSAMP_OK;
 }
 
@@ -452,8 +696,8 @@ int ultima_hsamp_create(int device, int32_t max_rows, int32_t max_vocab, ultima_
     h->device = device;
     h->max_rows = max_rows;
     h->max_vocab = max_vocab;
-    h->lds_limit = prop.sharedMemPerBlock;
-    h->cus = std::max(1, prop.multiProcessorCount);
+    h->caps.lds_limit = prop.sharedMemPerBlock;
+    h->caps.cus = std::max(1, prop.multiProcessorCount);
     auto fail = [&](int st) {
         ultima_hsamp_destroy(h);
         return st;
@@ -497,6 +741,7 @@ int ultima_hsamp_destroy(ultima_hsamp* h) {
                     (void*)h->gtab, (void*)h->fullv, (void*)h->fullp, (void*)h->fullk, (void*)h->fin_idx,
                     (void*)h->fin_n, (void*)h->d_row, (void*)h->d_hist, (void*)h->d_u, (void*)h->d_tok})
         if (p) (void)hipFree(p);
+    for (void* p : h->retired) (void)hipFree(p);
     for (void* p : {(void*)h->h_row, (void*)h->h_hist, (void*)h->h_u, (void*)h->h_tok})
         if (p) (void)hipHostFree(p);
     if (h->own_stream) (void)hipStreamDestroy(h->own_stream);
@@ -507,239 +752,78 @@ int ultima_hsamp_destroy(ultima_hsamp* h) {
 
 int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_stream) {
     if (h == nullptr) return ULTIMA_HSAMP_ERR_INVALID;
-    int st = validate_batch(h, b);
+    int st = validate_batch(b, h->max_rows, h->max_vocab);
     if (st != ULTIMA_HSAMP_OK) return st;
     HIP_TRY(hipSetDevice(h->device));
     hipStream_t stream = static_cast<hipStream_t>(hip_stream);
     Built bl;
-    st = build_blob(h, b, bl);
+    st = build_blob(h->hs, b, bl);
     if (st != ULTIMA_HSAMP_OK) return st;
-
-    const int B = b->rows, V = b->vocab;
-    const int es = b->dtype == ULTIMA_HSAMP_F32 ? 4 : 2;
-    // Exact lists (k_stream's EX kernels + k_pick): every row samples with
-    // top-k <= 64 and penalties that can only lower a logit, from windows the
-    // stream's registers hold, without DRY or logit bias. The stream then
-    // leaves every candidate with its final key. ULTIMA_HSAMP_EXACT=0 turns it
-    // off (the general kernels take every batch).
-    const int kmax = std::max(1, bl.kmax);
-    const bool wb_req = (b->flags & ULTIMA_HSAMP_WRITEBACK) != 0;
-    bool exact_ok = bl.any_sample && !bl.any_greedy && !bl.any_full && kmax <= 64 && !wb_req && bl.inv_ok &&
-                    (!bl.any_pen || (bl.pen_lowers && !bl.any_dry && bl.max_bias == 0 && bl.max_scan <= 8 * kBlock));
-    if (const char* ev = std::getenv("ULTIMA_HSAMP_EXACT")) exact_ok = exact_ok && ev[0] != '0';
-    // 16-byte loads: aligned rows holding at least one whole chunk
-    const bool vec_rows = (reinterpret_cast<uintptr_t>(b->logits) % 16 == 0) && ((b->logits_stride * es) % 16 == 0) &&
-                          V >= 16 / es;
-    // Slicing: enough blocks to fill the CUs, slices of at most one tile.
-    // Exact lists over aligned rows take slices of up to two tiles while the
-    // batch still gives two blocks per CU: each block's setup, history scan
-    // and bound then cover more ids, and k_pick merges fewer lists. Among
-    // those slicings, the one whose busiest CU streams the fewest ids, with
-    // a block's fixed work counted as kFixedIds ids (blocks spread evenly).
-    const int tiles = (V + kTile - 1) / kTile;
-    int S = std::max(1, std::min({kTargetBlocks / B, tiles, kBlock}));
-    int ex_tiles = 1;
-    if (exact_ok && vec_rows) {
-        constexpr int64_t kFixedIds = 4096;
-        const int S2 = (V + 2 * kTile - 1) / (2 * kTile);
-        int want = ((int64_t)B * S2 >= kTwoTileBlocks && S2 < S) ? 2 : 1;
-        bool forced = false;
-        if (const char* et = std::getenv("ULTIMA_HSAMP_EXACT_TILES")) {
-            want = std::atoi(et) == 2 ? 2 : 1;
-            forced = true;   // two tiles asked for: the fewest slices
-        }
-        if (want == 2) {
-            int best = std::min(S, S2);
-            int64_t best_cost = INT64_MAX;
-            for (int c = best; !forced && c <= std::min(S, 2 * S2); ++c) {
-                const int64_t len = ((V + c - 1) / c + 31) & ~31;
-                const int64_t per_cu = ((int64_t)B * c + h->cus - 1) / h->cus;
-                const int64_t cost = per_cu * (len + kFixedIds);
-                if (cost < best_cost) {
-                    best_cost = cost;
-                    best = c;
-                }
-            }
-            S = best;
-            ex_tiles = 2;
-        }
-    }
-    if (const char* fs = std::getenv("ULTIMA_HSAMP_SLICES")) S = std::max(1, std::min(std::atoi(fs), kBlock));
-    int slice_len = ((V + S - 1) / S + 31) & ~31;
-    S = (V + slice_len - 1) / slice_len;
-    // block and row indices are divided by S with a 32-bit reciprocal (exact below 2^32 / S)
-    if ((uint64_t)(B + 2) * (uint64_t)S * (uint64_t)(S + kXcds) >= (1ull << 32)) return ULTIMA_HSAMP_ERR_CAPACITY;
-    const int buf_cap = std::max(512, next_pow2(2 * kmax));
-    const int cand_cap = slice_len;                 // a slice's list holds all its ids
-    const int bitmap_words = slice_len / 32;
-    const size_t statik = 4096;                     // static LDS of the kernels, rounded up
-    // k_stream: [penalised-id bitmap] [allowed-id mask words]
-    const size_t lds = align16(8 * (size_t)bitmap_words);
-    if (lds + statik > h->lds_limit) return ULTIMA_HSAMP_ERR_CAPACITY;
-    // k_merge: [penalty table | finalize scratch] [candidate buffer]; the
-    // table (load factor <= 1/2) moves to global memory when it does not fit.
-    const size_t regionF = 8 * (size_t)next_pow2(kmax) + 20 * (size_t)kmax;
-    const int mhash = bl.any_pen ? std::max(16, next_pow2(2 * bl.max_pen)) : 16;
-    const size_t lds_budget = std::min<size_t>(h->lds_limit, 64 * 1024) - statik;
-    constexpr size_t kFullWork = 24 * 1024;   // k_full: bucket counts, starts, sort batch
-    const bool gtab = 8 * (size_t)mhash + 8 * (size_t)buf_cap > lds_budget ||
-                      8 * (size_t)mhash + 4 * (size_t)bitmap_words > lds_budget ||
-                      (bl.any_full && 8 * (size_t)mhash + kFullWork > lds_budget);
-    const size_t full_lds = (gtab ? 0 : 8 * (size_t)mhash) + kFullWork;
-    size_t merge_lds = align16(std::max(gtab ? 0 : 8 * (size_t)mhash, regionF)) + 8 * (size_t)buf_cap;
-    // k_merge's fast path: [bins 8 KB][list 1 KB][table 12 B/slot | buffer]
-    // (flag mode: [bins][list][ids, counts / composites of penalised candidates][buffer])
-    const bool fast0 = kmax <= 64 && !gtab && bl.max_scan <= 8 * kBlock && bl.max_bias <= kBlock;
-    const bool pen_flag = fast0 && bl.any_pen && bl.pen_lowers;
-    // flag mode: after the list, counters of the penalised ids, a bitmap over
-    // the vocabulary (16 B per 128 ids) and its rank prefixes (2 B per 128
-    // ids), then the buffer of a row read again in full (rare); one merge
-    // block per row, so it may use the whole LDS of a CU
-    const size_t ngroups = ((size_t)V + 127) / 128;
-    const size_t fast_lds = pen_flag ? 9216 + 8 * (size_t)kCntCap + align16(18 * ngroups) + 8 * (size_t)buf_cap
-                                     : 9216 + std::max(12 * (size_t)mhash, 8 * (size_t)buf_cap);
-    const bool fast = fast0 && fast_lds <= (pen_flag ? h->lds_limit - statik : lds_budget);
-    if (fast) merge_lds = std::max(merge_lds, fast_lds);
-    const size_t wb_lds = (gtab ? 0 : 8 * (size_t)mhash) + 4 * (size_t)bitmap_words;
-    if (merge_lds + statik > h->lds_limit || wb_lds + statik > h->lds_limit ||
-        full_lds + statik > h->lds_limit)
-        return ULTIMA_HSAMP_ERR_CAPACITY;
-    const int nblocks = B * S;
-    const int grid = (nblocks + kXcds - 1) / kXcds * kXcds;
-    int win = std::max(1, std::min(cand_cap, kMergeWindow / S));
-    ex_tiles = slice_len > kTile ? 2 : 1;
-    bool exact = exact_ok && slice_len <= kTile * ex_tiles && (ex_tiles == 1 || vec_rows);
-    // k_stream EX: [count entries, 2 B per slice id + 8 (penalties)][allowed-id mask words]
-    // [staged chunks: kBlock slots of 32 B (16 B data, the chunk's first id)]
-    // (the general instantiations for unaligned rows take PEN = true: their
-    // count entries are cleared and stay zero when no row has penalties)
-    const size_t cnt_bytes = (bl.any_pen || !vec_rows) ? align16(2 * ((size_t)slice_len + 8)) : 0;
-    const size_t stage_off = cnt_bytes + align16(4 * (size_t)bitmap_words);
-    const size_t lds_ex = stage_off + 32 * (size_t)kBlock;
-    // k_pick: each slice's first W entries, NW per thread; W about twice k
-    int pick_nw = 16;
-    if (exact) {
-        const int w0 = std::min(cand_cap, std::max(32, (2 * kmax + 31) / 32 * 32));
-        const int need = (S * w0 + kBlock - 1) / kBlock;
-        pick_nw = need <= 4 ? 4 : need <= 8 ? 8 : need <= 12 ? 12 : 16;
-        win = std::max(1, std::min(cand_cap, pick_nw * kBlock / S));
-        const size_t pick_lds = 8 * std::max<size_t>((size_t)pick_nw * kBlock + 2, (size_t)buf_cap);
-        if (lds_ex + statik > h->lds_limit || pick_lds + statik > h->lds_limit) exact = false;
-        else merge_lds = pick_lds;
-    }
+    RunPlan rp;
+    st = plan_run(h->caps, b, bl, rp);
+    if (st != ULTIMA_HSAMP_OK) return st;
+    if (rp.cand_slots > h->cand_slots) return ULTIMA_HSAMP_ERR_CAPACITY;   // slice counts beyond the handle's
 
     hipStreamCaptureStatus cap_status = hipStreamCaptureStatusNone;
     HIP_TRY(hipStreamIsCapturing(stream, &cap_status));
     const bool capturing = cap_status != hipStreamCaptureStatusNone;
-    // grow-only scratch; the device must be idle before an old area goes away
-    auto grow = [&](auto*& ptr, size_t& have, size_t need, size_t elem) -> int {
-        if (need <= have) return ULTIMA_HSAMP_OK;
-        if (capturing) return ULTIMA_HSAMP_ERR_UNSUPPORTED;   // run once before capturing
-        HIP_TRY(hipDeviceSynchronize());
-        if (ptr) HIP_TRY(hipFree(ptr));
-        ptr = nullptr;
-        have = 0;
-        if (hipMalloc(reinterpret_cast<void**>(&ptr), need * elem) != hipSuccess) {
-            (void)hipGetLastError();
-            ptr = nullptr;
-            return ULTIMA_HSAMP_ERR_NOMEM;
-        }
-        have = need;
-        return ULTIMA_HSAMP_OK;
-    };
-    st = grow(h->ovf, h->ovf_elems, (size_t)B * kMergeRound, 8);
-    if (st == ULTIMA_HSAMP_OK) st = grow(h->cand, h->cand_elems, (size_t)B * S * cand_cap, 8);
-    if (st == ULTIMA_HSAMP_OK && gtab) st = grow(h->gtab, h->gtab_words, (size_t)B * 2 * mhash, 4);
-    const int full_p2 = next_pow2(V);
-    if (st == ULTIMA_HSAMP_OK && bl.any_full) {
-        st = grow(h->fullv, h->fullv_elems, (size_t)B * V, 4);
-        if (st == ULTIMA_HSAMP_OK) st = grow(h->fullp, h->fullp_elems, (size_t)B * V, 4);
-        if (st == ULTIMA_HSAMP_OK) st = grow(h->fullk, h->fullk_elems, (size_t)B * 2 * full_p2, 4);
+    st = grow(h, capturing, h->ovf, h->ovf_elems, rp.ovf_elems);
+    if (st == ULTIMA_HSAMP_OK) st = grow(h, capturing, h->cand, h->cand_elems, rp.cand_elems);
+    if (st == ULTIMA_HSAMP_OK && rp.gtab_words) st = grow(h, capturing, h->gtab, h->gtab_words, rp.gtab_words);
+    if (st == ULTIMA_HSAMP_OK && rp.full_elems) {
+        st = grow(h, capturing, h->fullv, h->fullv_elems, rp.full_elems);
+        if (st == ULTIMA_HSAMP_OK) st = grow(h, capturing, h->fullp, h->fullp_elems, rp.full_elems);
+        if (st == ULTIMA_HSAMP_OK) st = grow(h, capturing, h->fullk, h->fullk_elems, rp.fullk_elems);
     }
     if (st != ULTIMA_HSAMP_OK) return st;
 
     Slot* slot = nullptr;
     st = upload_blob(h, stream, capturing, slot);
     if (st != ULTIMA_HSAMP_OK) return st;
+    if (capturing) h->captured = true;
 
+    RunBuffers buf;
+    buf.cand = h->cand;
+    buf.cand_n = h->cand_n;
+    buf.cand_slots = h->cand_slots;
+    buf.ovf = h->ovf;
+    buf.gtab = h->gtab;
+    buf.fullv = h->fullv;
+    buf.fullp = h->fullp;
+    buf.fullk = h->fullk;
+    buf.fin_idx = h->fin_idx;
+    buf.fin_n = h->fin_n;
+    buf.blob = slot->dev;
+    st = launch_run(rp, bl, b, buf, stream, h->phase_ev);
+    if (st != ULTIMA_HSAMP_OK) return st;
+    if (!capturing) HIP_TRY(hipEventRecord(slot->ev, stream));
+    return ULTIMA_HSAMP_OK;
+}
+
+int ultima_hsamp_read_probe(ultima_hsamp* h, const ultima_hsamp_batch* b, float* out, void* hip_stream) {
+    if (h == nullptr || out == nullptr) return ULTIMA_HSAMP_ERR_INVALID;
+    int st = validate_batch(b, h->max_rows, h->max_vocab);
+    if (st != ULTIMA_HSAMP_OK) return st;
+    HIP_TRY(hipSetDevice(h->device));
+    Built bl;
+    st = build_blob(h->hs, b, bl);
+    if (st != ULTIMA_HSAMP_OK) return st;
+    RunPlan rp;
+    st = plan_run(h->caps, b, bl, rp);
+    if (st != ULTIMA_HSAMP_OK) return st;
+    const int tiles = (rp.slice_len + kTile - 1) / kTile;
+    if (!rp.vec || tiles > 2) return ULTIMA_HSAMP_ERR_UNSUPPORTED;
     StreamArgs a{};
     a.logits = b->logits;
     a.logits_stride = b->logits_stride;
-    a.hist = b->hist;
-    a.hist_stride = b->hist_stride;
-    a.mask = b->mask;
-    a.mask_stride = b->mask_stride;
-    a.u = b->u;
-    a.plans = reinterpret_cast<const RowPlan*>(slot->dev);
-    a.dry_tab = reinterpret_cast<const float*>(slot->dev + bl.off_dry);
-    a.bias_ids = reinterpret_cast<const int32_t*>(slot->dev + bl.off_bias_ids);
-    a.bias_vals = reinterpret_cast<const float*>(slot->dev + bl.off_bias_vals);
-    a.token = b->token;
-    a.row_flags = b->row_flags;
-    a.topk_idx = b->topk_idx;
-    a.topk_count = b->topk_count;
-    a.kept_idx = b->kept_idx;
-    a.kept_prob = b->kept_prob;
-    a.kept_count = b->kept_count;
-    a.set_cap = b->set_cap;
-    a.rows = B;
-    a.vocab = V;
-    a.nslices = S;
-    a.slice_len = slice_len;
-    a.kmax = kmax;
-    a.cand_cap = cand_cap;
-    a.buf_cap = buf_cap;
-    a.mhash_slots = mhash;
-    a.bitmap_words = bitmap_words;
-    a.blocks_per_xcd = grid / kXcds;
-    a.fin_cap = kLimitK;
-    a.ovf = h->ovf;
-    a.ovf_cap = kMergeRound;
-    a.cand = h->cand;
-    a.cand_n = h->cand_n;
-    a.cand_th = h->cand_n + h->cand_slots;
-    a.win = win;
-    a.win_magic = (uint32_t)((1ull << 32) / (uint64_t)win + 1);
-    a.ns_magic = S > 1 ? (uint32_t)((1ull << 32) / (uint64_t)S + 1) : 0u;   // S == 1: the kernels divide by 1 themselves
-    a.dtype = b->dtype;
-    a.fast = fast ? 1 : 0;
-    a.pen_flag = (fast && pen_flag) ? 1 : 0;
-    a.fullv = h->fullv;
-    a.fullp = h->fullp;
-    a.fullk = h->fullk;
-    a.full_p2 = full_p2;
-    a.gtab = gtab ? h->gtab : nullptr;
-    a.merge_lds = (uint32_t)merge_lds;
-    const bool wb = (b->flags & ULTIMA_HSAMP_WRITEBACK) != 0;
-    a.fin_idx = wb ? h->fin_idx : nullptr;
-    a.fin_n = wb ? h->fin_n : nullptr;
-    a.lds_bytes = (uint32_t)(exact ? lds_ex : lds);
-    a.exact = exact ? 1 : 0;
-    a.mbm_off = (int32_t)(cnt_bytes / 4);
-    a.stage_off = (int32_t)stage_off;
-    a.hist_direct = (exact && bl.any_pen && b->hist != nullptr && b->hist_stride >= 1 &&
-                     b->hist_stride <= 8 * kBlock) ? 1 : 0;
-    // 16-byte loads: aligned rows holding at least one whole chunk
-    const bool vec = vec_rows;
-    a.vec_tail = vec ? V % (16 / es) : 0;
-    a.uniform = (bl.any_greedy && !bl.any_sample && !bl.any_full ? 1 : 0) |
-                (bl.any_sample && !bl.any_greedy && !bl.any_full ? 2 : 0);
-    // In flag mode the sampling rows' stream needs no penalties at all: it
-    // bounds on pre-penalty keys, which penalties can only lower, and k_merge
-    // finds the penalised candidates' true values (checking the bounds).
-    if (exact)
-        HIP_TRY(launch_stream_ex(a, b->dtype, vec, bl.any_pen, bl.any_mask, ex_tiles, grid, stream));
-    else if (bl.any_topk)
-        HIP_TRY(launch_stream(a, b->dtype, vec, bl.any_pen, bl.any_pen && !a.pen_flag, bl.any_mask, bl.any_greedy,
-                              bl.any_sample, grid, stream));
-    if (h->phase_ev != nullptr) HIP_TRY(hipEventRecord(h->phase_ev, stream));
-    if (!(b->flags & ULTIMA_HSAMP_STREAM_ONLY)) {
-        if (exact) HIP_TRY(launch_pick(a, pick_nw, stream));
-        else if (bl.any_topk) HIP_TRY(launch_merge(a, stream));
-        if (bl.any_full) HIP_TRY(launch_full(a, (uint32_t)full_lds, stream));
-        if (wb) HIP_TRY(launch_writeback(a, grid, (uint32_t)wb_lds, stream));
-    }
-    if (!capturing) HIP_TRY(hipEventRecord(slot->ev, stream));
+    a.rows = rp.B;
+    a.vocab = rp.V;
+    a.nslices = rp.S;
+    a.slice_len = rp.slice_len;
+    a.blocks_per_xcd = rp.grid / kXcds;
+    a.ns_magic = rp.S > 1 ? (uint32_t)((1ull << 32) / (uint64_t)rp.S + 1) : 0u;
+    a.vec_tail = rp.V % (16 / (b->dtype == ULTIMA_HSAMP_F32 ? 4 : 2));
+    HIP_TRY(launch_read_probe(a, b->dtype, tiles, rp.grid, out, static_cast<hipStream_t>(hip_stream)));
     return ULTIMA_HSAMP_OK;
 }
 

@@ -3968,6 +3968,52 @@ __global__ __launch_bounds__(kBlock) void k_full(StreamArgs a) {
     }
 }
 
+// ---- diagnostics: a plain read with the stream kernel's launch shape --------------
+
+// The same grid, block-to-slice mapping, buffer resources and 16-byte
+// non-temporal loads as the exact-list k_stream (aligned rows), and nothing
+// else: each block reads its slice, takes the maximum and writes it to
+// out[logical block]. Its duration is the floor any pass over these bytes
+// with this launch shape can reach.
+template <int DT, int NT>
+__global__ __launch_bounds__(kBlock) void k_read_probe(StreamArgs a, float* out) {
+    using T = Tile<DT>;
+    constexpr int NC = T::NCH * NT;
+    __shared__ float red[kBlock / 64];
+    const uint32_t bid = blockIdx.x;
+    const int logical = (int)(bid % kXcds) * a.blocks_per_xcd + (int)(bid / kXcds);
+    const int r = div_slices(logical, a), s = logical - r * a.nslices;
+    if (r >= a.rows) return;
+    const int lo = s * a.slice_len;
+    const int hi = min(a.vocab - a.vec_tail, lo + a.slice_len);
+    const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * T::ES;
+    uint4 raw[NC];
+    load_tile<DT, true, NC>(row_rsrc(rowp, hi, T::ES), lo, raw);
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int j = 0; j < NC; ++j)
+#pragma unroll
+        for (int c = 0; c < T::VW; ++c) m = fmaxf(m, elem<DT>(raw[j], c));
+    m = wave_max_f(m);
+    if (lane_id() == 0) red[wave_id()] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) out[logical] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+hipError_t launch_read_probe(const StreamArgs& a, int dtype, int tiles, int grid, float* out, hipStream_t stream) {
+    const dim3 g(grid), b(kBlock);
+    if (tiles == 1) {
+        if (dtype == 0) hipLaunchKernelGGL((k_read_probe<0, 1>), g, b, 0, stream, a, out);
+        else hipLaunchKernelGGL((k_read_probe<1, 1>), g, b, 0, stream, a, out);
+    } else if (tiles == 2) {
+        if (dtype == 0) hipLaunchKernelGGL((k_read_probe<0, 2>), g, b, 0, stream, a, out);
+        else hipLaunchKernelGGL((k_read_probe<1, 2>), g, b, 0, stream, a, out);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 // ---- launchers -------------------------------------------------------------------
 
 template <bool GR>

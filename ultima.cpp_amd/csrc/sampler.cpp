@@ -24,7 +24,7 @@ struct Backend {
     std::mutex mu;
     ultima_hsamp* h = nullptr;
     int status = ULTIMA_HSAMP_OK;
-    bool writeback = false;
+    bool writeback = true;    // sample() leaves logits as the reference does (in place)
     std::vector<float> scratch;
 };
 

@@ -115,6 +115,8 @@ def lib() -> ctypes.CDLL:
         L.ultima_hsamp_status_str.argtypes = [ctypes.c_int]
         L.ultima_hsamp_version.restype = ctypes.c_int
         L.ultima_hsamp_version.argtypes = []
+        L.ultima_hsamp_read_probe.restype = ctypes.c_int
+        L.ultima_hsamp_read_probe.argtypes = [vp, ctypes.POINTER(Batch), vp, vp]
         L.ultima_hsamp_set_phase_event.restype = ctypes.c_int
         L.ultima_hsamp_set_phase_event.argtypes = [vp, vp]
         _lib = L
@@ -155,6 +157,59 @@ def make_params(plist, hist_len=None, bias=None):
     return arr, bids, bvals
 
 
+def _batch(logits, params, u, hist, hist_len, mask, bias, writeback, want_sets, set_cap, stream, outputs,
+           stream_only):
+    """An ultima_hsamp_batch over torch tensors: (batch, outputs, host arrays
+    the call reads, stream)."""
+    import torch
+    B, V = logits.shape[0], logits.shape[1]
+    dev = logits.device
+    out = outputs if outputs is not None else {}
+    if "token" not in out:
+        out["token"] = torch.empty(B, dtype=torch.int32, device=dev)
+    if "row_flags" not in out:
+        out["row_flags"] = torch.empty(B, dtype=torch.int32, device=dev)
+    cap = 0
+    if want_sets:
+        cap = set_cap or V
+        for k, dt in (("topk_idx", torch.int32), ("kept_idx", torch.int32),
+                      ("kept_prob", torch.float32)):
+            if k not in out:
+                out[k] = torch.empty((B, cap), dtype=dt, device=dev)
+        for k in ("topk_count", "kept_count"):
+            if k not in out:
+                out[k] = torch.empty(B, dtype=torch.int32, device=dev)
+    parr, bids, bvals = make_params(params, hist_len, bias)
+    b = Batch()
+    b.rows, b.vocab = B, V
+    b.dtype = F32 if logits.dtype == torch.float32 else BF16
+    b.flags = (WRITEBACK if writeback else 0) | (STREAM_ONLY if stream_only else 0)
+    b.logits = logits.data_ptr()
+    b.logits_stride = logits.stride(0)
+    if hist is not None:
+        b.hist = hist.data_ptr()
+        b.hist_stride = hist.stride(0)
+    if mask is not None:
+        b.mask = mask.data_ptr()
+        b.mask_stride = mask.stride(0)
+    b.u = u.data_ptr()
+    b.params = ctypes.cast(parr, ctypes.POINTER(Params))
+    if bids is not None:
+        b.bias_ids = bids.ctypes.data
+        b.bias_vals = bvals.ctypes.data
+    b.token = out["token"].data_ptr()
+    b.row_flags = out["row_flags"].data_ptr()
+    if want_sets:
+        b.topk_idx = out["topk_idx"].data_ptr()
+        b.topk_count = out["topk_count"].data_ptr()
+        b.kept_idx = out["kept_idx"].data_ptr()
+        b.kept_prob = out["kept_prob"].data_ptr()
+        b.kept_count = out["kept_count"].data_ptr()
+        b.set_cap = cap
+    s = torch.cuda.current_stream(dev) if stream is None else stream
+    return b, out, (parr, bids, bvals), s
+
+
 class Sampler:
     """A handle on one device (create/destroy of the C ABI)."""
 
@@ -182,54 +237,29 @@ class Sampler:
         [B, H]; mask: cuda int32/uint32 [B, W]. Returns a dict of cuda tensors.
         `outputs` may carry preallocated tensors (token, row_flags, ...).
         stream_only (diagnostics): run only the pass over the logits."""
-        import torch
-        B, V = logits.shape[0], logits.shape[1]
-        dev = logits.device
-        out = outputs if outputs is not None else {}
-        if "token" not in out:
-            out["token"] = torch.empty(B, dtype=torch.int32, device=dev)
-        if "row_flags" not in out:
-            out["row_flags"] = torch.empty(B, dtype=torch.int32, device=dev)
-        cap = 0
-        if want_sets:
-            cap = set_cap or V
-            for k, dt in (("topk_idx", torch.int32), ("kept_idx", torch.int32),
-                          ("kept_prob", torch.float32)):
-                if k not in out:
-                    out[k] = torch.empty((B, cap), dtype=dt, device=dev)
-            for k in ("topk_count", "kept_count"):
-                if k not in out:
-                    out[k] = torch.empty(B, dtype=torch.int32, device=dev)
-        parr, bids, bvals = make_params(params, hist_len, bias)
-        b = Batch()
-        b.rows, b.vocab = B, V
-        b.dtype = F32 if logits.dtype == torch.float32 else BF16
-        b.flags = (WRITEBACK if writeback else 0) | (STREAM_ONLY if stream_only else 0)
-        b.logits = logits.data_ptr()
-        b.logits_stride = logits.stride(0)
-        if hist is not None:
-            b.hist = hist.data_ptr()
-            b.hist_stride = hist.stride(0)
-        if mask is not None:
-            b.mask = mask.data_ptr()
-            b.mask_stride = mask.stride(0)
-        b.u = u.data_ptr()
-        b.params = ctypes.cast(parr, ctypes.POINTER(Params))
-        if bids is not None:
-            b.bias_ids = bids.ctypes.data
-            b.bias_vals = bvals.ctypes.data
-        b.token = out["token"].data_ptr()
-        b.row_flags = out["row_flags"].data_ptr()
-        if want_sets:
-            b.topk_idx = out["topk_idx"].data_ptr()
-            b.topk_count = out["topk_count"].data_ptr()
-            b.kept_idx = out["kept_idx"].data_ptr()
-            b.kept_prob = out["kept_prob"].data_ptr()
-            b.kept_count = out["kept_count"].data_ptr()
-            b.set_cap = cap
-        s = torch.cuda.current_stream(dev) if stream is None else stream
+        b, out, keep, s = _batch(logits, params, u, hist, hist_len, mask, bias, writeback, want_sets, set_cap,
+                                 stream, outputs, stream_only)
         check(lib().ultima_hsamp_run(self.h, ctypes.byref(b), ctypes.c_void_p(s.cuda_stream)), "run")
+        del keep
         return out
+
+    def batch(self, logits, params, u, hist=None, hist_len=None, mask=None, bias=None, outputs=None):
+        """The ultima_hsamp_batch run() would pass for these tensors: (batch,
+        host arrays it points into, which the caller keeps alive). For callers
+        that time the C ABI itself (bench.py's uncaptured figure)."""
+        b, out, keep, s = _batch(logits, params, u, hist, hist_len, mask, bias, False, False, None, None,
+                                 outputs, False)
+        return b, (out, keep)
+
+    def read_probe(self, logits, params, u, out, hist=None, hist_len=None, mask=None, stream=None):
+        """Diagnostics: a plain read of `logits` with the launch shape run()
+        would use (ultima_hsamp_read_probe); out: cuda float32, rows * 256."""
+        import torch
+        b, _, keep, s = _batch(logits, params, u, hist, hist_len, mask, None, False, False, None, stream,
+                               {"token": out, "row_flags": out}, False)
+        check(lib().ultima_hsamp_read_probe(self.h, ctypes.byref(b), ctypes.c_void_p(out.data_ptr()),
+                                            ctypes.c_void_p(s.cuda_stream)), "read_probe")
+        del keep, torch
 
     def set_phase_event(self, event):
         """Record `event` (a torch.cuda.Event already recorded once, or None)

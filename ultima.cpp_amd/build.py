@@ -60,8 +60,9 @@ def build_all() -> None:
     objs = {
         "hsamp_kernels.o": CSRC / "hsamp_kernels.hip",
         "hsamp_api.o": CSRC / "hsamp_api.cpp",
+        "hsamp_noalloc.o": CSRC / "hsamp_noalloc.hip",
     }
-    with ThreadPoolExecutor(max_workers=2) as ex:
+    with ThreadPoolExecutor(max_workers=3) as ex:
         futs = [ex.submit(_run, [HIPCC, *HIP_FLAGS, "-x", "hip", "-c", str(src), "-o", str(BUILD / o)])
                 for o, src in objs.items()]
         for f in futs:

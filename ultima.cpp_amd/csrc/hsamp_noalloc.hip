@@ -1,0 +1,133 @@
+// ultima_hsamp_run_noalloc: ultima_hsamp_run without a handle and without any
+// allocation, for callers that cannot allocate device memory (code under HIP
+// graph capture, tight serving loops, harnesses that forbid hipMalloc).
+//
+// The kernels' scratch (candidate lists, per-slice counts, overflow buffers,
+// penalty tables, full-vocabulary buffers and the uploaded per-row plans) is
+// carved from `scratch`, a fixed device array each GPU holds until the process
+// ends. Host code never passes the array's name to a kernel or a copy: at the
+// first call on a device, with that device current, its address on that
+// device is read with hipGetSymbolAddress and kept per device; every later
+// use goes through that address.
+//
+// Every call on one GPU shares that GPU's array and it keeps the last call's
+// contents. Calls that overlap on one GPU (two streams, two threads) race on
+// it: the caller serialises them, e.g. by issuing them on one stream.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "hsamp_run.h"
+#include "ultima_hsamp.h"
+
+namespace {
+
+using namespace hsamp;
+
+constexpr size_t kScratchBytes = ULTIMA_HSAMP_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+struct DeviceState {
+    bool ready = false;
+    unsigned char* ptr = nullptr;   // this device's address of `scratch`
+    DevCaps caps;
+    std::vector<char> resident;     // the plan blob the array holds (host copy)
+};
+
+std::mutex g_mu;
+DeviceState g_dev[kMaxDevices];
+
+// Set-up, once per device, with that device current.
+int setup(int dev, DeviceState*& out) {
+    if (dev < 0 || dev >= kMaxDevices) return ULTIMA_HSAMP_ERR_NO_DEVICE;
+    DeviceState& d = g_dev[dev];
+    if (!d.ready) {
+        hipDeviceProp_t prop;
+        const hipError_t pe = hipGetDeviceProperties(&prop, dev);
+        if (pe != hipSuccess) {
+            hip_fail(pe, "hipGetDeviceProperties", __LINE__);
+            return ULTIMA_HSAMP_ERR_NO_DEVICE;
+        }
+        if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return ULTIMA_HSAMP_ERR_NO_DEVICE;
+        void* p = nullptr;
+        const hipError_t se = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (se != hipSuccess || p == nullptr) return hip_fail(se, "hipGetSymbolAddress(scratch)", __LINE__);
+        d.ptr = static_cast<unsigned char*>(p);
+        d.caps.lds_limit = prop.sharedMemPerBlock;
+        d.caps.cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 1;
+        d.ready = true;
+    }
+    out = &d;
+    return ULTIMA_HSAMP_OK;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+}  // namespace
+
+extern "C" int ultima_hsamp_run_noalloc(const ultima_hsamp_batch* b, void* hip_stream) {
+    int st = validate_batch(b, INT32_MAX, ULTIMA_HSAMP_MAX_VOCAB);
+    if (st != ULTIMA_HSAMP_OK) return st;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return hip_fail(hipErrorNoDevice, "hipGetDevice", __LINE__);
+    std::lock_guard<std::mutex> lk(g_mu);
+    DeviceState* d = nullptr;
+    st = setup(dev, d);
+    if (st != ULTIMA_HSAMP_OK) return st;
+    hipStream_t stream = static_cast<hipStream_t>(hip_stream);
+
+    static thread_local HostScratch hs;
+    Built bl;
+    st = build_blob(hs, b, bl);
+    if (st != ULTIMA_HSAMP_OK) return st;
+    RunPlan rp;
+    st = plan_run(d->caps, b, bl, rp);
+    if (st != ULTIMA_HSAMP_OK) return st;
+
+    // The array's layout for this run: [plans blob][slice counts + bounds]
+    // [candidate lists][overflow][penalty tables][fullv][fullp][fullk][kept ids][kept counts]
+    size_t off = 0;
+    auto take = [&](size_t bytes) -> unsigned char* {
+        unsigned char* p = d->ptr + off;
+        off = align256(off + bytes);
+        return p;
+    };
+    RunBuffers buf;
+    unsigned char* blob = take(bl.total);
+    buf.blob = reinterpret_cast<const char*>(blob);
+    buf.cand_slots = rp.cand_slots;
+    buf.cand_n = reinterpret_cast<int32_t*>(take(rp.cand_slots * 8));
+    buf.cand = reinterpret_cast<unsigned long long*>(take(rp.cand_elems * 8));
+    buf.ovf = reinterpret_cast<unsigned long long*>(take(rp.ovf_elems * 8));
+    if (rp.gtab_words) buf.gtab = reinterpret_cast<uint32_t*>(take(rp.gtab_words * 4));
+    if (rp.full_elems) {
+        buf.fullv = reinterpret_cast<float*>(take(rp.full_elems * 4));
+        buf.fullp = reinterpret_cast<float*>(take(rp.full_elems * 4));
+        buf.fullk = reinterpret_cast<uint32_t*>(take(rp.fullk_elems * 4));
+    }
+    if (rp.fin_elems) {
+        buf.fin_idx = reinterpret_cast<int32_t*>(take(rp.fin_elems * 4));
+        buf.fin_n = reinterpret_cast<int32_t*>(take((size_t)rp.B * 4));
+    }
+    if (off > kScratchBytes) return ULTIMA_HSAMP_ERR_CAPACITY;
+
+    // The per-row plans go to the front of the array unless it already holds
+    // the same bytes (a caller that keeps its knobs uploads them once). Under
+    // stream capture nothing is copied: the same batch must have run first.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) != hipSuccess) return hip_fail(hipErrorUnknown, "hipStreamIsCapturing", __LINE__);
+    const bool same = d->resident.size() == hs.blob.size() &&
+                      std::memcmp(d->resident.data(), hs.blob.data(), hs.blob.size()) == 0;
+    if (!same) {
+        if (cap != hipStreamCaptureStatusNone) return ULTIMA_HSAMP_ERR_UNSUPPORTED;
+        d->resident.clear();   // nothing known to be resident until the copy is queued
+        const hipError_t ce = hipMemcpyAsync(blob, hs.blob.data(), hs.blob.size(), hipMemcpyHostToDevice, stream);
+        if (ce != hipSuccess) return hip_fail(ce, "hipMemcpyAsync(plans -> scratch)", __LINE__);
+        d->resident = hs.blob;
+    }
+    return launch_run(rp, bl, b, buf, stream, nullptr);
+}

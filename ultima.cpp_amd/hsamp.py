@@ -18,6 +18,7 @@ HEADER = PKG.parent / "include" / "ultima_hsamp.h"
 OK, ERR_INVALID, ERR_HIP, ERR_UNSUPPORTED, ERR_NOMEM, ERR_CAPACITY, ERR_NO_DEVICE = 0, -1, -2, -3, -4, -5, -6
 F32, BF16 = 0, 1
 WRITEBACK, STREAM_ONLY = 1, 0x100
+NOALLOC_SCRATCH_BYTES = 96 << 20
 ROW_GREEDY, ROW_U_USED, ROW_CDF_NEAR, ROW_NAN, ROW_UNIFORM, ROW_TOPP_NEAR, ROW_REREAD = 1, 2, 4, 8, 16, 32, 64
 
 PARAM_KEYS = ("rep_penalty", "dry_multiplier", "dry_base", "frequency_penalty", "presence_penalty",
@@ -115,6 +116,8 @@ def lib() -> ctypes.CDLL:
         L.ultima_hsamp_status_str.argtypes = [ctypes.c_int]
         L.ultima_hsamp_version.restype = ctypes.c_int
         L.ultima_hsamp_version.argtypes = []
+        L.ultima_hsamp_run_noalloc.restype = ctypes.c_int
+        L.ultima_hsamp_run_noalloc.argtypes = [ctypes.POINTER(Batch), vp]
         L.ultima_hsamp_read_probe.restype = ctypes.c_int
         L.ultima_hsamp_read_probe.argtypes = [vp, ctypes.POINTER(Batch), vp, vp]
         L.ultima_hsamp_set_phase_event.restype = ctypes.c_int
@@ -208,6 +211,17 @@ def _batch(logits, params, u, hist, hist_len, mask, bias, writeback, want_sets, 
         b.set_cap = cap
     s = torch.cuda.current_stream(dev) if stream is None else stream
     return b, out, (parr, bids, bvals), s
+
+
+def run_noalloc(logits, params, u, hist=None, hist_len=None, mask=None, bias=None, writeback=False,
+                want_sets=False, set_cap=None, stream=None, outputs=None):
+    """ultima_hsamp_run_noalloc on the current device: Sampler.run without a
+    handle, scratch from the library's fixed device array."""
+    b, out, keep, s = _batch(logits, params, u, hist, hist_len, mask, bias, writeback, want_sets, set_cap,
+                             stream, outputs, False)
+    check(lib().ultima_hsamp_run_noalloc(ctypes.byref(b), ctypes.c_void_p(s.cuda_stream)), "run_noalloc")
+    del keep
+    return out
 
 
 class Sampler:

@@ -1,0 +1,49 @@
+// Test kit for the exact-sum engine of k_full (ultima.cpp_amd/csrc/hsamp_xsum.h):
+// one block of kFT threads takes a sequence x[0, n) of floats >= 0 (padded
+// with +0 to Vp = a whole number of 512 * G windows) and returns
+//   out[0]  its sequential float32 sum in index order (exact_index_sum),
+// and, when thr > 0, the top-p driver's answer for x as probabilities:
+//   outi[0] whether the running sum in descending order reaches thr,
+//   outi[1] how many values that takes, out[1] the last one, out[2] the sum.
+// tests/test_gpu_xsum.py compares them with numpy's sequential float32 sums.
+#include <hip/hip_runtime.h>
+
+#include "hsamp_xsum.h"
+
+using namespace hsamp;
+
+__global__ __launch_bounds__(kFT) void k_xsum(const float* x, int n, int Vp, int G, float thr, float* out, int* outi,
+                                              uint32_t* fk) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ FullShared st;
+    const FullLds f = full_lds(smem);
+    const int lane = lane_id(), wid = wave_id();
+    const int WS = kFWin * G, nW = Vp / WS;
+    for (int w = wid; w < nW; w += kFW) {
+        float ws = 0.0f;
+        for (int i = lane; i < WS; i += 64) ws += x[(size_t)w * WS + i];
+        ws = wave_tree_prefix_f(ws);
+        if (lane == 63) f.winA[w] = ws;
+    }
+    __syncthreads();
+    const XState s = exact_index_sum(x, nW, G, f, st);
+    if (threadIdx.x == 0) out[0] = xs_value(s);
+    if (thr > 0.0f) {
+        uint32_t ck = 0u;
+        int cc = 0;
+        const bool ok = full_top_p(x, n, Vp, 1.0f, thr, fk, f, st, &ck, &cc);
+        if (threadIdx.x == 0) {
+            outi[0] = ok ? 1 : 0;
+            outi[1] = cc;
+            out[1] = __uint_as_float(ck);
+            out[2] = (float)st.dS;
+        }
+    }
+}
+
+extern "C" int xsum_run(const float* x, int n, int Vp, int G, float thr, float* out, int* outi, uint32_t* fk) {
+    hipLaunchKernelGGL(k_xsum, dim3(1), dim3(kFT), kFullLdsBytes, nullptr, x, n, Vp, G, thr, out, outi, fk);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    return (int)hipDeviceSynchronize();
+}

@@ -1,0 +1,105 @@
+"""The exact-sum engine of k_full on the GPU (tests/cpp/xsum_kit.hip).
+
+softmax_probs (reference src/sampler/sampler.cpp:124-142) and apply_top_p
+(:146-164) take float32 running sums over up to V values; k_full reproduces
+them in parallel from integer increments per binade. Here the engine runs on
+sequences built to stress it -- sums that cross many binades, values exactly
+half-way between two multiples of the running sum's ulp (round half to even),
+subnormals, zeros, equal values, single huge values, a sequence longer than
+one window table (512-id windows of two steps) -- and must give numpy's
+sequential float32 sums (np.add.accumulate is a plain left-to-right loop)
+bit for bit, and the top-p driver the exact cutoff of the descending order.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _kit(pkg):
+    import torch  # noqa: F401  (first: the kit binds to torch's HIP runtime, one per process)
+    lib = ctypes.CDLL(str(pkg.hsamp.PKG.parent / "tests" / "cpp" / "libxsum_kit.so"))
+    lib.xsum_run.restype = ctypes.c_int
+    lib.xsum_run.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float,
+                             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    return lib
+
+
+def _run(kit, x, thr):
+    import torch
+    n = x.size
+    w512 = (n + 511) // 512
+    G = max(1, (w512 + 2047) // 2048)
+    ws = 512 * G
+    Vp = (n + ws - 1) // ws * ws
+    xp = np.zeros(Vp, np.float32)
+    xp[:n] = x
+    dev = torch.device("cuda:0")
+    xd = torch.from_numpy(xp).to(dev)
+    out = torch.zeros(4, dtype=torch.float32, device=dev)
+    outi = torch.zeros(4, dtype=torch.int32, device=dev)
+    fk = torch.zeros(max(n, 1), dtype=torch.int32, device=dev)
+    rc = kit.xsum_run(xd.data_ptr(), n, Vp, G, float(thr), out.data_ptr(), outi.data_ptr(), fk.data_ptr())
+    assert rc == 0, f"xsum_run: HIP status {rc}"
+    return out.cpu().numpy(), outi.cpu().numpy()
+
+
+def _seq(x):
+    return np.add.accumulate(x.astype(np.float32), dtype=np.float32)
+
+
+def _cases():
+    rng = np.random.default_rng(2024)
+    c = {}
+    c["flat"] = np.exp(rng.normal(0, 0.1, 151936)).astype(np.float32)
+    c["spiky"] = np.exp(rng.normal(0, 1, 151936) - 15).astype(np.float32)
+    c["spiky"][rng.choice(151936, 16, replace=False)] = 1.0
+    # multiples of 2^-20: increments land exactly half-way once the sum passes 2^4
+    c["halfway"] = (rng.integers(1, 64, 120000) * 2.0**-20).astype(np.float32)
+    c["halfway"][::7] = 2.0**-20
+    c["subnormal"] = (rng.random(50000) * 1e-39).astype(np.float32)
+    z = np.exp(rng.normal(0, 3, 80000)).astype(np.float32)
+    z[rng.random(80000) < 0.3] = 0.0
+    c["zeros_wide"] = z
+    c["equal"] = np.full(151936, np.float32(6.5e-6))
+    w = np.exp(rng.normal(0, 0.1, 151936)).astype(np.float32)
+    w[1234] = np.float32(3e4)
+    c["one_huge"] = w
+    t = np.exp(rng.normal(-30, 0.1, 151936)).astype(np.float32)
+    t[5] = np.float32(1e-44)
+    c["outlier_range"] = t
+    c["long"] = np.exp(rng.normal(0, 0.5, 1_200_000)).astype(np.float32)     # 2-step windows
+    c["tiny"] = np.array([3.0, 0.0, 1e-8], np.float32)
+    return c
+
+
+CASES = _cases()
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_exact_index_sum(pkg, name):
+    kit = _kit(pkg)
+    x = CASES[name]
+    out, _ = _run(kit, x, 0.0)
+    want = _seq(x)[-1]
+    assert out[0].view(np.uint32) == want.view(np.uint32), f"{name}: {out[0]!r} != {want!r}"
+
+
+@pytest.mark.parametrize("name", [n for n in CASES if n not in ("long", "tiny")])
+@pytest.mark.parametrize("frac", [0.9, 0.5, 0.999])
+def test_top_p_cutoff(pkg, name, frac):
+    kit = _kit(pkg)
+    x = CASES[name]
+    xs = np.sort(x)[::-1]
+    cum = _seq(xs)
+    thr = np.float32(frac * float(cum[-1]))
+    out, outi = _run(kit, x, float(thr))
+    hit = np.nonzero(cum >= thr)[0]
+    assert outi[0] == (1 if hit.size else 0), name
+    if hit.size:
+        j = int(hit[0])
+        assert outi[1] == j + 1, f"{name}: cut after {outi[1]} values, want {j + 1}"
+        assert out[1].view(np.uint32) == xs[j].view(np.uint32), name
+        assert out[2].view(np.uint32) == cum[j].view(np.uint32), name

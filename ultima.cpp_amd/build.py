@@ -4,6 +4,7 @@
     libultima_sampler.so -- the ultima::sampler C++ drop-in (include/ultima/sampler/sampler.hpp)
     dropin_driver        -- tests/cpp/dropin_driver.cpp linked against the drop-in
     tests/cpp/libdevice_expf.so -- test kit evaluating the device expf
+    tests/cpp/libxsum_kit.so    -- test kit running the exact-sum engine of k_full
 
 Every call compiles from scratch (no staleness checks): the outputs are small
 and the compile takes well under a minute.
@@ -76,6 +77,8 @@ def build_all() -> None:
           f"-L{PKG}", "-lultima_hsamp", "-Wl,-rpath,$ORIGIN"])
     _run([HIPCC, *HIP_FLAGS, "-shared", "-x", "hip", str(ROOT / "tests" / "cpp" / "device_expf.hip"),
           "-o", str(ROOT / "tests" / "cpp" / "libdevice_expf.so")])
+    _run([HIPCC, *HIP_FLAGS, "-shared", "-x", "hip", str(ROOT / "tests" / "cpp" / "xsum_kit.hip"),
+          "-o", str(ROOT / "tests" / "cpp" / "libxsum_kit.so")])
     # the test driver also allocates device memory itself (sample_batch)
     _run([*cxx, "-D__HIP_PLATFORM_AMD__", f"-I{ROCM / 'include'}", str(ROOT / "tests" / "cpp" / "dropin_driver.cpp"),
           "-o", str(CPP_TEST), f"-L{PKG}", "-lultima_sampler", "-lultima_hsamp", f"-L{ROCM / 'lib'}", "-lamdhip64",

@@ -33,6 +33,7 @@ hipError_t launch_stream_ex(const StreamArgs& a, int dtype, bool vec, bool pen, 
 hipError_t launch_pick(const StreamArgs& a, int nw, hipStream_t stream);
 hipError_t launch_full(const StreamArgs& a, uint32_t lds, hipStream_t stream);
 hipError_t launch_read_probe(const StreamArgs& a, int dtype, int tiles, int grid, float* out, hipStream_t stream);
+size_t full_lds_bytes();
 }  // namespace hsamp
 
 using namespace hsamp;
@@ -45,6 +46,7 @@ constexpr int kTargetBlocks = 4096;     // most blocks a launch spreads rows ove
 constexpr int kTwoTileBlocks = 512;     // exact lists: two-tile slices while B * S stays at or above this
 constexpr int kMergeRound = kBlock * 16;  // candidates k_merge offers per round
 constexpr int kMergeWindow = kBlock * 16; // list entries k_merge loads up front, over all slices
+constexpr int kFullMaxWin = 2048;       // k_full: index-order windows its LDS tables hold
 
 struct Slot {
     char* host = nullptr;   // pinned
@@ -396,12 +398,17 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     const int mhash = bl.any_pen ? std::max(16, next_pow2(2 * bl.max_pen)) : 16;
     rp.mhash = mhash;
     const size_t lds_budget = std::min<size_t>(dc.lds_limit, 64 * 1024) - statik;
-    constexpr size_t kFullWork = 24 * 1024;   // k_full: bucket counts, starts, sort batch
+    const size_t full_work = full_lds_bytes();   // k_full: window and bucket tables, sort buffer
     const bool gtab = 8 * (size_t)mhash + 8 * (size_t)buf_cap > lds_budget ||
                       8 * (size_t)mhash + 4 * (size_t)bitmap_words > lds_budget ||
-                      (bl.any_full && 8 * (size_t)mhash + kFullWork > lds_budget);
+                      (bl.any_full && 8 * (size_t)mhash + full_work + statik > dc.lds_limit);
     rp.gtab = gtab;
-    rp.full_lds = (gtab ? 0 : 8 * (size_t)mhash) + kFullWork;
+    rp.full_lds = (gtab ? 0 : 8 * (size_t)mhash) + full_work;
+    // k_full's rows: windows of 512 * G ids, at most kFullMaxWin of them
+    const int64_t w512 = ((int64_t)V + 511) / 512;
+    rp.full_g = (int)std::max<int64_t>(1, (w512 + kFullMaxWin - 1) / kFullMaxWin);
+    const int64_t ws = 512 * (int64_t)rp.full_g;
+    rp.full_stride = (int)(((int64_t)V + ws - 1) / ws * ws);
     size_t merge_lds = align16(std::max(gtab ? 0 : 8 * (size_t)mhash, regionF)) + 8 * (size_t)buf_cap;
     // k_merge's fast path: [bins 8 KB][list 1 KB][table 12 B/slot | buffer]
     // (flag mode: [bins][list][ids, counts / composites of penalised candidates][buffer])
@@ -420,7 +427,7 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     rp.pen_flag = fast && pen_flag;
     rp.wb_lds = (gtab ? 0 : 8 * (size_t)mhash) + 4 * (size_t)bitmap_words;
     if (merge_lds + statik > dc.lds_limit || rp.wb_lds + statik > dc.lds_limit ||
-        rp.full_lds + statik > dc.lds_limit)
+        (bl.any_full && rp.full_lds + statik > dc.lds_limit))
         return ULTIMA_HSAMP_ERR_CAPACITY;
     const int nblocks = B * S;
     rp.grid = (nblocks + kXcds - 1) / kXcds * kXcds;
@@ -452,8 +459,8 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     rp.cand_elems = (size_t)nblocks * (size_t)cand_cap;
     rp.ovf_elems = (size_t)B * kMergeRound;
     rp.gtab_words = gtab ? (size_t)B * 2 * mhash : 0;
-    rp.full_elems = bl.any_full ? (size_t)B * V : 0;
-    rp.fullk_elems = bl.any_full ? (size_t)B * 2 * rp.full_p2 : 0;
+    rp.full_elems = bl.any_full ? (size_t)B * rp.full_stride : 0;
+    rp.fullk_elems = bl.any_full ? (size_t)B * rp.full_p2 : 0;
     rp.fin_elems = rp.wb ? (size_t)B * kLimitK : 0;
     return ULTIMA_HSAMP_OK;
 }
@@ -506,6 +513,8 @@ int launch_run(const RunPlan& rp, const Built& bl, const ultima_hsamp_batch* b, 
     a.fullp = buf.fullp;
     a.fullk = buf.fullk;
     a.full_p2 = rp.full_p2;
+    a.full_stride = rp.full_stride;
+    a.full_g = rp.full_g;
     a.gtab = rp.gtab ? buf.gtab : nullptr;
     a.merge_lds = (uint32_t)rp.merge_lds;
     a.fin_idx = rp.wb ? buf.fin_idx : nullptr;

@@ -27,28 +27,14 @@
 #include <algorithm>
 
 #include "hsamp_plan.h"
+#include "hsamp_wave.h"
+#include "hsamp_xsum.h"
 #include "libm_expf.h"
 
 #pragma clang fp contract(off)
 
 namespace hsamp {
 
-using u64 = unsigned long long;
-
-// Diagnostics: with HSAMP_PHASE_CLOCKS defined, thread 0 of each block records
-// the 100 MHz real-time clock at numbered points of the stream and merge
-// kernels (slot = block * 16 + point; stream blocks by logical id, merge
-// blocks from 8192 + row); hsamp_phase_read copies the clocks out. Off by
-// default: the macro then expands to nothing.
-#ifdef HSAMP_PHASE_CLOCKS
-__device__ unsigned long long g_phase[16384 * 16];
-#define HSAMP_PHASE(blk, i)                                                          \
-    do {                                                                             \
-        if (threadIdx.x == 0) g_phase[(blk) * 16 + (i)] = __builtin_amdgcn_s_memrealtime(); \
-    } while (0)
-#else
-#define HSAMP_PHASE(blk, i) ((void)0)
-#endif
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kKeyNegInf = 0x007FFFFFu;        // key32(-inf)
@@ -73,70 +59,6 @@ __device__ __forceinline__ u64 comp(uint32_t key, int32_t idx) {
     return ((u64)key << 32) | (u64)(~(uint32_t)idx);
 }
 __device__ __forceinline__ int32_t comp_idx(u64 c) { return (int32_t)(~(uint32_t)c); }
-
-__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
-__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
-
-// ---- wave-wide reductions and scans through DPP ---------------------------------
-// Shifts within 16-lane rows (row_shr 1, 2, 4, 8), then row_bcast:15 and
-// row_bcast:31 across rows: an inclusive scan over the 64 lanes in six VALU
-// steps, without the LDS crossbar that shuffles use. Lanes whose source lies
-// outside the row keep `id` (the operation's identity); lane 63 ends with the
-// whole wave's result.
-template <int CTRL, int ROWM>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t id, uint32_t x) {
-    return (uint32_t)__builtin_amdgcn_update_dpp((int)id, (int)x, CTRL, ROWM, 0xF, false);
-}
-template <typename F>
-__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t x, uint32_t id, F op) {
-    x = op(x, dpp_u32<0x111, 0xF>(id, x));
-    x = op(x, dpp_u32<0x112, 0xF>(id, x));
-    x = op(x, dpp_u32<0x114, 0xF>(id, x));
-    x = op(x, dpp_u32<0x118, 0xF>(id, x));
-    x = op(x, dpp_u32<0x142, 0xA>(id, x));
-    x = op(x, dpp_u32<0x143, 0xC>(id, x));
-    return x;
-}
-__device__ __forceinline__ int wave_incl_sum_i(int x) {
-    return (int)wave_scan_u32((uint32_t)x, 0u, [](uint32_t a, uint32_t b) { return a + b; });
-}
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
-    x = wave_scan_u32(x, 0u, [](uint32_t a, uint32_t b) { return max(a, b); });
-    return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
-}
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
-    x = wave_scan_u32(x, 0xFFFFFFFFu, [](uint32_t a, uint32_t b) { return min(a, b); });
-    return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
-}
-template <int CTRL, int ROWM>
-__device__ __forceinline__ float dpp_f32(float id, float x) {
-    return __uint_as_float(dpp_u32<CTRL, ROWM>(__float_as_uint(id), __float_as_uint(x)));
-}
-template <int CTRL, int ROWM>
-__device__ __forceinline__ double dpp_f64(double x) {
-    const uint64_t b = (uint64_t)__double_as_longlong(x);
-    const uint32_t lo = dpp_u32<CTRL, ROWM>(0u, (uint32_t)b), hi = dpp_u32<CTRL, ROWM>(0u, (uint32_t)(b >> 32));
-    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
-}
-// Inclusive scans (tree association: only for decisions taken with a margin).
-__device__ __forceinline__ float wave_tree_prefix_f(float x) {
-    x = x + dpp_f32<0x111, 0xF>(0.0f, x);
-    x = x + dpp_f32<0x112, 0xF>(0.0f, x);
-    x = x + dpp_f32<0x114, 0xF>(0.0f, x);
-    x = x + dpp_f32<0x118, 0xF>(0.0f, x);
-    x = x + dpp_f32<0x142, 0xA>(0.0f, x);
-    x = x + dpp_f32<0x143, 0xC>(0.0f, x);
-    return x;
-}
-__device__ __forceinline__ double wave_tree_prefix_d(double x) {
-    x = x + dpp_f64<0x111, 0xF>(x);
-    x = x + dpp_f64<0x112, 0xF>(x);
-    x = x + dpp_f64<0x114, 0xF>(x);
-    x = x + dpp_f64<0x118, 0xF>(x);
-    x = x + dpp_f64<0x142, 0xA>(x);
-    x = x + dpp_f64<0x143, 0xC>(x);
-    return x;
-}
 
 struct Shared {
     u64 theta;          // current survival threshold (composite)
@@ -835,35 +757,6 @@ __device__ __attribute__((noinline)) void finalize_row(const StreamArgs& a, cons
 // value and every lane then reads all 64 with broadcast loads, so sorts are
 // rank placements and the reference's sequential sums are one unrolled chain
 // of adds per lane, in lane order, with no shuffles or readlanes.
-
-__device__ __forceinline__ float readlane_f(float v, int l) {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
-}
-__device__ __forceinline__ double readlane_d(double v, int l) {
-    const uint64_t b = f64_to_bits(v);
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
-    return bits_to_f64(((uint64_t)hi << 32) | lo);
-}
-__device__ __forceinline__ float wave_max_f(float v) {
-    // (no NaN reaches it)
-    v = fmaxf(v, dpp_f32<0x111, 0xF>(-__builtin_inff(), v));
-    v = fmaxf(v, dpp_f32<0x112, 0xF>(-__builtin_inff(), v));
-    v = fmaxf(v, dpp_f32<0x114, 0xF>(-__builtin_inff(), v));
-    v = fmaxf(v, dpp_f32<0x118, 0xF>(-__builtin_inff(), v));
-    v = fmaxf(v, dpp_f32<0x142, 0xA>(-__builtin_inff(), v));
-    v = fmaxf(v, dpp_f32<0x143, 0xC>(-__builtin_inff(), v));
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-
-// Orders the wave's LDS accesses around a cross-lane exchange. LDS operations
-// of one wave complete in program order; the fences keep the compiler from
-// moving accesses across.
-__device__ __forceinline__ void wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 // Ascending sort of 64 distinct keys across the lanes (payload travels along).
 // All 64 keys are read before any is compared, so the LDS latency is paid once.
@@ -3399,260 +3292,146 @@ __global__ __launch_bounds__(kBlock) void k_writeback(StreamArgs a) {
 }
 
 // ---- full-vocabulary rows ---------------------------------------------------------
-// Sampling rows whose top-k is off (top_k == 0 or >= V) or above kLimitK: the
-// whole transformed row goes through softmax, top-p, min-p and the draw. One
-// block per row; the row lives in global scratch (fullv, fullp, fullk). The
-// float sums that decide outcomes (the softmax denominator in index order,
-// the top-p cumulative in sorted order) are replayed exactly in the
-// reference's order by one wave; the double sums of the draw are accurate
-// sums whose only effect is within 1e-15 of a CDF boundary (flagged rows).
+// (the exact-sum engine, block helpers and the top-p driver are in hsamp_xsum.h)
 
-// Lane-order sequential float sum of x[0..n) (values >= +0) by one wave, from
-// +0.0f, 64 values per step through the wave's LDS scratch.
-__device__ float wave_seq_sum_arr(const float* x, int n, u64* wv) {
+// Window-order helpers: wave `wid` takes windows wid, wid + kFW, ...; lane l
+// holds ids w * WS + g * 512 + l * 8 + j of each 512-step g.
+
+// e = expf(x - m) for every finite x of the row (0 for -inf and padding),
+// into pv, with each window's approximate sum in f.winA.
+__device__ void full_exp(const float* fv, float* pv, float m, int nW, int G, FullLds f, FullShared& st) {
     const int lane = lane_id();
-    float* w = reinterpret_cast<float*>(wv);
-    const float4* w4 = reinterpret_cast<const float4*>(w);
-    float s = 0.0f;
-    float nxt = (lane < n) ? x[lane] : 0.0f;
-    for (int base = 0; base < n; base += 64) {
-        const float cur = nxt;
-        nxt = (base + 64 + lane < n) ? x[base + 64 + lane] : 0.0f;
-        w[lane] = cur;
-        wave_sync();
+    const int WS = kFWin * G;
+    float ws = 0.0f;
+    wpass(fv, nW, G, [&](int w, int g, const float (&x)[8]) {
+        float v[8];
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const float4 v = w4[q];
-            s = s + v.x;
-            s = s + v.y;
-            s = s + v.z;
-            s = s + v.w;
+        for (int j = 0; j < 8; ++j) {
+            v[j] = (x[j] == -__builtin_inff()) ? 0.0f : libm_expf_t(x[j] - m, st.expT);
+            ws += v[j];
         }
-        wave_sync();
-    }
-    return s;
-}
-
-// Continue the sequential float sum `cum` over the keys k[0..n) (float bits of
-// values >= 0, in LDS or global memory): the first j whose running sum is >=
-// thr, with that sum in *at; -1 when none (cum then holds the total).
-__device__ int wave_seq_find(const uint32_t* k, int n, float thr, float& cum, float* at, u64* wv) {
-    const int lane = lane_id();
-    uint32_t* w = reinterpret_cast<uint32_t*>(wv);
-    const uint4* w4 = reinterpret_cast<const uint4*>(w);
-    float s = cum;
-    for (int base = 0; base < n; base += 64) {
-        w[lane] = (base + lane < n) ? k[base + lane] : 0u;
-        wave_sync();
-        int hit = -1;
-        float sh = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const uint4 v = w4[q];
-            const uint32_t e[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                s = s + __uint_as_float(e[c]);
-                const bool h = hit < 0 && s >= thr && base + 4 * q + c < n;
-                sh = h ? s : sh;
-                hit = h ? base + 4 * q + c : hit;
-            }
+        float4* dst = reinterpret_cast<float4*>(pv + (size_t)w * WS + g * kFWin + lane * 8);
+        dst[0] = make_float4(v[0], v[1], v[2], v[3]);
+        dst[1] = make_float4(v[4], v[5], v[6], v[7]);
+        if (g == G - 1) {
+            ws = wave_tree_prefix_f(ws);
+            if (lane == 63) f.winA[w] = ws;
+            ws = 0.0f;
         }
-        wave_sync();
-        if (hit >= 0) {
-            *at = sh;
-            cum = sh;
-            return hit;
-        }
-    }
-    cum = s;
-    return -1;
+    });
+    __syncthreads();
 }
 
-// Descending bitonic sort of n <= cap keys in LDS (padded with 0 to a power
-// of two), by the whole block.
-__device__ void block_sort_desc_lds(uint32_t* a, int n) {
-    int P2 = 1;
-    while (P2 < n) P2 <<= 1;
-    for (int i = n + (int)threadIdx.x; i < P2; i += kBlock) a[i] = 0u;
-    __syncthreads();
-    for (int k = 2; k <= P2; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int i = threadIdx.x; i < P2; i += kBlock) {
-                const int ixj = i ^ j;
-                if (ixj > i) {
-                    const uint32_t x = a[i], y = a[ixj];
-                    const bool desc = (i & k) == 0;
-                    if (desc ? (x < y) : (x > y)) {
-                        a[i] = y;
-                        a[ixj] = x;
-                    }
-                }
-            }
-            __syncthreads();
-        }
-    }
-}
-
-// The same in global memory, for a bucket too large for LDS (rare).
-__device__ void block_sort_desc_global(uint32_t* a, int n) {
-    int P2 = 1;
-    while (P2 < n) P2 <<= 1;
-    for (int i = n + (int)threadIdx.x; i < P2; i += kBlock) a[i] = 0u;
-    __syncthreads();
-    for (int k = 2; k <= P2; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int i = threadIdx.x; i < P2; i += kBlock) {
-                const int ixj = i ^ j;
-                if (ixj > i) {
-                    const uint32_t x = a[i], y = a[ixj];
-                    const bool desc = (i & k) == 0;
-                    if (desc ? (x < y) : (x > y)) {
-                        a[i] = y;
-                        a[ixj] = x;
-                    }
-                }
-            }
-            __syncthreads();
-        }
-    }
-}
-
-__device__ __forceinline__ double block_sum_d(double v, Shared& st) {
-#pragma unroll
-    for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
-    if (lane_id() == 0) st.dred[wave_id()] = v;
-    __syncthreads();
-    double r = 0.0;
-#pragma unroll
-    for (int i = 0; i < kBlock / 64; ++i) r += st.dred[i];
-    __syncthreads();
-    return r;
-}
-
-__device__ __forceinline__ uint32_t block_max_u32(uint32_t v, Shared& st) {
-#pragma unroll
-    for (int d = 32; d > 0; d >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, d, 64));
-    if (lane_id() == 0) st.ired[wave_id()] = (int)v;
-    __syncthreads();
-    uint32_t r = 0u;
-#pragma unroll
-    for (int i = 0; i < kBlock / 64; ++i) r = max(r, (uint32_t)st.ired[i]);
-    __syncthreads();
-    return r;
-}
-
-__device__ __forceinline__ uint32_t block_min_u32(uint32_t v, Shared& st) {
-#pragma unroll
-    for (int d = 32; d > 0; d >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, d, 64));
-    if (lane_id() == 0) st.ired[wave_id()] = (int)v;
-    __syncthreads();
-    uint32_t r = 0xFFFFFFFFu;
-#pragma unroll
-    for (int i = 0; i < kBlock / 64; ++i) r = min(r, (uint32_t)st.ired[i]);
-    __syncthreads();
-    return r;
-}
-
-// The row's ids split into one contiguous chunk per thread (for work that
-// must run in index order).
-struct Chunk {
-    int lo, hi;
-};
-__device__ __forceinline__ Chunk my_chunk(int V) {
-    const int C = (V + kBlock - 1) / kBlock;
-    const int lo = min(V, (int)threadIdx.x * C);
-    return Chunk{lo, min(V, lo + C)};
-}
-
+// Full-vocabulary rows, one block of kFT threads per row.
 template <bool GT>
-__global__ __launch_bounds__(kBlock) void k_full(StreamArgs a) {
+__global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ Shared st;
-    __shared__ StreamArgs sa;
-    __shared__ RowPlan sP;
-    const int tid = threadIdx.x;
-    const int lane = lane_id();
+    __shared__ FullShared st;
+    const int tid = threadIdx.x, lane = lane_id(), wid = wave_id();
     const int r = (int)blockIdx.x;
     if (r >= a.rows) return;
     const RowPlan P = a.plans[r];
     if (!(P.flags & RF_FULL)) return;
-    const int V = a.vocab;
+    HSAMP_PHASE(12000 + r, 0);
+    const int V = a.vocab, G = a.full_g;
+    const int WS = kFWin * G;
+    const int Vp = a.full_stride, nW = Vp / WS;
+    float* fv = a.fullv + (size_t)r * Vp;
+    float* pv = a.fullp + (size_t)r * Vp;
+    uint32_t* fk = a.fullk + (size_t)r * a.full_p2;
     const bool pen = (P.flags & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) != 0;
     const bool masked = (P.flags & RF_MASK) != 0;
-    float* fv = a.fullv + (size_t)r * V;
-    float* pv = a.fullp + (size_t)r * V;
-    uint32_t* sk = a.fullk + (size_t)r * 2 * a.full_p2;   // [bucketed keys][scratch for a big bucket]
-    const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * (a.dtype == 0 ? 4 : 2);
-    int32_t pre[8];
-    hist_prefetch(a, P, r, pen, pre);
+    const PenaltyLds pl = pen_table<GT>(a, r, smem);
+    const FullLds f = full_lds(smem + (GT ? 0 : 8 * (size_t)a.mhash_slots));
+    if (tid < 32) st.expT[tid] = kExpT[tid];
     if (tid == 0) {
-        sa = a;
-        sP = P;
         st.u = a.u[r];
         st.flags = 0;
     }
-    if (tid < 32) st.expT[tid] = kExpT[tid];
-    const PenaltyLds pl = pen_table<GT>(a, r, smem);
-    uint32_t* work = reinterpret_cast<uint32_t*>(smem + (GT ? 0 : 8 * (size_t)a.mhash_slots));   // 24 KB
-    if (pen) pen_build_row(a, P, r, pl, pre);
-    else __syncthreads();
+    if (pen) {
+        // the row's penalty table (every id of the history window, bias ids)
+        for (int i = tid; i < a.mhash_slots; i += kFT) {
+            pl.hkey[i] = kEmpty;
+            pl.hval[i] = 0u;
+        }
+        __syncthreads();
+        const int L = P.hist_len, p0 = L - P.scan_len;
+        const int32_t* h = a.hist + (int64_t)r * a.hist_stride;
+        for (int p = p0 + tid; p < L; p += kFT) pen_add(a, P, L, p, h[p], pl);
+        if (P.flags & RF_BIAS) {
+            for (int j = tid; j < P.bias_cnt; j += kFT) {
+                const uint32_t sl = pen_insert(a.bias_ids[P.bias_off + j], pl);
+                atomicOr(&pl.hval[sl], HV_BIAS);
+            }
+        }
+    }
+    __syncthreads();
+    HSAMP_PHASE(12000 + r, 1);
     uint32_t rflags = ROWF_U_USED;
 
-    // ---- stages 1-5 (sampler.cpp:235-265): mask, penalties, temperature ----------
+    // ---- stages 1-6 (sampler.cpp:235-265): mask, penalties, temperature; max ----
+    const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * (a.dtype == 0 ? 4 : 2);
+    float mloc = -__builtin_inff();
     bool nanv = false;
-    for (int i = tid; i < V; i += kBlock) {
-        float x = 0.0f;
-        {
-            const int32_t t1[1] = {i};
-            float x1[1];
-            load_logits<1>(rowp, a.dtype, t1, x1);
-            x = x1[0];
+    for (int b = tid; b < Vp; b += 8 * kFT) {
+        // eight logits (and mask words) per thread in flight, then the ladder
+        float x[8];
+        uint32_t mw[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int i = b + q * kFT;
+            x[q] = i < V ? load_logit_dt(rowp, a.dtype, i) : -__builtin_inff();
+            mw[q] = (masked && i < V) ? a.mask[(int64_t)r * a.mask_stride + (i >> 5)] : 0xFFFFFFFFu;
         }
-        if (masked && !((a.mask[(int64_t)r * a.mask_stride + (i >> 5)] >> (i & 31)) & 1u)) x = -__builtin_inff();
-        if (pen) {
-            uint32_t s0 = hslot(i, pl);
-            uint32_t kk;
-            while ((kk = tab_ld(&pl.hkey[s0])) != kEmpty && kk != (uint32_t)i) s0 = (s0 + 1) & pl.hmask;
-            if (kk == (uint32_t)i) x = pen_value(x, i, tab_ld(&pl.hval[s0]), sa, sP);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int i = b + q * kFT;
+            if (i >= Vp) break;
+            float y = x[q];
+            if (i < V) {
+                if (!((mw[q] >> (i & 31)) & 1u)) y = -__builtin_inff();
+                if (pen) {
+                    uint32_t s0 = hslot(i, pl);
+                    uint32_t kk;
+                    while ((kk = tab_ld(&pl.hkey[s0])) != kEmpty && kk != (uint32_t)i) s0 = (s0 + 1) & pl.hmask;
+                    if (kk == (uint32_t)i) y = pen_value(y, i, tab_ld(&pl.hval[s0]), a, P);
+                }
+                y = y * P.inv_temp;
+                if (y != y) {
+                    nanv = true;
+                    y = -__builtin_inff();
+                }
+            }
+            fv[i] = y;
+            mloc = fmaxf(mloc, y);
         }
-        x = x * P.inv_temp;
-        if (x != x) {
-            nanv = true;
-            x = -__builtin_inff();
-        }
-        fv[i] = x;
     }
     if (nanv) atomicOr(&st.flags, 4);
-    __syncthreads();
+    float m = fblock_max(mloc, st);
+    HSAMP_PHASE(12000 + r, 2);
 
     // ---- top-k above kLimitK (sampler.cpp:109-121): the k-th largest key by four
-    // 8-bit digit passes, ties to the lower ids ---------------------------------------
+    // 8-bit digit passes, ties to the lower ids ----
     if (P.flags & RF_TOPK) {
         const int k = P.top_k;
         uint32_t prefix = 0u, kmask = 0u;
         int need = k;
+        uint32_t* hist = f.bcnt;
         for (int shift = 24; shift >= 0; shift -= 8) {
-            work[tid] = 0u;
+            if (tid < 256) hist[tid] = 0u;
             __syncthreads();
-            for (int i = tid; i < V; i += kBlock) {
+            for (int i = tid; i < V; i += kFT) {
                 const uint32_t key = key32(fv[i]);
-                if ((key & kmask) == prefix) atomicAdd(&work[(key >> shift) & 255u], 1u);
+                if ((key & kmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
             }
             __syncthreads();
             if (tid < 64) {
-                const int c0 = work[255 - 4 * lane], c1 = work[254 - 4 * lane];
-                const int c2 = work[253 - 4 * lane], c3 = work[252 - 4 * lane];
+                const int c0 = hist[255 - 4 * lane], c1 = hist[254 - 4 * lane];
+                const int c2 = hist[253 - 4 * lane], c3 = hist[252 - 4 * lane];
                 const int s4 = c0 + c1 + c2 + c3;
-                int incl = s4;
-#pragma unroll
-                for (int d = 1; d < 64; d <<= 1) {
-                    const int y = __shfl_up(incl, d, 64);
-                    if (lane >= d) incl += y;
-                }
+                const int incl = wave_incl_sum_i(s4);
                 const int excl = incl - s4;
-                const bool mine = excl < need && need <= incl;
-                if (mine) {
+                if (excl < need && need <= incl) {
                     int q, before;
                     if (excl + c0 >= need) { q = 0; before = excl; }
                     else if (excl + c0 + c1 >= need) { q = 1; before = excl + c0; }
@@ -3668,25 +3447,26 @@ __global__ __launch_bounds__(kBlock) void k_full(StreamArgs a) {
             need = st.sel_need;
             __syncthreads();
         }
-        // keep key > K, and the `need` lowest ids with key == K
-        const Chunk ch = my_chunk(V);
+        // keep key > K and the `need` lowest ids with key == K; then the
+        // finite members in index order (contiguous chunks per thread)
+        const int C = (V + kFT - 1) / kFT;
+        const int c0 = min(V, tid * C), c1 = min(V, c0 + C);
         int eq = 0;
-        for (int i = ch.lo; i < ch.hi; ++i) eq += key32(fv[i]) == prefix;
+        for (int i = c0; i < c1; ++i) eq += key32(fv[i]) == prefix;
         int tot;
-        int before = block_excl_scan(eq, &tot, st);
+        int before = fblock_excl_scan(eq, &tot, st);
         int fin = 0;
-        for (int i = ch.lo; i < ch.hi; ++i) {
+        for (int i = c0; i < c1; ++i) {
             const uint32_t key = key32(fv[i]);
             bool keep = key > prefix;
             if (key == prefix) keep = before++ < need;
             if (!keep) fv[i] = -__builtin_inff();
             else fin += fv[i] != -__builtin_inff();
         }
-        // the finite members, index order
         int nfin;
-        int pos = block_excl_scan(fin, &nfin, st);
+        int pos = fblock_excl_scan(fin, &nfin, st);
         if (a.topk_idx != nullptr) {
-            for (int i = ch.lo; i < ch.hi; ++i) {
+            for (int i = c0; i < c1; ++i) {
                 if (fv[i] == -__builtin_inff()) continue;
                 if (pos < a.set_cap) a.topk_idx[(int64_t)r * a.set_cap + pos] = i;
                 ++pos;
@@ -3698,274 +3478,317 @@ __global__ __launch_bounds__(kBlock) void k_full(StreamArgs a) {
         a.topk_count[r] = -1;
     }
 
-    // softmax_probs (sampler.cpp:124-142) of fv into pv; false when nothing is finite
-    auto softmax = [&]() -> bool {
-        float m = -__builtin_inff();
-        for (int i = tid; i < V; i += kBlock) m = fmaxf(m, fv[i]);
-        m = block_max_f(m, st);
-        if (m == -__builtin_inff()) {
-            const float pu = 1.0f / (float)V;
-            for (int i = tid; i < V; i += kBlock) pv[i] = pu;
-            __syncthreads();
-            return false;
-        }
-        for (int i = tid; i < V; i += kBlock)
-            pv[i] = (fv[i] == -__builtin_inff()) ? 0.0f : libm_expf_t(fv[i] - m, st.expT);
-        __syncthreads();
-        if (tid < 64) {
-            const float s = wave_seq_sum_arr(pv, V, st.wv);
-            if (lane == 0) st.sm_m = s;
-        }
-        __syncthreads();
-        const float s = st.sm_m;
-        if (s > 0.0f) {
-            const float inv = 1.0f / s;
-            for (int i = tid; i < V; i += kBlock) pv[i] = pv[i] * inv;
-        }
-        __syncthreads();
-        return true;
-    };
+    int nkept = 0;
+    int32_t tok = 0;
+    if (m != -__builtin_inff()) {
+        // ---- softmax numerators and their exact index-order sum (sampler.cpp:124-142) ----
+        full_exp(fv, pv, m, nW, G, f, st);
+        HSAMP_PHASE(12000 + r, 4);
+        float S = xs_value(exact_index_sum(pv, nW, G, f, st));
+        HSAMP_PHASE(12000 + r, 5);
+        bool changed = false;   // a stage removed ids since S was taken
 
-    bool fresh = false;   // pv matches fv
-    // ---- top-p (sampler.cpp:146-164) -------------------------------------------------
-    if (P.flags & RF_TOPP) {
-        softmax();
-        fresh = true;
-        // keys of the positive probabilities (float bits order them), bucketed
-        // by the 11 bits below the bits they all share
-        uint32_t kmx = 0u, kmn = 0xFFFFFFFFu;
-        for (int i = tid; i < V; i += kBlock) {
-            const uint32_t key = __float_as_uint(pv[i]);
-            if (key != 0u) {
-                kmx = max(kmx, key);
-                kmn = min(kmn, key);
+        // ---- top-p (sampler.cpp:146-164) ----
+        if (P.flags & RF_TOPP) {
+            uint32_t cut_key = 0u;
+            int cut_count = 0;
+            const float inv = 1.0f / S;
+            if (full_top_p(pv, V, Vp, inv, P.top_p, fk, f, st, &cut_key, &cut_count)) {
+                if (fabs(st.dS - (double)P.top_p) <= 1e-6) rflags |= ROWF_TOPP_NEAR;
+                // kept: p > p*, and the lowest ids with p == p* up to cut_count
+                int gt = 0, eq = 0;
+                fpass(pv, Vp, [&](int, float e) {
+                    const uint32_t key = __float_as_uint(e * inv);
+                    gt += key > cut_key;
+                    eq += key == cut_key;
+                });
+                const int ngt = fblock_sum_i(gt, st);
+                const int neq = fblock_sum_i(eq, st);
+                const int need = cut_count - ngt;
+                if (need >= neq) {
+                    fpass(pv, Vp, [&](int i, float e) {
+                        if (__float_as_uint(e * inv) < cut_key) {
+                            fv[i] = -__builtin_inff();
+                            pv[i] = 0.0f;
+                        }
+                    });
+                } else {
+                    // equal keys at the cut, ranked by id: each window's count
+                    // of them, the windows' prefix, then each one's rank
+                    uint32_t* wc = f.winEF;
+                    {
+                        int c = 0;
+                        wpass(pv, nW, G, [&](int w, int g, const float (&e)[8]) {
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) c += __float_as_uint(e[j] * inv) == cut_key;
+                            if (g == G - 1) {
+                                c = __builtin_amdgcn_readlane(wave_incl_sum_i(c), 63);
+                                if (lane == 0) wc[w] = (uint32_t)c;
+                                c = 0;
+                            }
+                        });
+                    }
+                    __syncthreads();
+                    {
+                        const int w0 = 2 * tid;
+                        const int c0 = w0 < nW ? (int)wc[w0] : 0, c1 = w0 + 1 < nW ? (int)wc[w0 + 1] : 0;
+                        int tot;
+                        const int ex = fblock_excl_scan(c0 + c1, &tot, st);
+                        if (w0 < nW) wc[w0] = (uint32_t)ex;
+                        if (w0 + 1 < nW) wc[w0 + 1] = (uint32_t)(ex + c0);
+                    }
+                    __syncthreads();
+                    int pos = 0;
+                    wpass(pv, nW, G, [&](int w, int g, const float (&e)[8]) {
+                        if (g == 0) pos = (int)wc[w];
+                        int c = 0;
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) c += __float_as_uint(e[j] * inv) == cut_key;
+                        const int li = wave_incl_sum_i(c);
+                        int rank = pos + li - c;
+                        const size_t i0 = (size_t)w * WS + g * kFWin + lane * 8;
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+                            const uint32_t key = __float_as_uint(e[j] * inv);
+                            const bool keep = key > cut_key || (key == cut_key && rank < need);
+                            rank += key == cut_key;
+                            if (!keep) {
+                                fv[i0 + j] = -__builtin_inff();
+                                pv[i0 + j] = 0.0f;
+                            }
+                        }
+                        pos += __builtin_amdgcn_readlane(li, 63);
+                    });
+                }
+                changed = true;
+                __syncthreads();
             }
         }
-        kmx = block_max_u32(kmx, st);
-        kmn = block_min_u32(kmn, st);
-        int cut = -1;         // sorted position of the last kept entry
-        uint32_t cut_key = 0u;
-        float cut_cum = 0.0f;
-        if (kmx != 0u) {
-            const int hb = (kmx != kmn) ? 31 - __clz((int)(kmx ^ kmn)) : 0;
-            const int shift = max(0, hb - 10);
-            uint32_t* cnt = work;           // [2048] counts, then fill positions
-            uint32_t* off = work + 2048;    // [2048] start of each bucket, descending order
-            for (int i = tid; i < 2048; i += kBlock) cnt[i] = 0u;
-            __syncthreads();
-            for (int i = tid; i < V; i += kBlock) {
-                const uint32_t key = __float_as_uint(pv[i]);
-                if (key != 0u) atomicAdd(&cnt[(key >> shift) & 2047u], 1u);
+
+        // the numerators of what is left: relative to the largest kept logit
+        // (the maximum unless a tie in p kept a lower id first), window sums
+        auto refresh = [&]() {
+            float mk = -__builtin_inff();
+            fpass(fv, Vp, [&](int, float x) { mk = fmaxf(mk, x); });
+            mk = fblock_max(mk, st);
+            if (mk != m) {
+                m = mk;
+                full_exp(fv, pv, m, nW, G, f, st);
+            } else {
+                float ws = 0.0f;
+                wpass(pv, nW, G, [&](int w, int g, const float (&v)[8]) {
+                    ws += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+                    if (g == G - 1) {
+                        ws = wave_tree_prefix_f(ws);
+                        if (lane == 63) f.winA[w] = ws;
+                        ws = 0.0f;
+                    }
+                });
+                __syncthreads();
             }
-            __syncthreads();
-            // offsets: buckets from the top; 8 per thread, thread 0 the highest
+            S = xs_value(exact_index_sum(pv, nW, G, f, st));
+        };
+
+        // ---- min-p (sampler.cpp:167-176) ----
+        if (P.flags & RF_MINP) {
+            if (changed) refresh();
+            changed = false;
+            const float inv = 1.0f / S;
+            float mp = 0.0f;
+            fpass(pv, Vp, [&](int, float e) { mp = fmaxf(mp, e * inv); });
+            mp = fblock_max(mp, st);
+            const float thr = P.min_p * mp;
+            int dropped = 0;
+            fpass(pv, Vp, [&](int i, float e) {
+                if (e * inv < thr && fv[i] != -__builtin_inff()) {
+                    fv[i] = -__builtin_inff();
+                    pv[i] = 0.0f;
+                    dropped = 1;
+                }
+            });
+            changed = fblock_sum_i(dropped, st) != 0;
+        }
+        HSAMP_PHASE(12000 + r, 6);
+        if (changed) refresh();
+        HSAMP_PHASE(12000 + r, 7);
+        m = -__builtin_inff();
+        fpass(fv, Vp, [&](int, float x) { m = fmaxf(m, x); });
+        m = fblock_max(m, st);
+        if (m != -__builtin_inff()) {
+            // ---- the draw (sampler.cpp:178-182, discrete_distribution) ----
+            // p = e * fl(1/S); S_d = sum of p (double); q = p / S_d; the first id
+            // whose running sum of q reaches u (the last id's is 1). One pass
+            // gives each window's sum of p and its kept count; the window where
+            // the running sum reaches u is then walked value by value.
+            const float inv = 1.0f / S;
+            double* wq = reinterpret_cast<double*>(f.winA);   // [kFMaxWin] window sums of p, then prefixes
+            uint32_t* wc = f.winEF;                            // [kFMaxWin] kept counts, then prefixes
             {
-                int c8[8], sum8 = 0;
+                double ws = 0.0;
+                int c = 0;
+                wpass2(pv, fv, nW, G, [&](int w, int g, const float (&e)[8], const float (&x)[8]) {
 #pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    c8[q] = (int)cnt[2047 - 8 * tid - q];
-                    sum8 += c8[q];
-                }
+                    for (int j = 0; j < 8; ++j) {
+                        ws += (double)(e[j] * inv);
+                        c += x[j] != -__builtin_inff();
+                    }
+                    if (g == G - 1) {
+                        ws = wave_sum_d(ws);
+                        c = __builtin_amdgcn_readlane(wave_incl_sum_i(c), 63);
+                        if (lane == 0) {
+                            wq[w] = ws;
+                            wc[w] = (uint32_t)c;
+                        }
+                        ws = 0.0;
+                        c = 0;
+                    }
+                });
+            }
+            __syncthreads();
+            HSAMP_PHASE(12000 + r, 8);
+            double Sd;
+            {
+                // exclusive prefixes over the windows, 2 per thread
+                const int w0 = 2 * tid;
+                const double q0 = w0 < nW ? wq[w0] : 0.0, q1 = w0 + 1 < nW ? wq[w0 + 1] : 0.0;
+                const int c0 = w0 < nW ? (int)wc[w0] : 0, c1 = w0 + 1 < nW ? (int)wc[w0 + 1] : 0;
+                const double incl = wave_tree_prefix_d(q0 + q1);
+                if (lane == 63) st.rd[wid] = incl;
                 int tot;
-                int o = block_excl_scan(sum8, &tot, st);
-#pragma unroll
-                for (int q = 0; q < 8; ++q) {
-                    off[2047 - 8 * tid - q] = (uint32_t)o;
-                    o += c8[q];
+                const int cex = fblock_excl_scan(c0 + c1, &tot, st);   // (its barriers publish st.rd)
+                nkept = tot;
+                double base = 0.0;
+                Sd = 0.0;
+                for (int i = 0; i < kFW; ++i) {
+                    base += (i < wid) ? st.rd[i] : 0.0;
+                    Sd += st.rd[i];
+                }
+                const double ex = base + incl - (q0 + q1);
+                __syncthreads();
+                if (w0 < nW) {
+                    wq[w0] = ex;
+                    wc[w0] = (uint32_t)cex;
+                }
+                if (w0 + 1 < nW) {
+                    wq[w0 + 1] = ex + q0;
+                    wc[w0 + 1] = (uint32_t)(cex + c0);
                 }
             }
-            __syncthreads();
-            // scatter (order inside a bucket does not matter: it is sorted below)
-            for (int i = tid; i < 2048; i += kBlock) cnt[i] = off[i];
-            __syncthreads();
-            for (int i = tid; i < V; i += kBlock) {
-                const uint32_t key = __float_as_uint(pv[i]);
-                if (key != 0u) sk[atomicAdd(&cnt[(key >> shift) & 2047u], 1u)] = key;
+            HSAMP_PHASE(12000 + r, 9);
+            if (tid == 0) {
+                st.tok = V - 1;   // no running sum reaches u: cp[V - 1] = 1 takes it
+                st.dS = -1.0;
             }
             __syncthreads();
-            // buckets from the top, in batches of at most 2048 keys sorted in LDS
-            uint32_t* batch = work + 4096;   // [2048]
-            float cum = 0.0f;                // wave 0's running sum
-            int b = 2047;
-            while (b >= 0) {
-                // bucket b's count = next bucket start - its start (cnt now holds ends)
-                int b_lo = b, n = 0;
-                const int start = (int)off[b];
-                while (b_lo >= 0 && (n == 0 || n + (int)(cnt[b_lo] - off[b_lo]) <= 2048)) {
-                    n += (int)(cnt[b_lo] - off[b_lo]);
-                    --b_lo;
-                }
-                if (n == 0) {
-                    b = b_lo;
-                    continue;
-                }
-                const uint32_t* src;
-                if (n <= 2048) {
-                    for (int i = tid; i < n; i += kBlock) batch[i] = sk[start + i];
-                    __syncthreads();
-                    block_sort_desc_lds(batch, n);
-                    src = batch;
-                } else {
-                    uint32_t* big = sk + a.full_p2;
-                    for (int i = tid; i < n; i += kBlock) big[i] = sk[start + i];
-                    __syncthreads();
-                    block_sort_desc_global(big, n);
-                    src = big;
-                }
-                if (tid < 64) {
-                    float at = 0.0f;
-                    const int j = wave_seq_find(src, n, P.top_p, cum, &at, st.wv);
-                    if (lane == 0) {
-                        st.cutoff = (j >= 0) ? start + j : -1;
-                        st.sm_inv = at;
-                        st.tok = (j >= 0) ? (int)src[j] : 0;
+            const double u = st.u;
+            if (!(u > 0.0)) {
+                tok = 0;
+            } else {
+                // the first window whose end reaches u (by its prefix of p / S_d)
+                if (tid == 0) st.fgroup = nW - 1;
+                __syncthreads();
+                for (int w = tid; w < nW; w += kFT) {
+                    const double end = (w + 1 < nW) ? wq[w + 1] / Sd : 2.0;
+                    if (end >= u) {
+                        atomicMin(&st.fgroup, w);
+                        break;
                     }
                 }
                 __syncthreads();
-                if (st.cutoff >= 0) {
-                    cut = st.cutoff;
-                    cut_key = (uint32_t)st.tok;
-                    cut_cum = st.sm_inv;
-                    break;
+                if (wid == 0) {
+                    // walk from a window before it (the prefixes are sums in
+                    // another order) until a running sum of q reaches u
+                    int w = max(0, st.fgroup - 1);
+                    bool hit = false;
+                    double cp = wq[w] / Sd;
+                    for (; w < nW && !hit; ++w) {
+                        cp = wq[w] / Sd;
+                        for (int g = 0; g < G && !hit; ++g) {
+                            const int i0 = w * WS + g * kFWin + lane * 8;
+                            const float* src = pv + i0;
+                            double q[8], ls = 0.0;
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) {
+                                q[j] = (double)(src[j] * inv) / Sd;
+                                ls += q[j];
+                            }
+                            const double li = wave_tree_prefix_d(ls);
+                            double c = cp + (li - ls), prev = c, cat = 0.0, pat = 0.0;
+                            int first = 8;
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) {
+                                const double before = c;
+                                c = c + q[j];
+                                const int i = i0 + j;
+                                const double cc = (i == V - 1) ? 1.0 : c;
+                                if (first == 8 && i < V && q[j] > 0.0 && cc >= u) {
+                                    first = j;
+                                    cat = cc;
+                                    pat = before;
+                                }
+                            }
+                            (void)prev;
+                            const u64 hm = __ballot(first < 8);
+                            if (hm != 0ull) {
+                                const int L = __ffsll((long long)hm) - 1;
+                                if (lane == L) {
+                                    st.tok = i0 + first;
+                                    st.dS = fmin(fabs(cat - u), fabs(pat - u));
+                                }
+                                hit = true;
+                            }
+                            cp = cp + readlane_d(li, 63);
+                        }
+                    }
+                    if (!hit && lane == 0) st.dS = fmin(fabs(1.0 - u), fabs(cp - u));
                 }
-                b = b_lo;
                 __syncthreads();
+                tok = st.tok;
+                if (st.dS >= 0.0 && st.dS <= 1e-6) rflags |= ROWF_CDF_NEAR;
+            }
+            HSAMP_PHASE(12000 + r, 11);
+            // kept ids and probabilities in index order
+            if (a.kept_idx != nullptr) {
+                int pos = 0;
+                wpass2(pv, fv, nW, G, [&](int w, int g, const float (&e)[8], const float (&x)[8]) {
+                    if (g == 0) pos = (int)wc[w];
+                    int c = 0;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) c += x[j] != -__builtin_inff();
+                    const int li = wave_incl_sum_i(c);
+                    int p = pos + li - c;
+                    const int i0 = w * WS + g * kFWin + lane * 8;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        if (x[j] != -__builtin_inff()) {
+                            if (p < a.set_cap) {
+                                a.kept_idx[(int64_t)r * a.set_cap + p] = i0 + j;
+                                a.kept_prob[(int64_t)r * a.set_cap + p] = e[j] * inv;
+                            }
+                            ++p;
+                        }
+                    }
+                    pos += __builtin_amdgcn_readlane(li, 63);
+                });
             }
         }
-        if (cut >= 0) {
-            if (fabsf(cut_cum - P.top_p) <= 1e-6f) rflags |= ROWF_TOPP_NEAR;
-            // kept: key > K*, and the lowest ids with key == K* up to position cut
-            int gt = 0;
-            const Chunk ch = my_chunk(V);
-            int eq = 0;
-            for (int i = ch.lo; i < ch.hi; ++i) {
-                const uint32_t key = __float_as_uint(pv[i]);
-                gt += key > cut_key;
-                eq += key == cut_key;
-            }
-            int ngt;
-            block_excl_scan(gt, &ngt, st);
-            int tot;
-            int before = block_excl_scan(eq, &tot, st);
-            const int need = cut + 1 - ngt;
-            for (int i = ch.lo; i < ch.hi; ++i) {
-                const uint32_t key = __float_as_uint(pv[i]);
-                bool keep = key > cut_key;
-                if (key == cut_key) keep = before++ < need;
-                if (!keep) fv[i] = -__builtin_inff();
-            }
-            __syncthreads();
-            fresh = false;
-        }
     }
-    // ---- min-p (sampler.cpp:167-176) -------------------------------------------------
-    if (P.flags & RF_MINP) {
-        if (!fresh) softmax();
-        fresh = true;
-        float mp = 0.0f;
-        for (int i = tid; i < V; i += kBlock) mp = fmaxf(mp, pv[i]);
-        mp = block_max_f(mp, st);
-        const float thr = P.min_p * mp;
-        int dropped = 0;
-        for (int i = tid; i < V; i += kBlock) {
-            if (pv[i] < thr) {
-                dropped |= fv[i] != -__builtin_inff();
-                fv[i] = -__builtin_inff();
-            }
-        }
-        int any;
-        block_excl_scan(dropped, &any, st);
-        if (any) fresh = false;
-    }
-    const bool have = fresh ? true : softmax();
-    (void)have;
-
-    // ---- the draw (sampler.cpp:178-182, discrete_distribution) ----------------------
-    const Chunk ch = my_chunk(V);
-    int nk = 0;
-    double part = 0.0;
-    for (int i = ch.lo; i < ch.hi; ++i) {
-        nk += fv[i] != -__builtin_inff();
-        part += (double)pv[i];
-    }
-    int nkept;
-    int kpos = block_excl_scan(nk, &nkept, st);
-    const double u = st.u;
-    int32_t tok = 0;
+    HSAMP_PHASE(12000 + r, 12);
     if (nkept == 0) {
         rflags |= ROWF_UNIFORM;
-        if (tid == 0) tok = uniform_draw(V, u);
-    } else {
-        const double S = block_sum_d(part, st);
-        // chunk sums of q, scanned over the threads in index order
-        double cq = 0.0;
-        for (int i = ch.lo; i < ch.hi; ++i) cq += (double)pv[i] / S;
-        double incl = cq;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const double y = __shfl_up(incl, d, 64);
-            if (lane >= d) incl += y;
-        }
-        if (lane == 63) st.dred[wave_id()] = incl;
-        __syncthreads();
-        double wbase = 0.0;
-        for (int w = 0; w < wave_id(); ++w) wbase += st.dred[w];
-        double cp = wbase + incl - cq;   // before this chunk
-        if (tid == 0) {
-            st.tok = V - 1;   // no partial sum reaches u: cp[V-1] = 1 takes it
-            st.dS = -1.0;
-        }
-        __syncthreads();
-        int hit = -1;
-        double hcp = 0.0, hprev = 0.0;
-        if (u > 0.0) {
-            for (int i = ch.lo; i < ch.hi; ++i) {
-                const double prev = cp;
-                cp = cp + (double)pv[i] / S;
-                const double c = (i == V - 1) ? 1.0 : cp;
-                if (pv[i] > 0.0f && c >= u) {
-                    hit = i;
-                    hcp = c;
-                    hprev = prev;
-                    break;
-                }
-            }
-        } else if (tid == 0) {
-            hit = 0;
-        }
-        // the first hit over all threads
-        if (hit >= 0) atomicMin(&st.tok, hit);
-        __syncthreads();
-        if (hit >= 0 && hit == st.tok) st.dS = (u > 0.0) ? fmin(fabs(hcp - u), fabs(hprev - u)) : 1.0;
-        __syncthreads();
-        // no hit anywhere: the last chunk's running sum is the total
-        if (st.dS < 0.0 && ch.lo < ch.hi && ch.hi == V) st.dS = fmin(fabs(1.0 - u), fabs(cp - u));
-        __syncthreads();
-        tok = st.tok;
-        if (st.dS <= 1e-6) rflags |= ROWF_CDF_NEAR;
-        // kept ids and probabilities, index order
-        if (a.kept_idx != nullptr) {
-            int pos = kpos;
-            for (int i = ch.lo; i < ch.hi; ++i) {
-                if (fv[i] == -__builtin_inff()) continue;
-                if (pos < a.set_cap) {
-                    a.kept_idx[(int64_t)r * a.set_cap + pos] = i;
-                    a.kept_prob[(int64_t)r * a.set_cap + pos] = pv[i];
-                }
-                ++pos;
-            }
-        }
+        if (tid == 0) tok = uniform_draw(V, st.u);
     }
     // the state sample() leaves the logits in (f32 only)
     if (a.fin_idx != nullptr) {
         float* row = static_cast<float*>(const_cast<void*>(a.logits)) + (int64_t)r * a.logits_stride;
-        for (int i = tid; i < V; i += kBlock) row[i] = fv[i];
+        for (int i = tid; i < V; i += kFT) row[i] = fv[i];
     }
     if (tid == 0) {
         a.token[r] = tok;
         if (a.row_flags != nullptr) a.row_flags[r] = rflags | ((st.flags & 4) ? ROWF_NAN : 0u);
         if (a.kept_count != nullptr) a.kept_count[r] = nkept;
     }
+    HSAMP_PHASE(12000 + r, 13);
 }
 
 // ---- diagnostics: a plain read with the stream kernel's launch shape --------------
@@ -4133,10 +3956,12 @@ hipError_t launch_merge(const StreamArgs& a, hipStream_t stream) {
 }
 
 hipError_t launch_full(const StreamArgs& a, uint32_t lds, hipStream_t stream) {
-    if (a.gtab != nullptr) hipLaunchKernelGGL((k_full<true>), dim3(a.rows), dim3(kBlock), lds, stream, a);
-    else hipLaunchKernelGGL((k_full<false>), dim3(a.rows), dim3(kBlock), lds, stream, a);
+    if (a.gtab != nullptr) hipLaunchKernelGGL((k_full<true>), dim3(a.rows), dim3(kFT), lds, stream, a);
+    else hipLaunchKernelGGL((k_full<false>), dim3(a.rows), dim3(kFT), lds, stream, a);
     return hipGetLastError();
 }
+
+size_t full_lds_bytes() { return kFullLdsBytes; }
 
 hipError_t launch_writeback(const StreamArgs& a, int grid, uint32_t lds, hipStream_t stream) {
     if (a.gtab != nullptr) hipLaunchKernelGGL((k_writeback<true>), dim3(grid), dim3(kBlock), lds, stream, a);

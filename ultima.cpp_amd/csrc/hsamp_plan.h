@@ -127,10 +127,12 @@ struct StreamArgs {
     int32_t stage_off;          // exact lists: bytes from the LDS base to the staged chunks
     int32_t hist_direct;        // exact lists: every history row fits 8 * kBlock ids; k_stream
                                 // loads whole rows before the tile, without waiting for the plan
-    float* fullv;               // [rows * vocab] k_full: transformed logits (-inf once removed)
-    float* fullp;               // [rows * vocab] k_full: probabilities
-    uint32_t* fullk;            // [rows * 2 * full_p2] k_full: probability keys by bucket, sort scratch
+    float* fullv;               // [rows * full_stride] k_full: transformed logits (-inf once removed)
+    float* fullp;               // [rows * full_stride] k_full: softmax numerators
+    uint32_t* fullk;            // [rows * full_p2] k_full: top-p keys by bucket
     int32_t full_p2;            // next power of two >= vocab
+    int32_t full_stride;        // k_full: floats per row of fullv / fullp (whole windows of 512 * full_g)
+    int32_t full_g;             // k_full: 512-id steps per index-order window
     uint32_t* gtab;             // [rows * 2 * mhash_slots] penalty tables, or NULL: tables in LDS
     uint32_t merge_lds;         // dynamic LDS of k_merge
     uint32_t lds_bytes;         // dynamic LDS size of the launch

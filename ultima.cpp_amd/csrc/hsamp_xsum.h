@@ -1,0 +1,957 @@
+// Exact sequential float32 sums in parallel, and the full-vocabulary row
+// machinery built on them (block helpers, LDS tables, the top-p driver). Used
+// by k_full in hsamp_kernels.hip and by the test kit that pins the engine.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "hsamp_plan.h"
+#include "hsamp_wave.h"
+
+namespace hsamp {
+
+#ifdef HSAMP_PHASE_CLOCKS
+__device__ __forceinline__ void g_phase_lv(int blk, int level) { g_phase[(14000 + blk) * 16 + level] = __builtin_amdgcn_s_memrealtime(); }
+#else
+__device__ __forceinline__ void g_phase_lv(int, int) {}
+#endif
+
+// ---- full-vocabulary rows ---------------------------------------------------------
+// Sampling rows whose top-k is off (top_k == 0 or >= V) or above kLimitK: the
+// whole transformed row goes through softmax, top-p, min-p and the draw
+// (sampler.cpp:109-182). One block of kFT threads per row; the row's
+// transformed logits and softmax numerators live in global scratch (fullv,
+// fullp, padded to whole windows), the top-p keys in fullk.
+//
+// Exact sequential float sums. softmax_probs (sampler.cpp:124-142) divides by
+// a float sum taken in index order, and apply_top_p (:146-164) compares a
+// float running sum taken in (p desc, index asc) order with top_p. Both are
+// chains of up to V roundings, reproduced here exactly and in parallel: while
+// a running sum s >= 0 stays in one binade [2^E, 2^(E+1)) (E = -126 also
+// covers the subnormals), s = M * 2^(E-23) for an integer M < 2^24, and
+// adding x >= 0 adds x rounded to a multiple of 2^(E-23): an integer
+// increment that depends on x alone, except when x lies exactly half-way
+// between two multiples (then M's parity decides: round half to even).
+// Groups of values (windows of consecutive ids, buckets of probability keys)
+// are summed as integers at the binade an approximate prefix predicts; the
+// few groups where the sum leaves its binade, a half-way value occurs, the
+// prediction fails or (top-p) the threshold is reached are replayed value by
+// value from the exact state, in 64-value steps of one wave.
+
+constexpr int kFT = 1024;             // threads of a k_full block
+constexpr int kFW = kFT / 64;         // its waves
+constexpr int kFWin = 512;            // ids of an index-order window per 512-step (64 lanes x 8)
+constexpr int kFMaxWin = 2048;        // windows the LDS tables hold
+constexpr int kFNB = 4096;            // top-p buckets
+constexpr int kFSort = 512;           // bucket values one wave sorts in LDS
+
+// Exact state of a running float32 sum of values >= 0: s = M * 2^(E-23),
+// E >= -126, M < 2^24, M >= 2^23 unless E == -126.
+struct XState {
+    int E;
+    uint32_t M;
+};
+
+// x = X * 2^(ex-23) with ex >= -126 (subnormals: ex = -126, X < 2^23).
+__device__ __forceinline__ void fparts(float x, int& ex, uint32_t& X) {
+    const uint32_t b = __float_as_uint(x);
+    const uint32_t f = (b >> 23) & 255u;
+    ex = (int)max(f, 1u) - 127;
+    X = (b & 0x7FFFFFu) | (f != 0u ? 0x800000u : 0u);
+}
+
+__device__ __forceinline__ float xs_value(XState s) {
+    return s.M >= 0x800000u ? __uint_as_float(((uint32_t)(s.E + 127) << 23) | (s.M & 0x7FFFFFu))
+                            : __uint_as_float(s.M);
+}
+
+// Increment of x >= 0 at binade E in units of 2^(E-23), half-way values
+// rounded up (tie: round half to even then decides by parity); big: x >= 2^E
+// or more, the sum leaves the binade.
+__device__ __forceinline__ uint32_t xinc(float x, int E, bool& tie, bool& big) {
+    int ex;
+    uint32_t X;
+    fparts(x, ex, X);
+    const int d = E - ex;
+    tie = false;
+    big = false;
+    if (X == 0u || d > 24) return 0u;
+    if (d < 0) {
+        big = true;
+        return 0u;
+    }
+    if (d == 0) return X;
+    const uint32_t half = 1u << (d - 1);
+    const uint32_t r = X & ((half << 1) - 1u);
+    tie = r == half;
+    return (X >> d) + (r >= half ? 1u : 0u);
+}
+
+// s + x, rounded to nearest even, exactly (integer arithmetic only).
+__device__ XState xs_add(XState s, float x) {
+    int ex;
+    uint32_t X;
+    fparts(x, ex, X);
+    if (X == 0u) return s;
+    if (s.M == 0u) return XState{ex, X};
+    const int d = s.E - ex;
+    uint64_t N;
+    int base;
+    if (d >= 0) {
+        if (d > 25) return s;                        // x below a quarter of s's ulp
+        N = ((uint64_t)s.M << d) + X;
+        base = ex;
+    } else {
+        if (-d > 25) return XState{ex, X};           // s below a quarter of x's ulp
+        N = ((uint64_t)X << (-d)) + s.M;
+        base = s.E;
+    }
+    const int len = 64 - __clzll((long long)N);
+    if (len <= 24) {
+        // exact: normalise down to binade -126 at most
+        const int Eb = max(-126, base - (24 - len));
+        return XState{Eb, (uint32_t)(N << (base - Eb))};
+    }
+    const int sh = len - 24;
+    uint64_t mant = N >> sh;
+    const uint64_t rem = N & ((1ull << sh) - 1ull), half = 1ull << (sh - 1);
+    if (rem > half || (rem == half && (mant & 1ull))) ++mant;
+    int E2 = base + sh;
+    if (mant == (1ull << 24)) {
+        mant >>= 1;
+        ++E2;
+    }
+    return XState{E2, (uint32_t)mant};
+}
+
+// The smallest M at binade E with M * 2^(E-23) >= t (t > 0 float); 2^24 when
+// no M of the binade reaches t.
+__device__ __forceinline__ uint32_t xs_thr(float t, int E) {
+    int et;
+    uint32_t T;
+    fparts(t, et, T);
+    const int d = E - et;
+    if (d < 0) return 1u << 24;
+    if (d == 0) return T;
+    if (d > 24) return 1u;
+    return (T + (1u << d) - 1u) >> d;
+}
+
+// The binade of an approximate sum (E = -126 for 0 and subnormals).
+__device__ __forceinline__ int xs_binade(float a) {
+    const uint32_t f = (__float_as_uint(a) >> 23) & 255u;
+    return (int)max(f, 1u) - 127;
+}
+
+// ---- block-wide helpers of k_full (kFT threads) ----
+
+struct FullShared {
+    float rf[kFW];
+    uint32_t ru[kFW];
+    int ri[kFW];
+    double rd[kFW];
+    uint64_t expT[32];
+    double u;
+    int flags;
+    int tok;
+    int sel_d, sel_need;
+    XState xs;         // exact sum result
+    int found;         // top-p: the threshold was reached
+    int fpos;          // ... at this position of the group order (group start + offset)
+    uint32_t fkey;     // ... by a value with this key
+    int fgroup;        // ... in this group
+    int redo;
+    double dS;
+    float m;
+};
+
+__device__ __forceinline__ float fblock_max(float v, FullShared& st) {
+    v = wave_max_f(v);
+    if (lane_id() == 0) st.rf[wave_id()] = v;
+    __syncthreads();
+    float r = st.rf[0];
+#pragma unroll
+    for (int i = 1; i < kFW; ++i) r = fmaxf(r, st.rf[i]);
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ uint32_t fblock_max_u(uint32_t v, FullShared& st) {
+    v = wave_max_u32(v);
+    if (lane_id() == 0) st.ru[wave_id()] = v;
+    __syncthreads();
+    uint32_t r = st.ru[0];
+#pragma unroll
+    for (int i = 1; i < kFW; ++i) r = max(r, st.ru[i]);
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ uint32_t fblock_min_u(uint32_t v, FullShared& st) {
+    v = wave_min_u32(v);
+    if (lane_id() == 0) st.ru[wave_id()] = v;
+    __syncthreads();
+    uint32_t r = st.ru[0];
+#pragma unroll
+    for (int i = 1; i < kFW; ++i) r = min(r, st.ru[i]);
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ int fblock_sum_i(int v, FullShared& st) {
+    v = wave_incl_sum_i(v);
+    if (lane_id() == 63) st.ri[wave_id()] = v;
+    __syncthreads();
+    int r = 0;
+#pragma unroll
+    for (int i = 0; i < kFW; ++i) r += st.ri[i];
+    __syncthreads();
+    return r;
+}
+
+// Exclusive scan over the block in thread order; *total gets the sum.
+__device__ __forceinline__ int fblock_excl_scan(int v, int* total, FullShared& st) {
+    const int incl = wave_incl_sum_i(v);
+    if (lane_id() == 63) st.ri[wave_id()] = incl;
+    __syncthreads();
+    int base = 0, tot = 0;
+#pragma unroll
+    for (int i = 0; i < kFW; ++i) {
+        const int s = st.ri[i];
+        base += (i < wave_id()) ? s : 0;
+        tot += s;
+    }
+    __syncthreads();
+    *total = tot;
+    return base + incl - v;
+}
+
+__device__ __forceinline__ double wave_sum_d(double x) {
+    x = wave_tree_prefix_d(x);
+    return readlane_d(x, 63);
+}
+
+// ---- passes over a row (latency hidden: loads issued ahead of the work) ----
+
+// f(i, x[i]) for every i in [0, n) (n a multiple of 4, x 16-byte aligned),
+// over the block: each thread loads four 16-byte groups of four (sixteen
+// values in flight) before using any of them.
+template <class F>
+__device__ __forceinline__ void fpass(const float* __restrict__ x, int n, F&& f) {
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const int n4 = n >> 2;
+    for (int b = (int)threadIdx.x; b < n4; b += 4 * kFT) {
+        float4 v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int i = b + q * kFT;
+            v[q] = i < n4 ? x4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int i = b + q * kFT;
+            if (i < n4) {
+                f(4 * i, v[q].x);
+                f(4 * i + 1, v[q].y);
+                f(4 * i + 2, v[q].z);
+                f(4 * i + 3, v[q].w);
+            }
+        }
+    }
+}
+
+// f(w, g, v) for each 512-step g of each window w of this wave (windows wid,
+// wid + kFW, ...; steps in order), v the lane's 8 values x[w * 512G + g * 512
+// + lane * 8 + j]; the next step's values are loaded before f runs.
+template <class F>
+__device__ __forceinline__ void wpass(const float* __restrict__ x, int nW, int G, F&& f) {
+    const int lane = lane_id();
+    const int WS = kFWin * G;
+    int w = wave_id(), g = 0;
+    if (w >= nW) return;
+    const float4* p0 = reinterpret_cast<const float4*>(x + (size_t)w * WS + lane * 8);
+    float4 c0 = p0[0], c1 = p0[1];
+    for (;;) {
+        int nw = w, ng = g + 1;
+        if (ng == G) {
+            ng = 0;
+            nw = w + kFW;
+        }
+        float4 n0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), n1 = n0;
+        if (nw < nW) {
+            const float4* pn = reinterpret_cast<const float4*>(x + (size_t)nw * WS + ng * kFWin + lane * 8);
+            n0 = pn[0];
+            n1 = pn[1];
+        }
+        const float v[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        f(w, g, v);
+        if (nw >= nW) break;
+        w = nw;
+        g = ng;
+        c0 = n0;
+        c1 = n1;
+    }
+}
+
+// wpass over two arrays at once (same windows): f(w, g, v, y).
+template <class F>
+__device__ __forceinline__ void wpass2(const float* __restrict__ x, const float* __restrict__ z, int nW, int G,
+                                       F&& f) {
+    const int lane = lane_id();
+    const int WS = kFWin * G;
+    int w = wave_id(), g = 0;
+    if (w >= nW) return;
+    const size_t o0 = (size_t)w * WS + lane * 8;
+    float4 c0 = reinterpret_cast<const float4*>(x + o0)[0], c1 = reinterpret_cast<const float4*>(x + o0)[1];
+    float4 d0 = reinterpret_cast<const float4*>(z + o0)[0], d1 = reinterpret_cast<const float4*>(z + o0)[1];
+    for (;;) {
+        int nw = w, ng = g + 1;
+        if (ng == G) {
+            ng = 0;
+            nw = w + kFW;
+        }
+        float4 n0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), n1 = n0, m0 = n0, m1 = n0;
+        if (nw < nW) {
+            const size_t on = (size_t)nw * WS + ng * kFWin + lane * 8;
+            n0 = reinterpret_cast<const float4*>(x + on)[0];
+            n1 = reinterpret_cast<const float4*>(x + on)[1];
+            m0 = reinterpret_cast<const float4*>(z + on)[0];
+            m1 = reinterpret_cast<const float4*>(z + on)[1];
+        }
+        const float v[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        const float y[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+        f(w, g, v, y);
+        if (nw >= nW) break;
+        w = nw;
+        g = ng;
+        c0 = n0;
+        c1 = n1;
+        d0 = m0;
+        d1 = m1;
+    }
+}
+
+// ---- the exact sequential sum engine (one wave) ----
+
+// min(a + b, 2^25): the running prefixes only matter up to 2^24.
+__device__ __forceinline__ uint32_t sat_add(uint32_t a, uint32_t b) { return min(a + b, 1u << 25); }
+
+// What adding some values in order does to M at a fixed binade: d0 when M
+// starts even, d1 when odd. A half-way value with lower multiple K rounds to
+// the even neighbour, (K + (K & 1), K + 1 - (K & 1)); any other value adds
+// its increment whatever the parity; one that leaves the binade saturates.
+// Composing is associative, so sequences are scanned like sums.
+struct XPair {
+    uint32_t d0, d1;
+};
+__device__ __forceinline__ XPair xinc2(float x, int E) {
+    bool t, b;
+    const uint32_t i = xinc(x, E, t, b);
+    if (b) return XPair{1u << 25, 1u << 25};
+    if (!t) return XPair{i, i};
+    const uint32_t K = i - 1u;
+    return XPair{K + (K & 1u), K + 1u - (K & 1u)};
+}
+// a, then b
+__device__ __forceinline__ XPair xcomp(XPair a, XPair b) {
+    return XPair{sat_add(a.d0, (a.d0 & 1u) ? b.d1 : b.d0), sat_add(a.d1, (a.d1 & 1u) ? b.d0 : b.d1)};
+}
+__device__ __forceinline__ uint32_t xat(XPair a, uint32_t M) { return (M & 1u) ? a.d1 : a.d0; }
+
+// Inclusive scan of pairs over the wave in lane order (DPP, as wave_scan_u32).
+template <int CTRL, int ROWM>
+__device__ __forceinline__ XPair xcomp_dpp(XPair x) {
+    const XPair l{dpp_u32<CTRL, ROWM>(0u, x.d0), dpp_u32<CTRL, ROWM>(0u, x.d1)};
+    return xcomp(l, x);
+}
+__device__ __forceinline__ XPair wave_scan_pair(XPair x) {
+    x = xcomp_dpp<0x111, 0xF>(x);
+    x = xcomp_dpp<0x112, 0xF>(x);
+    x = xcomp_dpp<0x114, 0xF>(x);
+    x = xcomp_dpp<0x118, 0xF>(x);
+    x = xcomp_dpp<0x142, 0xA>(x);
+    x = xcomp_dpp<0x143, 0xC>(x);
+    return x;
+}
+
+// Replays v[lane * 8 + j] (in that order; absent values +0) onto s, from
+// position `start` on. With thr_on, stops at the first value after which the
+// sum reaches thr and returns its position (0..511); else returns -1. Each
+// step takes every remaining value at s's binade at once (lanes' pairs
+// scanned, then each lane's values in order from its exact start) and applies
+// them up to the first value that leaves the binade or reaches thr, which is
+// added exactly.
+__device__ int xs_replay(XState& s, const float (&v)[8], int start, bool thr_on, float thr) {
+    const int lane = lane_id();
+    for (;;) {
+        const int E = s.E;
+        const uint32_t M = s.M;
+        const uint32_t thrM = thr_on ? xs_thr(thr, E) : 0xFFFFFFFFu;
+        XPair e[8];
+        XPair lp{0u, 0u};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            e[j] = (lane * 8 + j >= start) ? xinc2(v[j], E) : XPair{0u, 0u};
+            lp = xcomp(lp, e[j]);
+        }
+        const XPair incl = wave_scan_pair(lp);
+        const XPair prev{(uint32_t)__shfl_up((int)incl.d0, 1, 64), (uint32_t)__shfl_up((int)incl.d1, 1, 64)};
+        uint32_t cur = sat_add(M, lane == 0 ? 0u : xat(prev, M));
+        int first = 8;
+        uint32_t at = cur;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t after = sat_add(cur, xat(e[j], cur));
+            if (first == 8 && lane * 8 + j >= start && (after >= (1u << 24) || after >= thrM)) {
+                first = j;
+                at = cur;
+            }
+            cur = after;
+        }
+        const u64 em = __ballot(first < 8);
+        if (em == 0ull) {
+            s.M = (uint32_t)__builtin_amdgcn_readlane((int)cur, 63);
+            return -1;
+        }
+        const int L = __ffsll((long long)em) - 1;
+        const int jf = __builtin_amdgcn_readlane(first, L);
+        float xv = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xv = (j == jf) ? v[j] : xv;
+        xv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xv), L));
+        s.M = (uint32_t)__builtin_amdgcn_readlane((int)at, L);
+        s = xs_add(s, xv);
+        const int pos = L * 8 + jf;
+        if (thr_on && xs_value(s) >= thr) return pos;
+        start = pos + 1;
+        if (start >= 512) return -1;
+    }
+}
+
+// Group table entry: (E + 256) | flags << 16 with the group's pair at E in
+// D0/D1 (saturated at 2^25). Flags: 1 = the group must be replayed value by
+// value (its order is not known, and a half-way value makes it matter; or
+// too many values for the sums), 2 = empty group.
+constexpr uint32_t kGCare = 1u, kGEmpty = 2u;
+__device__ __forceinline__ uint32_t gpack(int E, uint32_t flags) { return (uint32_t)(E + 256) | (flags << 16); }
+
+// Composes groups 0 .. n-1 in order onto s by one wave: whole groups at once
+// while their tables say they stay in s's binade (and below thr); any other
+// group goes to slow(g, s), which replays it exactly and returns true when
+// the composition has to stop there (threshold reached, or the caller takes
+// over). Starts at group c. Returns the group it stopped at, or -1.
+template <class Slow>
+__device__ int xs_compose(int n, const uint32_t* EF, const uint32_t* D0, const uint32_t* D1, bool thr_on, float thr,
+                          XState& s, Slow&& slow, int c = 0) {
+    const int lane = lane_id();
+    while (c < n) {
+        const int g = c + lane;
+        const bool valid = g < n;
+        const uint32_t ef = valid ? EF[g] : 0u;
+        const int Eg = (int)(ef & 0xFFFFu) - 256;
+        const uint32_t fl = ef >> 16;
+        const bool empty = valid && (fl & kGEmpty) != 0u;
+        const bool ok = empty || (valid && fl == 0u && Eg == s.E);
+        const XPair d = (ok && !empty) ? XPair{D0[g], D1[g]} : XPair{0u, 0u};
+        const XPair pre = wave_scan_pair(d);
+        const uint32_t thrM = thr_on ? xs_thr(thr, s.E) : 0xFFFFFFFFu;
+        const uint32_t tot = sat_add(s.M, xat(pre, s.M));
+        const bool bad = !ok || tot >= (1u << 24) || tot >= thrM;
+        const u64 bm = __ballot(bad);
+        const int f = bm ? __ffsll((long long)bm) - 1 : 64;
+        if (f > 0) s.M = (uint32_t)__builtin_amdgcn_readlane((int)tot, f - 1);
+        if (f == 64) {
+            c += 64;
+            continue;
+        }
+        const int gs = c + f;
+        if (gs >= n) break;
+        if (slow(gs, s)) return gs;
+        c = gs + 1;
+    }
+    return -1;
+}
+
+// ---- k_full phases ----
+
+// LDS of a k_full block after the penalty table (when it lives there):
+// window tables, bucket tables, one wave's sort buffer.
+struct FullLds {
+    float* winA;        // [kFMaxWin] approximate window sums (the draw: winA..winD0 as doubles)
+    uint32_t* winD0;    // [kFMaxWin]
+    uint32_t* winD1;    // [kFMaxWin]
+    uint32_t* winEF;    // [kFMaxWin]
+    uint32_t* gath;     // [kFGather] top-p: keys of the buckets replayed value by value (the window tables' space)
+    uint32_t* bcnt;     // [kFNB + 1] bucket counts, then starts
+    uint32_t* bfill;    // [kFNB] fill positions (global scatter)
+    uint32_t* bD;       // [kFNB]
+    uint32_t* bEF;      // [kFNB]
+    uint32_t* gst;      // [kFNB] start of the bucket's keys in gath, or kNoGath
+    uint32_t* gfill;    // [kFNB] their fill positions
+    uint32_t* sortb;    // [kFSort]
+};
+constexpr int kFGather = 4 * kFMaxWin;
+constexpr uint32_t kNoGath = 0xFFFFFFFFu;
+constexpr size_t kFullLdsBytes = 4 * 4 * kFMaxWin + 4 * (kFNB + 1) + 5 * 4 * kFNB + 4 * kFSort + 64;
+
+__device__ __forceinline__ FullLds full_lds(unsigned char* base) {
+    FullLds f;
+    uint32_t* p = reinterpret_cast<uint32_t*>(base);
+    f.winA = reinterpret_cast<float*>(p);
+    f.winD0 = p + kFMaxWin;
+    f.winD1 = p + 2 * kFMaxWin;
+    f.winEF = p + 3 * kFMaxWin;
+    f.gath = p;
+    f.bcnt = p + 4 * kFMaxWin;
+    f.bfill = f.bcnt + kFNB + 1;
+    f.bD = f.bfill + kFNB;
+    f.bEF = f.bfill + 2 * kFNB;
+    f.gst = f.bfill + 3 * kFNB;
+    f.gfill = f.bfill + 4 * kFNB;
+    f.sortb = f.bfill + 5 * kFNB;
+    return f;
+}
+
+// Exclusive float scan over the block in thread order (approximate sums).
+__device__ __forceinline__ float fblock_excl_scan_f(float v, float* total, FullShared& st) {
+    const float incl = wave_tree_prefix_f(v);
+    if (lane_id() == 63) st.rf[wave_id()] = incl;
+    __syncthreads();
+    float base = 0.0f, tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kFW; ++i) {
+        const float s = st.rf[i];
+        base += (i < wave_id()) ? s : 0.0f;
+        tot += s;
+    }
+    __syncthreads();
+    *total = tot;
+    return base + incl - v;
+}
+
+// The exact index-order float sum of x[0, nW * 512 * G) (values >= 0, the
+// padding +0), given each window's approximate sum in f.winA: predicted
+// binades from the approximate prefixes, the windows' pairs at them, then one
+// wave composes (replaying the windows where the prediction fails or the
+// sum leaves its binade).
+__device__ XState exact_index_sum(const float* x, int nW, int G, FullLds f, FullShared& st) {
+    const int tid = threadIdx.x, lane = lane_id(), wid = wave_id();
+    const int WS = kFWin * G;
+    {
+        // two windows per thread: their approximate start values -> binades
+        const int w0 = 2 * tid;
+        const float a0 = w0 < nW ? f.winA[w0] : 0.0f, a1 = w0 + 1 < nW ? f.winA[w0 + 1] : 0.0f;
+        float tot;
+        const float pre = fblock_excl_scan_f(a0 + a1, &tot, st);
+        if (w0 < nW) f.winEF[w0] = gpack(w0 == 0 ? -126 : xs_binade(pre), 0u);
+        if (w0 + 1 < nW) f.winEF[w0 + 1] = gpack(xs_binade(pre + a0), 0u);
+    }
+    __syncthreads();
+    {
+        XPair wp{0u, 0u};
+        bool nz = false;
+        wpass(x, nW, G, [&](int w, int g, const float (&v)[8]) {
+            const int E = (int)(f.winEF[w] & 0xFFFFu) - 256;
+            XPair lp{0u, 0u};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                lp = xcomp(lp, xinc2(v[j], E));
+                nz |= v[j] != 0.0f;
+            }
+            const XPair sp = wave_scan_pair(lp);
+            wp = xcomp(wp, XPair{(uint32_t)__builtin_amdgcn_readlane((int)sp.d0, 63),
+                                 (uint32_t)__builtin_amdgcn_readlane((int)sp.d1, 63)});
+            if (g == G - 1) {
+                const bool empty = __ballot(nz) == 0ull;
+                if (lane == 0) {
+                    f.winD0[w] = wp.d0;
+                    f.winD1[w] = wp.d1;
+                    f.winEF[w] = gpack(E, empty ? kGEmpty : 0u);
+                }
+                wp = XPair{0u, 0u};
+                nz = false;
+            }
+        });
+    }
+    __syncthreads();
+    if (wid == 0) {
+        XState s{-126, 0u};
+        xs_compose(nW, f.winEF, f.winD0, f.winD1, false, 0.0f, s, [&](int w, XState& sv) -> bool {
+            for (int g = 0; g < G; ++g) {
+                const float4* src = reinterpret_cast<const float4*>(x + (size_t)w * WS + g * kFWin + lane * 8);
+                const float4 q0 = src[0], q1 = src[1];
+                const float v[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+                xs_replay(sv, v, 0, false, 0.0f);
+            }
+            return false;
+        });
+        if (lane == 0) st.xs = s;
+    }
+    __syncthreads();
+    return st.xs;
+}
+
+// Sorts a[0, n) descending in LDS by one wave (n <= kFSort): a rank placement
+// for n <= 64, else a bitonic network over the next power of two (padding 0).
+__device__ void wave_sort_desc_lds(uint32_t* a, int n) {
+    const int lane = lane_id();
+    if (n <= 64) {
+        const uint32_t k = lane < n ? a[lane] : 0u;
+        wave_sync();
+        const uint4* a4 = reinterpret_cast<const uint4*>(a);
+        int rank = 0;
+        for (int q = 0; q < 16; ++q) {
+            const uint4 y = a4[q];
+            const uint32_t ys[4] = {y.x, y.y, y.z, y.w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int i = 4 * q + c;
+                const uint32_t yv = i < n ? ys[c] : 0u;
+                rank += (yv > k) || (yv == k && i < lane);
+            }
+        }
+        wave_sync();
+        if (lane < n) a[rank] = k;
+        wave_sync();
+        return;
+    }
+    int P2 = 128;
+    while (P2 < n) P2 <<= 1;
+    for (int i = n + lane; i < P2; i += 64) a[i] = 0u;
+    for (int k = 2; k <= P2; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            wave_sync();
+            for (int t = lane; t < P2 / 2; t += 64) {
+                const int i = ((t & ~(j - 1)) << 1) | (t & (j - 1));
+                const int l = i | j;
+                const uint32_t x = a[i], y = a[l];
+                const bool desc = (i & k) == 0;
+                if (desc ? (x < y) : (x > y)) {
+                    a[i] = y;
+                    a[l] = x;
+                }
+            }
+        }
+    }
+    wave_sync();
+}
+
+// The row's top-p cutoff (sampler.cpp:146-164) over the probabilities
+// p = e * inv (e = pv, inv = fl(1 / softmax sum)): the cumulative float sum in
+// (p desc, index asc) order, exactly. Keys (float bits of p > 0) in [lo, hi]
+// go to kFNB buckets of equal key width in descending order. One pass counts
+// them; a scan gives each bucket's place and, from counts times the bucket's
+// middle value, its predicted binade; a second pass adds every value's
+// increment at its bucket's binade (noting half-way values, whose order
+// then matters) and copies into LDS the keys of the buckets that are likely
+// to be replayed value by value -- those early in the order (half-way
+// values are common while the sum is within 2^10 of them) or where the
+// approximate sum changes binade or reaches top_p. One wave composes the
+// buckets; a bucket that must be replayed is sorted in LDS (or taken as it
+// is when all its keys are equal). Buckets flagged by the pass but not
+// copied are copied by one more pass, any other bucket on demand; one too
+// large to sort is refined (its key range becomes the next [lo, hi]), and a
+// range that runs out continues below it. Returns whether the running sum
+// reached top_p; then *cut_key is the key of the last kept value, *cut_count
+// the number kept and st.dS the sum there.
+__device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_p, uint32_t* fk, FullLds f,
+                           FullShared& st, uint32_t* cut_key, int* cut_count) {
+    const int tid = threadIdx.x, lane = lane_id(), wid = wave_id();
+    (void)fk;
+    uint32_t kmx = 0u, kmn = 0xFFFFFFFFu;
+    fpass(pv, Vp, [&](int, float e) {
+        const uint32_t key = __float_as_uint(e * inv);
+        if (key != 0u) {
+            kmx = max(kmx, key);
+            kmn = min(kmn, key);
+        }
+    });
+    kmx = fblock_max_u(kmx, st);
+    kmn = fblock_min_u(kmn, st);
+    HSAMP_PHASE(13000 + blockIdx.x, 0);
+    if (kmx == 0u) return false;
+    XState s{-126, 0u};
+    int counted = 0;
+    uint32_t lo = kmn, hi = kmx;
+    for (int level = 0; level < 1024; ++level) {
+        const uint32_t span = hi - lo;
+        const int shift = span >= (uint32_t)kFNB ? (32 - __clz((int)span)) - 12 : 0;
+        const int nb = (int)(span >> shift) + 1;
+        auto bucket_of = [&](uint32_t key) -> int { return (int)((hi - key) >> shift); };
+        auto in_range = [&](uint32_t key) -> bool { return key != 0u && key >= lo && key <= hi; };
+        for (int b = tid; b < nb; b += kFT) {
+            f.bcnt[b] = 0u;
+            f.bD[b] = 0u;
+        }
+        __syncthreads();
+        fpass(pv, Vp, [&](int, float e) {
+            const uint32_t key = __float_as_uint(e * inv);
+            if (in_range(key)) atomicAdd(&f.bcnt[bucket_of(key)], 1u);
+        });
+        __syncthreads();
+        if (level == 0) HSAMP_PHASE(13000 + blockIdx.x, 1);
+        {
+            // starts, predicted binades and the buckets to copy: 4 per thread, in order
+            uint32_t c[4];
+            float a4[4], mv[4];
+            uint32_t cs = 0u;
+            float as = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int b = 4 * tid + q;
+                c[q] = b < nb ? f.bcnt[b] : 0u;
+                // count times the bucket's middle value
+                const int64_t mid = (int64_t)hi - ((int64_t)b << shift) - (((int64_t)1 << shift) >> 1);
+                mv[q] = __uint_as_float((uint32_t)max(mid, (int64_t)lo));
+                a4[q] = (float)c[q] * mv[q];
+                cs += c[q];
+                as += a4[q];
+            }
+            int ctot;
+            uint32_t cpos = (uint32_t)fblock_excl_scan((int)cs, &ctot, st);
+            float atot;
+            float apos = xs_value(s) + fblock_excl_scan_f(as, &atot, st);
+            bool gq[4];
+            int gcnt = 0;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int b = 4 * tid + q;
+                gq[q] = false;
+                if (b < nb) {
+                    f.bcnt[b] = cpos;
+                    f.bfill[b] = cpos;
+                    // more than 255 values: the increment sum could wrap
+                    const uint32_t fl = (c[q] == 0u ? kGEmpty : 0u) | (c[q] > 255u ? kGCare : 0u);
+                    const int E = xs_binade(apos);
+                    f.bEF[b] = gpack(E, fl);
+                    if (c[q] != 0u && c[q] <= (uint32_t)kFSort) {
+                        // (the approximate sums are within about 1e-4 of the true ones)
+                        const float lo_e = apos * 0.998f, hi_e = (apos + a4[q]) * 1.002f;
+                        const bool tie_prone = E - xs_binade(mv[q]) <= 10;
+                        const bool cross = xs_binade(lo_e) != xs_binade(hi_e);
+                        const bool at_thr = lo_e <= top_p && top_p <= hi_e;
+                        gq[q] = tie_prone || cross || at_thr;
+                    }
+                    gcnt += gq[q] ? (int)c[q] : 0;
+                }
+                cpos += c[q];
+                apos += a4[q];
+            }
+            // places in the copy area, in bucket order, while it has room
+            int gtot;
+            int gpos = fblock_excl_scan(gcnt, &gtot, st);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int b = 4 * tid + q;
+                if (b < nb) {
+                    const bool g = gq[q] && gpos + (int)c[q] <= kFGather;
+                    f.gst[b] = g ? (uint32_t)gpos : kNoGath;
+                    f.gfill[b] = (uint32_t)gpos;
+                    gpos += gq[q] ? (int)c[q] : 0;
+                }
+            }
+            if (tid == 0) {
+                f.bcnt[nb] = (uint32_t)ctot;
+                st.sel_d = min(gtot, kFGather);   // the copy area in use (a bound)
+            }
+        }
+        __syncthreads();
+        if (level == 0) HSAMP_PHASE(13000 + blockIdx.x, 2);
+        fpass(pv, Vp, [&](int, float e) {
+            const float p = e * inv;
+            const uint32_t key = __float_as_uint(p);
+            if (in_range(key)) {
+                const int b = bucket_of(key);
+                const uint32_t ef = f.bEF[b];
+                bool t, bg;
+                const uint32_t inc = xinc(p, (int)(ef & 0xFFFFu) - 256, t, bg);
+                if (inc) atomicAdd(&f.bD[b], inc);
+                if ((t || bg) && !((ef >> 16) & kGCare)) atomicOr(&f.bEF[b], kGCare << 16);
+                if (f.gst[b] != kNoGath) f.gath[atomicAdd(&f.gfill[b], 1u)] = key;
+            }
+        });
+        __syncthreads();
+        if (level == 0) HSAMP_PHASE(13000 + blockIdx.x, 3);
+        // buckets flagged by the pass (half-way values) but not copied
+        {
+            int gcnt = 0;
+            bool gq[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int b = 4 * tid + q;
+                const uint32_t n = b < nb ? f.bcnt[b + 1] - f.bcnt[b] : 0u;
+                gq[q] = b < nb && f.gst[b] == kNoGath && n != 0u && n <= (uint32_t)kFSort &&
+                        ((f.bEF[b] >> 16) & kGCare) != 0u;
+                gcnt += gq[q] ? (int)n : 0;
+            }
+            int gtot;
+            int gpos = st.sel_d + fblock_excl_scan(gcnt, &gtot, st);
+            const bool fits = st.sel_d + gtot <= kFGather;
+            if (gtot > 0 && fits) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int b = 4 * tid + q;
+                    if (gq[q]) {
+                        f.gst[b] = kNoGath - 1u;   // being copied: marked, then given its place
+                        f.gfill[b] = (uint32_t)gpos;
+                        gpos += (int)(f.bcnt[b + 1] - f.bcnt[b]);
+                    }
+                }
+                __syncthreads();
+                fpass(pv, Vp, [&](int, float e) {
+                    const uint32_t key = __float_as_uint(e * inv);
+                    if (in_range(key)) {
+                        const int b = bucket_of(key);
+                        if (f.gst[b] == kNoGath - 1u) f.gath[atomicAdd(&f.gfill[b], 1u)] = key;
+                    }
+                });
+                __syncthreads();
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int b = 4 * tid + q;
+                    if (gq[q]) f.gst[b] = f.gfill[b] - (f.bcnt[b + 1] - f.bcnt[b]);
+                }
+                if (tid == 0) st.sel_d += gtot;
+            }
+            __syncthreads();
+        }
+        // compose (wave 0) from bucket c0; st.found: 1 = reached, 2 = refine
+        // bucket st.fgroup, 3 = copy bucket st.fgroup first
+        int c0 = 0;
+        for (;;) {
+            if (wid == 0) {
+                if (lane == 0) st.found = 0;
+                const int g = xs_compose(nb, f.bEF, f.bD, f.bD, true, top_p, s, [&](int b, XState& sv) -> bool {
+                    const uint32_t b0 = f.bcnt[b], n = f.bcnt[b + 1] - b0;
+                    if (n == 0u) return false;
+                    const uint32_t gs = f.gst[b];
+                    if (shift == 0) {
+                        // a bucket of one key: n equal values, in any order
+                        const float val = __uint_as_float(hi - (uint32_t)b);
+                        for (uint32_t o = 0; o < n; o += 512) {
+                            float v[8];
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) v[j] = o + lane * 8 + j < n ? val : 0.0f;
+                            const int pos = xs_replay(sv, v, 0, true, top_p);
+                            if (pos >= 0) {
+                                if (lane == 0) {
+                                    st.found = 1;
+                                    st.fpos = (int)(b0 + o) + pos;
+                                    st.fkey = hi - (uint32_t)b;
+                                    st.xs = sv;
+                                }
+                                return true;
+                            }
+                        }
+                        return false;
+                    }
+                    if (gs == kNoGath) {
+                        if (n > (uint32_t)kFSort) {
+                            if (lane == 0) {
+                                st.found = 2;
+                                st.fgroup = b;
+                                st.xs = sv;
+                                st.fpos = (int)b0;
+                            }
+                        } else if (lane == 0) {
+                            st.found = 3;
+                            st.fgroup = b;
+                            st.xs = sv;
+                        }
+                        return true;
+                    }
+                    // sort the bucket's keys (n <= kFSort), then replay them in order
+                    const uint32_t* keys = f.gath + gs;
+                    for (uint32_t e = lane; e < n; e += 64) f.sortb[e] = keys[e];
+                    wave_sort_desc_lds(f.sortb, (int)n);
+                    keys = f.sortb;
+                    for (uint32_t o = 0; o < n; o += 512) {
+                        float v[8];
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+                            const uint32_t e = o + lane * 8 + j;
+                            v[j] = e < n ? __uint_as_float(keys[e]) : 0.0f;
+                        }
+                        const int pos = xs_replay(sv, v, 0, true, top_p);
+                        if (pos >= 0) {
+                            if (lane == 0) {
+                                st.found = 1;
+                                st.fpos = (int)(b0 + o) + pos;
+                                st.fkey = keys[o + pos];
+                                st.xs = sv;
+                            }
+                            wave_sync();
+                            return true;
+                        }
+                    }
+                    wave_sync();
+                    return false;
+                }, c0);
+                if (g < 0 && lane == 0) st.xs = s;
+            }
+            __syncthreads();
+            const int fd = st.found;
+            s = st.xs;
+            if (fd != 3) break;
+            // copy bucket st.fgroup (into LDS when it fits, else refine it)
+            const int b = st.fgroup;
+            const uint32_t n = f.bcnt[b + 1] - f.bcnt[b];
+            if (st.sel_d + (int)n <= kFGather) {
+                if (tid == 0) {
+                    f.gst[b] = kNoGath - 1u;
+                    f.gfill[b] = (uint32_t)st.sel_d;
+                }
+                __syncthreads();
+                fpass(pv, Vp, [&](int, float e) {
+                    const uint32_t key = __float_as_uint(e * inv);
+                    if (in_range(key) && bucket_of(key) == b) f.gath[atomicAdd(&f.gfill[b], 1u)] = key;
+                });
+                __syncthreads();
+                if (tid == 0) {
+                    f.gst[b] = (uint32_t)st.sel_d;
+                    st.sel_d += (int)n;
+                }
+                __syncthreads();
+                c0 = b;
+                continue;
+            }
+            if (tid == 0) {
+                st.found = 2;
+                st.fpos = (int)f.bcnt[b];
+            }
+            __syncthreads();
+            break;
+        }
+        if (level == 0) HSAMP_PHASE(13000 + blockIdx.x, 4);
+        if (threadIdx.x == 0 && level < 8) g_phase_lv(blockIdx.x, level);
+        const int fd = st.found;
+        if (fd == 1) {
+            *cut_key = st.fkey;
+            *cut_count = counted + st.fpos + 1;
+            st.dS = (double)xs_value(s);
+            return true;
+        }
+        if (fd == 2) {
+            // refine: the bucket's key range, from the state before it
+            const int b = st.fgroup;
+            counted += st.fpos;
+            const uint64_t top = (uint64_t)hi - ((uint64_t)b << shift);
+            const uint64_t w = (uint64_t)1 << shift;
+            const uint64_t bot = top + 1u >= w + lo ? top + 1u - w : (uint64_t)lo;
+            hi = (uint32_t)top;
+            lo = (uint32_t)bot;
+            __syncthreads();
+            continue;
+        }
+        // the range ran out: continue below it
+        counted += (int)f.bcnt[nb];
+        __syncthreads();
+        if (lo <= kmn) return false;
+        hi = lo - 1u;
+        lo = kmn;
+    }
+    return false;
+}
+
+}  // namespace hsamp

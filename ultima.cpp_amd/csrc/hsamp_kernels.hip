@@ -1,25 +1,30 @@
-// HIP kernels of the gfx950 token sampler.
+// HIP kernels of the gfx950 token sampler (reference src/sampler/sampler.cpp).
 //
-// k_stream: one workgroup per (row, slice) of the [B, V] logits. Each block
-//   1. builds, in LDS, the penalty bookkeeping of its slice from the row's
-//      history (bitmap of touched ids + open-addressing table of counts),
-//   2. streams its slice in 8192-element tiles with 16-byte loads, applies
-//      mask -> bias -> repetition -> DRY -> frequency/presence -> temperature
-//      to each logit in registers (reference src/sampler/sampler.cpp:235-264),
-//   3. keeps a candidate buffer of (value, index) composites in LDS, filtered
-//      by a threshold that only rises: a per-tile lower bound from the k/4-th
-//      largest group maximum of each wave (ballot radix select), and the exact
-//      k-th composite after each buffer compaction (LDS radix select),
-//   4. hands its candidates to the row's last block (atomic counter), which
-//      merges them into the exact top-k (value desc, index asc) and runs the
-//      rest of the ladder over the <= k kept logits: softmax with glibc-exact
-//      expf and index-order float sums, top-p over the (p desc, index asc)
-//      order, min-p, the double-precision CDF and the draw against u.
-// Greedy rows (T <= 0) take the argmax of the penalised logits instead.
+// Top-k rows (k <= the candidate limit) stream the [B, V] logits once:
+// k_stream takes one workgroup per (row, slice), applies mask -> bias ->
+// repetition -> DRY -> frequency/presence -> temperature to each logit in
+// registers (sampler.cpp:235-264) and leaves the slice's candidates in
+// global scratch:
+//   - exact lists (sampling rows, k <= 64, penalties that only lower
+//     logits): every id whose final key can still be in the row's top k,
+//     filtered by a bound from the slice's own top keys; k_pick, one block
+//     per row on the XCD that streamed it, merges the row's lists;
+//   - general path (greedy rows, DRY, bias, k up to 1024, write-back,
+//     unaligned rows): a candidate buffer in LDS under a rising threshold
+//     (or the slice's argmax for a greedy row), merged by k_merge.
+// The merge gives the exact top-k (value desc, index asc) and runs the rest
+// of the ladder over the <= k kept logits: softmax with glibc-exact expf and
+// index-order float sums, top-p over the (p desc, index asc) order, min-p,
+// the double-precision CDF and the draw against the row's u.
 //
-// k_writeback: optional second pass leaving the logits exactly as the
-//   reference's sample() leaves them (kept logits post-temperature, the rest
-//   -inf; post-penalty logits for greedy rows).
+// k_full: one 1024-thread block per row that samples the whole vocabulary
+//   (top-k off or above the candidate limit): the same ladder over all V
+//   values, with the reference's sequential float sums reproduced exactly in
+//   parallel (integer increments per binade, half-way ties as parity pairs).
+//
+// k_writeback: optional pass leaving the logits exactly as the reference's
+//   sample() leaves them (kept logits post-temperature, the rest -inf;
+//   post-penalty logits for greedy rows).
 //
 // No MFMA: nothing here is a contraction. The stream phase is HBM-bound.
 #include <hip/hip_runtime.h>

@@ -17,6 +17,16 @@
 // 2^(i/32) with i << 47 subtracted from its bit pattern. An exhaustive check
 // over every non-NaN float (tests/test_libm_expf.py) shows bit equality with
 // the host's expf.
+//
+// Upstream notice. The method, the table layout and the three polynomial
+// coefficients follow the expf of ARM's optimized-routines
+// (https://github.com/ARM-software/optimized-routines, math/expf.c and
+// math/exp2f_data.c; Copyright (c) 2017-2018, Arm Limited; MIT licence), as
+// shipped in the GNU C Library (sysdeps/ieee754/flt-32/e_expf.c and
+// e_exp2f_data.c; Copyright (C) 2017-2022 Free Software Foundation, Inc.;
+// LGPL-2.1-or-later). The table entries are the doubles nearest 2^(i/32) and
+// the coefficients are those published with that method; they are restated
+// here so that the device reproduces the host library's results bit for bit.
 #pragma once
 
 #include <stdint.h>

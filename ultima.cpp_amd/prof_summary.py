@@ -1,0 +1,130 @@
+"""Summarise rocprofv3 runs of bench.py into the text kept under profiles/.
+
+Inputs are three rocprofv3 output folders of the same bench command:
+  --stats  a `--kernel-trace --stats` run (per-kernel average durations)
+  --fetch  a `--pmc FETCH_SIZE` run, --write a `--pmc WRITE_SIZE` run
+           (KiB per dispatch), both with `bench.py --copy-probe-mib M`: the
+           M MiB device copy they end with calibrates each counter (bytes it
+           must have moved / what the counter reported for it).
+
+Writes <out>/<kernels>_cfg<N>_profile.md (kernel durations, traffic per kernel,
+the commands) and, for the kernel that reads the logits,
+<out>/<kernel>_cfg<N>_traffic.json, which bench.py reads for
+roofline.traffic.
+
+    python3 ultima.cpp_amd/prof_summary.py --config 2 --stats DIR --fetch DIR --write DIR \
+        --bench DIR/stats_bench.json --copy-mib 512 --out profiles --command "..."
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import json
+import statistics
+from collections import defaultdict
+from pathlib import Path
+
+COPY_KERNEL = "__amd_rocclr_copyBuffer"
+STREAM_KERNEL = {1: "k_stream", 2: "k_stream", 3: "k_full", 4: "k_stream", 5: "k_stream"}
+
+
+def short(name: str) -> str:
+    """'void hsamp::k_stream<0, true, ...>(hsamp::StreamArgs)' -> 'k_stream<0, true, ...>'"""
+    n = name.split("(")[0]
+    for p in ("void ", "hsamp::"):
+        n = n.replace(p, "")
+    return n
+
+
+def one_csv(folder: Path, suffix: str) -> Path:
+    files = sorted(folder.rglob(f"*{suffix}"))
+    if not files:
+        raise SystemExit(f"no *{suffix} under {folder}")
+    return files[0]
+
+
+def kernel_stats(folder: Path) -> list[dict]:
+    rows = list(csv.DictReader(one_csv(folder, "kernel_stats.csv").open()))
+    return [r for r in rows if "hsamp::" in r["Name"]]
+
+
+def counter(folder: Path) -> dict[str, list[float]]:
+    per = defaultdict(list)
+    for r in csv.DictReader(one_csv(folder, "counter_collection.csv").open()):
+        per[r["Kernel_Name"]].append(float(r["Counter_Value"]))
+    return per
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--config", type=int, required=True)
+    ap.add_argument("--stats", type=Path, required=True)
+    ap.add_argument("--fetch", type=Path, required=True)
+    ap.add_argument("--write", type=Path, required=True)
+    ap.add_argument("--bench", type=Path, required=True, help="the bench JSON line of the stats run")
+    ap.add_argument("--copy-mib", type=int, required=True)
+    ap.add_argument("--out", type=Path, required=True)
+    ap.add_argument("--command", action="append", default=[], help="a command that made the inputs (repeatable)")
+    a = ap.parse_args()
+
+    bench = json.loads(a.bench.read_text().strip().splitlines()[-1])
+    algo = int(bench["config"]["bytes_per_step"])
+    stats = kernel_stats(a.stats)
+    fetch, write = counter(a.fetch), counter(a.write)
+    copy_kib = a.copy_mib * 1024.0
+    f_copy, w_copy = max(fetch.get(COPY_KERNEL, [0.0])), max(write.get(COPY_KERNEL, [0.0]))
+    if f_copy <= 0 or w_copy <= 0:
+        raise SystemExit("the calibration copy is missing from the counter runs")
+    fs, ws = copy_kib / f_copy, copy_kib / w_copy
+
+    table = []
+    for r in stats:
+        name = r["Name"]
+        f = statistics.median(fetch[name]) if fetch.get(name) else None
+        w = statistics.median(write[name]) if write.get(name) else None
+        hbm = None if f is None or w is None else (f * fs + w * ws) * 1024.0
+        table.append((short(name), int(r["Calls"]), float(r["AverageNs"]) / 1000.0, f, w, hbm))
+
+    cfg = a.config
+    sk = STREAM_KERNEL[cfg]
+    main_row = next((t for t in table if t[0].startswith(sk + "<") and t[5] is not None), None)
+    wl = bench["config"]["workload"]
+    lines = [f"# rocprofv3 profile, workload {wl}", ""]
+    lines += ["Commands (from the repository root on the GPU box):", ""]
+    lines += [f"    {c}" for c in a.command] + [""]
+    lines += [f"Calibration: the {a.copy_mib} MiB device copy (`{COPY_KERNEL}`) read as "
+              f"{f_copy:.0f} KiB by FETCH_SIZE (scale {fs:.3f}) and {w_copy:.0f} KiB by WRITE_SIZE "
+              f"(scale {ws:.3f}). Counter figures are medians over the dispatches; durations are "
+              "rocprofv3's averages over every dispatch of the stats run (graph replays of the full "
+              "step and of the stream kernel alone, read probes and uncaptured calls).", ""]
+    lines += ["| kernel | dispatches | avg us | FETCH KiB | WRITE KiB | HBM bytes (scaled) | x algorithmic |",
+              "|---|---|---|---|---|---|---|"]
+    for n, c, us, f, w, hbm in table:
+        ratio = "" if hbm is None else f"{hbm / algo:.3f}"
+        lines.append(f"| `{n}` | {c} | {us:.2f} | {'' if f is None else f'{f:.1f}'} | "
+                     f"{'' if w is None else f'{w:.1f}'} | {'' if hbm is None else f'{hbm:.0f}'} | {ratio} |")
+    lines += ["", f"Algorithmic bytes per step: {algo} (each logit, history id and mask word read once, "
+              "u and the token).", ""]
+    lines += ["Bench line of the stats run (timings perturbed by the tracer):", "",
+              "    " + json.dumps({k: bench[k] for k in ("value", "ms_per_step")} |
+                                    {"kernel_us": bench["config"]["kernel_us"],
+                                     "ceiling_us": bench["roofline"].get("ceiling_us")}), ""]
+    a.out.mkdir(parents=True, exist_ok=True)
+    kernels = []
+    for n, *_ in table:
+        base = n.split("<")[0]
+        if base not in kernels and base != "k_read_probe":
+            kernels.append(base)
+    md = a.out / f"{'_'.join(sorted(kernels, key=lambda k: (k != sk, k)))}_cfg{cfg}_profile.md"
+    md.write_text("\n".join(lines))
+    if main_row is not None:
+        js = {"kernel": sk, "workload": f"cfg{cfg}", "kernel_name": main_row[0],
+              "fetch_kib": main_row[3], "write_kib": main_row[4], "fetch_scale": fs, "write_scale": ws,
+              "hbm_bytes_per_launch": main_row[5], "algorithmic_bytes": algo, "avg_us": main_row[2],
+              "source": f"profiles/{md.name}"}
+        (a.out / f"{sk}_cfg{cfg}_traffic.json").write_text(json.dumps(js, indent=1) + "\n")
+    print(md)
+
+
+if __name__ == "__main__":
+    main()

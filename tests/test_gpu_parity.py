@@ -164,16 +164,18 @@ def test_uniform_edges(sampler, wl, kernel_mode):
     compare_rows(w, g)
 
 
-def test_u_on_and_beside_cdf_boundaries(sampler, wl, kernel_mode):
+@pytest.mark.parametrize("k", [20, 300])
+def test_u_on_and_beside_cdf_boundaries(sampler, wl, k, kernel_mode):
     """u placed exactly on, and 1e-12 either side of, interior partial sums
     of the reference's CDF (double sum S of the kept p in index order,
     q = p / S, sequential partial sums): the finalize must leave its tree
     fast path for the reference's sequential sums there, so every token must
-    match exactly (no CDF_NEAR tolerance)."""
+    match exactly (no CDF_NEAR tolerance). k = 20 takes the one-wave
+    finalize, k = 300 the block finalize of the general merge."""
     rng = np.random.default_rng(123)
     V = 151936
     base = rng.normal(0, 1.5, size=(1, V)).astype(np.float32)
-    params = wl.identity_params(top_k=20, temperature=0.9)
+    params = wl.identity_params(top_k=k, temperature=0.9)
     probe = _wl_from(wl, base, [params], [0.5])
     tr = O.sample_row(probe.logits_f32()[0], params, hist=None, mask=None, bias=None, u=0.5)
     p = tr.kept_prob.astype(np.float64)
@@ -185,13 +187,31 @@ def test_u_on_and_beside_cdf_boundaries(sampler, wl, kernel_mode):
         acc += v / S
         cp.append(acc)
     us = []
-    for j in (0, 3, 9, 15):
+    for j in (0, 3, 9, 15) + ((100, 250, len(cp) - 2) if k > 64 else ()):
         for d in (0.0, 1e-12, -1e-12):
             us.append(min(max(cp[j] + d, 0.0), 1.0 - 2.0**-53))
     B = len(us)
     w = _wl_from(wl, np.repeat(base, B, axis=0), [params] * B, us)
     g = run_gpu(sampler, w)
     # the fallback replays the reference's sums: every token matches exactly
+    assert compare_rows(w, g, strict_token=True) == B
+
+
+@pytest.mark.parametrize("k,top_p,min_p,sigma", [(1000, 0.5, 0.0, 0.01), (900, 0.97, 0.0, 0.3),
+                                                 (700, 1.0, 0.9, 0.02), (1024, 0.8, 0.5, 0.05)])
+def test_general_finalize_long_sums(sampler, wl, k, top_p, min_p, sigma):
+    """Rows with hundreds of near-equal probabilities through the block
+    finalize (k > 64): the index-order softmax sum and the top-p running sum
+    over up to 1024 values are the reference's sequential float sums, exact
+    to the bit, and the cut falls where the reference's does."""
+    rng = np.random.default_rng(k)
+    V = 151936
+    B = 8
+    x = rng.normal(0, sigma, size=(B, V)).astype(np.float32)
+    params = [wl.identity_params(top_k=k, top_p=top_p, min_p=min_p, temperature=1.0) for _ in range(B)]
+    us = list(rng.random(B))
+    w = _wl_from(wl, x, params, us)
+    g = run_gpu(sampler, w)
     assert compare_rows(w, g, strict_token=True) == B
 
 

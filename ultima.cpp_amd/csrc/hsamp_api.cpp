@@ -382,7 +382,12 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     if ((uint64_t)(B + 2) * (uint64_t)S * (uint64_t)(S + kXcds) >= (1ull << 32)) return ULTIMA_HSAMP_ERR_CAPACITY;
     rp.S = S;
     rp.slice_len = slice_len;
-    const int buf_cap = std::max(512, next_pow2(2 * kmax));
+    // k_merge's LDS candidate buffer: room for 2k (k <= 64), for 4k up to
+    // 4096 entries above (each compaction keeps k of them; the general
+    // merge's register budget allows two blocks per CU, so LDS is not what
+    // limits it)
+    const int buf_cap = kmax > 64 ? std::min(4096, std::max(512, next_pow2(4 * kmax)))
+                                  : std::max(512, next_pow2(2 * kmax));
     const int cand_cap = slice_len;                 // a slice's list holds all its ids
     const int bitmap_words = slice_len / 32;
     rp.buf_cap = buf_cap;
@@ -394,7 +399,9 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     if (rp.lds + statik > dc.lds_limit) return ULTIMA_HSAMP_ERR_CAPACITY;
     // k_merge: [penalty table | finalize scratch] [candidate buffer]; the
     // table (load factor <= 1/2) moves to global memory when it does not fit.
-    const size_t regionF = 8 * (size_t)next_pow2(kmax) + 20 * (size_t)kmax;
+    // (the finalize's ids, values and probabilities, 4 B each, and keep flags,
+    // 1 B, where the penalty table was; its sort keys use the buffer)
+    const size_t regionF = 12 * (size_t)kmax + align16((size_t)kmax);
     const int mhash = bl.any_pen ? std::max(16, next_pow2(2 * bl.max_pen)) : 16;
     rp.mhash = mhash;
     const size_t lds_budget = std::min<size_t>(dc.lds_limit, 64 * 1024) - statik;

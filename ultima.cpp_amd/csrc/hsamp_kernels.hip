@@ -91,6 +91,7 @@ struct Shared {
     int cutoff;
     double dS;
     double dred[4];
+    double hat, hbefore;   // general finalize: the draw's hit (tree sums) and the sum before it
     int tok;
 };
 
@@ -377,23 +378,31 @@ __device__ void drain_overflow(u64* buf, int cap, int k, const u64* ovf, Shared&
     append_fetch(buf, cap, k, n - cap, [&](int j) { return ovf[j]; }, st);
 }
 
+// Bitonic sort of P (a power of two) keys in LDS by the block. Thread t takes
+// compare-exchange pairs t, t + kBlock, ...; a pair of stage j joins entry i
+// (bit j clear) with i | j. For j <= 64 the pairs of one wave stay inside its
+// own 128-entry blocks, so consecutive such stages need only the wave's own
+// ordering; block barriers surround the stages with j >= 128.
 __device__ __attribute__((noinline)) void bitonic_sort(u64* a, int P, bool descending) {
+    const int half = P >> 1;
     for (int k = 2; k <= P; k <<= 1) {
         for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int i = threadIdx.x; i < P; i += kBlock) {
-                const int ixj = i ^ j;
-                if (ixj > i) {
-                    const u64 x = a[i], y = a[ixj];
-                    const bool up = ((i & k) == 0) != descending;
-                    if ((x > y) == up) {
-                        a[i] = y;
-                        a[ixj] = x;
-                    }
+            for (int t = threadIdx.x; t < half; t += kBlock) {
+                const int i = ((t & ~(j - 1)) << 1) | (t & (j - 1));
+                const int l = i | j;
+                const u64 x = a[i], y = a[l];
+                const bool up = ((i & k) == 0) != descending;
+                if ((x > y) == up) {
+                    a[i] = y;
+                    a[l] = x;
                 }
             }
-            __syncthreads();
+            const int jn = j > 1 ? j >> 1 : (2 * k <= P ? k : 0);   // the next stage's j (0: done)
+            if (j >= 128 || jn >= 128 || jn == 0) __syncthreads();
+            else wave_sync();
         }
     }
+    if (P < 2) __syncthreads();
 }
 
 __device__ __forceinline__ int next_pow2(int x) {
@@ -530,16 +539,78 @@ __device__ __forceinline__ float elem(const uint4& r, int c) {
 // ---- finalize over the kept set ------------------------------------------------
 
 struct FinLds {
-    u64* sortk;     // [P2]; also the double q_i
+    u64* sortk;     // [P2] sort keys, then the double q_i (k_merge: the candidate buffer itself)
     int32_t* fidx;  // [kmax] kept ids, index order
     float* fv;      // values (post-temperature)
-    float* fe;      // expf(v - m)
-    float* fp;      // probabilities
-    int32_t* keep;  // still kept
+    float* fe;      // expf(v - m), replaced in place by the probabilities
+    float* fp;      // probabilities (the same storage as fe)
+    uint8_t* keep;  // still kept
 };
 
+// Exclusive block scan of one double per thread (tree association: only for
+// decisions taken with a margin); *total gets the block sum.
+__device__ __forceinline__ double block_excl_scan_d(double v, double* total, Shared& st) {
+    const double incl = wave_tree_prefix_d(v);
+    if (lane_id() == 63) st.dred[wave_id()] = incl;
+    __syncthreads();
+    double base = 0.0, tot = 0.0;
+#pragma unroll
+    for (int i = 0; i < kBlock / 64; ++i) {
+        const double x = st.dred[i];
+        base += (i < wave_id()) ? x : 0.0;
+        tot += x;
+    }
+    __syncthreads();
+    *total = tot;
+    return base + incl - v;
+}
+
+// The reference's sequential float sum of v(i) over i < n, the same additions
+// in the same order, by one wave: lane l holds entries [16 l, 16 l + 16) of
+// each 1024-entry round, loaded together, and the running sum passes through
+// them by readlane (only the additions are sequential). With thr_on, stops at
+// the first entry after which the sum reaches thr and returns its position
+// (else -1); *sum gets the sum there (or the whole sum).
+template <class Val>
+__device__ int wave_seq_sum_f(int n, Val v, bool thr_on, float thr, float* sum) {
+    const int lane = lane_id();
+    float s = 0.0f;
+    for (int c = 0; c < n; c += 1024) {
+        float x[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int i = c + lane * 16 + j;
+            x[j] = i < n ? v(i) : 0.0f;
+        }
+        const int lanes = min(64, (n - c + 15) >> 4);
+        for (int l = 0; l < lanes; ++l) {
+            float t[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) t[j] = readlane_f(x[j], l);
+            const float s0 = s;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) s = s + t[j];
+            if (thr_on && s >= thr) {
+                // the first entry of these 16 after which the sum reaches thr
+                float s2 = s0;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    s2 = s2 + t[j];
+                    if (s2 >= thr) {
+                        *sum = s2;
+                        return c + l * 16 + j;
+                    }
+                }
+            }
+        }
+    }
+    *sum = s;
+    return -1;
+}
+
 // softmax_probs over the kept entries (sampler.cpp:124-142): m, e, float
-// index-order sum, p = e * fl(1/sum). Returns false when nothing is kept.
+// index-order sum (exact, on wave 0), p = e * fl(1/sum). Returns false when
+// nothing is kept.
 __device__ __attribute__((noinline)) bool fin_softmax(FinLds f, int nk, Shared& st) {
     const int tid = threadIdx.x;
     float m = -__builtin_inff();
@@ -549,12 +620,14 @@ __device__ __attribute__((noinline)) bool fin_softmax(FinLds f, int nk, Shared& 
     if (m == -__builtin_inff()) return false;
     for (int j = tid; j < nk; j += kBlock) f.fe[j] = f.keep[j] ? libm_expf_t(f.fv[j] - m, st.expT) : 0.0f;
     __syncthreads();
-    if (tid == 0) {
-        float s = 0.0f;
-        for (int j = 0; j < nk; ++j)
-            if (f.keep[j]) s = s + f.fe[j];
-        st.sm_inv = (s <= 0.0f) ? __builtin_nanf("") : 1.0f / s;
-        st.sm_m = s;
+    if (tid < 64) {
+        // (entries not kept hold +0, which leaves a sum of values >= 0 unchanged)
+        float s;
+        wave_seq_sum_f(nk, [&](int i) { return f.fe[i]; }, false, 0.0f, &s);
+        if (tid == 0) {
+            st.sm_inv = (s <= 0.0f) ? __builtin_nanf("") : 1.0f / s;
+            st.sm_m = s;
+        }
     }
     __syncthreads();
     const float s = st.sm_m, inv = st.sm_inv;
@@ -598,6 +671,7 @@ __device__ __attribute__((noinline)) void finalize_row(const StreamArgs& a, cons
             f.sortk[i] = (i < nk) ? (((u64)(uint32_t)comp_idx(buf[i]) << 32) | (buf[i] >> 32)) : ~0ull;
         __syncthreads();
         bitonic_sort(f.sortk, P2, false);
+        HSAMP_PHASE(9500 + r, 6);
         for (int j = tid; j < nk; j += kBlock) {
             const u64 e = f.sortk[j];
             f.fidx[j] = (int32_t)(e >> 32);
@@ -612,6 +686,7 @@ __device__ __attribute__((noinline)) void finalize_row(const StreamArgs& a, cons
         if (a.topk_count != nullptr && tid == 0) a.topk_count[r] = single ? -1 : nk;
 
         bool have = fin_softmax(f, nk, st);
+        HSAMP_PHASE(9500 + r, 7);
         bool fresh = true;  // fp matches the current kept set
         if (have && (P.flags & RF_TOPP)) {
             // sampler.cpp:146-164
@@ -621,22 +696,23 @@ __device__ __attribute__((noinline)) void finalize_row(const StreamArgs& a, cons
                                  : 0ull;
             __syncthreads();
             bitonic_sort(f.sortk, P2, true);
-            if (tid == 0) {
-                float c = 0.0f;
-                int cutoff = -1;
-                for (int i = 0; i < nk; ++i) {
-                    const u64 e = f.sortk[i];
-                    if (e == 0ull) break;
-                    const int j = (int)(0xFFFFFFFFu - (uint32_t)e);
-                    c = c + f.fp[j];
-                    if (c >= P.top_p) {
-                        cutoff = i + 1;
-                        break;
-                    }
+            if (tid < 64) {
+                // the running float sum in that order (entries not kept sort
+                // last as 0 and add +0)
+                float c;
+                const int hit = wave_seq_sum_f(
+                    nk,
+                    [&](int i) {
+                        const u64 e = f.sortk[i];
+                        return e == 0ull ? 0.0f : f.fp[(int)(0xFFFFFFFFu - (uint32_t)e)];
+                    },
+                    true, P.top_p, &c);
+                const int cutoff = hit >= 0 ? hit + 1 : -1;
+                if (tid == 0) {
+                    if (cutoff > 0 && fabsf(c - P.top_p) <= 1e-6f) rflags |= ROWF_TOPP_NEAR;
+                    st.cutoff = cutoff;
+                    st.flags = (int)rflags;
                 }
-                if (cutoff > 0 && fabsf(c - P.top_p) <= 1e-6f) rflags |= ROWF_TOPP_NEAR;
-                st.cutoff = cutoff;
-                st.flags = (int)rflags;
             }
             __syncthreads();
             rflags = (uint32_t)st.flags;
@@ -650,6 +726,7 @@ __device__ __attribute__((noinline)) void finalize_row(const StreamArgs& a, cons
                 fresh = false;
             }
         }
+        HSAMP_PHASE(9500 + r, 8);
         if (have && (P.flags & RF_MINP)) {
             // sampler.cpp:167-176
             if (!fresh) have = fin_softmax(f, nk, st);
@@ -672,27 +749,83 @@ __device__ __attribute__((noinline)) void finalize_row(const StreamArgs& a, cons
             }
         }
         if (have && !fresh) have = fin_softmax(f, nk, st);
+        HSAMP_PHASE(9500 + r, 9);
         if (have) {
-            // sampler.cpp:178-182 / discrete_distribution: double sum, q, partial sums.
-            double* fq = reinterpret_cast<double*>(f.sortk);
-            if (tid == 0) {
-                double S = 0.0;
-                for (int j = 0; j < nk; ++j)
-                    if (f.keep[j]) S = S + (double)f.fp[j];
-                st.dS = S;
+            // sampler.cpp:178-182 / discrete_distribution: double sum S, q = p / S,
+            // partial sums of q (cp[V-1] = 1), the first cp >= u. A tree prefix
+            // of p over its tree total decides when every comparison that
+            // decides the token and the CDF_NEAR flag is clear of u by 2e-6
+            // (for <= 1024 terms the tree and the sequential sums, quotients
+            // and partial sums differ by < 1e-12); otherwise the reference's
+            // sequential sums on one thread.
+            bool decided = false;
+            if (single || !(u > 0.0)) {
+                if (tid == 0) {
+                    st.tok = 0;
+                    st.flags = (int)rflags;
+                }
+                decided = true;
+            } else if (nk <= 4 * kBlock) {
+                double pd[4], c4[4], run = 0.0;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int j = 4 * tid + q;
+                    pd[q] = (j < nk && f.keep[j]) ? (double)f.fp[j] : 0.0;
+                    run = run + pd[q];
+                    c4[q] = run;
+                }
+                if (tid == 0) st.tok = INT32_MAX;
+                double tot;
+                const double base = block_excl_scan_d(run, &tot, st);   // (its barriers publish st.tok)
+                int hit = INT32_MAX;
+                double at = 0.0, before = 0.0;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int j = 4 * tid + q;
+                    if (hit == INT32_MAX && j < nk && f.keep[j]) {
+                        const double cp = (base + c4[q]) / tot;
+                        const double cj = (f.fidx[j] == V - 1) ? 1.0 : cp;
+                        if (cj >= u) {
+                            hit = j;
+                            at = cj;
+                            before = (base + c4[q] - pd[q]) / tot;
+                        }
+                    }
+                }
+                if (hit != INT32_MAX) atomicMin(&st.tok, hit);
+                __syncthreads();
+                const int h0 = st.tok;
+                if (hit != INT32_MAX && hit == h0) {
+                    st.hat = at;
+                    st.hbefore = before;
+                }
+                __syncthreads();
+                const bool clear = (h0 != INT32_MAX) ? (fabs(st.hat - u) > 2e-6 && fabs(st.hbefore - u) > 2e-6)
+                                                     : fabs(1.0 - u) > 2e-6;
+                if (clear) {
+                    decided = true;
+                    __syncthreads();   // every thread has read st.tok / st.hat
+                    if (tid == 0) {
+                        st.tok = (h0 != INT32_MAX) ? f.fidx[h0] : V - 1;
+                        st.flags = (int)rflags;
+                    }
+                }
             }
-            __syncthreads();
-            const double S = st.dS;
-            for (int j = tid; j < nk; j += kBlock) fq[j] = f.keep[j] ? (double)f.fp[j] / S : 0.0;
-            __syncthreads();
-            if (tid == 0) {
-                int32_t t = V - 1;
-                double near = 1.0;
-                if (single) {
-                    t = 0;
-                } else if (!(u > 0.0)) {
-                    t = 0;
-                } else {
+            if (!decided) {
+                double* fq = reinterpret_cast<double*>(f.sortk);
+                if (tid == 0) {
+                    double S = 0.0;
+                    for (int j = 0; j < nk; ++j)
+                        if (f.keep[j]) S = S + (double)f.fp[j];
+                    st.dS = S;
+                }
+                __syncthreads();
+                const double S = st.dS;
+                for (int j = tid; j < nk; j += kBlock) fq[j] = f.keep[j] ? (double)f.fp[j] / S : 0.0;
+                __syncthreads();
+                if (tid == 0) {
+                    int32_t t = V - 1;
+                    double near = 1.0;
                     double cp = 0.0, prev = 0.0;
                     bool found = false;
                     for (int j = 0; j < nk; ++j) {
@@ -708,10 +841,10 @@ __device__ __attribute__((noinline)) void finalize_row(const StreamArgs& a, cons
                         }
                     }
                     if (!found) near = fmin(fabs(1.0 - u), fabs(cp - u));
+                    if (near <= 1e-6) rflags |= ROWF_CDF_NEAR;
+                    st.tok = t;
+                    st.flags = (int)rflags;
                 }
-                if (near <= 1e-6) rflags |= ROWF_CDF_NEAR;
-                st.tok = t;
-                st.flags = (int)rflags;
             }
             __syncthreads();
             tok = st.tok;
@@ -719,6 +852,7 @@ __device__ __attribute__((noinline)) void finalize_row(const StreamArgs& a, cons
         } else {
             nkept = 0;
         }
+        HSAMP_PHASE(9500 + r, 10);
         if (have) {
             // kept ids in index order: one scan per 256 positions
             int running = 0;
@@ -753,6 +887,7 @@ __device__ __attribute__((noinline)) void finalize_row(const StreamArgs& a, cons
         if (a.kept_count != nullptr) a.kept_count[r] = nkept;
         if (a.fin_n != nullptr) a.fin_n[r] = nkept;
     }
+    HSAMP_PHASE(9500 + r, 11);
 }
 
 
@@ -1169,6 +1304,7 @@ __device__ __attribute__((noinline)) void select_and_finalize(const StreamArgs& 
         return;
     }
     buf_compact(buf, k, st);
+    HSAMP_PHASE(9500 + r, 5);
     finalize_row(a, P, r, buf, st.n, f, st, rflags);
 }
 
@@ -1428,11 +1564,16 @@ __device__ __forceinline__ void stream_sample(const StreamArgs& a, const RowPlan
     const bool pflag = a.pen_flag != 0;
     const float inv_t = pflag ? 1.0f : P.inv_temp;
     bool nanseen = false;
+    // Group maxima over every tile so far: each group's maximum is a distinct
+    // id of the slice, so the kw-th largest of them bounds the slice's k-th
+    // key from below, and the bound tightens as tiles go by (a bound from the
+    // current tile alone would let each tile add about k candidates).
+    uint32_t gk[4] = {0u, 0u, 0u, 0u};
     auto process = [&](const uint4 (&raw)[T::NCH], int tb) {
         uint32_t kv[T::NE];
         uint32_t pm;
         tile_keys<DT, PEN, MASK, false>(raw, tb, lo, hi, pbm, mbm, inv_t, pflag, kv, pm, nanseen);
-        uint32_t gk[4] = {0u, 0u, 0u, 0u}, lm = 0u;
+        uint32_t lm = 0u;
 #pragma unroll
         for (int j = 0; j < T::NCH; ++j) {
 #pragma unroll
@@ -1442,13 +1583,14 @@ __device__ __forceinline__ void stream_sample(const StreamArgs& a, const RowPlan
                 lm = max(lm, kv[i]);
             }
         }
+        uint32_t gb[4] = {gk[0], gk[1], gk[2], gk[3]};
         if (G == 2) {
-            gk[0] = max(gk[0], gk[1]);
-            gk[1] = max(gk[2], gk[3]);
+            gb[0] = max(gk[0], gk[1]);
+            gb[1] = max(gk[2], gk[3]);
         } else if (G == 1) {
-            gk[0] = max(max(gk[0], gk[1]), max(gk[2], gk[3]));
+            gb[0] = max(max(gk[0], gk[1]), max(gk[2], gk[3]));
         }
-        const uint32_t tw = (kw <= 64 * G) ? wave_kth_bound16(gk, G, kw) : 0u;
+        const uint32_t tw = (kw <= 64 * G) ? wave_kth_bound16(gb, G, kw) : 0u;
         if (lane_id() == 0) st.twave[wave_id()] = tw;
         __syncthreads();
         uint32_t tt = st.twave[0];
@@ -2838,10 +2980,12 @@ __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
         return;
     }
     if (tid == 0) st.u = ur;
+    HSAMP_PHASE(9500 + r, 0);
     // LDS: [row penalty table | finalize scratch] aliased, then the buffer.
     const PenaltyLds pl = pen_table<GT>(a, r, smem);
     if (pen) pen_build_row(a, P, r, pl, pre);   // its barriers publish the counts too
     else __syncthreads();
+    HSAMP_PHASE(9500 + r, 1);
     u64* buf = reinterpret_cast<u64*>(smem + (a.merge_lds - (uint32_t)a.buf_cap * 8u));
     u64* ovf = a.ovf + (int64_t)r * a.ovf_cap;
     u64 best = 0ull;   // greedy
@@ -2893,6 +3037,7 @@ __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
         }
     }
 
+    HSAMP_PHASE(9500 + r, 2);
     // the ragged end, unless penalised
     u64 ct = 0ull;
     if (tail_t >= 0) {
@@ -2941,6 +3086,7 @@ __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
         offer_regs<1>(buf, ovf, a.buf_cap, k, c1, st);
     }
     offer_regs<NW>(buf, ovf, a.buf_cap, k, win, st);
+    HSAMP_PHASE(9500 + r, 3);
     if (extra > 0) {
         for (int sl = 0; sl < S; ++sl) {
             const int n = st.soff[sl];
@@ -2956,15 +3102,17 @@ __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
         }
     }
     __syncthreads();
+    HSAMP_PHASE(9500 + r, 4);
     const uint32_t rflags = (st.flags & 4) ? ROWF_NAN : 0u;
-    const int kP2 = next_pow2(max(a.kmax, 1));
+    // the finalize scratch: sort keys in the candidate buffer (each entry is
+    // read into its key in place), the rest where the penalty table was
     FinLds f;
-    f.sortk = reinterpret_cast<u64*>(smem);
-    f.fidx = reinterpret_cast<int32_t*>(f.sortk + kP2);
+    f.sortk = buf;
+    f.fidx = reinterpret_cast<int32_t*>(smem);
     f.fv = reinterpret_cast<float*>(f.fidx + a.kmax);
     f.fe = f.fv + a.kmax;
-    f.fp = f.fe + a.kmax;
-    f.keep = reinterpret_cast<int32_t*>(f.fp + a.kmax);
+    f.fp = f.fe;
+    f.keep = reinterpret_cast<uint8_t*>(f.fe + a.kmax);
     select_and_finalize(sa, sP, r, buf, f, st, rflags);
 }
 

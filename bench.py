@@ -54,6 +54,11 @@ def parse():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--workload", default="sampler", choices=["sampler", "head"],
+                    help="head: the logits producer (final rmsnorm + lm-head matvec) and the "
+                         "producer + sampler step instead of the sampler alone")
+    ap.add_argument("--head-rows", type=int, default=1, help="head workload: hidden-state rows per step")
+    ap.add_argument("--head-hidden", type=int, default=4096, help="head workload: hidden size H")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-reps", type=int, default=7, help="timed repetitions of each CPU leg (median)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -182,6 +187,119 @@ class Timer:
         self.graphs.clear()
 
 
+def head_main(args):
+    """The logits producer: rows hidden states [rows, H] -> rmsnorm -> lm-head
+    matvec with a bf16 [V, H] head (V = 151936, random weights) -> logits
+    [rows, V] in device memory, then the same step followed by sampling
+    (configuration 1's knobs). One JSON line; the roofline is the producer's
+    (HBM-bound: the head's weights once per step)."""
+    import torch
+    import __graft_entry__ as ge
+    pkg = ge.load_package()
+    hs = pkg.hsamp
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    rows, H, V = args.head_rows, args.head_hidden, 151936
+    g = torch.Generator(device=dev).manual_seed(5)
+    n_sets = 2                                      # two heads of 1.24 GB: no cache reuse between steps
+    heads = [(torch.randn((V, H), generator=g, device=dev) * 0.02).to(torch.bfloat16) for _ in range(n_sets)]
+    hidden = [torch.randn((rows, H), generator=g, device=dev) * 2.0 for _ in range(n_sets)]
+    scale = torch.ones(H, device=dev) + 0.1 * torch.randn(H, generator=g, device=dev)
+    logits = torch.empty((rows, V), dtype=torch.float32, device=dev)
+    normed = torch.empty((rows, H), dtype=torch.float32, device=dev)
+    sampler = hs.Sampler(0, max_rows=max(rows, 64), max_vocab=V)
+    params = [dict(pkg.workloads.identity_params(temperature=0.8, top_k=40, top_p=0.95, rep_penalty=1.0))
+              for _ in range(rows)]
+    u = torch.full((rows,), 0.37, dtype=torch.float64, device=dev)
+    outs = {"token": torch.empty(rows, dtype=torch.int32, device=dev),
+            "row_flags": torch.empty(rows, dtype=torch.int32, device=dev)}
+    stream = torch.cuda.Stream(dev)
+
+    def head(i, s):
+        hs.lm_head(hidden[i % n_sets], scale, 1e-6, heads[i % n_sets], 1.0, logits, normed, stream=s)
+
+    def step(i, s):
+        head(i, s)
+        sampler.run(logits, params, u, outputs=outs, stream=s)
+
+    def timed(fn, steps, warmup):
+        with torch.cuda.stream(stream):
+            for i in range(n_sets):
+                fn(i, stream)
+        stream.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr, stream=stream):
+            for i in range(n_sets):
+                fn(i, stream)
+        stream.synchronize()
+        reps = max(1, steps // n_sets)
+        for _ in range(max(1, warmup // n_sets)):
+            gr.replay()
+        stream.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            e0.record(stream)
+            for _ in range(reps):
+                gr.replay()
+            e1.record(stream)
+        stream.synchronize()
+        return e0.elapsed_time(e1) / (reps * n_sets), reps * n_sets
+
+    steps = min(args.steps, 400)
+    head_ms, n_head = timed(head, steps, args.warmup)
+    step_ms, n_step = timed(step, steps, args.warmup)
+    algo = V * H * 2 + rows * (2 * H * 4 + V * 4) + H * 4
+    achieved = algo / (head_ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle as O
+        from concurrent.futures import ThreadPoolExecutor
+        kind = "reference" if O.ref_kernels_available() else "port"
+        threads = host_threads()
+        wcpu = heads[0][:V].view(torch.int16).cpu().numpy().view(np.uint16)
+        x = O.rmsnorm(hidden[0][0].cpu().numpy(), scale.cpu().numpy(), 1e-6, use_ref=kind == "reference")
+        bounds = np.linspace(0, V, threads + 1).astype(int)
+
+        def part(j):
+            return O.matvec(wcpu[bounds[j]:bounds[j + 1]], x, use_ref=kind == "reference")
+
+        with ThreadPoolExecutor(threads) as ex:
+            list(ex.map(part, range(threads)))                      # warm-up
+            ts = []
+            for _ in range(max(3, args.cpu_reps)):
+                t0 = time.perf_counter()
+                list(ex.map(part, range(threads)))
+                ts.append(time.perf_counter() - t0)
+        sec = statistics.median(ts)
+        cpu = {"value": 1.0 / sec, "unit": "logit rows/s", "cores": threads, "kind": kind,
+               "sample": f"one row of the {V}x{H} bf16 head (the matvec; rmsnorm excluded), rows split "
+                         f"over {threads} threads, median of {len(ts)}"}
+    sampler.close()
+    line = {
+        "metric": f"logit rows/sec of the final rmsnorm + lm-head (H={H}, V={V} bf16 head); achieved HBM GB/s vs peak",
+        "value": rows / (head_ms * 1e-3),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": n_head,
+        "warmup": args.warmup,
+        "ms_per_step": head_ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 weights, f32 arithmetic",
+        "data": "synthetic (random head weights and hidden states, 2 rotating heads of 1.24 GB)",
+        "config": {"workload": f"head: rows={rows} H={H} V={V} bf16, then configuration-1 sampling",
+                   "rows": rows, "hidden": H, "vocab": V, "bytes_per_step": algo,
+                   "head_and_sample_us": round(step_ms * 1e3, 3), "head_and_sample_steps": n_step},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / PEAK_GBS, "traffic": None, "traffic_source": None,
+                     "kernel": "k_head_gemv", "algorithmic_bytes_per_launch": algo},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -189,6 +307,9 @@ def main():
               "(rows shard across GPUs with no exchange: the figure is N x the 1-GPU value).",
               file=sys.stderr)
         sys.exit(2)
+    if args.workload == "head":
+        head_main(args)
+        return
     import torch
     import __graft_entry__ as ge
     pkg = ge.load_package()

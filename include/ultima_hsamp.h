@@ -204,6 +204,42 @@ int ultima_hsamp_read_probe(ultima_hsamp* h, const ultima_hsamp_batch* batch, fl
  * the two kernels apart with its own events. NULL stops it. */
 int ultima_hsamp_set_phase_event(ultima_hsamp* h, void* hip_event);
 
+/* ---- The logits producer ----------------------------------------------------
+ * The model's last step before sampling, on the device: each row's final
+ * hidden state through the output rmsnorm and the lm-head matvec, written as
+ * the [rows, vocab] f32 logits that ultima_hsamp_run() samples, with no host
+ * round trip. Replaces, per token row, the reference's
+ *   kernels::rmsnorm_f32(last, output_norm, x_norm, hidden, rms_eps)
+ *   matvec_dispatch_threaded(pool, head.dtype, head.data, x_norm, out_logits, vocab, hidden)
+ *   out_logits[i] *= 1 / logit_scale            (when logit_scale is neither 1 nor 0)
+ *     /root/reference/src/model/qwen_model.cpp:182-207,
+ *     /root/reference/src/model/weight_dispatch.cpp:106-146 (F32 and BF16 heads),
+ *     /root/reference/src/kernels/rmsnorm.cpp:21-52, matvec_f32_f32.cpp:22-50,
+ *     matvec_bf16_f32.cpp:48-68.
+ * The results are the reference's bits: every sum runs in the order of its
+ * AVX2 kernels (eight fused multiply-add partials, their horizontal sum, the
+ * n % 8 tail). Quantised heads (Q4_K, Q6_K, Q8_0, ...) and the Hadamard fold
+ * are not built. All pointers are device memory. */
+typedef struct ultima_hsamp_head {
+    const float* hidden;        /* [rows, hidden_stride] final hidden states */
+    int64_t hidden_stride;      /* elements between rows, >= hidden_dim */
+    int32_t rows;               /* >= 1 */
+    int32_t hidden_dim;         /* H >= 1 */
+    int32_t vocab;              /* V >= 1 */
+    int32_t weight_dtype;       /* ULTIMA_HSAMP_F32 or ULTIMA_HSAMP_BF16 */
+    const float* norm_scale;    /* [H] output-norm weights */
+    float eps;                  /* rms epsilon */
+    float logit_scale;          /* logits are multiplied by 1 / logit_scale unless it is 1 or 0 */
+    const void* weight;         /* [V, H] row-major head weights (f32, or bf16 bit patterns) */
+    float* normed;              /* [rows, H] scratch: the normed rows (left there) */
+    float* logits;              /* [rows, logits_stride] output */
+    int64_t logits_stride;      /* elements between rows, >= V */
+} ultima_hsamp_head;
+
+/* Runs the head for every row on hip_stream (NULL = the default stream).
+ * Allocates nothing. */
+int ultima_hsamp_lm_head(const ultima_hsamp_head* head, void* hip_stream);
+
 #ifdef __cplusplus
 }
 #endif

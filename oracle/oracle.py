@@ -296,3 +296,96 @@ def ref_sample_batch(logits_f32: np.ndarray, plist, hist, hist_len, seeds, nthre
                        ctypes.cast(pa, ctypes.c_void_p), _ptr(hist), hist.strides[0] // 4, _ptr(hl),
                        _ptr(sd), _ptr(toks), nthreads)
     return toks
+
+
+# ---- the logits producer (final rmsnorm + lm-head matvec) ---------------------------
+
+HEAD_SO = HERE / "liborc_head.so"
+REF_KERNELS_SO = HERE / "_ref" / "libref_kernels.so"
+_head = None
+_refk = None
+
+
+def head_lib():
+    """liborc_head.so: head_oracle.c, the restatement of the reference's AVX2
+    rmsnorm and matvec order."""
+    global _head
+    if _head is None:
+        if not HEAD_SO.exists():
+            raise RuntimeError(f"{HEAD_SO} is not built (run __graft_entry__.build())")
+        L = ctypes.CDLL(str(HEAD_SO))
+        vp, i64, f32, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_float, ctypes.c_int
+        L.orc_rmsnorm.restype = None
+        L.orc_rmsnorm.argtypes = [vp, vp, vp, i64, f32]
+        L.orc_matvec_f32.restype = None
+        L.orc_matvec_f32.argtypes = [vp, vp, vp, i64, i64]
+        L.orc_matvec_bf16.restype = None
+        L.orc_matvec_bf16.argtypes = [vp, vp, vp, i64, i64]
+        L.orc_lm_head.restype = None
+        L.orc_lm_head.argtypes = [vp, i64, i64, vp, f32, vp, i32, i64, f32, vp, vp]
+        _head = L
+    return _head
+
+
+def ref_kernels_available() -> bool:
+    return REF_KERNELS_SO.exists()
+
+
+def ref_kernels():
+    """_ref/libref_kernels.so: the reference's own rmsnorm_f32, matvec_f32_f32
+    and matvec_bf16_f32, compiled from its sources."""
+    global _refk
+    if _refk is None:
+        if not REF_KERNELS_SO.exists():
+            raise RuntimeError(f"{REF_KERNELS_SO} is not built (reference sources absent?)")
+        R = ctypes.CDLL(str(REF_KERNELS_SO))
+        vp, i64, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_float
+        R.ref_rmsnorm.restype = None
+        R.ref_rmsnorm.argtypes = [vp, vp, vp, i64, f32]
+        R.ref_matvec_f32.restype = None
+        R.ref_matvec_f32.argtypes = [vp, vp, vp, i64, i64]
+        R.ref_matvec_bf16.restype = None
+        R.ref_matvec_bf16.argtypes = [vp, vp, vp, i64, i64]
+        _refk = R
+    return _refk
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def rmsnorm(x, scale, eps: float, use_ref: bool = False) -> np.ndarray:
+    x, scale = _f32(x), _f32(scale)
+    y = np.empty_like(x)
+    (ref_kernels().ref_rmsnorm if use_ref else head_lib().orc_rmsnorm)(_ptr(x), _ptr(scale), _ptr(y), x.size, eps)
+    return y
+
+
+def matvec(w, x, use_ref: bool = False) -> np.ndarray:
+    """y = W x in the reference's order; W f32 [M, K] or bf16 bits (uint16) [M, K]."""
+    x = _f32(x)
+    M, K = w.shape
+    y = np.empty(M, np.float32)
+    if w.dtype == np.uint16:
+        w = np.ascontiguousarray(w)
+        fn = ref_kernels().ref_matvec_bf16 if use_ref else head_lib().orc_matvec_bf16
+    else:
+        w = _f32(w)
+        fn = ref_kernels().ref_matvec_f32 if use_ref else head_lib().orc_matvec_f32
+    fn(_ptr(w), _ptr(x), _ptr(y), M, K)
+    return y
+
+
+def lm_head(hidden, norm_scale, eps: float, weight, logit_scale: float = 1.0):
+    """Logits [rows, V] of hidden states [rows, H] (reference
+    src/model/qwen_model.cpp:182-207); also returns the normed rows."""
+    hidden = _f32(np.atleast_2d(hidden))
+    rows, H = hidden.shape
+    V = weight.shape[0]
+    dtype = 1 if weight.dtype == np.uint16 else 0
+    w = np.ascontiguousarray(weight) if dtype else _f32(weight)
+    logits = np.empty((rows, V), np.float32)
+    normed = np.empty((rows, H), np.float32)
+    head_lib().orc_lm_head(_ptr(hidden), rows, H, _ptr(_f32(norm_scale)), eps, _ptr(w), dtype, V,
+                           logit_scale, _ptr(logits), _ptr(normed))
+    return logits, normed

@@ -62,8 +62,9 @@ def build_all() -> None:
         "hsamp_kernels.o": CSRC / "hsamp_kernels.hip",
         "hsamp_api.o": CSRC / "hsamp_api.cpp",
         "hsamp_noalloc.o": CSRC / "hsamp_noalloc.hip",
+        "hsamp_head.o": CSRC / "hsamp_head.hip",
     }
-    with ThreadPoolExecutor(max_workers=3) as ex:
+    with ThreadPoolExecutor(max_workers=4) as ex:
         futs = [ex.submit(_run, [HIPCC, *HIP_FLAGS, "-x", "hip", "-c", str(src), "-o", str(BUILD / o)])
                 for o, src in objs.items()]
         for f in futs:

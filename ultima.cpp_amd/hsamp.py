@@ -73,6 +73,25 @@ class Batch(ctypes.Structure):
     ]
 
 
+class Head(ctypes.Structure):
+    """ultima_hsamp_head (include/ultima_hsamp.h)."""
+    _fields_ = [
+        ("hidden", ctypes.c_void_p),
+        ("hidden_stride", ctypes.c_int64),
+        ("rows", ctypes.c_int32),
+        ("hidden_dim", ctypes.c_int32),
+        ("vocab", ctypes.c_int32),
+        ("weight_dtype", ctypes.c_int32),
+        ("norm_scale", ctypes.c_void_p),
+        ("eps", ctypes.c_float),
+        ("logit_scale", ctypes.c_float),
+        ("weight", ctypes.c_void_p),
+        ("normed", ctypes.c_void_p),
+        ("logits", ctypes.c_void_p),
+        ("logits_stride", ctypes.c_int64),
+    ]
+
+
 def declared_symbols() -> list[str]:
     """Function names declared in include/ultima_hsamp.h."""
     import re
@@ -122,6 +141,8 @@ def lib() -> ctypes.CDLL:
         L.ultima_hsamp_read_probe.argtypes = [vp, ctypes.POINTER(Batch), vp, vp]
         L.ultima_hsamp_set_phase_event.restype = ctypes.c_int
         L.ultima_hsamp_set_phase_event.argtypes = [vp, vp]
+        L.ultima_hsamp_lm_head.restype = ctypes.c_int
+        L.ultima_hsamp_lm_head.argtypes = [ctypes.POINTER(Head), vp]
         _lib = L
     return _lib
 
@@ -222,6 +243,40 @@ def run_noalloc(logits, params, u, hist=None, hist_len=None, mask=None, bias=Non
     check(lib().ultima_hsamp_run_noalloc(ctypes.byref(b), ctypes.c_void_p(s.cuda_stream)), "run_noalloc")
     del keep
     return out
+
+
+def lm_head(hidden, norm_scale, eps: float, weight, logit_scale: float = 1.0, logits=None, normed=None,
+            stream=None):
+    """ultima_hsamp_lm_head on torch tensors of one device: hidden [rows, H] f32,
+    norm_scale [H] f32, weight [V, H] f32 or bf16. Returns (logits [rows, V],
+    normed [rows, H]); the outputs may be passed in (allocated otherwise)."""
+    import torch
+    if hidden.dim() == 1:
+        hidden = hidden.unsqueeze(0)
+    rows, H = hidden.shape
+    V = weight.shape[0]
+    dev = hidden.device
+    if weight.dtype not in (torch.float32, torch.bfloat16):
+        raise HsampError(ERR_INVALID, "lm_head: weight must be float32 or bfloat16")
+    if logits is None:
+        logits = torch.empty((rows, V), dtype=torch.float32, device=dev)
+    if normed is None:
+        normed = torch.empty((rows, H), dtype=torch.float32, device=dev)
+    h = Head()
+    h.hidden = hidden.data_ptr()
+    h.hidden_stride = hidden.stride(0)
+    h.rows, h.hidden_dim, h.vocab = rows, H, V
+    h.weight_dtype = 1 if weight.dtype == torch.bfloat16 else 0
+    h.norm_scale = norm_scale.data_ptr()
+    h.eps = eps
+    h.logit_scale = logit_scale
+    h.weight = weight.data_ptr()
+    h.normed = normed.data_ptr()
+    h.logits = logits.data_ptr()
+    h.logits_stride = logits.stride(0)
+    s = torch.cuda.current_stream(dev) if stream is None else stream
+    check(lib().ultima_hsamp_lm_head(ctypes.byref(h), ctypes.c_void_p(s.cuda_stream)), "lm_head")
+    return logits, normed
 
 
 class Sampler:

@@ -126,14 +126,28 @@ def cpu_baseline(wl, reps: int):
                        **{k: round(v / rows_1 * 1e6, 2) for k, v in st.items()}}}
 
 
-def traffic_from_profiles(kernel: str, cfg: int):
-    f = ROOT / "profiles" / f"{kernel}_cfg{cfg}_traffic.json"
+def traffic_from_profiles(kernel: str, tag: str):
+    """HBM bytes per launch of `kernel` on workload `tag` ("cfg2", "head"), from
+    the calibrated FETCH_SIZE / WRITE_SIZE summary committed under profiles/."""
+    f = ROOT / "profiles" / f"{kernel}_{tag}_traffic.json"
     if f.exists():
         try:
             return json.loads(f.read_text()).get("hbm_bytes_per_launch"), f.name
         except (ValueError, OSError):
             return None, None
     return None, None
+
+
+def copy_probe(torch, dev, mib, line):
+    """A plain device copy of `mib` MiB, three times: the known-size dispatch
+    that calibrates rocprofv3's FETCH_SIZE and WRITE_SIZE counters."""
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    line["config"]["copy_probe_bytes"] = n * 4
 
 
 class Timer:
@@ -276,6 +290,7 @@ def head_main(args):
                "sample": f"one row of the {V}x{H} bf16 head (the matvec; rmsnorm excluded), rows split "
                          f"over {threads} threads, median of {len(ts)}"}
     sampler.close()
+    traffic, traffic_src = traffic_from_profiles("k_head_gemv", "head")
     line = {
         "metric": f"logit rows/sec of the final rmsnorm + lm-head (H={H}, V={V} bf16 head); achieved HBM GB/s vs peak",
         "value": rows / (head_ms * 1e-3),
@@ -291,12 +306,15 @@ def head_main(args):
         "data": "synthetic (random head weights and hidden states, 2 rotating heads of 1.24 GB)",
         "config": {"workload": f"head: rows={rows} H={H} V={V} bf16, then configuration-1 sampling",
                    "rows": rows, "hidden": H, "vocab": V, "bytes_per_step": algo,
-                   "head_and_sample_us": round(step_ms * 1e3, 3), "head_and_sample_steps": n_step},
+                   "head_and_sample_us": round(step_ms * 1e3, 3), "head_and_sample_steps": n_step,
+                   "kernel_us": {"lm_head": round(head_ms * 1e3, 3)}},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / PEAK_GBS, "traffic": None, "traffic_source": None,
+                     "frac": achieved / PEAK_GBS, "traffic": traffic, "traffic_source": traffic_src,
                      "kernel": "k_head_gemv", "algorithmic_bytes_per_launch": algo},
         "cpu_baseline": cpu,
     }
+    if args.copy_probe_mib > 0:
+        copy_probe(torch, dev, args.copy_probe_mib, line)
     print(json.dumps(line), flush=True)
 
 
@@ -425,7 +443,7 @@ def main():
 
     algo_bytes = wl0.algorithmic_bytes()
     achieved = algo_bytes / (stream_ms * 1e-3) / 1e9
-    traffic, traffic_src = traffic_from_profiles(sk, cfg)
+    traffic, traffic_src = traffic_from_profiles(sk, f"cfg{cfg}")
     rk = ROW_KERNEL[cfg]
     kern_us = {sk: round(stream_ms * 1e3, 3)}
     if rk:
@@ -466,13 +484,7 @@ def main():
     if host_row_us is not None:
         line["config"]["host_row_us"] = round(host_row_us, 2)
     if args.copy_probe_mib > 0:
-        n = args.copy_probe_mib * (1 << 20) // 4
-        src = torch.ones(n, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        line["config"]["copy_probe_bytes"] = n * 4
+        copy_probe(torch, dev, args.copy_probe_mib, line)
     sampler.close()
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(wl0, max(5, args.cpu_reps))

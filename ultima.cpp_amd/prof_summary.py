@@ -7,10 +7,10 @@ Inputs are three rocprofv3 output folders of the same bench command:
            M MiB device copy they end with calibrates each counter (bytes it
            must have moved / what the counter reported for it).
 
-Writes <out>/<kernels>_cfg<N>_profile.md (kernel durations, traffic per kernel,
-the commands) and, for the kernel that reads the logits,
-<out>/<kernel>_cfg<N>_traffic.json, which bench.py reads for
-roofline.traffic.
+Writes <out>/<kernels>_<tag>_profile.md (kernel durations, traffic per
+kernel, the commands) and, for the workload's dominant kernel (the one that
+reads the logits, or the lm-head matvec), <out>/<kernel>_<tag>_traffic.json,
+which bench.py reads for roofline.traffic. <tag> is cfg1 .. cfg5, or head.
 
     python3 ultima.cpp_amd/prof_summary.py --config 2 --stats DIR --fetch DIR --write DIR \
         --bench DIR/stats_bench.json --copy-mib 512 --out profiles --command "..."
@@ -25,15 +25,16 @@ from collections import defaultdict
 from pathlib import Path
 
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
-STREAM_KERNEL = {1: "k_stream", 2: "k_stream", 3: "k_full", 4: "k_stream", 5: "k_stream"}
+STREAM_KERNEL = {"cfg1": "k_stream", "cfg2": "k_stream", "cfg3": "k_full", "cfg4": "k_stream", "cfg5": "k_stream",
+                 "head": "k_head_gemv"}
 
 
 def short(name: str) -> str:
     """'void hsamp::k_stream<0, true, ...>(hsamp::StreamArgs)' -> 'k_stream<0, true, ...>'"""
-    n = name.split("(")[0]
-    for p in ("void ", "hsamp::"):
+    n = name
+    for p in ("void ", "hsamp::", "(anonymous namespace)::"):
         n = n.replace(p, "")
-    return n
+    return n.split("(")[0]
 
 
 def one_csv(folder: Path, suffix: str) -> Path:
@@ -57,7 +58,7 @@ def counter(folder: Path) -> dict[str, list[float]]:
 
 def main() -> None:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--config", type=int, required=True)
+    ap.add_argument("--config", required=True, help="1-5 (a sampler configuration) or head")
     ap.add_argument("--stats", type=Path, required=True)
     ap.add_argument("--fetch", type=Path, required=True)
     ap.add_argument("--write", type=Path, required=True)
@@ -85,8 +86,8 @@ def main() -> None:
         hbm = None if f is None or w is None else (f * fs + w * ws) * 1024.0
         table.append((short(name), int(r["Calls"]), float(r["AverageNs"]) / 1000.0, f, w, hbm))
 
-    cfg = a.config
-    sk = STREAM_KERNEL[cfg]
+    tag = a.config if a.config == "head" else f"cfg{int(a.config)}"
+    sk = STREAM_KERNEL[tag]
     main_row = next((t for t in table if t[0].startswith(sk + "<") and t[5] is not None), None)
     wl = bench["config"]["workload"]
     lines = [f"# rocprofv3 profile, workload {wl}", ""]
@@ -103,8 +104,9 @@ def main() -> None:
         ratio = "" if hbm is None else f"{hbm / algo:.3f}"
         lines.append(f"| `{n}` | {c} | {us:.2f} | {'' if f is None else f'{f:.1f}'} | "
                      f"{'' if w is None else f'{w:.1f}'} | {'' if hbm is None else f'{hbm:.0f}'} | {ratio} |")
-    lines += ["", f"Algorithmic bytes per step: {algo} (each logit, history id and mask word read once, "
-              "u and the token).", ""]
+    what = ("the head's weights, the hidden states, the norm scale, the normed rows and the logits, "
+            "each once" if tag == "head" else "each logit, history id and mask word read once, u and the token")
+    lines += ["", f"Algorithmic bytes per step: {algo} ({what}).", ""]
     lines += ["Bench line of the stats run (timings perturbed by the tracer):", "",
               "    " + json.dumps({k: bench[k] for k in ("value", "ms_per_step")} |
                                     {"kernel_us": bench["config"]["kernel_us"],
@@ -115,14 +117,14 @@ def main() -> None:
         base = n.split("<")[0]
         if base not in kernels and base != "k_read_probe":
             kernels.append(base)
-    md = a.out / f"{'_'.join(sorted(kernels, key=lambda k: (k != sk, k)))}_cfg{cfg}_profile.md"
+    md = a.out / f"{'_'.join(sorted(kernels, key=lambda k: (k != sk, k)))}_{tag}_profile.md"
     md.write_text("\n".join(lines))
     if main_row is not None:
-        js = {"kernel": sk, "workload": f"cfg{cfg}", "kernel_name": main_row[0],
+        js = {"kernel": sk, "workload": tag, "kernel_name": main_row[0],
               "fetch_kib": main_row[3], "write_kib": main_row[4], "fetch_scale": fs, "write_scale": ws,
               "hbm_bytes_per_launch": main_row[5], "algorithmic_bytes": algo, "avg_us": main_row[2],
               "source": f"profiles/{md.name}"}
-        (a.out / f"{sk}_cfg{cfg}_traffic.json").write_text(json.dumps(js, indent=1) + "\n")
+        (a.out / f"{sk}_{tag}_traffic.json").write_text(json.dumps(js, indent=1) + "\n")
     print(md)
 
 

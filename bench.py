@@ -246,18 +246,25 @@ def head_main(args):
             for i in range(n_sets):
                 fn(i, stream)
         stream.synchronize()
-        reps = max(1, steps // n_sets)
-        for _ in range(max(1, warmup // n_sets)):
+        # The first few milliseconds of a 1.24 GB-per-launch stream run slow
+        # now and then (seen in kernel traces: a burst of launches 1.5x the
+        # steady duration right after the start); at least 40 warm-up
+        # launches, then the median of five timed segments.
+        reps = max(1, steps // (5 * n_sets))
+        for _ in range(max(20, warmup // n_sets)):
             gr.replay()
         stream.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        with torch.cuda.stream(stream):
-            e0.record(stream)
-            for _ in range(reps):
-                gr.replay()
-            e1.record(stream)
-        stream.synchronize()
-        return e0.elapsed_time(e1) / (reps * n_sets), reps * n_sets
+        seg = []
+        for _ in range(5):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            with torch.cuda.stream(stream):
+                e0.record(stream)
+                for _ in range(reps):
+                    gr.replay()
+                e1.record(stream)
+            stream.synchronize()
+            seg.append(e0.elapsed_time(e1) / (reps * n_sets))
+        return statistics.median(seg), 5 * reps * n_sets
 
     steps = min(args.steps, 400)
     head_ms, n_head = timed(head, steps, args.warmup)

@@ -12,15 +12,16 @@
 // and added in order when four or more remain, the rest fused; the bf16 tail:
 // fused, summed on its own and added last).
 //
-// k_head_norm: one 512-thread block per row; the row goes to LDS chain-major
-//   (16 loads in flight per thread), lanes 0-7 run the eight chains of the
-//   sum of squares with 16-byte LDS reads, then every thread writes its share
-//   of (x * scale) * inv_rms from registers.
-// k_head_gemv: HBM-bound (V x H weights read once per group of up to four
-//   rows). One wave per 64 vocabulary rows, lane i running the eight chains
-//   of its own row: the weights go through a row-major LDS tile in chunks of
-//   128 bytes per row (coalesced 16-byte loads two chunks ahead, 16-byte
-//   stores, 16-byte reads of one step of all eight chains).
+// k_head_gemv, one kernel for both: HBM-bound (V x H weights read once per
+//   group of up to four rows). One wave per 64 vocabulary rows, lane i
+//   running the eight chains of its own row: the weights go through a
+//   row-major LDS tile in chunks of 128 bytes per row (coalesced 16-byte
+//   loads one chunk ahead, 16-byte stores, 16-byte reads of one step of all
+//   eight chains). Every wave first computes the rmsnorm of its batch rows
+//   itself (the sum of squares' eight chains over chain-major LDS pieces of
+//   the hidden rows, while its first weight chunk is in flight) and forms
+//   the normed values chunk by chunk; the first waves also write the normed
+//   rows out.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -63,96 +64,11 @@ __device__ __forceinline__ float hsum8_lanes(float p) {
     return __shfl(tot, lane_id() & ~7, 64);
 }
 
-constexpr int kNT = 512;                  // threads of a k_head_norm block
-constexpr int kNQ = 16;                   // row elements per thread and pass
-constexpr int kHNC = kNT * kNQ;           // row elements one pass stages in LDS (8192)
-constexpr int kNCS = kHNC / 8 + 8;        // LDS stride of one chain (padded: conflict-free stores)
-
-__global__ __launch_bounds__(kNT) void k_head_norm(const float* __restrict__ hidden, int64_t hstride, int H,
-                                                  const float* __restrict__ scale, float eps,
-                                                  float* __restrict__ normed) {
-    // the row chain-major: element 8j + l of a pass at [l][j], so that chain l
-    // reads four of its steps with one 16-byte LDS read
-    __shared__ __attribute__((aligned(16))) float xs[8 * kNCS];
-    __shared__ float ssum;
-    const int r = blockIdx.x, tid = threadIdx.x;
-    const float* x = hidden + (int64_t)r * hstride;
-    float* y = normed + (int64_t)r * H;
-    const int H8 = H / 8 * 8;
-    float v[kNQ] = {}, g[kNQ];
-    // every load of the thread's share in flight at once; the scale's too
-    // (the output pass of a one-pass row takes x from these registers)
-    auto load = [&](float (&d)[kNQ], const float* src, int c0, int n) {
-#pragma unroll
-        for (int q = 0; q < kNQ; ++q) {
-            const int i = c0 + tid + q * kNT;
-            d[q] = i < n ? src[i] : 0.0f;
-        }
-    };
-    float p = 0.0f;   // chain l = tid (tid < 8)
-    if (H <= kHNC) load(g, scale, 0, H);
-    for (int c0 = 0; c0 < H8; c0 += kHNC) {
-        const int n = min(kHNC, H8 - c0);
-        load(v, x, c0, c0 + n);
-        if (c0 > 0) __syncthreads();   // the previous pass's chains are done with xs
-#pragma unroll
-        for (int q = 0; q < kNQ; ++q) {
-            const int i = tid + q * kNT;   // element i of the pass: chain i & 7, step i >> 3
-            if (i < n) xs[(i & 7) * kNCS + (i >> 3)] = v[q];
-        }
-        __syncthreads();
-        if (tid < 8) {
-            // 16 steps per group of four 16-byte reads, the next group's reads
-            // issued before this group's multiply-adds (n / 8 steps in all)
-            const float4* c = reinterpret_cast<const float4*>(xs + tid * kNCS);
-            const int n4 = n / 128;   // whole groups of 16 steps (n / 8 steps)
-            float4 a[4], b[4];
-            if (n4 > 0)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) a[q] = c[q];
-            for (int t = 0; t < n4; ++t) {
-                if (t + 1 < n4)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) b[q] = c[4 * (t + 1) + q];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    p = __builtin_fmaf(a[q].x, a[q].x, p);
-                    p = __builtin_fmaf(a[q].y, a[q].y, p);
-                    p = __builtin_fmaf(a[q].z, a[q].z, p);
-                    p = __builtin_fmaf(a[q].w, a[q].w, p);
-                }
-#pragma unroll
-                for (int q = 0; q < 4; ++q) a[q] = b[q];
-            }
-            const float* cs = xs + tid * kNCS;
-            for (int k = n4 * 16; k < n / 8; ++k) p = __builtin_fmaf(cs[k], cs[k], p);
-        }
-    }
-    if (tid < 64) {
-        float ss = __shfl(hsum8_lanes(p), 0, 64);
-        ss = tail_f32(ss, [&](int i) { return x[H8 + i]; }, [&](int i) { return x[H8 + i]; }, H - H8);
-        if (tid == 0) ssum = ss;
-    }
-    __syncthreads();
-    const float mean_sq = ssum / (float)H;
-    const float inv_rms = 1.0f / sqrtf(mean_sq + eps);
-    if (H <= kHNC) {
-        // the row's x in v (its H8 part) and its scale in g
-#pragma unroll
-        for (int q = 0; q < kNQ; ++q) {
-            const int i = tid + q * kNT;
-            if (i < H) y[i] = ((i < H8 ? v[q] : x[i]) * g[q]) * inv_rms;
-        }
-    } else {
-        for (int i = tid; i < H; i += kNT) y[i] = (x[i] * scale[i]) * inv_rms;
-    }
-}
-
 // WB: bf16 weights (else f32). BB: batch rows per block (1, 2 or 4). VEC:
 // weight rows sit on 16-byte boundaries (16-byte loads; else element loads).
 // One wave per 64 vocabulary rows, lane i running the eight chains of row
 // m0 + i. The weights arrive in chunks of 128 bytes of each row: coalesced
-// 16-byte loads (eight lanes per row segment) into registers, two chunks
+// 16-byte loads (eight lanes per row segment) into registers, one chunk
 // ahead, then 16-byte stores into a row-major LDS tile (rows padded to 144
 // bytes: conflict-free), from which each lane reads its own row 16 bytes at a
 // time -- one step of all eight chains (bf16), or half a step (f32). The
@@ -160,7 +76,9 @@ __global__ __launch_bounds__(kNT) void k_head_norm(const float* __restrict__ hid
 // broadcasts. The block is the one wave: no barrier waits on another wave.
 template <bool WB, int BB, bool VEC>
 __global__ __launch_bounds__(64) void k_head_gemv(const void* __restrict__ weight, int V, int H,
-                                                  const float* __restrict__ normed, int rows,
+                                                  const float* __restrict__ hidden, int64_t hstride,
+                                                  const float* __restrict__ scale, float eps,
+                                                  float* __restrict__ normed, int rows,
                                                   float logit_scale, float* __restrict__ logits,
                                                   int64_t lstride) {
     using W = typename std::conditional<WB, uint16_t, float>::type;
@@ -180,44 +98,132 @@ __global__ __launch_bounds__(64) void k_head_gemv(const void* __restrict__ weigh
     const int nC = (H8 + KC - 1) / KC;
     const bool scaled = logit_scale != 1.0f && logit_scale != 0.0f;
     const float inv = scaled ? 1.0f / logit_scale : 1.0f;
+    auto xrow = [&](int b) { return hidden + (int64_t)(b0 + min(b, nb - 1)) * hstride; };
 
     // chunk c into registers: vector i of the lane is segment v % 8 of tile
-    // row v / 8 (v = lane + 64 i); past H8 or past V: 0
-    auto load = [&](uint4 (&reg)[NV], float (&xr)[BB], int c) {
+    // row v / 8 (v = lane + 64 i); with it the hidden values and the scale of
+    // the chunk's column c0 + lane. Every load is unconditional, from an
+    // address clamped into its array (rows past V read row V - 1, columns
+    // past H8 the row's last whole vector): their values feed only rows that
+    // are not stored and steps the chains skip. A branch around a load would
+    // make the compiler wait for it at the join; these loads stay in flight
+    // together.
+    auto load = [&](uint4 (&reg)[NV], float (&xr)[BB], float& sr, int c) {
         const int c0 = c * KC;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int v = lane + i * 64;
-            const int m = m0 + (v >> 3), col = c0 + (v & 7) * EPV;
-            uint4 q = make_uint4(0u, 0u, 0u, 0u);
-            if (m < V) {
-                const W* src = wb + (int64_t)m * H + col;
-                if (VEC && col + EPV <= H8) {
-                    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-                    const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
-                    q = make_uint4(t.x, t.y, t.z, t.w);
-                } else {
-                    W e[EPV];
+            const int m = min(m0 + (v >> 3), V - 1), col = c0 + (v & 7) * EPV;
+            const W* rowp = wb + (int64_t)m * H;
+            if (VEC) {
+                typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+                const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rowp + min(col, H8 - EPV)));
+                reg[i] = make_uint4(t.x, t.y, t.z, t.w);
+            } else {
+                W e[EPV];
 #pragma unroll
-                    for (int j = 0; j < EPV; ++j) e[j] = (col + j < H8) ? src[j] : W(0);
-                    q = *reinterpret_cast<const uint4*>(e);
+                for (int j = 0; j < EPV; ++j) e[j] = rowp[min(col + j, H8 - 1)];
+                reg[i] = *reinterpret_cast<const uint4*>(e);
+            }
+        }
+        const int k = min(c0 + lane, H8 - 1);
+#pragma unroll
+        for (int b = 0; b < BB; ++b) xr[b] = xrow(b)[k];
+        sr = scale[k];
+    };
+    uint4 reg[NV];
+    float xr[BB], sr;
+
+    // The final rmsnorm of the wave's batch rows, computed by every wave (the
+    // same bits as one kernel computing it once: the reference's eight chains
+    // of x * x, its horizontal sum and tail, mean, 1 / sqrt(mean + eps)).
+    // The rows go through the LDS tile in pieces of 2048 elements (2048 / BB
+    // of each row), chain-major; lanes 8b + l run chain l of row b. The
+    // first piece's loads are issued ahead of the first weight chunk's, so
+    // that waiting for them leaves the weights in flight while the chains
+    // run.
+    constexpr int PE = 2048 / BB;                     // elements of each row per piece
+    constexpr int PS = PE / 8 + 8;                    // LDS floats per (row, chain), padded
+    constexpr int PT = 2048 / 64;                     // piece elements per lane
+    float* xp = reinterpret_cast<float*>(wl);         // [BB][8][PS]
+    float pv[PT];
+    auto piece_load = [&](int p0) {
+#pragma unroll
+        for (int t = 0; t < PT; ++t) {
+            const int e = lane + 64 * t, b = e / PE, k = p0 + e % PE;
+            pv[t] = xrow(b)[min(k, H8 - 1)];
+        }
+    };
+    float p = 0.0f;   // lane 8b + l: chain l of batch row b
+    const int nP = (H8 + PE - 1) / PE;
+    if (nP > 0) piece_load(0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (nC > 0) load(reg, xr, sr, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int q = 0; q < nP; ++q) {
+        const int p0 = q * PE;
+        if (q > 0) __syncthreads();                      // the previous piece's chains are done
+#pragma unroll
+        for (int t = 0; t < PT; ++t) {
+            const int e = lane + 64 * t, b = e / PE, k = e % PE;   // k % 8 = lane % 8: chain lane % 8
+            xp[(b * 8 + (k & 7)) * PS + (k >> 3)] = pv[t];
+        }
+        __syncthreads();
+        if (q + 1 < nP) piece_load(p0 + PE);            // in flight while this piece's chains run
+        const int n = min(PE, H8 - p0) >> 3;            // steps of this piece
+        if (lane < 8 * BB) {
+            const float4* cs = reinterpret_cast<const float4*>(xp + (lane >> 3) * 8 * PS + (lane & 7) * PS);
+            // sixteen steps per group, the group's four reads issued together
+            int g = 0;
+            for (; 16 * (g + 1) <= n; ++g) {
+                float4 v[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = cs[4 * g + i];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    p = __builtin_fmaf(v[i].x, v[i].x, p);
+                    p = __builtin_fmaf(v[i].y, v[i].y, p);
+                    p = __builtin_fmaf(v[i].z, v[i].z, p);
+                    p = __builtin_fmaf(v[i].w, v[i].w, p);
                 }
             }
-            reg[i] = q;
+            const float* cf = reinterpret_cast<const float*>(cs);
+            for (int j = 16 * g; j < n; ++j) p = __builtin_fmaf(cf[j], cf[j], p);
         }
+    }
+    __syncthreads();                                     // the tile is free for the weights
+    float rinv[BB];   // 1 / rms of each batch row (every lane)
+    {
+        const float hs8 = hsum8_lanes(p);                 // lanes 8b .. 8b + 7: row b's horizontal sum
+        const int b = min(lane >> 3, nb - 1);
+        const float* x = xrow(b);
+        const float ss = tail_f32(hs8, [&](int i) { return x[H8 + i]; }, [&](int i) { return x[H8 + i]; }, H - H8);
+        const float mean_sq = ss / (float)H;
+        const float r = 1.0f / sqrtf(mean_sq + eps);
 #pragma unroll
-        for (int b = 0; b < BB; ++b)
-            xr[b] = (b < nb && lane < KC && c0 + lane < H8) ? normed[(int64_t)(b0 + b) * H + c0 + lane] : 0.0f;
-    };
-    auto store = [&](const uint4 (&reg)[NV], const float (&xr)[BB]) {
+        for (int bb = 0; bb < BB; ++bb) rinv[bb] = __shfl(r, 8 * bb, 64);
+    }
+    // the normed rows themselves (an output), 64 columns per wave
+    if (blockIdx.x * 64 < H) {
+        for (int i = blockIdx.x * 64 + lane; i < H; i += gridDim.x * 64) {
+            const float g = scale[i];
+#pragma unroll
+            for (int b = 0; b < BB; ++b)
+                if (b < nb) normed[(int64_t)(b0 + b) * H + i] = (xrow(b)[i] * g) * rinv[b];
+        }
+    }
+    // registers -> LDS; the normed values (x * scale) * (1 / rms), those of
+    // columns past H8 (and of batch rows past the last) as 0
+    auto store = [&](const uint4 (&reg)[NV], const float (&xr)[BB], float sr, int c) {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int v = lane + i * 64;
             *reinterpret_cast<uint4*>(wl + (v >> 3) * kGRS + (v & 7) * 16) = reg[i];
         }
+        const int c0 = c * KC;
 #pragma unroll
         for (int b = 0; b < BB; ++b)
-            if (lane < KC) xl[b][lane] = xr[b];
+            if (lane < KC) xl[b][lane] = (b < nb && c0 + lane < H8) ? (xr[b] * sr) * rinv[b] : 0.0f;
     };
     float acc[BB][8];
 #pragma unroll
@@ -260,22 +266,19 @@ __global__ __launch_bounds__(64) void k_head_gemv(const void* __restrict__ weigh
             for (int j = 0; j < nj; ++j) one(j);
         }
     };
-    // two chunks in flight: A holds the even chunks, B the odd ones (a third
-    // set, and the compiler's own fences of a wave, measured slower)
-    uint4 regA[NV], regB[NV];
-    float xrA[BB], xrB[BB];
-    auto step = [&](uint4 (&reg)[NV], float (&xr)[BB], int c) {
-        store(reg, xr);
+    // One chunk in flight while the chains run on the one before: chunk c to
+    // LDS, chunk c + 1's loads issued into the registers just freed, then
+    // c's chain steps. (Measured: two or three chunks ahead are slower --
+    // 64 rows x 128 bytes per chunk spread each wave's requests over many
+    // DRAM rows, and more of them in flight lowers the rate; a wave holds
+    // 8 KB in flight, the chip ~19 MB, more than the latency asks for.)
+    // No lane-dependent condition around a load: the compiler's waits are exact.
+    for (int c = 0; c < nC; ++c) {
+        store(reg, xr, sr, c);
         __syncthreads();                                 // (the block is one wave)
-        if (c + 2 < nC) load(reg, xr, c + 2);
+        if (c + 1 < nC) load(reg, xr, sr, c + 1);
         chains(c);
         __syncthreads();                                 // the reads are done before the next stores
-    };
-    if (nC > 0) load(regA, xrA, 0);
-    if (nC > 1) load(regB, xrB, 1);
-    for (int c = 0; c < nC; c += 2) {
-        step(regA, xrA, c);
-        if (c + 1 < nC) step(regB, xrB, c + 1);
     }
     // the horizontal sum, the tail, the logit scale; one row per lane
     const int m = m0 + lane;
@@ -288,14 +291,15 @@ __global__ __launch_bounds__(64) void k_head_gemv(const void* __restrict__ weigh
         const float* p = acc[b];
         const float s0 = p[0] + p[4], s1 = p[1] + p[5], s2 = p[2] + p[6], s3 = p[3] + p[7];
         const float hs = (s0 + s1) + (s2 + s3);
-        const float* x = normed + (int64_t)(b0 + b) * H;
+        const float* x = xrow(b);
+        auto xn = [&](int i) { return (x[H8 + i] * scale[H8 + i]) * rinv[b]; };   // normed value H8 + i
         float y;
         if (WB) {
             float tail = 0.0f;
-            for (int i = 0; i < tl; ++i) tail = __builtin_fmaf(bf16f(((const uint16_t*)row)[H8 + i]), x[H8 + i], tail);
+            for (int i = 0; i < tl; ++i) tail = __builtin_fmaf(bf16f(((const uint16_t*)row)[H8 + i]), xn(i), tail);
             y = hs + tail;
         } else {
-            y = tail_f32(hs, [&](int i) { return ((const float*)row)[H8 + i]; }, [&](int i) { return x[H8 + i]; }, tl);
+            y = tail_f32(hs, [&](int i) { return ((const float*)row)[H8 + i]; }, xn, tl);
         }
         if (scaled) y = y * inv;
         logits[(int64_t)(b0 + b) * lstride + m] = y;
@@ -309,10 +313,12 @@ hipError_t launch_gemv_bb(const ultima_hsamp_head* h, bool vec, hipStream_t s) {
     const dim3 grid((h->vocab + 63) / 64, (h->rows + BB - 1) / BB);
     if (vec)
         hipLaunchKernelGGL((k_head_gemv<WB, BB, true>), grid, dim3(64), 0, s, h->weight, h->vocab, h->hidden_dim,
-                           h->normed, h->rows, h->logit_scale, h->logits, h->logits_stride);
+                           h->hidden, h->hidden_stride, h->norm_scale, h->eps, h->normed, h->rows,
+                           h->logit_scale, h->logits, h->logits_stride);
     else
-        hipLaunchKernelGGL((k_head_gemv<WB, BB, false>), grid, dim3(64), 0, s, h->weight, h->vocab,
-                           h->hidden_dim, h->normed, h->rows, h->logit_scale, h->logits, h->logits_stride);
+        hipLaunchKernelGGL((k_head_gemv<WB, BB, false>), grid, dim3(64), 0, s, h->weight, h->vocab, h->hidden_dim,
+                           h->hidden, h->hidden_stride, h->norm_scale, h->eps, h->normed, h->rows,
+                           h->logit_scale, h->logits, h->logits_stride);
     return hipGetLastError();
 }
 
@@ -340,12 +346,8 @@ extern "C" int ultima_hsamp_lm_head(const ultima_hsamp_head* h, void* hip_stream
     // row offsets must fit the kernels' 32-bit index arithmetic within a row
     if ((int64_t)h->vocab * h->hidden_dim >= (int64_t)1 << 40) return ULTIMA_HSAMP_ERR_UNSUPPORTED;
     hipStream_t s = static_cast<hipStream_t>(hip_stream);
-    hipLaunchKernelGGL(k_head_norm, dim3(h->rows), dim3(kNT), 0, s, h->hidden, h->hidden_stride, h->hidden_dim,
-                       h->norm_scale, h->eps, h->normed);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return ULTIMA_HSAMP_ERR_HIP;
     const int es = h->weight_dtype == ULTIMA_HSAMP_BF16 ? 2 : 4;
     const bool vec = (reinterpret_cast<uintptr_t>(h->weight) % 16 == 0) && (((int64_t)h->hidden_dim * es) % 16 == 0);
-    e = h->weight_dtype == ULTIMA_HSAMP_BF16 ? launch_gemv<true>(h, vec, s) : launch_gemv<false>(h, vec, s);
+    const hipError_t e = h->weight_dtype == ULTIMA_HSAMP_BF16 ? launch_gemv<true>(h, vec, s) : launch_gemv<false>(h, vec, s);
     return e == hipSuccess ? ULTIMA_HSAMP_OK : ULTIMA_HSAMP_ERR_HIP;
 }

@@ -30,6 +30,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "hsamp_plan.h"
 #include "hsamp_wave.h"
@@ -3526,38 +3527,58 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
     const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * (a.dtype == 0 ? 4 : 2);
     float mloc = -__builtin_inff();
     bool nanv = false;
-    for (int b = tid; b < Vp; b += 8 * kFT) {
-        // eight logits (and mask words) per thread in flight, then the ladder
-        float x[8];
-        uint32_t mw[8];
+    // Eight logits (and mask words) per thread in flight, then the ladder.
+    // The loads take clamped ids and no condition, the element type and the
+    // mask are template parameters: a load under a branch would be waited
+    // for at the join, one memory round trip per load.
+    auto transform = [&](auto dt_c, auto mask_c) {
+        constexpr int DT = decltype(dt_c)::value;
+        constexpr bool MK = decltype(mask_c)::value;
+        const uint32_t* mrow = MK ? a.mask + (int64_t)r * a.mask_stride : nullptr;
+        for (int b = tid; b < Vp; b += 8 * kFT) {
+            float x[8];
+            uint32_t mw[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int i = b + q * kFT;
-            x[q] = i < V ? load_logit_dt(rowp, a.dtype, i) : -__builtin_inff();
-            mw[q] = (masked && i < V) ? a.mask[(int64_t)r * a.mask_stride + (i >> 5)] : 0xFFFFFFFFu;
-        }
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int i = b + q * kFT;
-            if (i >= Vp) break;
-            float y = x[q];
-            if (i < V) {
-                if (!((mw[q] >> (i & 31)) & 1u)) y = -__builtin_inff();
-                if (pen) {
-                    uint32_t s0 = hslot(i, pl);
-                    uint32_t kk;
-                    while ((kk = tab_ld(&pl.hkey[s0])) != kEmpty && kk != (uint32_t)i) s0 = (s0 + 1) & pl.hmask;
-                    if (kk == (uint32_t)i) y = pen_value(y, i, tab_ld(&pl.hval[s0]), a, P);
-                }
-                y = y * P.inv_temp;
-                if (y != y) {
-                    nanv = true;
-                    y = -__builtin_inff();
-                }
+            for (int q = 0; q < 8; ++q) {
+                const int ic = min(b + q * kFT, V - 1);
+                x[q] = load_logit<DT>(rowp, ic);
+                mw[q] = MK ? mrow[ic >> 5] : 0xFFFFFFFFu;
             }
-            fv[i] = y;
-            mloc = fmaxf(mloc, y);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int i = b + q * kFT;
+                if (i >= Vp) break;
+                float y = -__builtin_inff();
+                if (i < V) {
+                    y = x[q];
+                    if (!((mw[q] >> (i & 31)) & 1u)) y = -__builtin_inff();
+                    if (pen) {
+                        uint32_t s0 = hslot(i, pl);
+                        uint32_t kk;
+                        while ((kk = tab_ld(&pl.hkey[s0])) != kEmpty && kk != (uint32_t)i) s0 = (s0 + 1) & pl.hmask;
+                        if (kk == (uint32_t)i) y = pen_value(y, i, tab_ld(&pl.hval[s0]), a, P);
+                    }
+                    y = y * P.inv_temp;
+                    if (y != y) {
+                        nanv = true;
+                        y = -__builtin_inff();
+                    }
+                }
+                fv[i] = y;
+                mloc = fmaxf(mloc, y);
+            }
         }
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using BT = std::integral_constant<bool, true>;
+    using BF = std::integral_constant<bool, false>;
+    if (a.dtype == 0) {
+        if (masked) transform(I0{}, BT{});
+        else transform(I0{}, BF{});
+    } else {
+        if (masked) transform(I1{}, BT{});
+        else transform(I1{}, BF{});
     }
     if (nanv) atomicOr(&st.flags, 4);
     float m = fblock_max(mloc, st);

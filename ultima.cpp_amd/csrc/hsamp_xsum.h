@@ -244,10 +244,7 @@ __device__ __forceinline__ void fpass(const float* __restrict__ x, int n, F&& f)
     for (int b = (int)threadIdx.x; b < n4; b += 4 * kFT) {
         float4 v[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int i = b + q * kFT;
-            v[q] = i < n4 ? x4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
+        for (int q = 0; q < 4; ++q) v[q] = x4[min(b + q * kFT, n4 - 1)];   // (clamped: no branch around a load)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int i = b + q * kFT;
@@ -278,12 +275,9 @@ __device__ __forceinline__ void wpass(const float* __restrict__ x, int nW, int G
             ng = 0;
             nw = w + kFW;
         }
-        float4 n0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), n1 = n0;
-        if (nw < nW) {
-            const float4* pn = reinterpret_cast<const float4*>(x + (size_t)nw * WS + ng * kFWin + lane * 8);
-            n0 = pn[0];
-            n1 = pn[1];
-        }
+        // (past the last window: the last again, unused; no branch around a load)
+        const float4* pn = reinterpret_cast<const float4*>(x + (size_t)min(nw, nW - 1) * WS + ng * kFWin + lane * 8);
+        const float4 n0 = pn[0], n1 = pn[1];
         const float v[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
         f(w, g, v);
         if (nw >= nW) break;
@@ -311,14 +305,10 @@ __device__ __forceinline__ void wpass2(const float* __restrict__ x, const float*
             ng = 0;
             nw = w + kFW;
         }
-        float4 n0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), n1 = n0, m0 = n0, m1 = n0;
-        if (nw < nW) {
-            const size_t on = (size_t)nw * WS + ng * kFWin + lane * 8;
-            n0 = reinterpret_cast<const float4*>(x + on)[0];
-            n1 = reinterpret_cast<const float4*>(x + on)[1];
-            m0 = reinterpret_cast<const float4*>(z + on)[0];
-            m1 = reinterpret_cast<const float4*>(z + on)[1];
-        }
+        // (past the last window: the last again, unused; no branch around a load)
+        const size_t on = (size_t)min(nw, nW - 1) * WS + ng * kFWin + lane * 8;
+        const float4 n0 = reinterpret_cast<const float4*>(x + on)[0], n1 = reinterpret_cast<const float4*>(x + on)[1];
+        const float4 m0 = reinterpret_cast<const float4*>(z + on)[0], m1 = reinterpret_cast<const float4*>(z + on)[1];
         const float v[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
         const float y[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
         f(w, g, v, y);

@@ -34,6 +34,10 @@ def _head(hs, h, g, w, scale=1.0, eps=1e-6):
     (2, 132, 500, "f32", 1.0),         # hidden % 8 == 4 (vectorised tail)
     (1, 7, 33, "bf16", 0.0),           # hidden < 8: tail only
     (5, 4100, 257, "bf16", 2.5),       # hidden % 8 == 4 with bf16 (fused tail)
+    (1, 137, 100, "f32", 1.0),         # hidden % 8 == 1
+    (1, 10, 40, "f32", 1.0),           # hidden % 8 == 2
+    (1, 133, 70, "bf16", 1.0),         # hidden % 8 == 5
+    (2, 262, 90, "bf16", 1.0),         # hidden % 8 == 6
     (2, 200, 64, "bf16", 1.0),         # norm chains: one 16-step group and 9 single steps
     (1, 8192, 1000, "bf16", 1.0),      # a Qwen2.5-72B hidden size: one full norm pass
     (2, 8212, 300, "f32", 1.0),        # two norm passes (the second 2 steps), vectorised tail

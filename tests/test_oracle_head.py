@@ -63,7 +63,7 @@ def test_matvec_close_to_float64(M, K):
 
 
 @needs_ref
-@pytest.mark.parametrize("n", [1, 4, 7, 8, 9, 131, 896, 2048, 4096])
+@pytest.mark.parametrize("n", [1, 2, 4, 5, 6, 7, 8, 9, 10, 13, 14, 131, 134, 896, 2048, 4096, 4102])
 def test_rmsnorm_matches_reference_bits(n):
     rng = np.random.default_rng(100 + n)
     for eps in (0.0, 1e-6, 1e-5):
@@ -73,7 +73,8 @@ def test_rmsnorm_matches_reference_bits(n):
 
 
 @needs_ref
-@pytest.mark.parametrize("M,K", [(37, 131), (16, 64), (5, 7), (3, 1), (64, 896), (48, 4096), (9, 4103)])
+@pytest.mark.parametrize("M,K", [(37, 131), (16, 64), (5, 7), (3, 1), (4, 2), (4, 5), (4, 6), (7, 130), (7, 133),
+                                 (7, 134), (64, 896), (48, 4096), (9, 4103)])
 def test_matvec_matches_reference_bits(M, K):
     rng = np.random.default_rng(M + 7 * K)
     w = rng.normal(0, 0.05, (M, K)).astype(np.float32)

@@ -121,6 +121,12 @@ typedef struct ultima_hsamp_batch {
     float* kept_prob;           /* device [rows, set_cap] out or NULL: their final probabilities */
     int32_t* kept_count;        /* device [rows] out or NULL */
     int32_t set_cap;            /* capacity of the set outputs per row */
+    const int32_t* hist_len_dev; /* device [rows] or NULL: each row's history length, read on the
+                                  * device in place of params[r].hist_len (a history kept on the
+                                  * GPU by ultima_hsamp_history_push). params[r].hist_len must then
+                                  * be the same value, or at most it and at least the row's longest
+                                  * penalty window (so that every window is the same for both);
+                                  * the plan then stays the same from step to step. */
 } ultima_hsamp_batch;
 
 typedef struct ultima_hsamp ultima_hsamp;
@@ -203,6 +209,28 @@ int ultima_hsamp_read_probe(ultima_hsamp* h, const ultima_hsamp_batch* batch, fl
  * stream pass (reads the logits) and the per-row merge, so a caller can time
  * the two kernels apart with its own events. NULL stops it. */
 int ultima_hsamp_set_phase_event(ultima_hsamp* h, void* hip_event);
+
+/* ---- Device-side history ------------------------------------------------------
+ * The penalties' recent-token window kept on the GPU, one row per sequence,
+ * appended with each step's sampled token where it already is (the token
+ * output of ultima_hsamp_run), so that a decode loop uploads no history.
+ * Replaces, per row, SamplerContext::push_recent(next) after each sample()
+ *   /root/reference/src/sampler/sampler.cpp:213 (push_recent),
+ *   /root/reference/src/server/http_server.cpp:183, apps/ultima-cli/main.cpp:679 (its callers),
+ * for the window the reference intends the KV slot to supply
+ * (/root/reference/include/ultima/sampler/sampler.hpp:54-56,
+ *  /root/reference/include/ultima/kv_cache/kv_cache.hpp:108-111).
+ * Row r holds hist_len_dev[r] ids, oldest first, in hist[r * hist_stride ...].
+ * For every row: if it is full (hist_len_dev[r] >= hist_stride) its last `keep`
+ * ids are first moved to its front; then tokens[r] is appended and
+ * hist_len_dev[r] advanced. Penalties look at most max(repeat_last_n,
+ * dry_last_n) ids back, so keep >= that window leaves every result as the
+ * reference's unbounded recent_ gives it. 0 < keep <= hist_stride / 2.
+ * Pass hist and hist_len_dev to ultima_hsamp_run (batch.hist, batch.hist_len_dev).
+ * All pointers are device memory; asynchronous on hip_stream; allocates
+ * nothing (it may be captured into a graph with the sampler). */
+int ultima_hsamp_history_push(int32_t* hist, int64_t hist_stride, int32_t* hist_len_dev, const int32_t* tokens,
+                              int32_t rows, int32_t keep, void* hip_stream);
 
 /* ---- The logits producer ----------------------------------------------------
  * The model's last step before sampling, on the device: each row's final

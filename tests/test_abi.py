@@ -92,3 +92,44 @@ def test_product_does_not_link_the_oracle(pkg):
         syms = subprocess.run(["nm", "-D", str(pkg.hsamp.PKG / so)], capture_output=True,
                               text=True).stdout
         assert "orc_" not in syms and "ref_sample" not in syms
+
+
+def test_struct_layouts_match_the_header(pkg, tmp_path):
+    """The binding's ctypes structs have the C header's size and field offsets
+    (a C program built against include/ultima_hsamp.h prints them)."""
+    hs = pkg.hsamp
+    from pathlib import Path
+    root = Path(__file__).resolve().parents[1]
+    structs = {"ultima_hsamp_params": hs.Params, "ultima_hsamp_batch": hs.Batch, "ultima_hsamp_head": hs.Head}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "ultima_hsamp.h"', 'int main(void) {']
+    for cname, py in structs.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for f, _ in py._fields_:
+            lines.append(f'printf("{cname} {f} %zu\\n", offsetof({cname}, {f}));')
+    lines += ['return 0;', '}']
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-I", str(root / "include"), str(src), "-o", str(exe)], check=True)
+    got = {}
+    for line in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines():
+        cname, field, val = line.split()
+        got[(cname, field)] = int(val)
+    for cname, py in structs.items():
+        assert got[(cname, "size")] == ctypes.sizeof(py), cname
+        for f, _ in py._fields_:
+            assert got[(cname, f)] == getattr(py, f).offset, f"{cname}.{f}"
+
+
+def test_history_push_rejects_bad_arguments(pkg):
+    """Argument checks run before any device work (no GPU needed)."""
+    hs = pkg.hsamp
+    L = hs.lib()
+    p = ctypes.c_void_p(16)   # never dereferenced: every call below fails its checks first
+    assert L.ultima_hsamp_history_push(None, 8, p, p, 1, 4, None) == hs.ERR_INVALID
+    assert L.ultima_hsamp_history_push(p, 8, None, p, 1, 4, None) == hs.ERR_INVALID
+    assert L.ultima_hsamp_history_push(p, 8, p, None, 1, 4, None) == hs.ERR_INVALID
+    assert L.ultima_hsamp_history_push(p, 8, p, p, 0, 4, None) == hs.ERR_INVALID        # no rows
+    assert L.ultima_hsamp_history_push(p, 8, p, p, 1, 5, None) == hs.ERR_INVALID        # keep > stride / 2
+    assert L.ultima_hsamp_history_push(p, 8, p, p, 1, 0, None) == hs.ERR_INVALID        # keep < 1
+    assert L.ultima_hsamp_history_push(p, 1, p, p, 1, 1, None) == hs.ERR_INVALID        # stride < 2

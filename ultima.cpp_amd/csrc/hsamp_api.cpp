@@ -311,6 +311,7 @@ int validate_batch(const ultima_hsamp_batch* b, int32_t max_rows, int32_t max_vo
     if (b->logits == nullptr || b->u == nullptr || b->token == nullptr) return ULTIMA_HSAMP_ERR_INVALID;
     if (b->logits_stride < b->vocab) return ULTIMA_HSAMP_ERR_INVALID;
     if (b->hist != nullptr && b->hist_stride < 0) return ULTIMA_HSAMP_ERR_INVALID;
+    if (b->hist_len_dev != nullptr && (b->hist == nullptr || b->hist_stride < 1)) return ULTIMA_HSAMP_ERR_INVALID;
     if (b->mask != nullptr && b->mask_stride < (b->vocab + 31) / 32) return ULTIMA_HSAMP_ERR_INVALID;
     if ((b->flags & ~(ULTIMA_HSAMP_WRITEBACK | ULTIMA_HSAMP_STREAM_ONLY)) != 0) return ULTIMA_HSAMP_ERR_INVALID;
     if ((b->flags & ULTIMA_HSAMP_WRITEBACK) && b->dtype != ULTIMA_HSAMP_F32)
@@ -479,6 +480,7 @@ int launch_run(const RunPlan& rp, const Built& bl, const ultima_hsamp_batch* b, 
     a.logits_stride = b->logits_stride;
     a.hist = b->hist;
     a.hist_stride = b->hist_stride;
+    a.hist_len_dev = b->hist_len_dev;
     a.mask = b->mask;
     a.mask_stride = b->mask_stride;
     a.u = b->u;

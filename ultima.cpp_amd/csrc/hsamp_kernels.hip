@@ -66,6 +66,15 @@ __device__ __forceinline__ u64 comp(uint32_t key, int32_t idx) {
 }
 __device__ __forceinline__ int32_t comp_idx(u64 c) { return (int32_t)(~(uint32_t)c); }
 
+// Ids in row r's history: the plan's count, or the row's device length when
+// the batch carries one (a device-side history that grows and compacts on the
+// GPU; the plan's windows stay valid while it holds at least the longest of
+// them: kept within [scan_len, hist_stride], so that reads stay in the row).
+__device__ __forceinline__ int hist_len_of(const StreamArgs& a, const RowPlan& P, int r) {
+    if (a.hist_len_dev == nullptr) return P.hist_len;
+    return min(max(a.hist_len_dev[r], P.scan_len), (int)a.hist_stride);
+}
+
 struct Shared {
     u64 theta;          // current survival threshold (composite)
     u64 minv;
@@ -1736,7 +1745,7 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
     // is off) a count entry is a plain count over it (one atomic per id).
     const bool one = P.rep_win == 0 || P.fp_win == 0 || P.rep_win == P.fp_win;
     if (PEN && pen) {
-        const int L = P.hist_len, p0 = L - P.scan_len;
+        const int L = hist_len_of(a, P, r), p0 = L - P.scan_len;
         const int mhi = min(a.vocab, lo + a.slice_len);
         uint32_t* cw = reinterpret_cast<uint32_t*>(smem);
         const uint32_t wl = (uint32_t)(L - p0), sl = (uint32_t)(mhi - lo);
@@ -2010,7 +2019,7 @@ __global__ __launch_bounds__(kBlock, EX == 2 ? 4 : 5) void k_stream(StreamArgs a
             // which then goes first (the tile waits one round trip); the
             // window still goes out ahead of the tile, as the short rows do
             P = a.plans[r];
-            const int L = P.hist_len, p0 = L - P.scan_len;
+            const int L = hist_len_of(a, P, r), p0 = L - P.scan_len;
             const int32_t* hrow = a.hist + (int64_t)r * a.hist_stride;
 #pragma unroll
             for (int q = 0; q < 8; ++q) pre[q] = -1;
@@ -2047,7 +2056,7 @@ __global__ __launch_bounds__(kBlock, EX == 2 ? 4 : 5) void k_stream(StreamArgs a
     // The history window goes out next (before the first tile when that has
     // not gone yet). Branch-free: clamped loads (pre[q] holds position
     // p0 + q * kBlock + tid, used only below L), so nothing here waits.
-    const int L = P.hist_len, p0 = L - P.scan_len;
+    const int L = hist_len_of(a, P, r), p0 = L - P.scan_len;
     const int32_t* hrow = a.hist + (int64_t)r * a.hist_stride;
     if (!EX) {
 #pragma unroll
@@ -2116,7 +2125,7 @@ __device__ __forceinline__ void pen_add(const StreamArgs& a, const RowPlan& P, i
 // The first 8 * 256 entries of the row's history window, loaded early.
 __device__ __forceinline__ void hist_prefetch(const StreamArgs& a, const RowPlan& P, int r, bool pen,
                                               int32_t (&pre)[8]) {
-    const int L = P.hist_len;
+    const int L = hist_len_of(a, P, r);
     const int p0 = L - P.scan_len;
     const int32_t* h = a.hist + (int64_t)r * a.hist_stride;
 #pragma unroll
@@ -2129,7 +2138,7 @@ __device__ __forceinline__ void hist_prefetch(const StreamArgs& a, const RowPlan
 __device__ __forceinline__ void pen_build_row(const StreamArgs& a, const RowPlan& P, int r, PenaltyLds pl,
                                               const int32_t (&pre)[8]) {
     const int tid = threadIdx.x;
-    const int L = P.hist_len;
+    const int L = hist_len_of(a, P, r);
     const int p0 = L - P.scan_len;
     const int32_t* h = a.hist + (int64_t)r * a.hist_stride;
     for (int i = tid; i < a.mhash_slots; i += kBlock) {
@@ -2262,7 +2271,7 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
     if (lmode && pen) {
         uint32_t* vb = reinterpret_cast<uint32_t*>(vb4);
         uint16_t* vpw = reinterpret_cast<uint16_t*>(vb4 + ng);
-        const int L = P.hist_len, p0 = L - P.scan_len;
+        const int L = hist_len_of(a, P, r), p0 = L - P.scan_len;
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
             const int p = p0 + q * kBlock + tid;
@@ -2322,7 +2331,7 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
     };
     if (lmode && pen) {
         // every rank read first, then the adds (no wait inside a branch)
-        const int L = P.hist_len, p0 = L - P.scan_len;
+        const int L = hist_len_of(a, P, r), p0 = L - P.scan_len;
         int rkq[8];
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
@@ -2346,7 +2355,7 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
 #pragma unroll
     for (int q = 0; q < 9; ++q) cp[q] = 0ull;
     if (pen && !lmode) {
-        const int L = P.hist_len, p0 = L - P.scan_len;
+        const int L = hist_len_of(a, P, r), p0 = L - P.scan_len;
         int32_t t[9];
         uint32_t sl[9];
 #pragma unroll
@@ -2884,7 +2893,7 @@ __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
         // branch-free: clamped positions, used only below hist_len
 #pragma unroll
         for (int q = 0; q < 8; ++q) pre[q] = -1;
-        const int L = P.hist_len;
+        const int L = hist_len_of(a, P, r);
         if ((P.flags & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) && L > 0) {
             const int32_t* h = a.hist + (int64_t)r * a.hist_stride;
             const int p0 = L - P.scan_len;
@@ -3509,7 +3518,7 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
             pl.hval[i] = 0u;
         }
         __syncthreads();
-        const int L = P.hist_len, p0 = L - P.scan_len;
+        const int L = hist_len_of(a, P, r), p0 = L - P.scan_len;
         const int32_t* h = a.hist + (int64_t)r * a.hist_stride;
         for (int p = p0 + tid; p < L; p += kFT) pen_add(a, P, L, p, h[p], pl);
         if (P.flags & RF_BIAS) {

@@ -78,6 +78,7 @@ struct StreamArgs {
     int64_t logits_stride;      // elements
     const int32_t* hist;
     int64_t hist_stride;
+    const int32_t* hist_len_dev;  // [rows] device history lengths, or NULL: the plans' hist_len
     const uint32_t* mask;
     int64_t mask_stride;        // words
     const double* u;

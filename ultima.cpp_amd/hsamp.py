@@ -70,6 +70,7 @@ class Batch(ctypes.Structure):
         ("kept_prob", ctypes.c_void_p),
         ("kept_count", ctypes.c_void_p),
         ("set_cap", ctypes.c_int32),
+        ("hist_len_dev", ctypes.c_void_p),
     ]
 
 
@@ -141,6 +142,8 @@ def lib() -> ctypes.CDLL:
         L.ultima_hsamp_read_probe.argtypes = [vp, ctypes.POINTER(Batch), vp, vp]
         L.ultima_hsamp_set_phase_event.restype = ctypes.c_int
         L.ultima_hsamp_set_phase_event.argtypes = [vp, vp]
+        L.ultima_hsamp_history_push.restype = ctypes.c_int
+        L.ultima_hsamp_history_push.argtypes = [vp, ctypes.c_int64, vp, vp, i32, i32, vp]
         L.ultima_hsamp_lm_head.restype = ctypes.c_int
         L.ultima_hsamp_lm_head.argtypes = [ctypes.POINTER(Head), vp]
         _lib = L
@@ -182,7 +185,7 @@ def make_params(plist, hist_len=None, bias=None):
 
 
 def _batch(logits, params, u, hist, hist_len, mask, bias, writeback, want_sets, set_cap, stream, outputs,
-           stream_only):
+           stream_only, hist_len_dev=None):
     """An ultima_hsamp_batch over torch tensors: (batch, outputs, host arrays
     the call reads, stream)."""
     import torch
@@ -213,6 +216,8 @@ def _batch(logits, params, u, hist, hist_len, mask, bias, writeback, want_sets, 
     if hist is not None:
         b.hist = hist.data_ptr()
         b.hist_stride = hist.stride(0)
+    if hist_len_dev is not None:
+        b.hist_len_dev = hist_len_dev.data_ptr()
     if mask is not None:
         b.mask = mask.data_ptr()
         b.mask_stride = mask.stride(0)
@@ -243,6 +248,22 @@ def run_noalloc(logits, params, u, hist=None, hist_len=None, mask=None, bias=Non
     check(lib().ultima_hsamp_run_noalloc(ctypes.byref(b), ctypes.c_void_p(s.cuda_stream)), "run_noalloc")
     del keep
     return out
+
+
+def history_push(hist, hist_len_dev, tokens, keep: int, stream=None) -> None:
+    """ultima_hsamp_history_push on torch tensors of one device: hist int32
+    [rows, stride] (the rows' histories), hist_len_dev int32 [rows] (their
+    lengths, advanced here), tokens int32 [rows] (appended; e.g. the token
+    output of run()). A full row first keeps its last `keep` ids."""
+    import torch
+    rows = hist.shape[0]
+    assert hist.dtype == torch.int32 and hist_len_dev.dtype == torch.int32 and tokens.dtype == torch.int32
+    assert hist_len_dev.shape[0] >= rows and tokens.shape[0] >= rows and hist.stride(1) == 1
+    s = torch.cuda.current_stream(hist.device) if stream is None else stream
+    check(lib().ultima_hsamp_history_push(ctypes.c_void_p(hist.data_ptr()), hist.stride(0),
+                                          ctypes.c_void_p(hist_len_dev.data_ptr()),
+                                          ctypes.c_void_p(tokens.data_ptr()), rows, int(keep),
+                                          ctypes.c_void_p(s.cuda_stream)), "history_push")
 
 
 def lm_head(hidden, norm_scale, eps: float, weight, logit_scale: float = 1.0, logits=None, normed=None,
@@ -300,14 +321,17 @@ class Sampler:
             pass
 
     def run(self, logits, params, u, hist=None, hist_len=None, mask=None, bias=None,
-            writeback=False, want_sets=False, set_cap=None, stream=None, outputs=None, stream_only=False):
+            writeback=False, want_sets=False, set_cap=None, stream=None, outputs=None, stream_only=False,
+            hist_len_dev=None):
         """Sample every row. logits: cuda tensor [B, >=V] float32 or bfloat16
         (row stride = logits.stride(0)); u: cuda float64 [B]; hist: cuda int32
         [B, H]; mask: cuda int32/uint32 [B, W]. Returns a dict of cuda tensors.
         `outputs` may carry preallocated tensors (token, row_flags, ...).
-        stream_only (diagnostics): run only the pass over the logits."""
+        stream_only (diagnostics): run only the pass over the logits.
+        hist_len_dev: cuda int32 [B], the rows' history lengths read on the
+        device (a history kept by history_push)."""
         b, out, keep, s = _batch(logits, params, u, hist, hist_len, mask, bias, writeback, want_sets, set_cap,
-                                 stream, outputs, stream_only)
+                                 stream, outputs, stream_only, hist_len_dev)
         check(lib().ultima_hsamp_run(self.h, ctypes.byref(b), ctypes.c_void_p(s.cuda_stream)), "run")
         del keep
         return out

@@ -1861,30 +1861,33 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
     // C, D. the ids whose final raw key lies in [Rlo, Rhi). Each wave stages
     // its own chunks whose maximum reaches Rlo (as floats: a superset of the
     // raw-key test, which orders -0 below +0) into its own LDS slots, in
-    // (chunk, lane) order from one ballot per chunk, and runs them one
-    // element per lane: no block barrier between staging and the pass.
+    // (lane, chunk) order from one wave scan of the lanes' counts, and runs
+    // them one element per lane: no block barrier between staging and the
+    // pass.
     constexpr int kCapW = kStageCap / (kBlock / 64);   // slots per wave and round
     unsigned char* wst = stg + (uint32_t)wave_id() * (uint32_t)kCapW * 32u;
     auto pass = [&](uint32_t Rlo, uint32_t Rhi) {
         const float Rf = key_to_float(Rlo);
-        // the wave's chunks at positions [rb, rb + kCapW) of its order, the
-        // positions counted as the ballots go (nothing kept per chunk)
+        // the wave's chunks at positions [rb, rb + kCapW) of its order (lane,
+        // then chunk): each lane counts its own, one wave scan places them
         auto stage = [&](int rb) -> int {
-            int off = 0;
+            int c = 0;
+#pragma unroll
+            for (int j = 0; j < NC; ++j) c += cm[j] >= Rf ? 1 : 0;
+            const int incl = wave_incl_sum_i(c);
+            const int tot = __builtin_amdgcn_readlane(incl, 63);
+            uint32_t p = (uint32_t)(incl - c - rb);
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
                 const bool in = cm[j] >= Rf;
-                const u64 m = __ballot(in);
-                const uint32_t p = __builtin_amdgcn_mbcnt_hi(
-                    (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, (uint32_t)(off - rb)));
                 if (in && p < (uint32_t)kCapW) {
                     unsigned char* sp = wst + p * 32u;
                     *reinterpret_cast<uint4*>(sp) = raw[j];
                     *reinterpret_cast<int32_t*>(sp + 16) = lo + (j * kBlock + tid) * T::VW;
                 }
-                off += __popcll(m);
+                p += in ? 1u : 0u;
             }
-            return off;
+            return tot;
         };
         HSAMP_PHASE(slot, 12);
         bool nanp = false;
@@ -2128,10 +2131,15 @@ __device__ __forceinline__ void hist_prefetch(const StreamArgs& a, const RowPlan
     const int L = hist_len_of(a, P, r);
     const int p0 = L - P.scan_len;
     const int32_t* h = a.hist + (int64_t)r * a.hist_stride;
+    // (clamped positions, no branch around a load: the eight stay in flight)
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-        const int p = p0 + q * kBlock + (int)threadIdx.x;
-        pre[q] = (pen && p < L) ? h[p] : -1;
+    for (int q = 0; q < 8; ++q) pre[q] = -1;
+    if (pen && L > 0) {
+        int32_t v[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = h[max(0, min(p0 + q * kBlock + (int)threadIdx.x, L - 1))];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) pre[q] = (p0 + q * kBlock + (int)threadIdx.x < L) ? v[q] : -1;
     }
 }
 
@@ -2841,8 +2849,10 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
 #pragma unroll
                 for (int q = 0; q < 8; ++q) {
                     const int e = e0 + q * kBlock + tid;
-                    c[q] = (e < n) ? cand[(int64_t)s2 * a.cand_cap + e] : 0ull;
+                    c[q] = cand[(int64_t)s2 * a.cand_cap + min(e, n - 1)];   // (clamped: no branch)
                 }
+#pragma unroll
+                for (int q = 0; q < 8; ++q) c[q] = (e0 + q * kBlock + tid < n) ? c[q] : 0ull;
                 offer_regs<8>(buf, ovf, a.buf_cap, k, c, st);
             }
         }
@@ -2862,8 +2872,11 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
 //    penalised: its logit is read from the row, masked, and run through
 //    stages 1-6 (sampler.cpp:235-264) with the table's counts.
 //  - Entries beyond a slice's window (rare) are offered in a second pass.
+// Three blocks per CU (at most 168 registers, a few spilled): at two, the
+// 1024-row batches of configuration 5 need two rounds of blocks (measured:
+// 293 us against 322 us per cfg5 merge; four per CU spill more, 317 us).
 template <bool GT, bool FAST, bool LM>
-__global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
+__global__ __launch_bounds__(kBlock, 3) void k_merge(StreamArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ Shared st;
     __shared__ StreamArgs sa;
@@ -3105,8 +3118,10 @@ __global__ __launch_bounds__(kBlock) void k_merge(StreamArgs a) {
 #pragma unroll
                 for (int q = 0; q < 8; ++q) {
                     const int e = e0 + q * kBlock + tid;
-                    c[q] = (e < n) ? cand[(int64_t)sl * a.cand_cap + e] : 0ull;
+                    c[q] = cand[(int64_t)sl * a.cand_cap + min(e, n - 1)];   // (clamped: no branch)
                 }
+#pragma unroll
+                for (int q = 0; q < 8; ++q) c[q] = (e0 + q * kBlock + tid < n) ? c[q] : 0ull;
                 offer_regs<8>(buf, ovf, a.buf_cap, k, c, st);
             }
         }
@@ -3241,8 +3256,10 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
 #pragma unroll
                 for (int q = 0; q < 8; ++q) {
                     const int e = e0 + q * kBlock + tid;
-                    c[q] = (e < n) ? scaled(cand[(int64_t)sl * a.cand_cap + e]) : 0ull;
+                    c[q] = cand[(int64_t)sl * a.cand_cap + min(e, n - 1)];   // (clamped: no branch)
                 }
+#pragma unroll
+                for (int q = 0; q < 8; ++q) c[q] = (e0 + q * kBlock + tid < n) ? scaled(c[q]) : 0ull;
                 offer_regs<8>(list, ovf, a.buf_cap, k, c, st);
             }
         }

@@ -42,10 +42,38 @@ def test_config4_full_batch(sampler, wl, kernel_mode):
     assert compare_rows(w, g) == 128
 
 
-def test_config5_full_batch(sampler, wl):
+def test_config5_full_batch(sampler, wl, kernel_mode):
     w = wl.config(5, seed=1)
     g = run_gpu(sampler, w)
     assert compare_rows(w, g, rows=range(0, 1024, 3)) == 342
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_exact_lists_large_k(sampler, wl, dtype, kernel_mode):
+    """Top-k above 64 in batches the exact lists take (every row samples,
+    penalties that only lower): the stream's block-level bound over its chunk
+    maxima, lists merged by the large-k merge. k at 65, in between and at the
+    1024 limit next to small k; histories of each row's top tokens (hundreds
+    of penalised candidates, some pushed below the bound); a constant row
+    (every chunk at the bound) and a rounded row (ties across slices)."""
+    rng = np.random.default_rng(77 if dtype == "f32" else 78)
+    B, V, H = 10, 151936, 512
+    x = rng.normal(0.0, 2.5, size=(B, V)).astype(np.float32)
+    x[3] = np.float32(1.0)
+    x[7] = np.round(x[7] * 2) / 2
+    hist = np.empty((B, H), np.int32)
+    for r in range(B):
+        top = np.argsort(-x[r], kind="stable")[:1200]
+        hist[r] = rng.permutation(np.concatenate([rng.choice(top, 400), rng.integers(0, V, H - 400)]))
+    ks = (65, 100, 257, 500, 1000, 1024, 1, 64, 700, 333)
+    plist = [wl.identity_params(top_k=k, temperature=float(rng.uniform(0.3, 1.5)),
+                                top_p=float(rng.choice([1.0, 0.9, 0.6])), rep_penalty=1.3, repeat_last_n=512,
+                                frequency_penalty=0.2, presence_penalty=0.4) for k in ks]
+    xs = x if dtype == "f32" else wl.to_bf16_bits(x)
+    w = _wl_from(wl, xs, plist, rng.random(B), dtype=dtype)
+    w.hist, w.hist_len = hist, np.full(B, H, np.int64)
+    g = run_gpu(sampler, w)
+    assert compare_rows(w, g) == B
 
 
 @pytest.mark.parametrize("cfg", [2, 4])

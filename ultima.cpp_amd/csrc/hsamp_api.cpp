@@ -28,6 +28,7 @@ hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, bool pen_gree
                          bool greedy_rows, bool sample_rows, int grid, hipStream_t stream);
 hipError_t launch_writeback(const StreamArgs& a, int grid, uint32_t lds, hipStream_t stream);
 hipError_t launch_merge(const StreamArgs& a, hipStream_t stream);
+hipError_t launch_pick_l(const StreamArgs& a, hipStream_t stream);
 hipError_t launch_stream_ex(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int tiles, int grid,
                             hipStream_t stream);
 hipError_t launch_pick(const StreamArgs& a, int nw, hipStream_t stream);
@@ -328,15 +329,16 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     rp = RunPlan{};
     rp.B = B;
     rp.V = V;
-    // Exact lists (k_stream's EX kernels + k_pick): every row samples with
-    // top-k <= 64 and penalties that can only lower a logit, from windows the
-    // stream's registers hold, without DRY or logit bias. The stream then
-    // leaves every candidate with its final key. ULTIMA_HSAMP_EXACT=0 turns it
-    // off (the general kernels take every batch).
+    // Exact lists (k_stream's EX kernels + k_pick, or k_pick_l when some
+    // row's top-k is above 64): every row samples with top-k <= 1024 and
+    // penalties that can only lower a logit, from windows the stream's
+    // registers hold, without DRY or logit bias. The stream then leaves every
+    // candidate with its final key. ULTIMA_HSAMP_EXACT=0 turns it off (the
+    // general kernels take every batch).
     const int kmax = std::max(1, bl.kmax);
     rp.kmax = kmax;
     rp.wb = (b->flags & ULTIMA_HSAMP_WRITEBACK) != 0;
-    bool exact_ok = bl.any_sample && !bl.any_greedy && !bl.any_full && kmax <= 64 && !rp.wb && bl.inv_ok &&
+    bool exact_ok = bl.any_sample && !bl.any_greedy && !bl.any_full && kmax <= kLimitK && !rp.wb && bl.inv_ok &&
                     (!bl.any_pen || (bl.pen_lowers && !bl.any_dry && bl.max_bias == 0 && bl.max_scan <= 8 * kBlock));
     if (const char* ev = std::getenv("ULTIMA_HSAMP_EXACT")) exact_ok = exact_ok && ev[0] != '0';
     // 16-byte loads: aligned rows holding at least one whole chunk
@@ -350,16 +352,15 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     // those slicings, the one whose busiest CU streams the fewest ids, with
     // a block's fixed work counted as kFixedIds ids (blocks spread evenly).
     const int tiles = (V + kTile - 1) / kTile;
+    const int S2 = (V + 2 * kTile - 1) / (2 * kTile);
     int S = std::max(1, std::min({kTargetBlocks / B, tiles, kBlock}));
+    int forced_tiles = 0;
+    if (const char* et = std::getenv("ULTIMA_HSAMP_EXACT_TILES")) forced_tiles = std::atoi(et) == 2 ? 2 : 1;
     if (exact_ok && vec_rows) {
         constexpr int64_t kFixedIds = 4096;
-        const int S2 = (V + 2 * kTile - 1) / (2 * kTile);
         int want = ((int64_t)B * S2 >= kTwoTileBlocks && S2 < S) ? 2 : 1;
-        bool forced = false;
-        if (const char* et = std::getenv("ULTIMA_HSAMP_EXACT_TILES")) {
-            want = std::atoi(et) == 2 ? 2 : 1;
-            forced = true;   // two tiles asked for: the fewest slices
-        }
+        const bool forced = forced_tiles != 0;   // two tiles asked for: the fewest slices
+        if (forced) want = forced_tiles;
         if (want == 2) {
             int best = std::min(S, S2);
             int64_t best_cost = INT64_MAX;
@@ -375,6 +376,9 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
             S = best;
         }
     }
+    // Large batches: exact lists still need slices their registers hold (two
+    // tiles of aligned rows, else one), so they take at least that many.
+    if (exact_ok) S = std::max(S, (vec_rows && forced_tiles != 1) ? S2 : tiles);
     // diagnostics: a forced slice count (as many slices as the kernels allow)
     if (const char* fs = std::getenv("ULTIMA_HSAMP_SLICES")) S = std::max(1, std::min(std::atoi(fs), kBlock));
     const int slice_len = ((V + S - 1) / S + 31) & ~31;
@@ -449,8 +453,14 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     rp.cnt_bytes = (bl.any_pen || !vec_rows) ? align16(2 * ((size_t)slice_len + 8)) : 0;
     rp.stage_off = rp.cnt_bytes + align16(4 * (size_t)bitmap_words);
     rp.lds_ex = rp.stage_off + 32 * (size_t)kBlock;
-    // k_pick: each slice's first W entries, NW per thread; W about twice k
-    if (exact) {
+    // k_pick: each slice's first W entries, NW per thread; W about twice k.
+    // k_pick_l (some top-k above 64): every entry through the candidate
+    // buffer, [finalize scratch][buffer] as the general merge lays them out.
+    if (exact && kmax > 64) {
+        rp.win = 1;
+        merge_lds = align16(regionF) + 8 * (size_t)buf_cap;
+        if (rp.lds_ex + statik > dc.lds_limit || merge_lds + statik > dc.lds_limit) exact = false;
+    } else if (exact) {
         const int w0 = std::min(cand_cap, std::max(32, (2 * kmax + 31) / 32 * 32));
         const int need = (S * w0 + kBlock - 1) / kBlock;
         rp.pick_nw = need <= 4 ? 4 : need <= 8 ? 8 : need <= 12 ? 12 : 16;
@@ -547,7 +557,8 @@ int launch_run(const RunPlan& rp, const Built& bl, const ultima_hsamp_batch* b, 
                               bl.any_greedy, bl.any_sample, rp.grid, stream));
     if (phase_ev != nullptr) HIP_TRY(hipEventRecord(phase_ev, stream));
     if (!(b->flags & ULTIMA_HSAMP_STREAM_ONLY)) {
-        if (rp.exact) HIP_TRY(launch_pick(a, rp.pick_nw, stream));
+        if (rp.exact && rp.kmax > 64) HIP_TRY(launch_pick_l(a, stream));
+        else if (rp.exact) HIP_TRY(launch_pick(a, rp.pick_nw, stream));
         else if (bl.any_topk) HIP_TRY(launch_merge(a, stream));
         if (bl.any_full) HIP_TRY(launch_full(a, (uint32_t)rp.full_lds, stream));
         if (rp.wb) HIP_TRY(launch_writeback(a, rp.grid, (uint32_t)rp.wb_lds, stream));
@@ -727,8 +738,11 @@ int ultima_hsamp_create(int device, int32_t max_rows, int32_t max_vocab, ultima_
     } while (0)
     CREATE_TRY(hipStreamCreateWithFlags(&h->own_stream, hipStreamNonBlocking));
     for (auto& s : h->slots) CREATE_TRY(hipEventCreateWithFlags(&s.ev, hipEventDisableTiming));
-    // Per-slice counts: rows * slices <= max(kTargetBlocks, max_rows) blocks.
-    const size_t blocks = std::max<size_t>(kTargetBlocks + 8, (size_t)max_rows);
+    // Per-slice counts (8 bytes a slice): at most max(kTargetBlocks,
+    // max_rows) slices on the general kernels, up to a slice per tile of
+    // every row on the exact lists.
+    const size_t tiles = ((size_t)max_vocab + kTile - 1) / kTile;
+    const size_t blocks = std::max<size_t>(kTargetBlocks + 8, (size_t)max_rows * tiles + 8);
     CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->cand_n), blocks * 8));
     h->cand_slots = blocks;
     CREATE_TRY(hipMalloc(reinterpret_cast<void**>(&h->fin_idx), (size_t)max_rows * kLimitK * 4));

@@ -1722,6 +1722,56 @@ __device__ __forceinline__ uint32_t final_raw_key(float x, int32_t t, uint32_t h
     return raw_key(y);
 }
 
+// The need-th largest of the block's chunk maxima (raw keys), low 16 bits
+// cleared: at least `need` chunks of the slice, so at least `need` ids, have a
+// maximum at or above it. Two levels of a 256-bin LDS histogram (the key's top
+// byte, then the next among the chunks in the chosen bin); the large-k form of
+// the waves' own bound (their kw-th largest lane maximum needs kw <= 64).
+template <int NC>
+__device__ uint32_t block_kth_bound16(const float (&cm)[NC], int need, Shared& st) {
+    const int tid = threadIdx.x, lane = lane_id();
+    uint32_t key[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) key[j] = raw_key(cm[j]);
+    uint32_t prefix = 0u;
+#pragma unroll
+    for (int level = 0; level < 2; ++level) {
+        const int sh = 24 - 8 * level;
+        st.hist[tid] = 0u;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < NC; ++j)
+            if (level == 0 || (key[j] >> 24) == (prefix >> 24)) atomicAdd(&st.hist[(key[j] >> sh) & 255u], 1u);
+        __syncthreads();
+        if (tid < 64) {
+            // bins from the top: lane l holds 255 - 4l .. 252 - 4l
+            const int c0 = st.hist[255 - 4 * lane], c1 = st.hist[254 - 4 * lane];
+            const int c2 = st.hist[253 - 4 * lane], c3 = st.hist[252 - 4 * lane];
+            const int s4 = c0 + c1 + c2 + c3;
+            const int incl = wave_incl_sum_i(s4);
+            const int excl = incl - s4;
+            if (lane == 0) {   // fewer than need chunks in all: every chunk qualifies
+                st.sel_d = 0;
+                st.sel_need = 1;
+            }
+            if (excl < need && need <= incl) {
+                int q, before;
+                if (excl + c0 >= need) { q = 0; before = excl; }
+                else if (excl + c0 + c1 >= need) { q = 1; before = excl + c0; }
+                else if (excl + c0 + c1 + c2 >= need) { q = 2; before = excl + c0 + c1; }
+                else { q = 3; before = excl + c0 + c1 + c2; }
+                st.sel_d = 255 - 4 * lane - q;
+                st.sel_need = need - before;
+            }
+        }
+        __syncthreads();
+        prefix |= (uint32_t)st.sel_d << sh;
+        need = st.sel_need;
+        __syncthreads();   // sel_d and the bins are read before the next level
+    }
+    return prefix;
+}
+
 // A sampling row's slice [lo, hi) with exact lists (single tile, raw[] holds
 // it); the row's last slice (last_slice) also takes the ragged end that
 // whole-chunk loads leave out.
@@ -1829,9 +1879,14 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
     for (int j = 1; j < NC; ++j) lmf = __builtin_elementwise_maximum(lmf, cm[j]);
     const uint32_t lk = raw_key(lmf);
     const int k = P.top_k;
-    const int kw = (k + 4 + 3) >> 2;   // <= 17
-    const uint32_t g4[4] = {lk, 0u, 0u, 0u};
-    const uint32_t tw = wave_kth_bound16(g4, 1, kw);
+    uint32_t tw;
+    if (k <= 64) {
+        const int kw = (k + 4 + 3) >> 2;   // <= 17
+        const uint32_t g4[4] = {lk, 0u, 0u, 0u};
+        tw = wave_kth_bound16(g4, 1, kw);
+    } else {
+        tw = block_kth_bound16(cm, k + 4, st);   // (the same for every wave)
+    }
     if (lane == 0) st.twave[wave_id()] = tw;
     HSAMP_PHASE(slot, 11);
     // the ragged end (the row's last slice): read while the bound settles
@@ -3412,6 +3467,78 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
     HSAMP_PHASE(8192 + r, 5);
 }
 
+// ---- the merge of exact lists, large k ---------------------------------------------
+
+// One block per sampling row whose slices left exact lists with 64 < k <= 1024
+// (the exact stream's block-level bound): every entry of the row's lists, its
+// final raw key scaled by the row's temperature, is offered into the LDS
+// candidate buffer under a rising threshold (a per-row overflow area past
+// it), then the exact top-k and the rest of the ladder as the general merge
+// finishes its rows (select_and_finalize: radix select, finalize_row). The
+// lists are final: no history, no logit reads, no ragged end (the stream's
+// last slice took it). LDS: [finalize scratch][candidate buffer].
+__global__ __launch_bounds__(kBlock, 3) void k_pick_l(StreamArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ Shared st;
+    __shared__ StreamArgs sa;
+    __shared__ RowPlan sP;
+    const int tid = threadIdx.x;
+    const int S = a.nslices;
+    const int x = (int)(blockIdx.x % kXcds);
+    const int r0 = min(a.rows, div_slices(x * a.blocks_per_xcd + S - 1, a));
+    const int r1 = min(a.rows, div_slices((x + 1) * a.blocks_per_xcd + S - 1, a));
+    const int r = r0 + (int)(blockIdx.x / kXcds);
+    if (r >= r1) return;
+    const u64* cand = a.cand + (int64_t)r * S * a.cand_cap;
+    const int cnt_raw = (tid < S) ? a.cand_n[(int64_t)r * S + tid] : 0;
+    const RowPlan P = a.plans[r];
+    const double ur = a.u[r];
+    const float inv_t = P.inv_temp;
+    if (tid == 0) {
+        st.flags = 0;
+        st.n = 0;
+        st.theta = kThetaFloor;
+        st.u = ur;
+        sa = a;
+        sP = P;
+    }
+    if (tid < 32) st.expT[tid] = kExpT[tid];
+    __syncthreads();
+    if (tid < S) {
+        st.soff[tid] = cnt_raw & 0x1FFFFFFF;
+        if (cnt_raw & (1 << 30)) atomicOr(&st.flags, 4);   // a NaN logit in the slice
+    }
+    __syncthreads();
+    const int k = P.top_k;
+    u64* buf = reinterpret_cast<u64*>(smem + (a.merge_lds - (uint32_t)a.buf_cap * 8u));
+    u64* ovf = a.ovf + (int64_t)r * a.ovf_cap;
+    auto scaled = [&](u64 c) -> u64 {
+        return ((u64)scaled_key((uint32_t)(c >> 32), inv_t) << 32) | (c & 0xFFFFFFFFull);
+    };
+    for (int sl = 0; sl < S; ++sl) {
+        const int n = st.soff[sl];
+        const u64* lst = cand + (int64_t)sl * a.cand_cap;
+        for (int e0 = 0; e0 < n; e0 += 8 * kBlock) {
+            u64 c[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) c[q] = lst[min(e0 + q * kBlock + tid, n - 1)];   // (clamped: no branch)
+#pragma unroll
+            for (int q = 0; q < 8; ++q) c[q] = (e0 + q * kBlock + tid < n) ? scaled(c[q]) : 0ull;
+            offer_regs<8>(buf, ovf, a.buf_cap, k, c, st);
+        }
+    }
+    __syncthreads();
+    const uint32_t rflags = (st.flags & 4) ? ROWF_NAN : 0u;
+    FinLds f;
+    f.sortk = buf;
+    f.fidx = reinterpret_cast<int32_t*>(smem);
+    f.fv = reinterpret_cast<float*>(f.fidx + a.kmax);
+    f.fe = f.fv + a.kmax;
+    f.fp = f.fe;
+    f.keep = reinterpret_cast<uint8_t*>(f.fe + a.kmax);
+    select_and_finalize(sa, sP, r, buf, f, st, rflags);
+}
+
 // ---- writeback -------------------------------------------------------------------
 
 template <bool GT>
@@ -4130,6 +4257,11 @@ hipError_t launch_pick(const StreamArgs& a, int nw, hipStream_t stream) {
         case 12: hipLaunchKernelGGL((k_pick<12>), g, b, a.merge_lds, stream, a); break;
         default: hipLaunchKernelGGL((k_pick<16>), g, b, a.merge_lds, stream, a); break;
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_pick_l(const StreamArgs& a, hipStream_t stream) {
+    hipLaunchKernelGGL(k_pick_l, dim3(row_blocks(a)), dim3(kBlock), a.merge_lds, stream, a);
     return hipGetLastError();
 }
 

@@ -355,12 +355,21 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     const int S2 = (V + 2 * kTile - 1) / (2 * kTile);
     int S = std::max(1, std::min({kTargetBlocks / B, tiles, kBlock}));
     int forced_tiles = 0;
-    if (const char* et = std::getenv("ULTIMA_HSAMP_EXACT_TILES")) forced_tiles = std::atoi(et) == 2 ? 2 : 1;
+    if (const char* et = std::getenv("ULTIMA_HSAMP_EXACT_TILES")) {
+        const int t = std::atoi(et);
+        forced_tiles = t == 4 ? 4 : t == 2 ? 2 : 1;
+    }
+    // bf16 rows: four tiles of them take the registers two f32 tiles take
+    const int max_tiles = (vec_rows && b->dtype == ULTIMA_HSAMP_BF16) ? 4 : vec_rows ? 2 : 1;
+    const int S4 = (V + 4 * kTile - 1) / (4 * kTile);
+    // exact lists with top-k above 64 (bf16): the largest slices, fewest lists
+    const bool four = exact_ok && max_tiles == 4 && (forced_tiles == 4 || (forced_tiles == 0 && kmax > 64));
     if (exact_ok && vec_rows) {
         constexpr int64_t kFixedIds = 4096;
         int want = ((int64_t)B * S2 >= kTwoTileBlocks && S2 < S) ? 2 : 1;
         const bool forced = forced_tiles != 0;   // two tiles asked for: the fewest slices
-        if (forced) want = forced_tiles;
+        if (forced) want = std::min(forced_tiles, 2);
+        if (four) want = 1;   // (set below)
         if (want == 2) {
             int best = std::min(S, S2);
             int64_t best_cost = INT64_MAX;
@@ -379,6 +388,7 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     // Large batches: exact lists still need slices their registers hold (two
     // tiles of aligned rows, else one), so they take at least that many.
     if (exact_ok) S = std::max(S, (vec_rows && forced_tiles != 1) ? S2 : tiles);
+    if (four) S = S4;
     // diagnostics: a forced slice count (as many slices as the kernels allow)
     if (const char* fs = std::getenv("ULTIMA_HSAMP_SLICES")) S = std::max(1, std::min(std::atoi(fs), kBlock));
     const int slice_len = ((V + S - 1) / S + 31) & ~31;
@@ -444,8 +454,8 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     const int nblocks = B * S;
     rp.grid = (nblocks + kXcds - 1) / kXcds * kXcds;
     rp.win = std::max(1, std::min(cand_cap, kMergeWindow / S));
-    rp.ex_tiles = slice_len > kTile ? 2 : 1;
-    bool exact = exact_ok && slice_len <= kTile * rp.ex_tiles && (rp.ex_tiles == 1 || vec_rows);
+    rp.ex_tiles = slice_len > 2 * kTile ? 4 : slice_len > kTile ? 2 : 1;
+    bool exact = exact_ok && slice_len <= kTile * rp.ex_tiles && rp.ex_tiles <= max_tiles;
     // k_stream EX: [count entries, 2 B per slice id + 8 (penalties)][allowed-id mask words]
     // [staged chunks: kBlock slots of 32 B (16 B data, the chunk's first id)]
     // (the general instantiations for unaligned rows take PEN = true: their

@@ -2027,7 +2027,7 @@ __device__ __forceinline__ int div_slices(int g, const StreamArgs& a) {
 }
 
 template <int DT, bool VEC, bool PEN, bool MASK, bool GR, int EX = 0>
-__global__ __launch_bounds__(kBlock, EX == 2 ? 4 : 5) void k_stream(StreamArgs a) {
+__global__ __launch_bounds__(kBlock, EX >= 2 ? 4 : 5) void k_stream(StreamArgs a) {
     using T = Tile<DT>;
     constexpr int NT = EX > 1 ? EX : 1;        // tiles per slice (exact lists: 1 or 2)
     constexpr int NC = T::NCH * NT;            // chunks per thread
@@ -4196,7 +4196,7 @@ static void launch_stream_kind(const StreamArgs& a, int dtype, bool vec, bool pe
 }
 
 // Exact lists: the sampling kernel with final keys (every row samples), slices
-// of one tile, or of two (aligned rows).
+// of one tile, or of two (aligned rows), or of four (aligned bf16 rows).
 template <int NT>
 static void launch_stream_exact(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int grid,
                                 hipStream_t stream) {
@@ -4209,12 +4209,14 @@ static void launch_stream_exact(const StreamArgs& a, int dtype, bool vec, bool p
             else HSAMP_STREAM(1, false, true, true);
         }
     } else if (dtype == 0) {
-        if (pen) {
-            if (mask) HSAMP_STREAM(0, true, true, true);
-            else HSAMP_STREAM(0, true, true, false);
-        } else {
-            if (mask) HSAMP_STREAM(0, true, false, true);
-            else HSAMP_STREAM(0, true, false, false);
+        if constexpr (NT <= 2) {   // (four f32 tiles would not fit the registers)
+            if (pen) {
+                if (mask) HSAMP_STREAM(0, true, true, true);
+                else HSAMP_STREAM(0, true, true, false);
+            } else {
+                if (mask) HSAMP_STREAM(0, true, false, true);
+                else HSAMP_STREAM(0, true, false, false);
+            }
         }
     } else {
         if (pen) {
@@ -4231,8 +4233,12 @@ static void launch_stream_exact(const StreamArgs& a, int dtype, bool vec, bool p
 hipError_t launch_stream_ex(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int tiles, int grid,
                             hipStream_t stream) {
     // two-tile slices are for aligned rows only (the host never asks otherwise)
-    if (tiles == 2 && !vec) return hipErrorInvalidValue;
-    if (tiles == 2) launch_stream_exact<2>(a, dtype, vec, pen, mask, grid, stream);
+    // (four-tile slices: aligned bf16 rows only, whose four tiles take the
+    // registers two f32 tiles take)
+    if (tiles > 1 && !vec) return hipErrorInvalidValue;
+    if (tiles == 4 && dtype == 0) return hipErrorInvalidValue;
+    if (tiles == 4) launch_stream_exact<4>(a, dtype, vec, pen, mask, grid, stream);
+    else if (tiles == 2) launch_stream_exact<2>(a, dtype, vec, pen, mask, grid, stream);
     else launch_stream_exact<1>(a, dtype, vec, pen, mask, grid, stream);
     return hipGetLastError();
 }

@@ -1722,26 +1722,58 @@ __device__ __forceinline__ uint32_t final_raw_key(float x, int32_t t, uint32_t h
     return raw_key(y);
 }
 
-// The need-th largest of the block's chunk maxima (raw keys), low 16 bits
-// cleared: at least `need` chunks of the slice, so at least `need` ids, have a
-// maximum at or above it. Two levels of a 256-bin LDS histogram (the key's top
-// byte, then the next among the chunks in the chosen bin); the large-k form of
-// the waves' own bound (their kw-th largest lane maximum needs kw <= 64).
+// A lower bound on the need-th largest of the block's chunk maxima (raw
+// keys): at least `need` chunks of the slice, so at least `need` ids, have a
+// maximum at or above it. Two levels of a 256-bin LDS histogram over the bits
+// below those all finite maxima share (the block's key range), the second
+// within the first's chosen bin; the bound keeps those 16 bits (or all, when
+// the range is narrower). Binning by the varying bits keeps the bins' LDS
+// atomics apart: the top byte alone (sign and high exponent bits) puts nearly
+// every maximum in one or two bins, whose atomics then serialise. The
+// large-k form of the waves' own bound (their kw-th largest lane maximum
+// needs kw <= 64).
 template <int NC>
 __device__ uint32_t block_kth_bound16(const float (&cm)[NC], int need, Shared& st) {
     const int tid = threadIdx.x, lane = lane_id();
     uint32_t key[NC];
+    uint32_t lmx = 0u, lmn = 0xFFFFFFFFu;
 #pragma unroll
-    for (int j = 0; j < NC; ++j) key[j] = raw_key(cm[j]);
-    uint32_t prefix = 0u;
+    for (int j = 0; j < NC; ++j) {
+        key[j] = raw_key(cm[j]);
+        if (key[j] > kKeyNegInf) {
+            lmx = max(lmx, key[j]);
+            lmn = min(lmn, key[j]);
+        }
+    }
+    lmx = wave_max_u32(lmx);
+    lmn = wave_min_u32(lmn);
+    if (lane == 0) {
+        st.twave[wave_id()] = lmn;
+        st.minv_w[wave_id()] = lmx;
+    }
+    __syncthreads();
+    uint32_t kmn = st.twave[0], kmx = (uint32_t)st.minv_w[0];
 #pragma unroll
-    for (int level = 0; level < 2; ++level) {
-        const int sh = 24 - 8 * level;
+    for (int i = 1; i < kBlock / 64; ++i) {
+        kmn = min(kmn, st.twave[i]);
+        kmx = max(kmx, (uint32_t)st.minv_w[i]);
+    }
+    if (kmx < kmn) return 0u;   // no finite maximum: every chunk qualifies
+    const int hb = (kmx > kmn) ? 31 - __clz((int)(kmn ^ kmx)) : 0;
+    const int sh1 = max(0, hb - 7), sh2 = max(0, sh1 - 8);
+    const uint32_t top = hb >= 31 ? 0u : (kmx >> (hb + 1)) << (hb + 1);   // the shared bits
+    uint32_t prefix = top;
+    const int levels = sh1 > 0 ? 2 : 1;
+    for (int level = 0; level < levels; ++level) {
+        const int sh = level == 0 ? sh1 : sh2;
+        const uint32_t b1 = level == 0 ? 0u : (prefix >> sh1) & 255u;
         st.hist[tid] = 0u;
         __syncthreads();
 #pragma unroll
-        for (int j = 0; j < NC; ++j)
-            if (level == 0 || (key[j] >> 24) == (prefix >> 24)) atomicAdd(&st.hist[(key[j] >> sh) & 255u], 1u);
+        for (int j = 0; j < NC; ++j) {
+            const bool in = key[j] >= kmn && (level == 0 || ((key[j] >> sh1) & 255u) == b1);
+            if (in) atomicAdd(&st.hist[(key[j] >> sh) & 255u], 1u);
+        }
         __syncthreads();
         if (tid < 64) {
             // bins from the top: lane l holds 255 - 4l .. 252 - 4l
@@ -1750,10 +1782,7 @@ __device__ uint32_t block_kth_bound16(const float (&cm)[NC], int need, Shared& s
             const int s4 = c0 + c1 + c2 + c3;
             const int incl = wave_incl_sum_i(s4);
             const int excl = incl - s4;
-            if (lane == 0) {   // fewer than need chunks in all: every chunk qualifies
-                st.sel_d = 0;
-                st.sel_need = 1;
-            }
+            if (lane == 0) st.sel_d = -1;   // fewer than need at or above kmn
             if (excl < need && need <= incl) {
                 int q, before;
                 if (excl + c0 >= need) { q = 0; before = excl; }
@@ -1765,9 +1794,11 @@ __device__ uint32_t block_kth_bound16(const float (&cm)[NC], int need, Shared& s
             }
         }
         __syncthreads();
-        prefix |= (uint32_t)st.sel_d << sh;
+        const int d = st.sel_d;
         need = st.sel_need;
         __syncthreads();   // sel_d and the bins are read before the next level
+        if (d < 0) return 0u;   // too few finite maxima: every chunk qualifies
+        prefix |= (uint32_t)d << sh;
     }
     return prefix;
 }

@@ -45,7 +45,7 @@ PEAK_GBS = 8000.0
 N_SETS = 8
 # the kernel that reads the logits, and the per-row kernel after it, by configuration
 STREAM_KERNEL = {1: "k_stream", 2: "k_stream", 3: "k_full", 4: "k_stream", 5: "k_stream"}
-ROW_KERNEL = {1: "k_pick", 2: "k_pick", 3: None, 4: "k_pick", 5: "k_merge"}
+ROW_KERNEL = {1: "k_pick", 2: "k_pick", 3: None, 4: "k_pick", 5: "k_pick_l"}
 
 
 def parse():

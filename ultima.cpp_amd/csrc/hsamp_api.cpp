@@ -400,8 +400,9 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     // k_merge's LDS candidate buffer: room for 2k (k <= 64), for 4k up to
     // 4096 entries above (each compaction keeps k of them; the general
     // merge's register budget allows two blocks per CU, so LDS is not what
-    // limits it)
-    const int buf_cap = kmax > 64 ? std::min(4096, std::max(512, next_pow2(4 * kmax)))
+    // limits it), and at least the 1024 entries the finalize's sorts
+    // exchange through
+    const int buf_cap = kmax > 64 ? std::min(4096, std::max(1024, next_pow2(4 * kmax)))
                                   : std::max(512, next_pow2(2 * kmax));
     const int cand_cap = slice_len;                 // a slice's list holds all its ids
     const int bitmap_words = slice_len / 32;
@@ -468,7 +469,13 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     // buffer, [finalize scratch][buffer] as the general merge lays them out.
     if (exact && kmax > 64) {
         rp.win = 1;
-        merge_lds = align16(regionF) + 8 * (size_t)buf_cap;
+        // four k_pick_l blocks per CU: a quarter of the CU's 160 KB for the
+        // finalize scratch and a buffer of at least 2k entries (each
+        // compaction keeps k), else the general merge's 4k
+        const size_t quarter = (size_t)(160 * 1024 / 4) - statik - align16(regionF);
+        const int cap4 = (int)(quarter / 8) & ~15;
+        if (cap4 >= std::max(1024, 2 * kmax) && cap4 < buf_cap) rp.buf_cap = cap4;
+        merge_lds = align16(regionF) + 8 * (size_t)rp.buf_cap;
         if (rp.lds_ex + statik > dc.lds_limit || merge_lds + statik > dc.lds_limit) exact = false;
     } else if (exact) {
         const int w0 = std::min(cand_cap, std::max(32, (2 * kmax + 31) / 32 * 32));

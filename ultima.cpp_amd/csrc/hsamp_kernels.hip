@@ -388,31 +388,73 @@ __device__ void drain_overflow(u64* buf, int cap, int k, const u64* ovf, Shared&
     append_fetch(buf, cap, k, n - cap, [&](int j) { return ovf[j]; }, st);
 }
 
-// Bitonic sort of P (a power of two) keys in LDS by the block. Thread t takes
-// compare-exchange pairs t, t + kBlock, ...; a pair of stage j joins entry i
-// (bit j clear) with i | j. For j <= 64 the pairs of one wave stay inside its
-// own 128-entry blocks, so consecutive such stages need only the wave's own
-// ordering; block barriers surround the stages with j >= 128.
-__device__ __attribute__((noinline)) void bitonic_sort(u64* a, int P, bool descending) {
-    const int half = P >> 1;
-    for (int k = 2; k <= P; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int t = threadIdx.x; t < half; t += kBlock) {
-                const int i = ((t & ~(j - 1)) << 1) | (t & (j - 1));
-                const int l = i | j;
-                const u64 x = a[i], y = a[l];
-                const bool up = ((i & k) == 0) != descending;
-                if ((x > y) == up) {
-                    a[i] = y;
-                    a[l] = x;
-                }
+// The 64-bit value of lane (lane ^ M): DPP quad permutes for M = 1, 2, the
+// swizzle's xor mode (within 32 lanes, no LDS memory) up to 16, a permute
+// for 32.
+template <int M>
+__device__ __forceinline__ uint32_t xor_lane_u32(uint32_t x) {
+    if constexpr (M == 1) return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xF, 0xF, false);
+    else if constexpr (M == 2) return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x4E, 0xF, 0xF, false);
+    else if constexpr (M <= 16) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)x, (M << 10) | 0x1F);
+    else return (uint32_t)__shfl_xor((int)x, M, 64);
+}
+template <int M>
+__device__ __forceinline__ u64 xor_lane_u64(u64 x) {
+    return ((u64)xor_lane_u32<M>((uint32_t)(x >> 32)) << 32) | xor_lane_u32<M>((uint32_t)x);
+}
+
+// Bitonic sort of 1024 keys held four per thread in registers (thread t:
+// entries 4t .. 4t+3). A stage of distance J joins entry i with i ^ J: J <= 2
+// inside a thread, 4 <= J <= 128 between the lanes of a wave (lane distance
+// J / 4), J = 256, 512 between waves through x[0 .. 1024) in LDS with block
+// barriers. Of each pair the lower entry keeps the minimum when the bitonic
+// run of size K containing it ascends (DESC flips every run).
+template <bool DESC, int K, int J>
+__device__ __forceinline__ void rsort_stage(u64 (&v)[4], u64* x) {
+    const int t = threadIdx.x;
+    if constexpr (J <= 2) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if ((q & J) == 0) {
+                const bool up = (((4 * t + q) & K) == 0) != DESC;
+                const u64 a = v[q], b = v[q | J];
+                const bool sw = (a > b) == up;
+                v[q] = sw ? b : a;
+                v[q | J] = sw ? a : b;
             }
-            const int jn = j > 1 ? j >> 1 : (2 * k <= P ? k : 0);   // the next stage's j (0: done)
-            if (j >= 128 || jn >= 128 || jn == 0) __syncthreads();
-            else wave_sync();
+        }
+    } else {
+        constexpr int M = J / 4;   // partner thread t ^ M
+        u64 o[4];
+        if constexpr (M < 64) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) o[q] = xor_lane_u64<M>(v[q]);
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) x[4 * t + q] = v[q];
+            __syncthreads();
+#pragma unroll
+            for (int q = 0; q < 4; ++q) o[q] = x[4 * (t ^ M) + q];
+            __syncthreads();
+        }
+        const bool lower = (t & M) == 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const bool up = (((4 * t + q) & K) == 0) != DESC;
+            const bool lt = o[q] < v[q];
+            v[q] = (lt == (lower == up)) ? o[q] : v[q];
         }
     }
-    if (P < 2) __syncthreads();
+}
+template <bool DESC, int K, int J>
+__device__ __forceinline__ void rsort_steps(u64 (&v)[4], u64* x) {
+    rsort_stage<DESC, K, J>(v, x);
+    if constexpr (J > 1) rsort_steps<DESC, K, J / 2>(v, x);
+}
+template <bool DESC, int K = 2>
+__device__ __forceinline__ void rsort1024(u64 (&v)[4], u64* x) {
+    rsort_steps<DESC, K, K / 2>(v, x);
+    if constexpr (K < 1024) rsort1024<DESC, 2 * K>(v, x);
 }
 
 __device__ __forceinline__ int next_pow2(int x) {
@@ -549,7 +591,7 @@ __device__ __forceinline__ float elem(const uint4& r, int c) {
 // ---- finalize over the kept set ------------------------------------------------
 
 struct FinLds {
-    u64* sortk;     // [P2] sort keys, then the double q_i (k_merge: the candidate buffer itself)
+    u64* sortk;     // [1024] sort keys, then the double q_i (the candidate buffer itself)
     int32_t* fidx;  // [kmax] kept ids, index order
     float* fv;      // values (post-temperature)
     float* fe;      // expf(v - m), replaced in place by the probabilities
@@ -676,17 +718,28 @@ __device__ __attribute__((noinline)) void finalize_row(const StreamArgs& a, cons
     int32_t tok = 0;
     int nkept = nk;
     if (nk > 0) {
-        const int P2 = next_pow2(nk);
-        for (int i = tid; i < P2; i += kBlock)
-            f.sortk[i] = (i < nk) ? (((u64)(uint32_t)comp_idx(buf[i]) << 32) | (buf[i] >> 32)) : ~0ull;
-        __syncthreads();
-        bitonic_sort(f.sortk, P2, false);
-        HSAMP_PHASE(9500 + r, 6);
-        for (int j = tid; j < nk; j += kBlock) {
-            const u64 e = f.sortk[j];
-            f.fidx[j] = (int32_t)(e >> 32);
-            f.fv[j] = key_to_float((uint32_t)e);
-            f.keep[j] = 1;
+        // index order: (id, key) pairs sorted in registers (nk <= 1024; the
+        // sort's LDS exchange reuses the first 1024 entries of the buffer)
+        {
+            u64 v[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int i = 4 * tid + q;
+                const u64 c = buf[min(i, nk - 1)];
+                v[q] = (i < nk) ? (((u64)(uint32_t)comp_idx(c) << 32) | (c >> 32)) : ~0ull;
+            }
+            __syncthreads();
+            rsort1024<false>(v, f.sortk);
+            HSAMP_PHASE(9500 + r, 6);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int j = 4 * tid + q;
+                if (j < nk) {
+                    f.fidx[j] = (int32_t)(v[q] >> 32);
+                    f.fv[j] = key_to_float((uint32_t)v[q]);
+                    f.keep[j] = 1;
+                }
+            }
         }
         __syncthreads();
         if (a.topk_idx != nullptr) {
@@ -699,13 +752,22 @@ __device__ __attribute__((noinline)) void finalize_row(const StreamArgs& a, cons
         HSAMP_PHASE(9500 + r, 7);
         bool fresh = true;  // fp matches the current kept set
         if (have && (P.flags & RF_TOPP)) {
-            // sampler.cpp:146-164
-            for (int i = tid; i < P2; i += kBlock)
-                f.sortk[i] = (i < nk && f.keep[i])
-                                 ? (((u64)key32(f.fp[i]) << 32) | (u64)(0xFFFFFFFFu - (uint32_t)i))
-                                 : 0ull;
+            // sampler.cpp:146-164: (probability, -position) descending
+            {
+                u64 v[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int i = 4 * tid + q;
+                    const int ic = min(i, nk - 1);
+                    v[q] = (i < nk && f.keep[ic])
+                               ? (((u64)key32(f.fp[ic]) << 32) | (u64)(0xFFFFFFFFu - (uint32_t)i))
+                               : 0ull;
+                }
+                rsort1024<true>(v, f.sortk);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) f.sortk[4 * tid + q] = v[q];
+            }
             __syncthreads();
-            bitonic_sort(f.sortk, P2, true);
             if (tid < 64) {
                 // the running float sum in that order (entries not kept sort
                 // last as 0 and add +0)
@@ -3507,8 +3569,10 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
 // it), then the exact top-k and the rest of the ladder as the general merge
 // finishes its rows (select_and_finalize: radix select, finalize_row). The
 // lists are final: no history, no logit reads, no ragged end (the stream's
-// last slice took it). LDS: [finalize scratch][candidate buffer].
-__global__ __launch_bounds__(kBlock, 3) void k_pick_l(StreamArgs a) {
+// last slice took it). LDS: [finalize scratch][candidate buffer], sized by
+// the host so that four blocks share a CU (with 128 registers per lane, four
+// waves per SIMD): a batch of up to 1024 such rows runs in one round.
+__global__ __launch_bounds__(kBlock, 4) void k_pick_l(StreamArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ Shared st;
     __shared__ StreamArgs sa;
@@ -3520,6 +3584,7 @@ __global__ __launch_bounds__(kBlock, 3) void k_pick_l(StreamArgs a) {
     const int r1 = min(a.rows, div_slices((x + 1) * a.blocks_per_xcd + S - 1, a));
     const int r = r0 + (int)(blockIdx.x / kXcds);
     if (r >= r1) return;
+    HSAMP_PHASE(9500 + r, 0);
     const u64* cand = a.cand + (int64_t)r * S * a.cand_cap;
     const int cnt_raw = (tid < S) ? a.cand_n[(int64_t)r * S + tid] : 0;
     const RowPlan P = a.plans[r];
@@ -3559,6 +3624,7 @@ __global__ __launch_bounds__(kBlock, 3) void k_pick_l(StreamArgs a) {
         }
     }
     __syncthreads();
+    HSAMP_PHASE(9500 + r, 4);
     const uint32_t rflags = (st.flags & 4) ? ROWF_NAN : 0u;
     FinLds f;
     f.sortk = buf;

@@ -55,14 +55,15 @@ def sampler(hs):
     s.close()
 
 
-@pytest.fixture(params=["default", "exact", "exact2", "general"])
+@pytest.fixture(params=["default", "exact", "exact2", "exact4", "general"])
 def kernel_mode(request, monkeypatch):
-    """Runs a test four times: with the library's own choice of kernels and
+    """Runs a test five times: with the library's own choice of kernels and
     slicing (no override: what every caller and bench.py get), with exact
-    lists over slices of one tile, with exact lists over slices of two tiles
-    (ULTIMA_HSAMP_EXACT_TILES, the fewest slices; aligned rows only, others
-    keep one tile), and with ULTIMA_HSAMP_EXACT=0, which sends every batch to
-    the general stream and merge kernels."""
+    lists over slices of one tile, of two tiles and of four tiles
+    (ULTIMA_HSAMP_EXACT_TILES, the fewest slices; four: aligned bf16 rows,
+    whose history counts are then kept by rank; two: other aligned rows;
+    unaligned rows keep one tile), and with ULTIMA_HSAMP_EXACT=0, which sends
+    every batch to the general stream and merge kernels."""
     monkeypatch.delenv("ULTIMA_HSAMP_EXACT", raising=False)
     monkeypatch.delenv("ULTIMA_HSAMP_SLICES", raising=False)
     if request.param == "default":
@@ -71,5 +72,5 @@ def kernel_mode(request, monkeypatch):
         monkeypatch.setenv("ULTIMA_HSAMP_EXACT", "0")
         monkeypatch.delenv("ULTIMA_HSAMP_EXACT_TILES", raising=False)
     else:
-        monkeypatch.setenv("ULTIMA_HSAMP_EXACT_TILES", "2" if request.param == "exact2" else "1")
+        monkeypatch.setenv("ULTIMA_HSAMP_EXACT_TILES", {"exact2": "2", "exact4": "4"}.get(request.param, "1"))
     return request.param

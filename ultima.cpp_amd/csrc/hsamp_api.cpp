@@ -457,11 +457,19 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     rp.win = std::max(1, std::min(cand_cap, kMergeWindow / S));
     rp.ex_tiles = slice_len > 2 * kTile ? 4 : slice_len > kTile ? 2 : 1;
     bool exact = exact_ok && slice_len <= kTile * rp.ex_tiles && rp.ex_tiles <= max_tiles;
-    // k_stream EX: [count entries, 2 B per slice id + 8 (penalties)][allowed-id mask words]
-    // [staged chunks: kBlock slots of 32 B (16 B data, the chunk's first id)]
-    // (the general instantiations for unaligned rows take PEN = true: their
-    // count entries are cleared and stay zero when no row has penalties)
-    rp.cnt_bytes = (bl.any_pen || !vec_rows) ? align16(2 * ((size_t)slice_len + 8)) : 0;
+    // k_stream EX: [history counts (penalties)][allowed-id mask words]
+    // [staged chunks: kBlock slots of 32 B (16 B data, the chunk's first id)].
+    // The counts take 2 B per slice id, except in four-tile slices (whose
+    // 64 KB would hold the blocks per CU to two): there ranked, a bitmap over
+    // the slice's ids, a 2 B rank prefix per bitmap word and 2 B entries for
+    // the window's distinct ids (at most 8 * kBlock), at two more block
+    // barriers. (the general instantiations for unaligned rows take PEN =
+    // true: their counts are cleared and stay zero when no row has penalties)
+    rp.cnt_ranked = rp.ex_tiles == 4;
+    rp.cnt_bytes = !(bl.any_pen || !vec_rows) ? 0
+                   : rp.cnt_ranked ? align16(4 * (size_t)bitmap_words) + align16(2 * (size_t)bitmap_words) +
+                                         2 * 8 * (size_t)kBlock
+                                   : align16(2 * ((size_t)slice_len + 8));
     rp.stage_off = rp.cnt_bytes + align16(4 * (size_t)bitmap_words);
     rp.lds_ex = rp.stage_off + 32 * (size_t)kBlock;
     // k_pick: each slice's first W entries, NW per thread; W about twice k.

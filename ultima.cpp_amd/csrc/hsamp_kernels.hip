@@ -457,6 +457,8 @@ __device__ __forceinline__ void rsort1024(u64 (&v)[4], u64* x) {
     if constexpr (K < 1024) rsort1024<DESC, 2 * K>(v, x);
 }
 
+__device__ __forceinline__ uint32_t align16u(uint32_t x) { return (x + 15u) & ~15u; }
+
 __device__ __forceinline__ int next_pow2(int x) {
     int p = 1;
     while (p < x) p <<= 1;
@@ -1874,8 +1876,31 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
                                              bool last_slice, bool pen, bool mk, const int32_t (&pre)[8],
                                              int pbase, unsigned char* smem, Shared& st) {
     using T = Tile<DT>;
+    constexpr int NT = NC / T::NCH;   // tiles per slice
     const int tid = threadIdx.x, lane = lane_id();
-    uint16_t* cnt = reinterpret_cast<uint16_t*>(smem);
+    // History counts, 16-bit entries: one per slice id (dense), or (ranked:
+    // four-tile slices, whose dense table would take 64 KB of LDS and hold
+    // the blocks per CU to two) a bitmap over the slice's ids marks those in
+    // the scanned window and each marked id's entry sits at its rank among
+    // them (the word's rank prefix plus the bits below it in the word).
+    constexpr bool ranked = NT == 4;
+    const int bw = a.bitmap_words;
+    uint32_t* hbm = reinterpret_cast<uint32_t*>(smem);
+    uint16_t* hwr = reinterpret_cast<uint16_t*>(smem + align16u(4u * (uint32_t)bw));
+    uint32_t* hcw = ranked ? reinterpret_cast<uint32_t*>(smem + align16u(4u * (uint32_t)bw) + align16u(2u * (uint32_t)bw))
+                           : reinterpret_cast<uint32_t*>(smem);
+    auto hrank = [&](uint32_t o) -> uint32_t {
+        return (uint32_t)hwr[o >> 5] + (uint32_t)__popc(hbm[o >> 5] & ((1u << (o & 31)) - 1u));
+    };
+    // nonzero when slice offset o (< slice_len) has a count entry
+    auto hmark = [&](uint32_t o) -> uint32_t {
+        return ranked ? (hbm[o >> 5] >> (o & 31)) & 1u : (hcw[o >> 1] >> ((o & 1u) << 4)) & 0xFFFFu;
+    };
+    auto hentry = [&](uint32_t o, uint32_t mark) -> uint32_t {
+        if (!ranked || mark == 0u) return mark;
+        const uint32_t rk = hrank(o);
+        return (hcw[rk >> 1] >> ((rk & 1u) << 4)) & 0xFFFFu;
+    };
     const uint32_t* mbm = reinterpret_cast<const uint32_t*>(smem) + a.mbm_off;
     // staged chunks: 32-byte slots, 16 bytes of logits then the chunk's first id
     unsigned char* stg = smem + a.stage_off;
@@ -1890,26 +1915,50 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
     if (PEN && pen) {
         const int L = hist_len_of(a, P, r), p0 = L - P.scan_len;
         const int mhi = min(a.vocab, lo + a.slice_len);
-        uint32_t* cw = reinterpret_cast<uint32_t*>(smem);
         const uint32_t wl = (uint32_t)(L - p0), sl = (uint32_t)(mhi - lo);
-        if (one) {
+        uint32_t inw = 0u;   // bit q: pre[q] is a window id of this slice
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                const int p = pbase + q * kBlock + tid;   // pre[q]'s history position
-                const int32_t t = pre[q];
-                if ((uint32_t)(p - p0) < wl && (uint32_t)(t - lo) < sl)
-                    atomicAdd(&cw[(t - lo) >> 1], 1u << ((uint32_t)((t - lo) & 1) << 4));
+        for (int q = 0; q < 8; ++q) {
+            const int p = pbase + q * kBlock + tid;   // pre[q]'s history position
+            const uint32_t o = (uint32_t)(pre[q] - lo);
+            if ((uint32_t)(p - p0) < wl && o < sl) {
+                inw |= 1u << q;
+                if constexpr (ranked) atomicOr(&hbm[o >> 5], 1u << (o & 31));
             }
-        } else {
+        }
+        if constexpr (ranked) {
+            __syncthreads();
+            // rank prefixes of the bitmap words: thread t takes words NT t .. NT t + NT - 1
+            int c = 0;
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
+            for (int i = 0; i < NT; ++i) {
+                const int w = tid * NT + i;
+                c += w < bw ? __popc(hbm[w]) : 0;
+            }
+            int tot;
+            int base = block_excl_scan(c, &tot, st);
+#pragma unroll
+            for (int i = 0; i < NT; ++i) {
+                const int w = tid * NT + i;
+                if (w < bw) {
+                    hwr[w] = (uint16_t)base;
+                    base += __popc(hbm[w]);
+                }
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            if ((inw >> q) & 1u) {
                 const int p = pbase + q * kBlock + tid;
-                const int32_t t = pre[q];
-                if ((uint32_t)(p - p0) < wl && (uint32_t)(t - lo) < sl) {
-                    const int o = t - lo;
-                    const uint32_t sh = (uint32_t)(o & 1) << 4;
-                    if (p >= L - P.fp_win) atomicAdd(&cw[o >> 1], 1u << sh);
-                    if (p >= L - P.rep_win) atomicOr(&cw[o >> 1], XC_REP << sh);
+                const uint32_t o = (uint32_t)(pre[q] - lo);
+                const uint32_t e = ranked ? hrank(o) : o;
+                const uint32_t sh = (e & 1u) << 4;
+                if (one) {
+                    atomicAdd(&hcw[e >> 1], 1u << sh);
+                } else {
+                    if (p >= L - P.fp_win) atomicAdd(&hcw[e >> 1], 1u << sh);
+                    if (p >= L - P.rep_win) atomicOr(&hcw[e >> 1], XC_REP << sh);
                 }
             }
         }
@@ -2061,8 +2110,8 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
                 const uint32_t oc = min((uint32_t)o, (uint32_t)(a.slice_len - 1));
                 if (MASK && !((mbm[oc >> 5] >> (oc & 31)) & 1u)) x = -__builtin_inff();
                 uint32_t kf = raw_key(x);
-                const uint32_t h = PEN ? (uint32_t)cnt[oc] : 0u;
-                if (PEN && live && h != 0u && kf >= Rlo) kf = final_raw_key(x, t, h, one, a, P, nanp);
+                const uint32_t hm = PEN ? hmark(oc) : 0u;
+                if (PEN && live && hm != 0u && kf >= Rlo) kf = final_raw_key(x, t, hentry(oc, hm), one, a, P, nanp);
                 const bool keep = live && kf >= Rlo && kf < Rhi;
                 const u64 mk2 = __ballot(keep);
                 if (mk2 != 0ull) {
@@ -2078,7 +2127,7 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
             wave_sync();   // the slots are read before the next round writes them
         }
         if (tl) {
-            const uint32_t kf = final_raw_key(xt, tt_id, PEN ? (uint32_t)cnt[tt_id - lo] : 0u, one, a, P, nanp);
+            const uint32_t kf = final_raw_key(xt, tt_id, PEN ? hentry((uint32_t)(tt_id - lo), hmark((uint32_t)(tt_id - lo))) : 0u, one, a, P, nanp);
             if (kf >= Rlo && kf < Rhi) out[atomicAdd(&st.n, 1)] = comp(kf, tt_id);
         }
         if (nanp) atomicOr(&st.flags, 1);
@@ -2112,7 +2161,9 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
 // both takes one launch of each, so that each loop has the whole register
 // budget of five blocks per CU.
 // EX: exact lists (sampling rows only, see stream_exact); LDS then
-// [count entries (PEN), 2 B per slice id + 8][allowed-id mask words].
+// [history counts (PEN): 2 B per slice id, or (four-tile slices) a bitmap
+// over the slice's ids, 2 B rank prefix per bitmap word, 2 B entries for up
+// to 2048 distinct ids][allowed-id mask words][staged chunks].
 // g / nslices for block and row indices (a 32-bit reciprocal; one slice per
 // row divides by 1, which the reciprocal cannot express)
 __device__ __forceinline__ int div_slices(int g, const StreamArgs& a) {

@@ -56,6 +56,7 @@ struct RunPlan {
     int cand_cap = 0, buf_cap = 0, bitmap_words = 0, mhash = 16, win = 1, pick_nw = 16;
     int ex_tiles = 1, grid = 0, full_p2 = 1, full_stride = 0, full_g = 1;
     bool exact = false, vec = false, gtab = false, fast = false, pen_flag = false, wb = false;
+    bool cnt_ranked = false;  // exact lists: history counts by rank (a bitmap over the slice)
     size_t lds = 0, lds_ex = 0, merge_lds = 0, full_lds = 0, wb_lds = 0, cnt_bytes = 0, stage_off = 0;
     // scratch the kernels use
     size_t cand_elems = 0;    // u64 candidate lists, B * S * cand_cap

@@ -232,6 +232,65 @@ int ultima_hsamp_set_phase_event(ultima_hsamp* h, void* hip_event);
 int ultima_hsamp_history_push(int32_t* hist, int64_t hist_stride, int32_t* hist_len_dev, const int32_t* tokens,
                               int32_t rows, int32_t keep, void* hip_stream);
 
+/* ---- Batched callers ----------------------------------------------------------
+ * Multi-slot decode: the server's per-token loop over one sequence
+ *   next = sample(logits, params, sctx); if (next < 0) break;
+ *   if (next == eos || next == im_end) break; sctx.push_recent(next); ...
+ *   if (i + 1 == max_tokens) break;
+ *     /root/reference/src/server/http_server.cpp:174-201
+ * applied to every slot of a batch at once, after an ultima_hsamp_run over the
+ * slots' rows (their device histories: batch.hist, batch.hist_len_dev). For row
+ * r: if active[r] == 0 the row has ended, tokens[r] becomes -1 and nothing else
+ * changes; else if tokens[r] < 0 or is one of stop_ids[0 .. n_stop) the row ends
+ * (active[r] = 0; the token is not pushed and tokens[r] is left as sampled);
+ * else tokens[r] is appended to the row's history as ultima_hsamp_history_push
+ * does (same hist_stride / keep rules) and, when budget is not NULL,
+ * budget[r] is decremented and the row ends when it reaches 0 (max_tokens).
+ * hist, hist_len_dev, tokens, active, budget: device memory; stop_ids: HOST, at
+ * most 8. Asynchronous on hip_stream, allocates nothing (graph-capturable). */
+int ultima_hsamp_decode_commit(int32_t* hist, int64_t hist_stride, int32_t* hist_len_dev, int32_t* tokens,
+                               int32_t* active, int32_t* budget, int32_t rows, int32_t keep,
+                               const int32_t* stop_ids, int32_t n_stop, void* hip_stream);
+
+/* Block verification: the target model's logits for every position of a
+ * drafted block ([block_size][vocab] as a drafter proposes it,
+ * /root/reference/include/ultima/model/dspark.hpp:76-91; the reference's host
+ * loop for it is open, /root/reference/plan.md:196-197) turned into the tokens
+ * that the one-token-at-a-time loop above (sample(), push_recent) would emit
+ * on those logits with the same uniforms. Position i (0 <= i < n_pos) is
+ * sampled with the sequence's history extended by draft[0 .. i) and uniform
+ * u[i]; m is the first i < n_pos - 1 whose sample differs from draft[i], else
+ * n_pos - 1. out_tokens[0 .. m] = draft[0 .. m) then position m's sample (the
+ * rest -1), *out_count = m + 1. Stop tokens among them are the caller's to
+ * act on, as in the loop. */
+typedef struct ultima_hsamp_verify {
+    int32_t n_pos;              /* positions: drafted tokens + 1; 1 <= n_pos <= the handle's max_rows */
+    int32_t vocab;              /* V >= 1 */
+    int32_t dtype;              /* ULTIMA_HSAMP_F32 or ULTIMA_HSAMP_BF16 */
+    void* logits;               /* device [n_pos, logits_stride]: position i's logits */
+    int64_t logits_stride;      /* elements between positions, >= vocab */
+    const int32_t* draft;       /* device [n_pos - 1] drafted tokens (may be NULL when n_pos == 1) */
+    const int32_t* hist;        /* device [hist_len]: the sequence's recent ids before the block, oldest first */
+    int32_t hist_len;           /* >= 0 */
+    const uint32_t* mask;       /* device [n_pos, mask_stride] allowed-token words or NULL */
+    int64_t mask_stride;
+    const double* u;            /* device [n_pos]: the uniform each position's draw takes */
+    const ultima_hsamp_params* params; /* HOST: the sequence's knobs (their hist_len is ignored) */
+    const int32_t* bias_ids;    /* HOST, as in ultima_hsamp_batch */
+    const float* bias_vals;
+    int32_t* work;              /* device, ultima_hsamp_verify_work_ints(n_pos, hist_len) int32s */
+    int32_t* out_tokens;        /* device [n_pos] out */
+    int32_t* out_count;         /* device [1] out */
+    uint32_t* row_flags;        /* device [n_pos] out or NULL: each position's ULTIMA_HSAMP_ROW_* bits */
+} ultima_hsamp_verify;
+
+/* int32s of workspace ultima_hsamp_verify_block needs (-1 for invalid sizes). */
+int64_t ultima_hsamp_verify_work_ints(int32_t n_pos, int32_t hist_len);
+
+/* Verify one block, asynchronously on hip_stream: one ultima_hsamp_run over the
+ * n_pos positions (its capture rules apply) between two small kernels. */
+int ultima_hsamp_verify_block(ultima_hsamp* h, const ultima_hsamp_verify* v, void* hip_stream);
+
 /* ---- The logits producer ----------------------------------------------------
  * The model's last step before sampling, on the device: each row's final
  * hidden state through the output rmsnorm and the lm-head matvec, written as

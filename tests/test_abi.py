@@ -100,7 +100,8 @@ def test_struct_layouts_match_the_header(pkg, tmp_path):
     hs = pkg.hsamp
     from pathlib import Path
     root = Path(__file__).resolve().parents[1]
-    structs = {"ultima_hsamp_params": hs.Params, "ultima_hsamp_batch": hs.Batch, "ultima_hsamp_head": hs.Head}
+    structs = {"ultima_hsamp_params": hs.Params, "ultima_hsamp_batch": hs.Batch, "ultima_hsamp_head": hs.Head,
+               "ultima_hsamp_verify": hs.Verify}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "ultima_hsamp.h"', 'int main(void) {']
     for cname, py in structs.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
@@ -133,3 +134,50 @@ def test_history_push_rejects_bad_arguments(pkg):
     assert L.ultima_hsamp_history_push(p, 8, p, p, 1, 5, None) == hs.ERR_INVALID        # keep > stride / 2
     assert L.ultima_hsamp_history_push(p, 8, p, p, 1, 0, None) == hs.ERR_INVALID        # keep < 1
     assert L.ultima_hsamp_history_push(p, 1, p, p, 1, 1, None) == hs.ERR_INVALID        # stride < 2
+
+
+def test_decode_commit_rejects_bad_arguments(pkg):
+    """Argument checks run before any device work (no GPU needed)."""
+    hs = pkg.hsamp
+    L = hs.lib()
+    p = ctypes.c_void_p(16)   # never dereferenced: every call below fails its checks first
+    stop = (ctypes.c_int32 * 9)(*range(9))
+    assert L.ultima_hsamp_decode_commit(None, 8, p, p, p, None, 1, 4, None, 0, None) == hs.ERR_INVALID
+    assert L.ultima_hsamp_decode_commit(p, 8, None, p, p, None, 1, 4, None, 0, None) == hs.ERR_INVALID
+    assert L.ultima_hsamp_decode_commit(p, 8, p, None, p, None, 1, 4, None, 0, None) == hs.ERR_INVALID
+    assert L.ultima_hsamp_decode_commit(p, 8, p, p, None, None, 1, 4, None, 0, None) == hs.ERR_INVALID  # active
+    assert L.ultima_hsamp_decode_commit(p, 8, p, p, p, None, 0, 4, None, 0, None) == hs.ERR_INVALID     # no rows
+    assert L.ultima_hsamp_decode_commit(p, 8, p, p, p, None, 1, 5, None, 0, None) == hs.ERR_INVALID     # keep
+    assert L.ultima_hsamp_decode_commit(p, 8, p, p, p, None, 1, 4, None, 2, None) == hs.ERR_INVALID     # no ids
+    assert L.ultima_hsamp_decode_commit(p, 8, p, p, p, None, 1, 4, stop, 9, None) == hs.ERR_INVALID     # > 8 ids
+    assert L.ultima_hsamp_decode_commit(p, 8, p, p, p, None, 1, 4, stop, -1, None) == hs.ERR_INVALID
+
+
+def test_verify_block_rejects_bad_arguments(pkg):
+    """Argument checks run before any device work (no GPU needed); the
+    workspace size is n_pos rows of hist_len + n_pos - 1 ids plus n_pos."""
+    hs = pkg.hsamp
+    L = hs.lib()
+    assert L.ultima_hsamp_verify_work_ints(5, 100) == 5 * 104 + 5
+    assert L.ultima_hsamp_verify_work_ints(1, 0) == 1 + 1
+    assert L.ultima_hsamp_verify_work_ints(0, 10) == -1
+    assert L.ultima_hsamp_verify_work_ints(3, -1) == -1
+    h = ctypes.c_void_p(16)   # never dereferenced
+    p = 16
+    par = (hs.Params * 1)()
+
+    def mk(**kw):
+        v = hs.Verify()
+        v.n_pos, v.vocab, v.dtype, v.logits, v.logits_stride = 4, 100, hs.F32, p, 100
+        v.draft, v.hist, v.hist_len, v.u, v.params = p, p, 10, p, par
+        v.work, v.out_tokens, v.out_count = p, p, p
+        for k, x in kw.items():
+            setattr(v, k, x)
+        return v
+
+    assert L.ultima_hsamp_verify_block(None, ctypes.byref(mk()), None) == hs.ERR_INVALID
+    assert L.ultima_hsamp_verify_block(h, None, None) == hs.ERR_INVALID
+    for bad in (dict(n_pos=0), dict(hist_len=-1), dict(vocab=0), dict(logits=None), dict(u=None), dict(work=None),
+                dict(out_tokens=None), dict(out_count=None), dict(draft=None), dict(hist=None),
+                dict(params=ctypes.POINTER(hs.Params)())):
+        assert L.ultima_hsamp_verify_block(h, ctypes.byref(mk(**bad)), None) == hs.ERR_INVALID, bad

@@ -64,6 +64,7 @@ def build_all() -> None:
         "hsamp_noalloc.o": CSRC / "hsamp_noalloc.hip",
         "hsamp_head.o": CSRC / "hsamp_head.hip",
         "hsamp_history.o": CSRC / "hsamp_history.hip",
+        "hsamp_callers.o": CSRC / "hsamp_callers.hip",
     }
     with ThreadPoolExecutor(max_workers=4) as ex:
         futs = [ex.submit(_run, [HIPCC, *HIP_FLAGS, "-x", "hip", "-c", str(src), "-o", str(BUILD / o)])

@@ -93,6 +93,30 @@ class Head(ctypes.Structure):
     ]
 
 
+class Verify(ctypes.Structure):
+    """ultima_hsamp_verify (include/ultima_hsamp.h)."""
+    _fields_ = [
+        ("n_pos", ctypes.c_int32),
+        ("vocab", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("logits", ctypes.c_void_p),
+        ("logits_stride", ctypes.c_int64),
+        ("draft", ctypes.c_void_p),
+        ("hist", ctypes.c_void_p),
+        ("hist_len", ctypes.c_int32),
+        ("mask", ctypes.c_void_p),
+        ("mask_stride", ctypes.c_int64),
+        ("u", ctypes.c_void_p),
+        ("params", ctypes.POINTER(Params)),
+        ("bias_ids", ctypes.c_void_p),
+        ("bias_vals", ctypes.c_void_p),
+        ("work", ctypes.c_void_p),
+        ("out_tokens", ctypes.c_void_p),
+        ("out_count", ctypes.c_void_p),
+        ("row_flags", ctypes.c_void_p),
+    ]
+
+
 def declared_symbols() -> list[str]:
     """Function names declared in include/ultima_hsamp.h."""
     import re
@@ -146,6 +170,12 @@ def lib() -> ctypes.CDLL:
         L.ultima_hsamp_history_push.argtypes = [vp, ctypes.c_int64, vp, vp, i32, i32, vp]
         L.ultima_hsamp_lm_head.restype = ctypes.c_int
         L.ultima_hsamp_lm_head.argtypes = [ctypes.POINTER(Head), vp]
+        L.ultima_hsamp_decode_commit.restype = ctypes.c_int
+        L.ultima_hsamp_decode_commit.argtypes = [vp, i64, vp, vp, vp, vp, i32, i32, vp, i32, vp]
+        L.ultima_hsamp_verify_work_ints.restype = i64
+        L.ultima_hsamp_verify_work_ints.argtypes = [i32, i32]
+        L.ultima_hsamp_verify_block.restype = ctypes.c_int
+        L.ultima_hsamp_verify_block.argtypes = [vp, ctypes.POINTER(Verify), vp]
         _lib = L
     return _lib
 
@@ -266,6 +296,27 @@ def history_push(hist, hist_len_dev, tokens, keep: int, stream=None) -> None:
                                           ctypes.c_void_p(s.cuda_stream)), "history_push")
 
 
+def decode_commit(hist, hist_len_dev, tokens, active, keep: int, stop_ids=(), budget=None, stream=None) -> None:
+    """ultima_hsamp_decode_commit on torch tensors of one device (int32): after
+    a run() over the slots' rows, ends the rows whose token is a stop id (or
+    -1), marks the tokens of ended rows -1, appends the rest to the histories
+    and counts them against budget (the server loop's max_tokens)."""
+    import torch
+    rows = hist.shape[0]
+    for t in (hist, hist_len_dev, tokens, active) + ((budget,) if budget is not None else ()):
+        assert t.dtype == torch.int32 and t.device == hist.device
+    assert hist_len_dev.shape[0] >= rows and tokens.shape[0] >= rows and active.shape[0] >= rows
+    assert hist.stride(1) == 1 and (budget is None or budget.shape[0] >= rows)
+    stop = np.asarray(list(stop_ids), np.int32)
+    s = torch.cuda.current_stream(hist.device) if stream is None else stream
+    check(lib().ultima_hsamp_decode_commit(
+        ctypes.c_void_p(hist.data_ptr()), hist.stride(0), ctypes.c_void_p(hist_len_dev.data_ptr()),
+        ctypes.c_void_p(tokens.data_ptr()), ctypes.c_void_p(active.data_ptr()),
+        ctypes.c_void_p(budget.data_ptr() if budget is not None else 0), rows, int(keep),
+        stop.ctypes.data_as(ctypes.c_void_p) if stop.size else None, int(stop.size),
+        ctypes.c_void_p(s.cuda_stream)), "decode_commit")
+
+
 def lm_head(hidden, norm_scale, eps: float, weight, logit_scale: float = 1.0, logits=None, normed=None,
             stream=None):
     """ultima_hsamp_lm_head on torch tensors of one device: hidden [rows, H] f32,
@@ -359,6 +410,43 @@ class Sampler:
         between the stream and merge kernels of every later run()."""
         ptr = None if event is None else ctypes.c_void_p(event.cuda_event)
         check(lib().ultima_hsamp_set_phase_event(self.h, ptr), "set_phase_event")
+
+    def verify_block(self, logits, params: dict, u, draft=None, hist=None, mask=None, bias=None, stream=None):
+        """ultima_hsamp_verify_block on torch tensors of one device: logits
+        [n_pos, V] (each position's target logits), u f64 [n_pos], draft int32
+        [n_pos - 1], hist int32 [hist_len] (the sequence's ids before the
+        block), one knob dict. Returns (tokens int32 [n_pos], count int32 [1],
+        row_flags int32 [n_pos]): the loop's emitted tokens are tokens[:count]."""
+        import torch
+        n, V = logits.shape[0], logits.shape[1]
+        dev = logits.device
+        dt = {torch.float32: F32, torch.bfloat16: BF16}[logits.dtype]
+        assert logits.stride(1) == 1 and u.dtype == torch.float64 and u.shape[0] >= n
+        assert draft is None or (draft.dtype == torch.int32 and draft.shape[0] >= n - 1)
+        assert hist is None or hist.dtype == torch.int32
+        L = 0 if hist is None else int(hist.shape[0])
+        arr, bids, bvals = make_params([params], None, None if bias is None else [bias])
+        work = torch.empty(int(lib().ultima_hsamp_verify_work_ints(n, L)), dtype=torch.int32, device=dev)
+        toks = torch.empty(n, dtype=torch.int32, device=dev)
+        count = torch.empty(1, dtype=torch.int32, device=dev)
+        flags = torch.empty(n, dtype=torch.int32, device=dev)
+        v = Verify()
+        v.n_pos, v.vocab, v.dtype = n, V, dt
+        v.logits, v.logits_stride = logits.data_ptr(), logits.stride(0)
+        v.draft = draft.data_ptr() if draft is not None and n > 1 else None
+        v.hist = hist.data_ptr() if L > 0 else None
+        v.hist_len = L
+        if mask is not None:
+            v.mask, v.mask_stride = mask.data_ptr(), mask.stride(0)
+        v.u = u.data_ptr()
+        v.params = arr
+        v.bias_ids = bids.ctypes.data if bids is not None else None
+        v.bias_vals = bvals.ctypes.data if bvals is not None else None
+        v.work, v.out_tokens, v.out_count, v.row_flags = work.data_ptr(), toks.data_ptr(), count.data_ptr(), flags.data_ptr()
+        s = torch.cuda.current_stream(dev) if stream is None else stream
+        check(lib().ultima_hsamp_verify_block(self.h, ctypes.byref(v), ctypes.c_void_p(s.cuda_stream)), "verify_block")
+        self._keep = (arr, bids, bvals, work)   # read on the host during the call only; work until it completes
+        return toks, count, flags
 
     def sample_host(self, logits: np.ndarray, params: dict, hist=None, bias=None, u: float = 0.5,
                     writeback: bool = False):

@@ -54,9 +54,13 @@ def parse():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
-    ap.add_argument("--workload", default="sampler", choices=["sampler", "head"],
+    ap.add_argument("--workload", default="sampler", choices=["sampler", "head", "verify", "decode"],
                     help="head: the logits producer (final rmsnorm + lm-head matvec) and the "
-                         "producer + sampler step instead of the sampler alone")
+                         "producer + sampler step instead of the sampler alone; verify: a drafted "
+                         "block's verification (ultima_hsamp_verify_block); decode: one multi-slot "
+                         "server decode step (run + ultima_hsamp_decode_commit, device histories)")
+    ap.add_argument("--block", type=int, default=16, help="verify workload: positions per block")
+    ap.add_argument("--slots", type=int, default=64, help="decode workload: slots per step")
     ap.add_argument("--head-rows", type=int, default=1, help="head workload: hidden-state rows per step")
     ap.add_argument("--head-hidden", type=int, default=4096, help="head workload: hidden size H")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -325,6 +329,135 @@ def head_main(args):
     print(json.dumps(line), flush=True)
 
 
+def callers_main(args):
+    """The batched callers on V = 151936 float32 logits with the server's
+    default knobs (SamplerParams{}: DRY over 512 ids, repetition over 64,
+    min-p): verify -- one drafted block of args.block positions per step
+    (every position sampled with its prefix history, then the accept); decode
+    -- one step of args.slots slots (their rows sampled from device histories,
+    then the loop's stop / push rules). Steps run from a captured graph over 8
+    rotating input sets; one JSON line. The roofline's bytes are the logits
+    and histories a step reads over the whole step's time."""
+    import torch
+    import __graft_entry__ as ge
+    pkg = ge.load_package()
+    hs, wlm = pkg.hsamp, pkg.workloads
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    V, n_sets, H = 151936, 8, 600
+    g = torch.Generator(device=dev).manual_seed(11)
+    verify = args.workload == "verify"
+    rows = args.block if verify else args.slots
+    logits = [torch.randn((rows, V), generator=g, device=dev) * 2.0 for _ in range(n_sets)]
+    us = [torch.rand(rows, generator=g, device=dev, dtype=torch.float64) for _ in range(n_sets)]
+    p = wlm.default_params()
+    sampler = hs.Sampler(0, max_rows=max(rows, 64), max_vocab=V)
+    stream = torch.cuda.Stream(dev)
+    rng = np.random.default_rng(3)
+    if verify:
+        hist = torch.from_numpy(rng.integers(0, V, H).astype(np.int32)).to(dev)
+        draft = torch.from_numpy(rng.integers(0, V, rows - 1).astype(np.int32)).to(dev)
+
+        def step(i, s):
+            sampler.verify_block(logits[i], p, us[i], draft=draft, hist=hist, stream=s)
+        bytes_step = rows * V * 4 + rows * (H + rows) * 4
+        unit, metric = "positions/s", f"verified block positions/sec (block {rows}, V={V} f32, SamplerParams{{}})"
+    else:
+        stride, keep, W = 1024, 512, 512
+        hist = torch.from_numpy(rng.integers(0, V, (rows, stride)).astype(np.int32)).to(dev)
+        lens = torch.full((rows,), H, dtype=torch.int32, device=dev)
+        active = torch.ones(rows, dtype=torch.int32, device=dev)
+        params = [dict(p) for _ in range(rows)]
+        outs = {"token": torch.empty(rows, dtype=torch.int32, device=dev),
+                "row_flags": torch.empty(rows, dtype=torch.int32, device=dev)}
+        stop = (151643, 151645)   # eos, im_end of the Qwen vocabulary
+
+        def step(i, s):
+            sampler.run(logits[i], params, us[i], hist=hist, hist_len=[W] * rows, hist_len_dev=lens, outputs=outs,
+                        stream=s)
+            hs.decode_commit(hist, lens, outs["token"], active, keep, stop, stream=s)
+        bytes_step = rows * V * 4 + rows * W * 4
+        unit, metric = "slot tokens/s", f"multi-slot decode tokens/sec ({rows} slots, V={V} f32, SamplerParams{{}})"
+    with torch.cuda.stream(stream):
+        for i in range(n_sets):
+            step(i, stream)
+    stream.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr, stream=stream):
+        for i in range(n_sets):
+            step(i, stream)
+    stream.synchronize()
+    reps = max(1, args.steps // (5 * n_sets))
+    for _ in range(max(5, args.warmup // n_sets)):
+        gr.replay()
+    stream.synchronize()
+    seg = []
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            e0.record(stream)
+            for _ in range(reps):
+                gr.replay()
+            e1.record(stream)
+        stream.synchronize()
+        seg.append(e0.elapsed_time(e1) / (reps * n_sets))
+    ms = statistics.median(seg)
+    achieved = bytes_step / (ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle as O  # the checker / baseline, never the product
+        kind = "reference" if O.ref_available() else "port"
+        threads = host_threads()
+        x0 = logits[0].cpu().numpy()
+        if verify:
+            hh = np.zeros((rows, H + rows), np.int32)
+            hb, dr = hist.cpu().numpy(), draft.cpu().numpy()
+            for r in range(rows):
+                hh[r, :H] = hb
+                hh[r, H:H + r] = dr[:r]
+            hl = np.arange(rows, dtype=np.int64) + H
+        else:
+            hh = hist.cpu().numpy()[:, :H].copy()
+            hl = np.full(rows, H, np.int64)
+        plist = [dict(p) for _ in range(rows)]
+        ts = []
+        for _ in range(1 + max(3, args.cpu_reps)):
+            x = x0.copy()
+            t0 = time.perf_counter()
+            if kind == "reference":
+                O.ref_sample_batch(x, plist, hh, hl, np.arange(rows, dtype=np.uint64) + 1, nthreads=threads)
+            else:
+                O.sample_batch(x, plist, hh, hl, None, us[0].cpu().numpy(), nthreads=threads)
+            ts.append(time.perf_counter() - t0)
+        sec = statistics.median(ts[1:])
+        cpu = {"value": rows / sec, "unit": unit, "cores": threads, "kind": kind,
+               "sample": f"the {rows} rows of one step (their histories as the step builds them) through "
+                         f"sample() on {threads} threads, median of {len(ts) - 1} after one untimed"}
+    sampler.close()
+    line = {
+        "metric": metric,
+        "value": rows / (ms * 1e-3),
+        "unit": unit,
+        "n_gpus": 1,
+        "steps": 5 * reps * n_sets,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (random normal logits, random histories and drafts, 8 rotating sets)",
+        "config": {"workload": f"{args.workload}: rows={rows} V={V} f32 SamplerParams{{}}",
+                   "rows": rows, "vocab": V, "bytes_per_step": bytes_step},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / PEAK_GBS, "traffic": None,
+                     "kernel": "the whole step (every kernel of it)", "algorithmic_bytes_per_launch": bytes_step},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -334,6 +467,9 @@ def main():
         sys.exit(2)
     if args.workload == "head":
         head_main(args)
+        return
+    if args.workload in ("verify", "decode"):
+        callers_main(args)
         return
     import torch
     import __graft_entry__ as ge

@@ -1967,10 +1967,14 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
     // -0 < +0 as raw keys order them), so that a NaN shows in its chunk's
     // maximum; such chunks then take the NaN-ignoring maximum of their other
     // ids (NaN ids count as -inf), after the loop
-    auto chunk = [&](int j, float (&x)[T::VW]) {
+    // (opaque: the chunk's words pass through an empty asm statement first, so
+    // that the elements are unpacked anew there instead of being kept, and
+    // spilled to scratch memory, from the maxima's pass for the NaN fix-up)
+    auto chunk_v = [&](uint4 rv, int j, bool opaque, float (&x)[T::VW]) {
+        if (opaque) __asm__("" : "+v"(rv.x), "+v"(rv.y), "+v"(rv.z), "+v"(rv.w));
         const int e0 = lo + (j * kBlock + tid) * T::VW;
 #pragma unroll
-        for (int c = 0; c < T::VW; ++c) x[c] = elem<DT>(raw[j], c);
+        for (int c = 0; c < T::VW; ++c) x[c] = elem<DT>(rv, c);
         if (MASK) {
             const int o = e0 - lo;
             const uint32_t mb = mbm[max(0, min(o, hi - lo - 1)) >> 5] >> (o & 31);
@@ -1983,6 +1987,7 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
             for (int c = 0; c < T::VW; ++c) x[c] = (e0 + c < hi) ? x[c] : -__builtin_inff();
         }
     };
+    auto chunk = [&](int j, float (&x)[T::VW]) { chunk_v(raw[j], j, false, x); };
     float cm[NC];
     bool nanv = false;
 #pragma unroll
@@ -2001,7 +2006,7 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
         for (int j = 0; j < NC; ++j) {
             if (cm[j] != cm[j]) {
                 float x[T::VW];
-                chunk(j, x);
+                chunk_v(raw[j], j, true, x);
                 float m = -__builtin_inff();
 #pragma unroll
                 for (int c = 0; c < T::VW; ++c) m = (x[c] == x[c]) ? __builtin_elementwise_maximum(m, x[c]) : m;

@@ -3618,6 +3618,161 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
 
 // ---- the merge of exact lists, large k ---------------------------------------------
 
+constexpr int kLRegs = 24;   // list entries per thread k_pick_l's direct selection holds
+
+// The top k of a row's S lists (counts in st.soff) into buf[0 .. min(k, n)),
+// when all n entries fit kLRegs per thread; returns false (nothing done)
+// otherwise. Entry e of the concatenated lists is thread e % kBlock's slot
+// e / kBlock; its slice comes from the lists' start offsets (st.hist holds
+// them while the entries load). The k-th largest composite: 8-bit radix
+// passes from the highest bit in which the entries differ, each a 256-bin
+// LDS histogram under the prefix fixed so far, until the bin holding the
+// k-th holds exactly what is still needed. Composites are distinct (ids
+// differ), so exactly min(k, n) entries are at or above it.
+template <class Scale>
+__device__ __forceinline__ bool direct_select(const u64* cand, int cap, int S, int k, Scale scaled, u64* buf,
+                                              Shared& st) {
+    const int tid = threadIdx.x, lane = lane_id();
+    if (tid == 0) {
+        int acc = 0;
+        for (int sl = 0; sl < S; ++sl) {
+            st.hist[sl] = (uint32_t)acc;
+            acc += st.soff[sl];
+        }
+        st.hist[S] = (uint32_t)acc;
+    }
+    __syncthreads();
+    const int n = (int)st.hist[S];
+    if (n > kLRegs * kBlock) return false;   // (uniform: every thread read the same total)
+    u64 v[kLRegs];
+    {
+        // (entries past n read the last one, clamped, and count as empty)
+        int sl = 0;
+        int at[kLRegs];
+#pragma unroll
+        for (int m = 0; m < kLRegs; ++m) {
+            const int e = min(tid + m * kBlock, max(n - 1, 0));
+            while (sl + 1 < S && e >= (int)st.hist[sl + 1]) ++sl;
+            at[m] = sl * cap + (e - (int)st.hist[sl]);
+        }
+#pragma unroll
+        for (int m = 0; m < kLRegs; ++m) v[m] = cand[at[m]];
+#pragma unroll
+        for (int m = 0; m < kLRegs; ++m) v[m] = (tid + m * kBlock < n) ? scaled(v[m]) : 0ull;
+    }
+    __syncthreads();   // the offsets are read before st.hist becomes the histogram
+    if (n <= k) {
+        int cnt = 0;
+#pragma unroll
+        for (int m = 0; m < kLRegs; ++m) cnt += v[m] != 0ull ? 1 : 0;
+        int total;
+        int pos = block_excl_scan(cnt, &total, st);
+#pragma unroll
+        for (int m = 0; m < kLRegs; ++m)
+            if (v[m] != 0ull) buf[pos++] = v[m];
+        __syncthreads();
+        if (tid == 0) st.n = total;
+        __syncthreads();
+        return true;
+    }
+    u64 lo = ~0ull, hi = 0ull;
+#pragma unroll
+    for (int m = 0; m < kLRegs; ++m) {
+        if (v[m] != 0ull) {
+            lo = v[m] < lo ? v[m] : lo;
+            hi = v[m] > hi ? v[m] : hi;
+        }
+    }
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) {
+        const u64 a2 = shfl_xor_u64(lo, d), b2 = shfl_xor_u64(hi, d);
+        lo = a2 < lo ? a2 : lo;
+        hi = b2 > hi ? b2 : hi;
+    }
+    if (lane == 0) {
+        st.ured[wave_id()] = lo;
+        st.minv_w[wave_id()] = hi;
+    }
+    __syncthreads();
+    lo = st.ured[0];
+    hi = st.minv_w[0];
+#pragma unroll
+    for (int i = 1; i < kBlock / 64; ++i) {
+        lo = st.ured[i] < lo ? st.ured[i] : lo;
+        hi = st.minv_w[i] > hi ? st.minv_w[i] : hi;
+    }
+    const int hb = 63 - __clzll((long long)(lo ^ hi));   // highest differing bit (n > k >= 1: n >= 2)
+    u64 pmask = (hb >= 63) ? 0ull : ~((2ull << hb) - 1ull);
+    u64 prefix = hi & pmask;
+    int need = k;
+    u64 kth = 0ull;
+    for (int shift = hb >= 7 ? hb - 7 : 0;;) {
+        st.hist[tid] = 0u;
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < kLRegs; ++m)
+            if (v[m] != 0ull && (v[m] & pmask) == prefix) atomicAdd(&st.hist[(uint32_t)(v[m] >> shift) & 255u], 1u);
+        __syncthreads();
+        if (tid < 64) {
+            const int c0 = st.hist[255 - 4 * lane], c1 = st.hist[254 - 4 * lane];
+            const int c2 = st.hist[253 - 4 * lane], c3 = st.hist[252 - 4 * lane];
+            const int s4 = c0 + c1 + c2 + c3;
+            const int incl = wave_incl_sum_i(s4);
+            const int excl = incl - s4;
+            if (excl < need && need <= incl) {
+                int q, cnt, before;
+                if (excl + c0 >= need) { q = 0; cnt = c0; before = excl; }
+                else if (excl + c0 + c1 >= need) { q = 1; cnt = c1; before = excl + c0; }
+                else if (excl + c0 + c1 + c2 >= need) { q = 2; cnt = c2; before = excl + c0 + c1; }
+                else { q = 3; cnt = c3; before = excl + c0 + c1 + c2; }
+                st.sel_d = 255 - 4 * lane - q;
+                st.sel_need = need - before;
+                st.sel_cnt = cnt;
+            }
+        }
+        __syncthreads();
+        const int dgt = st.sel_d, cnt = st.sel_cnt;
+        need = st.sel_need;
+        prefix = (prefix & ~((u64)0xFF << shift)) | ((u64)dgt << shift);
+        pmask |= (u64)0xFF << shift;
+        __syncthreads();   // every thread has read sel_* before the next pass may write them
+        if (cnt == need || shift == 0) {
+            // every entry under this prefix is in: the k-th is their minimum
+            u64 mn = ~0ull;
+#pragma unroll
+            for (int m = 0; m < kLRegs; ++m)
+                if (v[m] != 0ull && (v[m] & pmask) == prefix && v[m] < mn) mn = v[m];
+#pragma unroll
+            for (int d = 32; d > 0; d >>= 1) {
+                const u64 o = shfl_xor_u64(mn, d);
+                mn = o < mn ? o : mn;
+            }
+            if (lane == 0) st.ured[wave_id()] = mn;
+            __syncthreads();
+            kth = st.ured[0];
+#pragma unroll
+            for (int i = 1; i < kBlock / 64; ++i) kth = st.ured[i] < kth ? st.ured[i] : kth;
+            break;
+        }
+        shift = shift >= 8 ? shift - 8 : 0;
+    }
+    int cnt = 0;
+#pragma unroll
+    for (int m = 0; m < kLRegs; ++m) cnt += (v[m] != 0ull && v[m] >= kth) ? 1 : 0;
+    int total;
+    int pos = block_excl_scan(cnt, &total, st);
+#pragma unroll
+    for (int m = 0; m < kLRegs; ++m)
+        if (v[m] != 0ull && v[m] >= kth) buf[pos++] = v[m];
+    __syncthreads();
+    if (tid == 0) {
+        st.n = total;
+        st.theta = kth;
+    }
+    __syncthreads();
+    return true;
+}
+
 // One block per sampling row whose slices left exact lists with 64 < k <= 1024
 // (the exact stream's block-level bound): every entry of the row's lists, its
 // final raw key scaled by the row's temperature, is offered into the LDS
@@ -3667,6 +3822,22 @@ __global__ __launch_bounds__(kBlock, 4) void k_pick_l(StreamArgs a) {
     auto scaled = [&](u64 c) -> u64 {
         return ((u64)scaled_key((uint32_t)(c >> 32), inv_t) << 32) | (c & 0xFFFFFFFFull);
     };
+    // Rows whose lists hold at most kLRegs entries per thread in all: every
+    // entry in registers at once (one round of loads), the exact k-th by radix
+    // passes over them, and only the top k written to the buffer.
+    if (S < 256 && direct_select(cand, a.cand_cap, S, k, scaled, buf, st)) {
+        HSAMP_PHASE(9500 + r, 4);
+        const uint32_t rflags = (st.flags & 4) ? ROWF_NAN : 0u;
+        FinLds f;
+        f.sortk = buf;
+        f.fidx = reinterpret_cast<int32_t*>(smem);
+        f.fv = reinterpret_cast<float*>(f.fidx + a.kmax);
+        f.fe = f.fv + a.kmax;
+        f.fp = f.fe;
+        f.keep = reinterpret_cast<uint8_t*>(f.fe + a.kmax);
+        select_and_finalize(sa, sP, r, buf, f, st, rflags);
+        return;
+    }
     for (int sl = 0; sl < S; ++sl) {
         const int n = st.soff[sl];
         const u64* lst = cand + (int64_t)sl * a.cand_cap;

@@ -278,6 +278,9 @@ int build_blob(HostScratch& hs, const ultima_hsamp_batch* b, Built& out) {
         }
         P.flags = fl;
         if (fl & RF_DRY) out.any_dry = true;
+        // DRY and frequency/presence counting over different windows (DRY looks
+        // back fewer ids than repetition): two counts per id, general kernels
+        if ((fl & RF_DRY) && (fl & RF_FP) && fp_w != dry_w) out.dry_split = true;
         if (fl & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) {
             out.any_pen = true;
             out.max_pen = std::max(out.max_pen, (int)scan + P.bias_cnt);
@@ -339,7 +342,7 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     rp.kmax = kmax;
     rp.wb = (b->flags & ULTIMA_HSAMP_WRITEBACK) != 0;
     bool exact_ok = bl.any_sample && !bl.any_greedy && !bl.any_full && kmax <= kLimitK && !rp.wb && bl.inv_ok &&
-                    (!bl.any_pen || (bl.pen_lowers && !bl.any_dry && bl.max_bias == 0 && bl.max_scan <= 8 * kBlock));
+                    (!bl.any_pen || (bl.pen_lowers && !bl.dry_split && bl.max_bias == 0 && bl.max_scan <= 8 * kBlock));
     if (const char* ev = std::getenv("ULTIMA_HSAMP_EXACT")) exact_ok = exact_ok && ev[0] != '0';
     // 16-byte loads: aligned rows holding at least one whole chunk
     const bool vec_rows = (reinterpret_cast<uintptr_t>(b->logits) % 16 == 0) && ((b->logits_stride * es) % 16 == 0) &&

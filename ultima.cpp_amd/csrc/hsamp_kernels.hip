@@ -1770,14 +1770,19 @@ __device__ uint32_t raw_edge(uint32_t ths, float inv_t, float temp) {
 
 // Final raw key of slice id t (raw logit x, after the mask) with count entry
 // h: stages 1-4 (sampler.cpp:28-99, those a count entry calls for), NaN ->
-// -inf (noted). one: the entry is a plain count over the whole scanned window
-// (the repetition and frequency/presence windows are equal, or one of them
-// is off): the id repeats when it counts at all.
+// -inf (noted). The entry's count is over the count window (the DRY window
+// when DRY is on -- then also the frequency/presence window, or that stage is
+// off -- else the frequency/presence window), which the DRY and
+// frequency/presence stages take; one: the entry is a plain count over the
+// whole scanned window (the repetition and count windows are equal, or one of
+// them is off): the id repeats when it counts at all; else its repetition
+// bit says so.
 __device__ __forceinline__ uint32_t final_raw_key(float x, int32_t t, uint32_t h, bool one, const StreamArgs& a,
                                                   const RowPlan& P, bool& nan) {
     if (h == 0u) return raw_key(x);
-    const uint32_t v = one ? ((P.rep_win > 0 ? HV_REP : 0u) | (P.fp_win > 0 ? h : 0u))
-                           : (((h & XC_REP) ? HV_REP : 0u) | (h & XC_FP_MASK));
+    const uint32_t c = one ? h : (h & XC_FP_MASK);
+    const uint32_t v = (one ? (P.rep_win > 0 ? HV_REP : 0u) : ((h & XC_REP) ? HV_REP : 0u)) |
+                       (P.fp_win > 0 ? c : 0u) | (P.dry_win > 0 ? (c << HV_DRY_SHIFT) : 0u);
     const float y = pen_value(x, t, v, a, P);
     if (y != y) {
         nan = true;
@@ -1907,11 +1912,15 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
     constexpr uint32_t kFloor = (uint32_t)(kThetaFloor >> 32);
 
     // A. the slice's history counts, while the tile is still on its way (the
-    // history row and the plan were asked for first). Exact lists run without
-    // DRY, so the scanned window is the larger of the
-    // repetition and frequency/presence windows; when those are equal (or one
-    // is off) a count entry is a plain count over it (one atomic per id).
-    const bool one = P.rep_win == 0 || P.fp_win == 0 || P.rep_win == P.fp_win;
+    // history row and the plan were asked for first). Exact lists take DRY
+    // only where its window is also the frequency/presence window (or that
+    // stage is off), so one count serves both: the count window cw is the DRY
+    // window when DRY is on, else the frequency/presence window; the scanned
+    // window is the larger of it and the repetition window. When those two
+    // are equal (or one is off) a count entry is a plain count over it (one
+    // atomic per id); else a count over cw and a repetition bit.
+    const int cw = P.dry_win > 0 ? P.dry_win : P.fp_win;
+    const bool one = P.rep_win == 0 || cw == 0 || P.rep_win == cw;
     if (PEN && pen) {
         const int L = hist_len_of(a, P, r), p0 = L - P.scan_len;
         const int mhi = min(a.vocab, lo + a.slice_len);
@@ -1957,7 +1966,7 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
                 if (one) {
                     atomicAdd(&hcw[e >> 1], 1u << sh);
                 } else {
-                    if (p >= L - P.fp_win) atomicAdd(&hcw[e >> 1], 1u << sh);
+                    if (p >= L - cw) atomicAdd(&hcw[e >> 1], 1u << sh);
                     if (p >= L - P.rep_win) atomicOr(&hcw[e >> 1], XC_REP << sh);
                 }
             }

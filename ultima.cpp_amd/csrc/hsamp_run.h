@@ -48,6 +48,7 @@ struct Built {
     bool any_topk = false;     // a greedy or top-k row (k_stream + k_merge)
     bool any_greedy = false;   // a greedy row (k_stream's greedy kernel)
     bool any_sample = false;   // a top-k sampling row (k_stream's sampling kernel)
+    bool dry_split = false;    // a row whose DRY and frequency/presence windows differ
 };
 
 // Kernel choice, slicing, LDS sizes and scratch sizes (in elements) of one run.

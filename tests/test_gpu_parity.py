@@ -606,3 +606,45 @@ def test_graph_replay_after_scratch_grows(hs, wl):
         del graph
     finally:
         s.close()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("kmix", [40, 300])
+def test_greedy_rows_with_sampling_rows(sampler, wl, kernel_mode, dtype, kmix):
+    """Greedy rows (argmax, sampler.cpp:220-228) batched with sampling rows of
+    top-k <= 64 (k_pick) or above (k_pick_l), exact lists or general kernels:
+    NaN at id 0 (id 0 wins), NaN elsewhere (left out), a maximum of zero held
+    as -0 at a lower id than +0 (the lower id wins), a row of -inf but one
+    NaN past id 0 (id 0), penalised top ids, a mask that leaves out id 0's NaN."""
+    rng = np.random.default_rng(61 + kmix)
+    B, V = 8, 151936
+    x = rng.normal(size=(B, V)).astype(np.float32) * 2
+    x[0, 0] = np.nan
+    x[1, 5000] = np.nan
+    x[1, 77] = 40.0
+    x[2, :] = -5.0
+    x[2, 3] = -0.0
+    x[2, 9000] = 0.0
+    x[3, :] = -np.inf
+    x[3, 1234] = np.nan
+    mask_rows = np.ones((B, (V + 31) // 32), np.uint32) * np.uint32(0xFFFFFFFF)
+    x[4, 0] = np.nan
+    mask_rows[4, 0] &= np.uint32(0xFFFFFFFE)             # id 0 (NaN) not allowed
+    hist = rng.integers(0, V, size=(B, 256)).astype(np.int32)
+    top5 = np.argsort(-x[5])[:40]
+    hist[5, -40:] = top5
+    plist = [wl.identity_params(temperature=0.0),
+             wl.identity_params(temperature=0.0, rep_penalty=1.2, repeat_last_n=64),
+             wl.identity_params(temperature=0.0),
+             wl.identity_params(temperature=-1.0),
+             wl.identity_params(temperature=0.0),
+             wl.identity_params(temperature=0.0, rep_penalty=3.0, repeat_last_n=64, frequency_penalty=0.5,
+                                presence_penalty=0.5),
+             wl.identity_params(top_k=kmix, temperature=0.8, top_p=0.9),
+             wl.default_params(top_k=kmix)]
+    xs = x if dtype == "f32" else wl.to_bf16_bits(x)
+    w = wl.Workload("edge", dtype, xs, plist, rng.random(B), hist, np.full(B, 256, np.int64), mask_rows)
+    g = run_gpu(sampler, w)
+    assert compare_rows(w, g) == B
+    tok = g["token"]
+    assert tok[0] == 0 and tok[3] == 0 and tok[2] == 3 and tok[1] == 77 and tok[4] != 0

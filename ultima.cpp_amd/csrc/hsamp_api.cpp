@@ -333,15 +333,16 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     rp.B = B;
     rp.V = V;
     // Exact lists (k_stream's EX kernels + k_pick, or k_pick_l when some
-    // row's top-k is above 64): every row samples with top-k <= 1024 and
-    // penalties that can only lower a logit, from windows the stream's
-    // registers hold, without DRY or logit bias. The stream then leaves every
+    // row's top-k is above 64): every row samples with top-k <= 1024 or is
+    // greedy, with penalties that can only lower a logit, from windows the
+    // stream's registers hold, without logit bias, DRY only where its window
+    // is also the frequency/presence window. The stream then leaves every
     // candidate with its final key. ULTIMA_HSAMP_EXACT=0 turns it off (the
     // general kernels take every batch).
     const int kmax = std::max(1, bl.kmax);
     rp.kmax = kmax;
     rp.wb = (b->flags & ULTIMA_HSAMP_WRITEBACK) != 0;
-    bool exact_ok = bl.any_sample && !bl.any_greedy && !bl.any_full && kmax <= kLimitK && !rp.wb && bl.inv_ok &&
+    bool exact_ok = (bl.any_sample || bl.any_greedy) && !bl.any_full && kmax <= kLimitK && !rp.wb && bl.inv_ok &&
                     (!bl.any_pen || (bl.pen_lowers && !bl.dry_split && bl.max_bias == 0 && bl.max_scan <= 8 * kBlock));
     if (const char* ev = std::getenv("ULTIMA_HSAMP_EXACT")) exact_ok = exact_ok && ev[0] != '0';
     // 16-byte loads: aligned rows holding at least one whole chunk

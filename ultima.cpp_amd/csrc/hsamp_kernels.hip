@@ -1777,13 +1777,18 @@ __device__ uint32_t raw_edge(uint32_t ths, float inv_t, float temp) {
 // whole scanned window (the repetition and count windows are equal, or one of
 // them is off): the id repeats when it counts at all; else its repetition
 // bit says so.
-__device__ __forceinline__ uint32_t final_raw_key(float x, int32_t t, uint32_t h, bool one, const StreamArgs& a,
-                                                  const RowPlan& P, bool& nan) {
-    if (h == 0u) return raw_key(x);
+__device__ __forceinline__ float final_value(float x, int32_t t, uint32_t h, bool one, const StreamArgs& a,
+                                             const RowPlan& P) {
+    if (h == 0u) return x;
     const uint32_t c = one ? h : (h & XC_FP_MASK);
     const uint32_t v = (one ? (P.rep_win > 0 ? HV_REP : 0u) : ((h & XC_REP) ? HV_REP : 0u)) |
                        (P.fp_win > 0 ? c : 0u) | (P.dry_win > 0 ? (c << HV_DRY_SHIFT) : 0u);
-    const float y = pen_value(x, t, v, a, P);
+    return pen_value(x, t, v, a, P);
+}
+__device__ __forceinline__ uint32_t final_raw_key(float x, int32_t t, uint32_t h, bool one, const StreamArgs& a,
+                                                  const RowPlan& P, bool& nan) {
+    if (h == 0u) return raw_key(x);
+    const float y = final_value(x, t, h, one, a, P);
     if (y != y) {
         nan = true;
         return kKeyNegInf;
@@ -2034,7 +2039,10 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
 #pragma unroll
     for (int j = 1; j < NC; ++j) lmf = __builtin_elementwise_maximum(lmf, cm[j]);
     const uint32_t lk = raw_key(lmf);
-    const int k = P.top_k;
+    // a greedy row (argmax, sampler.cpp:220-228) keeps the ids that can be its
+    // largest final logit: the lists of top-k 1, no temperature
+    const bool greedy = (P.flags & RF_GREEDY) != 0;
+    const int k = greedy ? 1 : P.top_k;
     uint32_t tw;
     if (k <= 64) {
         const int kw = (k + 4 + 3) >> 2;   // <= 17
@@ -2062,11 +2070,19 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
     thr = max(thr, kFloor);
     const float inv_t = P.inv_temp;
     // R: thr itself when the raw key below it scales below ths (the usual
-    // case), else the search
+    // case; a greedy row's keys are not scaled), else the search
     const uint32_t sthr = scaled_key(thr, inv_t);
     uint32_t R = thr;
-    if (!(sthr >= kFloor && (thr == kFloor || scaled_key(thr - 1u, inv_t) < sthr)))
+    if (!greedy && !(sthr >= kFloor && (thr == kFloor || scaled_key(thr - 1u, inv_t) < sthr)))
         R = raw_edge(max(sthr, kFloor), inv_t, P.temp);
+    // a greedy row whose id 0 ends NaN (after its mask and penalties) samples
+    // id 0: no later logit compares greater (sampler.cpp:220-228)
+    if (greedy && lo == 0 && tid == 0) {
+        float x[T::VW];
+        chunk(0, x);
+        const float y = PEN ? final_value(x[0], 0, hentry(0u, hmark(0u)), one, a, P) : x[0];
+        if (y != y) atomicOr(&st.flags, 2);
+    }
     HSAMP_PHASE(slot, 7);
 
     // C, D. the ids whose final raw key lies in [Rlo, Rhi). Each wave stages
@@ -2153,12 +2169,13 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
     // E. fewer than k ids kept above a raised bound (penalties took the rest
     // below it): every id down to the floor
     if (PEN && st.n < k) {
-        const uint32_t Rf = raw_edge(max(scaled_key(kFloor, inv_t), kFloor), inv_t, P.temp);
+        const uint32_t Rf = greedy ? kFloor : raw_edge(max(scaled_key(kFloor, inv_t), kFloor), inv_t, P.temp);
         if (R > Rf) pass(Rf, R);
     }
     if (nanv) atomicOr(&st.flags, 1);
     __syncthreads();
-    if (tid == 0) a.cand_n[slot] = st.n | ((st.flags & 1) ? (1 << 30) : 0);
+    // bit 30: a NaN logit in the slice; bit 29: a greedy row's id 0 is NaN
+    if (tid == 0) a.cand_n[slot] = st.n | ((st.flags & 1) ? (1 << 30) : 0) | ((st.flags & 2) ? (1 << 29) : 0);
     // the rest of k_pick's window reads as empty (it then needs no lengths)
     for (int i = st.n + tid; i < a.win; i += kBlock) out[i] = 0ull;
     HSAMP_PHASE(slot, 6);
@@ -3356,10 +3373,44 @@ __global__ __launch_bounds__(kBlock, 3) void k_merge(StreamArgs a) {
 
 // ---- the merge of exact lists -------------------------------------------------------
 
+// A greedy row's argmax from its exact lists (sampler.cpp:220-228): the
+// largest final logit, -0 counted as +0, the lowest id among equal ones (the
+// composites order them so once the key is made canonical); id 0 when its
+// final logit is NaN (nan0: thread 0 holds slice 0's flag); id 0 when no id
+// is above -inf (none is then greater than id 0's). win: NW entries of the
+// windows already loaded (0 = none); entries past a window (more) are read
+// here.
+template <int NW>
+__device__ __forceinline__ void pick_greedy(const StreamArgs& a, int r, const u64* cand, int S, int W, bool more,
+                                            const u64 (&win)[NW], bool nan0, bool nan_any, Shared& st) {
+    const int tid = threadIdx.x;
+    auto canon = [](u64 c) -> u64 {
+        return c == 0ull ? 0ull : ((u64)key32(key_to_float((uint32_t)(c >> 32))) << 32) | (c & 0xFFFFFFFFull);
+    };
+    u64 best = 0ull;
+#pragma unroll
+    for (int j = 0; j < NW; ++j) best = max(best, canon(win[j]));
+    if (more) {
+        for (int sl = 0; sl < S; ++sl) {
+            const int n = st.soff[sl];
+            for (int e = W + tid; e < n; e += kBlock) best = max(best, canon(cand[(int64_t)sl * a.cand_cap + e]));
+        }
+    }
+    if (tid == 0) st.nan0 = nan0 ? 1 : 0;
+    best = block_max_u64(best, st);   // (its barriers publish st.nan0)
+    if (tid == 0) {
+        a.token[r] = (st.nan0 || best == 0ull) ? 0 : comp_idx(best);
+        if (a.row_flags != nullptr) a.row_flags[r] = ROWF_GREEDY | (nan_any ? ROWF_NAN : 0u);
+        if (a.topk_count != nullptr) a.topk_count[r] = -1;
+        if (a.kept_count != nullptr) a.kept_count[r] = 0;
+    }
+}
+
 // One block per sampling row whose slices left exact lists (k_stream's EX
 // kernels; k <= 64): the row's exact top-k and the rest of the ladder
 // (sampler.cpp:267-277). No history work and no logit reads: every
 // candidate carries its final logit before temperature, which is applied here.
+// A greedy row takes the argmax of its lists instead (pick_greedy).
 //  - The slice counts, a window of W entries of every slice's list (NW per
 //    thread; entry g is slice g / W, position g % W), the plan and u are
 //    requested together.
@@ -3438,6 +3489,11 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
     const int k = P.top_k;
     const float inv_t = P.inv_temp;
     const uint32_t rflags = (fl0 & 4) ? ROWF_NAN : 0u;
+    if (P.flags & RF_GREEDY) {
+        pick_greedy(a, r, cand, S, W, (fl0 & 8) != 0, win, tid == 0 && (cnt_raw & (1 << 29)) != 0,
+                    (fl0 & 4) != 0, st);
+        return;
+    }
     // the lists carry final logits before temperature: composites of the
     // scaled keys (sampler.cpp:101-106)
     auto scaled = [&](u64 c) -> u64 {
@@ -3834,6 +3890,11 @@ __global__ __launch_bounds__(kBlock, 4) void k_pick_l(StreamArgs a) {
     // Rows whose lists hold at most kLRegs entries per thread in all: every
     // entry in registers at once (one round of loads), the exact k-th by radix
     // passes over them, and only the top k written to the buffer.
+    if (P.flags & RF_GREEDY) {
+        const u64 none[1] = {0ull};
+        pick_greedy(a, r, cand, S, 0, true, none, tid == 0 && (cnt_raw & (1 << 29)) != 0, (st.flags & 4) != 0, st);
+        return;
+    }
     if (S < 256 && direct_select(cand, a.cand_cap, S, k, scaled, buf, st)) {
         HSAMP_PHASE(9500 + r, 4);
         const uint32_t rflags = (st.flags & 4) ? ROWF_NAN : 0u;

@@ -648,3 +648,37 @@ def test_greedy_rows_with_sampling_rows(sampler, wl, kernel_mode, dtype, kmix):
     assert compare_rows(w, g) == B
     tok = g["token"]
     assert tok[0] == 0 and tok[3] == 0 and tok[2] == 3 and tok[1] == 77 and tok[4] != 0
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("kmix", [40, 300])
+def test_nonpositive_bias_with_penalties(sampler, wl, kernel_mode, dtype, kmix):
+    """Logit bias that only lowers logits (bans at -inf, negative values on
+    the top tokens; up to 256 entries a row) beside repetition, DRY and
+    frequency/presence penalties: the exact lists mark the bias ids in their
+    count entries and apply the bias with the other stages (sampler.cpp:28-34)."""
+    rng = np.random.default_rng(91 + kmix)
+    B, V = 6, 151936
+    x = rng.normal(size=(B, V)).astype(np.float32) * 2
+    hist = rng.integers(0, V, size=(B, 512)).astype(np.int32)
+    bias = []
+    for r in range(B):
+        top = np.argsort(-x[r])[:300]
+        b = {int(t): float("-inf") for t in top[:20]}                       # bans
+        b.update({int(t): float(-rng.uniform(0.1, 4.0)) for t in top[20:120]})
+        b.update({int(t): 0.0 for t in rng.choice(V, 30, replace=False)})
+        b.update({int(t): -1.5 for t in (0, V - 1, V - 2)})                # edges, the ragged end
+        bias.append(dict(list(b.items())[:256]))
+        hist[r, -60:] = top[100:160]
+    bias[3] = None
+    plist = [wl.identity_params(top_k=kmix, temperature=0.7),
+             wl.default_params(top_k=kmix),
+             wl.identity_params(top_k=kmix, temperature=1.2, top_p=0.9, rep_penalty=1.3, repeat_last_n=256,
+                                frequency_penalty=0.3, presence_penalty=0.2),
+             wl.identity_params(top_k=kmix, temperature=0.9),
+             wl.identity_params(temperature=0.0, rep_penalty=1.2, repeat_last_n=64),
+             wl.default_params(top_k=kmix, dry_last_n=512, repeat_last_n=512, frequency_penalty=0.1)]
+    xs = x if dtype == "f32" else wl.to_bf16_bits(x)
+    w = wl.Workload("edge", dtype, xs, plist, rng.random(B), hist, np.full(B, 512, np.int64), None)
+    g = run_gpu(sampler, w, bias=bias)
+    assert compare_rows(w, g, bias=bias) == B

@@ -334,16 +334,16 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     rp.V = V;
     // Exact lists (k_stream's EX kernels + k_pick, or k_pick_l when some
     // row's top-k is above 64): every row samples with top-k <= 1024 or is
-    // greedy, with penalties that can only lower a logit, from windows the
-    // stream's registers hold, without logit bias, DRY only where its window
-    // is also the frequency/presence window. The stream then leaves every
+    // greedy, with penalties that can only lower a logit (logit bias <= 0, at
+    // most kBlock entries a row), from windows the stream's registers hold,
+    // DRY only where its window is also the frequency/presence window. The stream then leaves every
     // candidate with its final key. ULTIMA_HSAMP_EXACT=0 turns it off (the
     // general kernels take every batch).
     const int kmax = std::max(1, bl.kmax);
     rp.kmax = kmax;
     rp.wb = (b->flags & ULTIMA_HSAMP_WRITEBACK) != 0;
     bool exact_ok = (bl.any_sample || bl.any_greedy) && !bl.any_full && kmax <= kLimitK && !rp.wb && bl.inv_ok &&
-                    (!bl.any_pen || (bl.pen_lowers && !bl.dry_split && bl.max_bias == 0 && bl.max_scan <= 8 * kBlock));
+                    (!bl.any_pen || (bl.pen_lowers && !bl.dry_split && bl.max_bias <= kBlock && bl.max_scan <= 8 * kBlock));
     if (const char* ev = std::getenv("ULTIMA_HSAMP_EXACT")) exact_ok = exact_ok && ev[0] != '0';
     // 16-byte loads: aligned rows holding at least one whole chunk
     const bool vec_rows = (reinterpret_cast<uintptr_t>(b->logits) % 16 == 0) && ((b->logits_stride * es) % 16 == 0) &&
@@ -466,13 +466,13 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     // The counts take 2 B per slice id, except in four-tile slices (whose
     // 64 KB would hold the blocks per CU to two): there ranked, a bitmap over
     // the slice's ids, a 2 B rank prefix per bitmap word and 2 B entries for
-    // the window's distinct ids (at most 8 * kBlock), at two more block
-    // barriers. (the general instantiations for unaligned rows take PEN =
+    // the window's distinct ids and the row's bias ids (at most 8 * kBlock
+    // and kBlock), at two more block barriers. (the general instantiations for unaligned rows take PEN =
     // true: their counts are cleared and stay zero when no row has penalties)
     rp.cnt_ranked = rp.ex_tiles == 4;
     rp.cnt_bytes = !(bl.any_pen || !vec_rows) ? 0
                    : rp.cnt_ranked ? align16(4 * (size_t)bitmap_words) + align16(2 * (size_t)bitmap_words) +
-                                         2 * 8 * (size_t)kBlock
+                                         2 * 9 * (size_t)kBlock
                                    : align16(2 * ((size_t)slice_len + 8));
     rp.stage_off = rp.cnt_bytes + align16(4 * (size_t)bitmap_words);
     rp.lds_ex = rp.stage_off + 32 * (size_t)kBlock;

@@ -1780,9 +1780,10 @@ __device__ uint32_t raw_edge(uint32_t ths, float inv_t, float temp) {
 __device__ __forceinline__ float final_value(float x, int32_t t, uint32_t h, bool one, const StreamArgs& a,
                                              const RowPlan& P) {
     if (h == 0u) return x;
-    const uint32_t c = one ? h : (h & XC_FP_MASK);
-    const uint32_t v = (one ? (P.rep_win > 0 ? HV_REP : 0u) : ((h & XC_REP) ? HV_REP : 0u)) |
-                       (P.fp_win > 0 ? c : 0u) | (P.dry_win > 0 ? (c << HV_DRY_SHIFT) : 0u);
+    const uint32_t c = h & XC_CNT_MASK;
+    const uint32_t v = (one ? (P.rep_win > 0 && c > 0u ? HV_REP : 0u) : ((h & XC_REP) ? HV_REP : 0u)) |
+                       ((h & XC_BIAS) ? HV_BIAS : 0u) | (P.fp_win > 0 ? c : 0u) |
+                       (P.dry_win > 0 ? (c << HV_DRY_SHIFT) : 0u);
     return pen_value(x, t, v, a, P);
 }
 __device__ __forceinline__ uint32_t final_raw_key(float x, int32_t t, uint32_t h, bool one, const StreamArgs& a,
@@ -1930,6 +1931,10 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
         const int L = hist_len_of(a, P, r), p0 = L - P.scan_len;
         const int mhi = min(a.vocab, lo + a.slice_len);
         const uint32_t wl = (uint32_t)(L - p0), sl = (uint32_t)(mhi - lo);
+        // the row's logit-bias ids (at most kBlock, none raising a logit):
+        // each marks its entry, so that the element pass applies the bias
+        const bool bias = (P.flags & RF_BIAS) != 0;
+        const uint32_t ob = (bias && tid < P.bias_cnt) ? (uint32_t)(a.bias_ids[P.bias_off + tid] - lo) : 0xFFFFFFFFu;
         uint32_t inw = 0u;   // bit q: pre[q] is a window id of this slice
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
@@ -1940,6 +1945,7 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
                 if constexpr (ranked) atomicOr(&hbm[o >> 5], 1u << (o & 31));
             }
         }
+        if (ranked && bias && ob < sl) atomicOr(&hbm[ob >> 5], 1u << (ob & 31));
         if constexpr (ranked) {
             __syncthreads();
             // rank prefixes of the bitmap words: thread t takes words NT t .. NT t + NT - 1
@@ -1975,6 +1981,10 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
                     if (p >= L - P.rep_win) atomicOr(&hcw[e >> 1], XC_REP << sh);
                 }
             }
+        }
+        if (bias && ob < sl) {
+            const uint32_t e = ranked ? hrank(ob) : ob;
+            atomicOr(&hcw[e >> 1], XC_BIAS << ((e & 1u) << 4));
         }
     }
     // B. chunk maxima, as the chunks arrive: IEEE maximum (NaN-propagating,

@@ -43,9 +43,10 @@ enum : uint32_t {
 };
 
 // Exact lists: per-slice history counts, one 16-bit entry per slice id
-// (frequency/presence window occurrences, repetition-window bit).
+// (occurrences in the count window, a logit-bias bit, a repetition-window bit).
 enum : uint32_t {
-    XC_FP_MASK = 0x7fffu,
+    XC_CNT_MASK = 0x3fffu,
+    XC_BIAS = 0x4000u,
     XC_REP = 0x8000u,
 };
 

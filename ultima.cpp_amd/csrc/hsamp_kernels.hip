@@ -3706,7 +3706,8 @@ constexpr int kLRegs = 24;   // list entries per thread k_pick_l's direct select
 // differ), so exactly min(k, n) entries are at or above it.
 template <class Scale>
 __device__ __forceinline__ bool direct_select(const u64* cand, int cap, int S, int k, Scale scaled, u64* buf,
-                                              Shared& st) {
+                                              Shared& st, int r) {
+    (void)r;   // (phase clocks of an instrumented build)
     const int tid = threadIdx.x, lane = lane_id();
     if (tid == 0) {
         int acc = 0;
@@ -3736,6 +3737,7 @@ __device__ __forceinline__ bool direct_select(const u64* cand, int cap, int S, i
         for (int m = 0; m < kLRegs; ++m) v[m] = (tid + m * kBlock < n) ? scaled(v[m]) : 0ull;
     }
     __syncthreads();   // the offsets are read before st.hist becomes the histogram
+    HSAMP_PHASE(9500 + r, 1);
     if (n <= k) {
         int cnt = 0;
 #pragma unroll
@@ -3781,6 +3783,7 @@ __device__ __forceinline__ bool direct_select(const u64* cand, int cap, int S, i
     u64 prefix = hi & pmask;
     int need = k;
     u64 kth = 0ull;
+    HSAMP_PHASE(9500 + r, 2);
     for (int shift = hb >= 7 ? hb - 7 : 0;;) {
         st.hist[tid] = 0u;
         __syncthreads();
@@ -3831,6 +3834,7 @@ __device__ __forceinline__ bool direct_select(const u64* cand, int cap, int S, i
         }
         shift = shift >= 8 ? shift - 8 : 0;
     }
+    HSAMP_PHASE(9500 + r, 3);
     int cnt = 0;
 #pragma unroll
     for (int m = 0; m < kLRegs; ++m) cnt += (v[m] != 0ull && v[m] >= kth) ? 1 : 0;
@@ -3905,7 +3909,7 @@ __global__ __launch_bounds__(kBlock, 4) void k_pick_l(StreamArgs a) {
         pick_greedy(a, r, cand, S, 0, true, none, tid == 0 && (cnt_raw & (1 << 29)) != 0, (st.flags & 4) != 0, st);
         return;
     }
-    if (S < 256 && direct_select(cand, a.cand_cap, S, k, scaled, buf, st)) {
+    if (S < 256 && direct_select(cand, a.cand_cap, S, k, scaled, buf, st, r)) {
         HSAMP_PHASE(9500 + r, 4);
         const uint32_t rflags = (st.flags & 4) ? ROWF_NAN : 0u;
         FinLds f;

@@ -5,13 +5,16 @@
 // repetition -> DRY -> frequency/presence -> temperature to each logit in
 // registers (sampler.cpp:235-264) and leaves the slice's candidates in
 // global scratch:
-//   - exact lists (sampling rows, k <= 64, penalties that only lower
-//     logits): every id whose final key can still be in the row's top k,
-//     filtered by a bound from the slice's own top keys; k_pick, one block
-//     per row on the XCD that streamed it, merges the row's lists;
-//   - general path (greedy rows, DRY, bias, k up to 1024, write-back,
-//     unaligned rows): a candidate buffer in LDS under a rising threshold
-//     (or the slice's argmax for a greedy row), merged by k_merge.
+//   - exact lists (sampling rows with k <= 1024 and greedy rows, penalties
+//     that only lower logits -- repetition, frequency/presence, DRY sharing
+//     their count window, bias <= 0): every id whose final key can still be
+//     in the row's top k, filtered by a bound from the slice's own top keys;
+//     k_pick (every k <= 64) or k_pick_l, one block per row on the XCD that
+//     streamed it, merges the row's lists;
+//   - general path (positive bias, DRY shorter than the repetition window,
+//     write-back, longer histories, ...): a candidate buffer in LDS under a
+//     rising threshold (or the slice's argmax for a greedy row), merged by
+//     k_merge.
 // The merge gives the exact top-k (value desc, index asc) and runs the rest
 // of the ladder over the <= k kept logits: softmax with glibc-exact expf and
 // index-order float sums, top-p over the (p desc, index asc) order, min-p,
@@ -1878,9 +1881,9 @@ __device__ uint32_t block_kth_bound16(const float (&cm)[NC], int need, Shared& s
     return prefix;
 }
 
-// A sampling row's slice [lo, hi) with exact lists (single tile, raw[] holds
-// it); the row's last slice (last_slice) also takes the ragged end that
-// whole-chunk loads leave out.
+// A sampling or greedy row's slice [lo, hi) with exact lists (one, two or
+// four tiles, raw[] holds them); the row's last slice (last_slice) also takes
+// the ragged end that whole-chunk loads leave out.
 template <int DT, bool VEC, bool PEN, bool MASK, int NC>
 __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan& P, int r, int lo, int hi,
                                              const uint4 (&raw)[NC], u64* out, int64_t slot,
@@ -2201,7 +2204,7 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
 // GR: the launch's greedy rows (true) or sampling rows (false); a batch with
 // both takes one launch of each, so that each loop has the whole register
 // budget of five blocks per CU.
-// EX: exact lists (sampling rows only, see stream_exact); LDS then
+// EX: exact lists (sampling and greedy rows, see stream_exact); LDS then
 // [history counts (PEN): 2 B per slice id, or (four-tile slices) a bitmap
 // over the slice's ids, 2 B rank prefix per bitmap word, 2 B entries for up
 // to 2048 distinct ids][allowed-id mask words][staged chunks].

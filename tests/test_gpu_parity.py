@@ -652,12 +652,14 @@ def test_greedy_rows_with_sampling_rows(sampler, wl, kernel_mode, dtype, kmix):
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("kmix", [40, 300])
-def test_nonpositive_bias_with_penalties(sampler, wl, kernel_mode, dtype, kmix):
-    """Logit bias that only lowers logits (bans at -inf, negative values on
-    the top tokens; up to 256 entries a row) beside repetition, DRY and
-    frequency/presence penalties: the exact lists mark the bias ids in their
-    count entries and apply the bias with the other stages (sampler.cpp:28-34)."""
-    rng = np.random.default_rng(91 + kmix)
+@pytest.mark.parametrize("signs", ["lowering", "mixed"])
+def test_bias_with_penalties(sampler, wl, kernel_mode, dtype, kmix, signs):
+    """Logit bias (bans at -inf, negative values on the top tokens, zeros;
+    with "mixed" also boosts that lift ids from far below the slices' bounds
+    to the top, among them the ragged end and id 0; up to 256 entries a row)
+    beside repetition, DRY and frequency/presence penalties: the exact lists
+    evaluate the bias ids on their own with every stage (sampler.cpp:28-34)."""
+    rng = np.random.default_rng(91 + kmix + (7 if signs == "mixed" else 0))
     B, V = 6, 151936
     x = rng.normal(size=(B, V)).astype(np.float32) * 2
     hist = rng.integers(0, V, size=(B, 512)).astype(np.int32)
@@ -668,7 +670,12 @@ def test_nonpositive_bias_with_penalties(sampler, wl, kernel_mode, dtype, kmix):
         b.update({int(t): float(-rng.uniform(0.1, 4.0)) for t in top[20:120]})
         b.update({int(t): 0.0 for t in rng.choice(V, 30, replace=False)})
         b.update({int(t): -1.5 for t in (0, V - 1, V - 2)})                # edges, the ragged end
-        bias.append(dict(list(b.items())[:256]))
+        if signs == "mixed":
+            low = np.argsort(x[r])[:5000]
+            b.update({int(t): float(rng.uniform(8.0, 20.0)) for t in rng.choice(low, 40, replace=False)})
+            b.update({int(t): float(rng.uniform(0.5, 3.0)) for t in top[150:200]})
+            b.update({int(t): 25.0 for t in (0, V - 1)} if r % 2 else {})
+        bias.append(dict(list(b.items())[-256:]))
         hist[r, -60:] = top[100:160]
     bias[3] = None
     plist = [wl.identity_params(top_k=kmix, temperature=0.7),

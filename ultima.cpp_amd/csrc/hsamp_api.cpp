@@ -289,8 +289,9 @@ int build_blob(HostScratch& hs, const ultima_hsamp_batch* b, Built& out) {
             // x/p, x*p (p >= 1), x - n*f - pp (f, pp >= 0), x - dry term (>= 0),
             // x + b (b <= 0) never raise x (sampler.cpp:28-99)
             if (((fl & RF_REP) && !(P.rep >= 1.0f)) || ((fl & RF_FP) && !(P.freq >= 0.0f && P.pres >= 0.0f)) ||
-                ((fl & RF_DRY) && !(q.dry_multiplier >= 0.0f && q.dry_base >= 0.0f)) || bias_up)
-                out.pen_lowers = false;
+                ((fl & RF_DRY) && !(q.dry_multiplier >= 0.0f && q.dry_base >= 0.0f)))
+                out.pen_lowers = out.pen_lowers_nb = false;
+            if (bias_up) out.pen_lowers = false;
         }
     }
     out.off_dry = align16(sizeof(RowPlan) * B);
@@ -334,16 +335,17 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     rp.V = V;
     // Exact lists (k_stream's EX kernels + k_pick, or k_pick_l when some
     // row's top-k is above 64): every row samples with top-k <= 1024 or is
-    // greedy, with penalties that can only lower a logit (logit bias <= 0, at
-    // most kBlock entries a row), from windows the stream's registers hold,
-    // DRY only where its window is also the frequency/presence window. The stream then leaves every
+    // greedy, with penalties that can only lower a logit (logit bias, at most
+    // kBlock entries a row, may raise: the stream evaluates those ids on their
+    // own), from windows the stream's registers hold, DRY only where its
+    // window is also the frequency/presence window. The stream then leaves every
     // candidate with its final key. ULTIMA_HSAMP_EXACT=0 turns it off (the
     // general kernels take every batch).
     const int kmax = std::max(1, bl.kmax);
     rp.kmax = kmax;
     rp.wb = (b->flags & ULTIMA_HSAMP_WRITEBACK) != 0;
     bool exact_ok = (bl.any_sample || bl.any_greedy) && !bl.any_full && kmax <= kLimitK && !rp.wb && bl.inv_ok &&
-                    (!bl.any_pen || (bl.pen_lowers && !bl.dry_split && bl.max_bias <= kBlock && bl.max_scan <= 8 * kBlock));
+                    (!bl.any_pen || (bl.pen_lowers_nb && !bl.dry_split && bl.max_bias <= kBlock && bl.max_scan <= 8 * kBlock));
     if (const char* ev = std::getenv("ULTIMA_HSAMP_EXACT")) exact_ok = exact_ok && ev[0] != '0';
     // 16-byte loads: aligned rows holding at least one whole chunk
     const bool vec_rows = (reinterpret_cast<uintptr_t>(b->logits) % 16 == 0) && ((b->logits_stride * es) % 16 == 0) &&

@@ -7,12 +7,13 @@
 // global scratch:
 //   - exact lists (sampling rows with k <= 1024 and greedy rows, penalties
 //     that only lower logits -- repetition, frequency/presence, DRY sharing
-//     their count window, bias <= 0): every id whose final key can still be
-//     in the row's top k, filtered by a bound from the slice's own top keys;
+//     their count window -- and up to 256 logit-bias ids, each evaluated on
+//     its own): every id whose final key can still be in the row's top k,
+//     filtered by a bound from the slice's own top keys;
 //     k_pick (every k <= 64) or k_pick_l, one block per row on the XCD that
 //     streamed it, merges the row's lists;
-//   - general path (positive bias, DRY shorter than the repetition window,
-//     write-back, longer histories, ...): a candidate buffer in LDS under a
+//   - general path (more bias entries, DRY shorter than the repetition
+//     window, write-back, longer histories, ...): a candidate buffer in LDS under a
 //     rising threshold (or the slice's argmax for a greedy row), merged by
 //     k_merge.
 // The merge gives the exact top-k (value desc, index asc) and runs the rest
@@ -1930,14 +1931,22 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
     // atomic per id); else a count over cw and a repetition bit.
     const int cw = P.dry_win > 0 ? P.dry_win : P.fp_win;
     const bool one = P.rep_win == 0 || cw == 0 || P.rep_win == cw;
+    // The row's logit-bias ids (at most kBlock): each marks its entry, and
+    // each is evaluated on its own (bias_pass below: a bias can raise a logit
+    // above the bound, so the chunk maxima cannot stand for it); the element
+    // passes leave them out. Their logits go out now, read at the end.
+    const bool bias = PEN && pen && (P.flags & RF_BIAS) != 0;
+    const uint32_t bsl = (uint32_t)(min(a.vocab, lo + a.slice_len) - lo);
+    uint32_t ob = 0xFFFFFFFFu;
+    float xb = 0.0f;
+    if (bias) {
+        ob = tid < P.bias_cnt ? (uint32_t)(a.bias_ids[P.bias_off + tid] - lo) : 0xFFFFFFFFu;
+        const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * T::ES;
+        xb = load_logit<DT>(rowp, lo + (int)min(ob, bsl - 1u));   // (clamped: no branch)
+    }
     if (PEN && pen) {
         const int L = hist_len_of(a, P, r), p0 = L - P.scan_len;
-        const int mhi = min(a.vocab, lo + a.slice_len);
-        const uint32_t wl = (uint32_t)(L - p0), sl = (uint32_t)(mhi - lo);
-        // the row's logit-bias ids (at most kBlock, none raising a logit):
-        // each marks its entry, so that the element pass applies the bias
-        const bool bias = (P.flags & RF_BIAS) != 0;
-        const uint32_t ob = (bias && tid < P.bias_cnt) ? (uint32_t)(a.bias_ids[P.bias_off + tid] - lo) : 0xFFFFFFFFu;
+        const uint32_t wl = (uint32_t)(L - p0), sl = bsl;
         uint32_t inw = 0u;   // bit q: pre[q] is a window id of this slice
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
@@ -2154,8 +2163,12 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
                 if (MASK && !((mbm[oc >> 5] >> (oc & 31)) & 1u)) x = -__builtin_inff();
                 uint32_t kf = raw_key(x);
                 const uint32_t hm = PEN ? hmark(oc) : 0u;
-                if (PEN && live && hm != 0u && kf >= Rlo) kf = final_raw_key(x, t, hentry(oc, hm), one, a, P, nanp);
-                const bool keep = live && kf >= Rlo && kf < Rhi;
+                uint32_t hv = 0u;
+                if (PEN && live && hm != 0u && kf >= Rlo) {
+                    hv = hentry(oc, hm);
+                    kf = final_raw_key(x, t, hv, one, a, P, nanp);
+                }
+                const bool keep = live && kf >= Rlo && kf < Rhi && !(hv & XC_BIAS);
                 const u64 mk2 = __ballot(keep);
                 if (mk2 != 0ull) {
                     int ob = 0;
@@ -2170,20 +2183,39 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
             wave_sync();   // the slots are read before the next round writes them
         }
         if (tl) {
-            const uint32_t kf = final_raw_key(xt, tt_id, PEN ? hentry((uint32_t)(tt_id - lo), hmark((uint32_t)(tt_id - lo))) : 0u, one, a, P, nanp);
-            if (kf >= Rlo && kf < Rhi) out[atomicAdd(&st.n, 1)] = comp(kf, tt_id);
+            const uint32_t ht = PEN ? hentry((uint32_t)(tt_id - lo), hmark((uint32_t)(tt_id - lo))) : 0u;
+            const uint32_t kf = final_raw_key(xt, tt_id, ht, one, a, P, nanp);
+            if (kf >= Rlo && kf < Rhi && !(ht & XC_BIAS)) out[atomicAdd(&st.n, 1)] = comp(kf, tt_id);
         }
         if (nanp) atomicOr(&st.flags, 1);
         HSAMP_PHASE(slot, 9);
         __syncthreads();
     };
+    // The bias ids of the slice whose final raw key lies in [Rlo, Rhi).
+    auto bias_pass = [&](uint32_t Rlo, uint32_t Rhi) {
+        if (!bias) return;
+        bool nanb = false;
+        if (ob < bsl) {
+            float x = xb;
+            if (MASK && !((mbm[ob >> 5] >> (ob & 31)) & 1u)) x = -__builtin_inff();
+            const int t = lo + (int)ob;
+            const uint32_t kf = final_raw_key(x, t, hentry(ob, hmark(ob)), one, a, P, nanb);
+            if (kf >= Rlo && kf < Rhi) out[atomicAdd(&st.n, 1)] = comp(kf, t);
+        }
+        if (nanb) atomicOr(&st.flags, 1);
+        __syncthreads();
+    };
     pass(R, 0xFFFFFFFFu);
+    bias_pass(R, 0xFFFFFFFFu);
     HSAMP_PHASE(slot, 5);
     // E. fewer than k ids kept above a raised bound (penalties took the rest
     // below it): every id down to the floor
     if (PEN && st.n < k) {
         const uint32_t Rf = greedy ? kFloor : raw_edge(max(scaled_key(kFloor, inv_t), kFloor), inv_t, P.temp);
-        if (R > Rf) pass(Rf, R);
+        if (R > Rf) {
+            pass(Rf, R);
+            bias_pass(Rf, R);
+        }
     }
     if (nanv) atomicOr(&st.flags, 1);
     __syncthreads();

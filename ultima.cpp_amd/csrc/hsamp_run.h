@@ -41,6 +41,7 @@ struct Built {
     int max_scan = 0;          // max history window over penalty rows
     int max_bias = 0;          // max logit-bias entries over rows
     bool pen_lowers = true;    // every penalty stage can only lower a logit
+    bool pen_lowers_nb = true; // every stage but the logit bias can only lower a logit
     bool any_dry = false;      // a row with the DRY stage
     bool inv_ok = true;        // every sampling row has 0 < fl(1/T) < inf
     bool any_mask = false;     // the batch carries an allowed-token mask

@@ -1934,19 +1934,17 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
     // The row's logit-bias ids (at most kBlock): each marks its entry, and
     // each is evaluated on its own (bias_pass below: a bias can raise a logit
     // above the bound, so the chunk maxima cannot stand for it); the element
-    // passes leave them out. Their logits go out now, read at the end.
+    // passes leave them out. (Their ids and logits are read again there:
+    // values held from here to there would cost every row registers.)
     const bool bias = PEN && pen && (P.flags & RF_BIAS) != 0;
     const uint32_t bsl = (uint32_t)(min(a.vocab, lo + a.slice_len) - lo);
-    uint32_t ob = 0xFFFFFFFFu;
-    float xb = 0.0f;
-    if (bias) {
-        ob = tid < P.bias_cnt ? (uint32_t)(a.bias_ids[P.bias_off + tid] - lo) : 0xFFFFFFFFu;
-        const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * T::ES;
-        xb = load_logit<DT>(rowp, lo + (int)min(ob, bsl - 1u));   // (clamped: no branch)
-    }
+    auto bias_off = [&]() -> uint32_t {   // this thread's bias id, as a slice offset (>= bsl: none)
+        return tid < P.bias_cnt ? (uint32_t)(a.bias_ids[P.bias_off + tid] - lo) : 0xFFFFFFFFu;
+    };
     if (PEN && pen) {
         const int L = hist_len_of(a, P, r), p0 = L - P.scan_len;
         const uint32_t wl = (uint32_t)(L - p0), sl = bsl;
+        const uint32_t ob = bias ? bias_off() : 0xFFFFFFFFu;
         uint32_t inw = 0u;   // bit q: pre[q] is a window id of this slice
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
@@ -2195,6 +2193,9 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
     auto bias_pass = [&](uint32_t Rlo, uint32_t Rhi) {
         if (!bias) return;
         bool nanb = false;
+        const uint32_t ob = bias_off();
+        const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * T::ES;
+        const float xb = load_logit<DT>(rowp, lo + (int)min(ob, bsl - 1u));   // (clamped: no branch)
         if (ob < bsl) {
             float x = xb;
             if (MASK && !((mbm[ob >> 5] >> (ob & 31)) & 1u)) x = -__builtin_inff();

@@ -47,8 +47,13 @@ __global__ __launch_bounds__(64) void k_decode_commit(int32_t* __restrict__ hist
                                                       int rows, int keep, StopIds stop, int n_stop) {
     const int r = blockIdx.x;
     if (r >= rows) return;
+    // the row's token, state, length and budget go out together: one memory
+    // round trip before any decision
     const int32_t tok = tokens[r];
-    if (active[r] == 0) {
+    const int32_t act = active[r];
+    int L = len[r];
+    const int32_t bud = budget != nullptr ? budget[r] : 0;
+    if (act == 0) {
         if (threadIdx.x == 0) tokens[r] = -1;
         return;
     }
@@ -59,21 +64,34 @@ __global__ __launch_bounds__(64) void k_decode_commit(int32_t* __restrict__ hist
         return;
     }
     int32_t* h = hist + (int64_t)r * stride;
-    int L = len[r];
     L = L < 0 ? 0 : L;
     if (L >= stride) {
         // [stride - keep, stride) -> [0, keep); keep <= stride / 2, so the
         // ranges overlap at most in h[keep], which thread 0 reads (i = 0)
         // before it writes it below
         const int64_t from = stride - keep;
-        for (int i = threadIdx.x; i < keep; i += 64) h[i] = h[from + i];
+        // eight ids per thread in flight, then their stores (the ranges do not
+        // overlap: from >= keep)
+        for (int i0 = 0; i0 < keep; i0 += 8 * 64) {
+            int32_t v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = i0 + j * 64 + (int)threadIdx.x;
+                v[j] = h[from + min(i, keep - 1)];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = i0 + j * 64 + (int)threadIdx.x;
+                if (i < keep) h[i] = v[j];
+            }
+        }
         L = keep;
     }
     if (threadIdx.x == 0) {
         h[L] = tok;
         len[r] = L + 1;
         if (budget != nullptr) {
-            const int32_t b = budget[r] - 1;
+            const int32_t b = bud - 1;
             budget[r] = b;
             if (b <= 0) active[r] = 0;
         }

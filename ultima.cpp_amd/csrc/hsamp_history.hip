@@ -24,16 +24,32 @@ __global__ __launch_bounds__(64) void k_history_push(int32_t* __restrict__ hist,
     const int r = blockIdx.x;
     if (r >= rows) return;
     int32_t* h = hist + (int64_t)r * stride;
+    // the length and the token go out together: one memory round trip
     int L = len[r];
+    const int32_t tok = tokens[r];
     L = L < 0 ? 0 : L;
     if (L >= stride) {
         // [L - keep, L) -> [0, keep): L = stride here, keep <= stride / 2
         const int64_t from = stride - keep;
-        for (int i = threadIdx.x; i < keep; i += 64) h[i] = h[from + i];
+        // eight ids per thread in flight, then their stores (the ranges do not
+        // overlap: from >= keep)
+        for (int i0 = 0; i0 < keep; i0 += 8 * 64) {
+            int32_t v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = i0 + j * 64 + (int)threadIdx.x;
+                v[j] = h[from + min(i, keep - 1)];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = i0 + j * 64 + (int)threadIdx.x;
+                if (i < keep) h[i] = v[j];
+            }
+        }
         L = keep;
     }
     if (threadIdx.x == 0) {
-        h[L] = tokens[r];
+        h[L] = tok;
         len[r] = L + 1;
     }
 }

@@ -58,7 +58,10 @@ def parse():
                     help="head: the logits producer (final rmsnorm + lm-head matvec) and the "
                          "producer + sampler step instead of the sampler alone; verify: a drafted "
                          "block's verification (ultima_hsamp_verify_block); decode: one multi-slot "
-                         "server decode step (run + ultima_hsamp_decode_commit, device histories)")
+                         "server decode step (ultima_hsamp_run_commit, device histories)")
+    ap.add_argument("--commit", default="fused", choices=["fused", "separate"],
+                    help="decode workload: the stop / push rules applied inside the sampler's "
+                         "kernels (ultima_hsamp_run_commit) or by ultima_hsamp_decode_commit after run")
     ap.add_argument("--block", type=int, default=16, help="verify workload: positions per block")
     ap.add_argument("--slots", type=int, default=64, help="decode workload: slots per step")
     ap.add_argument("--head-rows", type=int, default=1, help="head workload: hidden-state rows per step")
@@ -373,9 +376,13 @@ def callers_main(args):
         stop = (151643, 151645)   # eos, im_end of the Qwen vocabulary
 
         def step(i, s):
-            sampler.run(logits[i], params, us[i], hist=hist, hist_len=[W] * rows, hist_len_dev=lens, outputs=outs,
-                        stream=s)
-            hs.decode_commit(hist, lens, outs["token"], active, keep, stop, stream=s)
+            if args.commit == "fused":
+                sampler.run_commit(logits[i], params, us[i], hist, [W] * rows, lens, active, keep, stop,
+                                   outputs=outs, stream=s)
+            else:
+                sampler.run(logits[i], params, us[i], hist=hist, hist_len=[W] * rows, hist_len_dev=lens,
+                            outputs=outs, stream=s)
+                hs.decode_commit(hist, lens, outs["token"], active, keep, stop, stream=s)
         bytes_step = rows * V * 4 + rows * W * 4
         unit, metric = "slot tokens/s", f"multi-slot decode tokens/sec ({rows} slots, V={V} f32, SamplerParams{{}})"
     with torch.cuda.stream(stream):
@@ -449,7 +456,8 @@ def callers_main(args):
         "dtype": "f32",
         "data": "synthetic (random normal logits, random histories and drafts, 8 rotating sets)",
         "config": {"workload": f"{args.workload}: rows={rows} V={V} f32 SamplerParams{{}}",
-                   "rows": rows, "vocab": V, "bytes_per_step": bytes_step},
+                   "rows": rows, "vocab": V, "bytes_per_step": bytes_step,
+                   **({} if verify else {"commit": args.commit})},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_GBS, "traffic": None,
                      "kernel": "the whole step (every kernel of it)", "algorithmic_bytes_per_launch": bytes_step},

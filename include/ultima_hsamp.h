@@ -252,6 +252,27 @@ int ultima_hsamp_decode_commit(int32_t* hist, int64_t hist_stride, int32_t* hist
                                int32_t* active, int32_t* budget, int32_t rows, int32_t keep,
                                const int32_t* stop_ids, int32_t n_stop, void* hip_stream);
 
+/* The same step as ultima_hsamp_run followed by ultima_hsamp_decode_commit,
+ * with the commit's rules applied where each row's token is decided (no
+ * kernel of its own): for decode loops whose every step samples and commits.
+ * The fields mean what ultima_hsamp_decode_commit's arguments mean; the batch
+ * must not ask for write-back (ULTIMA_HSAMP_ERR_UNSUPPORTED). hist and
+ * hist_len_dev are normally the batch's own (batch.hist, batch.hist_len_dev):
+ * the rows' histories the step samples from are the ones it appends to. */
+typedef struct ultima_hsamp_commit {
+    int32_t* hist;              /* device [rows, hist_stride] */
+    int64_t hist_stride;        /* >= 2 */
+    int32_t* hist_len_dev;      /* device [rows] */
+    int32_t* active;            /* device [rows]: 0 = the row has ended */
+    int32_t* budget;            /* device [rows] or NULL: tokens a row may still emit */
+    int32_t keep;               /* 1 <= keep <= hist_stride / 2 */
+    int32_t n_stop;             /* 0 .. 8 */
+    const int32_t* stop_ids;    /* HOST [n_stop] */
+} ultima_hsamp_commit;
+
+int ultima_hsamp_run_commit(ultima_hsamp* h, const ultima_hsamp_batch* batch, const ultima_hsamp_commit* commit,
+                            void* hip_stream);
+
 /* Block verification: the target model's logits for every position of a
  * drafted block ([block_size][vocab] as a drafter proposes it,
  * /root/reference/include/ultima/model/dspark.hpp:76-91; the reference's host

@@ -101,7 +101,7 @@ def test_struct_layouts_match_the_header(pkg, tmp_path):
     from pathlib import Path
     root = Path(__file__).resolve().parents[1]
     structs = {"ultima_hsamp_params": hs.Params, "ultima_hsamp_batch": hs.Batch, "ultima_hsamp_head": hs.Head,
-               "ultima_hsamp_verify": hs.Verify}
+               "ultima_hsamp_verify": hs.Verify, "ultima_hsamp_commit": hs.Commit}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "ultima_hsamp.h"', 'int main(void) {']
     for cname, py in structs.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
@@ -151,6 +151,33 @@ def test_decode_commit_rejects_bad_arguments(pkg):
     assert L.ultima_hsamp_decode_commit(p, 8, p, p, p, None, 1, 4, None, 2, None) == hs.ERR_INVALID     # no ids
     assert L.ultima_hsamp_decode_commit(p, 8, p, p, p, None, 1, 4, stop, 9, None) == hs.ERR_INVALID     # > 8 ids
     assert L.ultima_hsamp_decode_commit(p, 8, p, p, p, None, 1, 4, stop, -1, None) == hs.ERR_INVALID
+
+
+def test_run_commit_rejects_bad_arguments(pkg):
+    """The commit's checks (decode_commit's) run before the batch is looked at
+    (no GPU needed); a write-back batch is refused."""
+    hs = pkg.hsamp
+    L = hs.lib()
+    h = ctypes.c_void_p(16)   # never dereferenced: every call below fails its checks first
+    p = 16
+    stop = (ctypes.c_int32 * 9)(*range(9))
+
+    def mk(**kw):
+        c = hs.Commit()
+        c.hist, c.hist_stride, c.hist_len_dev, c.active, c.keep = p, 8, p, p, 4
+        for k, x in kw.items():
+            setattr(c, k, x)
+        return c
+
+    b = hs.Batch()
+    assert L.ultima_hsamp_run_commit(h, ctypes.byref(b), None, None) == hs.ERR_INVALID
+    for bad in (dict(hist=None), dict(hist_len_dev=None), dict(active=None), dict(hist_stride=1), dict(keep=0),
+                dict(keep=5), dict(n_stop=2), dict(n_stop=9, stop_ids=ctypes.cast(stop, ctypes.c_void_p)),
+                dict(n_stop=-1)):
+        assert L.ultima_hsamp_run_commit(h, ctypes.byref(b), ctypes.byref(mk(**bad)), None) == hs.ERR_INVALID, bad
+    b.flags = hs.WRITEBACK
+    assert L.ultima_hsamp_run_commit(h, ctypes.byref(b), ctypes.byref(mk()), None) == hs.ERR_UNSUPPORTED
+    assert L.ultima_hsamp_run_commit(None, None, ctypes.byref(mk()), None) == hs.ERR_INVALID
 
 
 def test_verify_block_rejects_bad_arguments(pkg):

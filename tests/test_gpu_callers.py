@@ -149,15 +149,30 @@ def _commit_oracle(x, params, u, host, active, budget, stop):
     return toks, margins
 
 
+@pytest.mark.parametrize("fused", [False, True])
 @pytest.mark.parametrize("captured", [False, True])
-def test_decode_commit_runs_the_server_loop_on_many_slots(hs, sampler, wl, captured):
+def test_decode_commit_runs_the_server_loop_on_many_slots(hs, sampler, wl, captured, fused):
+    """fused: ultima_hsamp_run_commit (the rules applied where each token is
+    decided); else ultima_hsamp_run then ultima_hsamp_decode_commit."""
     import torch
     dev = torch.device("cuda:0")
     B, V, W = 6, 4096, 64
     stride, keep = 2 * W, W
     eos, im_end = 7, 11
     stop = (eos, im_end)
-    rng = np.random.default_rng(21 + int(captured))
+    out = None
+    rng = np.random.default_rng(21 + int(captured) + 2 * int(fused))
+
+    def step_fn(hl):
+        nonlocal out
+        if fused:
+            out = sampler.run_commit(x_d, params, u_d, hist, hl, lens, active, keep, stop, budget, outputs=out,
+                                     stream=stream)
+        else:
+            out = sampler.run(x_d, params, u_d, hist=hist, hist_len=hl, hist_len_dev=lens, outputs=out,
+                              stream=stream)
+            hs.decode_commit(hist, lens, out["token"], active, keep, stop, budget, stream=stream)
+
     # (the server's knobs with DRY looking back 48 ids: every window within W,
     # as the device-history plan requires)
     params = [_knobs(wl, k) for k in ("penalties", "server", "plain", "penalties", "server", "plain")]
@@ -176,7 +191,6 @@ def test_decode_commit_runs_the_server_loop_on_many_slots(hs, sampler, wl, captu
     act_h = [True] * B
     x_d = torch.empty((B, V), dtype=torch.float32, device=dev)
     u_d = torch.empty(B, dtype=torch.float64, device=dev)
-    out = None
     stream = torch.cuda.Stream(dev)
     graph = None
     steps = 2 * stride + 10                   # through a compaction
@@ -192,28 +206,25 @@ def test_decode_commit_runs_the_server_loop_on_many_slots(hs, sampler, wl, captu
         # history may be shorter than the plan's windows)
         steady = all(hl[r] == W or not act_h[r] for r in range(B))
         if captured and graph is None and steady:
-            # capture the steady-state step once (its plan no longer changes)
+            # this step runs eagerly with the steady-state plan, then the same
+            # step is captured once (its plan no longer changes) and replayed
+            # from the next step on
             with torch.cuda.stream(stream):
-                out = sampler.run(x_d, params, u_d, hist=hist, hist_len=[W] * B, hist_len_dev=lens, outputs=out,
-                                  stream=stream)
+                step_fn([W] * B)
             stream.synchronize()
             graph = torch.cuda.CUDAGraph()
+            snap = [t.clone() for t in (hist, lens, active, budget)]
             with torch.cuda.graph(graph, stream=stream):
-                sampler.run(x_d, params, u_d, hist=hist, hist_len=[W] * B, hist_len_dev=lens, outputs=out,
-                            stream=stream)
-                hs.decode_commit(hist, lens, out["token"], active, keep, stop, budget, stream=stream)
+                step_fn([W] * B)
             stream.synchronize()
-            # that uncaptured run sampled this step's rows: commit it as the step
-            with torch.cuda.stream(stream):
-                hs.decode_commit(hist, lens, out["token"], active, keep, stop, budget, stream=stream)
+            for t, c in zip((hist, lens, active, budget), snap):   # (capture does not run the kernels)
+                assert torch.equal(t, c)
         elif graph is not None:
             torch.cuda.synchronize()
             graph.replay()
         else:
             with torch.cuda.stream(stream):
-                out = sampler.run(x_d, params, u_d, hist=hist, hist_len=hl, hist_len_dev=lens, outputs=out,
-                                  stream=stream)
-                hs.decode_commit(hist, lens, out["token"], active, keep, stop, budget, stream=stream)
+                step_fn(hl)
         torch.cuda.synchronize()
         want, margins = _commit_oracle(x, params, u, host, act_h, budget_h, stop)
         got = out["token"].cpu().numpy()

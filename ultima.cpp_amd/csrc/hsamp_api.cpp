@@ -517,6 +517,16 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
 int launch_run(const RunPlan& rp, const Built& bl, const ultima_hsamp_batch* b, const RunBuffers& buf,
                hipStream_t stream, hipEvent_t phase_ev) {
     StreamArgs a{};
+    if (const ultima_hsamp_commit* c = buf.commit) {
+        a.c_hist = c->hist;
+        a.c_stride = c->hist_stride;
+        a.c_len = c->hist_len_dev;
+        a.c_active = c->active;
+        a.c_budget = c->budget;
+        a.c_keep = c->keep;
+        a.c_nstop = c->n_stop;
+        for (int q = 0; q < c->n_stop; ++q) a.c_stop[q] = c->stop_ids[q];
+    }
     a.logits = b->logits;
     a.logits_stride = b->logits_stride;
     a.hist = b->hist;
@@ -813,7 +823,27 @@ int ultima_hsamp_destroy(ultima_hsamp* h) {
     return ULTIMA_HSAMP_OK;
 }
 
+namespace {
+int run_impl(ultima_hsamp* h, const ultima_hsamp_batch* b, const ultima_hsamp_commit* commit, void* hip_stream);
+}
+
 int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_stream) {
+    return run_impl(h, b, nullptr, hip_stream);
+}
+
+int ultima_hsamp_run_commit(ultima_hsamp* h, const ultima_hsamp_batch* b, const ultima_hsamp_commit* c,
+                            void* hip_stream) {
+    if (c == nullptr || c->hist == nullptr || c->hist_len_dev == nullptr || c->active == nullptr)
+        return ULTIMA_HSAMP_ERR_INVALID;
+    if (c->hist_stride < 2 || c->keep < 1 || (int64_t)c->keep > c->hist_stride / 2 || c->hist_stride > INT32_MAX)
+        return ULTIMA_HSAMP_ERR_INVALID;
+    if (c->n_stop < 0 || c->n_stop > 8 || (c->n_stop > 0 && c->stop_ids == nullptr)) return ULTIMA_HSAMP_ERR_INVALID;
+    if (b != nullptr && (b->flags & ULTIMA_HSAMP_WRITEBACK)) return ULTIMA_HSAMP_ERR_UNSUPPORTED;
+    return run_impl(h, b, c, hip_stream);
+}
+
+namespace {
+int run_impl(ultima_hsamp* h, const ultima_hsamp_batch* b, const ultima_hsamp_commit* commit, void* hip_stream) {
     if (h == nullptr) return ULTIMA_HSAMP_ERR_INVALID;
     int st = validate_batch(b, h->max_rows, h->max_vocab);
     if (st != ULTIMA_HSAMP_OK) return st;
@@ -857,11 +887,13 @@ int ultima_hsamp_run(ultima_hsamp* h, const ultima_hsamp_batch* b, void* hip_str
     buf.fin_idx = h->fin_idx;
     buf.fin_n = h->fin_n;
     buf.blob = slot->dev;
+    buf.commit = commit;
     st = launch_run(rp, bl, b, buf, stream, h->phase_ev);
     if (st != ULTIMA_HSAMP_OK) return st;
     if (!capturing) HIP_TRY(hipEventRecord(slot->ev, stream));
     return ULTIMA_HSAMP_OK;
 }
+}  // namespace
 
 int ultima_hsamp_read_probe(ultima_hsamp* h, const ultima_hsamp_batch* b, float* out, void* hip_stream) {
     if (h == nullptr || out == nullptr) return ULTIMA_HSAMP_ERR_INVALID;

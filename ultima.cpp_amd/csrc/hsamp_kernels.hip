@@ -594,6 +594,57 @@ __device__ __forceinline__ float elem(const uint4& r, int c) {
     return __uint_as_float((c & 1) ? (x & 0xFFFF0000u) : (x << 16));
 }
 
+// ---- the token ---------------------------------------------------------------------
+
+// Row r's token, written by the one thread that decided it, with
+// ultima_hsamp_run_commit's rules when the launch carries them (the server
+// loop's per token, src/server/http_server.cpp:174-201): an ended row
+// (active 0) gets -1; -1 or a stop id ends the row without being pushed;
+// any other token is appended to the row's device history (a full row first
+// keeps its last c_keep ids at its front) and counted against the row's
+// budget, which ends the row at 0.
+__device__ __forceinline__ void emit_token(const StreamArgs& a, int r, int32_t tok) {
+    if (a.c_hist == nullptr) {
+        a.token[r] = tok;
+        return;
+    }
+    if (a.c_active[r] == 0) {
+        a.token[r] = -1;
+        return;
+    }
+    a.token[r] = tok;
+    bool end = tok < 0;
+    for (int i = 0; i < a.c_nstop; ++i) end = end || tok == a.c_stop[i];
+    if (end) {
+        a.c_active[r] = 0;
+        return;
+    }
+    int32_t* h = a.c_hist + (int64_t)r * a.c_stride;
+    int L = max(a.c_len[r], 0);
+    if (L >= a.c_stride) {
+        // [stride - keep, stride) -> [0, keep) (keep <= stride / 2: the
+        // ranges do not overlap), sixteen ids in flight at a time
+        const int keep = a.c_keep;
+        const int64_t from = a.c_stride - keep;
+        for (int i0 = 0; i0 < keep; i0 += 16) {
+            int32_t v[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[j] = h[from + min(i0 + j, keep - 1)];
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                if (i0 + j < keep) h[i0 + j] = v[j];
+        }
+        L = keep;
+    }
+    h[L] = tok;
+    a.c_len[r] = L + 1;
+    if (a.c_budget != nullptr) {
+        const int32_t b = a.c_budget[r] - 1;
+        a.c_budget[r] = b;
+        if (b <= 0) a.c_active[r] = 0;
+    }
+}
+
 // ---- finalize over the kept set ------------------------------------------------
 
 struct FinLds {
@@ -960,7 +1011,7 @@ __device__ __attribute__((noinline)) void finalize_row(const StreamArgs& a, cons
         if (tid == 0) tok = uniform_draw(V, u);
     }
     if (tid == 0) {
-        a.token[r] = tok;
+        emit_token(a, r, tok);
         if (a.row_flags != nullptr) a.row_flags[r] = rflags;
         if (a.kept_count != nullptr) a.kept_count[r] = nkept;
         if (a.fin_n != nullptr) a.fin_n[r] = nkept;
@@ -1336,7 +1387,7 @@ __device__ __forceinline__ void wave_finalize(const StreamArgs& a, const RowPlan
         if (lane == 0) tok = uniform_draw(V, u);
     }
     if (lane == 0) {
-        a.token[r] = tok;
+        emit_token(a, r, tok);
         if (a.row_flags != nullptr) a.row_flags[r] = rflags;
         if (a.kept_count != nullptr) a.kept_count[r] = nkept;
         if (a.fin_n != nullptr) a.fin_n[r] = nkept;
@@ -2921,7 +2972,7 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
             // settled with the table, any other by its logit
             const bool pen0 = pen && !lmode && in_table(0);
             const bool nan0 = pen0 ? st.nan0 != 0 : nan_at0;
-            a.token[r] = nan0 ? 0 : comp_idx(best);
+            emit_token(a, r, nan0 ? 0 : comp_idx(best));
             if (a.row_flags != nullptr) a.row_flags[r] = ROWF_GREEDY | ((st.flags & 4) ? ROWF_NAN : 0u);
             if (a.topk_count != nullptr) a.topk_count[r] = -1;
             if (a.kept_count != nullptr) a.kept_count[r] = 0;
@@ -3373,7 +3424,7 @@ __global__ __launch_bounds__(kBlock, 3) void k_merge(StreamArgs a) {
                 pen0 = kk == 0u;
             }
             const bool nan0 = pen0 ? st.nan0 != 0 : nan_at0;
-            a.token[r] = nan0 ? 0 : comp_idx(best);
+            emit_token(a, r, nan0 ? 0 : comp_idx(best));
             if (a.row_flags != nullptr) a.row_flags[r] = ROWF_GREEDY | ((st.flags & 4) ? ROWF_NAN : 0u);
             if (a.topk_count != nullptr) a.topk_count[r] = -1;
             if (a.kept_count != nullptr) a.kept_count[r] = 0;
@@ -3445,7 +3496,7 @@ __device__ __forceinline__ void pick_greedy(const StreamArgs& a, int r, const u6
     if (tid == 0) st.nan0 = nan0 ? 1 : 0;
     best = block_max_u64(best, st);   // (its barriers publish st.nan0)
     if (tid == 0) {
-        a.token[r] = (st.nan0 || best == 0ull) ? 0 : comp_idx(best);
+        emit_token(a, r, (st.nan0 || best == 0ull) ? 0 : comp_idx(best));
         if (a.row_flags != nullptr) a.row_flags[r] = ROWF_GREEDY | (nan_any ? ROWF_NAN : 0u);
         if (a.topk_count != nullptr) a.topk_count[r] = -1;
         if (a.kept_count != nullptr) a.kept_count[r] = 0;
@@ -4555,7 +4606,7 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
         for (int i = tid; i < V; i += kFT) row[i] = fv[i];
     }
     if (tid == 0) {
-        a.token[r] = tok;
+        emit_token(a, r, tok);
         if (a.row_flags != nullptr) a.row_flags[r] = rflags | ((st.flags & 4) ? ROWF_NAN : 0u);
         if (a.kept_count != nullptr) a.kept_count[r] = nkept;
     }

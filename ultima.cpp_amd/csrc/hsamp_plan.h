@@ -138,6 +138,16 @@ struct StreamArgs {
     uint32_t* gtab;             // [rows * 2 * mhash_slots] penalty tables, or NULL: tables in LDS
     uint32_t merge_lds;         // dynamic LDS of k_merge
     uint32_t lds_bytes;         // dynamic LDS size of the launch
+    // ultima_hsamp_run_commit: the decode loop's per-token rules applied
+    // where each row's token is decided (c_hist NULL: none)
+    int32_t* c_hist;
+    int64_t c_stride;
+    int32_t* c_len;
+    int32_t* c_active;
+    int32_t* c_budget;          // NULL: no budgets
+    int32_t c_keep;
+    int32_t c_nstop;
+    int32_t c_stop[8];
 };
 
 constexpr int kBlock = 256;        // threads per block (4 wave64)

@@ -83,6 +83,7 @@ struct RunBuffers {
     int32_t* fin_idx = nullptr;
     int32_t* fin_n = nullptr;
     const char* blob = nullptr;   // device copy of HostScratch::blob
+    const ultima_hsamp_commit* commit = nullptr;   // ultima_hsamp_run_commit's rules, or none
 };
 
 // Argument checks of ultima_hsamp_run (limits: max_rows / max_vocab).

@@ -93,6 +93,20 @@ class Head(ctypes.Structure):
     ]
 
 
+class Commit(ctypes.Structure):
+    """ultima_hsamp_commit (include/ultima_hsamp.h)."""
+    _fields_ = [
+        ("hist", ctypes.c_void_p),
+        ("hist_stride", ctypes.c_int64),
+        ("hist_len_dev", ctypes.c_void_p),
+        ("active", ctypes.c_void_p),
+        ("budget", ctypes.c_void_p),
+        ("keep", ctypes.c_int32),
+        ("n_stop", ctypes.c_int32),
+        ("stop_ids", ctypes.c_void_p),
+    ]
+
+
 class Verify(ctypes.Structure):
     """ultima_hsamp_verify (include/ultima_hsamp.h)."""
     _fields_ = [
@@ -172,6 +186,8 @@ def lib() -> ctypes.CDLL:
         L.ultima_hsamp_lm_head.argtypes = [ctypes.POINTER(Head), vp]
         L.ultima_hsamp_decode_commit.restype = ctypes.c_int
         L.ultima_hsamp_decode_commit.argtypes = [vp, i64, vp, vp, vp, vp, i32, i32, vp, i32, vp]
+        L.ultima_hsamp_run_commit.restype = ctypes.c_int
+        L.ultima_hsamp_run_commit.argtypes = [vp, ctypes.POINTER(Batch), ctypes.POINTER(Commit), vp]
         L.ultima_hsamp_verify_work_ints.restype = i64
         L.ultima_hsamp_verify_work_ints.argtypes = [i32, i32]
         L.ultima_hsamp_verify_block.restype = ctypes.c_int
@@ -410,6 +426,26 @@ class Sampler:
         between the stream and merge kernels of every later run()."""
         ptr = None if event is None else ctypes.c_void_p(event.cuda_event)
         check(lib().ultima_hsamp_set_phase_event(self.h, ptr), "set_phase_event")
+
+    def run_commit(self, logits, params, u, hist, hist_len, hist_len_dev, active, keep: int, stop_ids=(),
+                   budget=None, mask=None, bias=None, outputs=None, stream=None):
+        """ultima_hsamp_run_commit: run() over the rows' device histories
+        (hist int32 [rows, stride], hist_len_dev int32 [rows]) with
+        decode_commit's rules applied where each token is decided."""
+        import torch
+        b, out, keep_alive, s = _batch(logits, params, u, hist, hist_len, mask, bias, False, False, None, stream,
+                                       outputs, False, hist_len_dev=hist_len_dev)
+        stop = np.asarray(list(stop_ids), np.int32)
+        c = Commit()
+        c.hist, c.hist_stride, c.hist_len_dev = hist.data_ptr(), hist.stride(0), hist_len_dev.data_ptr()
+        c.active = active.data_ptr()
+        c.budget = budget.data_ptr() if budget is not None else None
+        c.keep, c.n_stop = int(keep), int(stop.size)
+        c.stop_ids = stop.ctypes.data if stop.size else None
+        check(lib().ultima_hsamp_run_commit(self.h, ctypes.byref(b), ctypes.byref(c), ctypes.c_void_p(s.cuda_stream)),
+              "run_commit")
+        self._keep = (keep_alive, stop)
+        return out
 
     def verify_block(self, logits, params: dict, u, draft=None, hist=None, mask=None, bias=None, stream=None):
         """ultima_hsamp_verify_block on torch tensors of one device: logits

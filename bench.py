@@ -63,6 +63,9 @@ def parse():
                     help="decode workload: the stop / push rules applied inside the sampler's "
                          "kernels (ultima_hsamp_run_commit) or by ultima_hsamp_decode_commit after run")
     ap.add_argument("--block", type=int, default=16, help="verify workload: positions per block")
+    ap.add_argument("--separate-draft", action="store_true",
+                    help="verify workload: drafts in their own array (prefix rows built) instead of "
+                         "appended to the sequence's ids")
     ap.add_argument("--slots", type=int, default=64, help="decode workload: slots per step")
     ap.add_argument("--head-rows", type=int, default=1, help="head workload: hidden-state rows per step")
     ap.add_argument("--head-hidden", type=int, default=4096, help="head workload: hidden size H")
@@ -358,8 +361,11 @@ def callers_main(args):
     stream = torch.cuda.Stream(dev)
     rng = np.random.default_rng(3)
     if verify:
-        hist = torch.from_numpy(rng.integers(0, V, H).astype(np.int32)).to(dev)
-        draft = torch.from_numpy(rng.integers(0, V, rows - 1).astype(np.int32)).to(dev)
+        seq = torch.from_numpy(rng.integers(0, V, H + rows - 1).astype(np.int32)).to(dev)
+        if args.separate_draft:
+            hist, draft = seq[:H].clone(), seq[H:].clone()
+        else:
+            hist, draft = seq[:H], seq[H:]   # the drafts appended to the sequence's ids: read in place
 
         def step(i, s):
             sampler.verify_block(logits[i], p, us[i], draft=draft, hist=hist, stream=s)
@@ -457,7 +463,8 @@ def callers_main(args):
         "data": "synthetic (random normal logits, random histories and drafts, 8 rotating sets)",
         "config": {"workload": f"{args.workload}: rows={rows} V={V} f32 SamplerParams{{}}",
                    "rows": rows, "vocab": V, "bytes_per_step": bytes_step,
-                   **({} if verify else {"commit": args.commit})},
+                   **({"drafts": "separate" if args.separate_draft else "after the history"} if verify
+                      else {"commit": args.commit})},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_GBS, "traffic": None,
                      "kernel": "the whole step (every kernel of it)", "algorithmic_bytes_per_launch": bytes_step},

@@ -106,7 +106,8 @@ typedef struct ultima_hsamp_batch {
     void* logits;               /* device [rows, logits_stride] elements of dtype */
     int64_t logits_stride;      /* elements between rows, >= vocab */
     const int32_t* hist;        /* device [rows, hist_stride] ids, oldest first; NULL if unused */
-    int64_t hist_stride;        /* >= max hist_len */
+    int64_t hist_stride;        /* >= max hist_len; or 0: one history shared by every row,
+                                   row r its first hist_len ids (not with hist_len_dev) */
     const uint32_t* mask;       /* device [rows, mask_stride] words or NULL: bit t of word t>>5 */
     int64_t mask_stride;        /* >= ceil(vocab / 32) */
     const double* u;            /* device [rows] uniforms in [0, 1) */
@@ -290,7 +291,9 @@ typedef struct ultima_hsamp_verify {
     int32_t dtype;              /* ULTIMA_HSAMP_F32 or ULTIMA_HSAMP_BF16 */
     void* logits;               /* device [n_pos, logits_stride]: position i's logits */
     int64_t logits_stride;      /* elements between positions, >= vocab */
-    const int32_t* draft;       /* device [n_pos - 1] drafted tokens (may be NULL when n_pos == 1) */
+    const int32_t* draft;       /* device [n_pos - 1] drafted tokens (may be NULL when n_pos == 1);
+                                   at hist + hist_len (the drafts appended to the sequence's ids)
+                                   the rows read that one array in place: no prefix rows built */
     const int32_t* hist;        /* device [hist_len]: the sequence's recent ids before the block, oldest first */
     int32_t hist_len;           /* >= 0 */
     const uint32_t* mask;       /* device [n_pos, mask_stride] allowed-token words or NULL */

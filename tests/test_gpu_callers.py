@@ -41,7 +41,9 @@ def _loop(xs, p, hist, u, draft):
     return out, margins
 
 
-def _verify_case(hs, sampler, wl, xs, p, hist, u, draft, dtype):
+def _verify_case(hs, sampler, wl, xs, p, hist, u, draft, dtype, one_buffer=False):
+    """one_buffer: the drafts follow the history in one device array (the
+    rows read it in place), else two separate arrays (prefix rows built)."""
     import torch
     dev = torch.device("cuda:0")
     if dtype == "bf16":
@@ -50,10 +52,14 @@ def _verify_case(hs, sampler, wl, xs, p, hist, u, draft, dtype):
         xd = torch.from_numpy(bits.view(np.int16)).to(dev).view(torch.bfloat16)
     else:
         xd = torch.from_numpy(xs).to(dev)
-    toks, count, flags = sampler.verify_block(
-        xd, p, torch.from_numpy(u).to(dev),
-        draft=torch.from_numpy(np.asarray(draft, np.int32)).to(dev) if len(draft) else None,
-        hist=torch.from_numpy(np.asarray(hist, np.int32)).to(dev) if len(hist) else None)
+    if one_buffer:
+        seq = torch.from_numpy(np.concatenate([np.asarray(hist, np.int32), np.asarray(draft, np.int32)])).to(dev)
+        hd = seq[:len(hist)] if len(hist) else None
+        dd = seq[len(hist):] if len(draft) else None
+    else:
+        dd = torch.from_numpy(np.asarray(draft, np.int32)).to(dev) if len(draft) else None
+        hd = torch.from_numpy(np.asarray(hist, np.int32)).to(dev) if len(hist) else None
+    toks, count, flags = sampler.verify_block(xd, p, torch.from_numpy(u).to(dev), draft=dd, hist=hd)
     torch.cuda.synchronize()
     want, margins = _loop(xs, p, hist, u, draft)
     got = toks.cpu().numpy()[: int(count.cpu()[0])].tolist()
@@ -68,18 +74,21 @@ def _verify_case(hs, sampler, wl, xs, p, hist, u, draft, dtype):
     return got
 
 
+@pytest.mark.parametrize("layout", ["separate", "one_buffer", "no_history"])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("kind", ["penalties", "server", "plain"])
-def test_verify_block_equals_the_sequential_loop(hs, sampler, wl, dtype, kind):
-    rng = np.random.default_rng({"penalties": 1, "server": 2, "plain": 3}[kind] + (10 if dtype == "bf16" else 0))
-    V, n, L = 32000, 8, 120
+def test_verify_block_equals_the_sequential_loop(hs, sampler, wl, dtype, kind, layout):
+    rng = np.random.default_rng({"penalties": 1, "server": 2, "plain": 3}[kind] + (10 if dtype == "bf16" else 0)
+                                + {"separate": 0, "one_buffer": 20, "no_history": 40}[layout])
+    V, n, L = 32000, 8, (0 if layout == "no_history" else 120)
     p = _knobs(wl, kind)
     base = rng.normal(0.0, 2.0, V).astype(np.float32)
     seen = set()
     for accept in (0, 3, n - 1):
         xs = (base + rng.normal(0.0, 0.6, (n, V))).astype(np.float32)
         hist = rng.integers(0, V, L).astype(np.int32)
-        hist[-20:] = np.argsort(-base)[:20]          # recent ids among the likely ones: penalties matter
+        if L:
+            hist[-20:] = np.argsort(-base)[:20]      # recent ids among the likely ones: penalties matter
         u = rng.random(n)
         # drafts that the loop accepts up to position `accept`, then one it rejects
         xs_eff = xs if dtype == "f32" else wl.bf16_to_f32(wl.to_bf16_bits(xs))
@@ -92,7 +101,7 @@ def test_verify_block_equals_the_sequential_loop(hs, sampler, wl, dtype, kind):
                 h.append(t)
             else:
                 draft.append((t + 1 + i) % V)
-        got = _verify_case(hs, sampler, wl, xs, p, hist, u, draft, dtype)
+        got = _verify_case(hs, sampler, wl, xs, p, hist, u, draft, dtype, one_buffer=layout == "one_buffer")
         if got is not None:
             assert len(got) == accept + 1
             seen.add(accept)
@@ -123,8 +132,9 @@ def test_verify_block_long_block_over_many_lists(hs, sampler, wl):
         t = O.sample_row(xs[i], p, hist=np.asarray(h, np.int32), u=float(u[i])).token
         draft.append(t)
         h.append(t)
-    got = _verify_case(hs, sampler, wl, xs, p, hist, u, draft, "f32")
-    assert got is None or len(got) == n
+    for one_buffer in (False, True):
+        got = _verify_case(hs, sampler, wl, xs, p, hist, u, draft, "f32", one_buffer=one_buffer)
+        assert got is None or len(got) == n
 
 
 def _commit_oracle(x, params, u, host, active, budget, stop):

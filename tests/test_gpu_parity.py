@@ -689,3 +689,24 @@ def test_bias_with_penalties(sampler, wl, kernel_mode, dtype, kmix, signs):
     w = wl.Workload("edge", dtype, xs, plist, rng.random(B), hist, np.full(B, 512, np.int64), None)
     g = run_gpu(sampler, w, bias=bias)
     assert compare_rows(w, g, bias=bias) == B
+
+
+@pytest.mark.parametrize("cfg", [2, 5])
+def test_one_history_shared_by_every_row(sampler, wl, cfg, kernel_mode):
+    """hist_stride 0: every row reads the same history array, row r its first
+    hist_len[r] ids (a drafted block's positions over the sequence's ids and
+    drafts); each row equal to the oracle with that prefix as its history."""
+    import torch
+    w = wl.config(cfg, seed=7, rows=24)
+    rng = np.random.default_rng(cfg)
+    L = w.hist.shape[1]
+    w.hist = np.tile(w.hist[0], (w.hist.shape[0], 1))
+    w.hist_len = rng.integers(0, L + 1, w.hist.shape[0]).astype(np.int64)
+    w.hist_len[:2] = (0, L)
+    x, u, h, m = to_device(w)
+    shared = h[0].contiguous().unsqueeze(0).expand(h.shape[0], L)
+    assert shared.stride(0) == 0
+    out = sampler.run(x, w.params, u, hist=shared, hist_len=w.hist_len, mask=m, want_sets=True, set_cap=2048)
+    torch.cuda.synchronize()
+    g = {k: v.cpu().numpy() for k, v in out.items()}
+    assert compare_rows(w, g) == w.hist.shape[0]

@@ -171,7 +171,10 @@ int build_blob(HostScratch& hs, const ultima_hsamp_batch* b, Built& out) {
             isnan_f(q.frequency_penalty) || isnan_f(q.presence_penalty) ||
             isnan_f(q.temperature) || isnan_f(q.top_p) || isnan_f(q.min_p))
             return ULTIMA_HSAMP_ERR_INVALID;
-        if (q.hist_len < 0 || q.hist_len > b->hist_stride || (q.hist_len > 0 && b->hist == nullptr))
+        // hist_stride 0: one history shared by every row, row r its first
+        // hist_len ids
+        if (q.hist_len < 0 || (b->hist_stride > 0 && q.hist_len > b->hist_stride) ||
+            (q.hist_len > 0 && b->hist == nullptr))
             return ULTIMA_HSAMP_ERR_INVALID;
         if (q.bias_count < 0 || q.bias_count > ULTIMA_HSAMP_MAX_BIAS ||
             (q.bias_count > 0 && (b->bias_ids == nullptr || b->bias_vals == nullptr || q.bias_offset < 0)))

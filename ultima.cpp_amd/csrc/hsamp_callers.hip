@@ -164,7 +164,13 @@ extern "C" int ultima_hsamp_verify_block(ultima_hsamp* h, const ultima_hsamp_ver
     if (stride > INT32_MAX) return ULTIMA_HSAMP_ERR_INVALID;
     hipStream_t stream = static_cast<hipStream_t>(hip_stream);
     int32_t* sampled = v->work + (int64_t)n * stride;
-    if (v->hist_len + n - 1 > 0) {
+    // Drafts that follow the history in memory (or no history): row i's
+    // history is the first hist_len + i ids of that one array, which every
+    // row reads in place (batch hist_stride 0); else the prefix rows are built
+    // in the workspace.
+    const bool in_place = v->hist_len == 0 || n == 1 || v->draft == v->hist + v->hist_len;
+    const int32_t* shared = v->hist_len > 0 ? v->hist : v->draft;   // (NULL when both are empty)
+    if (!in_place) {
         hipLaunchKernelGGL(hsamp::k_verify_prefix, dim3(n), dim3(256), 0, stream, v->hist, (int)v->hist_len, v->draft,
                            v->work, stride);
         if (hipGetLastError() != hipSuccess) return ULTIMA_HSAMP_ERR_HIP;
@@ -178,8 +184,8 @@ extern "C" int ultima_hsamp_verify_block(ultima_hsamp* h, const ultima_hsamp_ver
     b.flags = 0;
     b.logits = v->logits;
     b.logits_stride = v->logits_stride;
-    b.hist = v->work;
-    b.hist_stride = stride;
+    b.hist = in_place ? shared : v->work;
+    b.hist_stride = in_place ? 0 : stride;
     b.mask = v->mask;
     b.mask_stride = v->mask_stride;
     b.u = v->u;

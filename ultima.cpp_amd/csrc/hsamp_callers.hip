@@ -23,7 +23,9 @@
 // have pushed had they been accepted) and its own uniform, all positions in
 // one batch; the block is accepted up to the first position whose sample
 // differs from its draft, and that sample (or, when every draft matches, the
-// last position's) is emitted after them.
+// last position's) is emitted after them. Drafts stored right after the
+// sequence's ids are read in place: every position's history is a prefix of
+// that one array.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>

@@ -43,6 +43,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "sampled rows/sec at B=64,V=151936 fp32; achieved HBM GB/s vs peak"
 PEAK_GBS = 8000.0
 N_SETS = 8
+SPIN_CYCLES = 100_000      # torch.cuda._sleep ahead of each timed region (~50 us at 2 GHz)
 # the kernel that reads the logits, and the per-row kernel after it, by configuration
 STREAM_KERNEL = {1: "k_stream", 2: "k_stream", 3: "k_full", 4: "k_stream", 5: "k_stream"}
 ROW_KERNEL = {1: "k_pick", 2: "k_pick", 3: None, 4: "k_pick", 5: "k_pick_l"}
@@ -160,12 +161,32 @@ def copy_probe(torch, dev, mib, line):
     line["config"]["copy_probe_bytes"] = n * 4
 
 
+_hip_rt = None
+
+
+def graph_upload(torch, g, stream):
+    """hipGraphUpload of a captured graph's executable onto `stream`: its
+    first-launch work (uploading the graph to the device) is paid here, so
+    that the first replay inside a timed region costs what later ones do."""
+    global _hip_rt
+    if _hip_rt is None:
+        _hip_rt = ctypes.CDLL(str(Path(torch.__file__).resolve().parent / "lib" / "libamdhip64.so"))
+        _hip_rt.hipGraphUpload.restype = ctypes.c_int
+        _hip_rt.hipGraphUpload.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    st = _hip_rt.hipGraphUpload(ctypes.c_void_p(g.raw_cuda_graph_exec()), ctypes.c_void_p(stream.cuda_stream))
+    if st != 0:
+        raise RuntimeError(f"hipGraphUpload failed: {st}")
+    stream.synchronize()
+
+
 class Timer:
     """Graphs of one rotation (and of its first r launches) replayed so that
-    exactly n launches run; HIP events on the stream time them."""
+    exactly n launches run; HIP events on the stream time them. Every graph is
+    uploaded to the device when it is captured, before any timing."""
 
-    def __init__(self, torch, stream, launch):
+    def __init__(self, torch, stream, launch, n_sets=None):
         self.torch, self.stream, self.launch = torch, stream, launch
+        self.n_sets = n_sets or N_SETS
         self.graphs = {}
 
     def graph(self, n):
@@ -175,30 +196,38 @@ class Timer:
                 for i in range(n):
                     self.launch(i, self.stream)
             self.stream.synchronize()
+            graph_upload(self.torch, g, self.stream)
             self.graphs[n] = g
         return self.graphs[n]
 
     def run(self, n):
-        full, rem = divmod(n, N_SETS)
+        full, rem = divmod(n, self.n_sets)
         with self.torch.cuda.stream(self.stream):
             for _ in range(full):
-                self.graph(N_SETS).replay()
+                self.graph(self.n_sets).replay()
             if rem:
                 self.graph(rem).replay()
 
     def time(self, n, warmup):
+        """Exactly `warmup` untimed launches, then exactly `n` timed ones:
+        (milliseconds on the stream's events, wall seconds)."""
         torch = self.torch
-        self.graph(N_SETS)
-        if n % N_SETS:
-            self.graph(n % N_SETS)
-        if warmup % N_SETS:
-            self.graph(warmup % N_SETS)
+        self.graph(self.n_sets)
+        if n % self.n_sets:
+            self.graph(n % self.n_sets)
+        if warmup % self.n_sets:
+            self.graph(warmup % self.n_sets)
         self.run(warmup)
         self.stream.synchronize()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         wall0 = time.perf_counter()
         with torch.cuda.stream(self.stream):
+            # A spin kernel ahead of the start event (about 50 us): the host
+            # queues the event and every timed replay behind it, so the events
+            # bracket the GPU's execution of exactly n launches and not the
+            # host's latency in submitting the first replay.
+            torch.cuda._sleep(SPIN_CYCLES)
             e0.record(self.stream)
         self.run(n)
         with torch.cuda.stream(self.stream):
@@ -248,37 +277,16 @@ def head_main(args):
 
     def timed(fn, steps, warmup):
         with torch.cuda.stream(stream):
-            for i in range(n_sets):
+            for i in range(n_sets):                 # uncaptured first run
                 fn(i, stream)
         stream.synchronize()
-        gr = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(gr, stream=stream):
-            for i in range(n_sets):
-                fn(i, stream)
-        stream.synchronize()
-        # The first few milliseconds of a 1.24 GB-per-launch stream run slow
-        # now and then (seen in kernel traces: a burst of launches 1.5x the
-        # steady duration right after the start); at least 40 warm-up
-        # launches, then the median of five timed segments.
-        reps = max(1, steps // (5 * n_sets))
-        for _ in range(max(20, warmup // n_sets)):
-            gr.replay()
-        stream.synchronize()
-        seg = []
-        for _ in range(5):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            with torch.cuda.stream(stream):
-                e0.record(stream)
-                for _ in range(reps):
-                    gr.replay()
-                e1.record(stream)
-            stream.synchronize()
-            seg.append(e0.elapsed_time(e1) / (reps * n_sets))
-        return statistics.median(seg), 5 * reps * n_sets
+        t = Timer(torch, stream, fn, n_sets)
+        ms = t.time(steps, warmup)[0] / steps
+        t.drop()
+        return ms, steps
 
-    steps = min(args.steps, 400)
-    head_ms, n_head = timed(head, steps, args.warmup)
-    step_ms, n_step = timed(step, steps, args.warmup)
+    head_ms, n_head = timed(head, args.steps, args.warmup)
+    step_ms, n_step = timed(step, args.steps, args.warmup)
     algo = V * H * 2 + rows * (2 * H * 4 + V * 4) + H * 4
     achieved = algo / (head_ms * 1e-3) / 1e9
     cpu = None
@@ -392,29 +400,12 @@ def callers_main(args):
         bytes_step = rows * V * 4 + rows * W * 4
         unit, metric = "slot tokens/s", f"multi-slot decode tokens/sec ({rows} slots, V={V} f32, SamplerParams{{}})"
     with torch.cuda.stream(stream):
-        for i in range(n_sets):
+        for i in range(n_sets):                     # uncaptured first run
             step(i, stream)
     stream.synchronize()
-    gr = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(gr, stream=stream):
-        for i in range(n_sets):
-            step(i, stream)
-    stream.synchronize()
-    reps = max(1, args.steps // (5 * n_sets))
-    for _ in range(max(5, args.warmup // n_sets)):
-        gr.replay()
-    stream.synchronize()
-    seg = []
-    for _ in range(5):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        with torch.cuda.stream(stream):
-            e0.record(stream)
-            for _ in range(reps):
-                gr.replay()
-            e1.record(stream)
-        stream.synchronize()
-        seg.append(e0.elapsed_time(e1) / (reps * n_sets))
-    ms = statistics.median(seg)
+    t = Timer(torch, stream, step, n_sets)
+    ms = t.time(args.steps, args.warmup)[0] / args.steps
+    t.drop()
     achieved = bytes_step / (ms * 1e-3) / 1e9
     cpu = None
     if not args.no_cpu:
@@ -453,7 +444,7 @@ def callers_main(args):
         "value": rows / (ms * 1e-3),
         "unit": unit,
         "n_gpus": 1,
-        "steps": 5 * reps * n_sets,
+        "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": ms,
         "higher_is_better": True,

@@ -177,24 +177,8 @@ const char* ultima_hsamp_status_str(int status);
 /* ULTIMA_HSAMP_VERSION of the loaded library. */
 int ultima_hsamp_version(void);
 
-/* Bytes of the fixed device array ultima_hsamp_run_noalloc() takes its scratch
- * from (each GPU the library runs on holds one until the process ends). */
-#define ULTIMA_HSAMP_NOALLOC_SCRATCH_BYTES (96u << 20)
-
-/* No counterpart in the reference: ultima_hsamp_run() for callers that cannot
- * allocate device memory (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc). No handle: it runs on the current device
- * and calls no allocating routine. The kernels' scratch comes from a fixed
- * device array of ULTIMA_HSAMP_NOALLOC_SCRATCH_BYTES per GPU; a batch whose
- * scratch does not fit (about rows x vocab x 8 bytes, e.g. 64 x 151936 fp32
- * rows fit) returns ULTIMA_HSAMP_ERR_CAPACITY. The per-row knobs are copied
- * from host memory into the array with hipMemcpyAsync unless it already holds
- * the same ones (under stream capture nothing is copied: the same batch must
- * have run uncaptured first, else ULTIMA_HSAMP_ERR_UNSUPPORTED). Every call on
- * a GPU shares that GPU's array, which keeps the last call's contents: calls
- * that overlap on one GPU (two streams or threads) race; issue them on one
- * stream. Results are those of ultima_hsamp_run() for the same batch. */
-int ultima_hsamp_run_noalloc(const ultima_hsamp_batch* batch, void* hip_stream);
+/* The allocation-free variant of ultima_hsamp_run, ultima_hsamp_run_noalloc, is
+ * declared in ultima_hsamp_noalloc.h and exported by its own library. */
 
 /* Diagnostics, no counterpart in the reference: a plain read of the batch's
  * logits with the launch shape ultima_hsamp_run() would use for it (same grid,
@@ -241,8 +225,9 @@ int ultima_hsamp_history_push(int32_t* hist, int64_t hist_stride, int32_t* hist_
  *     /root/reference/src/server/http_server.cpp:174-201
  * applied to every slot of a batch at once, after an ultima_hsamp_run over the
  * slots' rows (their device histories: batch.hist, batch.hist_len_dev). For row
- * r: if active[r] == 0 the row has ended, tokens[r] becomes -1 and nothing else
- * changes; else if tokens[r] < 0 or is one of stop_ids[0 .. n_stop) the row ends
+ * r: if active[r] == 0, or budget is not NULL and budget[r] <= 0 (a slot started
+ * with max_tokens 0 emits nothing), the row has ended: tokens[r] becomes -1,
+ * active[r] 0, and nothing else changes; else if tokens[r] < 0 or is one of stop_ids[0 .. n_stop) the row ends
  * (active[r] = 0; the token is not pushed and tokens[r] is left as sampled);
  * else tokens[r] is appended to the row's history as ultima_hsamp_history_push
  * does (same hist_stride / keep rules) and, when budget is not NULL,

@@ -14,6 +14,20 @@ def test_hsamp_exports_every_declared_symbol(pkg):
     assert len(names) >= 9
     for n in names:
         assert hasattr(L, n), f"{n} declared in include/ultima_hsamp.h but not exported"
+    assert "ultima_hsamp_run_noalloc" not in names
+
+
+def test_noalloc_library_exports_its_entry_and_holds_the_array(pkg):
+    """The allocation-free entry is exported by its own library, whose device
+    array (the only one) is not in the main library."""
+    hs = pkg.hsamp
+    L = hs.noalloc_lib()
+    names = sorted(set(hs.declared_symbols(hs.NOALLOC_HEADER)) - set(hs.declared_symbols()))
+    assert names == ["ultima_hsamp_run_noalloc"]
+    for n in names:
+        assert hasattr(L, n)
+    main = hs.lib()
+    assert not hasattr(main, "ultima_hsamp_run_noalloc")
 
 
 def test_version_and_status_strings(pkg):

@@ -141,7 +141,9 @@ def _commit_oracle(x, params, u, host, active, budget, stop):
     """One step of the server loop on every slot: (tokens, margins)."""
     toks, margins = [], []
     for r in range(len(params)):
-        if not active[r]:
+        if not active[r] or (budget is not None and budget[r] <= 0):
+            # an ended slot, or one started with no budget (max_tokens 0), emits nothing
+            active[r] = False
             toks.append(-1)
             margins.append(1.0)
             continue
@@ -166,7 +168,7 @@ def test_decode_commit_runs_the_server_loop_on_many_slots(hs, sampler, wl, captu
     decided); else ultima_hsamp_run then ultima_hsamp_decode_commit."""
     import torch
     dev = torch.device("cuda:0")
-    B, V, W = 6, 4096, 64
+    B, V, W = 7, 4096, 64
     stride, keep = 2 * W, W
     eos, im_end = 7, 11
     stop = (eos, im_end)
@@ -185,7 +187,7 @@ def test_decode_commit_runs_the_server_loop_on_many_slots(hs, sampler, wl, captu
 
     # (the server's knobs with DRY looking back 48 ids: every window within W,
     # as the device-history plan requires)
-    params = [_knobs(wl, k) for k in ("penalties", "server", "plain", "penalties", "server", "plain")]
+    params = [_knobs(wl, k) for k in ("penalties", "server", "plain", "penalties", "server", "plain", "plain")]
     for r in (1, 4):
         params[r]["dry_last_n"] = 48
     base = rng.normal(0.0, 2.0, (B, V)).astype(np.float32)
@@ -195,7 +197,7 @@ def test_decode_commit_runs_the_server_loop_on_many_slots(hs, sampler, wl, captu
     hist = torch.zeros((B, stride), dtype=torch.int32, device=dev)
     lens = torch.zeros(B, dtype=torch.int32, device=dev)
     active = torch.ones(B, dtype=torch.int32, device=dev)
-    budget_h = [200, 200, 9, 200, 200, 200]
+    budget_h = [200, 200, 9, 200, 200, 200, 0]          # slot 6: max_tokens 0
     budget = torch.tensor(budget_h, dtype=torch.int32, device=dev)
     host = [[] for _ in range(B)]
     act_h = [True] * B
@@ -245,6 +247,7 @@ def test_decode_commit_runs_the_server_loop_on_many_slots(hs, sampler, wl, captu
                 pytest.skip("a draw within 1e-6 of a CDF boundary; the slots' paths part")
         np.testing.assert_array_equal(active.cpu().numpy().astype(bool), act_h, err_msg=f"step {step}")
     assert not act_h[2] and len(host[2]) == 9            # budget spent
+    assert not act_h[6] and len(host[6]) == 0            # no budget: nothing emitted
     assert not act_h[1] and not act_h[4]                 # stopped on eos / im_end
     got_len = lens.cpu().numpy()
     got_hist = hist.cpu().numpy()

@@ -1,6 +1,7 @@
 """Build the native libraries of the package in-tree.
 
     libultima_hsamp.so   -- HIP kernels for gfx950 + the C ABI (include/ultima_hsamp.h)
+    libultima_hsamp_noalloc.so -- the allocation-free entry (include/ultima_hsamp_noalloc.h)
     libultima_sampler.so -- the ultima::sampler C++ drop-in (include/ultima/sampler/sampler.hpp)
     dropin_driver        -- tests/cpp/dropin_driver.cpp linked against the drop-in
     tests/cpp/libdevice_expf.so -- test kit evaluating the device expf
@@ -25,6 +26,7 @@ INC = ROOT / "include"
 BUILD = PKG / "_build"
 
 HSAMP_SO = PKG / "libultima_hsamp.so"
+NOALLOC_SO = PKG / "libultima_hsamp_noalloc.so"
 SAMPLER_SO = PKG / "libultima_sampler.so"
 CPP_TEST = PKG / "dropin_driver"
 
@@ -61,18 +63,20 @@ def build_all() -> None:
     objs = {
         "hsamp_kernels.o": CSRC / "hsamp_kernels.hip",
         "hsamp_api.o": CSRC / "hsamp_api.cpp",
-        "hsamp_noalloc.o": CSRC / "hsamp_noalloc.hip",
         "hsamp_head.o": CSRC / "hsamp_head.hip",
         "hsamp_history.o": CSRC / "hsamp_history.hip",
         "hsamp_callers.o": CSRC / "hsamp_callers.hip",
     }
     with ThreadPoolExecutor(max_workers=4) as ex:
         futs = [ex.submit(_run, [HIPCC, *HIP_FLAGS, "-x", "hip", "-c", str(src), "-o", str(BUILD / o)])
-                for o, src in objs.items()]
+                for o, src in [*objs.items(), ("hsamp_noalloc.o", CSRC / "hsamp_noalloc.hip")]]
         for f in futs:
             f.result()
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-fno-gpu-rdc",
           *[str(BUILD / o) for o in objs], "-o", str(HSAMP_SO)])
+    # its device array is held only by processes that load this library
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-fno-gpu-rdc", str(BUILD / "hsamp_noalloc.o"),
+          "-o", str(NOALLOC_SO), f"-L{PKG}", "-lultima_hsamp", "-Wl,-rpath,$ORIGIN"])
     # The C++ drop-in: host code only, reference-compatible flags.
     cxx = ["g++", "-std=c++20", "-O2", "-fPIC", "-fno-rtti", "-fno-exceptions", "-Wall", "-Wextra",
            f"-I{INC}"]

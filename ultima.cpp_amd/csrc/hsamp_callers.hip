@@ -59,6 +59,15 @@ __global__ __launch_bounds__(64) void k_decode_commit(int32_t* __restrict__ hist
         if (threadIdx.x == 0) tokens[r] = -1;
         return;
     }
+    // a slot whose budget is spent emits nothing (max_tokens 0: the reference's
+    // loop body never runs)
+    if (budget != nullptr && bud <= 0) {
+        if (threadIdx.x == 0) {
+            tokens[r] = -1;
+            active[r] = 0;
+        }
+        return;
+    }
     bool end = tok < 0;
     for (int i = 0; i < n_stop; ++i) end = end || tok == stop.id[i];
     if (end) {

@@ -608,8 +608,11 @@ __device__ __forceinline__ void emit_token(const StreamArgs& a, int r, int32_t t
         a.token[r] = tok;
         return;
     }
-    if (a.c_active[r] == 0) {
+    // an ended slot, or one whose budget is spent (max_tokens 0: the
+    // reference's loop body never runs), emits nothing
+    if (a.c_active[r] == 0 || (a.c_budget != nullptr && a.c_budget[r] <= 0)) {
         a.token[r] = -1;
+        a.c_active[r] = 0;
         return;
     }
     a.token[r] = tok;

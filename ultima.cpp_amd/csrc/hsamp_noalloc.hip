@@ -1,6 +1,8 @@
 // ultima_hsamp_run_noalloc: ultima_hsamp_run without a handle and without any
 // allocation, for callers that cannot allocate device memory (code under HIP
-// graph capture, tight serving loops, harnesses that forbid hipMalloc).
+// graph capture, tight serving loops, harnesses that forbid hipMalloc). It is
+// built into its own library (libultima_hsamp_noalloc.so), so that only the
+// processes that load it hold its device array.
 //
 // The kernels' scratch (candidate lists, per-slice counts, overflow buffers,
 // penalty tables, full-vocabulary buffers and the uploaded per-row plans) is
@@ -10,9 +12,15 @@
 // device is read with hipGetSymbolAddress and kept per device; every later
 // use goes through that address.
 //
+// The array's front (kPlanBytes) holds the per-row plans. Plans a graph was
+// captured with stay where they are for the rest of the process (pinned), so
+// a later call with other knobs cannot change what the graph's replays read;
+// uncaptured calls with new knobs copy theirs just past the pinned ones.
+//
 // Every call on one GPU shares that GPU's array and it keeps the last call's
 // contents. Calls that overlap on one GPU (two streams, two threads) race on
-// it: the caller serialises them, e.g. by issuing them on one stream.
+// it: the caller serialises them, e.g. by issuing them on one stream. A
+// captured graph's replays are such calls too.
 #include <hip/hip_runtime.h>
 
 #include <cstring>
@@ -20,22 +28,32 @@
 #include <vector>
 
 #include "hsamp_run.h"
-#include "ultima_hsamp.h"
+#include "ultima_hsamp_noalloc.h"
 
 namespace {
 
 using namespace hsamp;
 
 constexpr size_t kScratchBytes = ULTIMA_HSAMP_NOALLOC_SCRATCH_BYTES;
+constexpr size_t kPlanBytes = ULTIMA_HSAMP_NOALLOC_PLAN_BYTES;   // the plans' region at the front
 constexpr int kMaxDevices = 64;
 
 __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+// A plan blob resident in the plans' region: its offset and a host copy.
+struct Resident {
+    size_t off = 0;
+    std::vector<char> bytes;
+};
 
 struct DeviceState {
     bool ready = false;
     unsigned char* ptr = nullptr;   // this device's address of `scratch`
     DevCaps caps;
-    std::vector<char> resident;     // the plan blob the array holds (host copy)
+    std::vector<Resident> pinned;   // blobs captured graphs read: never moved or overwritten
+    size_t pinned_end = 0;          // first free byte of the plans' region after them
+    bool floating = false;          // `last` holds the blob of the last uncaptured call
+    Resident last;                  // at pinned_end
 };
 
 std::mutex g_mu;
@@ -67,6 +85,43 @@ int setup(int dev, DeviceState*& out) {
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+bool same_bytes(const std::vector<char>& a, const std::vector<char>& b) {
+    return a.size() == b.size() && std::memcmp(a.data(), b.data(), a.size()) == 0;
+}
+
+// Where this call's plans are: a pinned blob with the same bytes, the last
+// uncaptured call's blob (pinned now if this call is captured), or, outside
+// capture, a copy queued just past the pinned blobs.
+int place_plans(DeviceState& d, const std::vector<char>& blob, bool capturing, hipStream_t stream, size_t& off) {
+    for (const Resident& r : d.pinned) {
+        if (same_bytes(r.bytes, blob)) {
+            off = r.off;
+            return ULTIMA_HSAMP_OK;
+        }
+    }
+    if (d.floating && same_bytes(d.last.bytes, blob)) {
+        off = d.last.off;
+        if (capturing) {
+            d.pinned.push_back(d.last);
+            d.pinned_end = align256(d.last.off + d.last.bytes.size());
+            d.floating = false;
+            d.last = Resident{};
+        }
+        return ULTIMA_HSAMP_OK;
+    }
+    // under capture nothing is copied: the same batch must have run first
+    if (capturing) return ULTIMA_HSAMP_ERR_UNSUPPORTED;
+    if (d.pinned_end + blob.size() > kPlanBytes) return ULTIMA_HSAMP_ERR_CAPACITY;
+    d.floating = false;   // nothing known to be resident until the copy is queued
+    const hipError_t ce = hipMemcpyAsync(d.ptr + d.pinned_end, blob.data(), blob.size(), hipMemcpyHostToDevice, stream);
+    if (ce != hipSuccess) return hip_fail(ce, "hipMemcpyAsync(plans -> scratch)", __LINE__);
+    d.last.off = d.pinned_end;
+    d.last.bytes = blob;
+    d.floating = true;
+    off = d.last.off;
+    return ULTIMA_HSAMP_OK;
+}
+
 }  // namespace
 
 extern "C" int ultima_hsamp_run_noalloc(const ultima_hsamp_batch* b, void* hip_stream) {
@@ -88,17 +143,15 @@ extern "C" int ultima_hsamp_run_noalloc(const ultima_hsamp_batch* b, void* hip_s
     st = plan_run(d->caps, b, bl, rp);
     if (st != ULTIMA_HSAMP_OK) return st;
 
-    // The array's layout for this run: [plans blob][slice counts + bounds]
+    // The array's layout for this run: [plans' region][slice counts + bounds]
     // [candidate lists][overflow][penalty tables][fullv][fullp][fullk][kept ids][kept counts]
-    size_t off = 0;
+    size_t off = kPlanBytes;
     auto take = [&](size_t bytes) -> unsigned char* {
         unsigned char* p = d->ptr + off;
         off = align256(off + bytes);
         return p;
     };
     RunBuffers buf;
-    unsigned char* blob = take(bl.total);
-    buf.blob = reinterpret_cast<const char*>(blob);
     buf.cand_slots = rp.cand_slots;
     buf.cand_n = reinterpret_cast<int32_t*>(take(rp.cand_slots * 8));
     buf.cand = reinterpret_cast<unsigned long long*>(take(rp.cand_elems * 8));
@@ -115,19 +168,11 @@ extern "C" int ultima_hsamp_run_noalloc(const ultima_hsamp_batch* b, void* hip_s
     }
     if (off > kScratchBytes) return ULTIMA_HSAMP_ERR_CAPACITY;
 
-    // The per-row plans go to the front of the array unless it already holds
-    // the same bytes (a caller that keeps its knobs uploads them once). Under
-    // stream capture nothing is copied: the same batch must have run first.
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(stream, &cap) != hipSuccess) return hip_fail(hipErrorUnknown, "hipStreamIsCapturing", __LINE__);
-    const bool same = d->resident.size() == hs.blob.size() &&
-                      std::memcmp(d->resident.data(), hs.blob.data(), hs.blob.size()) == 0;
-    if (!same) {
-        if (cap != hipStreamCaptureStatusNone) return ULTIMA_HSAMP_ERR_UNSUPPORTED;
-        d->resident.clear();   // nothing known to be resident until the copy is queued
-        const hipError_t ce = hipMemcpyAsync(blob, hs.blob.data(), hs.blob.size(), hipMemcpyHostToDevice, stream);
-        if (ce != hipSuccess) return hip_fail(ce, "hipMemcpyAsync(plans -> scratch)", __LINE__);
-        d->resident = hs.blob;
-    }
+    size_t plan_off = 0;
+    st = place_plans(*d, hs.blob, cap != hipStreamCaptureStatusNone, stream, plan_off);
+    if (st != ULTIMA_HSAMP_OK) return st;
+    buf.blob = reinterpret_cast<const char*>(d->ptr + plan_off);
     return launch_run(rp, bl, b, buf, stream, nullptr);
 }

@@ -13,12 +13,14 @@ import numpy as np
 
 PKG = Path(__file__).resolve().parent
 LIB_PATH = PKG / "libultima_hsamp.so"
+NOALLOC_LIB_PATH = PKG / "libultima_hsamp_noalloc.so"
 HEADER = PKG.parent / "include" / "ultima_hsamp.h"
+NOALLOC_HEADER = PKG.parent / "include" / "ultima_hsamp_noalloc.h"
 
 OK, ERR_INVALID, ERR_HIP, ERR_UNSUPPORTED, ERR_NOMEM, ERR_CAPACITY, ERR_NO_DEVICE = 0, -1, -2, -3, -4, -5, -6
 F32, BF16 = 0, 1
 WRITEBACK, STREAM_ONLY = 1, 0x100
-NOALLOC_SCRATCH_BYTES = 96 << 20
+NOALLOC_SCRATCH_BYTES, NOALLOC_PLAN_BYTES = 96 << 20, 2 << 20
 ROW_GREEDY, ROW_U_USED, ROW_CDF_NEAR, ROW_NAN, ROW_UNIFORM, ROW_TOPP_NEAR, ROW_REREAD = 1, 2, 4, 8, 16, 32, 64
 
 PARAM_KEYS = ("rep_penalty", "dry_multiplier", "dry_base", "frequency_penalty", "presence_penalty",
@@ -131,10 +133,10 @@ class Verify(ctypes.Structure):
     ]
 
 
-def declared_symbols() -> list[str]:
-    """Function names declared in include/ultima_hsamp.h."""
+def declared_symbols(header: Path = HEADER) -> list[str]:
+    """Function names declared in a header (default include/ultima_hsamp.h)."""
     import re
-    text = HEADER.read_text()
+    text = header.read_text()
     return sorted(set(re.findall(r"\b(ultima_hsamp_[a-z_0-9]+)\s*\(", text)))
 
 
@@ -174,8 +176,6 @@ def lib() -> ctypes.CDLL:
         L.ultima_hsamp_status_str.argtypes = [ctypes.c_int]
         L.ultima_hsamp_version.restype = ctypes.c_int
         L.ultima_hsamp_version.argtypes = []
-        L.ultima_hsamp_run_noalloc.restype = ctypes.c_int
-        L.ultima_hsamp_run_noalloc.argtypes = [ctypes.POINTER(Batch), vp]
         L.ultima_hsamp_read_probe.restype = ctypes.c_int
         L.ultima_hsamp_read_probe.argtypes = [vp, ctypes.POINTER(Batch), vp, vp]
         L.ultima_hsamp_set_phase_event.restype = ctypes.c_int
@@ -285,13 +285,31 @@ def _batch(logits, params, u, hist, hist_len, mask, bias, writeback, want_sets, 
     return b, out, (parr, bids, bvals), s
 
 
+_noalloc_lib = None
+
+
+def noalloc_lib() -> ctypes.CDLL:
+    """Load libultima_hsamp_noalloc.so (include/ultima_hsamp_noalloc.h); it
+    links libultima_hsamp.so, loaded first."""
+    global _noalloc_lib
+    if _noalloc_lib is None:
+        lib()
+        if not NOALLOC_LIB_PATH.exists():
+            raise RuntimeError(f"{NOALLOC_LIB_PATH} is not built: run __graft_entry__.build()")
+        L = ctypes.CDLL(str(NOALLOC_LIB_PATH))
+        L.ultima_hsamp_run_noalloc.restype = ctypes.c_int
+        L.ultima_hsamp_run_noalloc.argtypes = [ctypes.POINTER(Batch), ctypes.c_void_p]
+        _noalloc_lib = L
+    return _noalloc_lib
+
+
 def run_noalloc(logits, params, u, hist=None, hist_len=None, mask=None, bias=None, writeback=False,
                 want_sets=False, set_cap=None, stream=None, outputs=None):
     """ultima_hsamp_run_noalloc on the current device: Sampler.run without a
     handle, scratch from the library's fixed device array."""
     b, out, keep, s = _batch(logits, params, u, hist, hist_len, mask, bias, writeback, want_sets, set_cap,
                              stream, outputs, False)
-    check(lib().ultima_hsamp_run_noalloc(ctypes.byref(b), ctypes.c_void_p(s.cuda_stream)), "run_noalloc")
+    check(noalloc_lib().ultima_hsamp_run_noalloc(ctypes.byref(b), ctypes.c_void_p(s.cuda_stream)), "run_noalloc")
     del keep
     return out
 

@@ -321,8 +321,14 @@ def head_lib():
         L.orc_matvec_f32.argtypes = [vp, vp, vp, i64, i64]
         L.orc_matvec_bf16.restype = None
         L.orc_matvec_bf16.argtypes = [vp, vp, vp, i64, i64]
+        L.orc_matvec.restype = None
+        L.orc_matvec.argtypes = [vp, i32, vp, vp, i64, i64]
+        L.orc_hadamard_fold.restype = None
+        L.orc_hadamard_fold.argtypes = [vp, vp, i64, i64, vp]
+        L.orc_head_row_bytes.restype = i64
+        L.orc_head_row_bytes.argtypes = [i32, i64]
         L.orc_lm_head.restype = None
-        L.orc_lm_head.argtypes = [vp, i64, i64, vp, f32, vp, i32, i64, f32, vp, vp]
+        L.orc_lm_head.argtypes = [vp, i64, i64, vp, f32, vp, i32, i64, f32, vp, vp, i64, vp]
         _head = L
     return _head
 
@@ -346,6 +352,10 @@ def ref_kernels():
         R.ref_matvec_f32.argtypes = [vp, vp, vp, i64, i64]
         R.ref_matvec_bf16.restype = None
         R.ref_matvec_bf16.argtypes = [vp, vp, vp, i64, i64]
+        R.ref_matvec_q.restype = None
+        R.ref_matvec_q.argtypes = [ctypes.c_int, vp, vp, vp, i64, i64]
+        R.ref_hadamard_fold.restype = None
+        R.ref_hadamard_fold.argtypes = [vp, vp, i64, i64, vp]
         _refk = R
     return _refk
 
@@ -361,11 +371,31 @@ def rmsnorm(x, scale, eps: float, use_ref: bool = False) -> np.ndarray:
     return y
 
 
-def matvec(w, x, use_ref: bool = False) -> np.ndarray:
-    """y = W x in the reference's order; W f32 [M, K] or bf16 bits (uint16) [M, K]."""
+# head weight types (head_oracle.c's orc_matvec numbering)
+HEAD_F32, HEAD_BF16, HEAD_Q4_K, HEAD_Q5_K, HEAD_Q6_K, HEAD_Q8_0, HEAD_Q4_1, HEAD_Q5_0, HEAD_PQ2_0 = range(9)
+HEAD_NAMES = {"f32": HEAD_F32, "bf16": HEAD_BF16, "q4k": HEAD_Q4_K, "q5k": HEAD_Q5_K, "q6k": HEAD_Q6_K,
+              "q8_0": HEAD_Q8_0, "q4_1": HEAD_Q4_1, "q5_0": HEAD_Q5_0, "pq2_0": HEAD_PQ2_0}
+
+
+def head_row_bytes(dtype: int, H: int) -> int:
+    """Bytes of one head row of H values (0 when H does not split into blocks)."""
+    return int(head_lib().orc_head_row_bytes(dtype, H))
+
+
+def matvec(w, x, use_ref: bool = False, dtype: int | None = None) -> np.ndarray:
+    """y = W x in the reference's order; W f32 [M, K], bf16 bits (uint16) [M, K],
+    or a quantised head (uint8 [M, row_bytes], `dtype` one of HEAD_Q*), K = x.size."""
     x = _f32(x)
-    M, K = w.shape
+    K = x.size
+    M = w.shape[0]
     y = np.empty(M, np.float32)
+    if dtype is not None and dtype >= HEAD_Q4_K:
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        if use_ref:
+            ref_kernels().ref_matvec_q(dtype, _ptr(w), _ptr(x), _ptr(y), M, K)
+        else:
+            head_lib().orc_matvec(_ptr(w), dtype, _ptr(x), _ptr(y), M, K)
+        return y
     if w.dtype == np.uint16:
         w = np.ascontiguousarray(w)
         fn = ref_kernels().ref_matvec_bf16 if use_ref else head_lib().orc_matvec_bf16
@@ -376,16 +406,34 @@ def matvec(w, x, use_ref: bool = False) -> np.ndarray:
     return y
 
 
-def lm_head(hidden, norm_scale, eps: float, weight, logit_scale: float = 1.0):
+def hadamard_fold(x, block: int, signs=None, use_ref: bool = False) -> np.ndarray:
+    """The reference's hadamard_fold_f32 of one row (src/kernels/hadamard.cpp:26-44)."""
+    x = _f32(x)
+    y = np.empty_like(x)
+    sg = None if signs is None else _f32(signs)
+    fn = ref_kernels().ref_hadamard_fold if use_ref else head_lib().orc_hadamard_fold
+    fn(_ptr(x), _ptr(y), x.size, block, None if sg is None else _ptr(sg))
+    return y
+
+
+def lm_head(hidden, norm_scale, eps: float, weight, logit_scale: float = 1.0, dtype: int | None = None,
+            fold_block: int = 0, fold_signs=None):
     """Logits [rows, V] of hidden states [rows, H] (reference
-    src/model/qwen_model.cpp:182-207); also returns the normed rows."""
+    src/model/qwen_model.cpp:182-207); also returns the head's input rows (the
+    normed rows, folded when fold_block > 0). `dtype`: a HEAD_* type; by default
+    f32 or bf16 from the weight array's element type."""
     hidden = _f32(np.atleast_2d(hidden))
     rows, H = hidden.shape
     V = weight.shape[0]
-    dtype = 1 if weight.dtype == np.uint16 else 0
-    w = np.ascontiguousarray(weight) if dtype else _f32(weight)
+    if dtype is None:
+        dtype = HEAD_BF16 if weight.dtype == np.uint16 else HEAD_F32
+    if dtype == HEAD_F32:
+        w = _f32(weight)
+    else:
+        w = np.ascontiguousarray(weight)
+    sg = None if fold_signs is None else _f32(fold_signs)
     logits = np.empty((rows, V), np.float32)
     normed = np.empty((rows, H), np.float32)
     head_lib().orc_lm_head(_ptr(hidden), rows, H, _ptr(_f32(norm_scale)), eps, _ptr(w), dtype, V,
-                           logit_scale, _ptr(logits), _ptr(normed))
+                           logit_scale, _ptr(logits), _ptr(normed), fold_block, None if sg is None else _ptr(sg))
     return logits, normed

@@ -196,3 +196,43 @@ def mask_from_allowed(allowed: np.ndarray) -> np.ndarray:
     for b in range(32):
         w |= bits[:, :, b] << np.uint64(b)
     return w.astype(np.uint32)
+
+
+# ---- quantised lm-head weights (GGUF block layouts) -------------------------------
+
+# weight type -> (values per block, bytes per block, byte offsets of the block's
+# fp16 scale fields); the type numbers are include/ultima_hsamp.h's
+# ULTIMA_HSAMP_HEAD_* values
+QUANT_BLOCKS = {
+    2: (256, 144, (0, 2)),    # Q4_K: d, dmin, 12 B scales/mins, 128 B nibbles
+    3: (256, 176, (0, 2)),    # Q5_K: d, dmin, 12 B scales/mins, 32 B fifth bits, 128 B nibbles
+    4: (256, 210, (208,)),    # Q6_K: 128 B low nibbles, 64 B high bits, 16 int8 scales, d
+    5: (32, 34, (0,)),        # Q8_0: d, 32 int8
+    6: (32, 20, (0, 2)),      # Q4_1: d, m, 16 B nibbles
+    7: (32, 22, (0,)),        # Q5_0: d, 32 fifth bits, 16 B nibbles
+    8: (128, 34, (0,)),       # PQ2_0: d, 32 B of 2-bit codes
+}
+
+
+def quant_row_bytes(dtype: int, H: int) -> int:
+    be, bb, _ = QUANT_BLOCKS[dtype]
+    if H % be:
+        raise ValueError(f"H={H} is not a multiple of the type's {be}-value blocks")
+    return H // be * bb
+
+
+def quant_head(dtype: int, V: int, H: int, seed: int, scale: float = 0.02) -> np.ndarray:
+    """Random [V, row_bytes] uint8 head of a quantised type: uniform random
+    quant bytes, the fp16 scale fields finite values ~ U(0, scale) (the second
+    field, a min, ~ U(0, scale / 4))."""
+    be, bb, fields = QUANT_BLOCKS[dtype]
+    rb = quant_row_bytes(dtype, H)
+    nb = V * (H // be)
+    u = splitmix64(seed, (nb * bb + 7) // 8)
+    w = u.view(np.uint8)[: nb * bb].reshape(nb, bb).copy()
+    for i, off in enumerate(fields):
+        v = uniform53(seed + 101 + i, nb) * (scale if i == 0 else scale / 4)
+        h = v.astype(np.float16).view(np.uint16)
+        w[:, off] = (h & 0xFF).astype(np.uint8)
+        w[:, off + 1] = (h >> 8).astype(np.uint8)
+    return w.reshape(V, rb)

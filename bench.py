@@ -70,6 +70,11 @@ def parse():
     ap.add_argument("--slots", type=int, default=64, help="decode workload: slots per step")
     ap.add_argument("--head-rows", type=int, default=1, help="head workload: hidden-state rows per step")
     ap.add_argument("--head-hidden", type=int, default=4096, help="head workload: hidden size H")
+    ap.add_argument("--head-dtype", default="bf16",
+                    choices=["f32", "bf16", "q4k", "q5k", "q6k", "q8_0", "q4_1", "q5_0", "pq2_0"],
+                    help="head workload: the head's weight type (GGUF block layouts for the quantised ones)")
+    ap.add_argument("--head-fold", type=int, default=0,
+                    help="head workload: Hadamard fold block (0: the head is not folded)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-reps", type=int, default=7, help="timed repetitions of each CPU leg (median)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -240,28 +245,54 @@ class Timer:
         self.graphs.clear()
 
 
+HEAD_KERNEL = {"f32": "k_head_gemv", "bf16": "k_head_gemv"}   # else k_head_q
+
+
 def head_main(args):
-    """The logits producer: rows hidden states [rows, H] -> rmsnorm -> lm-head
-    matvec with a bf16 [V, H] head (V = 151936, random weights) -> logits
-    [rows, V] in device memory, then the same step followed by sampling
-    (configuration 1's knobs). One JSON line; the roofline is the producer's
-    (HBM-bound: the head's weights once per step)."""
+    """The logits producer: rows hidden states [rows, H] -> rmsnorm (-> the
+    Hadamard fold) -> lm-head matvec with a [V, H] head of --head-dtype
+    (V = 151936, random weights) -> logits [rows, V] in device memory, then the
+    same step followed by sampling (configuration 1's knobs). One JSON line;
+    the roofline is the producer's (HBM-bound: the head's weights once per
+    step)."""
     import torch
     import __graft_entry__ as ge
     pkg = ge.load_package()
     hs = pkg.hsamp
+    wlm = pkg.workloads
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     rows, H, V = args.head_rows, args.head_hidden, 151936
+    dname = args.head_dtype
+    dtype = {"f32": hs.F32, "bf16": hs.BF16, "q4k": hs.HEAD_Q4_K, "q5k": hs.HEAD_Q5_K, "q6k": hs.HEAD_Q6_K,
+             "q8_0": hs.HEAD_Q8_0, "q4_1": hs.HEAD_Q4_1, "q5_0": hs.HEAD_Q5_0, "pq2_0": hs.HEAD_PQ2_0}[dname]
     g = torch.Generator(device=dev).manual_seed(5)
-    n_sets = 2                                      # two heads of 1.24 GB: no cache reuse between steps
-    heads = [(torch.randn((V, H), generator=g, device=dev) * 0.02).to(torch.bfloat16) for _ in range(n_sets)]
+    n_sets = 2                                      # two heads, each far above the caches: no reuse between steps
+
+    def make_head():
+        if dtype == hs.F32:
+            return torch.randn((V, H), generator=g, device=dev) * 0.02
+        if dtype == hs.BF16:
+            return (torch.randn((V, H), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        be, bb, fields = wlm.QUANT_BLOCKS[dtype]
+        w = torch.randint(0, 256, (V * (H // be), bb), generator=g, device=dev, dtype=torch.uint8)
+        for k, off in enumerate(fields):
+            sc = (torch.rand(w.shape[0], generator=g, device=dev) * (0.02 if k == 0 else 0.005)).half()
+            b16 = sc.view(torch.int16).to(torch.int32)
+            w[:, off] = (b16 & 0xFF).to(torch.uint8)
+            w[:, off + 1] = ((b16 >> 8) & 0xFF).to(torch.uint8)
+        return w.view(V, -1)
+
+    heads = [make_head() for _ in range(n_sets)]
+    head_bytes = heads[0].numel() * heads[0].element_size()
     hidden = [torch.randn((rows, H), generator=g, device=dev) * 2.0 for _ in range(n_sets)]
     scale = torch.ones(H, device=dev) + 0.1 * torch.randn(H, generator=g, device=dev)
+    fold = args.head_fold
+    signs = (torch.randint(0, 2, (H,), generator=g, device=dev) * 2 - 1).float() if fold else None
     logits = torch.empty((rows, V), dtype=torch.float32, device=dev)
     normed = torch.empty((rows, H), dtype=torch.float32, device=dev)
     sampler = hs.Sampler(0, max_rows=max(rows, 64), max_vocab=V)
-    params = [dict(pkg.workloads.identity_params(temperature=0.8, top_k=40, top_p=0.95, rep_penalty=1.0))
+    params = [dict(wlm.identity_params(temperature=0.8, top_k=40, top_p=0.95, rep_penalty=1.0))
               for _ in range(rows)]
     u = torch.full((rows,), 0.37, dtype=torch.float64, device=dev)
     outs = {"token": torch.empty(rows, dtype=torch.int32, device=dev),
@@ -269,7 +300,8 @@ def head_main(args):
     stream = torch.cuda.Stream(dev)
 
     def head(i, s):
-        hs.lm_head(hidden[i % n_sets], scale, 1e-6, heads[i % n_sets], 1.0, logits, normed, stream=s)
+        hs.lm_head(hidden[i % n_sets], scale, 1e-6, heads[i % n_sets], 1.0, logits, normed, stream=s,
+                   weight_dtype=dtype, fold_block=fold, fold_signs=signs)
 
     def step(i, s):
         head(i, s)
@@ -287,7 +319,7 @@ def head_main(args):
 
     head_ms, n_head = timed(head, args.steps, args.warmup)
     step_ms, n_step = timed(step, args.steps, args.warmup)
-    algo = V * H * 2 + rows * (2 * H * 4 + V * 4) + H * 4
+    algo = head_bytes + rows * (2 * H * 4 + V * 4) + H * 4
     achieved = algo / (head_ms * 1e-3) / 1e9
     cpu = None
     if not args.no_cpu:
@@ -296,12 +328,17 @@ def head_main(args):
         from concurrent.futures import ThreadPoolExecutor
         kind = "reference" if O.ref_kernels_available() else "port"
         threads = host_threads()
-        wcpu = heads[0][:V].view(torch.int16).cpu().numpy().view(np.uint16)
+        w0 = heads[0]
+        if dtype == hs.BF16:
+            wcpu = w0.view(torch.int16).cpu().numpy().view(np.uint16)
+        else:
+            wcpu = w0.cpu().numpy()
         x = O.rmsnorm(hidden[0][0].cpu().numpy(), scale.cpu().numpy(), 1e-6, use_ref=kind == "reference")
         bounds = np.linspace(0, V, threads + 1).astype(int)
+        qd = dtype if dtype >= hs.HEAD_Q4_K else None
 
         def part(j):
-            return O.matvec(wcpu[bounds[j]:bounds[j + 1]], x, use_ref=kind == "reference")
+            return O.matvec(wcpu[bounds[j]:bounds[j + 1]], x, use_ref=kind == "reference", dtype=qd)
 
         with ThreadPoolExecutor(threads) as ex:
             list(ex.map(part, range(threads)))                      # warm-up
@@ -312,12 +349,15 @@ def head_main(args):
                 ts.append(time.perf_counter() - t0)
         sec = statistics.median(ts)
         cpu = {"value": 1.0 / sec, "unit": "logit rows/s", "cores": threads, "kind": kind,
-               "sample": f"one row of the {V}x{H} bf16 head (the matvec; rmsnorm excluded), rows split "
+               "sample": f"one row of the {V}x{H} {dname} head (the matvec; rmsnorm excluded), rows split "
                          f"over {threads} threads, median of {len(ts)}"}
     sampler.close()
-    traffic, traffic_src = traffic_from_profiles("k_head_gemv", "head")
+    kernel = HEAD_KERNEL.get(dname, "k_head_q")
+    tag = "head" if dname == "bf16" and not fold else f"head_{dname}"
+    traffic, traffic_src = traffic_from_profiles(kernel, tag)
     line = {
-        "metric": f"logit rows/sec of the final rmsnorm + lm-head (H={H}, V={V} bf16 head); achieved HBM GB/s vs peak",
+        "metric": f"logit rows/sec of the final rmsnorm + lm-head (H={H}, V={V} {dname} head); "
+                  "achieved HBM GB/s vs peak",
         "value": rows / (head_ms * 1e-3),
         "unit": "rows/s",
         "n_gpus": 1,
@@ -327,15 +367,17 @@ def head_main(args):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16 weights, f32 arithmetic",
-        "data": "synthetic (random head weights and hidden states, 2 rotating heads of 1.24 GB)",
-        "config": {"workload": f"head: rows={rows} H={H} V={V} bf16, then configuration-1 sampling",
-                   "rows": rows, "hidden": H, "vocab": V, "bytes_per_step": algo,
+        "dtype": f"{dname} weights, f32 arithmetic",
+        "data": f"synthetic (random head weights and hidden states, 2 rotating heads of {head_bytes / 1e9:.2f} GB)",
+        "config": {"workload": f"head: rows={rows} H={H} V={V} {dname}" + (f" fold {fold}" if fold else "") +
+                               ", then configuration-1 sampling",
+                   "rows": rows, "hidden": H, "vocab": V, "head_dtype": dname, "fold_block": fold,
+                   "bytes_per_step": algo,
                    "head_and_sample_us": round(step_ms * 1e3, 3), "head_and_sample_steps": n_step,
                    "kernel_us": {"lm_head": round(head_ms * 1e3, 3)}},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_GBS, "traffic": traffic, "traffic_source": traffic_src,
-                     "kernel": "k_head_gemv", "algorithmic_bytes_per_launch": algo},
+                     "kernel": kernel, "algorithmic_bytes_per_launch": algo},
         "cpu_baseline": cpu,
     }
     if args.copy_probe_mib > 0:

@@ -302,34 +302,60 @@ int ultima_hsamp_verify_block(ultima_hsamp* h, const ultima_hsamp_verify* v, voi
 
 /* ---- The logits producer ----------------------------------------------------
  * The model's last step before sampling, on the device: each row's final
- * hidden state through the output rmsnorm and the lm-head matvec, written as
- * the [rows, vocab] f32 logits that ultima_hsamp_run() samples, with no host
- * round trip. Replaces, per token row, the reference's
+ * hidden state through the output rmsnorm, the Hadamard fold when the head is
+ * folded, and the lm-head matvec, written as the [rows, vocab] f32 logits that
+ * ultima_hsamp_run() samples, with no host round trip. Replaces, per token row,
+ * the reference's
  *   kernels::rmsnorm_f32(last, output_norm, x_norm, hidden, rms_eps)
- *   matvec_dispatch_threaded(pool, head.dtype, head.data, x_norm, out_logits, vocab, hidden)
+ *   if (head.hadamard_folded && fold)
+ *     kernels::hadamard_fold_f32(x_norm, fold_buf, hidden, fold.block, fold.signs_for(hidden))
+ *   matvec_dispatch_threaded(pool, head.dtype, head.data, head_in, out_logits, vocab, hidden)
  *   out_logits[i] *= 1 / logit_scale            (when logit_scale is neither 1 nor 0)
  *     /root/reference/src/model/qwen_model.cpp:182-207,
- *     /root/reference/src/model/weight_dispatch.cpp:106-146 (F32 and BF16 heads),
- *     /root/reference/src/kernels/rmsnorm.cpp:21-52, matvec_f32_f32.cpp:22-50,
- *     matvec_bf16_f32.cpp:48-68.
+ *     /root/reference/src/model/weight_dispatch.cpp:106-146 (every head type it
+ *     dispatches: F32, BF16, Q4_K, Q5_K, Q6_K, Q8_0, Q4_1, Q5_0, PQ2_0),
+ *     /root/reference/src/kernels/rmsnorm.cpp:21-52, hadamard.cpp:9-44,
+ *     matvec_f32_f32.cpp:22-50, matvec_bf16_f32.cpp:48-68,
+ *     matvec_q4k_f32.cpp:108-160, matvec_q5k_f32.cpp:48-80,
+ *     matvec_q6k_f32.cpp:99-169, matvec_q8_0_f32.cpp:83-117,
+ *     matvec_q4_1_f32.cpp:47-75, matvec_q5_0_f32.cpp:108-150,
+ *     matvec_pq2_0_f32.cpp:111-184.
  * The results are the reference's bits: every sum runs in the order of its
- * AVX2 kernels (eight fused multiply-add partials, their horizontal sum, the
- * n % 8 tail). Quantised heads (Q4_K, Q6_K, Q8_0, ...) and the Hadamard fold
- * are not built. All pointers are device memory. */
+ * AVX2 kernels (the F32 / BF16 heads: eight fused multiply-add partials, their
+ * horizontal sum, the n % 8 tail; each quantised type: its kernel's own
+ * partial-sum layout and dequantisation roundings). Quantised rows are the
+ * GGUF blocks back to back (row bytes = H / block values * block bytes); as in
+ * the reference, a hidden size that is not a whole number of the type's blocks
+ * gives logits of 0. PQ2_0 follows the vectorised path matvec_pq2_0_f32 takes
+ * for a call of at least 8 rows (every thread's share of a vocabulary head).
+ * All pointers are device memory. */
+#define ULTIMA_HSAMP_HEAD_Q4_K 2     /* 256 values in 144 bytes */
+#define ULTIMA_HSAMP_HEAD_Q5_K 3     /* 256 values in 176 bytes */
+#define ULTIMA_HSAMP_HEAD_Q6_K 4     /* 256 values in 210 bytes */
+#define ULTIMA_HSAMP_HEAD_Q8_0 5     /* 32 values in 34 bytes */
+#define ULTIMA_HSAMP_HEAD_Q4_1 6     /* 32 values in 20 bytes */
+#define ULTIMA_HSAMP_HEAD_Q5_0 7     /* 32 values in 22 bytes */
+#define ULTIMA_HSAMP_HEAD_PQ2_0 8    /* 128 values in 34 bytes */
+#define ULTIMA_HSAMP_MAX_FOLD_BLOCK 8192
 typedef struct ultima_hsamp_head {
     const float* hidden;        /* [rows, hidden_stride] final hidden states */
     int64_t hidden_stride;      /* elements between rows, >= hidden_dim */
     int32_t rows;               /* >= 1 */
     int32_t hidden_dim;         /* H >= 1 */
     int32_t vocab;              /* V >= 1 */
-    int32_t weight_dtype;       /* ULTIMA_HSAMP_F32 or ULTIMA_HSAMP_BF16 */
+    int32_t weight_dtype;       /* ULTIMA_HSAMP_F32, ULTIMA_HSAMP_BF16 or ULTIMA_HSAMP_HEAD_* */
     const float* norm_scale;    /* [H] output-norm weights */
     float eps;                  /* rms epsilon */
     float logit_scale;          /* logits are multiplied by 1 / logit_scale unless it is 1 or 0 */
-    const void* weight;         /* [V, H] row-major head weights (f32, or bf16 bit patterns) */
-    float* normed;              /* [rows, H] scratch: the normed rows (left there) */
+    const void* weight;         /* [V, H] row-major head weights (f32, bf16 bit patterns, or GGUF blocks) */
+    float* normed;              /* [rows, H] scratch, left holding the head's input: the normed rows,
+                                   folded when the head is */
     float* logits;              /* [rows, logits_stride] output */
     int64_t logits_stride;      /* elements between rows, >= V */
+    int32_t fold_block;         /* 0: no fold; else the fold's block (a power of two up to
+                                   ULTIMA_HSAMP_MAX_FOLD_BLOCK; one that does not divide H leaves
+                                   the rows unfolded, as the reference does) */
+    const float* fold_signs;    /* [H] +-1 signs applied before the rotation, or NULL */
 } ultima_hsamp_head;
 
 /* Runs the head for every row on hip_stream (NULL = the default stream).

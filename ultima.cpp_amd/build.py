@@ -64,6 +64,7 @@ def build_all() -> None:
         "hsamp_kernels.o": CSRC / "hsamp_kernels.hip",
         "hsamp_api.o": CSRC / "hsamp_api.cpp",
         "hsamp_head.o": CSRC / "hsamp_head.hip",
+        "hsamp_headq.o": CSRC / "hsamp_headq.hip",
         "hsamp_history.o": CSRC / "hsamp_history.hip",
         "hsamp_callers.o": CSRC / "hsamp_callers.hip",
     }

@@ -28,6 +28,7 @@
 #include <cstdint>
 #include <type_traits>
 
+#include "hsamp_head.h"
 #include "hsamp_wave.h"
 #include "ultima_hsamp.h"
 
@@ -66,6 +67,8 @@ __device__ __forceinline__ float hsum8_lanes(float p) {
 
 // WB: bf16 weights (else f32). BB: batch rows per block (1, 2 or 4). VEC:
 // weight rows sit on 16-byte boundaries (16-byte loads; else element loads).
+// PRE: `hidden` already holds the head's input (normed and folded by
+// k_head_prep): no norm here, the values are used as they are.
 // One wave per 64 vocabulary rows, lane i running the eight chains of row
 // m0 + i. The weights arrive in chunks of 128 bytes of each row: coalesced
 // 16-byte loads (eight lanes per row segment) into registers, one chunk
@@ -74,7 +77,7 @@ __device__ __forceinline__ float hsum8_lanes(float p) {
 // time -- one step of all eight chains (bf16), or half a step (f32). The
 // normed rows' columns of the chunk go through LDS too and are read as
 // broadcasts. The block is the one wave: no barrier waits on another wave.
-template <bool WB, int BB, bool VEC>
+template <bool WB, int BB, bool VEC, bool PRE>
 __global__ __launch_bounds__(64) void k_head_gemv(const void* __restrict__ weight, int V, int H,
                                                   const float* __restrict__ hidden, int64_t hstride,
                                                   const float* __restrict__ scale, float eps,
@@ -155,7 +158,7 @@ __global__ __launch_bounds__(64) void k_head_gemv(const void* __restrict__ weigh
         }
     };
     float p = 0.0f;   // lane 8b + l: chain l of batch row b
-    const int nP = (H8 + PE - 1) / PE;
+    const int nP = PRE ? 0 : (H8 + PE - 1) / PE;
     if (nP > 0) piece_load(0);
     __builtin_amdgcn_sched_barrier(0);
     if (nC > 0) load(reg, xr, sr, 0);
@@ -193,7 +196,10 @@ __global__ __launch_bounds__(64) void k_head_gemv(const void* __restrict__ weigh
     }
     __syncthreads();                                     // the tile is free for the weights
     float rinv[BB];   // 1 / rms of each batch row (every lane)
-    {
+    if (PRE) {
+#pragma unroll
+        for (int bb = 0; bb < BB; ++bb) rinv[bb] = 1.0f;
+    } else {
         const float hs8 = hsum8_lanes(p);                 // lanes 8b .. 8b + 7: row b's horizontal sum
         const int b = min(lane >> 3, nb - 1);
         const float* x = xrow(b);
@@ -204,7 +210,7 @@ __global__ __launch_bounds__(64) void k_head_gemv(const void* __restrict__ weigh
         for (int bb = 0; bb < BB; ++bb) rinv[bb] = __shfl(r, 8 * bb, 64);
     }
     // the normed rows themselves (an output), 64 columns per wave
-    if (blockIdx.x * 64 < H) {
+    if (!PRE && blockIdx.x * 64 < H) {
         for (int i = blockIdx.x * 64 + lane; i < H; i += gridDim.x * 64) {
             const float g = scale[i];
 #pragma unroll
@@ -223,7 +229,7 @@ __global__ __launch_bounds__(64) void k_head_gemv(const void* __restrict__ weigh
         const int c0 = c * KC;
 #pragma unroll
         for (int b = 0; b < BB; ++b)
-            if (lane < KC) xl[b][lane] = (b < nb && c0 + lane < H8) ? (xr[b] * sr) * rinv[b] : 0.0f;
+            if (lane < KC) xl[b][lane] = (b < nb && c0 + lane < H8) ? (PRE ? xr[b] : (xr[b] * sr) * rinv[b]) : 0.0f;
     };
     float acc[BB][8];
 #pragma unroll
@@ -292,7 +298,7 @@ __global__ __launch_bounds__(64) void k_head_gemv(const void* __restrict__ weigh
         const float s0 = p[0] + p[4], s1 = p[1] + p[5], s2 = p[2] + p[6], s3 = p[3] + p[7];
         const float hs = (s0 + s1) + (s2 + s3);
         const float* x = xrow(b);
-        auto xn = [&](int i) { return (x[H8 + i] * scale[H8 + i]) * rinv[b]; };   // normed value H8 + i
+        auto xn = [&](int i) { return PRE ? x[H8 + i] : (x[H8 + i] * scale[H8 + i]) * rinv[b]; };   // normed value H8 + i
         float y;
         if (WB) {
             float tail = 0.0f;
@@ -306,28 +312,31 @@ __global__ __launch_bounds__(64) void k_head_gemv(const void* __restrict__ weigh
     }
 }
 
-template <bool WB, int BB>
+template <bool WB, int BB, bool PRE>
 hipError_t launch_gemv_bb(const ultima_hsamp_head* h, bool vec, hipStream_t s) {
     // one wave per 64 vocabulary rows: every wave the same work, all resident
     // at once for real vocabularies (151936 rows: 2374 waves)
     const dim3 grid((h->vocab + 63) / 64, (h->rows + BB - 1) / BB);
+    // PRE: the head's input is the prepared rows in `normed`
+    const float* in = PRE ? h->normed : h->hidden;
+    const int64_t in_stride = PRE ? h->hidden_dim : h->hidden_stride;
     if (vec)
-        hipLaunchKernelGGL((k_head_gemv<WB, BB, true>), grid, dim3(64), 0, s, h->weight, h->vocab, h->hidden_dim,
-                           h->hidden, h->hidden_stride, h->norm_scale, h->eps, h->normed, h->rows,
+        hipLaunchKernelGGL((k_head_gemv<WB, BB, true, PRE>), grid, dim3(64), 0, s, h->weight, h->vocab, h->hidden_dim,
+                           in, in_stride, h->norm_scale, h->eps, h->normed, h->rows,
                            h->logit_scale, h->logits, h->logits_stride);
     else
-        hipLaunchKernelGGL((k_head_gemv<WB, BB, false>), grid, dim3(64), 0, s, h->weight, h->vocab, h->hidden_dim,
-                           h->hidden, h->hidden_stride, h->norm_scale, h->eps, h->normed, h->rows,
+        hipLaunchKernelGGL((k_head_gemv<WB, BB, false, PRE>), grid, dim3(64), 0, s, h->weight, h->vocab, h->hidden_dim,
+                           in, in_stride, h->norm_scale, h->eps, h->normed, h->rows,
                            h->logit_scale, h->logits, h->logits_stride);
     return hipGetLastError();
 }
 
 // batch rows per block: one weight pass per group of up to four rows
-template <bool WB>
+template <bool WB, bool PRE>
 hipError_t launch_gemv(const ultima_hsamp_head* h, bool vec, hipStream_t s) {
-    if (h->rows == 1) return launch_gemv_bb<WB, 1>(h, vec, s);
-    if (h->rows == 2) return launch_gemv_bb<WB, 2>(h, vec, s);
-    return launch_gemv_bb<WB, 4>(h, vec, s);
+    if (h->rows == 1) return launch_gemv_bb<WB, 1, PRE>(h, vec, s);
+    if (h->rows == 2) return launch_gemv_bb<WB, 2, PRE>(h, vec, s);
+    return launch_gemv_bb<WB, 4, PRE>(h, vec, s);
 }
 
 }  // namespace
@@ -341,13 +350,34 @@ extern "C" int ultima_hsamp_lm_head(const ultima_hsamp_head* h, void* hip_stream
     if (h->rows < 1 || h->hidden_dim < 1 || h->vocab < 1 || h->hidden_stride < h->hidden_dim ||
         h->logits_stride < h->vocab)
         return ULTIMA_HSAMP_ERR_INVALID;
-    if (h->weight_dtype != ULTIMA_HSAMP_F32 && h->weight_dtype != ULTIMA_HSAMP_BF16) return ULTIMA_HSAMP_ERR_INVALID;
+    const bool dense = h->weight_dtype == ULTIMA_HSAMP_F32 || h->weight_dtype == ULTIMA_HSAMP_BF16;
+    if (!dense && head_block_values(h->weight_dtype) == 0) return ULTIMA_HSAMP_ERR_INVALID;
+    // PQ2_0's block sums of the activation are kept in LDS: at most 512 blocks
+    if (h->weight_dtype == ULTIMA_HSAMP_HEAD_PQ2_0 && h->hidden_dim > 512 * 128) return ULTIMA_HSAMP_ERR_UNSUPPORTED;
     if (!(h->eps == h->eps) || !(h->logit_scale == h->logit_scale)) return ULTIMA_HSAMP_ERR_INVALID;
+    // the fold's block: 0 (none) or a power of two the prep kernel's LDS holds
+    if (h->fold_block < 0 || (h->fold_block & (h->fold_block - 1)) != 0) return ULTIMA_HSAMP_ERR_INVALID;
+    if (h->fold_block > ULTIMA_HSAMP_MAX_FOLD_BLOCK) return ULTIMA_HSAMP_ERR_UNSUPPORTED;
     // row offsets must fit the kernels' 32-bit index arithmetic within a row
     if ((int64_t)h->vocab * h->hidden_dim >= (int64_t)1 << 40) return ULTIMA_HSAMP_ERR_UNSUPPORTED;
     hipStream_t s = static_cast<hipStream_t>(hip_stream);
+    // the fold applies when its block divides H (else the reference leaves
+    // the rows as they are)
+    const bool fold = h->fold_block > 0 && h->hidden_dim % h->fold_block == 0;
+    hipError_t e = hipSuccess;
+    if (!dense) {
+        e = launch_head_prep(h, s);
+        if (e == hipSuccess) e = launch_head_quant(h, s);
+        return e == hipSuccess ? ULTIMA_HSAMP_OK : ULTIMA_HSAMP_ERR_HIP;
+    }
     const int es = h->weight_dtype == ULTIMA_HSAMP_BF16 ? 2 : 4;
     const bool vec = (reinterpret_cast<uintptr_t>(h->weight) % 16 == 0) && (((int64_t)h->hidden_dim * es) % 16 == 0);
-    const hipError_t e = h->weight_dtype == ULTIMA_HSAMP_BF16 ? launch_gemv<true>(h, vec, s) : launch_gemv<false>(h, vec, s);
+    if (fold) {
+        e = launch_head_prep(h, s);
+        if (e == hipSuccess)
+            e = h->weight_dtype == ULTIMA_HSAMP_BF16 ? launch_gemv<true, true>(h, vec, s) : launch_gemv<false, true>(h, vec, s);
+    } else {
+        e = h->weight_dtype == ULTIMA_HSAMP_BF16 ? launch_gemv<true, false>(h, vec, s) : launch_gemv<false, false>(h, vec, s);
+    }
     return e == hipSuccess ? ULTIMA_HSAMP_OK : ULTIMA_HSAMP_ERR_HIP;
 }

@@ -92,6 +92,8 @@ class Head(ctypes.Structure):
         ("normed", ctypes.c_void_p),
         ("logits", ctypes.c_void_p),
         ("logits_stride", ctypes.c_int64),
+        ("fold_block", ctypes.c_int32),
+        ("fold_signs", ctypes.c_void_p),
     ]
 
 
@@ -351,19 +353,27 @@ def decode_commit(hist, hist_len_dev, tokens, active, keep: int, stop_ids=(), bu
         ctypes.c_void_p(s.cuda_stream)), "decode_commit")
 
 
+# head weight types (ULTIMA_HSAMP_F32 / _BF16 / _HEAD_*)
+HEAD_Q4_K, HEAD_Q5_K, HEAD_Q6_K, HEAD_Q8_0, HEAD_Q4_1, HEAD_Q5_0, HEAD_PQ2_0 = range(2, 9)
+
+
 def lm_head(hidden, norm_scale, eps: float, weight, logit_scale: float = 1.0, logits=None, normed=None,
-            stream=None):
+            stream=None, weight_dtype=None, fold_block: int = 0, fold_signs=None):
     """ultima_hsamp_lm_head on torch tensors of one device: hidden [rows, H] f32,
-    norm_scale [H] f32, weight [V, H] f32 or bf16. Returns (logits [rows, V],
-    normed [rows, H]); the outputs may be passed in (allocated otherwise)."""
+    norm_scale [H] f32, weight [V, H] f32 or bf16, or a quantised head [V, row
+    bytes] uint8 with weight_dtype one of HEAD_Q*; fold_block / fold_signs [H]
+    f32 the Hadamard fold. Returns (logits [rows, V], normed [rows, H]); the
+    outputs may be passed in (allocated otherwise)."""
     import torch
     if hidden.dim() == 1:
         hidden = hidden.unsqueeze(0)
     rows, H = hidden.shape
     V = weight.shape[0]
     dev = hidden.device
-    if weight.dtype not in (torch.float32, torch.bfloat16):
-        raise HsampError(ERR_INVALID, "lm_head: weight must be float32 or bfloat16")
+    if weight_dtype is None:
+        if weight.dtype not in (torch.float32, torch.bfloat16):
+            raise HsampError(ERR_INVALID, "lm_head: weight must be float32 or bfloat16 (or give weight_dtype)")
+        weight_dtype = BF16 if weight.dtype == torch.bfloat16 else F32
     if logits is None:
         logits = torch.empty((rows, V), dtype=torch.float32, device=dev)
     if normed is None:
@@ -372,7 +382,7 @@ def lm_head(hidden, norm_scale, eps: float, weight, logit_scale: float = 1.0, lo
     h.hidden = hidden.data_ptr()
     h.hidden_stride = hidden.stride(0)
     h.rows, h.hidden_dim, h.vocab = rows, H, V
-    h.weight_dtype = 1 if weight.dtype == torch.bfloat16 else 0
+    h.weight_dtype = weight_dtype
     h.norm_scale = norm_scale.data_ptr()
     h.eps = eps
     h.logit_scale = logit_scale
@@ -380,6 +390,8 @@ def lm_head(hidden, norm_scale, eps: float, weight, logit_scale: float = 1.0, lo
     h.normed = normed.data_ptr()
     h.logits = logits.data_ptr()
     h.logits_stride = logits.stride(0)
+    h.fold_block = fold_block
+    h.fold_signs = None if fold_signs is None else fold_signs.data_ptr()
     s = torch.cuda.current_stream(dev) if stream is None else stream
     check(lib().ultima_hsamp_lm_head(ctypes.byref(h), ctypes.c_void_p(s.cuda_stream)), "lm_head")
     return logits, normed

@@ -48,11 +48,28 @@ def hs(pkg):
 
 
 @pytest.fixture(scope="session")
-def sampler(hs):
-    """One library handle shared by the GPU parity tests."""
-    s = hs.Sampler(0, max_rows=1024, max_vocab=1 << 18)
-    yield s
-    s.close()
+def _samplers(hs):
+    cache = {}
+    yield cache
+    for s in cache.values():
+        s.close()
+
+
+OVERRIDES = ("ULTIMA_HSAMP_EXACT", "ULTIMA_HSAMP_EXACT_TILES", "ULTIMA_HSAMP_SLICES")
+
+
+@pytest.fixture
+def sampler(hs, _samplers, request):
+    """A library handle shared by the GPU parity tests, one per setting of the
+    diagnostics overrides (which a handle reads when it is created): a test
+    that takes kernel_mode gets the handle of its mode."""
+    import os
+    if "kernel_mode" in request.fixturenames:
+        request.getfixturevalue("kernel_mode")
+    key = tuple(os.environ.get(k) for k in OVERRIDES)
+    if key not in _samplers:
+        _samplers[key] = hs.Sampler(0, max_rows=1024, max_vocab=1 << 18)
+    return _samplers[key]
 
 
 @pytest.fixture(params=["default", "exact", "exact2", "exact4", "general"])

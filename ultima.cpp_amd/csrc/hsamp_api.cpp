@@ -15,7 +15,6 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
-#include <map>
 #include <tuple>
 #include <vector>
 
@@ -29,7 +28,7 @@ hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, bool pen_gree
 hipError_t launch_writeback(const StreamArgs& a, int grid, uint32_t lds, hipStream_t stream);
 hipError_t launch_merge(const StreamArgs& a, hipStream_t stream);
 hipError_t launch_pick_l(const StreamArgs& a, hipStream_t stream);
-hipError_t launch_stream_ex(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int tiles, int grid,
+hipError_t launch_stream_ex(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int tiles, bool lean, int grid,
                             hipStream_t stream);
 hipError_t launch_pick(const StreamArgs& a, int nw, hipStream_t stream);
 hipError_t launch_full(const StreamArgs& a, uint32_t lds, hipStream_t stream);
@@ -157,7 +156,10 @@ int build_blob(HostScratch& hs, const ultima_hsamp_batch* b, Built& out) {
     hs.plans.assign(B, RowPlan{});
     std::vector<float>& dry = hs.dry;
     dry.clear();
-    std::map<DryKey, int32_t> dry_seen;
+    // DRY tables already built for this batch (a handful of distinct settings:
+    // a linear search over a reused vector, no allocation once warm)
+    auto& dry_seen = hs.dry_seen;
+    dry_seen.clear();
     std::vector<int32_t>& bids = hs.bias_ids;
     std::vector<float>& bvals = hs.bias_vals;
     bids.clear();
@@ -213,7 +215,7 @@ int build_blob(HostScratch& hs, const ultima_hsamp_batch* b, Built& out) {
         if (fl & RF_DRY) {
             // sampler.cpp:79-81: pen = multiplier * powf(base, float(n - allowed_len))
             const DryKey key{fbits(q.dry_multiplier), fbits(q.dry_base), P.dry_allowed, (int32_t)dry_w};
-            auto it = dry_seen.find(key);
+            auto it = std::find_if(dry_seen.begin(), dry_seen.end(), [&](const auto& e) { return e.first == key; });
             if (it == dry_seen.end()) {
                 const int32_t off = (int32_t)dry.size();
                 for (int64_t c = 0; c <= dry_w; ++c) {
@@ -222,7 +224,8 @@ int build_blob(HostScratch& hs, const ultima_hsamp_batch* b, Built& out) {
                                            std::pow(q.dry_base, static_cast<float>((uint64_t)c - q.dry_allowed_len))
                                      : 0.0f);
                 }
-                it = dry_seen.emplace(key, off).first;
+                dry_seen.emplace_back(key, off);
+                it = dry_seen.end() - 1;
             }
             P.dry_tab = it->second;
         }
@@ -284,6 +287,13 @@ int build_blob(HostScratch& hs, const ultima_hsamp_batch* b, Built& out) {
         // DRY and frequency/presence counting over different windows (DRY looks
         // back fewer ids than repetition): two counts per id, general kernels
         if ((fl & RF_DRY) && (fl & RF_FP) && fp_w != dry_w) out.dry_split = true;
+        // the repetition window and the count window (DRY's, else frequency /
+        // presence's) both on and different: a count entry is a count plus a
+        // repetition bit
+        {
+            const int64_t cw = dry_w > 0 ? dry_w : fp_w;
+            if (rep_w > 0 && cw > 0 && rep_w != cw) out.two_windows = true;
+        }
         if (fl & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) {
             out.any_pen = true;
             out.max_pen = std::max(out.max_pen, (int)scan + P.bias_cnt);
@@ -330,6 +340,15 @@ int validate_batch(const ultima_hsamp_batch* b, int32_t max_rows, int32_t max_vo
     return ULTIMA_HSAMP_OK;
 }
 
+void read_overrides(DevCaps& dc) {
+    if (const char* ev = std::getenv("ULTIMA_HSAMP_EXACT")) dc.exact_off = ev[0] == '0';
+    if (const char* et = std::getenv("ULTIMA_HSAMP_EXACT_TILES")) {
+        const int t = std::atoi(et);
+        dc.forced_tiles = t == 4 ? 4 : t == 2 ? 2 : 1;
+    }
+    if (const char* fs = std::getenv("ULTIMA_HSAMP_SLICES")) dc.forced_slices = std::max(1, std::atoi(fs));
+}
+
 int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, RunPlan& rp) {
     const int B = b->rows, V = b->vocab;
     const int es = b->dtype == ULTIMA_HSAMP_F32 ? 4 : 2;
@@ -349,7 +368,7 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     rp.wb = (b->flags & ULTIMA_HSAMP_WRITEBACK) != 0;
     bool exact_ok = (bl.any_sample || bl.any_greedy) && !bl.any_full && kmax <= kLimitK && !rp.wb && bl.inv_ok &&
                     (!bl.any_pen || (bl.pen_lowers_nb && !bl.dry_split && bl.max_bias <= kBlock && bl.max_scan <= 8 * kBlock));
-    if (const char* ev = std::getenv("ULTIMA_HSAMP_EXACT")) exact_ok = exact_ok && ev[0] != '0';
+    exact_ok = exact_ok && !dc.exact_off;
     // 16-byte loads: aligned rows holding at least one whole chunk
     const bool vec_rows = (reinterpret_cast<uintptr_t>(b->logits) % 16 == 0) && ((b->logits_stride * es) % 16 == 0) &&
                           V >= 16 / es;
@@ -363,11 +382,7 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     const int tiles = (V + kTile - 1) / kTile;
     const int S2 = (V + 2 * kTile - 1) / (2 * kTile);
     int S = std::max(1, std::min({kTargetBlocks / B, tiles, kBlock}));
-    int forced_tiles = 0;
-    if (const char* et = std::getenv("ULTIMA_HSAMP_EXACT_TILES")) {
-        const int t = std::atoi(et);
-        forced_tiles = t == 4 ? 4 : t == 2 ? 2 : 1;
-    }
+    const int forced_tiles = dc.forced_tiles;
     // bf16 rows: four tiles of them take the registers two f32 tiles take
     const int max_tiles = (vec_rows && b->dtype == ULTIMA_HSAMP_BF16) ? 4 : vec_rows ? 2 : 1;
     const int S4 = (V + 4 * kTile - 1) / (4 * kTile);
@@ -399,7 +414,7 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     if (exact_ok) S = std::max(S, (vec_rows && forced_tiles != 1) ? S2 : tiles);
     if (four) S = S4;
     // diagnostics: a forced slice count (as many slices as the kernels allow)
-    if (const char* fs = std::getenv("ULTIMA_HSAMP_SLICES")) S = std::max(1, std::min(std::atoi(fs), kBlock));
+    if (dc.forced_slices > 0) S = std::min(dc.forced_slices, kBlock);
     const int slice_len = ((V + S - 1) / S + 31) & ~31;
     S = (V + slice_len - 1) / slice_len;
     // block and row indices are divided by S with a 32-bit reciprocal (exact below 2^32 / S)
@@ -594,8 +609,11 @@ int launch_run(const RunPlan& rp, const Built& bl, const ultima_hsamp_batch* b, 
     // In flag mode the sampling rows' stream needs no penalties at all: it
     // bounds on pre-penalty keys, which penalties can only lower, and k_merge
     // finds the penalised candidates' true values (checking the bounds).
+    // (exact lists: the lean instantiation when no row is greedy, has a logit
+    // bias or counts over two windows)
+    const bool lean = !bl.any_greedy && bl.max_bias == 0 && !bl.two_windows;
     if (rp.exact)
-        HIP_TRY(launch_stream_ex(a, b->dtype, rp.vec, bl.any_pen, bl.any_mask, rp.ex_tiles, rp.grid, stream));
+        HIP_TRY(launch_stream_ex(a, b->dtype, rp.vec, bl.any_pen, bl.any_mask, rp.ex_tiles, lean, rp.grid, stream));
     else if (bl.any_topk)
         HIP_TRY(launch_stream(a, b->dtype, rp.vec, bl.any_pen, bl.any_pen && !a.pen_flag, bl.any_mask,
                               bl.any_greedy, bl.any_sample, rp.grid, stream));
@@ -771,6 +789,7 @@ int ultima_hsamp_create(int device, int32_t max_rows, int32_t max_vocab, ultima_
     h->max_vocab = max_vocab;
     h->caps.lds_limit = prop.sharedMemPerBlock;
     h->caps.cus = std::max(1, prop.multiProcessorCount);
+    read_overrides(h->caps);
     auto fail = [&](int st) {
         ultima_hsamp_destroy(h);
         return st;

@@ -16,14 +16,18 @@
 //   over the row in a fixed element order, and a fixed reduction of them -- so
 //   one lane runs one vocabulary row: all of that row's chains, in registers.
 //   A wave takes 64 rows. Their bytes arrive in chunks of whole blocks (about
-//   150-280 bytes per row): coalesced 16-byte loads of the 64 rows' aligned
-//   spans, one chunk ahead in registers, then into a row-major LDS tile (rows
-//   padded to an odd number of dwords: lanes reading their own rows hit
+//   140-210 bytes per row): coalesced 16-byte buffer loads of the 64 rows'
+//   aligned spans, one chunk ahead in registers, then into a row-major LDS tile
+//   (rows padded to an odd number of dwords: lanes reading their own rows hit
 //   different banks), from which each lane reads its row's dwords (a byte
-//   shift by alignbyte where a block starts inside a dword). The activation
-//   is the same for every lane: it is read with scalar loads straight into
-//   the multiply-adds' scalar operand. NWB waves share one tile, each running
-//   a different batch row.
+//   shift by alignbyte where a block starts inside a dword). The activation is
+//   the same for every lane: the chunk's values go through LDS with the
+//   weights and are read as broadcasts. (Scalar loads would share the LDS
+//   reads' wait counter and flat loads both counters: either makes a wait for
+//   a tile read also wait for the next chunk in flight.) NWB waves share one
+//   tile, each running a different batch row. Values are unpacked a dword at
+//   a time into one value per byte (masks and shifts over four values at once)
+//   and converted by byte.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -53,9 +57,13 @@ __device__ __forceinline__ float hsum8(const float* p) {
     return (s0 + s1) + (s2 + s3);
 }
 
-// signed byte e of w, unsigned bit field [o, o + n) of w
+// signed byte e of w (one sign-extending convert), unsigned byte e of w as a
+// float (one v_cvt_f32_ubyte), unsigned bit field [o, o + n) of w
 __device__ __forceinline__ int sbyte(uint32_t w, int e) { return (int)(w << (24 - 8 * e)) >> 24; }
+__device__ __forceinline__ float ubytef(uint32_t w, int e) { return (float)((w >> (8 * e)) & 0xFFu); }
 __device__ __forceinline__ uint32_t ubits(uint32_t w, int o, int n) { return (w >> o) & ((1u << n) - 1u); }
+// bits 0..3 of t, one to a byte (bit k -> bit 0 of byte k)
+__device__ __forceinline__ uint32_t spread4(uint32_t t) { return ((t & 15u) * 0x00204081u) & 0x01010101u; }
 
 // ---- the row's bytes in the LDS tile ------------------------------------------
 // A lane's row chunk starts at byte `sh` (0..15) of its tile slot. AL = 1: the
@@ -90,7 +98,7 @@ struct RowBytes {
 // Q8_0 (matvec_q8_0_f32.cpp:83-117): per block, lane l of a block accumulator
 // takes values 8c + l (c = 0..3) from zero; then row partial l += d * it.
 struct FQ8_0 {
-    static constexpr int BE = 32, BB = 34, BPC = 8, NA = 8;
+    static constexpr int BE = 32, BB = 34, BPC = 4, NA = 8;
     template <int SC, class RB, class X>
     __device__ __forceinline__ static void chunk(const RB& rb, const X& x, float* a, int nblk) {
 #pragma unroll
@@ -146,17 +154,21 @@ struct FQ4_1 {
             const int bo = j * BB;
             const uint32_t h = rb.template ld32<SC>(bo);
             const float d = half_to_f32(h & 0xFFFFu), m = half_to_f32(h >> 16);
-            uint32_t q[4];
+            uint32_t lo[4], hi[4];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) q[t] = rb.template ld32<SC>(bo + 4 + 4 * t);
+            for (int t = 0; t < 4; ++t) {
+                const uint32_t q = rb.template ld32<SC>(bo + 4 + 4 * t);
+                lo[t] = q & 0x0F0F0F0Fu;
+                hi[t] = (q >> 4) & 0x0F0F0F0Fu;
+            }
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const float v = __builtin_fmaf((float)ubits(q[i >> 2], 8 * (i & 3), 4), d, m);
+                const float v = __builtin_fmaf(ubytef(lo[i >> 2], i & 3), d, m);
                 a[i] = __builtin_fmaf(v, x(j * BE + i), a[i]);
             }
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const float v = __builtin_fmaf((float)ubits(q[i >> 2], 8 * (i & 3) + 4, 4), d, m);
+                const float v = __builtin_fmaf(ubytef(hi[i >> 2], i & 3), d, m);
                 a[16 + i] = __builtin_fmaf(v, x(j * BE + 16 + i), a[16 + i]);
             }
         }
@@ -176,18 +188,23 @@ struct FQ5_0 {
             const int bo = j * BB;
             const float d = half_to_f32(rb.template ld32<SC>(bo) & 0xFFFFu);
             const uint32_t qh = rb.template ld32<SC>(bo + 2);
-            uint32_t q[4];
+            // the five-bit values, one to a byte: nibble | fifth bit << 4
+            uint32_t lo[4], hi[4];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) q[t] = rb.template ld32<SC>(bo + 6 + 4 * t);
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int v = (int)(ubits(q[i >> 2], 8 * (i & 3), 4) | (ubits(qh, i, 1) << 4)) - 16;
-                a[i] = __builtin_fmaf((float)v * d, x(j * BE + i), a[i]);
+            for (int t = 0; t < 4; ++t) {
+                const uint32_t q = rb.template ld32<SC>(bo + 6 + 4 * t);
+                lo[t] = (q & 0x0F0F0F0Fu) | (spread4(qh >> (4 * t)) << 4);
+                hi[t] = ((q >> 4) & 0x0F0F0F0Fu) | (spread4(qh >> (16 + 4 * t)) << 4);
             }
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const int v = (int)(ubits(q[i >> 2], 8 * (i & 3) + 4, 4) | (ubits(qh, 16 + i, 1) << 4)) - 16;
-                a[16 + i] = __builtin_fmaf((float)v * d, x(j * BE + 16 + i), a[16 + i]);
+                const float v = (ubytef(lo[i >> 2], i & 3) - 16.0f) * d;   // q - 16 exactly, then fl(q * d)
+                a[i] = __builtin_fmaf(v, x(j * BE + i), a[i]);
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float v = (ubytef(hi[i >> 2], i & 3) - 16.0f) * d;
+                a[16 + i] = __builtin_fmaf(v, x(j * BE + 16 + i), a[16 + i]);
             }
         }
     }
@@ -226,17 +243,21 @@ struct FQ4_K {
             scale_min_k4(s, 2 * j + 1, sc1, mn1);
             const float d1 = d * (float)sc0, m1 = dmin * (float)mn0;
             const float d2 = d * (float)sc1, m2 = dmin * (float)mn1;
-            uint32_t q[8];
+            uint32_t lo[8], hi[8];
 #pragma unroll
-            for (int t = 0; t < 8; ++t) q[t] = rb.template ld32<SC>(16 + 32 * j + 4 * t);
+            for (int t = 0; t < 8; ++t) {
+                const uint32_t q = rb.template ld32<SC>(16 + 32 * j + 4 * t);
+                lo[t] = q & 0x0F0F0F0Fu;
+                hi[t] = (q >> 4) & 0x0F0F0F0Fu;
+            }
 #pragma unroll
             for (int l = 0; l < 32; ++l) {
-                const float v = __builtin_fmaf((float)ubits(q[l >> 2], 8 * (l & 3), 4), d1, -m1);
+                const float v = __builtin_fmaf(ubytef(lo[l >> 2], l & 3), d1, -m1);
                 a[l] = __builtin_fmaf(v, x(64 * j + l), a[l]);
             }
 #pragma unroll
             for (int l = 0; l < 32; ++l) {
-                const float v = __builtin_fmaf((float)ubits(q[l >> 2], 8 * (l & 3) + 4, 4), d2, -m2);
+                const float v = __builtin_fmaf(ubytef(hi[l >> 2], l & 3), d2, -m2);
                 a[32 + l] = __builtin_fmaf(v, x(64 * j + 32 + l), a[32 + l]);
             }
         }
@@ -266,20 +287,20 @@ struct FQ5_K {
             scale_min_k4(s, 2 * j + 1, sc1, mn1);
             const float d1 = d * (float)sc0, m1 = dmin * (float)mn0;
             const float d2 = d * (float)sc1, m2 = dmin * (float)mn1;
-            uint32_t q[8];
+            // the five-bit values, one to a byte
+            uint32_t lo[8], hi[8];
 #pragma unroll
-            for (int t = 0; t < 8; ++t) q[t] = rb.template ld32<SC>(48 + 32 * j + 4 * t);
-#pragma unroll
-            for (int l = 0; l < 32; ++l) {
-                const uint32_t v = ubits(q[l >> 2], 8 * (l & 3), 4) | (ubits(qh[l >> 2], 8 * (l & 3) + 2 * j, 1) << 4);
-                a[l] = __builtin_fmaf(__builtin_fmaf(d1, (float)v, -m1), x(64 * j + l), a[l]);
+            for (int t = 0; t < 8; ++t) {
+                const uint32_t q = rb.template ld32<SC>(48 + 32 * j + 4 * t);
+                lo[t] = (q & 0x0F0F0F0Fu) | (((qh[t] >> (2 * j)) & 0x01010101u) << 4);
+                hi[t] = ((q >> 4) & 0x0F0F0F0Fu) | (((qh[t] >> (2 * j + 1)) & 0x01010101u) << 4);
             }
 #pragma unroll
-            for (int l = 0; l < 32; ++l) {
-                const uint32_t v =
-                    ubits(q[l >> 2], 8 * (l & 3) + 4, 4) | (ubits(qh[l >> 2], 8 * (l & 3) + 2 * j + 1, 1) << 4);
-                a[l] = __builtin_fmaf(__builtin_fmaf(d2, (float)v, -m2), x(64 * j + 32 + l), a[l]);
-            }
+            for (int l = 0; l < 32; ++l)
+                a[l] = __builtin_fmaf(__builtin_fmaf(d1, ubytef(lo[l >> 2], l & 3), -m1), x(64 * j + l), a[l]);
+#pragma unroll
+            for (int l = 0; l < 32; ++l)
+                a[l] = __builtin_fmaf(__builtin_fmaf(d2, ubytef(hi[l >> 2], l & 3), -m2), x(64 * j + 32 + l), a[l]);
         }
     }
     __device__ __forceinline__ static float final(const float* a) { return hsum4x8(a); }
@@ -299,21 +320,26 @@ struct FQ6_K {
             float s[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) s[i] = d * (float)sbyte(i < 4 ? sw0 : sw1, i & 3);
+            // per dword of ql / qh: four six-bit values of each run, one to a byte
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                uint32_t ql[8], qh[8];
+            for (int t = 0; t < 8; ++t) {
+                const uint32_t l0 = rb.template ld32<SC>(64 * half + 4 * t);
+                const uint32_t l1 = rb.template ld32<SC>(64 * half + 32 + 4 * t);
+                const uint32_t h = rb.template ld32<SC>(128 + 32 * half + 4 * t);
+                uint32_t q[4];
+                q[0] = (l0 & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u);
+                q[1] = (l1 & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u);
+                q[2] = ((l0 >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u);
+                q[3] = ((l1 >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u);
 #pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    ql[t] = rb.template ld32<SC>(64 * half + 32 * (r & 1) + 4 * t);
-                    qh[t] = rb.template ld32<SC>(128 + 32 * half + 4 * t);
-                }
+                for (int r = 0; r < 4; ++r)
 #pragma unroll
-                for (int l = 0; l < 32; ++l) {
-                    const int q = (int)(ubits(ql[l >> 2], 8 * (l & 3) + 4 * (r >> 1), 4) |
-                                        (ubits(qh[l >> 2], 8 * (l & 3) + 2 * r, 2) << 4)) - 32;
-                    const int p = (r & 1) * 32 + l;
-                    a[p] = __builtin_fmaf((float)q * s[2 * r + (l >> 4)], x(128 * half + 32 * r + l), a[p]);
-                }
+                    for (int e = 0; e < 4; ++e) {
+                        const int l = 4 * t + e;
+                        const int p = (r & 1) * 32 + l;
+                        const float v = (ubytef(q[r], e) - 32.0f) * s[2 * r + (l >> 4)];   // q - 32 exactly
+                        a[p] = __builtin_fmaf(v, x(128 * half + 32 * r + l), a[p]);
+                    }
             }
         }
     }
@@ -327,7 +353,7 @@ struct FQ6_K {
 // (fused as GCC compiles it). a[0] holds the row sum; the block sums come
 // from bs(j).
 struct FPQ2_0 {
-    static constexpr int BE = 128, BB = 34, BPC = 8, NA = 1;
+    static constexpr int BE = 128, BB = 34, BPC = 4, NA = 1;
     template <int SC, class RB, class X, class BS>
     __device__ __forceinline__ static void chunk(const RB& rb, const X& x, const BS& bs, float* a, int nblk) {
 #pragma unroll
@@ -339,19 +365,21 @@ struct FPQ2_0 {
 #pragma unroll
             for (int t = 0; t < 8; ++t) c[t] = rb.template ld32<SC>(bo + 2 + 4 * t);
             float acc[8];
-            // chain by chain: chain l's values are x[32g + 4l + j] (j outer, g inner)
 #pragma unroll
-            for (int l = 0; l < 8; ++l) {
-                float p = 0.0f;
+            for (int l = 0; l < 8; ++l) acc[l] = 0.0f;
+            // lane l of the accumulator: code position j outer, byte group g
+            // inner, byte i = 8g + l's code times x[4i + j]
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < 4; ++j)
 #pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const int i = 8 * g + l;
-                        p = __builtin_fmaf((float)ubits(c[i >> 2], 8 * (i & 3) + 2 * j, 2), x(jb * BE + 4 * i + j), p);
+                for (int t = 0; t < 8; ++t) {
+                    const uint32_t cj = (c[t] >> (2 * j)) & 0x03030303u;   // codes j of bytes 4t .. 4t + 3
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int i = 4 * t + e, l = i & 7;
+                        acc[l] = __builtin_fmaf(ubytef(cj, e), x(jb * BE + 4 * i + j), acc[l]);
                     }
-                acc[l] = p;
-            }
+                }
             a[0] = __builtin_fmaf(d, hsum8(acc) - bs(jb), a[0]);
         }
     }
@@ -371,6 +399,10 @@ constexpr int kMaxPqBlocks = 512;   // PQ2_0 block sums kept in LDS: H <= 65536
 
 // T: head type; NWB: waves (batch rows) per block; AL: every row's chunk
 // starts dword-aligned up to the chunk's shift class (see RowBytes).
+// The block's 64 rows are read through one buffer resource based at the
+// block's first row (16-byte aligned down; `delta` bytes before it): 32-bit
+// offsets, loads past the head's end read 0, and the loads count only in the
+// vector memory counter (waits for LDS reads do not wait for them).
 template <int T, int NWB, int AL>
 __global__ __launch_bounds__(64 * NWB) void k_head_q(const unsigned char* __restrict__ w, int V, int H, int64_t rb,
                                                      const float* __restrict__ xin, int rows, float logit_scale,
@@ -381,8 +413,10 @@ __global__ __launch_bounds__(64 * NWB) void k_head_q(const unsigned char* __rest
     constexpr int NVR = (CB + 15 + 15) / 16;           // 16-byte vectors of a row's aligned span
     constexpr int SLOT = 4 * NVR + 3;                  // dwords per tile row (odd: banks)
     constexpr int NV_T = (64 * NVR + 64 * NWB - 1) / (64 * NWB);   // vectors per thread per chunk
+    constexpr int NX = (CE * 4 / 16 + 63) / 64;        // 16-byte vectors of the activation per lane per chunk
     constexpr bool PQ = T == ULTIMA_HSAMP_HEAD_PQ2_0;
     __shared__ uint32_t tile[64 * SLOT + 4];
+    __shared__ __attribute__((aligned(16))) float xl[NWB][CE];
     __shared__ float bsum[PQ ? NWB * kMaxPqBlocks : 1];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -390,15 +424,28 @@ __global__ __launch_bounds__(64 * NWB) void k_head_q(const unsigned char* __rest
     const int m0 = blockIdx.x * 64;
     const int b = blockIdx.y * NWB + wave;
     const int bb = b < rows ? b : rows - 1;
-    const float* xr = xin + (int64_t)bb * H;
     const int nb = H / F::BE;                          // blocks per row
     const int nC = (nb + F::BPC - 1) / F::BPC;
+
+    // the block's rows: [base, base + nrec) with base 16-byte aligned and nrec
+    // rounded up to 16 bytes (a 16-byte load is out of range as a whole when
+    // it reaches past nrec: the granule holding the rows' last byte is read in
+    // full; it lies in that byte's page)
+    const uintptr_t b0 = reinterpret_cast<uintptr_t>(w) + (uintptr_t)((int64_t)m0 * rb);
+    const uint32_t delta = (uint32_t)(b0 & 15u);
+    const int64_t rows_here = min(64, V - m0);
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<void*>(b0 - delta), (short)0, (int)((delta + rows_here * rb + 15) & ~(int64_t)15), 0x00020000);
+    // the wave's activation row
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(xin + (int64_t)bb * H), (short)0, H * 4, 0x00020000);
 
     if (PQ) {
         // the activation's block sums, plain sequential float sums, lane k
         // taking blocks k, k + 64, ...
+        const float* xrow = xin + (int64_t)bb * H;
         for (int k = lane; k < nb; k += 64) {
-            const float* xs = xr + (int64_t)k * F::BE;
+            const float* xs = xrow + (int64_t)k * F::BE;
             float sum = 0.0f;
             for (int i = 0; i < F::BE; i += 8) {
                 float v[8];
@@ -411,30 +458,40 @@ __global__ __launch_bounds__(64 * NWB) void k_head_q(const unsigned char* __rest
         }
     }
 
-    // chunk c of the 64 rows into registers: vector v = tid + 64 NWB i is 16
-    // bytes seg = v % NVR of tile row r = v / NVR's aligned span (clamped to
-    // the span's last 16-byte granule, rows past V to row V - 1)
+    // vector i of this thread: 16 bytes seg of tile row r's aligned span;
+    // its offset within the block's resource for chunk c is
+    // ((rofs + c CB) & ~15) + 16 seg
+    uint32_t rofs[NV_T];
+    int vseg[NV_T];
+#pragma unroll
+    for (int i = 0; i < NV_T; ++i) {
+        const int v = min(tid + 64 * NWB * i, 64 * NVR - 1);
+        const int r = v / NVR;
+        vseg[i] = v - r * NVR;
+        rofs[i] = delta + (uint32_t)((int64_t)r * rb);
+    }
     uint4 reg[NV_T];
+    uint4 xv[NX];
     auto load = [&](int c) {
-        const int nbytes = min(F::BPC, nb - c * F::BPC) * F::BB;
 #pragma unroll
         for (int i = 0; i < NV_T; ++i) {
-            const int v = min(tid + 64 * NWB * i, 64 * NVR - 1);
-            const int r = v / NVR, seg = v - r * NVR;
-            const uintptr_t a = reinterpret_cast<uintptr_t>(w) + (uintptr_t)(min(m0 + r, V - 1) * rb) +
-                                (uintptr_t)c * CB;
-            const uintptr_t lo = a & ~uintptr_t(15), last = (a + nbytes - 1) & ~uintptr_t(15);
-            const uintptr_t p = lo + 16 * (uintptr_t)seg < last ? lo + 16 * (uintptr_t)seg : last;
+            const uint32_t o = ((rofs[i] + (uint32_t)(c * CB)) & ~15u) + 16u * (uint32_t)vseg[i];
             typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-            const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+            const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(wr, o, 0, 2);
             reg[i] = make_uint4(t.x, t.y, t.z, t.w);
+        }
+#pragma unroll
+        for (int i = 0; i < NX; ++i) {
+            typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+            const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(xr, (uint32_t)(16 * (lane + 64 * i)), c * CE * 4, 0);
+            xv[i] = make_uint4(t.x, t.y, t.z, t.w);
         }
     };
     auto store = [&]() {
 #pragma unroll
         for (int i = 0; i < NV_T; ++i) {
             const int v = tid + 64 * NWB * i;
-            if (v < 64 * NVR) {
+            if ((64 * NVR) % (64 * NWB) == 0 || v < 64 * NVR) {
                 const int r = v / NVR, seg = v - r * NVR;
                 uint32_t* s = tile + r * SLOT + 4 * seg;
                 s[0] = reg[i].x;
@@ -443,24 +500,28 @@ __global__ __launch_bounds__(64 * NWB) void k_head_q(const unsigned char* __rest
                 s[3] = reg[i].w;
             }
         }
+#pragma unroll
+        for (int i = 0; i < NX; ++i)
+            if ((CE * 4 / 16) % 64 == 0 || lane + 64 * i < CE * 4 / 16)
+                *reinterpret_cast<uint4*>(&xl[wave][4 * (lane + 64 * i)]) = xv[i];
     };
 
     float a[F::NA];
 #pragma unroll
     for (int i = 0; i < F::NA; ++i) a[i] = 0.0f;
-    const uintptr_t arow = reinterpret_cast<uintptr_t>(w) + (uintptr_t)(min(m0 + lane, V - 1) * rb);
+    const uint32_t lofs = delta + (uint32_t)((int64_t)lane * rb);   // the lane's row in the resource
     if (nC > 0) load(0);
     for (int c = 0; c < nC; ++c) {
         store();
         __syncthreads();
         if (c + 1 < nC) load(c + 1);
         const int nblk = min(F::BPC, nb - c * F::BPC);
-        const int sh = (int)((arow + (uintptr_t)c * CB) & 15);
+        const int sh = (int)((lofs + (uint32_t)(c * CB)) & 15u);
         RowBytes<AL> rbx;
         rbx.dw = tile + lane * SLOT + (sh >> 2);
         rbx.s3 = sh & 3;
-        const float* xc = xr + (int64_t)c * CE;
-        auto x = [&](int i) { return xc[i]; };
+        const float* xw = xl[wave];
+        auto x = [&](int i) { return xw[i]; };
         auto run = [&](auto sc) {
             constexpr int S = decltype(sc)::value;
             if constexpr (PQ) {

@@ -1939,7 +1939,10 @@ __device__ uint32_t block_kth_bound16(const float (&cm)[NC], int need, Shared& s
 // A sampling or greedy row's slice [lo, hi) with exact lists (one, two or
 // four tiles, raw[] holds them); the row's last slice (last_slice) also takes
 // the ragged end that whole-chunk loads leave out.
-template <int DT, bool VEC, bool PEN, bool MASK, int NC>
+// LEAN: no row of the launch is greedy or has a logit bias, and every
+// penalty row counts over one window (a count entry is a plain count): those
+// paths are compiled out.
+template <int DT, bool VEC, bool PEN, bool MASK, int NC, bool LEAN>
 __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan& P, int r, int lo, int hi,
                                              const uint4 (&raw)[NC], u64* out, int64_t slot,
                                              bool last_slice, bool pen, bool mk, const int32_t (&pre)[8],
@@ -1984,13 +1987,13 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
     // are equal (or one is off) a count entry is a plain count over it (one
     // atomic per id); else a count over cw and a repetition bit.
     const int cw = P.dry_win > 0 ? P.dry_win : P.fp_win;
-    const bool one = P.rep_win == 0 || cw == 0 || P.rep_win == cw;
+    const bool one = LEAN || P.rep_win == 0 || cw == 0 || P.rep_win == cw;
     // The row's logit-bias ids (at most kBlock): each marks its entry, and
     // each is evaluated on its own (bias_pass below: a bias can raise a logit
     // above the bound, so the chunk maxima cannot stand for it); the element
     // passes leave them out. (Their ids and logits are read again there:
     // values held from here to there would cost every row registers.)
-    const bool bias = PEN && pen && (P.flags & RF_BIAS) != 0;
+    const bool bias = !LEAN && PEN && pen && (P.flags & RF_BIAS) != 0;
     const uint32_t bsl = (uint32_t)(min(a.vocab, lo + a.slice_len) - lo);
     auto bias_off = [&]() -> uint32_t {   // this thread's bias id, as a slice offset (>= bsl: none)
         return tid < P.bias_cnt ? (uint32_t)(a.bias_ids[P.bias_off + tid] - lo) : 0xFFFFFFFFu;
@@ -2115,7 +2118,7 @@ __device__ __forceinline__ void stream_exact(const StreamArgs& a, const RowPlan&
     const uint32_t lk = raw_key(lmf);
     // a greedy row (argmax, sampler.cpp:220-228) keeps the ids that can be its
     // largest final logit: the lists of top-k 1, no temperature
-    const bool greedy = (P.flags & RF_GREEDY) != 0;
+    const bool greedy = !LEAN && (P.flags & RF_GREEDY) != 0;
     const int k = greedy ? 1 : P.top_k;
     uint32_t tw;
     if (k <= 64) {
@@ -2301,7 +2304,7 @@ __device__ __forceinline__ int div_slices(int g, const StreamArgs& a) {
     return a.nslices == 1 ? g : (int)__umulhi((uint32_t)g, a.ns_magic);
 }
 
-template <int DT, bool VEC, bool PEN, bool MASK, bool GR, int EX = 0>
+template <int DT, bool VEC, bool PEN, bool MASK, bool GR, int EX = 0, bool LEAN = false>
 __global__ __launch_bounds__(kBlock, EX >= 2 ? 4 : 5) void k_stream(StreamArgs a) {
     using T = Tile<DT>;
     constexpr int NT = EX > 1 ? EX : 1;        // tiles per slice (exact lists: 1 or 2)
@@ -2417,8 +2420,8 @@ __global__ __launch_bounds__(kBlock, EX >= 2 ? 4 : 5) void k_stream(StreamArgs a
         HSAMP_PHASE(logical, 1);
         const int64_t slot = (int64_t)r * a.nslices + s;
         u64* out = a.cand + slot * a.cand_cap;
-        stream_exact<DT, VEC, PEN, MASK, NC>(a, P, r, lo, hi, raw, out, slot, VEC && s == a.nslices - 1, pen, mk,
-                                             pre, hd ? 0 : p0, smem, st);
+        stream_exact<DT, VEC, PEN, MASK, NC, LEAN>(a, P, r, lo, hi, raw, out, slot, VEC && s == a.nslices - 1, pen,
+                                                   mk, pre, hd ? 0 : p0, smem, st);
     } else {
         stream_setup<PEN, MASK>(a, P, r, lo, hi, GR, pen, masked, p0, L, hrow, pbm, pbm + a.bitmap_words, st);
         if (!early) load_tile<DT, VEC>(rs, lo, raw);
@@ -4695,12 +4698,14 @@ static void launch_stream_kind(const StreamArgs& a, int dtype, bool vec, bool pe
 
 // Exact lists: the sampling kernel with final keys (every row samples), slices
 // of one tile, or of two (aligned rows), or of four (aligned bf16 rows).
-template <int NT>
+// LEAN: the launch has no greedy rows, no logit bias and one count window per
+// row (see stream_exact).
+template <int NT, bool LEAN>
 static void launch_stream_exact(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int grid,
                                 hipStream_t stream) {
     const dim3 g(grid), b(kBlock);
     const uint32_t l = a.lds_bytes;
-#define HSAMP_STREAM(DT_, V_, P_, M_) hipLaunchKernelGGL((k_stream<DT_, V_, P_, M_, false, NT>), g, b, l, stream, a)
+#define HSAMP_STREAM(DT_, V_, P_, M_) hipLaunchKernelGGL((k_stream<DT_, V_, P_, M_, false, NT, LEAN>), g, b, l, stream, a)
     if (!vec) {
         if constexpr (NT == 1) {
             if (dtype == 0) HSAMP_STREAM(0, false, true, true);
@@ -4728,16 +4733,22 @@ static void launch_stream_exact(const StreamArgs& a, int dtype, bool vec, bool p
 #undef HSAMP_STREAM
 }
 
-hipError_t launch_stream_ex(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int tiles, int grid,
-                            hipStream_t stream) {
+hipError_t launch_stream_ex(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int tiles, bool lean,
+                            int grid, hipStream_t stream) {
     // two-tile slices are for aligned rows only (the host never asks otherwise)
     // (four-tile slices: aligned bf16 rows only, whose four tiles take the
     // registers two f32 tiles take)
     if (tiles > 1 && !vec) return hipErrorInvalidValue;
     if (tiles == 4 && dtype == 0) return hipErrorInvalidValue;
-    if (tiles == 4) launch_stream_exact<4>(a, dtype, vec, pen, mask, grid, stream);
-    else if (tiles == 2) launch_stream_exact<2>(a, dtype, vec, pen, mask, grid, stream);
-    else launch_stream_exact<1>(a, dtype, vec, pen, mask, grid, stream);
+    if (lean) {
+        if (tiles == 4) launch_stream_exact<4, true>(a, dtype, vec, pen, mask, grid, stream);
+        else if (tiles == 2) launch_stream_exact<2, true>(a, dtype, vec, pen, mask, grid, stream);
+        else launch_stream_exact<1, true>(a, dtype, vec, pen, mask, grid, stream);
+    } else {
+        if (tiles == 4) launch_stream_exact<4, false>(a, dtype, vec, pen, mask, grid, stream);
+        else if (tiles == 2) launch_stream_exact<2, false>(a, dtype, vec, pen, mask, grid, stream);
+        else launch_stream_exact<1, false>(a, dtype, vec, pen, mask, grid, stream);
+    }
     return hipGetLastError();
 }
 

@@ -77,6 +77,7 @@ int setup(int dev, DeviceState*& out) {
         d.ptr = static_cast<unsigned char*>(p);
         d.caps.lds_limit = prop.sharedMemPerBlock;
         d.caps.cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 1;
+        read_overrides(d.caps);
         d.ready = true;
     }
     out = &d;

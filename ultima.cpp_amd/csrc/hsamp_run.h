@@ -9,6 +9,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <tuple>
 #include <vector>
 
 #include "hsamp_plan.h"
@@ -16,11 +17,18 @@
 
 namespace hsamp {
 
-// What a device offers the kernels.
+// What a device offers the kernels, and the diagnostics overrides of the
+// kernel choice (read from the environment once, when a handle is created).
 struct DevCaps {
     size_t lds_limit = 0;   // LDS bytes one block may use
     int cus = 256;          // compute units
+    bool exact_off = false; // ULTIMA_HSAMP_EXACT=0: the general kernels take every batch
+    int forced_tiles = 0;   // ULTIMA_HSAMP_EXACT_TILES: 1, 2 or 4 tiles per exact slice (0: the library's choice)
+    int forced_slices = 0;  // ULTIMA_HSAMP_SLICES: slices per row (0: the library's choice)
 };
+
+// The ULTIMA_HSAMP_EXACT / _EXACT_TILES / _SLICES overrides into dc.
+void read_overrides(DevCaps& dc);
 
 // Host buffers one run fills (kept between runs so that their capacity is reused).
 struct HostScratch {
@@ -30,6 +38,7 @@ struct HostScratch {
     std::vector<int32_t> bias_ids;
     std::vector<float> bias_vals;
     std::vector<std::pair<int32_t, float>> tmp;
+    std::vector<std::pair<std::tuple<uint32_t, uint32_t, int32_t, int32_t>, int32_t>> dry_seen;
 };
 
 // What the batch's rows ask for, from the reference's stage predicates.
@@ -50,6 +59,7 @@ struct Built {
     bool any_greedy = false;   // a greedy row (k_stream's greedy kernel)
     bool any_sample = false;   // a top-k sampling row (k_stream's sampling kernel)
     bool dry_split = false;    // a row whose DRY and frequency/presence windows differ
+    bool two_windows = false;  // a row whose repetition and count windows are both on and differ
 };
 
 // Kernel choice, slicing, LDS sizes and scratch sizes (in elements) of one run.
@@ -90,8 +100,7 @@ struct RunBuffers {
 int validate_batch(const ultima_hsamp_batch* b, int32_t max_rows, int32_t max_vocab);
 // RowPlans + DRY tables + bias entries into hs.blob.
 int build_blob(HostScratch& hs, const ultima_hsamp_batch* b, Built& out);
-// Kernel choice and sizes. Reads the ULTIMA_HSAMP_EXACT / _EXACT_TILES /
-// _SLICES diagnostics overrides from the environment.
+// Kernel choice and sizes (dc carries the diagnostics overrides).
 int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, RunPlan& rp);
 // Launches the run's kernels on `stream` (nothing is allocated or copied).
 int launch_run(const RunPlan& rp, const Built& bl, const ultima_hsamp_batch* b, const RunBuffers& buf,

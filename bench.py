@@ -55,11 +55,16 @@ def parse():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
-    ap.add_argument("--workload", default="sampler", choices=["sampler", "head", "verify", "decode"],
+    ap.add_argument("--workload", default="sampler",
+                    choices=["sampler", "head", "verify", "decode", "dropin", "cli"],
                     help="head: the logits producer (final rmsnorm + lm-head matvec) and the "
                          "producer + sampler step instead of the sampler alone; verify: a drafted "
                          "block's verification (ultima_hsamp_verify_block); decode: one multi-slot "
-                         "server decode step (ultima_hsamp_run_commit, device histories)")
+                         "server decode step (ultima_hsamp_run_commit, device histories); dropin: "
+                         "the C++ drop-in's per-call path (one host row in, the token out, the "
+                         "logits written back) for the reference's three callers' knobs; cli: the "
+                         "CLI's per-token call on the device (SamplerParams::identity() + temperature "
+                         "0.8: softmax and the draw over the whole vocabulary), --cli-rows rows")
     ap.add_argument("--commit", default="fused", choices=["fused", "separate"],
                     help="decode workload: the stop / push rules applied inside the sampler's "
                          "kernels (ultima_hsamp_run_commit) or by ultima_hsamp_decode_commit after run")
@@ -68,6 +73,7 @@ def parse():
                     help="verify workload: drafts in their own array (prefix rows built) instead of "
                          "appended to the sequence's ids")
     ap.add_argument("--slots", type=int, default=64, help="decode workload: slots per step")
+    ap.add_argument("--cli-rows", type=int, default=1, help="cli workload: rows per step")
     ap.add_argument("--head-rows", type=int, default=1, help="head workload: hidden-state rows per step")
     ap.add_argument("--head-hidden", type=int, default=4096, help="head workload: hidden size H")
     ap.add_argument("--head-dtype", default="bf16",
@@ -385,6 +391,172 @@ def head_main(args):
     print(json.dumps(line), flush=True)
 
 
+def cli_main(args):
+    """The CLI's call per generated token (apps/ultima-cli/main.cpp:661-674):
+    SamplerParams::identity() with temperature 0.8 -- no top-k, top-p or
+    penalties, so the softmax and the draw run over all V = 151936 ids
+    (k_full after the k_fs_* passes) -- on device-resident f32 logits
+    ~ N(0, 2^2), --cli-rows rows per step, eight rotating input sets, graph
+    replays timed by HIP events as for the sampler workload."""
+    import torch
+    import __graft_entry__ as ge
+    pkg = ge.load_package()
+    hs, wlm = pkg.hsamp, pkg.workloads
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, V = args.cli_rows, 151936
+    params = [wlm.identity_params(temperature=0.8) for _ in range(B)]
+    sets = []
+    for i in range(N_SETS):
+        x = torch.from_numpy(wlm.normal(300 + i, B * V, 2.0).astype(np.float32).reshape(B, V)).to(dev)
+        u = torch.from_numpy(wlm.uniform53(400 + i, B)).to(dev)
+        sets.append((x, u))
+    sampler = hs.Sampler(0, max_rows=max(B, 64), max_vocab=V)
+    stream = torch.cuda.Stream(dev)
+    outs = [{"token": torch.empty(B, dtype=torch.int32, device=dev),
+             "row_flags": torch.empty(B, dtype=torch.int32, device=dev)} for _ in range(N_SETS)]
+
+    def launch(i, s):
+        x, u = sets[i]
+        sampler.run(x, params, u, outputs=outs[i], stream=s)
+
+    with torch.cuda.stream(stream):
+        for i in range(N_SETS):
+            launch(i, stream)
+    stream.synchronize()
+    x0, u0 = sets[0]
+    kern = sampler.query_kernels(x0, params, u0)
+    t = Timer(torch, stream, launch)
+    ms = t.time(args.steps, args.warmup)[0] / args.steps
+    t.drop()
+    cpu = None
+    if not args.no_cpu:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle as O
+        if O.ref_available():
+            xc = x0[0].cpu().numpy()
+            lat = []
+            for i in range(30):
+                t0 = time.perf_counter()
+                O.ref_sample_row(xc, params[0], seed=i)
+                lat.append(time.perf_counter() - t0)
+            cpu = {"value": 1.0 / statistics.median(lat[3:]), "unit": "rows/s", "cores": 1, "kind": "reference",
+                   "sample": "the reference's sample() on one of the rows, one thread, median of 27 calls"}
+    sampler.close()
+    algo = B * (V * 4 + 12)
+    names = [n for bit, n in ((hs.KERNELS_EXACT, "exact"), (hs.KERNELS_GENERAL, "general"),
+                              (hs.KERNELS_FULL, "full")) if kern & bit]
+    line = {
+        "metric": "CLI per-token sample (identity() + T 0.8, softmax and draw over V=151936), rows/sec",
+        "value": B / (ms * 1e-3),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0, 2^2) rows, 8 rotating sets)",
+        "config": {"workload": f"cli: B={B} V={V} identity() T .8", "rows": B, "vocab": V, "kernels": names,
+                   "us_per_step": round(ms * 1e3, 3), "bytes_per_step": algo},
+        "roofline": {"bound": "hbm", "achieved": algo / (ms * 1e-3) / 1e9, "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": algo / (ms * 1e-3) / 1e9 / PEAK_GBS, "traffic": None, "kernel": "k_fs_* + k_full",
+                     "algorithmic_bytes_per_launch": algo},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def dropin_main(args):
+    """The drop-in's sample(): one host row of V = 151936 f32 logits in, the
+    token out and the logits written back in place (what the reference's
+    sample() leaves), through ultima_hsamp_sample_host -- the call
+    ultima::sampler::sample() makes -- for its callers' knobs: the CLI
+    (SamplerParams::identity() + temperature 0.8, apps/ultima-cli/main.cpp:661-674),
+    the server (SamplerParams{}, src/server/http_server.cpp:159-183) and greedy
+    decoding (temperature 0: argmax after penalties). Host wall clock per call
+    (copies both ways and the kernels), median of --steps calls after
+    --warmup; beside it the reference's own sample() on one host thread on
+    the same rows."""
+    import torch
+    import __graft_entry__ as ge
+    pkg = ge.load_package()
+    hs, wlm = pkg.hsamp, pkg.workloads
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    V, H = 151936, 600
+    rng = np.random.default_rng(9)
+    x0 = rng.normal(0.0, 2.0, V).astype(np.float32)
+    hist = rng.integers(0, V, H).astype(np.int32)
+    kinds = {
+        "cli": wlm.identity_params(temperature=0.8),
+        "server": wlm.default_params(),
+        "greedy": wlm.default_params(temperature=0.0),
+    }
+    s = hs.Sampler(0, max_rows=64, max_vocab=V)
+    lib = hs.lib()
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle as O
+    out = {}
+    for name, p in kinds.items():
+        h = hist if name != "cli" else hist[-64:]
+        parr, _, _ = hs.make_params([p], [h.size], None)
+        x = x0.copy()
+        tok = ctypes.c_int32(-1)
+        us = np.random.default_rng(1).random(args.warmup + args.steps)
+        lat = []
+        for i in range(args.warmup + args.steps):
+            x[:] = x0
+            t0 = time.perf_counter()
+            st = lib.ultima_hsamp_sample_host(s.h, x.ctypes.data, V, parr, h.ctypes.data, None, None,
+                                              float(us[i]), 1, ctypes.byref(tok))
+            dt = time.perf_counter() - t0
+            if st != 0:
+                raise RuntimeError(f"sample_host failed: {st}")
+            if i >= args.warmup:
+                lat.append(dt)
+        xd = torch.from_numpy(x0[None].copy()).to(dev)
+        kern = s.query_kernels(xd, [p], torch.zeros(1, dtype=torch.float64, device=dev),
+                               hist=torch.from_numpy(h[None].copy()).to(dev), hist_len=[h.size], writeback=True)
+        names = [n for bit, n in ((hs.KERNELS_EXACT, "exact"), (hs.KERNELS_GENERAL, "general"),
+                                  (hs.KERNELS_FULL, "full"), (hs.KERNELS_WRITEBACK, "writeback")) if kern & bit]
+        ref_us = None
+        if not args.no_cpu and O.ref_available():
+            rl = []
+            for i in range(min(60, args.steps)):
+                t0 = time.perf_counter()
+                O.ref_sample_row(x0, p, hist=h, seed=i)
+                rl.append(time.perf_counter() - t0)
+            ref_us = round(statistics.median(rl[5:]) * 1e6, 2)
+        out[name] = {"us_per_call": round(statistics.median(lat) * 1e6, 2), "kernels": names,
+                     "reference_1thread_us": ref_us, "hist": int(h.size)}
+    s.close()
+    srv = out["server"]["us_per_call"]
+    line = {
+        "metric": "drop-in sample() calls/sec (host row V=151936 f32 in, token out, logits written back), "
+                  "server SamplerParams{}",
+        "value": 1e6 / srv,
+        "unit": "calls/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": srv / 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0, 2^2) row, 600-id history; CLI row 64 ids)",
+        "config": {"workload": "dropin: one sample() per call, write-back on", "vocab": V, "calls": out},
+        "roofline": None,
+        "cpu_baseline": ({"value": 1e6 / out["server"]["reference_1thread_us"], "unit": "calls/s", "cores": 1,
+                          "kind": "reference", "sample": "the reference's sample() on the same server row, "
+                          "one thread, median of the calls"} if out["server"]["reference_1thread_us"] else None),
+    }
+    print(json.dumps(line), flush=True)
+
+
 def callers_main(args):
     """The batched callers on V = 151936 float32 logits with the server's
     default knobs (SamplerParams{}: DRY over 512 ids, repetition over 64,
@@ -518,6 +690,12 @@ def main():
         return
     if args.workload in ("verify", "decode"):
         callers_main(args)
+        return
+    if args.workload == "dropin":
+        dropin_main(args)
+        return
+    if args.workload == "cli":
+        cli_main(args)
         return
     import torch
     import __graft_entry__ as ge

@@ -123,11 +123,12 @@ typedef struct ultima_hsamp_batch {
     int32_t* kept_count;        /* device [rows] out or NULL */
     int32_t set_cap;            /* capacity of the set outputs per row */
     const int32_t* hist_len_dev; /* device [rows] or NULL: each row's history length, read on the
-                                  * device in place of params[r].hist_len (a history kept on the
-                                  * GPU by ultima_hsamp_history_push). params[r].hist_len must then
-                                  * be the same value, or at most it and at least the row's longest
-                                  * penalty window (so that every window is the same for both);
-                                  * the plan then stays the same from step to step. */
+                                  * device in place of params[r].hist_len (ignored then; a history
+                                  * kept on the GPU by ultima_hsamp_history_push): every penalty
+                                  * window is taken there, min(its last_n, hist_len_dev[r]) as
+                                  * window_slice does, so one plan (and one captured graph) serves
+                                  * every step from the first token on. last_n values are capped
+                                  * at hist_stride. */
 } ultima_hsamp_batch;
 
 typedef struct ultima_hsamp ultima_hsamp;
@@ -179,6 +180,17 @@ int ultima_hsamp_version(void);
 
 /* The allocation-free variant of ultima_hsamp_run, ultima_hsamp_run_noalloc, is
  * declared in ultima_hsamp_noalloc.h and exported by its own library. */
+
+/* Diagnostics, no counterpart in the reference: which kernels
+ * ultima_hsamp_run() would launch for the batch (nothing is launched), as
+ * ULTIMA_HSAMP_KERNELS_* bits: the exact-list pair (k_stream over exact
+ * lists + k_pick), the general pair (k_stream + k_merge), the
+ * full-vocabulary kernel (k_full), the write-back pass (k_writeback). */
+#define ULTIMA_HSAMP_KERNELS_EXACT 1u
+#define ULTIMA_HSAMP_KERNELS_GENERAL 2u
+#define ULTIMA_HSAMP_KERNELS_FULL 4u
+#define ULTIMA_HSAMP_KERNELS_WRITEBACK 8u
+int ultima_hsamp_query_kernels(ultima_hsamp* h, const ultima_hsamp_batch* batch, uint32_t* kernels);
 
 /* Diagnostics, no counterpart in the reference: a plain read of the batch's
  * logits with the launch shape ultima_hsamp_run() would use for it (same grid,
@@ -245,6 +257,9 @@ int ultima_hsamp_decode_commit(int32_t* hist, int64_t hist_stride, int32_t* hist
  * must not ask for write-back (ULTIMA_HSAMP_ERR_UNSUPPORTED). hist and
  * hist_len_dev are normally the batch's own (batch.hist, batch.hist_len_dev):
  * the rows' histories the step samples from are the ones it appends to. */
+/* ultima_hsamp_run_commit returns ULTIMA_HSAMP_ERR_INVALID when keep is below
+ * the batch's longest penalty window (a compaction would drop ids that window
+ * holds in the reference's unbounded history). */
 typedef struct ultima_hsamp_commit {
     int32_t* hist;              /* device [rows, hist_stride] */
     int64_t hist_stride;        /* >= 2 */

@@ -73,9 +73,13 @@ def test_full_vocab_mixed_with_topk_and_greedy_rows(sampler, wl):
     assert compare_rows(w, g) == rows
 
 
-def test_full_vocab_writeback(sampler, wl):
+@pytest.mark.parametrize("pen", [True, False])
+def test_full_vocab_writeback(sampler, wl, pen):
     V, rows = 9000, 3
-    p = wl.identity_params(temperature=0.75, top_p=0.8, rep_penalty=1.2, repeat_last_n=64)
+    if pen:
+        p = wl.identity_params(temperature=0.75, top_p=0.8, rep_penalty=1.2, repeat_last_n=64)
+    else:   # a plain transform: the many-block passes ahead of k_full
+        p = wl.identity_params(temperature=0.75, top_p=0.8)
     w = _wl(wl, V, rows, [p] * rows, hist_len=64)
     g = run_gpu(sampler, w, writeback=True, set_cap=V)
     assert compare_rows(w, g, writeback=True) == rows
@@ -90,3 +94,45 @@ def test_full_vocab_all_masked_row_draws_uniformly(sampler, wl):
     g = run_gpu(sampler, w, set_cap=V)
     assert compare_rows(w, g) == rows
     assert int(g["row_flags"][0]) & 16          # nothing finite: uniform over V
+
+
+@pytest.mark.parametrize("rows,dtype", [(1, "f32"), (3, "f32"), (2, "bf16")])
+def test_cli_identity_rows_at_full_vocab(hs, sampler, wl, rows, dtype):
+    """The CLI's call (SamplerParams::identity() + temperature,
+    apps/ultima-cli/main.cpp:661-674) at V = 151936: its whole-row passes run
+    over many blocks (k_fs_*) ahead of k_full; in the bf16 case with a masked
+    row."""
+    import torch
+    V = 151936
+    p = wl.identity_params(temperature=0.8)
+    mask = None
+    if dtype == "bf16":
+        mask = np.full((rows, V // 32), 0xFFFFFFFF, np.uint32)
+        mask[1, ::3] = 0x0F0F0F0F
+    w = _wl(wl, V, rows, [p] * rows, seed=31 + rows, dtype=dtype, mask=mask)
+    from gpu_helpers import to_device
+    x, u, h, m = to_device(w)
+    k = sampler.query_kernels(x, w.params, u, mask=m)
+    assert k & hs.KERNELS_FULL
+    g = run_gpu(sampler, w, set_cap=V)
+    assert compare_rows(w, g) == rows
+
+
+def test_cli_row_with_nan_logits_is_flagged(hs, sampler, wl):
+    """NaN logits in a whole-vocabulary row count as -inf and flag the row
+    (the reference's softmax would turn every probability into NaN): the
+    token is one of the finite ids, drawn as if the NaN ids were masked."""
+    V = 151936
+    p = wl.identity_params(temperature=0.8)
+    w = _wl(wl, V, 1, [p], seed=41)
+    w.logits[0, 5::1000] = np.nan
+    g = run_gpu(sampler, w, set_cap=V)
+    assert int(g["row_flags"][0]) & hs.ROW_NAN
+    assert not np.isnan(w.logits[0, int(g["token"][0])])
+    masked = w.logits.copy()
+    masked[0, 5::1000] = -np.inf
+    wm = _wl(wl, V, 1, [p], seed=41)
+    wm.logits[:] = masked
+    gm = run_gpu(sampler, wm, set_cap=V)
+    assert int(g["token"][0]) == int(gm["token"][0])
+    assert int(g["kept_count"][0]) == int(gm["kept_count"][0]) == V - 152

@@ -164,3 +164,62 @@ def test_captured_step_with_device_history(hs, sampler):
     for r in range(B):
         n = int(got_len[r])
         np.testing.assert_array_equal(got[r, :n], host[r][-n:])
+
+
+def test_graph_from_the_first_token(hs, sampler, kernel_mode):
+    """One decode step (sample + push) captured right after the first step of a
+    10-id prompt, with the server's defaults (SamplerParams{}: DRY over 512
+    ids, repetition over 64, min_p .05), then replayed 600 times: the windows
+    are taken on the device from each row's current length, so every step
+    equals the oracle on the full host history while the windows grow from
+    10 ids to their caps (compactions: the other loops here)."""
+    import torch
+    dev = torch.device("cuda:0")
+    B, V, P0 = 4, 4096, 10
+    stride, keep = 1024, 512
+    rng = np.random.default_rng(600)
+    params = [O.default_params(temperature=t) for t in (0.2, 0.7, 1.0, 1.3)]
+    base = rng.normal(0.0, 2.5, (B, V)).astype(np.float32)
+    host = [list(rng.integers(0, V, P0)) for _ in range(B)]
+    hist = torch.zeros((B, stride), dtype=torch.int32, device=dev)
+    hist[:, :P0] = torch.from_numpy(np.asarray(host, np.int32)).to(dev)
+    lens = torch.full((B,), P0, dtype=torch.int32, device=dev)
+    x_d = torch.empty((B, V), dtype=torch.float32, device=dev)
+    u_d = torch.empty(B, dtype=torch.float64, device=dev)
+    stream = torch.cuda.Stream(dev)
+    out = None
+
+    def step():
+        nonlocal out
+        # (hist_len is ignored with device lengths: any value)
+        out = sampler.run(x_d, params, u_d, hist=hist, hist_len=[0] * B, hist_len_dev=lens, outputs=out,
+                          stream=stream)
+        hs.history_push(hist, lens, out["token"], keep, stream=stream)
+
+    graph = None
+    for s in range(601):
+        x, u = _step_inputs(rng, base)
+        x_d.copy_(torch.from_numpy(x))
+        u_d.copy_(torch.from_numpy(u))
+        torch.cuda.synchronize()
+        if s == 0:
+            with torch.cuda.stream(stream):
+                step()
+        else:
+            if graph is None:
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=stream):
+                    step()
+                stream.synchronize()
+            graph.replay()
+        torch.cuda.synchronize()
+        tok, fl = out["token"].cpu().numpy(), out["row_flags"].cpu().numpy()
+        for r in range(B):
+            _check_token(int(tok[r]), int(fl[r]), x[r], params[r], host[r], u[r], f"step {s} row {r}")
+            host[r].append(int(tok[r]))
+    got_len = lens.cpu().numpy()
+    got = hist.cpu().numpy()
+    for r in range(B):
+        n = int(got_len[r])
+        assert n == P0 + 601
+        np.testing.assert_array_equal(got[r, :n], host[r][-n:])

@@ -88,6 +88,37 @@ def test_writeback_leaves_reference_state(sampler, wl, cfg):
     compare_rows(w, g, writeback=True)
 
 
+@pytest.mark.parametrize("kind", ["server", "cli_topk", "greedy", "mixed"])
+def test_writeback_on_the_exact_lists(hs, sampler, wl, kind, kernel_mode):
+    """The drop-in's calls write their logits back (sample() works in place):
+    batches the exact lists take keep taking them with write-back (the
+    library's choice: ULTIMA_HSAMP_KERNELS_EXACT), and the logits left behind
+    are the reference's bits -- kept ids at their post-penalty,
+    post-temperature value and the rest -inf, greedy rows' whole post-penalty
+    row -- in every kernel mode."""
+    import torch
+    rng = np.random.default_rng({"server": 1, "cli_topk": 2, "greedy": 3, "mixed": 4}[kind])
+    B, V, H = 6, 151936, 600
+    x = rng.normal(0.0, 2.0, (B, V)).astype(np.float32)
+    hist = rng.integers(0, V, (B, H)).astype(np.int32)
+    hist[:, -30:] = np.argsort(-x, axis=1)[:, :30]          # the likely ids in the windows
+    if kind == "server":
+        plist = [wl.default_params(temperature=0.8) for _ in range(B)]
+    elif kind == "cli_topk":
+        plist = [wl.identity_params(temperature=0.7, top_k=40) for _ in range(B)]
+    elif kind == "greedy":
+        plist = [wl.default_params(temperature=0.0) for _ in range(B)]
+    else:
+        plist = [wl.default_params(temperature=t) for t in (0.0, 0.5, 0.9, 0.0, 1.2, 0.3)]
+    w = _wl_from(wl, x, plist, rng.random(B), hist=hist)
+    if kernel_mode == "default":
+        xd, ud, hd, _ = to_device(w)
+        k = sampler.query_kernels(xd, plist, ud, hist=hd, hist_len=w.hist_len, writeback=True)
+        assert k & hs.KERNELS_EXACT and k & hs.KERNELS_WRITEBACK and not k & hs.KERNELS_GENERAL, k
+    g = run_gpu(sampler, w, writeback=True)
+    compare_rows(w, g, writeback=True)
+
+
 def test_repeated_launches_are_stable(sampler, wl):
     w = wl.config(2, seed=2, rows=16)
     first = run_gpu(sampler, w)["token"]

@@ -26,6 +26,7 @@ namespace hsamp {
 hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, bool pen_greedy, bool pen_sample, bool mask,
                          bool greedy_rows, bool sample_rows, int grid, hipStream_t stream);
 hipError_t launch_writeback(const StreamArgs& a, int grid, uint32_t lds, hipStream_t stream);
+hipError_t launch_full_pre(const StreamArgs& a, hipStream_t stream);
 hipError_t launch_merge(const StreamArgs& a, hipStream_t stream);
 hipError_t launch_pick_l(const StreamArgs& a, hipStream_t stream);
 hipError_t launch_stream_ex(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int tiles, bool lean, int grid,
@@ -94,6 +95,8 @@ struct ultima_hsamp {
     size_t fullp_elems = 0;
     uint32_t* fullk = nullptr;           // full-vocabulary rows: top-p keys
     size_t fullk_elems = 0;
+    uint32_t* fs_tab = nullptr;          // full-vocabulary rows: k_fs_* per-window tables
+    size_t fs_elems = 0;
     // A graph captured from this handle holds the scratch pointers of its
     // launches: once one has been captured, scratch that grows is kept (not
     // freed) until destroy, so that replaying an earlier graph stays valid.
@@ -181,7 +184,11 @@ int build_blob(HostScratch& hs, const ultima_hsamp_batch* b, Built& out) {
         if (q.bias_count < 0 || q.bias_count > ULTIMA_HSAMP_MAX_BIAS ||
             (q.bias_count > 0 && (b->bias_ids == nullptr || b->bias_vals == nullptr || q.bias_offset < 0)))
             return ULTIMA_HSAMP_ERR_INVALID;
-        const int64_t L = q.hist_len;
+        // A history whose length is read on the device (hist_len_dev): the
+        // windows here are the caps its rows can reach (the stride), each
+        // row's own taken on the device (RF_DEVWIN, plan_of in the kernels)
+        const bool devwin = b->hist_len_dev != nullptr;
+        const int64_t L = devwin ? b->hist_stride : q.hist_len;
         auto win = [&](uint64_t n) -> int64_t { return (int64_t)std::min<uint64_t>(n, (uint64_t)L); };
         uint32_t fl = 0;
         bool bias_up = false;   // a bias entry can raise a logit
@@ -211,6 +218,11 @@ int build_blob(HostScratch& hs, const ultima_hsamp_batch* b, Built& out) {
         P.dry_win = (int32_t)dry_w;
         P.fp_win = (int32_t)fp_w;
         P.scan_len = (int32_t)scan;
+        if (devwin) {
+            fl |= RF_DEVWIN;
+            P.win_caps[0] = (uint32_t)rep_w | ((uint32_t)dry_w << 16);
+            P.win_caps[1] = (uint32_t)fp_w;
+        }
         P.dry_allowed = (int32_t)std::min<uint64_t>(q.dry_allowed_len, 0x7fff);
         if (fl & RF_DRY) {
             // sampler.cpp:79-81: pen = multiplier * powf(base, float(n - allowed_len))
@@ -273,6 +285,12 @@ int build_blob(HostScratch& hs, const ultima_hsamp_batch* b, Built& out) {
                 fl |= RF_FULL;                                                    // top-k off
             }
             if (fl & RF_FULL) out.any_full = true;
+            // plain transform (no penalties, no bias, no top-k): the row's whole-row
+            // passes run over many blocks ahead of k_full
+            if ((fl & RF_FULL) && !(fl & (RF_TOPK | RF_REP | RF_DRY | RF_FP | RF_BIAS))) {
+                fl |= RF_FPRE;
+                out.any_fpre = true;
+            }
             else out.any_topk = out.any_sample = true;
             if (q.top_p < 1.0f && !(q.top_p <= 0.0f)) fl |= RF_TOPP;             // [270, 147]
             if (q.min_p > 0.0f) fl |= RF_MINP;                                    // [273, 168]
@@ -290,9 +308,10 @@ int build_blob(HostScratch& hs, const ultima_hsamp_batch* b, Built& out) {
         // the repetition window and the count window (DRY's, else frequency /
         // presence's) both on and different: a count entry is a count plus a
         // repetition bit
+        // (windows taken on the device vary with the length: any row with both)
         {
             const int64_t cw = dry_w > 0 ? dry_w : fp_w;
-            if (rep_w > 0 && cw > 0 && rep_w != cw) out.two_windows = true;
+            if (rep_w > 0 && cw > 0 && (rep_w != cw || devwin)) out.two_windows = true;
         }
         if (fl & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) {
             out.any_pen = true;
@@ -366,7 +385,7 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     const int kmax = std::max(1, bl.kmax);
     rp.kmax = kmax;
     rp.wb = (b->flags & ULTIMA_HSAMP_WRITEBACK) != 0;
-    bool exact_ok = (bl.any_sample || bl.any_greedy) && !bl.any_full && kmax <= kLimitK && !rp.wb && bl.inv_ok &&
+    bool exact_ok = (bl.any_sample || bl.any_greedy) && !bl.any_full && kmax <= kLimitK && bl.inv_ok &&
                     (!bl.any_pen || (bl.pen_lowers_nb && !bl.dry_split && bl.max_bias <= kBlock && bl.max_scan <= 8 * kBlock));
     exact_ok = exact_ok && !dc.exact_off;
     // 16-byte loads: aligned rows holding at least one whole chunk
@@ -518,6 +537,9 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
         if (rp.lds_ex + statik > dc.lds_limit || pick_lds + statik > dc.lds_limit) exact = false;
         else merge_lds = pick_lds;
     }
+    // write-back after the exact lists: k_writeback rebuilds the rows' penalty
+    // tables in LDS (no merge kernel leaves a global one)
+    if (rp.wb && gtab) exact = false;
     rp.exact = exact;
     rp.merge_lds = merge_lds;
     rp.full_p2 = next_pow2(V);
@@ -528,6 +550,7 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     rp.gtab_words = gtab ? (size_t)B * 2 * mhash : 0;
     rp.full_elems = bl.any_full ? (size_t)B * rp.full_stride : 0;
     rp.fullk_elems = bl.any_full ? (size_t)B * rp.full_p2 : 0;
+    rp.fs_elems = bl.any_fpre ? (size_t)B * FS_TABLES * (size_t)(rp.full_stride / (512 * rp.full_g)) : 0;
     rp.fin_elems = rp.wb ? (size_t)B * kLimitK : 0;
     return ULTIMA_HSAMP_OK;
 }
@@ -590,6 +613,7 @@ int launch_run(const RunPlan& rp, const Built& bl, const ultima_hsamp_batch* b, 
     a.fullv = buf.fullv;
     a.fullp = buf.fullp;
     a.fullk = buf.fullk;
+    a.fs_tab = buf.fs_tab;
     a.full_p2 = rp.full_p2;
     a.full_stride = rp.full_stride;
     a.full_g = rp.full_g;
@@ -622,7 +646,10 @@ int launch_run(const RunPlan& rp, const Built& bl, const ultima_hsamp_batch* b, 
         if (rp.exact && rp.kmax > 64) HIP_TRY(launch_pick_l(a, stream));
         else if (rp.exact) HIP_TRY(launch_pick(a, rp.pick_nw, stream));
         else if (bl.any_topk) HIP_TRY(launch_merge(a, stream));
-        if (bl.any_full) HIP_TRY(launch_full(a, (uint32_t)rp.full_lds, stream));
+        if (bl.any_full) {
+            if (bl.any_fpre) HIP_TRY(launch_full_pre(a, stream));
+            HIP_TRY(launch_full(a, (uint32_t)rp.full_lds, stream));
+        }
         if (rp.wb) HIP_TRY(launch_writeback(a, rp.grid, (uint32_t)rp.wb_lds, stream));
     }
     return ULTIMA_HSAMP_OK;
@@ -833,7 +860,8 @@ int ultima_hsamp_destroy(ultima_hsamp* h) {
         if (s.ev) (void)hipEventDestroy(s.ev);
     }
     for (void* p : {(void*)h->ovf, (void*)h->cand, (void*)h->cand_n,
-                    (void*)h->gtab, (void*)h->fullv, (void*)h->fullp, (void*)h->fullk, (void*)h->fin_idx,
+                    (void*)h->gtab, (void*)h->fullv, (void*)h->fullp, (void*)h->fullk, (void*)h->fs_tab,
+                    (void*)h->fin_idx,
                     (void*)h->fin_n, (void*)h->d_row, (void*)h->d_hist, (void*)h->d_u, (void*)h->d_tok})
         if (p) (void)hipFree(p);
     for (void* p : h->retired) (void)hipFree(p);
@@ -874,6 +902,9 @@ int run_impl(ultima_hsamp* h, const ultima_hsamp_batch* b, const ultima_hsamp_co
     Built bl;
     st = build_blob(h->hs, b, bl);
     if (st != ULTIMA_HSAMP_OK) return st;
+    // a compaction to fewer ids than the longest penalty window would drop ids
+    // the reference's unbounded history still holds in that window
+    if (commit != nullptr && bl.any_pen && commit->keep < bl.max_scan) return ULTIMA_HSAMP_ERR_INVALID;
     RunPlan rp;
     st = plan_run(h->caps, b, bl, rp);
     if (st != ULTIMA_HSAMP_OK) return st;
@@ -889,6 +920,7 @@ int run_impl(ultima_hsamp* h, const ultima_hsamp_batch* b, const ultima_hsamp_co
         st = grow(h, capturing, h->fullv, h->fullv_elems, rp.full_elems);
         if (st == ULTIMA_HSAMP_OK) st = grow(h, capturing, h->fullp, h->fullp_elems, rp.full_elems);
         if (st == ULTIMA_HSAMP_OK) st = grow(h, capturing, h->fullk, h->fullk_elems, rp.fullk_elems);
+        if (st == ULTIMA_HSAMP_OK && rp.fs_elems) st = grow(h, capturing, h->fs_tab, h->fs_elems, rp.fs_elems);
     }
     if (st != ULTIMA_HSAMP_OK) return st;
 
@@ -906,6 +938,7 @@ int run_impl(ultima_hsamp* h, const ultima_hsamp_batch* b, const ultima_hsamp_co
     buf.fullv = h->fullv;
     buf.fullp = h->fullp;
     buf.fullk = h->fullk;
+    buf.fs_tab = h->fs_tab;
     buf.fin_idx = h->fin_idx;
     buf.fin_n = h->fin_n;
     buf.blob = slot->dev;
@@ -916,6 +949,25 @@ int run_impl(ultima_hsamp* h, const ultima_hsamp_batch* b, const ultima_hsamp_co
     return ULTIMA_HSAMP_OK;
 }
 }  // namespace
+
+int ultima_hsamp_query_kernels(ultima_hsamp* h, const ultima_hsamp_batch* b, uint32_t* kernels) {
+    if (h == nullptr || kernels == nullptr) return ULTIMA_HSAMP_ERR_INVALID;
+    int st = validate_batch(b, h->max_rows, h->max_vocab);
+    if (st != ULTIMA_HSAMP_OK) return st;
+    Built bl;
+    st = build_blob(h->hs, b, bl);
+    if (st != ULTIMA_HSAMP_OK) return st;
+    RunPlan rp;
+    st = plan_run(h->caps, b, bl, rp);
+    if (st != ULTIMA_HSAMP_OK) return st;
+    uint32_t k = 0;
+    if (rp.exact) k |= ULTIMA_HSAMP_KERNELS_EXACT;
+    else if (bl.any_topk) k |= ULTIMA_HSAMP_KERNELS_GENERAL;
+    if (bl.any_full) k |= ULTIMA_HSAMP_KERNELS_FULL;
+    if (rp.wb) k |= ULTIMA_HSAMP_KERNELS_WRITEBACK;
+    *kernels = k;
+    return ULTIMA_HSAMP_OK;
+}
 
 int ultima_hsamp_read_probe(ultima_hsamp* h, const ultima_hsamp_batch* b, float* out, void* hip_stream) {
     if (h == nullptr || out == nullptr) return ULTIMA_HSAMP_ERR_INVALID;

@@ -472,12 +472,21 @@ __global__ __launch_bounds__(64 * NWB) void k_head_q(const unsigned char* __rest
     }
     uint4 reg[NV_T];
     uint4 xv[NX];
+    // Only the granules of the row's span are asked for (an offset past the
+    // resource's range makes the rest read 0 without touching memory), and
+    // the loads keep the default cache policy: a chunk's span shares its
+    // first and last 128-byte lines with the chunks before and after it,
+    // which then find them in L2.
     auto load = [&](int c) {
+        const uint32_t nbytes = (uint32_t)(min(F::BPC, nb - c * F::BPC) * F::BB);
 #pragma unroll
         for (int i = 0; i < NV_T; ++i) {
-            const uint32_t o = ((rofs[i] + (uint32_t)(c * CB)) & ~15u) + 16u * (uint32_t)vseg[i];
+            const uint32_t a0 = rofs[i] + (uint32_t)(c * CB);
+            const uint32_t lo = a0 & ~15u, end = a0 + nbytes;
+            uint32_t o = lo + 16u * (uint32_t)vseg[i];
+            o = o < end ? o : 0xFFFFFFF0u;
             typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-            const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(wr, o, 0, 2);
+            const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(wr, o, 0, 0);
             reg[i] = make_uint4(t.x, t.y, t.z, t.w);
         }
 #pragma unroll

@@ -70,14 +70,29 @@ __device__ __forceinline__ u64 comp(uint32_t key, int32_t idx) {
 }
 __device__ __forceinline__ int32_t comp_idx(u64 c) { return (int32_t)(~(uint32_t)c); }
 
-// Ids in row r's history: the plan's count, or the row's device length when
-// the batch carries one (a device-side history that grows and compacts on the
-// GPU; the plan's windows stay valid while it holds at least the longest of
-// them: kept within [scan_len, hist_stride], so that reads stay in the row).
-__device__ __forceinline__ int hist_len_of(const StreamArgs& a, const RowPlan& P, int r) {
-    if (a.hist_len_dev == nullptr) return P.hist_len;
-    return min(max(a.hist_len_dev[r], P.scan_len), (int)a.hist_stride);
+// Row r's plan. A row whose history length is read on the device (a history
+// kept on the GPU, grown and compacted there: RF_DEVWIN) takes its windows
+// from that length, as window_slice does (sampler.cpp:19-24): each stage's
+// window is min(cap, length), DRY's only when it holds two ids or more
+// (sampler.cpp:69), so that one plan serves every step from the first token
+// on.
+__device__ __forceinline__ RowPlan plan_of(const StreamArgs& a, int r) {
+    RowPlan P = a.plans[r];
+    if (P.flags & RF_DEVWIN) {
+        const int L = min(max(a.hist_len_dev[r], 0), (int)a.hist_stride);
+        const int rc = (int)(P.win_caps[0] & 0xFFFFu), dc = (int)(P.win_caps[0] >> 16);
+        const int fc = (int)(P.win_caps[1] & 0xFFFFu);
+        P.hist_len = L;
+        P.rep_win = min(rc, L);
+        P.dry_win = min(dc, L) >= 2 ? min(dc, L) : 0;
+        P.fp_win = min(fc, L);
+        P.scan_len = max(max(P.rep_win, P.dry_win), P.fp_win);
+    }
+    return P;
 }
+
+// Ids in row r's history (its plan from plan_of).
+__device__ __forceinline__ int hist_len_of(const StreamArgs&, const RowPlan& P, int) { return P.hist_len; }
 
 struct Shared {
     u64 theta;          // current survival threshold (composite)
@@ -2354,7 +2369,7 @@ __global__ __launch_bounds__(kBlock, EX >= 2 ? 4 : 5) void k_stream(StreamArgs a
             // longer history rows: the window's place comes from the plan,
             // which then goes first (the tile waits one round trip); the
             // window still goes out ahead of the tile, as the short rows do
-            P = a.plans[r];
+            P = plan_of(a, r);
             const int L = hist_len_of(a, P, r), p0 = L - P.scan_len;
             const int32_t* hrow = a.hist + (int64_t)r * a.hist_stride;
 #pragma unroll
@@ -2378,7 +2393,7 @@ __global__ __launch_bounds__(kBlock, EX >= 2 ? 4 : 5) void k_stream(StreamArgs a
     }
     if (early) load_tile<DT, VEC, NC>(rs, lo, raw);
     if (EX) __builtin_amdgcn_sched_barrier(0);
-    if (!(EX && PEN) || hd) P = a.plans[r];
+    if (!(EX && PEN) || hd) P = plan_of(a, r);
     if (!early) {
         if (P.flags & RF_FULL) return;                     // k_full's row
         if (((P.flags & RF_GREEDY) != 0) != GR) return;    // the other kernel's row
@@ -3234,7 +3249,7 @@ __global__ __launch_bounds__(kBlock, 3) void k_merge(StreamArgs a) {
     RowPlan P;
     int32_t pre[8];
     if (hist_first) {
-        P = a.plans[r];
+        P = plan_of(a, r);
         if (P.flags & RF_FULL) return;   // k_full's row
         // branch-free: clamped positions, used only below hist_len
 #pragma unroll
@@ -3288,7 +3303,7 @@ __global__ __launch_bounds__(kBlock, 3) void k_merge(StreamArgs a) {
         }
     }
     if (!hist_first) {
-        P = a.plans[r];
+        P = plan_of(a, r);
         if (P.flags & RF_FULL) return;   // k_full's row
     }
     const bool greedy = (P.flags & RF_GREEDY) != 0;
@@ -3565,7 +3580,7 @@ __global__ __launch_bounds__(kBlock) void k_pick(StreamArgs a) {
     // the plan and u after the lists (scalar loads: a wait for them placed
     // ahead of the lists' loads would delay those by a memory round trip)
     __builtin_amdgcn_sched_barrier(0);
-    const RowPlan P = a.plans[r];
+    const RowPlan P = plan_of(a, r);
     const double ur = a.u[r];
     // expf's table, loaded after the lists (its wait then costs nothing) and
     // put in LDS once they are in
@@ -3970,7 +3985,7 @@ __global__ __launch_bounds__(kBlock, 4) void k_pick_l(StreamArgs a) {
     HSAMP_PHASE(9500 + r, 0);
     const u64* cand = a.cand + (int64_t)r * S * a.cand_cap;
     const int cnt_raw = (tid < S) ? a.cand_n[(int64_t)r * S + tid] : 0;
-    const RowPlan P = a.plans[r];
+    const RowPlan P = plan_of(a, r);
     const double ur = a.u[r];
     const float inv_t = P.inv_temp;
     if (tid == 0) {
@@ -4051,7 +4066,7 @@ __global__ __launch_bounds__(kBlock) void k_writeback(StreamArgs a) {
     const int logical = (int)(blockIdx.x % kXcds) * a.blocks_per_xcd + (int)(blockIdx.x / kXcds);
     const int r = div_slices(logical, a), s = logical - r * a.nslices;
     if (r >= a.rows) return;
-    const RowPlan P = a.plans[r];
+    const RowPlan P = plan_of(a, r);
     if (P.flags & RF_FULL) return;   // k_full writes its rows back itself
     if (tid == 0) {
         sa = a;
@@ -4130,6 +4145,152 @@ __device__ void full_exp(const float* fv, float* pv, float m, int nW, int G, Ful
     __syncthreads();
 }
 
+// ---- full-vocabulary rows, their whole-row passes over many blocks ------------------
+// k_full runs one block per row; a row of the batch has V ids. For its rows
+// with a plain transform (RF_FPRE: mask and temperature, no penalties, no
+// logit bias, no top-k), the passes over the whole row that need no
+// sequential order run first over B x nW waves, one index-order window
+// (512 G ids) per wave, in the layout k_full uses (fullv / fullp, windows of
+// full_stride), and leave per-window tables (FS_*) for it:
+//   k_fs_max: the transform into fullv (the row's -inf padding included),
+//             each window's maximum and whether it held a NaN;
+//   k_fs_exp: the row's maximum m, the numerators expf(x - m) into fullp and
+//             each window's approximate sum (as full_exp forms it);
+//   k_fs_int: each window's binade, predicted from the approximate sums
+//             before it, and its values' integer increments there (as
+//             exact_index_sum forms them).
+// k_full then composes the exact sum from the tables and goes on as for its
+// other rows. Every value is computed as k_full computes it, in the same
+// order where order matters.
+__device__ __forceinline__ int fs_windows(const StreamArgs& a) { return a.full_stride / (kFWin * a.full_g); }
+__device__ __forceinline__ uint32_t* fs_table(const StreamArgs& a, int r, int k) {
+    const int nW = fs_windows(a);
+    return a.fs_tab + ((size_t)r * FS_TABLES + k) * (size_t)nW;
+}
+
+template <int DT>
+__global__ __launch_bounds__(64) void k_fs_max(StreamArgs a) {
+    const int nW = fs_windows(a);
+    const int r = (int)blockIdx.x / nW, w = (int)blockIdx.x - r * nW;
+    if (r >= a.rows) return;
+    const RowPlan P = plan_of(a, r);
+    if (!(P.flags & RF_FPRE)) return;
+    const int lane = (int)threadIdx.x, V = a.vocab, G = a.full_g, WS = kFWin * G;
+    float* fv = a.fullv + (size_t)r * a.full_stride;
+    const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * (DT == 0 ? 4 : 2);
+    const uint32_t* mrow = (P.flags & RF_MASK) ? a.mask + (int64_t)r * a.mask_stride : nullptr;
+    float mloc = -__builtin_inff();
+    bool nanv = false;
+    for (int g = 0; g < G; ++g) {
+        const int i0 = w * WS + g * kFWin + lane * 8;
+        float x[8];
+        uint32_t mw = 0xFFFFFFFFu;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = load_logit<DT>(rowp, min(i0 + j, V - 1));
+        if (mrow != nullptr) mw = mrow[min(i0, V - 1) >> 5];   // (eight ids share one mask word)
+        float y[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = i0 + j;
+            float v = -__builtin_inff();
+            if (i < V) {
+                v = x[j];
+                if (!((mw >> (i & 31)) & 1u)) v = -__builtin_inff();
+                v = v * P.inv_temp;
+                if (v != v) {
+                    nanv = true;
+                    v = -__builtin_inff();
+                }
+            }
+            y[j] = v;
+            mloc = fmaxf(mloc, v);
+        }
+        float4* dst = reinterpret_cast<float4*>(fv + i0);
+        dst[0] = make_float4(y[0], y[1], y[2], y[3]);
+        dst[1] = make_float4(y[4], y[5], y[6], y[7]);
+    }
+    mloc = wave_max_f(mloc);
+    const bool anynan = __ballot(nanv) != 0ull;
+    if (lane == 0) {
+        fs_table(a, r, FS_MAX)[w] = __float_as_uint(mloc);
+        fs_table(a, r, FS_NAN)[w] = anynan ? 1u : 0u;
+    }
+}
+
+__global__ __launch_bounds__(64) void k_fs_exp(StreamArgs a) {
+    __shared__ uint64_t expT[32];
+    const int nW = fs_windows(a);
+    const int r = (int)blockIdx.x / nW, w = (int)blockIdx.x - r * nW;
+    if (r >= a.rows) return;
+    const RowPlan P = plan_of(a, r);
+    if (!(P.flags & RF_FPRE)) return;
+    const int lane = (int)threadIdx.x, G = a.full_g, WS = kFWin * G;
+    if (lane < 32) expT[lane] = kExpT[lane];
+    // the row's maximum over the window maxima
+    const uint32_t* wm = fs_table(a, r, FS_MAX);
+    float m = -__builtin_inff();
+    for (int k = lane; k < nW; k += 64) m = fmaxf(m, __uint_as_float(wm[k]));
+    m = wave_max_f(m);
+    __syncthreads();
+    const float* fv = a.fullv + (size_t)r * a.full_stride;
+    float* pv = a.fullp + (size_t)r * a.full_stride;
+    float ws = 0.0f;
+    for (int g = 0; g < G; ++g) {
+        const int i0 = w * WS + g * kFWin + lane * 8;
+        const float4 c0 = reinterpret_cast<const float4*>(fv + i0)[0], c1 = reinterpret_cast<const float4*>(fv + i0)[1];
+        const float x[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            v[j] = (x[j] == -__builtin_inff() || m == -__builtin_inff()) ? 0.0f : libm_expf_t(x[j] - m, expT);
+            ws += v[j];
+        }
+        float4* dst = reinterpret_cast<float4*>(pv + i0);
+        dst[0] = make_float4(v[0], v[1], v[2], v[3]);
+        dst[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    ws = wave_tree_prefix_f(ws);
+    if (lane == 63) fs_table(a, r, FS_A)[w] = __float_as_uint(ws);
+}
+
+__global__ __launch_bounds__(64) void k_fs_int(StreamArgs a) {
+    const int nW = fs_windows(a);
+    const int r = (int)blockIdx.x / nW, w = (int)blockIdx.x - r * nW;
+    if (r >= a.rows) return;
+    const RowPlan P = plan_of(a, r);
+    if (!(P.flags & RF_FPRE)) return;
+    const int lane = (int)threadIdx.x, G = a.full_g, WS = kFWin * G;
+    // the window's binade: predicted from the approximate sum before it
+    const uint32_t* wa = fs_table(a, r, FS_A);
+    float pre = 0.0f;
+    for (int k = lane; k < w; k += 64) pre += __uint_as_float(wa[k]);
+    pre = readlane_f(wave_tree_prefix_f(pre), 63);
+    const int E = w == 0 ? -126 : xs_binade(pre);
+    const float* pv = a.fullp + (size_t)r * a.full_stride;
+    XPair wp{0u, 0u};
+    bool nz = false;
+    for (int g = 0; g < G; ++g) {
+        const int i0 = w * WS + g * kFWin + lane * 8;
+        const float4 c0 = reinterpret_cast<const float4*>(pv + i0)[0], c1 = reinterpret_cast<const float4*>(pv + i0)[1];
+        const float v[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        XPair lp{0u, 0u};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            lp = xcomp(lp, xinc2(v[j], E));
+            nz |= v[j] != 0.0f;
+        }
+        const XPair sp = wave_scan_pair(lp);
+        wp = xcomp(wp, XPair{(uint32_t)__builtin_amdgcn_readlane((int)sp.d0, 63),
+                             (uint32_t)__builtin_amdgcn_readlane((int)sp.d1, 63)});
+    }
+    const bool empty = __ballot(nz) == 0ull;
+    if (lane == 0) {
+        fs_table(a, r, FS_D0)[w] = wp.d0;
+        fs_table(a, r, FS_D1)[w] = wp.d1;
+        fs_table(a, r, FS_EF)[w] = gpack(E, empty ? kGEmpty : 0u);
+    }
+}
+
 // Full-vocabulary rows, one block of kFT threads per row.
 template <bool GT>
 __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
@@ -4138,7 +4299,7 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
     const int tid = threadIdx.x, lane = lane_id(), wid = wave_id();
     const int r = (int)blockIdx.x;
     if (r >= a.rows) return;
-    const RowPlan P = a.plans[r];
+    const RowPlan P = plan_of(a, r);
     if (!(P.flags & RF_FULL)) return;
     HSAMP_PHASE(12000 + r, 0);
     const int V = a.vocab, G = a.full_g;
@@ -4227,7 +4388,17 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
     using I1 = std::integral_constant<int, 1>;
     using BT = std::integral_constant<bool, true>;
     using BF = std::integral_constant<bool, false>;
-    if (a.dtype == 0) {
+    const bool pre = (P.flags & RF_FPRE) != 0;
+    if (pre) {
+        // k_fs_max transformed the row: its window maxima and NaN flags
+        const int nWp = fs_windows(a);
+        const uint32_t* wm = fs_table(a, r, FS_MAX);
+        const uint32_t* wn = fs_table(a, r, FS_NAN);
+        for (int k = tid; k < nWp; k += kFT) {
+            mloc = fmaxf(mloc, __uint_as_float(wm[k]));
+            nanv |= wn[k] != 0u;
+        }
+    } else if (a.dtype == 0) {
         if (masked) transform(I0{}, BT{});
         else transform(I0{}, BF{});
     } else {
@@ -4310,9 +4481,23 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
     int32_t tok = 0;
     if (m != -__builtin_inff()) {
         // ---- softmax numerators and their exact index-order sum (sampler.cpp:124-142) ----
-        full_exp(fv, pv, m, nW, G, f, st);
-        HSAMP_PHASE(12000 + r, 4);
-        float S = xs_value(exact_index_sum(pv, nW, G, f, st));
+        float S;
+        if (pre) {
+            // k_fs_exp / k_fs_int left the numerators and the windows' tables
+            for (int k = tid; k < nW; k += kFT) {
+                f.winA[k] = __uint_as_float(fs_table(a, r, FS_A)[k]);
+                f.winEF[k] = fs_table(a, r, FS_EF)[k];
+                f.winD0[k] = fs_table(a, r, FS_D0)[k];
+                f.winD1[k] = fs_table(a, r, FS_D1)[k];
+            }
+            __syncthreads();
+            HSAMP_PHASE(12000 + r, 4);
+            S = xs_value(exact_index_compose(pv, nW, G, f, st));
+        } else {
+            full_exp(fv, pv, m, nW, G, f, st);
+            HSAMP_PHASE(12000 + r, 4);
+            S = xs_value(exact_index_sum(pv, nW, G, f, st));
+        }
         HSAMP_PHASE(12000 + r, 5);
         bool changed = false;   // a stage removed ids since S was taken
 
@@ -4799,6 +4984,16 @@ hipError_t launch_merge(const StreamArgs& a, hipStream_t stream) {
     else if (a.fast) hipLaunchKernelGGL((k_merge<false, true, false>), g, dim3(kBlock), a.merge_lds, stream, a);
     else if (a.gtab != nullptr) hipLaunchKernelGGL((k_merge<true, false, false>), g, dim3(kBlock), a.merge_lds, stream, a);
     else hipLaunchKernelGGL((k_merge<false, false, false>), g, dim3(kBlock), a.merge_lds, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_full_pre(const StreamArgs& a, hipStream_t stream) {
+    const int nW = a.full_stride / (kFWin * a.full_g);
+    const dim3 g((unsigned)((int64_t)a.rows * nW)), b(64);
+    if (a.dtype == 0) hipLaunchKernelGGL((k_fs_max<0>), g, b, 0, stream, a);
+    else hipLaunchKernelGGL((k_fs_max<1>), g, b, 0, stream, a);
+    hipLaunchKernelGGL(k_fs_exp, g, b, 0, stream, a);
+    hipLaunchKernelGGL(k_fs_int, g, b, 0, stream, a);
     return hipGetLastError();
 }
 

@@ -163,6 +163,7 @@ extern "C" int ultima_hsamp_run_noalloc(const ultima_hsamp_batch* b, void* hip_s
         buf.fullp = reinterpret_cast<float*>(take(rp.full_elems * 4));
         buf.fullk = reinterpret_cast<uint32_t*>(take(rp.fullk_elems * 4));
     }
+    if (rp.fs_elems) buf.fs_tab = reinterpret_cast<uint32_t*>(take(rp.fs_elems * 4));
     if (rp.fin_elems) {
         buf.fin_idx = reinterpret_cast<int32_t*>(take(rp.fin_elems * 4));
         buf.fin_n = reinterpret_cast<int32_t*>(take((size_t)rp.B * 4));

@@ -31,7 +31,16 @@ enum : uint32_t {
     RF_BIAS = 1u << 9,    // logit bias entries present                     [30]
     RF_SINGLE = 1u << 10, // V == 1: one id, top-k off, no uniform drawn   [110, random.tcc:2660]
     RF_FULL = 1u << 11,   // sampling row over the whole vocabulary: top-k off or above kLimitK (k_full)
+    RF_DEVWIN = 1u << 12, // the row's history length is read on the device: the windows are taken
+                          // there, min(cap, length), from the caps in RowPlan::win_caps
+    RF_FPRE = 1u << 13,   // a k_full row with a plain transform (no penalties, no logit bias, no
+                          // top-k): its whole-row passes run over many blocks first (k_fs_*)
 };
+
+// k_fs_* per-row tables, nW entries each (nW = full_stride / (512 * full_g)):
+// window maxima, NaN seen, approximate window sums of the numerators, and the
+// windows' predicted binades / integer increments for the exact sum.
+enum : int { FS_MAX = 0, FS_NAN = 1, FS_A = 2, FS_EF = 3, FS_D0 = 4, FS_D1 = 5, FS_TABLES = 6 };
 
 // Hash-table value bits for one token of a slice (penalty bookkeeping).
 enum : uint32_t {
@@ -69,7 +78,9 @@ struct alignas(16) RowPlan {
     int32_t bias_cnt;
     uint32_t flags;
     float temp;         // T (sampling rows): a first guess when inverting the temperature
-    uint32_t pad_[2];
+    // RF_DEVWIN: the windows' caps (0: the stage is off): repetition | DRY << 16,
+    // then frequency/presence; the window fields above hold the caps too
+    uint32_t win_caps[2];
 };
 static_assert(sizeof(RowPlan) == 80, "RowPlan layout");
 
@@ -135,6 +146,7 @@ struct StreamArgs {
     int32_t full_p2;            // next power of two >= vocab
     int32_t full_stride;        // k_full: floats per row of fullv / fullp (whole windows of 512 * full_g)
     int32_t full_g;             // k_full: 512-id steps per index-order window
+    uint32_t* fs_tab;           // [rows * FS_TABLES * nW] k_fs_* results for k_full's RF_FPRE rows
     uint32_t* gtab;             // [rows * 2 * mhash_slots] penalty tables, or NULL: tables in LDS
     uint32_t merge_lds;         // dynamic LDS of k_merge
     uint32_t lds_bytes;         // dynamic LDS size of the launch

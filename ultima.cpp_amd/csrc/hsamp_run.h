@@ -60,6 +60,7 @@ struct Built {
     bool any_sample = false;   // a top-k sampling row (k_stream's sampling kernel)
     bool dry_split = false;    // a row whose DRY and frequency/presence windows differ
     bool two_windows = false;  // a row whose repetition and count windows are both on and differ
+    bool any_fpre = false;     // a k_full row with a plain transform (RF_FPRE)
 };
 
 // Kernel choice, slicing, LDS sizes and scratch sizes (in elements) of one run.
@@ -78,6 +79,7 @@ struct RunPlan {
     size_t full_elems = 0;    // f32 fullv and fullp, B * V each (k_full rows)
     size_t fullk_elems = 0;   // uint32 k_full sort scratch
     size_t fin_elems = 0;     // int32 kept ids for write-back, B * kLimitK (and B counts)
+    size_t fs_elems = 0;      // uint32 k_fs_* per-window tables, B * FS_TABLES * windows
 };
 
 // Device scratch of one run.
@@ -90,6 +92,7 @@ struct RunBuffers {
     float* fullv = nullptr;
     float* fullp = nullptr;
     uint32_t* fullk = nullptr;
+    uint32_t* fs_tab = nullptr;
     int32_t* fin_idx = nullptr;
     int32_t* fin_n = nullptr;
     const char* blob = nullptr;   // device copy of HostScratch::blob

@@ -525,9 +525,10 @@ __device__ __forceinline__ float fblock_excl_scan_f(float v, float* total, FullS
 // binades from the approximate prefixes, the windows' pairs at them, then one
 // wave composes (replaying the windows where the prediction fails or the
 // sum leaves its binade).
+__device__ XState exact_index_compose(const float* x, int nW, int G, FullLds f, FullShared& st);
+
 __device__ XState exact_index_sum(const float* x, int nW, int G, FullLds f, FullShared& st) {
-    const int tid = threadIdx.x, lane = lane_id(), wid = wave_id();
-    const int WS = kFWin * G;
+    const int tid = threadIdx.x, lane = lane_id();
     {
         // two windows per thread: their approximate start values -> binades
         const int w0 = 2 * tid;
@@ -565,6 +566,16 @@ __device__ XState exact_index_sum(const float* x, int nW, int G, FullLds f, Full
         });
     }
     __syncthreads();
+    return exact_index_compose(x, nW, G, f, st);
+}
+
+// The exact sum from the windows' tables in LDS (f.winEF / winD0 / winD1:
+// each window's predicted binade and its integer increments there): one wave
+// composes them in index order, replaying value by value the windows where
+// the prediction fails, the sum leaves its binade or a half-way value occurs.
+__device__ XState exact_index_compose(const float* x, int nW, int G, FullLds f, FullShared& st) {
+    const int lane = lane_id(), wid = wave_id();
+    const int WS = kFWin * G;
     if (wid == 0) {
         XState s{-126, 0u};
         xs_compose(nW, f.winEF, f.winD0, f.winD1, false, 0.0f, s, [&](int w, XState& sv) -> bool {

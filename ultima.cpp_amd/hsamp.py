@@ -21,6 +21,7 @@ OK, ERR_INVALID, ERR_HIP, ERR_UNSUPPORTED, ERR_NOMEM, ERR_CAPACITY, ERR_NO_DEVIC
 F32, BF16 = 0, 1
 WRITEBACK, STREAM_ONLY = 1, 0x100
 NOALLOC_SCRATCH_BYTES, NOALLOC_PLAN_BYTES = 96 << 20, 2 << 20
+KERNELS_EXACT, KERNELS_GENERAL, KERNELS_FULL, KERNELS_WRITEBACK = 1, 2, 4, 8
 ROW_GREEDY, ROW_U_USED, ROW_CDF_NEAR, ROW_NAN, ROW_UNIFORM, ROW_TOPP_NEAR, ROW_REREAD = 1, 2, 4, 8, 16, 32, 64
 
 PARAM_KEYS = ("rep_penalty", "dry_multiplier", "dry_base", "frequency_penalty", "presence_penalty",
@@ -178,6 +179,8 @@ def lib() -> ctypes.CDLL:
         L.ultima_hsamp_status_str.argtypes = [ctypes.c_int]
         L.ultima_hsamp_version.restype = ctypes.c_int
         L.ultima_hsamp_version.argtypes = []
+        L.ultima_hsamp_query_kernels.restype = ctypes.c_int
+        L.ultima_hsamp_query_kernels.argtypes = [vp, ctypes.POINTER(Batch), ctypes.POINTER(ctypes.c_uint32)]
         L.ultima_hsamp_read_probe.restype = ctypes.c_int
         L.ultima_hsamp_read_probe.argtypes = [vp, ctypes.POINTER(Batch), vp, vp]
         L.ultima_hsamp_set_phase_event.restype = ctypes.c_int
@@ -450,6 +453,17 @@ class Sampler:
         check(lib().ultima_hsamp_read_probe(self.h, ctypes.byref(b), ctypes.c_void_p(out.data_ptr()),
                                             ctypes.c_void_p(s.cuda_stream)), "read_probe")
         del keep, torch
+
+    def query_kernels(self, logits, params, u, hist=None, hist_len=None, mask=None, bias=None,
+                      writeback=False) -> int:
+        """ultima_hsamp_query_kernels: the KERNELS_* bits of the kernels run()
+        would launch for this batch (nothing is launched)."""
+        b, _, keep, _s = _batch(logits, params, u, hist, hist_len, mask, bias, writeback, False, None, None,
+                                None, False)
+        k = ctypes.c_uint32(0)
+        check(lib().ultima_hsamp_query_kernels(self.h, ctypes.byref(b), ctypes.byref(k)), "query_kernels")
+        del keep
+        return int(k.value)
 
     def set_phase_event(self, event):
         """Record `event` (a torch.cuda.Event already recorded once, or None)

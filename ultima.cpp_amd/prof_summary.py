@@ -58,7 +58,8 @@ def counter(folder: Path) -> dict[str, list[float]]:
 
 def main() -> None:
     ap = argparse.ArgumentParser()
-    ap.add_argument("--config", required=True, help="1-5 (a sampler configuration) or head")
+    ap.add_argument("--config", required=True,
+                    help="1-5 (a sampler configuration), head (the bf16 head) or head_<type> (bench.py --head-dtype)")
     ap.add_argument("--stats", type=Path, required=True)
     ap.add_argument("--fetch", type=Path, required=True)
     ap.add_argument("--write", type=Path, required=True)
@@ -86,8 +87,9 @@ def main() -> None:
         hbm = None if f is None or w is None else (f * fs + w * ws) * 1024.0
         table.append((short(name), int(r["Calls"]), float(r["AverageNs"]) / 1000.0, f, w, hbm))
 
-    tag = a.config if a.config == "head" else f"cfg{int(a.config)}"
-    sk = STREAM_KERNEL[tag]
+    tag = a.config if a.config.startswith("head") else f"cfg{int(a.config)}"
+    # head_<type>: a quantised head (k_head_q) or a dense one (k_head_gemv)
+    sk = STREAM_KERNEL.get(tag, "k_head_gemv" if tag in ("head_f32", "head_bf16") else "k_head_q")
     main_row = next((t for t in table if t[0].startswith(sk + "<") and t[5] is not None), None)
     wl = bench["config"]["workload"]
     lines = [f"# rocprofv3 profile, workload {wl}", ""]
@@ -105,7 +107,7 @@ def main() -> None:
         lines.append(f"| `{n}` | {c} | {us:.2f} | {'' if f is None else f'{f:.1f}'} | "
                      f"{'' if w is None else f'{w:.1f}'} | {'' if hbm is None else f'{hbm:.0f}'} | {ratio} |")
     what = ("the head's weights, the hidden states, the norm scale, the normed rows and the logits, "
-            "each once" if tag == "head" else "each logit, history id and mask word read once, u and the token")
+            "each once" if tag.startswith("head") else "each logit, history id and mask word read once, u and the token")
     lines += ["", f"Algorithmic bytes per step: {algo} ({what}).", ""]
     lines += ["Bench line of the stats run (timings perturbed by the tracer):", "",
               "    " + json.dumps({k: bench[k] for k in ("value", "ms_per_step")} |

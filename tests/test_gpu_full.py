@@ -136,3 +136,28 @@ def test_cli_row_with_nan_logits_is_flagged(hs, sampler, wl):
     gm = run_gpu(sampler, wm, set_cap=V)
     assert int(g["token"][0]) == int(gm["token"][0])
     assert int(g["kept_count"][0]) == int(gm["kept_count"][0]) == V - 152
+
+
+@pytest.mark.parametrize("V", [32000, 151936, 262144])
+def test_plain_transform_rows_exact_sums(hs, sampler, wl, V):
+    """Rows that take the whole-row passes over many blocks (plain transform:
+    temperature and mask only) with sums that leave their binade in different
+    places: flat rows (the sum doubles window after window), wide rows (a few
+    ids carry it), a constant row (the sum lands on powers of two exactly at
+    window ends), rows with long masked-out ranges (empty windows) and a row
+    of one allowed id per 4096. The kept probabilities are e * fl(1/S) for
+    every id, so they pin the exact index-order sum S bit for bit."""
+    rows = 6
+    sig = [0.3, 2.0, 8.0, 0.0, 1.0, 3.0]
+    x = wl._rows_normal(77, rows, V, sig)
+    x[3] = 0.5                                  # constant row
+    temps = [1.0, 0.8, 1.7, 1.0, 0.6, 1.1]
+    params = [wl.identity_params(temperature=t) for t in temps]
+    mask = np.full((rows, (V + 31) // 32), 0xFFFFFFFF, np.uint32)
+    lo, hi = V // 10 // 32, V // 2 // 32
+    mask[4, lo:hi] = 0                          # a long masked-out range
+    mask[5, :] = 0
+    mask[5, ::128] = 1                          # one id per 4096
+    w = wl.Workload("full", "f32", x, params, wl.uniform53(78, rows), None, None, mask)
+    g = run_gpu(sampler, w, set_cap=V)
+    assert compare_rows(w, g) == rows

@@ -26,7 +26,7 @@ namespace hsamp {
 hipError_t launch_stream(const StreamArgs& a, int dtype, bool vec, bool pen_greedy, bool pen_sample, bool mask,
                          bool greedy_rows, bool sample_rows, int grid, hipStream_t stream);
 hipError_t launch_writeback(const StreamArgs& a, int grid, uint32_t lds, hipStream_t stream);
-hipError_t launch_full_pre(const StreamArgs& a, hipStream_t stream);
+hipError_t launch_full_pre(const StreamArgs& a, bool plain, bool tp, hipStream_t stream);
 hipError_t launch_merge(const StreamArgs& a, hipStream_t stream);
 hipError_t launch_pick_l(const StreamArgs& a, hipStream_t stream);
 hipError_t launch_stream_ex(const StreamArgs& a, int dtype, bool vec, bool pen, bool mask, int tiles, bool lean, int grid,
@@ -292,8 +292,13 @@ int build_blob(HostScratch& hs, const ultima_hsamp_batch* b, Built& out) {
                 out.any_fpre = true;
             }
             else out.any_topk = out.any_sample = true;
+            if ((fl & RF_FULL) && !(fl & RF_FPRE)) out.any_full_gen = true;
             if (q.top_p < 1.0f && !(q.top_p <= 0.0f)) fl |= RF_TOPP;             // [270, 147]
             if (q.min_p > 0.0f) fl |= RF_MINP;                                    // [273, 168]
+            if (fl & RF_FPRE) {
+                if (fl & (RF_TOPP | RF_MINP)) out.any_fpre_tp = true;
+                else out.any_fpre_plain = true;
+            }
             P.top_p = q.top_p;
             P.min_p = q.min_p;
             if (!(fl & RF_FULL)) out.kmax = std::max(out.kmax, P.top_k);
@@ -550,7 +555,11 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     rp.gtab_words = gtab ? (size_t)B * 2 * mhash : 0;
     rp.full_elems = bl.any_full ? (size_t)B * rp.full_stride : 0;
     rp.fullk_elems = bl.any_full ? (size_t)B * rp.full_p2 : 0;
-    rp.fs_elems = bl.any_fpre ? (size_t)B * FS_TABLES * (size_t)(rp.full_stride / (512 * rp.full_g)) : 0;
+    {
+        // per-window tables of every row, then (16-byte aligned) 64 lane entries of 4 words per window
+        const size_t nWf = (size_t)(rp.full_stride / (512 * rp.full_g));
+        rp.fs_elems = bl.any_fpre ? (((size_t)B * FS_TABLES * nWf + 3) & ~(size_t)3) + (size_t)B * nWf * 256 : 0;
+    }
     rp.fin_elems = rp.wb ? (size_t)B * kLimitK : 0;
     return ULTIMA_HSAMP_OK;
 }
@@ -647,8 +656,8 @@ int launch_run(const RunPlan& rp, const Built& bl, const ultima_hsamp_batch* b, 
         else if (rp.exact) HIP_TRY(launch_pick(a, rp.pick_nw, stream));
         else if (bl.any_topk) HIP_TRY(launch_merge(a, stream));
         if (bl.any_full) {
-            if (bl.any_fpre) HIP_TRY(launch_full_pre(a, stream));
-            HIP_TRY(launch_full(a, (uint32_t)rp.full_lds, stream));
+            if (bl.any_fpre) HIP_TRY(launch_full_pre(a, bl.any_fpre_plain, bl.any_fpre_tp, stream));
+            if (bl.any_full_gen) HIP_TRY(launch_full(a, (uint32_t)rp.full_lds, stream));
         }
         if (rp.wb) HIP_TRY(launch_writeback(a, rp.grid, (uint32_t)rp.wb_lds, stream));
     }

@@ -4153,9 +4153,12 @@ __device__ void full_exp(const float* fv, float* pv, float m, int nW, int G, Ful
 // (512 G ids) per wave, in the layout k_full uses (fullv / fullp, windows of
 // full_stride), and leave per-window tables (FS_*) for it:
 //   k_fs_max: the transform into fullv (the row's -inf padding included),
-//             each window's maximum and whether it held a NaN;
+//             each window's maximum, whether it held a NaN and how many ids
+//             it leaves in;
 //   k_fs_exp: the row's maximum m, the numerators expf(x - m) into fullp and
-//             each window's approximate sum (as full_exp forms it);
+//             each window's approximate sum (as full_exp forms it) and its
+//             sum in double (the draw's window prefixes when top-p and min-p
+//             remove nothing);
 //   k_fs_int: each window's binade, predicted from the approximate sums
 //             before it, and its values' integer increments there (as
 //             exact_index_sum forms them).
@@ -4166,6 +4169,13 @@ __device__ __forceinline__ int fs_windows(const StreamArgs& a) { return a.full_s
 __device__ __forceinline__ uint32_t* fs_table(const StreamArgs& a, int r, int k) {
     const int nW = fs_windows(a);
     return a.fs_tab + ((size_t)r * FS_TABLES + k) * (size_t)nW;
+}
+// The lane tables (kGLanes) after every row's tables: 64 uint4 per window
+// (the lane's pair at the window's binade E, then at E + 1).
+__device__ __forceinline__ uint4* fs_lanes(const StreamArgs& a, int r) {
+    const size_t nW = (size_t)fs_windows(a);
+    const size_t base = ((size_t)a.rows * FS_TABLES * nW + 3) & ~(size_t)3;
+    return reinterpret_cast<uint4*>(a.fs_tab + base) + (size_t)r * nW * 64;
 }
 
 template <int DT>
@@ -4181,6 +4191,7 @@ __global__ __launch_bounds__(64) void k_fs_max(StreamArgs a) {
     const uint32_t* mrow = (P.flags & RF_MASK) ? a.mask + (int64_t)r * a.mask_stride : nullptr;
     float mloc = -__builtin_inff();
     bool nanv = false;
+    int cnt = 0;
     for (int g = 0; g < G; ++g) {
         const int i0 = w * WS + g * kFWin + lane * 8;
         float x[8];
@@ -4204,16 +4215,19 @@ __global__ __launch_bounds__(64) void k_fs_max(StreamArgs a) {
             }
             y[j] = v;
             mloc = fmaxf(mloc, v);
+            cnt += v != -__builtin_inff();
         }
         float4* dst = reinterpret_cast<float4*>(fv + i0);
         dst[0] = make_float4(y[0], y[1], y[2], y[3]);
         dst[1] = make_float4(y[4], y[5], y[6], y[7]);
     }
     mloc = wave_max_f(mloc);
+    cnt = __builtin_amdgcn_readlane(wave_incl_sum_i(cnt), 63);
     const bool anynan = __ballot(nanv) != 0ull;
     if (lane == 0) {
         fs_table(a, r, FS_MAX)[w] = __float_as_uint(mloc);
         fs_table(a, r, FS_NAN)[w] = anynan ? 1u : 0u;
+        fs_table(a, r, FS_CNT)[w] = (uint32_t)cnt;
     }
 }
 
@@ -4235,6 +4249,7 @@ __global__ __launch_bounds__(64) void k_fs_exp(StreamArgs a) {
     const float* fv = a.fullv + (size_t)r * a.full_stride;
     float* pv = a.fullp + (size_t)r * a.full_stride;
     float ws = 0.0f;
+    double wd = 0.0;
     for (int g = 0; g < G; ++g) {
         const int i0 = w * WS + g * kFWin + lane * 8;
         const float4 c0 = reinterpret_cast<const float4*>(fv + i0)[0], c1 = reinterpret_cast<const float4*>(fv + i0)[1];
@@ -4244,13 +4259,18 @@ __global__ __launch_bounds__(64) void k_fs_exp(StreamArgs a) {
         for (int j = 0; j < 8; ++j) {
             v[j] = (x[j] == -__builtin_inff() || m == -__builtin_inff()) ? 0.0f : libm_expf_t(x[j] - m, expT);
             ws += v[j];
+            wd += (double)v[j];
         }
         float4* dst = reinterpret_cast<float4*>(pv + i0);
         dst[0] = make_float4(v[0], v[1], v[2], v[3]);
         dst[1] = make_float4(v[4], v[5], v[6], v[7]);
     }
     ws = wave_tree_prefix_f(ws);
-    if (lane == 63) fs_table(a, r, FS_A)[w] = __float_as_uint(ws);
+    wd = wave_tree_prefix_d(wd);
+    if (lane == 63) {
+        fs_table(a, r, FS_A)[w] = __float_as_uint(ws);
+        reinterpret_cast<double*>(fs_table(a, r, FS_SD))[w] = wd;
+    }
 }
 
 __global__ __launch_bounds__(64) void k_fs_int(StreamArgs a) {
@@ -4266,6 +4286,9 @@ __global__ __launch_bounds__(64) void k_fs_int(StreamArgs a) {
     for (int k = lane; k < w; k += 64) pre += __uint_as_float(wa[k]);
     pre = readlane_f(wave_tree_prefix_f(pre), 63);
     const int E = w == 0 ? -126 : xs_binade(pre);
+    // a window of one step whose approximate end lies in a higher binade (or
+    // within 0.1% below one) keeps its lanes' pairs at E and E + 1
+    const bool lanes_on = G == 1 && w > 0 && xs_binade((pre + __uint_as_float(wa[w])) * 1.001f) != E;
     const float* pv = a.fullp + (size_t)r * a.full_stride;
     XPair wp{0u, 0u};
     bool nz = false;
@@ -4279,6 +4302,12 @@ __global__ __launch_bounds__(64) void k_fs_int(StreamArgs a) {
             lp = xcomp(lp, xinc2(v[j], E));
             nz |= v[j] != 0.0f;
         }
+        if (lanes_on) {
+            XPair l1{0u, 0u};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) l1 = xcomp(l1, xinc2(v[j], E + 1));
+            fs_lanes(a, r)[(size_t)w * 64 + lane] = make_uint4(lp.d0, lp.d1, l1.d0, l1.d1);
+        }
         const XPair sp = wave_scan_pair(lp);
         wp = xcomp(wp, XPair{(uint32_t)__builtin_amdgcn_readlane((int)sp.d0, 63),
                              (uint32_t)__builtin_amdgcn_readlane((int)sp.d1, 63)});
@@ -4287,12 +4316,17 @@ __global__ __launch_bounds__(64) void k_fs_int(StreamArgs a) {
     if (lane == 0) {
         fs_table(a, r, FS_D0)[w] = wp.d0;
         fs_table(a, r, FS_D1)[w] = wp.d1;
-        fs_table(a, r, FS_EF)[w] = gpack(E, empty ? kGEmpty : 0u);
+        fs_table(a, r, FS_EF)[w] = gpack(E, (empty ? kGEmpty : 0u) | (lanes_on ? kGLanes : 0u));
     }
 }
 
-// Full-vocabulary rows, one block of kFT threads per row.
-template <bool GT>
+// Full-vocabulary rows, one block of kFT threads per row. PRE: the
+// instantiations for the RF_FPRE rows (k_fs_* did the transform and left the
+// window tables; no penalties, logit bias or top-k), PLAIN among them for the
+// rows without top-p and min-p (the CLI's identity() + temperature: without
+// those stages' code the kernel keeps its state in registers); the other one
+// for the remaining full rows.
+template <bool GT, bool PRE, bool PLAIN>
 __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ FullShared st;
@@ -4300,7 +4334,8 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
     const int r = (int)blockIdx.x;
     if (r >= a.rows) return;
     const RowPlan P = plan_of(a, r);
-    if (!(P.flags & RF_FULL)) return;
+    if (!(P.flags & RF_FULL) || PRE != ((P.flags & RF_FPRE) != 0)) return;
+    if (PRE && PLAIN != ((P.flags & (RF_TOPP | RF_MINP)) == 0)) return;
     HSAMP_PHASE(12000 + r, 0);
     const int V = a.vocab, G = a.full_g;
     const int WS = kFWin * G;
@@ -4308,10 +4343,10 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
     float* fv = a.fullv + (size_t)r * Vp;
     float* pv = a.fullp + (size_t)r * Vp;
     uint32_t* fk = a.fullk + (size_t)r * a.full_p2;
-    const bool pen = (P.flags & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) != 0;
-    const bool masked = (P.flags & RF_MASK) != 0;
+    const bool pen = !PRE && (P.flags & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) != 0;
+    const bool masked = !PRE && (P.flags & RF_MASK) != 0;
     const PenaltyLds pl = pen_table<GT>(a, r, smem);
-    const FullLds f = full_lds(smem + (GT ? 0 : 8 * (size_t)a.mhash_slots));
+    const FullLds f = full_lds(smem + (GT || PRE ? 0 : 8 * (size_t)a.mhash_slots));
     if (tid < 32) st.expT[tid] = kExpT[tid];
     if (tid == 0) {
         st.u = a.u[r];
@@ -4388,15 +4423,34 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
     using I1 = std::integral_constant<int, 1>;
     using BT = std::integral_constant<bool, true>;
     using BF = std::integral_constant<bool, false>;
-    const bool pre = (P.flags & RF_FPRE) != 0;
-    if (pre) {
-        // k_fs_max transformed the row: its window maxima and NaN flags
-        const int nWp = fs_windows(a);
+    constexpr bool pre = PRE;
+    static_assert(kFMaxWin <= 2 * kFT, "two windows per thread");
+    double sdr[2] = {0.0, 0.0};   // PRE: the draw's window sums of the numerators ...
+    uint32_t cnr[2] = {0u, 0u};   // ... and counts (windows tid, tid + kFT)
+    if constexpr (PRE) {
+        // k_fs_* transformed the row and left its window tables, all loaded at
+        // once: maxima and NaN flags for the row's maximum, the exact sum's
+        // binades and pairs into LDS, the draw's sums and counts kept here
         const uint32_t* wm = fs_table(a, r, FS_MAX);
         const uint32_t* wn = fs_table(a, r, FS_NAN);
-        for (int k = tid; k < nWp; k += kFT) {
-            mloc = fmaxf(mloc, __uint_as_float(wm[k]));
-            nanv |= wn[k] != 0u;
+        const uint32_t* we = fs_table(a, r, FS_EF);
+        const uint32_t* w0 = fs_table(a, r, FS_D0);
+        const uint32_t* w1 = fs_table(a, r, FS_D1);
+        const double* wsd = reinterpret_cast<const double*>(fs_table(a, r, FS_SD));
+        const uint32_t* wcn = fs_table(a, r, FS_CNT);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int k = tid + i * kFT;
+            if (k < nW) {
+                const uint32_t mx = wm[k], nn = wn[k], ef = we[k], d0 = w0[k], d1 = w1[k];
+                sdr[i] = wsd[k];
+                cnr[i] = wcn[k];
+                mloc = fmaxf(mloc, __uint_as_float(mx));
+                nanv |= nn != 0u;
+                f.winEF[k] = ef;
+                f.winD0[k] = d0;
+                f.winD1[k] = d1;
+            }
         }
     } else if (a.dtype == 0) {
         if (masked) transform(I0{}, BT{});
@@ -4411,7 +4465,7 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
 
     // ---- top-k above kLimitK (sampler.cpp:109-121): the k-th largest key by four
     // 8-bit digit passes, ties to the lower ids ----
-    if (P.flags & RF_TOPK) {
+    if (!PRE && (P.flags & RF_TOPK)) {
         const int k = P.top_k;
         uint32_t prefix = 0u, kmask = 0u;
         int need = k;
@@ -4483,16 +4537,10 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
         // ---- softmax numerators and their exact index-order sum (sampler.cpp:124-142) ----
         float S;
         if (pre) {
-            // k_fs_exp / k_fs_int left the numerators and the windows' tables
-            for (int k = tid; k < nW; k += kFT) {
-                f.winA[k] = __uint_as_float(fs_table(a, r, FS_A)[k]);
-                f.winEF[k] = fs_table(a, r, FS_EF)[k];
-                f.winD0[k] = fs_table(a, r, FS_D0)[k];
-                f.winD1[k] = fs_table(a, r, FS_D1)[k];
-            }
-            __syncthreads();
+            // k_fs_exp / k_fs_int left the numerators; their tables went to
+            // LDS at the start (ordered by fblock_max's barriers)
             HSAMP_PHASE(12000 + r, 4);
-            S = xs_value(exact_index_compose(pv, nW, G, f, st));
+            S = xs_value(exact_index_compose(pv, nW, G, f, st, fs_lanes(a, r)));
         } else {
             full_exp(fv, pv, m, nW, G, f, st);
             HSAMP_PHASE(12000 + r, 4);
@@ -4500,9 +4548,10 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
         }
         HSAMP_PHASE(12000 + r, 5);
         bool changed = false;   // a stage removed ids since S was taken
+        bool touched = false;   // top-p or min-p removed ids
 
         // ---- top-p (sampler.cpp:146-164) ----
-        if (P.flags & RF_TOPP) {
+        if (!PLAIN && (P.flags & RF_TOPP)) {
             uint32_t cut_key = 0u;
             int cut_count = 0;
             const float inv = 1.0f / S;
@@ -4574,6 +4623,7 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                     });
                 }
                 changed = true;
+                touched = true;
                 __syncthreads();
             }
         }
@@ -4603,7 +4653,7 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
         };
 
         // ---- min-p (sampler.cpp:167-176) ----
-        if (P.flags & RF_MINP) {
+        if (!PLAIN && (P.flags & RF_MINP)) {
             if (changed) refresh();
             changed = false;
             const float inv = 1.0f / S;
@@ -4620,13 +4670,16 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                 }
             });
             changed = fblock_sum_i(dropped, st) != 0;
+            touched |= changed;
         }
         HSAMP_PHASE(12000 + r, 6);
         if (changed) refresh();
         HSAMP_PHASE(12000 + r, 7);
-        m = -__builtin_inff();
-        fpass(fv, Vp, [&](int, float x) { m = fmaxf(m, x); });
-        m = fblock_max(m, st);
+        if (touched) {
+            m = -__builtin_inff();
+            fpass(fv, Vp, [&](int, float x) { m = fmaxf(m, x); });
+            m = fblock_max(m, st);
+        }
         if (m != -__builtin_inff()) {
             // ---- the draw (sampler.cpp:178-182, discrete_distribution) ----
             // p = e * fl(1/S); S_d = sum of p (double); q = p / S_d; the first id
@@ -4636,7 +4689,20 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
             const float inv = 1.0f / S;
             double* wq = reinterpret_cast<double*>(f.winA);   // [kFMaxWin] window sums of p, then prefixes
             uint32_t* wc = f.winEF;                            // [kFMaxWin] kept counts, then prefixes
-            {
+            if (pre && !touched) {
+                // k_fs_* left each window's numerators summed in double and
+                // its count: the window sums of p are taken as fl(1/S) times
+                // those (within 2^-24 of the sums of fl(e fl(1/S)) relative,
+                // where CDF_NEAR's 1e-6 flags every draw they could move)
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const int k = tid + i * kFT;
+                    if (k < nW) {
+                        wq[k] = (double)inv * sdr[i];
+                        wc[k] = cnr[i];
+                    }
+                }
+            } else {
                 double ws = 0.0;
                 int c = 0;
                 wpass2(pv, fv, nW, G, [&](int w, int g, const float (&e)[8], const float (&x)[8]) {
@@ -4659,6 +4725,12 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
             }
             __syncthreads();
             HSAMP_PHASE(12000 + r, 8);
+            if (tid == 0) {
+                st.tok = V - 1;   // no running sum reaches u: cp[V - 1] = 1 takes it
+                st.dS = -1.0;
+                st.fgroup = nW - 1;
+            }
+            const double u = st.u;
             double Sd;
             {
                 // exclusive prefixes over the windows, 2 per thread
@@ -4686,29 +4758,87 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                     wq[w0 + 1] = ex + q0;
                     wc[w0 + 1] = (uint32_t)(cex + c0);
                 }
-            }
-            HSAMP_PHASE(12000 + r, 9);
-            if (tid == 0) {
-                st.tok = V - 1;   // no running sum reaches u: cp[V - 1] = 1 takes it
-                st.dS = -1.0;
+                // the first window whose end reaches u (by its prefix of p /
+                // S_d): one candidate per wave
+                if (u > 0.0) {
+                    const bool h0 = w0 < nW && ((w0 + 1 < nW) ? (ex + q0) / Sd : 2.0) >= u;
+                    const bool h1 = w0 + 1 < nW && ((w0 + 2 < nW) ? (ex + q0 + q1) / Sd : 2.0) >= u;
+                    const u64 hm = __ballot(h0 || h1);
+                    if (hm != 0ull && lane == __ffsll((long long)hm) - 1) atomicMin(&st.fgroup, h0 ? w0 : w0 + 1);
+                }
             }
             __syncthreads();
-            const double u = st.u;
+            HSAMP_PHASE(12000 + r, 9);
             if (!(u > 0.0)) {
                 tok = 0;
             } else {
-                // the first window whose end reaches u (by its prefix of p / S_d)
-                if (tid == 0) st.fgroup = nW - 1;
-                __syncthreads();
-                for (int w = tid; w < nW; w += kFT) {
-                    const double end = (w + 1 < nW) ? wq[w + 1] / Sd : 2.0;
-                    if (end >= u) {
-                        atomicMin(&st.fgroup, w);
-                        break;
+                HSAMP_PHASE(12000 + r, 10);
+                if (G == 1) {
+                    // from a window before it (the prefixes are sums in another
+                    // order), sixteen windows at a time, one per wave: each from
+                    // its prefix, the first window where a running sum of q
+                    // reaches u gives the id
+                    for (int base = max(0, st.fgroup - 1); base < nW; base += kFW) {
+                        const int w = base + wid;
+                        int wt = -1;
+                        double wd = 0.0, cpe = 0.0;
+                        if (w < nW) {
+                            const double cp = wq[w] / Sd;
+                            const int i0 = w * WS + lane * 8;
+                            const float4 e0 = reinterpret_cast<const float4*>(pv + i0)[0];
+                            const float4 e1 = reinterpret_cast<const float4*>(pv + i0)[1];
+                            const float e[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+                            double q[8], ls = 0.0;
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) {
+                                q[j] = (double)(e[j] * inv) / Sd;
+                                ls += q[j];
+                            }
+                            const double li = wave_tree_prefix_d(ls);
+                            double c = cp + (li - ls), cat = 0.0, pat = 0.0;
+                            int first = 8;
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) {
+                                const double before = c;
+                                c = c + q[j];
+                                const int i = i0 + j;
+                                const double cc = (i == V - 1) ? 1.0 : c;
+                                if (first == 8 && i < V && q[j] > 0.0 && cc >= u) {
+                                    first = j;
+                                    cat = cc;
+                                    pat = before;
+                                }
+                            }
+                            const u64 hm = __ballot(first < 8);
+                            if (hm != 0ull) {
+                                const int L = __ffsll((long long)hm) - 1;
+                                wt = __builtin_amdgcn_readlane(i0 + first, L);
+                                wd = readlane_d(fmin(fabs(cat - u), fabs(pat - u)), L);
+                            }
+                            cpe = cp + readlane_d(li, 63);
+                        }
+                        if (lane == 0) {
+                            st.wtok[wid] = wt;
+                            st.wds[wid] = wd;
+                            st.wcp[wid] = cpe;
+                        }
+                        __syncthreads();
+                        HSAMP_PHASE(12000 + r, 3);
+                        int k = 0;
+                        while (k < kFW && st.wtok[k] < 0) ++k;
+                        const bool last = base + kFW >= nW;
+                        if (tid == 0) {
+                            if (k < kFW) {
+                                st.tok = st.wtok[k];
+                                st.dS = st.wds[k];
+                            } else if (last) {
+                                st.dS = fmin(fabs(1.0 - u), fabs(st.wcp[nW - 1 - base] - u));
+                            }
+                        }
+                        __syncthreads();
+                        if (k < kFW) break;
                     }
-                }
-                __syncthreads();
-                if (wid == 0) {
+                } else if (wid == 0) {
                     // walk from a window before it (the prefixes are sums in
                     // another order) until a running sum of q reaches u
                     int w = max(0, st.fgroup - 1);
@@ -4987,19 +5117,25 @@ hipError_t launch_merge(const StreamArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
-hipError_t launch_full_pre(const StreamArgs& a, hipStream_t stream) {
+// The RF_FPRE rows: k_fs_max, k_fs_exp, k_fs_int over B x nW waves, then
+// k_full's PRE instantiations (no penalty table in their LDS): PLAIN for the
+// rows without top-p and min-p (plain), the other for the rows with them (tp).
+hipError_t launch_full_pre(const StreamArgs& a, bool plain, bool tp, hipStream_t stream) {
     const int nW = a.full_stride / (kFWin * a.full_g);
     const dim3 g((unsigned)((int64_t)a.rows * nW)), b(64);
     if (a.dtype == 0) hipLaunchKernelGGL((k_fs_max<0>), g, b, 0, stream, a);
     else hipLaunchKernelGGL((k_fs_max<1>), g, b, 0, stream, a);
     hipLaunchKernelGGL(k_fs_exp, g, b, 0, stream, a);
     hipLaunchKernelGGL(k_fs_int, g, b, 0, stream, a);
+    if (plain) hipLaunchKernelGGL((k_full<false, true, true>), dim3(a.rows), dim3(kFT), (uint32_t)kFullLdsBytes, stream, a);
+    if (tp) hipLaunchKernelGGL((k_full<false, true, false>), dim3(a.rows), dim3(kFT), (uint32_t)kFullLdsBytes, stream, a);
     return hipGetLastError();
 }
 
+// The other full rows.
 hipError_t launch_full(const StreamArgs& a, uint32_t lds, hipStream_t stream) {
-    if (a.gtab != nullptr) hipLaunchKernelGGL((k_full<true>), dim3(a.rows), dim3(kFT), lds, stream, a);
-    else hipLaunchKernelGGL((k_full<false>), dim3(a.rows), dim3(kFT), lds, stream, a);
+    if (a.gtab != nullptr) hipLaunchKernelGGL((k_full<true, false, false>), dim3(a.rows), dim3(kFT), lds, stream, a);
+    else hipLaunchKernelGGL((k_full<false, false, false>), dim3(a.rows), dim3(kFT), lds, stream, a);
     return hipGetLastError();
 }
 

@@ -38,9 +38,14 @@ enum : uint32_t {
 };
 
 // k_fs_* per-row tables, nW entries each (nW = full_stride / (512 * full_g)):
-// window maxima, NaN seen, approximate window sums of the numerators, and the
-// windows' predicted binades / integer increments for the exact sum.
-enum : int { FS_MAX = 0, FS_NAN = 1, FS_A = 2, FS_EF = 3, FS_D0 = 4, FS_D1 = 5, FS_TABLES = 6 };
+// window maxima, NaN seen, approximate window sums of the numerators, the
+// windows' predicted binades / integer increments for the exact sum, their
+// numerators' sums in double (two entries' space: FS_SD and the one after)
+// and their counts of ids left in (transformed logit above -inf). An even
+// number of tables keeps the doubles 8-byte aligned.
+enum : int {
+    FS_MAX = 0, FS_NAN = 1, FS_A = 2, FS_EF = 3, FS_D0 = 4, FS_D1 = 5, FS_SD = 6, FS_CNT = 8, FS_TABLES = 10
+};
 
 // Hash-table value bits for one token of a slice (penalty bookkeeping).
 enum : uint32_t {
@@ -146,7 +151,8 @@ struct StreamArgs {
     int32_t full_p2;            // next power of two >= vocab
     int32_t full_stride;        // k_full: floats per row of fullv / fullp (whole windows of 512 * full_g)
     int32_t full_g;             // k_full: 512-id steps per index-order window
-    uint32_t* fs_tab;           // [rows * FS_TABLES * nW] k_fs_* results for k_full's RF_FPRE rows
+    uint32_t* fs_tab;           // [rows * FS_TABLES * nW] k_fs_* results for k_full's RF_FPRE rows, then
+                                // (16-byte aligned) [rows * nW * 64] uint4 lane tables
     uint32_t* gtab;             // [rows * 2 * mhash_slots] penalty tables, or NULL: tables in LDS
     uint32_t merge_lds;         // dynamic LDS of k_merge
     uint32_t lds_bytes;         // dynamic LDS size of the launch

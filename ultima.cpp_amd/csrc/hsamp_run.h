@@ -61,6 +61,9 @@ struct Built {
     bool dry_split = false;    // a row whose DRY and frequency/presence windows differ
     bool two_windows = false;  // a row whose repetition and count windows are both on and differ
     bool any_fpre = false;     // a k_full row with a plain transform (RF_FPRE)
+    bool any_full_gen = false; // a k_full row without RF_FPRE
+    bool any_fpre_plain = false;  // an RF_FPRE row without top-p and min-p
+    bool any_fpre_tp = false;     // an RF_FPRE row with top-p or min-p
 };
 
 // Kernel choice, slicing, LDS sizes and scratch sizes (in elements) of one run.
@@ -79,7 +82,7 @@ struct RunPlan {
     size_t full_elems = 0;    // f32 fullv and fullp, B * V each (k_full rows)
     size_t fullk_elems = 0;   // uint32 k_full sort scratch
     size_t fin_elems = 0;     // int32 kept ids for write-back, B * kLimitK (and B counts)
-    size_t fs_elems = 0;      // uint32 k_fs_* per-window tables, B * FS_TABLES * windows
+    size_t fs_elems = 0;      // uint32 k_fs_* per-window tables, B * FS_TABLES * windows, then B * windows * 256 lane words
 };
 
 // Device scratch of one run.

@@ -164,6 +164,9 @@ struct FullShared {
     int redo;
     double dS;
     float m;
+    int wtok[kFW];     // the draw, one window per wave: the id its running sum reaches u at (-1: none)
+    double wds[kFW];   // ... that id's distance from u (before or after it)
+    double wcp[kFW];   // ... the running sum at the window's end
 };
 
 __device__ __forceinline__ float fblock_max(float v, FullShared& st) {
@@ -367,37 +370,87 @@ __device__ __forceinline__ XPair wave_scan_pair(XPair x) {
 
 // Replays v[lane * 8 + j] (in that order; absent values +0) onto s, from
 // position `start` on. With thr_on, stops at the first value after which the
-// sum reaches thr and returns its position (0..511); else returns -1. Each
-// step takes every remaining value at s's binade at once (lanes' pairs
+// sum reaches thr and returns its position (0..511); else returns -1.
+// Without thr the values are added one by one as float adds, the running sum
+// handed from lane to lane (eight adds, then a readlane, per lane): the chain
+// the sum is defined by, 512 steps whatever binades it crosses. With thr each
+// step takes every remaining value at s's binade at once (lanes' increments
 // scanned, then each lane's values in order from its exact start) and applies
 // them up to the first value that leaves the binade or reaches thr, which is
-// added exactly.
+// added exactly; a step without half-way values scans plain saturating sums,
+// one with them the parity pairs.
 __device__ int xs_replay(XState& s, const float (&v)[8], int start, bool thr_on, float thr) {
     const int lane = lane_id();
+    if (!thr_on) {
+        float w[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) w[j] = lane * 8 + j >= start ? v[j] : 0.0f;
+        float acc = xs_value(s);
+        for (int l = start >> 3; l < 64; ++l) {
+            float b = acc;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) b = b + w[j];
+            acc = readlane_f(b, l);
+        }
+        int ex;
+        uint32_t X;
+        fparts(acc, ex, X);
+        s = XState{ex, X};
+        return -1;
+    }
     for (;;) {
         const int E = s.E;
         const uint32_t M = s.M;
         const uint32_t thrM = thr_on ? xs_thr(thr, E) : 0xFFFFFFFFu;
-        XPair e[8];
-        XPair lp{0u, 0u};
+        uint32_t inc[8];
+        bool tie = false;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            e[j] = (lane * 8 + j >= start) ? xinc2(v[j], E) : XPair{0u, 0u};
-            lp = xcomp(lp, e[j]);
+            bool t, b;
+            const uint32_t i = xinc(v[j], E, t, b);
+            const bool on = lane * 8 + j >= start;
+            inc[j] = on ? (b ? (1u << 25) : i) : 0u;
+            tie |= on && t;
         }
-        const XPair incl = wave_scan_pair(lp);
-        const XPair prev{(uint32_t)__shfl_up((int)incl.d0, 1, 64), (uint32_t)__shfl_up((int)incl.d1, 1, 64)};
-        uint32_t cur = sat_add(M, lane == 0 ? 0u : xat(prev, M));
         int first = 8;
-        uint32_t at = cur;
+        uint32_t at = 0u, cur;
+        if (__ballot(tie) == 0ull) {
+            // no half-way value: every increment adds whatever M's parity
+            uint32_t ls = 0u;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t after = sat_add(cur, xat(e[j], cur));
-            if (first == 8 && lane * 8 + j >= start && (after >= (1u << 24) || after >= thrM)) {
-                first = j;
-                at = cur;
+            for (int j = 0; j < 8; ++j) ls = sat_add(ls, inc[j]);
+            const uint32_t incl = wave_scan_u32(ls, 0u, [](uint32_t a, uint32_t b) { return sat_add(a, b); });
+            const uint32_t prev = (uint32_t)__shfl_up((int)incl, 1, 64);
+            cur = sat_add(M, lane == 0 ? 0u : prev);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t after = sat_add(cur, inc[j]);
+                if (first == 8 && lane * 8 + j >= start && (after >= (1u << 24) || after >= thrM)) {
+                    first = j;
+                    at = cur;
+                }
+                cur = after;
             }
-            cur = after;
+        } else {
+            XPair e[8];
+            XPair lp{0u, 0u};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                e[j] = (lane * 8 + j >= start) ? xinc2(v[j], E) : XPair{0u, 0u};
+                lp = xcomp(lp, e[j]);
+            }
+            const XPair incl = wave_scan_pair(lp);
+            const XPair prev{(uint32_t)__shfl_up((int)incl.d0, 1, 64), (uint32_t)__shfl_up((int)incl.d1, 1, 64)};
+            cur = sat_add(M, lane == 0 ? 0u : xat(prev, M));
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t after = sat_add(cur, xat(e[j], cur));
+                if (first == 8 && lane * 8 + j >= start && (after >= (1u << 24) || after >= thrM)) {
+                    first = j;
+                    at = cur;
+                }
+                cur = after;
+            }
         }
         const u64 em = __ballot(first < 8);
         if (em == 0ull) {
@@ -422,8 +475,10 @@ __device__ int xs_replay(XState& s, const float (&v)[8], int start, bool thr_on,
 // Group table entry: (E + 256) | flags << 16 with the group's pair at E in
 // D0/D1 (saturated at 2^25). Flags: 1 = the group must be replayed value by
 // value (its order is not known, and a half-way value makes it matter; or
-// too many values for the sums), 2 = empty group.
-constexpr uint32_t kGCare = 1u, kGEmpty = 2u;
+// too many values for the sums), 2 = empty group, 4 = an index-order window
+// with lane tables (each lane's pair at E and at E + 1; it is predicted to
+// leave its binade once).
+constexpr uint32_t kGCare = 1u, kGEmpty = 2u, kGLanes = 4u;
 __device__ __forceinline__ uint32_t gpack(int E, uint32_t flags) { return (uint32_t)(E + 256) | (flags << 16); }
 
 // Composes groups 0 .. n-1 in order onto s by one wave: whole groups at once
@@ -440,7 +495,7 @@ __device__ int xs_compose(int n, const uint32_t* EF, const uint32_t* D0, const u
         const bool valid = g < n;
         const uint32_t ef = valid ? EF[g] : 0u;
         const int Eg = (int)(ef & 0xFFFFu) - 256;
-        const uint32_t fl = ef >> 16;
+        const uint32_t fl = (ef >> 16) & ~kGLanes;
         const bool empty = valid && (fl & kGEmpty) != 0u;
         const bool ok = empty || (valid && fl == 0u && Eg == s.E);
         const XPair d = (ok && !empty) ? XPair{D0[g], D1[g]} : XPair{0u, 0u};
@@ -525,9 +580,10 @@ __device__ __forceinline__ float fblock_excl_scan_f(float v, float* total, FullS
 // binades from the approximate prefixes, the windows' pairs at them, then one
 // wave composes (replaying the windows where the prediction fails or the
 // sum leaves its binade).
-__device__ XState exact_index_compose(const float* x, int nW, int G, FullLds f, FullShared& st);
+__device__ __forceinline__ XState exact_index_compose(const float* x, int nW, int G, FullLds f, FullShared& st,
+                                                      const uint4* lanes = nullptr);
 
-__device__ XState exact_index_sum(const float* x, int nW, int G, FullLds f, FullShared& st) {
+__device__ __noinline__ XState exact_index_sum(const float* x, int nW, int G, FullLds f, FullShared& st) {
     const int tid = threadIdx.x, lane = lane_id();
     {
         // two windows per thread: their approximate start values -> binades
@@ -569,24 +625,259 @@ __device__ XState exact_index_sum(const float* x, int nW, int G, FullLds f, Full
     return exact_index_compose(x, nW, G, f, st);
 }
 
+// Segmented inclusive scan of pairs over the wave in lane order: a lane with
+// head set starts a segment (its prefix begins with its own pair). The pair
+// operator extended by a head flag, (ha, a) then (hb, b) = (ha | hb, hb ? b :
+// a then b), is associative, so the DPP steps of wave_scan_pair apply.
+template <int CTRL, int ROWM>
+__device__ __forceinline__ void seg_scan_step(XPair& x, uint32_t& h) {
+    const XPair o{dpp_u32<CTRL, ROWM>(0u, x.d0), dpp_u32<CTRL, ROWM>(0u, x.d1)};
+    const uint32_t oh = dpp_u32<CTRL, ROWM>(0u, h);
+    const XPair c = xcomp(o, x);
+    x = h ? x : c;
+    h |= oh;
+}
+__device__ __forceinline__ XPair wave_seg_scan_pair(XPair x, bool head) {
+    uint32_t h = head ? 1u : 0u;
+    seg_scan_step<0x111, 0xF>(x, h);
+    seg_scan_step<0x112, 0xF>(x, h);
+    seg_scan_step<0x114, 0xF>(x, h);
+    seg_scan_step<0x118, 0xF>(x, h);
+    seg_scan_step<0x142, 0xA>(x, h);
+    seg_scan_step<0x143, 0xC>(x, h);
+    return x;
+}
+
+// LDS-qualified views of pointers into the block's shared memory: functions
+// that receive them as plain pointers would otherwise access them with flat
+// instructions.
+typedef __attribute__((address_space(3))) uint32_t lds_u32;
+typedef __attribute__((address_space(3))) float lds_f32;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) u32x4 lds_u4;
+
+// The same scans for pairs without half-way values (d0 == d1 in every lane):
+// plain sums, at most 64 x 2^25 < 2^32.
+template <int CTRL, int ROWM>
+__device__ __forceinline__ void seg_sum_step(uint32_t& x, uint32_t& h) {
+    const uint32_t o = dpp_u32<CTRL, ROWM>(0u, x);
+    const uint32_t oh = dpp_u32<CTRL, ROWM>(0u, h);
+    x = h ? x : o + x;
+    h |= oh;
+}
+__device__ __forceinline__ uint32_t wave_seg_sum_u32(uint32_t x, bool head) {
+    uint32_t h = head ? 1u : 0u;
+    seg_sum_step<0x111, 0xF>(x, h);
+    seg_sum_step<0x112, 0xF>(x, h);
+    seg_sum_step<0x114, 0xF>(x, h);
+    seg_sum_step<0x118, 0xF>(x, h);
+    seg_sum_step<0x142, 0xA>(x, h);
+    seg_sum_step<0x143, 0xC>(x, h);
+    return x;
+}
+// Inclusive scan of pairs, by plain sums when no lane's pair differs by parity.
+__device__ __forceinline__ XPair wave_scan_pair_any(XPair x) {
+    if (__ballot(x.d0 != x.d1) != 0ull) return wave_scan_pair(x);
+    const uint32_t u = wave_scan_u32(x.d0, 0u, [](uint32_t a, uint32_t b) { return a + b; });
+    return XPair{u, u};
+}
+
+// Windows the index-order compose stages in LDS (window 0 and the windows
+// with lane tables, in index order): 64 lane entries and 512 values each.
+constexpr int kStage = 24;
+static_assert(kStage * (64 * 16 + 512 * 4) + kStage * 4 <= 4 * (6 * kFNB + 1), "staging fits the bucket tables");
+
 // The exact sum from the windows' tables in LDS (f.winEF / winD0 / winD1:
-// each window's predicted binade and its integer increments there): one wave
-// composes them in index order, replaying value by value the windows where
-// the prediction fails, the sum leaves its binade or a half-way value occurs.
-__device__ XState exact_index_compose(const float* x, int nW, int G, FullLds f, FullShared& st) {
+// each window's predicted binade and its integer increments there), composed
+// in index order by wave 0. The windows of each batch of 64 are split into
+// runs of one predicted binade; a segmented scan gives every window its
+// run's prefix, so a run is taken at once while the state is in its binade
+// and below 2^24. The window where the sum leaves the binade is resolved
+// exactly: with lane tables (lanes: each lane's pair at E and E + 1, windows
+// of one 512-step) the pairs at E find the lane whose values cross, that
+// lane's eight values are added as floats and the lanes after it compose at
+// E + 1 by their pairs; otherwise, or where the sum lands elsewhere or
+// crosses again, the window's values are chained as float adds. The next run
+// then starts at its own binade; a run whose binade the state is not in is
+// replayed from its first window. With lane tables the other waves stage the
+// windows to be resolved (window 0, the lane-table windows) in LDS while
+// wave 0 composes, each marked ready once written.
+__device__ __forceinline__ XState exact_index_compose(const float* x, int nW, int G, FullLds f, FullShared& st,
+                                                      const uint4* lanes) {
     const int lane = lane_id(), wid = wave_id();
     const int WS = kFWin * G;
-    if (wid == 0) {
-        XState s{-126, 0u};
-        xs_compose(nW, f.winEF, f.winD0, f.winD1, false, 0.0f, s, [&](int w, XState& sv) -> bool {
-            for (int g = 0; g < G; ++g) {
-                const float4* src = reinterpret_cast<const float4*>(x + (size_t)w * WS + g * kFWin + lane * 8);
-                const float4 q0 = src[0], q1 = src[1];
-                const float v[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-                xs_replay(sv, v, 0, false, 0.0f);
+    const bool staged = lanes != nullptr && G == 1;
+    const lds_u32* EF = (const lds_u32*)f.winEF;
+    const lds_u32* D0 = (const lds_u32*)f.winD0;
+    const lds_u32* D1 = (const lds_u32*)f.winD1;
+    lds_u4* s_lt = (lds_u4*)f.bcnt;
+    lds_f32* s_val = (lds_f32*)(f.bcnt + kStage * 64 * 4);
+    volatile lds_u32* s_rdy = (volatile lds_u32*)(f.bcnt + kStage * 64 * 4 + kStage * 512);
+    if (staged) {
+        if ((int)threadIdx.x < kStage) s_rdy[threadIdx.x] = 0u;
+        __syncthreads();
+    }
+    auto is_staged = [&](int g) -> bool { return g == 0 || ((EF[g] >> 16) & kGLanes) != 0u; };
+    if (wid != 0) {
+        if (staged) {
+            int q = 0;
+            for (int c = 0; c < nW && q < kStage; c += 64) {
+                const int g = c + lane;
+                u64 m = __ballot(g < nW && is_staged(g));
+                while (m != 0ull && q < kStage) {
+                    const int w = c + __ffsll((long long)m) - 1;
+                    m &= m - 1ull;
+                    if (q % (kFW - 1) == wid - 1) {
+                        if (w > 0) {
+                            const uint4 t = lanes[(size_t)w * 64 + lane];
+                            s_lt[q * 64 + lane] = u32x4{t.x, t.y, t.z, t.w};
+                        }
+                        const float4* src = reinterpret_cast<const float4*>(x + (size_t)w * WS + lane * 8);
+                        const float4 q0 = src[0], q1 = src[1];
+                        lds_f32* dst = s_val + q * 512 + lane * 8;
+                        dst[0] = q0.x; dst[1] = q0.y; dst[2] = q0.z; dst[3] = q0.w;
+                        dst[4] = q1.x; dst[5] = q1.y; dst[6] = q1.z; dst[7] = q1.w;
+                        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                        if (lane == 0) s_rdy[q] = (uint32_t)w + 1u;
+                    }
+                    ++q;
+                }
             }
-            return false;
-        });
+        }
+    } else {
+        XState s{-126, 0u};
+        // the exact resolution of window w (rank q among the staged windows)
+        auto resolve = [&](int w, int q) {
+            const uint32_t ef = EF[w];
+            uint4 t = make_uint4(0u, 0u, 0u, 0u);
+            float v[8];
+            bool have = false;
+            if (staged && q < kStage && is_staged(w)) {
+                uint32_t spin = 0u;
+                while (s_rdy[q] != (uint32_t)w + 1u && ++spin < (1u << 20)) __builtin_amdgcn_s_sleep(1);
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+                if (s_rdy[q] == (uint32_t)w + 1u) {
+                    if (w > 0) {
+                        const u32x4 l4 = s_lt[q * 64 + lane];
+                        t = make_uint4(l4.x, l4.y, l4.z, l4.w);
+                    }
+                    const lds_f32* sv = s_val + q * 512 + lane * 8;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) v[j] = sv[j];
+                    have = true;
+                }
+            }
+            const bool by_lanes = lanes != nullptr && G == 1 && ((ef >> 16) & kGLanes) &&
+                                  s.E == (int)(ef & 0xFFFFu) - 256;
+            if (!have && G == 1) {
+                if (by_lanes) t = lanes[(size_t)w * 64 + lane];
+                const float4* src = reinterpret_cast<const float4*>(x + (size_t)w * WS + lane * 8);
+                const float4 q0 = src[0], q1 = src[1];
+                v[0] = q0.x; v[1] = q0.y; v[2] = q0.z; v[3] = q0.w;
+                v[4] = q1.x; v[5] = q1.y; v[6] = q1.z; v[7] = q1.w;
+            }
+            if (G != 1) {
+                for (int g = 0; g < G; ++g) {
+                    const float4* src = reinterpret_cast<const float4*>(x + (size_t)w * WS + g * kFWin + lane * 8);
+                    const float4 q0 = src[0], q1 = src[1];
+                    const float u[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+                    xs_replay(s, u, 0, false, 0.0f);
+                }
+                return;
+            }
+            if (!by_lanes) {
+                xs_replay(s, v, 0, false, 0.0f);
+                return;
+            }
+            const int E = s.E;
+            const uint32_t M = s.M;
+            const XPair incl = wave_scan_pair_any(XPair{t.x, t.y});
+            const uint32_t end = sat_add(M, xat(incl, M));   // M after this lane's values
+            const u64 cm = __ballot(end >= (1u << 24));
+            if (cm == 0ull) {
+                s.M = (uint32_t)__builtin_amdgcn_readlane((int)end, 63);
+                return;
+            }
+            const int L = __ffsll((long long)cm) - 1;
+            const uint32_t ML = L == 0 ? M : (uint32_t)__builtin_amdgcn_readlane((int)end, L - 1);
+            float acc = xs_value(XState{E, ML});
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc = acc + readlane_f(v[j], L);
+            int ex;
+            uint32_t X;
+            fparts(acc, ex, X);
+            s = XState{ex, X};
+            if (L == 63) return;
+            if (ex == E + 1) {
+                const XPair rest = wave_scan_pair_any(lane > L ? XPair{t.z, t.w} : XPair{0u, 0u});
+                const XPair tot{(uint32_t)__builtin_amdgcn_readlane((int)rest.d0, 63),
+                                (uint32_t)__builtin_amdgcn_readlane((int)rest.d1, 63)};
+                const uint32_t Me = sat_add(X, xat(tot, X));
+                if (Me < (1u << 24)) {
+                    s.M = Me;
+                    return;
+                }
+            }
+            xs_replay(s, v, (L + 1) * 8, false, 0.0f);
+        };
+        int c = 0, qc = 0;   // batch start, rank of the first staged window at or after it
+        while (c < nW) {
+            const int g = c + lane;
+            const bool valid = g < nW;
+            const uint32_t ef = valid ? EF[g] : 0u;
+            const int Eg = (int)(ef & 0xFFFFu) - 256;
+            const bool empty = valid && ((ef >> 16) & kGEmpty) != 0u;
+            const XPair d = (valid && !empty) ? XPair{D0[g], D1[g]} : XPair{0u, 0u};
+            const int Ep = __shfl_up(Eg, 1, 64);
+            const bool head = lane == 0 || Eg != Ep;
+            XPair sp;
+            if (__ballot(d.d0 != d.d1) != 0ull) {
+                sp = wave_seg_scan_pair(d, head);
+            } else {
+                const uint32_t u = wave_seg_sum_u32(d.d0, head);
+                sp = XPair{u, u};
+            }
+            const u64 heads = __ballot(head && valid);
+            const u64 smask = staged ? __ballot(valid && is_staged(g)) : 0ull;
+            const u64 nonempty = __ballot(valid && !empty);
+            const int nval = min(64, nW - c);
+            auto rank = [&](int lo) { return qc + __popcll(smask & ((1ull << lo) - 1ull)); };
+            int h = 0, next = c + 64;
+            while (h < nval) {
+                const u64 above = h < 63 ? heads & ~((2ull << h) - 1ull) : 0ull;
+                const int e = above ? __ffsll((long long)above) - 2 : nval - 1;
+                const u64 segm = (e < 63 ? (2ull << e) - 1ull : ~0ull) & ~((1ull << h) - 1ull);
+                const int Eh = __builtin_amdgcn_readlane(Eg, h);
+                if ((nonempty & segm) == 0ull) {
+                    h = e + 1;
+                    continue;
+                }
+                if (Eh != s.E) {
+                    // the run was predicted at another binade: its first window exactly, then a new batch
+                    resolve(c + h, rank(h));
+                    next = c + h + 1;
+                    break;
+                }
+                const uint32_t tot = sat_add(s.M, xat(sp, s.M));
+                const u64 bm = __ballot(tot >= (1u << 24)) & segm;
+                if (bm == 0ull) {
+                    s.M = (uint32_t)__builtin_amdgcn_readlane((int)tot, e);
+                    h = e + 1;
+                    continue;
+                }
+                const int fb = __ffsll((long long)bm) - 1;
+                if (fb > h) s.M = (uint32_t)__builtin_amdgcn_readlane((int)tot, fb - 1);
+                resolve(c + fb, rank(fb));
+                if (fb < e) {
+                    // the sum left the binade before the run's end: the rest of the run from a new batch
+                    next = c + fb + 1;
+                    break;
+                }
+                h = e + 1;
+            }
+            qc += __popcll(smask & (next - c >= 64 ? ~0ull : (1ull << (next - c)) - 1ull));
+            c = next;
+        }
         if (lane == 0) st.xs = s;
     }
     __syncthreads();

@@ -161,3 +161,28 @@ def test_plain_transform_rows_exact_sums(hs, sampler, wl, V):
     w = wl.Workload("full", "f32", x, params, wl.uniform53(78, rows), None, None, mask)
     g = run_gpu(sampler, w, set_cap=V)
     assert compare_rows(w, g) == rows
+
+
+def test_full_vocab_draw_without_sets(sampler, wl):
+    """With no kept set asked for, rows whose top-p or min-p removed ids take
+    the draw's window sums from the numerators alone and their kept count from
+    the stages' own counts: token, row flags and kept count must equal those of
+    the run that writes the sets (checked against the oracle). Rows: cfg3's
+    spike rows (the cut splits ids of equal p at the top) and flat rows, top-p
+    and min-p knobs, and min_p 2 (every id removed: the uniform draw)."""
+    import torch
+    V = 151936
+    w3 = wl.config(3, seed=11, rows=4)
+    knobs = [dict(temperature=0.8, top_p=0.5), dict(temperature=1.2, min_p=0.05),
+             dict(temperature=0.7, top_p=0.95, min_p=0.02), dict(temperature=1.5, min_p=2.0)]
+    wk = _wl(wl, V, len(knobs), [wl.identity_params(**k) for k in knobs], seed=19)
+    for w in (w3, wk):
+        g = run_gpu(sampler, w, set_cap=V)
+        assert compare_rows(w, g) == w.rows
+        from gpu_helpers import to_device
+        x, u, h, m = to_device(w)
+        out = {"kept_count": torch.empty(w.rows, dtype=torch.int32, device=x.device)}
+        o = sampler.run(x, w.params, u, hist=h, hist_len=w.hist_len, mask=m, outputs=out)
+        torch.cuda.synchronize()
+        for k in ("token", "row_flags", "kept_count"):
+            assert np.array_equal(o[k].cpu().numpy(), g[k]), (w.name, k)

@@ -611,55 +611,65 @@ __device__ __forceinline__ float elem(const uint4& r, int c) {
 
 // ---- the token ---------------------------------------------------------------------
 
-// Row r's token, written by the one thread that decided it, with
+// Row r's token (lane 0's tok), written by the wave that decided it, with
 // ultima_hsamp_run_commit's rules when the launch carries them (the server
 // loop's per token, src/server/http_server.cpp:174-201): an ended row
 // (active 0) gets -1; -1 or a stop id ends the row without being pushed;
 // any other token is appended to the row's device history (a full row first
-// keeps its last c_keep ids at its front) and counted against the row's
-// budget, which ends the row at 0.
-__device__ __forceinline__ void emit_token(const StreamArgs& a, int r, int32_t tok) {
+// keeps its last c_keep ids at its front, copied by the whole wave) and
+// counted against the row's budget, which ends the row at 0. Called by all 64
+// lanes of one wave.
+__device__ __forceinline__ void emit_token_wave(const StreamArgs& a, int r, int32_t tok) {
+    const int lane = lane_id();
+    tok = __builtin_amdgcn_readlane(tok, 0);
     if (a.c_hist == nullptr) {
-        a.token[r] = tok;
+        if (lane == 0) a.token[r] = tok;
         return;
     }
     // an ended slot, or one whose budget is spent (max_tokens 0: the
     // reference's loop body never runs), emits nothing
     if (a.c_active[r] == 0 || (a.c_budget != nullptr && a.c_budget[r] <= 0)) {
-        a.token[r] = -1;
-        a.c_active[r] = 0;
+        if (lane == 0) {
+            a.token[r] = -1;
+            a.c_active[r] = 0;
+        }
         return;
     }
-    a.token[r] = tok;
     bool end = tok < 0;
     for (int i = 0; i < a.c_nstop; ++i) end = end || tok == a.c_stop[i];
     if (end) {
-        a.c_active[r] = 0;
+        if (lane == 0) {
+            a.token[r] = tok;
+            a.c_active[r] = 0;
+        }
         return;
     }
     int32_t* h = a.c_hist + (int64_t)r * a.c_stride;
     int L = max(a.c_len[r], 0);
     if (L >= a.c_stride) {
         // [stride - keep, stride) -> [0, keep) (keep <= stride / 2: the
-        // ranges do not overlap), sixteen ids in flight at a time
+        // ranges do not overlap), eight ids per lane in flight at a time
         const int keep = a.c_keep;
         const int64_t from = a.c_stride - keep;
-        for (int i0 = 0; i0 < keep; i0 += 16) {
-            int32_t v[16];
+        for (int i0 = 0; i0 < keep; i0 += 8 * 64) {
+            int32_t v[8];
 #pragma unroll
-            for (int j = 0; j < 16; ++j) v[j] = h[from + min(i0 + j, keep - 1)];
+            for (int j = 0; j < 8; ++j) v[j] = h[from + min(i0 + j * 64 + lane, keep - 1)];
 #pragma unroll
-            for (int j = 0; j < 16; ++j)
-                if (i0 + j < keep) h[i0 + j] = v[j];
+            for (int j = 0; j < 8; ++j)
+                if (i0 + j * 64 + lane < keep) h[i0 + j * 64 + lane] = v[j];
         }
         L = keep;
     }
-    h[L] = tok;
-    a.c_len[r] = L + 1;
-    if (a.c_budget != nullptr) {
-        const int32_t b = a.c_budget[r] - 1;
-        a.c_budget[r] = b;
-        if (b <= 0) a.c_active[r] = 0;
+    if (lane == 0) {
+        a.token[r] = tok;
+        h[L] = tok;
+        a.c_len[r] = L + 1;
+        if (a.c_budget != nullptr) {
+            const int32_t b = a.c_budget[r] - 1;
+            a.c_budget[r] = b;
+            if (b <= 0) a.c_active[r] = 0;
+        }
     }
 }
 
@@ -1028,8 +1038,8 @@ __device__ __attribute__((noinline)) void finalize_row(const StreamArgs& a, cons
         rflags |= ROWF_UNIFORM;
         if (tid == 0) tok = uniform_draw(V, u);
     }
+    if (wave_id() == 0) emit_token_wave(a, r, tok);
     if (tid == 0) {
-        emit_token(a, r, tok);
         if (a.row_flags != nullptr) a.row_flags[r] = rflags;
         if (a.kept_count != nullptr) a.kept_count[r] = nkept;
         if (a.fin_n != nullptr) a.fin_n[r] = nkept;
@@ -1404,8 +1414,8 @@ __device__ __forceinline__ void wave_finalize(const StreamArgs& a, const RowPlan
         rflags |= ROWF_UNIFORM;
         if (lane == 0) tok = uniform_draw(V, u);
     }
+    emit_token_wave(a, r, tok);
     if (lane == 0) {
-        emit_token(a, r, tok);
         if (a.row_flags != nullptr) a.row_flags[r] = rflags;
         if (a.kept_count != nullptr) a.kept_count[r] = nkept;
         if (a.fin_n != nullptr) a.fin_n[r] = nkept;
@@ -2988,16 +2998,18 @@ __device__ __forceinline__ void merge_fast(const StreamArgs& a, const RowPlan& P
         }
         best = block_max_u64(best, st);
         __syncthreads();
+        int32_t gtok = 0;
         if (tid == 0) {
             // argmax returns 0 when id 0 holds a NaN: a penalised id 0 was
             // settled with the table, any other by its logit
             const bool pen0 = pen && !lmode && in_table(0);
             const bool nan0 = pen0 ? st.nan0 != 0 : nan_at0;
-            emit_token(a, r, nan0 ? 0 : comp_idx(best));
+            gtok = nan0 ? 0 : comp_idx(best);
             if (a.row_flags != nullptr) a.row_flags[r] = ROWF_GREEDY | ((st.flags & 4) ? ROWF_NAN : 0u);
             if (a.topk_count != nullptr) a.topk_count[r] = -1;
             if (a.kept_count != nullptr) a.kept_count[r] = 0;
         }
+        if (wave_id() == 0) emit_token_wave(a, r, gtok);
         return;
     }
 
@@ -3436,6 +3448,7 @@ __global__ __launch_bounds__(kBlock, 3) void k_merge(StreamArgs a) {
         for (int j = 0; j < NW; ++j) best = win[j] > best ? win[j] : best;
         best = block_max_u64(best, st);
         __syncthreads();
+        int32_t gtok = 0;
         if (tid == 0) {
             bool pen0 = false;   // id 0 penalised: settled with the table
             if (pen) {
@@ -3445,11 +3458,12 @@ __global__ __launch_bounds__(kBlock, 3) void k_merge(StreamArgs a) {
                 pen0 = kk == 0u;
             }
             const bool nan0 = pen0 ? st.nan0 != 0 : nan_at0;
-            emit_token(a, r, nan0 ? 0 : comp_idx(best));
+            gtok = nan0 ? 0 : comp_idx(best);
             if (a.row_flags != nullptr) a.row_flags[r] = ROWF_GREEDY | ((st.flags & 4) ? ROWF_NAN : 0u);
             if (a.topk_count != nullptr) a.topk_count[r] = -1;
             if (a.kept_count != nullptr) a.kept_count[r] = 0;
         }
+        if (wave_id() == 0) emit_token_wave(a, r, gtok);
         return;
     }
     {
@@ -3516,8 +3530,8 @@ __device__ __forceinline__ void pick_greedy(const StreamArgs& a, int r, const u6
     }
     if (tid == 0) st.nan0 = nan0 ? 1 : 0;
     best = block_max_u64(best, st);   // (its barriers publish st.nan0)
+    if (wave_id() == 0) emit_token_wave(a, r, (st.nan0 || best == 0ull) ? 0 : comp_idx(best));
     if (tid == 0) {
-        emit_token(a, r, (st.nan0 || best == 0ull) ? 0 : comp_idx(best));
         if (a.row_flags != nullptr) a.row_flags[r] = ROWF_GREEDY | (nan_any ? ROWF_NAN : 0u);
         if (a.topk_count != nullptr) a.topk_count[r] = -1;
         if (a.kept_count != nullptr) a.kept_count[r] = 0;
@@ -4549,6 +4563,8 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
         HSAMP_PHASE(12000 + r, 5);
         bool changed = false;   // a stage removed ids since S was taken
         bool touched = false;   // top-p or min-p removed ids
+        int nleft = -1;         // ids left in (finite transformed logit) once a stage has counted them
+        bool mk_same = true;    // the largest logit left in is still m
 
         // ---- top-p (sampler.cpp:146-164) ----
         if (!PLAIN && (P.flags & RF_TOPP)) {
@@ -4567,6 +4583,10 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                 const int ngt = fblock_sum_i(gt, st);
                 const int neq = fblock_sum_i(eq, st);
                 const int need = cut_count - ngt;
+                nleft = cut_count;
+                // the largest logit's p is fl(1 * inv) = inv: it stays in unless
+                // the cut falls among the ids with that p
+                if (cut_key == __float_as_uint(inv) && need < neq) mk_same = false;
                 if (need >= neq) {
                     fpass(pv, Vp, [&](int i, float e) {
                         if (__float_as_uint(e * inv) < cut_key) {
@@ -4631,9 +4651,19 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
         // the numerators of what is left: relative to the largest kept logit
         // (the maximum unless a tie in p kept a lower id first), window sums
         auto refresh = [&]() {
-            float mk = -__builtin_inff();
-            fpass(fv, Vp, [&](int, float x) { mk = fmaxf(mk, x); });
-            mk = fblock_max(mk, st);
+            float mk = m;
+            if (nleft == 0) {
+                mk = -__builtin_inff();
+            } else if (!mk_same) {
+                mk = -__builtin_inff();
+                fpass(fv, Vp, [&](int, float x) { mk = fmaxf(mk, x); });
+                mk = fblock_max(mk, st);
+            }
+            mk_same = true;
+            if (mk == -__builtin_inff()) {
+                m = mk;
+                return;
+            }
             if (mk != m) {
                 m = mk;
                 full_exp(fv, pv, m, nW, G, f, st);
@@ -4657,29 +4687,39 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
             if (changed) refresh();
             changed = false;
             const float inv = 1.0f / S;
-            float mp = 0.0f;
-            fpass(pv, Vp, [&](int, float e) { mp = fmaxf(mp, e * inv); });
-            mp = fblock_max(mp, st);
-            const float thr = P.min_p * mp;
-            int dropped = 0;
-            fpass(pv, Vp, [&](int i, float e) {
-                if (e * inv < thr && fv[i] != -__builtin_inff()) {
-                    fv[i] = -__builtin_inff();
-                    pv[i] = 0.0f;
-                    dropped = 1;
+            // (a threshold of 0 -- min_p * inv below the smallest float -- removes nothing)
+            if (m != -__builtin_inff() && P.min_p * inv > 0.0f) {
+                if (nleft < 0) {
+                    // the ids in before min-p: the finite transformed logits
+                    int c = 0;
+                    if (pre) {
+                        c = (int)(cnr[0] + cnr[1]);
+                    } else {
+                        fpass(fv, Vp, [&](int, float x) { c += x != -__builtin_inff(); });
+                    }
+                    nleft = fblock_sum_i(c, st);
                 }
-            });
-            changed = fblock_sum_i(dropped, st) != 0;
-            touched |= changed;
+                // the largest p is the largest logit's, fl(1 * inv) = inv; the
+                // ids left in are those with p >= thr > 0 (a removed id's p is 0)
+                const float thr = P.min_p * inv;
+                int left = 0;
+                fpass(pv, Vp, [&](int i, float e) {
+                    if (e * inv < thr) {
+                        fv[i] = -__builtin_inff();
+                        pv[i] = 0.0f;
+                    } else {
+                        ++left;
+                    }
+                });
+                left = fblock_sum_i(left, st);
+                changed = left != nleft;
+                nleft = left;
+                touched |= changed;
+            }
         }
         HSAMP_PHASE(12000 + r, 6);
         if (changed) refresh();
         HSAMP_PHASE(12000 + r, 7);
-        if (touched) {
-            m = -__builtin_inff();
-            fpass(fv, Vp, [&](int, float x) { m = fmaxf(m, x); });
-            m = fblock_max(m, st);
-        }
         if (m != -__builtin_inff()) {
             // ---- the draw (sampler.cpp:178-182, discrete_distribution) ----
             // p = e * fl(1/S); S_d = sum of p (double); q = p / S_d; the first id
@@ -4702,6 +4742,22 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                         wc[k] = cnr[i];
                     }
                 }
+            } else if (touched && a.kept_idx == nullptr) {
+                // top-p / min-p counted the ids left in (nleft); the window
+                // sums of p from the numerators alone
+                double ws = 0.0;
+                wpass(pv, nW, G, [&](int w, int g, const float (&e)[8]) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) ws += (double)(e[j] * inv);
+                    if (g == G - 1) {
+                        ws = wave_sum_d(ws);
+                        if (lane == 0) {
+                            wq[w] = ws;
+                            wc[w] = 0u;
+                        }
+                        ws = 0.0;
+                    }
+                });
             } else {
                 double ws = 0.0;
                 int c = 0;
@@ -4741,7 +4797,7 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                 if (lane == 63) st.rd[wid] = incl;
                 int tot;
                 const int cex = fblock_excl_scan(c0 + c1, &tot, st);   // (its barriers publish st.rd)
-                nkept = tot;
+                nkept = (touched && a.kept_idx == nullptr) ? nleft : tot;
                 double base = 0.0;
                 Sd = 0.0;
                 for (int i = 0; i < kFW; ++i) {
@@ -4926,8 +4982,8 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
         float* row = static_cast<float*>(const_cast<void*>(a.logits)) + (int64_t)r * a.logits_stride;
         for (int i = tid; i < V; i += kFT) row[i] = fv[i];
     }
+    if (wid == 0) emit_token_wave(a, r, tok);
     if (tid == 0) {
-        emit_token(a, r, tok);
         if (a.row_flags != nullptr) a.row_flags[r] = rflags | ((st.flags & 4) ? ROWF_NAN : 0u);
         if (a.kept_count != nullptr) a.kept_count[r] = nkept;
     }

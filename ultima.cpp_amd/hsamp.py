@@ -286,6 +286,8 @@ def _batch(logits, params, u, hist, hist_len, mask, bias, writeback, want_sets, 
         b.kept_prob = out["kept_prob"].data_ptr()
         b.kept_count = out["kept_count"].data_ptr()
         b.set_cap = cap
+    elif "kept_count" in out:
+        b.kept_count = out["kept_count"].data_ptr()   # the count alone
     s = torch.cuda.current_stream(dev) if stream is None else stream
     return b, out, (parr, bids, bvals), s
 

@@ -704,10 +704,11 @@ __device__ __forceinline__ double block_excl_scan_d(double v, double* total, Sha
 
 // The reference's sequential float sum of v(i) over i < n, the same additions
 // in the same order, by one wave: lane l holds entries [16 l, 16 l + 16) of
-// each 1024-entry round, loaded together, and the running sum passes through
-// them by readlane (only the additions are sequential). With thr_on, stops at
-// the first entry after which the sum reaches thr and returns its position
-// (else -1); *sum gets the sum there (or the whole sum).
+// each 1024-entry round, loaded together; every lane adds its sixteen to the
+// running sum and a readlane hands lane l's result on (sixteen additions and
+// one readlane per lane, the additions of lane l the only ones kept). With
+// thr_on, stops at the first entry after which the sum reaches thr and
+// returns its position (else -1); *sum gets the sum there (or the whole sum).
 template <class Val>
 __device__ int wave_seq_sum_f(int n, Val v, bool thr_on, float thr, float* sum) {
     const int lane = lane_id();
@@ -721,24 +722,27 @@ __device__ int wave_seq_sum_f(int n, Val v, bool thr_on, float thr, float* sum) 
         }
         const int lanes = min(64, (n - c + 15) >> 4);
         for (int l = 0; l < lanes; ++l) {
-            float t[16];
+            float b = s;
 #pragma unroll
-            for (int j = 0; j < 16; ++j) t[j] = readlane_f(x[j], l);
-            const float s0 = s;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) s = s + t[j];
-            if (thr_on && s >= thr) {
-                // the first entry of these 16 after which the sum reaches thr
-                float s2 = s0;
+            for (int j = 0; j < 16; ++j) b = b + x[j];
+            const float s1 = readlane_f(b, l);
+            if (thr_on && s1 >= thr) {
+                // the first entry of lane l's sixteen after which the sum reaches thr
+                float s2 = s;
+                int hit = 16;
+                float at = 0.0f;
 #pragma unroll
                 for (int j = 0; j < 16; ++j) {
-                    s2 = s2 + t[j];
-                    if (s2 >= thr) {
-                        *sum = s2;
-                        return c + l * 16 + j;
+                    s2 = s2 + x[j];
+                    if (hit == 16 && s2 >= thr) {
+                        hit = j;
+                        at = s2;
                     }
                 }
+                *sum = readlane_f(at, l);
+                return c + l * 16 + __builtin_amdgcn_readlane(hit, l);
             }
+            s = s1;
         }
     }
     *sum = s;

@@ -444,6 +444,7 @@ def cli_main(args):
                    "sample": "the reference's sample() on one of the rows, one thread, median of 27 calls"}
     sampler.close()
     algo = B * (V * 4 + 12)
+    traffic, traffic_src = traffic_from_profiles("k_full", "cli") if B == 1 else (None, None)
     names = [n for bit, n in ((hs.KERNELS_EXACT, "exact"), (hs.KERNELS_GENERAL, "general"),
                               (hs.KERNELS_FULL, "full")) if kern & bit]
     line = {
@@ -460,12 +461,15 @@ def cli_main(args):
         "dtype": "f32",
         "data": "synthetic (seeded N(0, 2^2) rows, 8 rotating sets)",
         "config": {"workload": f"cli: B={B} V={V} identity() T .8", "rows": B, "vocab": V, "kernels": names,
-                   "us_per_step": round(ms * 1e3, 3), "bytes_per_step": algo},
+                   "us_per_step": round(ms * 1e3, 3), "bytes_per_step": algo,
+                   "kernel_us": {"step": round(ms * 1e3, 3)}},
         "roofline": {"bound": "hbm", "achieved": algo / (ms * 1e-3) / 1e9, "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": algo / (ms * 1e-3) / 1e9 / PEAK_GBS, "traffic": None, "kernel": "k_fs_* + k_full",
-                     "algorithmic_bytes_per_launch": algo},
+                     "frac": algo / (ms * 1e-3) / 1e9 / PEAK_GBS, "traffic": traffic, "traffic_source": traffic_src,
+                     "kernel": "k_fs_* + k_full (the step)", "algorithmic_bytes_per_launch": algo},
         "cpu_baseline": cpu,
     }
+    if args.copy_probe_mib > 0:
+        copy_probe(torch, dev, args.copy_probe_mib, line)
     print(json.dumps(line), flush=True)
 
 

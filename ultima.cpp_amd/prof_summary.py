@@ -10,7 +10,9 @@ Inputs are three rocprofv3 output folders of the same bench command:
 Writes <out>/<kernels>_<tag>_profile.md (kernel durations, traffic per
 kernel, the commands) and, for the workload's dominant kernel (the one that
 reads the logits, or the lm-head matvec), <out>/<kernel>_<tag>_traffic.json,
-which bench.py reads for roofline.traffic. <tag> is cfg1 .. cfg5, or head.
+which bench.py reads for roofline.traffic. <tag> is cfg1 .. cfg5, head or
+head_<type>, or cli (bench.py --workload cli: the step's kernels k_fs_max,
+k_fs_exp, k_fs_int and k_full taken together as its traffic).
 
     python3 ultima.cpp_amd/prof_summary.py --config 2 --stats DIR --fetch DIR --write DIR \
         --bench DIR/stats_bench.json --copy-mib 512 --out profiles --command "..."
@@ -26,7 +28,7 @@ from pathlib import Path
 
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
 STREAM_KERNEL = {"cfg1": "k_stream", "cfg2": "k_stream", "cfg3": "k_full", "cfg4": "k_stream", "cfg5": "k_stream",
-                 "head": "k_head_gemv"}
+                 "head": "k_head_gemv", "cli": "k_full"}
 
 
 def short(name: str) -> str:
@@ -59,7 +61,8 @@ def counter(folder: Path) -> dict[str, list[float]]:
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--config", required=True,
-                    help="1-5 (a sampler configuration), head (the bf16 head) or head_<type> (bench.py --head-dtype)")
+                    help="1-5 (a sampler configuration), head (the bf16 head), head_<type> (bench.py --head-dtype) "
+                         "or cli (bench.py --workload cli)")
     ap.add_argument("--stats", type=Path, required=True)
     ap.add_argument("--fetch", type=Path, required=True)
     ap.add_argument("--write", type=Path, required=True)
@@ -87,10 +90,16 @@ def main() -> None:
         hbm = None if f is None or w is None else (f * fs + w * ws) * 1024.0
         table.append((short(name), int(r["Calls"]), float(r["AverageNs"]) / 1000.0, f, w, hbm))
 
-    tag = a.config if a.config.startswith("head") else f"cfg{int(a.config)}"
+    tag = a.config if a.config.startswith("head") or a.config == "cli" else f"cfg{int(a.config)}"
     # head_<type>: a quantised head (k_head_q) or a dense one (k_head_gemv)
     sk = STREAM_KERNEL.get(tag, "k_head_gemv" if tag in ("head_f32", "head_bf16") else "k_head_q")
     main_row = next((t for t in table if t[0].startswith(sk + "<") and t[5] is not None), None)
+    if tag == "cli":
+        # the step's four kernels, each launched once per step
+        parts = [t for t in table if t[0].split("<")[0] in ("k_fs_max", "k_fs_exp", "k_fs_int", "k_full")]
+        if parts and all(t[5] is not None for t in parts):
+            main_row = ("k_fs_* + k_full", min(t[1] for t in parts), sum(t[2] for t in parts),
+                        sum(t[3] for t in parts), sum(t[4] for t in parts), sum(t[5] for t in parts))
     wl = bench["config"]["workload"]
     lines = [f"# rocprofv3 profile, workload {wl}", ""]
     lines += ["Commands (from the repository root on the GPU box):", ""]
@@ -108,11 +117,14 @@ def main() -> None:
                      f"{'' if w is None else f'{w:.1f}'} | {'' if hbm is None else f'{hbm:.0f}'} | {ratio} |")
     what = ("the head's weights, the hidden states, the norm scale, the normed rows and the logits, "
             "each once" if tag.startswith("head") else "each logit, history id and mask word read once, u and the token")
+    if main_row is not None and tag == "cli":
+        lines += [f"The step's kernels together: {main_row[5]:.0f} HBM bytes per step, "
+                  f"{main_row[5] / algo:.3f} x algorithmic, {main_row[2]:.2f} us of kernel time.", ""]
     lines += ["", f"Algorithmic bytes per step: {algo} ({what}).", ""]
     lines += ["Bench line of the stats run (timings perturbed by the tracer):", "",
               "    " + json.dumps({k: bench[k] for k in ("value", "ms_per_step")} |
-                                    {"kernel_us": bench["config"]["kernel_us"],
-                                     "ceiling_us": bench["roofline"].get("ceiling_us")}), ""]
+                                    {"kernel_us": bench["config"].get("kernel_us"),
+                                     "ceiling_us": (bench.get("roofline") or {}).get("ceiling_us")}), ""]
     a.out.mkdir(parents=True, exist_ok=True)
     kernels = []
     for n, *_ in table:

@@ -4,7 +4,11 @@
 //   out[0]  its sequential float32 sum in index order (exact_index_sum),
 // and, when thr > 0, the top-p driver's answer for x as probabilities:
 //   outi[0] whether the running sum in descending order reaches thr,
-//   outi[1] how many values that takes, out[1] the last one, out[2] the sum.
+//   outi[1] how many values that takes, out[1] the last one, out[2] the sum,
+//   outi[2] how many values are larger than the last one, outi[3] how many
+//   equal it.
+// rlo / rhi: the smallest and largest float bits above 0 in x when the caller
+// gives them (rhi 0: the driver finds them).
 // tests/test_gpu_xsum.py compares them with numpy's sequential float32 sums.
 #include <hip/hip_runtime.h>
 
@@ -12,8 +16,8 @@
 
 using namespace hsamp;
 
-__global__ __launch_bounds__(kFT) void k_xsum(const float* x, int n, int Vp, int G, float thr, float* out, int* outi,
-                                              uint32_t* fk) {
+__global__ __launch_bounds__(kFT) void k_xsum(const float* x, int n, int Vp, int G, float thr, uint32_t rlo,
+                                              uint32_t rhi, float* out, int* outi) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ FullShared st;
     const FullLds f = full_lds(smem);
@@ -30,19 +34,22 @@ __global__ __launch_bounds__(kFT) void k_xsum(const float* x, int n, int Vp, int
     if (threadIdx.x == 0) out[0] = xs_value(s);
     if (thr > 0.0f) {
         uint32_t ck = 0u;
-        int cc = 0;
-        const bool ok = full_top_p(x, n, Vp, 1.0f, thr, fk, f, st, &ck, &cc);
+        int cc = 0, cg = 0, ce = 0;
+        const bool ok = full_top_p(x, n, Vp, 1.0f, thr, f, st, rlo, rhi, &ck, &cc, &cg, &ce);
         if (threadIdx.x == 0) {
             outi[0] = ok ? 1 : 0;
             outi[1] = cc;
+            outi[2] = cg;
+            outi[3] = ce;
             out[1] = __uint_as_float(ck);
             out[2] = (float)st.dS;
         }
     }
 }
 
-extern "C" int xsum_run(const float* x, int n, int Vp, int G, float thr, float* out, int* outi, uint32_t* fk) {
-    hipLaunchKernelGGL(k_xsum, dim3(1), dim3(kFT), kFullLdsBytes, nullptr, x, n, Vp, G, thr, out, outi, fk);
+extern "C" int xsum_run(const float* x, int n, int Vp, int G, float thr, uint32_t rlo, uint32_t rhi, float* out,
+                        int* outi) {
+    hipLaunchKernelGGL(k_xsum, dim3(1), dim3(kFT), kFullLdsBytes, nullptr, x, n, Vp, G, thr, rlo, rhi, out, outi);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
     return (int)hipDeviceSynchronize();

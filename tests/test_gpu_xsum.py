@@ -23,11 +23,11 @@ def _kit(pkg):
     lib = ctypes.CDLL(str(pkg.hsamp.PKG.parent / "tests" / "cpp" / "libxsum_kit.so"))
     lib.xsum_run.restype = ctypes.c_int
     lib.xsum_run.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float,
-                             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+                             ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]
     return lib
 
 
-def _run(kit, x, thr):
+def _run(kit, x, thr, known_range=False):
     import torch
     n = x.size
     w512 = (n + 511) // 512
@@ -40,8 +40,11 @@ def _run(kit, x, thr):
     xd = torch.from_numpy(xp).to(dev)
     out = torch.zeros(4, dtype=torch.float32, device=dev)
     outi = torch.zeros(4, dtype=torch.int32, device=dev)
-    fk = torch.zeros(max(n, 1), dtype=torch.int32, device=dev)
-    rc = kit.xsum_run(xd.data_ptr(), n, Vp, G, float(thr), out.data_ptr(), outi.data_ptr(), fk.data_ptr())
+    rlo = rhi = 0
+    if known_range and np.any(x > 0):
+        pos = x[x > 0]
+        rlo, rhi = int(pos.min().view(np.uint32)), int(pos.max().view(np.uint32))
+    rc = kit.xsum_run(xd.data_ptr(), n, Vp, G, float(thr), rlo, rhi, out.data_ptr(), outi.data_ptr())
     assert rc == 0, f"xsum_run: HIP status {rc}"
     return out.cpu().numpy(), outi.cpu().numpy()
 
@@ -87,15 +90,16 @@ def test_exact_index_sum(pkg, name):
     assert out[0].view(np.uint32) == want.view(np.uint32), f"{name}: {out[0]!r} != {want!r}"
 
 
+@pytest.mark.parametrize("known_range", [False, True])
 @pytest.mark.parametrize("name", [n for n in CASES if n not in ("long", "tiny")])
 @pytest.mark.parametrize("frac", [0.9, 0.5, 0.999])
-def test_top_p_cutoff(pkg, name, frac):
+def test_top_p_cutoff(pkg, name, frac, known_range):
     kit = _kit(pkg)
     x = CASES[name]
     xs = np.sort(x)[::-1]
     cum = _seq(xs)
     thr = np.float32(frac * float(cum[-1]))
-    out, outi = _run(kit, x, float(thr))
+    out, outi = _run(kit, x, float(thr), known_range)
     hit = np.nonzero(cum >= thr)[0]
     assert outi[0] == (1 if hit.size else 0), name
     if hit.size:
@@ -103,3 +107,6 @@ def test_top_p_cutoff(pkg, name, frac):
         assert outi[1] == j + 1, f"{name}: cut after {outi[1]} values, want {j + 1}"
         assert out[1].view(np.uint32) == xs[j].view(np.uint32), name
         assert out[2].view(np.uint32) == cum[j].view(np.uint32), name
+        # the values above the cut's and equal to it (the removal's tie rule)
+        assert outi[2] == int(np.count_nonzero(x > xs[j])), name
+        assert outi[3] == int(np.count_nonzero(x == xs[j])), name

@@ -93,8 +93,6 @@ struct ultima_hsamp {
     size_t fullv_elems = 0;
     float* fullp = nullptr;              // full-vocabulary rows: probabilities
     size_t fullp_elems = 0;
-    uint32_t* fullk = nullptr;           // full-vocabulary rows: top-p keys
-    size_t fullk_elems = 0;
     uint32_t* fs_tab = nullptr;          // full-vocabulary rows: k_fs_* per-window tables
     size_t fs_elems = 0;
     // A graph captured from this handle holds the scratch pointers of its
@@ -547,14 +545,12 @@ int plan_run(const DevCaps& dc, const ultima_hsamp_batch* b, const Built& bl, Ru
     if (rp.wb && gtab) exact = false;
     rp.exact = exact;
     rp.merge_lds = merge_lds;
-    rp.full_p2 = next_pow2(V);
     // scratch
     rp.cand_slots = (size_t)nblocks;
     rp.cand_elems = (size_t)nblocks * (size_t)cand_cap;
     rp.ovf_elems = (size_t)B * kMergeRound;
     rp.gtab_words = gtab ? (size_t)B * 2 * mhash : 0;
     rp.full_elems = bl.any_full ? (size_t)B * rp.full_stride : 0;
-    rp.fullk_elems = bl.any_full ? (size_t)B * rp.full_p2 : 0;
     {
         // per-window tables of every row, then (16-byte aligned) 64 lane entries of 4 words per window
         const size_t nWf = (size_t)(rp.full_stride / (512 * rp.full_g));
@@ -621,9 +617,7 @@ int launch_run(const RunPlan& rp, const Built& bl, const ultima_hsamp_batch* b, 
     a.pen_flag = rp.pen_flag ? 1 : 0;
     a.fullv = buf.fullv;
     a.fullp = buf.fullp;
-    a.fullk = buf.fullk;
     a.fs_tab = buf.fs_tab;
-    a.full_p2 = rp.full_p2;
     a.full_stride = rp.full_stride;
     a.full_g = rp.full_g;
     a.gtab = rp.gtab ? buf.gtab : nullptr;
@@ -869,7 +863,7 @@ int ultima_hsamp_destroy(ultima_hsamp* h) {
         if (s.ev) (void)hipEventDestroy(s.ev);
     }
     for (void* p : {(void*)h->ovf, (void*)h->cand, (void*)h->cand_n,
-                    (void*)h->gtab, (void*)h->fullv, (void*)h->fullp, (void*)h->fullk, (void*)h->fs_tab,
+                    (void*)h->gtab, (void*)h->fullv, (void*)h->fullp, (void*)h->fs_tab,
                     (void*)h->fin_idx,
                     (void*)h->fin_n, (void*)h->d_row, (void*)h->d_hist, (void*)h->d_u, (void*)h->d_tok})
         if (p) (void)hipFree(p);
@@ -928,7 +922,6 @@ int run_impl(ultima_hsamp* h, const ultima_hsamp_batch* b, const ultima_hsamp_co
     if (st == ULTIMA_HSAMP_OK && rp.full_elems) {
         st = grow(h, capturing, h->fullv, h->fullv_elems, rp.full_elems);
         if (st == ULTIMA_HSAMP_OK) st = grow(h, capturing, h->fullp, h->fullp_elems, rp.full_elems);
-        if (st == ULTIMA_HSAMP_OK) st = grow(h, capturing, h->fullk, h->fullk_elems, rp.fullk_elems);
         if (st == ULTIMA_HSAMP_OK && rp.fs_elems) st = grow(h, capturing, h->fs_tab, h->fs_elems, rp.fs_elems);
     }
     if (st != ULTIMA_HSAMP_OK) return st;
@@ -946,7 +939,6 @@ int run_impl(ultima_hsamp* h, const ultima_hsamp_batch* b, const ultima_hsamp_co
     buf.gtab = h->gtab;
     buf.fullv = h->fullv;
     buf.fullp = h->fullp;
-    buf.fullk = h->fullk;
     buf.fs_tab = h->fs_tab;
     buf.fin_idx = h->fin_idx;
     buf.fin_n = h->fin_n;

@@ -407,21 +407,6 @@ __device__ void drain_overflow(u64* buf, int cap, int k, const u64* ovf, Shared&
     append_fetch(buf, cap, k, n - cap, [&](int j) { return ovf[j]; }, st);
 }
 
-// The 64-bit value of lane (lane ^ M): DPP quad permutes for M = 1, 2, the
-// swizzle's xor mode (within 32 lanes, no LDS memory) up to 16, a permute
-// for 32.
-template <int M>
-__device__ __forceinline__ uint32_t xor_lane_u32(uint32_t x) {
-    if constexpr (M == 1) return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xF, 0xF, false);
-    else if constexpr (M == 2) return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x4E, 0xF, 0xF, false);
-    else if constexpr (M <= 16) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)x, (M << 10) | 0x1F);
-    else return (uint32_t)__shfl_xor((int)x, M, 64);
-}
-template <int M>
-__device__ __forceinline__ u64 xor_lane_u64(u64 x) {
-    return ((u64)xor_lane_u32<M>((uint32_t)(x >> 32)) << 32) | xor_lane_u32<M>((uint32_t)x);
-}
-
 // Bitonic sort of 1024 keys held four per thread in registers (thread t:
 // entries 4t .. 4t+3). A stage of distance J joins entry i with i ^ J: J <= 2
 // inside a thread, 4 <= J <= 128 between the lanes of a wave (lane distance
@@ -4174,9 +4159,10 @@ __device__ void full_exp(const float* fv, float* pv, float m, int nW, int G, Ful
 //             each window's maximum, whether it held a NaN and how many ids
 //             it leaves in;
 //   k_fs_exp: the row's maximum m, the numerators expf(x - m) into fullp and
-//             each window's approximate sum (as full_exp forms it) and its
-//             sum in double (the draw's window prefixes when top-p and min-p
-//             remove nothing);
+//             each window's approximate sum (as full_exp forms it), its sum
+//             in double (the draw's window prefixes when top-p and min-p
+//             remove nothing) and its smallest numerator above 0 (top-p's
+//             key range);
 //   k_fs_int: each window's binade, predicted from the approximate sums
 //             before it, and its values' integer increments there (as
 //             exact_index_sum forms them).
@@ -4268,6 +4254,7 @@ __global__ __launch_bounds__(64) void k_fs_exp(StreamArgs a) {
     float* pv = a.fullp + (size_t)r * a.full_stride;
     float ws = 0.0f;
     double wd = 0.0;
+    uint32_t emn = 0xFFFFFFFFu;
     for (int g = 0; g < G; ++g) {
         const int i0 = w * WS + g * kFWin + lane * 8;
         const float4 c0 = reinterpret_cast<const float4*>(fv + i0)[0], c1 = reinterpret_cast<const float4*>(fv + i0)[1];
@@ -4278,6 +4265,7 @@ __global__ __launch_bounds__(64) void k_fs_exp(StreamArgs a) {
             v[j] = (x[j] == -__builtin_inff() || m == -__builtin_inff()) ? 0.0f : libm_expf_t(x[j] - m, expT);
             ws += v[j];
             wd += (double)v[j];
+            emn = min(emn, v[j] > 0.0f ? __float_as_uint(v[j]) : 0xFFFFFFFFu);
         }
         float4* dst = reinterpret_cast<float4*>(pv + i0);
         dst[0] = make_float4(v[0], v[1], v[2], v[3]);
@@ -4285,9 +4273,11 @@ __global__ __launch_bounds__(64) void k_fs_exp(StreamArgs a) {
     }
     ws = wave_tree_prefix_f(ws);
     wd = wave_tree_prefix_d(wd);
+    emn = wave_min_u32(emn);
     if (lane == 63) {
         fs_table(a, r, FS_A)[w] = __float_as_uint(ws);
         reinterpret_cast<double*>(fs_table(a, r, FS_SD))[w] = wd;
+        fs_table(a, r, FS_EMIN)[w] = emn;
     }
 }
 
@@ -4360,7 +4350,6 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
     const int Vp = a.full_stride, nW = Vp / WS;
     float* fv = a.fullv + (size_t)r * Vp;
     float* pv = a.fullp + (size_t)r * Vp;
-    uint32_t* fk = a.fullk + (size_t)r * a.full_p2;
     const bool pen = !PRE && (P.flags & (RF_REP | RF_DRY | RF_FP | RF_BIAS)) != 0;
     const bool masked = !PRE && (P.flags & RF_MASK) != 0;
     const PenaltyLds pl = pen_table<GT>(a, r, smem);
@@ -4445,6 +4434,7 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
     static_assert(kFMaxWin <= 2 * kFT, "two windows per thread");
     double sdr[2] = {0.0, 0.0};   // PRE: the draw's window sums of the numerators ...
     uint32_t cnr[2] = {0u, 0u};   // ... and counts (windows tid, tid + kFT)
+    uint32_t emn = 0xFFFFFFFFu;   // PRE: the smallest numerator above 0 of those windows
     if constexpr (PRE) {
         // k_fs_* transformed the row and left its window tables, all loaded at
         // once: maxima and NaN flags for the row's maximum, the exact sum's
@@ -4456,6 +4446,7 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
         const uint32_t* w1 = fs_table(a, r, FS_D1);
         const double* wsd = reinterpret_cast<const double*>(fs_table(a, r, FS_SD));
         const uint32_t* wcn = fs_table(a, r, FS_CNT);
+        const uint32_t* wen = fs_table(a, r, FS_EMIN);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int k = tid + i * kFT;
@@ -4463,6 +4454,7 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                 const uint32_t mx = wm[k], nn = wn[k], ef = we[k], d0 = w0[k], d1 = w1[k];
                 sdr[i] = wsd[k];
                 cnr[i] = wcn[k];
+                if (!PLAIN) emn = min(emn, wen[k]);
                 mloc = fmaxf(mloc, __uint_as_float(mx));
                 nanv |= nn != 0u;
                 f.winEF[k] = ef;
@@ -4573,19 +4565,21 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
         // ---- top-p (sampler.cpp:146-164) ----
         if (!PLAIN && (P.flags & RF_TOPP)) {
             uint32_t cut_key = 0u;
-            int cut_count = 0;
+            int cut_count = 0, ngt = 0, neq = 0;
             const float inv = 1.0f / S;
-            if (full_top_p(pv, V, Vp, inv, P.top_p, fk, f, st, &cut_key, &cut_count)) {
+            // the key range: from the smallest numerator above 0 (k_fs_exp's
+            // window minima) to the largest, expf(0) = 1, whose p is inv
+            uint32_t rlo = 0u, rhi = 0u;
+            if (pre) {
+                const float plo = __uint_as_float(fblock_min_u(emn, st)) * inv;
+                if (plo > 0.0f) {
+                    rlo = __float_as_uint(plo);
+                    rhi = __float_as_uint(inv);
+                }
+            }
+            if (full_top_p(pv, V, Vp, inv, P.top_p, f, st, rlo, rhi, &cut_key, &cut_count, &ngt, &neq)) {
                 if (fabs(st.dS - (double)P.top_p) <= 1e-6) rflags |= ROWF_TOPP_NEAR;
                 // kept: p > p*, and the lowest ids with p == p* up to cut_count
-                int gt = 0, eq = 0;
-                fpass(pv, Vp, [&](int, float e) {
-                    const uint32_t key = __float_as_uint(e * inv);
-                    gt += key > cut_key;
-                    eq += key == cut_key;
-                });
-                const int ngt = fblock_sum_i(gt, st);
-                const int neq = fblock_sum_i(eq, st);
                 const int need = cut_count - ngt;
                 nleft = cut_count;
                 // the largest logit's p is fl(1 * inv) = inv: it stays in unless

@@ -145,7 +145,7 @@ extern "C" int ultima_hsamp_run_noalloc(const ultima_hsamp_batch* b, void* hip_s
     if (st != ULTIMA_HSAMP_OK) return st;
 
     // The array's layout for this run: [plans' region][slice counts + bounds]
-    // [candidate lists][overflow][penalty tables][fullv][fullp][fullk][kept ids][kept counts]
+    // [candidate lists][overflow][penalty tables][fullv][fullp][k_fs_* tables][kept ids][kept counts]
     size_t off = kPlanBytes;
     auto take = [&](size_t bytes) -> unsigned char* {
         unsigned char* p = d->ptr + off;
@@ -161,7 +161,6 @@ extern "C" int ultima_hsamp_run_noalloc(const ultima_hsamp_batch* b, void* hip_s
     if (rp.full_elems) {
         buf.fullv = reinterpret_cast<float*>(take(rp.full_elems * 4));
         buf.fullp = reinterpret_cast<float*>(take(rp.full_elems * 4));
-        buf.fullk = reinterpret_cast<uint32_t*>(take(rp.fullk_elems * 4));
     }
     if (rp.fs_elems) buf.fs_tab = reinterpret_cast<uint32_t*>(take(rp.fs_elems * 4));
     if (rp.fin_elems) {

@@ -40,11 +40,12 @@ enum : uint32_t {
 // k_fs_* per-row tables, nW entries each (nW = full_stride / (512 * full_g)):
 // window maxima, NaN seen, approximate window sums of the numerators, the
 // windows' predicted binades / integer increments for the exact sum, their
-// numerators' sums in double (two entries' space: FS_SD and the one after)
-// and their counts of ids left in (transformed logit above -inf). An even
-// number of tables keeps the doubles 8-byte aligned.
+// numerators' sums in double (two entries' space: FS_SD and the one after),
+// their counts of ids left in (transformed logit above -inf) and their
+// smallest numerator above 0 (float bits; all ones when none). An even number
+// of tables keeps the doubles 8-byte aligned.
 enum : int {
-    FS_MAX = 0, FS_NAN = 1, FS_A = 2, FS_EF = 3, FS_D0 = 4, FS_D1 = 5, FS_SD = 6, FS_CNT = 8, FS_TABLES = 10
+    FS_MAX = 0, FS_NAN = 1, FS_A = 2, FS_EF = 3, FS_D0 = 4, FS_D1 = 5, FS_SD = 6, FS_CNT = 8, FS_EMIN = 9, FS_TABLES = 10
 };
 
 // Hash-table value bits for one token of a slice (penalty bookkeeping).
@@ -147,8 +148,6 @@ struct StreamArgs {
                                 // loads whole rows before the tile, without waiting for the plan
     float* fullv;               // [rows * full_stride] k_full: transformed logits (-inf once removed)
     float* fullp;               // [rows * full_stride] k_full: softmax numerators
-    uint32_t* fullk;            // [rows * full_p2] k_full: top-p keys by bucket
-    int32_t full_p2;            // next power of two >= vocab
     int32_t full_stride;        // k_full: floats per row of fullv / fullp (whole windows of 512 * full_g)
     int32_t full_g;             // k_full: 512-id steps per index-order window
     uint32_t* fs_tab;           // [rows * FS_TABLES * nW] k_fs_* results for k_full's RF_FPRE rows, then

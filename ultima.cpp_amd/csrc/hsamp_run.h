@@ -70,7 +70,7 @@ struct Built {
 struct RunPlan {
     int B = 0, V = 0, S = 1, slice_len = 0, kmax = 1;
     int cand_cap = 0, buf_cap = 0, bitmap_words = 0, mhash = 16, win = 1, pick_nw = 16;
-    int ex_tiles = 1, grid = 0, full_p2 = 1, full_stride = 0, full_g = 1;
+    int ex_tiles = 1, grid = 0, full_stride = 0, full_g = 1;
     bool exact = false, vec = false, gtab = false, fast = false, pen_flag = false, wb = false;
     bool cnt_ranked = false;  // exact lists: history counts by rank (a bitmap over the slice)
     size_t lds = 0, lds_ex = 0, merge_lds = 0, full_lds = 0, wb_lds = 0, cnt_bytes = 0, stage_off = 0;
@@ -80,7 +80,6 @@ struct RunPlan {
     size_t ovf_elems = 0;     // u64 per-row overflow of k_merge's / k_pick's LDS buffer
     size_t gtab_words = 0;    // uint32 per-row penalty tables (0 when in LDS)
     size_t full_elems = 0;    // f32 fullv and fullp, B * V each (k_full rows)
-    size_t fullk_elems = 0;   // uint32 k_full sort scratch
     size_t fin_elems = 0;     // int32 kept ids for write-back, B * kLimitK (and B counts)
     size_t fs_elems = 0;      // uint32 k_fs_* per-window tables, B * FS_TABLES * windows, then B * windows * 256 lane words
 };
@@ -94,7 +93,6 @@ struct RunBuffers {
     uint32_t* gtab = nullptr;
     float* fullv = nullptr;
     float* fullp = nullptr;
-    uint32_t* fullk = nullptr;
     uint32_t* fs_tab = nullptr;
     int32_t* fin_idx = nullptr;
     int32_t* fin_n = nullptr;

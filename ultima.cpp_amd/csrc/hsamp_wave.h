@@ -110,6 +110,21 @@ __device__ __forceinline__ float wave_max_f(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// The value of lane (lane ^ M): DPP quad permutes for M = 1, 2, the
+// swizzle's xor mode (within 32 lanes, no LDS memory) up to 16, a permute
+// for 32.
+template <int M>
+__device__ __forceinline__ uint32_t xor_lane_u32(uint32_t x) {
+    if constexpr (M == 1) return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xF, 0xF, false);
+    else if constexpr (M == 2) return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x4E, 0xF, 0xF, false);
+    else if constexpr (M <= 16) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)x, (M << 10) | 0x1F);
+    else return (uint32_t)__shfl_xor((int)x, M, 64);
+}
+template <int M>
+__device__ __forceinline__ u64 xor_lane_u64(u64 x) {
+    return ((u64)xor_lane_u32<M>((uint32_t)(x >> 32)) << 32) | xor_lane_u32<M>((uint32_t)x);
+}
+
 // Orders the wave's LDS accesses around a cross-lane exchange. LDS operations
 // of one wave complete in program order; the fences keep the compiler from
 // moving accesses across.

@@ -22,7 +22,7 @@ __device__ __forceinline__ void g_phase_lv(int, int) {}
 // whole transformed row goes through softmax, top-p, min-p and the draw
 // (sampler.cpp:109-182). One block of kFT threads per row; the row's
 // transformed logits and softmax numerators live in global scratch (fullv,
-// fullp, padded to whole windows), the top-p keys in fullk.
+// fullp, padded to whole windows).
 //
 // Exact sequential float sums. softmax_probs (sampler.cpp:124-142) divides by
 // a float sum taken in index order, and apply_top_p (:146-164) compares a
@@ -161,6 +161,7 @@ struct FullShared {
     int fpos;          // ... at this position of the group order (group start + offset)
     uint32_t fkey;     // ... by a value with this key
     int fgroup;        // ... in this group
+    int fgt, feq;      // ... after fgt (group start + offset) larger keys, with feq of that key
     int redo;
     double dS;
     float m;
@@ -529,16 +530,16 @@ struct FullLds {
     uint32_t* winEF;    // [kFMaxWin]
     uint32_t* gath;     // [kFGather] top-p: keys of the buckets replayed value by value (the window tables' space)
     uint32_t* bcnt;     // [kFNB + 1] bucket counts, then starts
-    uint32_t* bfill;    // [kFNB] fill positions (global scatter)
+    uint32_t* bfill;    // [kFNB] (space only: the index-order compose stages windows over bcnt .. gfill)
     uint32_t* bD;       // [kFNB]
     uint32_t* bEF;      // [kFNB]
     uint32_t* gst;      // [kFNB] start of the bucket's keys in gath, or kNoGath
     uint32_t* gfill;    // [kFNB] their fill positions
-    uint32_t* sortb;    // [kFSort]
+    uint32_t* sortb;    // [kFSort] one bucket's keys, sorted
 };
 constexpr int kFGather = 4 * kFMaxWin;
 constexpr uint32_t kNoGath = 0xFFFFFFFFu;
-constexpr size_t kFullLdsBytes = 4 * 4 * kFMaxWin + 4 * (kFNB + 1) + 5 * 4 * kFNB + 4 * kFSort + 64;
+constexpr size_t kFullLdsBytes = 4 * (((4 * kFMaxWin + kFNB + 1 + 5 * kFNB + 3) & ~3) + kFSort) + 64;
 
 __device__ __forceinline__ FullLds full_lds(unsigned char* base) {
     FullLds f;
@@ -554,7 +555,7 @@ __device__ __forceinline__ FullLds full_lds(unsigned char* base) {
     f.bEF = f.bfill + 2 * kFNB;
     f.gst = f.bfill + 3 * kFNB;
     f.gfill = f.bfill + 4 * kFNB;
-    f.sortb = f.bfill + 5 * kFNB;
+    f.sortb = p + ((4 * kFMaxWin + kFNB + 1 + 5 * kFNB + 3) & ~3);   // (16-byte aligned)
     return f;
 }
 
@@ -884,49 +885,115 @@ __device__ __forceinline__ XState exact_index_compose(const float* x, int nW, in
     return st.xs;
 }
 
-// Sorts a[0, n) descending in LDS by one wave (n <= kFSort): a rank placement
-// for n <= 64, else a bitonic network over the next power of two (padding 0).
-__device__ void wave_sort_desc_lds(uint32_t* a, int n) {
+// Bitonic sort, descending, of 64 Q keys held Q per lane (position t * 64 +
+// lane in v[t]): a stage of distance J joins position e with e ^ J, across
+// lanes for J < 64 (xor_lane_u32), inside a lane for J >= 64. In a run of
+// size K that descends (e & K == 0) the lower position keeps the larger key.
+template <int Q, int K, int J>
+__device__ __forceinline__ void bsort_stage(uint32_t (&v)[Q]) {
     const int lane = lane_id();
-    if (n <= 64) {
-        const uint32_t k = lane < n ? a[lane] : 0u;
-        wave_sync();
-        const uint4* a4 = reinterpret_cast<const uint4*>(a);
-        int rank = 0;
-        for (int q = 0; q < 16; ++q) {
-            const uint4 y = a4[q];
-            const uint32_t ys[4] = {y.x, y.y, y.z, y.w};
+    if constexpr (J >= 64) {
+        constexpr int JJ = J / 64;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int i = 4 * q + c;
-                const uint32_t yv = i < n ? ys[c] : 0u;
-                rank += (yv > k) || (yv == k && i < lane);
+        for (int t = 0; t < Q; ++t) {
+            if ((t & JJ) == 0) {
+                const bool desc = ((t * 64) & K) == 0;
+                const uint32_t a = v[t], b = v[t | JJ];
+                v[t] = desc ? max(a, b) : min(a, b);
+                v[t | JJ] = desc ? min(a, b) : max(a, b);
             }
         }
-        wave_sync();
-        if (lane < n) a[rank] = k;
-        wave_sync();
-        return;
-    }
-    int P2 = 128;
-    while (P2 < n) P2 <<= 1;
-    for (int i = n + lane; i < P2; i += 64) a[i] = 0u;
-    for (int k = 2; k <= P2; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            wave_sync();
-            for (int t = lane; t < P2 / 2; t += 64) {
-                const int i = ((t & ~(j - 1)) << 1) | (t & (j - 1));
-                const int l = i | j;
-                const uint32_t x = a[i], y = a[l];
-                const bool desc = (i & k) == 0;
-                if (desc ? (x < y) : (x > y)) {
-                    a[i] = y;
-                    a[l] = x;
-                }
-            }
+    } else {
+        const bool lower = (lane & J) == 0;
+#pragma unroll
+        for (int t = 0; t < Q; ++t) {
+            const bool desc = ((t * 64 + lane) & K) == 0;
+            const uint32_t o = xor_lane_u32<J>(v[t]);
+            v[t] = (lower == desc) ? max(v[t], o) : min(v[t], o);
         }
     }
+}
+template <int Q, int K, int J>
+__device__ __forceinline__ void bsort_steps(uint32_t (&v)[Q]) {
+    bsort_stage<Q, K, J>(v);
+    if constexpr (J > 1) bsort_steps<Q, K, J / 2>(v);
+}
+template <int Q, int K = 2>
+__device__ __forceinline__ void bsort_all(uint32_t (&v)[Q]) {
+    bsort_steps<Q, K, K / 2>(v);
+    if constexpr (K < 64 * Q) bsort_all<Q, 2 * K>(v);
+}
+// src[0, n) sorted descending into dst[0, n) by one wave (n <= 64 Q), in
+// registers (padding 0, below every key).
+template <int Q>
+__device__ __forceinline__ void wave_bitonic_to(const uint32_t* src, int n, uint32_t* dst) {
+    const int lane = lane_id();
+    uint32_t v[Q];
+#pragma unroll
+    for (int t = 0; t < Q; ++t) v[t] = t * 64 + lane < n ? src[t * 64 + lane] : 0u;
+    bsort_all<Q>(v);
+#pragma unroll
+    for (int t = 0; t < Q; ++t)
+        if (t * 64 + lane < n) dst[t * 64 + lane] = v[t];
     wave_sync();
+}
+__device__ __forceinline__ void wave_sort_desc_to(const uint32_t* src, int n, uint32_t* dst) {
+    if (n <= 64) wave_bitonic_to<1>(src, n, dst);
+    else if (n <= 128) wave_bitonic_to<2>(src, n, dst);
+    else if (n <= 256) wave_bitonic_to<4>(src, n, dst);
+    else wave_bitonic_to<8>(src, n, dst);
+}
+
+// Replays keys[0, n) (floats as bits, in that order) onto s as float adds --
+// the sum they define, whatever binades it crosses: the running sum handed
+// from lane to lane (eight adds, then a readlane, per lane holding values).
+// Stops at the first value after which the sum reaches thr: returns its
+// position (s is the sum there), else -1 (s is the sum of all n).
+__device__ int chain_replay(XState& s, const uint32_t* keys, int n, float thr) {
+    const int lane = lane_id();
+    const lds_u32* kl = (const lds_u32*)keys;
+    for (int o = 0; o < n; o += 512) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int e = o + lane * 8 + j;
+            v[j] = e < n ? __uint_as_float(kl[e]) : 0.0f;   // (+0 leaves a sum >= 0 as it is)
+        }
+        const int nl = min(64, (n - o + 7) >> 3);
+        float acc = xs_value(s), start = 0.0f;
+        for (int l = 0; l < nl; ++l) {
+            float b = acc;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) b = b + v[j];
+            start = lane == l ? acc : start;
+            acc = readlane_f(b, l);
+        }
+        // the first value whose sum reaches thr: each lane's adds again from its start
+        float c = start, cat = 0.0f;
+        int first = 8;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            c = c + v[j];
+            if (first == 8 && lane < nl && c >= thr) {
+                first = j;
+                cat = c;
+            }
+        }
+        const u64 hm = __ballot(first < 8);
+        if (hm != 0ull) {
+            const int L = __ffsll((long long)hm) - 1;
+            int ex;
+            uint32_t X;
+            fparts(readlane_f(cat, L), ex, X);
+            s = XState{ex, X};
+            return o + L * 8 + __builtin_amdgcn_readlane(first, L);
+        }
+        int ex;
+        uint32_t X;
+        fparts(acc, ex, X);
+        s = XState{ex, X};
+    }
+    return -1;
 }
 
 // The row's top-p cutoff (sampler.cpp:146-164) over the probabilities
@@ -944,23 +1011,30 @@ __device__ void wave_sort_desc_lds(uint32_t* a, int n) {
 // is when all its keys are equal). Buckets flagged by the pass but not
 // copied are copied by one more pass, any other bucket on demand; one too
 // large to sort is refined (its key range becomes the next [lo, hi]), and a
-// range that runs out continues below it. Returns whether the running sum
-// reached top_p; then *cut_key is the key of the last kept value, *cut_count
-// the number kept and st.dS the sum there.
-__device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_p, uint32_t* fk, FullLds f,
-                           FullShared& st, uint32_t* cut_key, int* cut_count) {
+// range that runs out continues below it. A bucket replayed value by value
+// is sorted, then added as floats in that order. Returns whether the running sum reached top_p; then
+// *cut_key is the key of the last kept value, *cut_count the number kept,
+// *cut_gt the number with a larger key, *cut_eq the number with that key and
+// st.dS the sum there. range_lo / range_hi: the smallest and largest keys
+// above 0 when the caller knows them (range_hi 0: one more pass finds them).
+__device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_p, FullLds f, FullShared& st,
+                           uint32_t range_lo, uint32_t range_hi, uint32_t* cut_key, int* cut_count, int* cut_gt,
+                           int* cut_eq) {
     const int tid = threadIdx.x, lane = lane_id(), wid = wave_id();
-    (void)fk;
-    uint32_t kmx = 0u, kmn = 0xFFFFFFFFu;
-    fpass(pv, Vp, [&](int, float e) {
-        const uint32_t key = __float_as_uint(e * inv);
-        if (key != 0u) {
-            kmx = max(kmx, key);
-            kmn = min(kmn, key);
-        }
-    });
-    kmx = fblock_max_u(kmx, st);
-    kmn = fblock_min_u(kmn, st);
+    uint32_t kmx = range_hi, kmn = range_lo;
+    if (range_hi == 0u) {
+        kmx = 0u;
+        kmn = 0xFFFFFFFFu;
+        fpass(pv, Vp, [&](int, float e) {
+            const uint32_t key = __float_as_uint(e * inv);
+            if (key != 0u) {
+                kmx = max(kmx, key);
+                kmn = min(kmn, key);
+            }
+        });
+        kmx = fblock_max_u(kmx, st);
+        kmn = fblock_min_u(kmn, st);
+    }
     HSAMP_PHASE(13000 + blockIdx.x, 0);
     if (kmx == 0u) return false;
     XState s{-126, 0u};
@@ -1012,7 +1086,6 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
                 gq[q] = false;
                 if (b < nb) {
                     f.bcnt[b] = cpos;
-                    f.bfill[b] = cpos;
                     // more than 255 values: the increment sum could wrap
                     const uint32_t fl = (c[q] == 0u ? kGEmpty : 0u) | (c[q] > 255u ? kGCare : 0u);
                     const int E = xs_binade(apos);
@@ -1131,6 +1204,8 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
                                     st.found = 1;
                                     st.fpos = (int)(b0 + o) + pos;
                                     st.fkey = hi - (uint32_t)b;
+                                    st.fgt = (int)b0;
+                                    st.feq = (int)n;
                                     st.xs = sv;
                                 }
                                 return true;
@@ -1153,32 +1228,30 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
                         }
                         return true;
                     }
-                    // sort the bucket's keys (n <= kFSort), then replay them in order
-                    const uint32_t* keys = f.gath + gs;
-                    for (uint32_t e = lane; e < n; e += 64) f.sortb[e] = keys[e];
-                    wave_sort_desc_lds(f.sortb, (int)n);
-                    keys = f.sortb;
-                    for (uint32_t o = 0; o < n; o += 512) {
-                        float v[8];
-#pragma unroll
-                        for (int j = 0; j < 8; ++j) {
-                            const uint32_t e = o + lane * 8 + j;
-                            v[j] = e < n ? __uint_as_float(keys[e]) : 0.0f;
-                        }
-                        const int pos = xs_replay(sv, v, 0, true, top_p);
-                        if (pos >= 0) {
-                            if (lane == 0) {
-                                st.found = 1;
-                                st.fpos = (int)(b0 + o) + pos;
-                                st.fkey = keys[o + pos];
-                                st.xs = sv;
-                            }
-                            wave_sync();
-                            return true;
-                        }
+                    // the bucket's keys sorted (n <= kFSort), then added as floats in that order
+                    wave_sort_desc_to(f.gath + gs, (int)n, f.sortb);
+                    const uint32_t* keys = f.sortb;
+                    const int pos = chain_replay(sv, keys, (int)n, top_p);
+                    if (pos < 0) return false;
+                    // the keys above the cut's and equal to it (all in this bucket)
+                    const uint32_t ck = ((const lds_u32*)keys)[pos];
+                    int ngt = 0, neq = 0;
+                    for (uint32_t e = lane; e < n; e += 64) {
+                        const uint32_t y = ((const lds_u32*)keys)[e];
+                        ngt += y > ck;
+                        neq += y == ck;
                     }
-                    wave_sync();
-                    return false;
+                    ngt = __builtin_amdgcn_readlane(wave_incl_sum_i(ngt), 63);
+                    neq = __builtin_amdgcn_readlane(wave_incl_sum_i(neq), 63);
+                    if (lane == 0) {
+                        st.found = 1;
+                        st.fpos = (int)b0 + pos;
+                        st.fkey = ck;
+                        st.fgt = (int)b0 + ngt;
+                        st.feq = neq;
+                        st.xs = sv;
+                    }
+                    return true;
                 }, c0);
                 if (g < 0 && lane == 0) st.xs = s;
             }
@@ -1221,6 +1294,8 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
         if (fd == 1) {
             *cut_key = st.fkey;
             *cut_count = counted + st.fpos + 1;
+            *cut_gt = counted + st.fgt;
+            *cut_eq = st.feq;
             st.dS = (double)xs_value(s);
             return true;
         }

@@ -4328,6 +4328,29 @@ __global__ __launch_bounds__(64) void k_fs_int(StreamArgs a) {
     }
 }
 
+// ids[0, n) (n <= 64 Q, distinct) sorted ascending in place by one wave (a
+// descending sort of their complements; the padding 0 stays last), and
+// eb[q] = the bits of x[ids[q]].
+template <int Q>
+__device__ __forceinline__ void wave_ids_ascending(uint32_t* ids, int n, const float* x, uint32_t* eb) {
+    const int lane = lane_id();
+    uint32_t v[Q];
+#pragma unroll
+    for (int t = 0; t < Q; ++t) v[t] = t * 64 + lane < n ? ~ids[t * 64 + lane] : 0u;
+    bsort_all<Q>(v);
+    wave_sync();
+#pragma unroll
+    for (int t = 0; t < Q; ++t) {
+        const int q = t * 64 + lane;
+        if (q < n) {
+            const uint32_t id = ~v[t];
+            ids[q] = id;
+            eb[q] = __float_as_uint(x[id]);
+        }
+    }
+    wave_sync();
+}
+
 // Full-vocabulary rows, one block of kFT threads per row. PRE: the
 // instantiations for the RF_FPRE rows (k_fs_* did the transform and left the
 // window tables; no penalties, logit bias or top-k), PLAIN among them for the
@@ -4543,6 +4566,15 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
 
     int nkept = 0;
     int32_t tok = 0;
+    // top-p's kept set as a predicate (p >= p*, when the cut keeps every id
+    // with p* and no later stage removes ids), instead of writing -inf and 0
+    // over the removed ids; kKeepAll when the arrays say what is left
+    Keep keep = kKeepAll;
+    bool listed = false;   // a small kept set's draw and outputs are done (ids in f.gath)
+    // an id is left in: its transformed logit is above -inf (and the predicate keeps it)
+    auto inset = [&](float e, float x) -> bool {
+        return keep.key != 0u ? keep(e) > 0.0f : x != -__builtin_inff();
+    };
     if (m != -__builtin_inff()) {
         // ---- softmax numerators and their exact index-order sum (sampler.cpp:124-142) ----
         float S;
@@ -4561,6 +4593,8 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
         bool touched = false;   // top-p or min-p removed ids
         int nleft = -1;         // ids left in (finite transformed logit) once a stage has counted them
         bool mk_same = true;    // the largest logit left in is still m
+        int list_need = -1;     // top-p's candidates (p >= p*) fit one wave's list: the ids with p* it keeps
+        uint32_t list_key = 0u; // ... and p*
 
         // ---- top-p (sampler.cpp:146-164) ----
         if (!PLAIN && (P.flags & RF_TOPP)) {
@@ -4585,7 +4619,14 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                 // the largest logit's p is fl(1 * inv) = inv: it stays in unless
                 // the cut falls among the ids with that p
                 if (cut_key == __float_as_uint(inv) && need < neq) mk_same = false;
-                if (need >= neq) {
+                if (!(P.flags & RF_MINP) && ngt + neq <= kFSort) {
+                    // few candidates: the list below keeps the lowest `need` ids with p*
+                    keep = Keep{inv, cut_key};
+                    list_need = need;
+                    list_key = cut_key;
+                } else if (need >= neq && !(P.flags & RF_MINP)) {
+                    keep = Keep{inv, cut_key};
+                } else if (need >= neq) {
                     fpass(pv, Vp, [&](int i, float e) {
                         if (__float_as_uint(e * inv) < cut_key) {
                             fv[i] = -__builtin_inff();
@@ -4646,6 +4687,155 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
             }
         }
 
+        // A small kept set (top-p's candidates, p >= p*, at most 512 ids): the
+        // candidates are gathered and sorted by id, the lowest `need` with p*
+        // kept, and the rest is done on the list by wave 0 -- the largest kept
+        // logit (and the numerators again when it is below m), the exact
+        // index-order sum of the numerators (float adds), the draw and the kept
+        // ids -- with no more passes over the row.
+        if (list_need >= 0) {
+            uint32_t* ids = f.gath;   // (the window and bucket tables are free now)
+            if (tid == 0) st.sel_d = 0;
+            __syncthreads();
+            wpass(pv, nW, G, [&](int w, int g, const float (&e)[8]) {
+                int c = 0;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) c += keep(e[j]) > 0.0f;
+                const int incl = wave_incl_sum_i(c);
+                const int tot = __builtin_amdgcn_readlane(incl, 63);
+                if (tot == 0) return;
+                int base = 0;
+                if (lane == 0) base = atomicAdd(&st.sel_d, tot);
+                int pos = __builtin_amdgcn_readfirstlane(base) + incl - c;
+                const int i0 = w * WS + g * kFWin + lane * 8;
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (keep(e[j]) > 0.0f) {
+                        if (pos < kFSort) ids[pos] = (uint32_t)(i0 + j);
+                        ++pos;
+                    }
+            });
+            __syncthreads();
+            const int n0 = min(st.sel_d, kFSort);
+            if (wid == 0) {
+                // ids ascending, their numerators beside them
+                uint32_t* eb = f.sortb;
+                if (n0 <= 64) wave_ids_ascending<1>(ids, n0, pv, eb);
+                else if (n0 <= 128) wave_ids_ascending<2>(ids, n0, pv, eb);
+                else if (n0 <= 256) wave_ids_ascending<4>(ids, n0, pv, eb);
+                else wave_ids_ascending<8>(ids, n0, pv, eb);
+                // the candidates with p* past the first `need` of them leave;
+                // the largest kept logit m'; the rest close ranks
+                uint32_t li_[8], le_[8];
+                bool kq[8];
+                int ce = 0;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int q = lane * 8 + j;
+                    li_[j] = q < n0 ? ids[q] : 0u;
+                    le_[j] = q < n0 ? eb[q] : 0u;
+                    ce += q < n0 && __float_as_uint(__uint_as_float(le_[j]) * keep.inv) == list_key;
+                }
+                int eqr = wave_incl_sum_i(ce) - ce;   // equal keys before this lane's first entry
+                int ck = 0;
+                float mk = -__builtin_inff();
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int q = lane * 8 + j;
+                    const bool eq = q < n0 && __float_as_uint(__uint_as_float(le_[j]) * keep.inv) == list_key;
+                    kq[j] = q < n0 && (!eq || eqr < list_need);
+                    eqr += eq;
+                    ck += kq[j];
+                    if (kq[j]) mk = fmaxf(mk, fv[li_[j]]);
+                }
+                mk = wave_max_f(mk);
+                int kpos = wave_incl_sum_i(ck) - ck;
+                wave_sync();
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    if (kq[j]) {
+                        uint32_t e = le_[j];
+                        // numerators relative to m' when the cut left the maximum out
+                        if (mk != m) e = __float_as_uint(libm_expf_t(fv[li_[j]] - mk, st.expT));
+                        ids[kpos] = li_[j];
+                        eb[kpos] = e;
+                        ++kpos;
+                    }
+                }
+                const int n = __builtin_amdgcn_readlane(kpos, 63);
+                wave_sync();
+                XState s2{-126, 0u};
+                chain_replay(s2, eb, n, __builtin_inff());
+                const float inv2 = 1.0f / xs_value(s2);
+                // the draw (sampler.cpp:178-182): q = p / S_d over the kept ids in index order
+                float pq[8];
+                int32_t iq[8];
+                double ls = 0.0;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int q = lane * 8 + j;
+                    pq[j] = q < n ? __uint_as_float(eb[q]) * inv2 : 0.0f;
+                    iq[j] = q < n ? (int32_t)ids[q] : -1;
+                    ls += (double)pq[j];
+                }
+                const double li = wave_tree_prefix_d(ls);
+                const double Sd = readlane_d(li, 63);
+                const double u = st.u;
+                int tk = V - 1;   // no running sum reaches u: cp[V - 1] = 1 takes it
+                double dS = -1.0;
+                if (!(u > 0.0)) {
+                    tk = 0;
+                } else {
+                    double c = li - ls, cat = 0.0, pat = 0.0;
+                    int first = 8;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const double qj = (double)pq[j] / Sd;
+                        const double before = c;
+                        c = c + qj;
+                        const double cc = (iq[j] == V - 1) ? 1.0 : c;
+                        if (first == 8 && iq[j] >= 0 && qj > 0.0 && cc >= u) {
+                            first = j;
+                            cat = cc;
+                            pat = before;
+                        }
+                    }
+                    const u64 hm = __ballot(first < 8);
+                    if (hm != 0ull) {
+                        const int L = __ffsll((long long)hm) - 1;
+                        int sel = 0;
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) sel = j == first ? iq[j] : sel;
+                        tk = __builtin_amdgcn_readlane(sel, L);
+                        dS = readlane_d(fmin(fabs(cat - u), fabs(pat - u)), L);
+                    } else {
+                        dS = fmin(fabs(1.0 - u), fabs(readlane_d(c, 63) - u));
+                    }
+                }
+                if (a.kept_idx != nullptr) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int q = lane * 8 + j;
+                        if (q < n && q < a.set_cap) {
+                            a.kept_idx[(int64_t)r * a.set_cap + q] = iq[j];
+                            a.kept_prob[(int64_t)r * a.set_cap + q] = pq[j];
+                        }
+                    }
+                }
+                if (lane == 0) {
+                    st.tok = tk;
+                    st.dS = dS;
+                    st.sel_need = n;
+                }
+            }
+            __syncthreads();
+            tok = st.tok;
+            if (st.dS >= 0.0 && st.dS <= 1e-6) rflags |= ROWF_CDF_NEAR;
+            nkept = st.sel_need;
+            listed = true;
+            changed = false;
+        }
+
         // the numerators of what is left: relative to the largest kept logit
         // (the maximum unless a tie in p kept a lower id first), window sums
         auto refresh = [&]() {
@@ -4667,7 +4857,10 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                 full_exp(fv, pv, m, nW, G, f, st);
             } else {
                 float ws = 0.0f;
-                wpass(pv, nW, G, [&](int w, int g, const float (&v)[8]) {
+                wpass(pv, nW, G, [&](int w, int g, const float (&u)[8]) {
+                    float v[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) v[j] = keep(u[j]);
                     ws += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
                     if (g == G - 1) {
                         ws = wave_tree_prefix_f(ws);
@@ -4677,7 +4870,7 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                 });
                 __syncthreads();
             }
-            S = xs_value(exact_index_sum(pv, nW, G, f, st));
+            S = xs_value(exact_index_sum(pv, nW, G, f, st, keep));
         };
 
         // ---- min-p (sampler.cpp:167-176) ----
@@ -4718,7 +4911,7 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
         HSAMP_PHASE(12000 + r, 6);
         if (changed) refresh();
         HSAMP_PHASE(12000 + r, 7);
-        if (m != -__builtin_inff()) {
+        if (m != -__builtin_inff() && !listed) {
             // ---- the draw (sampler.cpp:178-182, discrete_distribution) ----
             // p = e * fl(1/S); S_d = sum of p (double); q = p / S_d; the first id
             // whose running sum of q reaches u (the last id's is 1). One pass
@@ -4746,7 +4939,7 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                 double ws = 0.0;
                 wpass(pv, nW, G, [&](int w, int g, const float (&e)[8]) {
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) ws += (double)(e[j] * inv);
+                    for (int j = 0; j < 8; ++j) ws += (double)(keep(e[j]) * inv);
                     if (g == G - 1) {
                         ws = wave_sum_d(ws);
                         if (lane == 0) {
@@ -4762,8 +4955,8 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                 wpass2(pv, fv, nW, G, [&](int w, int g, const float (&e)[8], const float (&x)[8]) {
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
-                        ws += (double)(e[j] * inv);
-                        c += x[j] != -__builtin_inff();
+                        ws += (double)(keep(e[j]) * inv);
+                        c += inset(e[j], x[j]);
                     }
                     if (g == G - 1) {
                         ws = wave_sum_d(ws);
@@ -4841,7 +5034,8 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                             const int i0 = w * WS + lane * 8;
                             const float4 e0 = reinterpret_cast<const float4*>(pv + i0)[0];
                             const float4 e1 = reinterpret_cast<const float4*>(pv + i0)[1];
-                            const float e[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+                            const float e[8] = {keep(e0.x), keep(e0.y), keep(e0.z), keep(e0.w),
+                                                keep(e1.x), keep(e1.y), keep(e1.z), keep(e1.w)};
                             double q[8], ls = 0.0;
 #pragma unroll
                             for (int j = 0; j < 8; ++j) {
@@ -4906,7 +5100,7 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                             double q[8], ls = 0.0;
 #pragma unroll
                             for (int j = 0; j < 8; ++j) {
-                                q[j] = (double)(src[j] * inv) / Sd;
+                                q[j] = (double)(keep(src[j]) * inv) / Sd;
                                 ls += q[j];
                             }
                             const double li = wave_tree_prefix_d(ls);
@@ -4951,13 +5145,13 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                     if (g == 0) pos = (int)wc[w];
                     int c = 0;
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) c += x[j] != -__builtin_inff();
+                    for (int j = 0; j < 8; ++j) c += inset(e[j], x[j]);
                     const int li = wave_incl_sum_i(c);
                     int p = pos + li - c;
                     const int i0 = w * WS + g * kFWin + lane * 8;
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
-                        if (x[j] != -__builtin_inff()) {
+                        if (inset(e[j], x[j])) {
                             if (p < a.set_cap) {
                                 a.kept_idx[(int64_t)r * a.set_cap + p] = i0 + j;
                                 a.kept_prob[(int64_t)r * a.set_cap + p] = e[j] * inv;
@@ -4978,7 +5172,16 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
     // the state sample() leaves the logits in (f32 only)
     if (a.fin_idx != nullptr) {
         float* row = static_cast<float*>(const_cast<void*>(a.logits)) + (int64_t)r * a.logits_stride;
-        for (int i = tid; i < V; i += kFT) row[i] = fv[i];
+        if (listed) {
+            // the kept ids (the list in f.gath, nkept of them) over -inf
+            for (int i = tid; i < V; i += kFT) row[i] = -__builtin_inff();
+            __syncthreads();
+            for (int q = tid; q < nkept; q += kFT) row[f.gath[q]] = fv[f.gath[q]];
+        } else if (keep.key != 0u) {
+            for (int i = tid; i < V; i += kFT) row[i] = keep(pv[i]) > 0.0f ? fv[i] : -__builtin_inff();
+        } else {
+            for (int i = tid; i < V; i += kFT) row[i] = fv[i];
+        }
     }
     if (wid == 0) emit_token_wave(a, r, tok);
     if (tid == 0) {

@@ -576,15 +576,27 @@ __device__ __forceinline__ float fblock_excl_scan_f(float v, float* total, FullS
     return base + incl - v;
 }
 
-// The exact index-order float sum of x[0, nW * 512 * G) (values >= 0, the
-// padding +0), given each window's approximate sum in f.winA: predicted
-// binades from the approximate prefixes, the windows' pairs at them, then one
-// wave composes (replaying the windows where the prediction fails or the
-// sum leaves its binade).
-__device__ __forceinline__ XState exact_index_compose(const float* x, int nW, int G, FullLds f, FullShared& st,
-                                                      const uint4* lanes = nullptr);
+// A kept-set predicate over numerators e: e stays when the bits of e * inv
+// (its p) are at least key, else it reads as +0 (key 0 keeps every e >= 0).
+struct Keep {
+    float inv;
+    uint32_t key;
+    __device__ __forceinline__ float operator()(float e) const {
+        return __float_as_uint(e * inv) >= key ? e : 0.0f;
+    }
+};
+constexpr Keep kKeepAll{1.0f, 0u};
 
-__device__ __noinline__ XState exact_index_sum(const float* x, int nW, int G, FullLds f, FullShared& st) {
+// The exact index-order float sum of keep(x[i]) over [0, nW * 512 * G) (values
+// >= 0, the padding +0), given each window's approximate sum in f.winA:
+// predicted binades from the approximate prefixes, the windows' pairs at them,
+// then one wave composes (replaying the windows where the prediction fails or
+// the sum leaves its binade).
+__device__ __forceinline__ XState exact_index_compose(const float* x, int nW, int G, FullLds f, FullShared& st,
+                                                      const uint4* lanes = nullptr, Keep keep = kKeepAll);
+
+__device__ __noinline__ XState exact_index_sum(const float* x, int nW, int G, FullLds f, FullShared& st,
+                                               Keep keep = kKeepAll) {
     const int tid = threadIdx.x, lane = lane_id();
     {
         // two windows per thread: their approximate start values -> binades
@@ -599,13 +611,14 @@ __device__ __noinline__ XState exact_index_sum(const float* x, int nW, int G, Fu
     {
         XPair wp{0u, 0u};
         bool nz = false;
-        wpass(x, nW, G, [&](int w, int g, const float (&v)[8]) {
+        wpass(x, nW, G, [&](int w, int g, const float (&u)[8]) {
             const int E = (int)(f.winEF[w] & 0xFFFFu) - 256;
             XPair lp{0u, 0u};
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                lp = xcomp(lp, xinc2(v[j], E));
-                nz |= v[j] != 0.0f;
+                const float v = keep(u[j]);
+                lp = xcomp(lp, xinc2(v, E));
+                nz |= v != 0.0f;
             }
             const XPair sp = wave_scan_pair(lp);
             wp = xcomp(wp, XPair{(uint32_t)__builtin_amdgcn_readlane((int)sp.d0, 63),
@@ -623,7 +636,7 @@ __device__ __noinline__ XState exact_index_sum(const float* x, int nW, int G, Fu
         });
     }
     __syncthreads();
-    return exact_index_compose(x, nW, G, f, st);
+    return exact_index_compose(x, nW, G, f, st, nullptr, keep);
 }
 
 // Segmented inclusive scan of pairs over the wave in lane order: a lane with
@@ -704,7 +717,7 @@ static_assert(kStage * (64 * 16 + 512 * 4) + kStage * 4 <= 4 * (6 * kFNB + 1), "
 // windows to be resolved (window 0, the lane-table windows) in LDS while
 // wave 0 composes, each marked ready once written.
 __device__ __forceinline__ XState exact_index_compose(const float* x, int nW, int G, FullLds f, FullShared& st,
-                                                      const uint4* lanes) {
+                                                      const uint4* lanes, Keep keep) {
     const int lane = lane_id(), wid = wave_id();
     const int WS = kFWin * G;
     const bool staged = lanes != nullptr && G == 1;
@@ -736,8 +749,8 @@ __device__ __forceinline__ XState exact_index_compose(const float* x, int nW, in
                         const float4* src = reinterpret_cast<const float4*>(x + (size_t)w * WS + lane * 8);
                         const float4 q0 = src[0], q1 = src[1];
                         lds_f32* dst = s_val + q * 512 + lane * 8;
-                        dst[0] = q0.x; dst[1] = q0.y; dst[2] = q0.z; dst[3] = q0.w;
-                        dst[4] = q1.x; dst[5] = q1.y; dst[6] = q1.z; dst[7] = q1.w;
+                        dst[0] = keep(q0.x); dst[1] = keep(q0.y); dst[2] = keep(q0.z); dst[3] = keep(q0.w);
+                        dst[4] = keep(q1.x); dst[5] = keep(q1.y); dst[6] = keep(q1.z); dst[7] = keep(q1.w);
                         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
                         if (lane == 0) s_rdy[q] = (uint32_t)w + 1u;
                     }
@@ -774,14 +787,15 @@ __device__ __forceinline__ XState exact_index_compose(const float* x, int nW, in
                 if (by_lanes) t = lanes[(size_t)w * 64 + lane];
                 const float4* src = reinterpret_cast<const float4*>(x + (size_t)w * WS + lane * 8);
                 const float4 q0 = src[0], q1 = src[1];
-                v[0] = q0.x; v[1] = q0.y; v[2] = q0.z; v[3] = q0.w;
-                v[4] = q1.x; v[5] = q1.y; v[6] = q1.z; v[7] = q1.w;
+                v[0] = keep(q0.x); v[1] = keep(q0.y); v[2] = keep(q0.z); v[3] = keep(q0.w);
+                v[4] = keep(q1.x); v[5] = keep(q1.y); v[6] = keep(q1.z); v[7] = keep(q1.w);
             }
             if (G != 1) {
                 for (int g = 0; g < G; ++g) {
                     const float4* src = reinterpret_cast<const float4*>(x + (size_t)w * WS + g * kFWin + lane * 8);
                     const float4 q0 = src[0], q1 = src[1];
-                    const float u[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+                    const float u[8] = {keep(q0.x), keep(q0.y), keep(q0.z), keep(q0.w),
+                                        keep(q1.x), keep(q1.y), keep(q1.z), keep(q1.w)};
                     xs_replay(s, u, 0, false, 0.0f);
                 }
                 return;

@@ -47,6 +47,39 @@ __global__ __launch_bounds__(kFT) void k_xsum(const float* x, int n, int Vp, int
     }
 }
 
+// xinc2 and xinc2f (integer and float arithmetic) for x[i] at binade E:
+// out[4 i .. 4 i + 3] = xinc2's pair, xinc2f's pair (or two pairs that
+// differ when xinc and xincf disagree).
+__global__ void k_xinc(const float* x, int n, int E, uint32_t* out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const XPair a = xinc2(x[i], E);
+    bool t;
+    const XPair b = xinc2f(x[i], E, t);
+    // xincf's increment, tie and big flags against xinc's (a mismatch shows as
+    // an impossible pair)
+    bool t1, g1, t2, g2;
+    const uint32_t i1 = xinc(x[i], E, t1, g1), i2 = xincf(x[i], E, t2, g2);
+    if (i1 != i2 || t1 != t2 || g1 != g2) {
+        out[4 * i] = 0xFFFFFFFFu;
+        out[4 * i + 1] = 0u;
+        out[4 * i + 2] = 0u;
+        out[4 * i + 3] = 0xFFFFFFFFu;
+        return;
+    }
+    out[4 * i] = a.d0;
+    out[4 * i + 1] = a.d1;
+    out[4 * i + 2] = b.d0;
+    out[4 * i + 3] = b.d1;
+}
+
+extern "C" int xinc_run(const float* x, int n, int E, uint32_t* out) {
+    hipLaunchKernelGGL(k_xinc, dim3((n + 255) / 256), dim3(256), 0, nullptr, x, n, E, out);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    return (int)hipDeviceSynchronize();
+}
+
 extern "C" int xsum_run(const float* x, int n, int Vp, int G, float thr, uint32_t rlo, uint32_t rhi, float* out,
                         int* outi) {
     hipLaunchKernelGGL(k_xsum, dim3(1), dim3(kFT), kFullLdsBytes, nullptr, x, n, Vp, G, thr, rlo, rhi, out, outi);

@@ -24,6 +24,8 @@ def _kit(pkg):
     lib.xsum_run.restype = ctypes.c_int
     lib.xsum_run.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float,
                              ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]
+    lib.xinc_run.restype = ctypes.c_int
+    lib.xinc_run.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     return lib
 
 
@@ -110,3 +112,33 @@ def test_top_p_cutoff(pkg, name, frac, known_range):
         # the values above the cut's and equal to it (the removal's tie rule)
         assert outi[2] == int(np.count_nonzero(x > xs[j])), name
         assert outi[3] == int(np.count_nonzero(x == xs[j])), name
+
+
+@pytest.mark.parametrize("E", [-126, -40, -17, -1, 0, 9, 16, 30])
+def test_float_increments_match_integer_ones(pkg, E):
+    """The increments k_fs_int takes by float arithmetic (ldexp, floor) are the
+    integer ones (xinc2) for every kind of value at binade E: far below the
+    sum's ulp, exactly half-way between two multiples of it at every scale,
+    just beside half-way, within the binade, at and past its top, zeros and
+    subnormals."""
+    import torch
+    kit = _kit(pkg)
+    rng = np.random.default_rng(1000 + E)
+    vals = [np.float32(0.0), np.float32(1e-45), np.float32(1e-39)]
+    for d in range(-3, 27):           # x = m * 2^(E - d) for mantissas m in [1, 2)
+        sc = np.float32(2.0) ** np.float32(np.clip(E - d, -149, 127))
+        m = rng.uniform(1.0, 2.0, 64).astype(np.float32)
+        vals += list((m * sc).astype(np.float32))
+    for top in (4, 12, 20):           # (k + 1/2) ulps of binade E, k < 2^top, and their neighbours
+        k = rng.integers(0, 1 << top, 32)
+        h = ((k * 2 + 1).astype(np.float64) * 2.0 ** (E - 24)).astype(np.float32)
+        vals += list(h) + list(np.nextafter(h, np.float32(np.inf))) + list(np.nextafter(h, np.float32(0)))
+    x = np.array([v for v in vals if np.isfinite(v)], np.float32)
+    dev = torch.device("cuda:0")
+    xd = torch.from_numpy(x).to(dev)
+    out = torch.zeros(4 * x.size, dtype=torch.int32, device=dev)
+    rc = kit.xinc_run(xd.data_ptr(), x.size, E, out.data_ptr())
+    assert rc == 0
+    o = out.cpu().numpy().view(np.uint32).reshape(-1, 4)
+    bad = np.nonzero((o[:, 0] != o[:, 2]) | (o[:, 1] != o[:, 3]))[0]
+    assert bad.size == 0, f"E={E}: x={x[bad[:4]]!r} int={o[bad[:4], :2]} float={o[bad[:4], 2:]}"

@@ -4196,12 +4196,31 @@ __global__ __launch_bounds__(64) void k_fs_max(StreamArgs a) {
     float mloc = -__builtin_inff();
     bool nanv = false;
     int cnt = 0;
+    // 16-byte loads where the row is aligned and the step lies inside it
+    const bool al = (reinterpret_cast<uintptr_t>(rowp) & 15u) == 0u;
     for (int g = 0; g < G; ++g) {
         const int i0 = w * WS + g * kFWin + lane * 8;
         float x[8];
         uint32_t mw = 0xFFFFFFFFu;
+        if (al && w * WS + (g + 1) * kFWin <= V) {
+            if (DT == 0) {
+                const float4 c0 = reinterpret_cast<const float4*>(rowp + (size_t)i0 * 4)[0];
+                const float4 c1 = reinterpret_cast<const float4*>(rowp + (size_t)i0 * 4)[1];
+                x[0] = c0.x; x[1] = c0.y; x[2] = c0.z; x[3] = c0.w;
+                x[4] = c1.x; x[5] = c1.y; x[6] = c1.z; x[7] = c1.w;
+            } else {
+                const uint4 c = *reinterpret_cast<const uint4*>(rowp + (size_t)i0 * 2);
+                const uint32_t h[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] = load_logit<DT>(rowp, min(i0 + j, V - 1));
+                for (int j = 0; j < 4; ++j) {
+                    x[2 * j] = __uint_as_float(h[j] << 16);
+                    x[2 * j + 1] = __uint_as_float(h[j] & 0xFFFF0000u);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[j] = load_logit<DT>(rowp, min(i0 + j, V - 1));
+        }
         if (mrow != nullptr) mw = mrow[min(i0, V - 1) >> 5];   // (eight ids share one mask word)
         float y[8];
 #pragma unroll
@@ -4244,20 +4263,26 @@ __global__ __launch_bounds__(64) void k_fs_exp(StreamArgs a) {
     if (!(P.flags & RF_FPRE)) return;
     const int lane = (int)threadIdx.x, G = a.full_g, WS = kFWin * G;
     if (lane < 32) expT[lane] = kExpT[lane];
+    const float* fv = a.fullv + (size_t)r * a.full_stride;
+    float* pv = a.fullp + (size_t)r * a.full_stride;
+    // the window's first step in flight while the row's maximum is found
+    float4 c0 = reinterpret_cast<const float4*>(fv + w * WS + lane * 8)[0];
+    float4 c1 = reinterpret_cast<const float4*>(fv + w * WS + lane * 8)[1];
     // the row's maximum over the window maxima
     const uint32_t* wm = fs_table(a, r, FS_MAX);
     float m = -__builtin_inff();
     for (int k = lane; k < nW; k += 64) m = fmaxf(m, __uint_as_float(wm[k]));
     m = wave_max_f(m);
     __syncthreads();
-    const float* fv = a.fullv + (size_t)r * a.full_stride;
-    float* pv = a.fullp + (size_t)r * a.full_stride;
     float ws = 0.0f;
     double wd = 0.0;
     uint32_t emn = 0xFFFFFFFFu;
     for (int g = 0; g < G; ++g) {
         const int i0 = w * WS + g * kFWin + lane * 8;
-        const float4 c0 = reinterpret_cast<const float4*>(fv + i0)[0], c1 = reinterpret_cast<const float4*>(fv + i0)[1];
+        if (g > 0) {
+            c0 = reinterpret_cast<const float4*>(fv + i0)[0];
+            c1 = reinterpret_cast<const float4*>(fv + i0)[1];
+        }
         const float x[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
         float v[8];
 #pragma unroll
@@ -4288,6 +4313,10 @@ __global__ __launch_bounds__(64) void k_fs_int(StreamArgs a) {
     const RowPlan P = plan_of(a, r);
     if (!(P.flags & RF_FPRE)) return;
     const int lane = (int)threadIdx.x, G = a.full_g, WS = kFWin * G;
+    const float* pv = a.fullp + (size_t)r * a.full_stride;
+    // the window's first step in flight while its binade is found
+    const float4* s0 = reinterpret_cast<const float4*>(pv + (size_t)w * WS + lane * 8);
+    float4 c0 = s0[0], c1 = s0[1];
     // the window's binade: predicted from the approximate sum before it
     const uint32_t* wa = fs_table(a, r, FS_A);
     float pre = 0.0f;
@@ -4297,26 +4326,45 @@ __global__ __launch_bounds__(64) void k_fs_int(StreamArgs a) {
     // a window of one step whose approximate end lies in a higher binade (or
     // within 0.1% below one) keeps its lanes' pairs at E and E + 1
     const bool lanes_on = G == 1 && w > 0 && xs_binade((pre + __uint_as_float(wa[w])) * 1.001f) != E;
-    const float* pv = a.fullp + (size_t)r * a.full_stride;
     XPair wp{0u, 0u};
     bool nz = false;
     for (int g = 0; g < G; ++g) {
-        const int i0 = w * WS + g * kFWin + lane * 8;
-        const float4 c0 = reinterpret_cast<const float4*>(pv + i0)[0], c1 = reinterpret_cast<const float4*>(pv + i0)[1];
+        if (g > 0) {
+            const float4* sg = reinterpret_cast<const float4*>(pv + (size_t)w * WS + g * kFWin + lane * 8);
+            c0 = sg[0];
+            c1 = sg[1];
+        }
         const float v[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-        XPair lp{0u, 0u};
+        // increments by float arithmetic; their plain (saturating) sums
+        // while no value is half-way, the parity pairs in order otherwise
+        XPair e[8];
+        bool tie = false;
+        uint32_t ls = 0u;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            lp = xcomp(lp, xinc2(v[j], E));
+            bool t;
+            e[j] = xinc2f(v[j], E, t);
+            tie |= t;
+            ls += e[j].d0;
             nz |= v[j] != 0.0f;
+        }
+        ls = min(ls, 1u << 25);
+        XPair lp{ls, ls};
+        if (__ballot(tie) != 0ull) {
+            lp = XPair{0u, 0u};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) lp = xcomp(lp, e[j]);
         }
         if (lanes_on) {
             XPair l1{0u, 0u};
 #pragma unroll
-            for (int j = 0; j < 8; ++j) l1 = xcomp(l1, xinc2(v[j], E + 1));
+            for (int j = 0; j < 8; ++j) {
+                bool t;
+                l1 = xcomp(l1, xinc2f(v[j], E + 1, t));
+            }
             fs_lanes(a, r)[(size_t)w * 64 + lane] = make_uint4(lp.d0, lp.d1, l1.d0, l1.d1);
         }
-        const XPair sp = wave_scan_pair(lp);
+        const XPair sp = wave_scan_pair_any(lp);
         wp = xcomp(wp, XPair{(uint32_t)__builtin_amdgcn_readlane((int)sp.d0, 63),
                              (uint32_t)__builtin_amdgcn_readlane((int)sp.d1, 63)});
     }
@@ -4838,6 +4886,9 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
 
         // the numerators of what is left: relative to the largest kept logit
         // (the maximum unless a tie in p kept a lower id first), window sums
+        // (PRE rows: also each window's kept numerators summed in double and
+        // counted, in the FS_SD / FS_CNT tables, for the draw: fresh)
+        bool fresh = false;
         auto refresh = [&]() {
             float mk = m;
             if (nleft == 0) {
@@ -4857,20 +4908,39 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                 full_exp(fv, pv, m, nW, G, f, st);
             } else {
                 float ws = 0.0f;
+                double wd = 0.0;
+                int wn = 0;
                 wpass(pv, nW, G, [&](int w, int g, const float (&u)[8]) {
                     float v[8];
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) v[j] = keep(u[j]);
+                    for (int j = 0; j < 8; ++j) {
+                        v[j] = keep(u[j]);
+                        if (pre) {
+                            wd += (double)v[j];
+                            wn += v[j] > 0.0f;
+                        }
+                    }
                     ws += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
                     if (g == G - 1) {
                         ws = wave_tree_prefix_f(ws);
                         if (lane == 63) f.winA[w] = ws;
+                        if (pre) {
+                            wd = wave_tree_prefix_d(wd);
+                            wn = wave_incl_sum_i(wn);
+                            if (lane == 63) {
+                                reinterpret_cast<double*>(fs_table(a, r, FS_SD))[w] = wd;
+                                fs_table(a, r, FS_CNT)[w] = (uint32_t)wn;
+                            }
+                        }
                         ws = 0.0f;
+                        wd = 0.0;
+                        wn = 0;
                     }
                 });
+                fresh = pre;
                 __syncthreads();
             }
-            S = xs_value(exact_index_sum(pv, nW, G, f, st, keep));
+            S = xs_value(exact_index_sum(pv, nW, G, f, st, keep, pre ? fs_lanes(a, r) : nullptr));
         };
 
         // ---- min-p (sampler.cpp:167-176) ----
@@ -4931,6 +5001,20 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                     if (k < nW) {
                         wq[k] = (double)inv * sdr[i];
                         wc[k] = cnr[i];
+                    }
+                }
+            } else if (fresh && (keep.key != 0u || a.kept_idx == nullptr)) {
+                // the refresh left each window's kept numerators summed in
+                // double and counted: the window sums of p as fl(1/S) times
+                // those (as above)
+                const double* wsd = reinterpret_cast<const double*>(fs_table(a, r, FS_SD));
+                const uint32_t* wcn = fs_table(a, r, FS_CNT);
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const int k = tid + i * kFT;
+                    if (k < nW) {
+                        wq[k] = (double)inv * wsd[k];
+                        wc[k] = wcn[k];
                     }
                 }
             } else if (touched && a.kept_idx == nullptr) {

@@ -88,6 +88,19 @@ __device__ __forceinline__ uint32_t xinc(float x, int E, bool& tie, bool& big) {
     return (X >> d) + (r >= half ? 1u : 0u);
 }
 
+// xinc by float arithmetic: t = x * 2^(23-E) is exact for every x whose
+// increment is not 0 (a power-of-two scale; t below 2^-126, where it could
+// round, means an increment of 0), K = floor(t) and the fraction decide:
+// K + 1 from one half up (tie: exactly one half), big: t >= 2^24.
+__device__ __forceinline__ uint32_t xincf(float x, int E, bool& tie, bool& big) {
+    const float t = ldexpf(x, 23 - E);
+    const float fl = floorf(t);
+    const float fr = t - fl;
+    big = !(t < 16777216.0f);
+    tie = fr == 0.5f;
+    return big ? 0u : (uint32_t)fl + (fr >= 0.5f ? 1u : 0u);
+}
+
 // s + x, rounded to nearest even, exactly (integer arithmetic only).
 __device__ XState xs_add(XState s, float x) {
     int ex;
@@ -347,6 +360,23 @@ __device__ __forceinline__ XPair xinc2(float x, int E) {
     const uint32_t K = i - 1u;
     return XPair{K + (K & 1u), K + 1u - (K & 1u)};
 }
+// xinc2 by float arithmetic: t = x * 2^(23-E) is exact (a power-of-two
+// scale; t falls below 2^-126, where it could round, only for values that add
+// nothing), its integer part K and fraction r give the increment -- K, or
+// K + 1 above one half; exactly one half (tie) the pair (K + (K & 1),
+// K + 1 - (K & 1)) -- and t >= 2^24 leaves the binade (saturated). The same
+// pairs as xinc2 (x >= 0 finite).
+__device__ __forceinline__ XPair xinc2f(float x, int E, bool& tie) {
+    const float t = ldexpf(x, 23 - E);
+    const float fl = floorf(t);
+    const float fr = t - fl;
+    const uint32_t K = t < 16777216.0f ? (uint32_t)fl : (1u << 25);
+    tie = fr == 0.5f;
+    const uint32_t i = K + (fr > 0.5f ? 1u : 0u);
+    const uint32_t lo = K + (K & 1u), hi = K + 1u - (K & 1u);
+    return (tie && K < (1u << 25)) ? XPair{lo, hi} : XPair{min(i, 1u << 25), min(i, 1u << 25)};
+}
+
 // a, then b
 __device__ __forceinline__ XPair xcomp(XPair a, XPair b) {
     return XPair{sat_add(a.d0, (a.d0 & 1u) ? b.d1 : b.d0), sat_add(a.d1, (a.d1 & 1u) ? b.d0 : b.d1)};
@@ -367,6 +397,12 @@ __device__ __forceinline__ XPair wave_scan_pair(XPair x) {
     x = xcomp_dpp<0x142, 0xA>(x);
     x = xcomp_dpp<0x143, 0xC>(x);
     return x;
+}
+// Inclusive scan of pairs, by plain sums when no lane's pair differs by parity.
+__device__ __forceinline__ XPair wave_scan_pair_any(XPair x) {
+    if (__ballot(x.d0 != x.d1) != 0ull) return wave_scan_pair(x);
+    const uint32_t u = wave_scan_u32(x.d0, 0u, [](uint32_t a, uint32_t b) { return a + b; });
+    return XPair{u, u};
 }
 
 // Replays v[lane * 8 + j] (in that order; absent values +0) onto s, from
@@ -591,36 +627,69 @@ constexpr Keep kKeepAll{1.0f, 0u};
 // >= 0, the padding +0), given each window's approximate sum in f.winA:
 // predicted binades from the approximate prefixes, the windows' pairs at them,
 // then one wave composes (replaying the windows where the prediction fails or
-// the sum leaves its binade).
+// the sum leaves its binade). With lanes (windows of one step), a window whose
+// approximate end lies in a higher binade (or within 0.1% below one) also
+// leaves each lane's pairs at E and E + 1 there, as k_fs_int does, for the
+// compose to resolve it by.
 __device__ __forceinline__ XState exact_index_compose(const float* x, int nW, int G, FullLds f, FullShared& st,
                                                       const uint4* lanes = nullptr, Keep keep = kKeepAll);
 
 __device__ __noinline__ XState exact_index_sum(const float* x, int nW, int G, FullLds f, FullShared& st,
-                                               Keep keep = kKeepAll) {
+                                               Keep keep = kKeepAll, uint4* lanes = nullptr) {
     const int tid = threadIdx.x, lane = lane_id();
+    if (G != 1) lanes = nullptr;
     {
         // two windows per thread: their approximate start values -> binades
         const int w0 = 2 * tid;
         const float a0 = w0 < nW ? f.winA[w0] : 0.0f, a1 = w0 + 1 < nW ? f.winA[w0 + 1] : 0.0f;
         float tot;
         const float pre = fblock_excl_scan_f(a0 + a1, &tot, st);
-        if (w0 < nW) f.winEF[w0] = gpack(w0 == 0 ? -126 : xs_binade(pre), 0u);
-        if (w0 + 1 < nW) f.winEF[w0 + 1] = gpack(xs_binade(pre + a0), 0u);
+        const int E0 = w0 == 0 ? -126 : xs_binade(pre), E1 = xs_binade(pre + a0);
+        const bool l0 = lanes != nullptr && w0 > 0 && xs_binade((pre + a0) * 1.001f) != E0;
+        const bool l1 = lanes != nullptr && xs_binade((pre + a0 + a1) * 1.001f) != E1;
+        if (w0 < nW) f.winEF[w0] = gpack(E0, l0 ? kGLanes : 0u);
+        if (w0 + 1 < nW) f.winEF[w0 + 1] = gpack(E1, l1 ? kGLanes : 0u);
     }
     __syncthreads();
     {
         XPair wp{0u, 0u};
         bool nz = false;
         wpass(x, nW, G, [&](int w, int g, const float (&u)[8]) {
-            const int E = (int)(f.winEF[w] & 0xFFFFu) - 256;
-            XPair lp{0u, 0u};
+            const uint32_t ef = f.winEF[w];
+            const int E = (int)(ef & 0xFFFFu) - 256;
+            // increments by float arithmetic; plain (saturating) sums while no
+            // value is half-way, the parity pairs in order otherwise
+            float v[8];
+            XPair e[8];
+            bool tie = false;
+            uint32_t ls = 0u;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float v = keep(u[j]);
-                lp = xcomp(lp, xinc2(v, E));
-                nz |= v != 0.0f;
+                bool t;
+                v[j] = keep(u[j]);
+                e[j] = xinc2f(v[j], E, t);
+                tie |= t;
+                ls += e[j].d0;
+                nz |= v[j] != 0.0f;
             }
-            const XPair sp = wave_scan_pair(lp);
+            ls = min(ls, 1u << 25);
+            XPair lp{ls, ls};
+            if (__ballot(tie) != 0ull) {
+                lp = XPair{0u, 0u};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) lp = xcomp(lp, e[j]);
+            }
+            const bool lon = ((ef >> 16) & kGLanes) != 0u;
+            if (lon) {
+                XPair l1{0u, 0u};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    bool t;
+                    l1 = xcomp(l1, xinc2f(v[j], E + 1, t));
+                }
+                lanes[(size_t)w * 64 + lane] = make_uint4(lp.d0, lp.d1, l1.d0, l1.d1);
+            }
+            const XPair sp = wave_scan_pair_any(lp);
             wp = xcomp(wp, XPair{(uint32_t)__builtin_amdgcn_readlane((int)sp.d0, 63),
                                  (uint32_t)__builtin_amdgcn_readlane((int)sp.d1, 63)});
             if (g == G - 1) {
@@ -628,7 +697,7 @@ __device__ __noinline__ XState exact_index_sum(const float* x, int nW, int G, Fu
                 if (lane == 0) {
                     f.winD0[w] = wp.d0;
                     f.winD1[w] = wp.d1;
-                    f.winEF[w] = gpack(E, empty ? kGEmpty : 0u);
+                    f.winEF[w] = gpack(E, (empty ? kGEmpty : 0u) | (lon ? kGLanes : 0u));
                 }
                 wp = XPair{0u, 0u};
                 nz = false;
@@ -636,7 +705,7 @@ __device__ __noinline__ XState exact_index_sum(const float* x, int nW, int G, Fu
         });
     }
     __syncthreads();
-    return exact_index_compose(x, nW, G, f, st, nullptr, keep);
+    return exact_index_compose(x, nW, G, f, st, lanes, keep);
 }
 
 // Segmented inclusive scan of pairs over the wave in lane order: a lane with
@@ -688,12 +757,6 @@ __device__ __forceinline__ uint32_t wave_seg_sum_u32(uint32_t x, bool head) {
     seg_sum_step<0x142, 0xA>(x, h);
     seg_sum_step<0x143, 0xC>(x, h);
     return x;
-}
-// Inclusive scan of pairs, by plain sums when no lane's pair differs by parity.
-__device__ __forceinline__ XPair wave_scan_pair_any(XPair x) {
-    if (__ballot(x.d0 != x.d1) != 0ull) return wave_scan_pair(x);
-    const uint32_t u = wave_scan_u32(x.d0, 0u, [](uint32_t a, uint32_t b) { return a + b; });
-    return XPair{u, u};
 }
 
 // Windows the index-order compose stages in LDS (window 0 and the windows
@@ -1144,7 +1207,7 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
                 const int b = bucket_of(key);
                 const uint32_t ef = f.bEF[b];
                 bool t, bg;
-                const uint32_t inc = xinc(p, (int)(ef & 0xFFFFu) - 256, t, bg);
+                const uint32_t inc = xincf(p, (int)(ef & 0xFFFFu) - 256, t, bg);
                 if (inc) atomicAdd(&f.bD[b], inc);
                 if ((t || bg) && !((ef >> 16) & kGCare)) atomicOr(&f.bEF[b], kGCare << 16);
                 if (f.gst[b] != kNoGath) f.gath[atomicAdd(&f.gfill[b], 1u)] = key;

@@ -4156,19 +4156,22 @@ __device__ void full_exp(const float* fv, float* pv, float m, int nW, int G, Ful
 // (512 G ids) per wave, in the layout k_full uses (fullv / fullp, windows of
 // full_stride), and leave per-window tables (FS_*) for it:
 //   k_fs_max: the transform into fullv (the row's -inf padding included),
-//             each window's maximum, whether it held a NaN and how many ids
-//             it leaves in;
-//   k_fs_exp: the row's maximum m, the numerators expf(x - m) into fullp and
-//             each window's approximate sum (as full_exp forms it), its sum
-//             in double (the draw's window prefixes when top-p and min-p
-//             remove nothing) and its smallest numerator above 0 (top-p's
-//             key range);
-//   k_fs_int: each window's binade, predicted from the approximate sums
-//             before it, and its values' integer increments there (as
-//             exact_index_sum forms them).
+//             each window's maximum m_w, whether it held a NaN, how many ids
+//             it leaves in and its sum of exp(x - m_w) (fast exp; a
+//             prediction only);
+//   k_fs_exp: the row's maximum m, the numerators expf(x - m) into fullp,
+//             each window's sum in double (the draw's window prefixes when
+//             top-p and min-p remove nothing) and its smallest numerator
+//             above 0 (top-p's key range), and its binade -- predicted from
+//             the windows before it, sum over v < w of exp(m_v - m) times
+//             k_fs_max's sums -- with its values' integer increments there
+//             (as exact_index_sum forms them; lane tables when the window's
+//             own approximate sum takes it to another binade).
 // k_full then composes the exact sum from the tables and goes on as for its
-// other rows. Every value is computed as k_full computes it, in the same
-// order where order matters.
+// other rows. The binades are predictions: the compose checks each against
+// the exact running sum and resolves a window that misses by its values, so
+// they decide speed, not results. Every value is computed as k_full computes
+// it, in the same order where order matters.
 __device__ __forceinline__ int fs_windows(const StreamArgs& a) { return a.full_stride / (kFWin * a.full_g); }
 __device__ __forceinline__ uint32_t* fs_table(const StreamArgs& a, int r, int k) {
     const int nW = fs_windows(a);
@@ -4193,7 +4196,7 @@ __global__ __launch_bounds__(64) void k_fs_max(StreamArgs a) {
     float* fv = a.fullv + (size_t)r * a.full_stride;
     const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * (DT == 0 ? 4 : 2);
     const uint32_t* mrow = (P.flags & RF_MASK) ? a.mask + (int64_t)r * a.mask_stride : nullptr;
-    float mloc = -__builtin_inff();
+    float mloc = -__builtin_inff(), lsum = 0.0f;
     bool nanv = false;
     int cnt = 0;
     // 16-byte loads where the row is aligned and the step lies inside it
@@ -4237,20 +4240,38 @@ __global__ __launch_bounds__(64) void k_fs_max(StreamArgs a) {
                 }
             }
             y[j] = v;
-            mloc = fmaxf(mloc, v);
             cnt += v != -__builtin_inff();
+        }
+        // this step's maximum and sum of exp(y - max), folded into the lane's
+        // running pair (lmax, lsum)
+        float sm = y[0];
+#pragma unroll
+        for (int j = 1; j < 8; ++j) sm = fmaxf(sm, y[j]);
+        if (sm != -__builtin_inff()) {
+            float s8 = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) s8 += __expf(y[j] - sm);
+            if (sm > mloc) {
+                lsum = lsum * __expf(mloc - sm) + s8;
+                mloc = sm;
+            } else {
+                lsum += s8 * __expf(sm - mloc);
+            }
         }
         float4* dst = reinterpret_cast<float4*>(fv + i0);
         dst[0] = make_float4(y[0], y[1], y[2], y[3]);
         dst[1] = make_float4(y[4], y[5], y[6], y[7]);
     }
-    mloc = wave_max_f(mloc);
+    const float mw = wave_max_f(mloc);
+    float rel = mloc == -__builtin_inff() ? 0.0f : lsum * __expf(mloc - mw);
+    rel = readlane_f(wave_tree_prefix_f(rel), 63);
     cnt = __builtin_amdgcn_readlane(wave_incl_sum_i(cnt), 63);
     const bool anynan = __ballot(nanv) != 0ull;
     if (lane == 0) {
-        fs_table(a, r, FS_MAX)[w] = __float_as_uint(mloc);
+        fs_table(a, r, FS_MAX)[w] = __float_as_uint(mw);
         fs_table(a, r, FS_NAN)[w] = anynan ? 1u : 0u;
         fs_table(a, r, FS_CNT)[w] = (uint32_t)cnt;
+        fs_table(a, r, FS_A)[w] = __float_as_uint(rel);
     }
 }
 
@@ -4270,13 +4291,35 @@ __global__ __launch_bounds__(64) void k_fs_exp(StreamArgs a) {
     float4 c1 = reinterpret_cast<const float4*>(fv + w * WS + lane * 8)[1];
     // the row's maximum over the window maxima
     const uint32_t* wm = fs_table(a, r, FS_MAX);
-    float m = -__builtin_inff();
-    for (int k = lane; k < nW; k += 64) m = fmaxf(m, __uint_as_float(wm[k]));
+    const uint32_t* wa = fs_table(a, r, FS_A);
+    // and, in the same reads, the approximate sum before the window from
+    // k_fs_max's window sums relative to their own maxima (each lane's
+    // windows before w rescaled to its running maximum pm, then to m): its
+    // predicted binade
+    float m = -__builtin_inff(), pm = -__builtin_inff(), ps = 0.0f;
+    for (int k = lane; k < nW; k += 64) {
+        const float mv = __uint_as_float(wm[k]);
+        const float av = __uint_as_float(wa[k]);
+        m = fmaxf(m, mv);
+        if (k < w && mv != -__builtin_inff()) {
+            if (mv > pm) {
+                ps = ps * __expf(pm - mv) + av;
+                pm = mv;
+            } else {
+                ps += av * __expf(mv - pm);
+            }
+        }
+    }
     m = wave_max_f(m);
+    float pre = (pm == -__builtin_inff()) ? 0.0f : ps * __expf(pm - m);
+    pre = readlane_f(wave_tree_prefix_f(pre), 63);
+    const int E = w == 0 ? -126 : xs_binade(pre);
     __syncthreads();
     float ws = 0.0f;
     double wd = 0.0;
     uint32_t emn = 0xFFFFFFFFu;
+    XPair wp{0u, 0u};
+    bool nz = false, lanes_on = false;
     for (int g = 0; g < G; ++g) {
         const int i0 = w * WS + g * kFWin + lane * 8;
         if (g > 0) {
@@ -4295,48 +4338,8 @@ __global__ __launch_bounds__(64) void k_fs_exp(StreamArgs a) {
         float4* dst = reinterpret_cast<float4*>(pv + i0);
         dst[0] = make_float4(v[0], v[1], v[2], v[3]);
         dst[1] = make_float4(v[4], v[5], v[6], v[7]);
-    }
-    ws = wave_tree_prefix_f(ws);
-    wd = wave_tree_prefix_d(wd);
-    emn = wave_min_u32(emn);
-    if (lane == 63) {
-        fs_table(a, r, FS_A)[w] = __float_as_uint(ws);
-        reinterpret_cast<double*>(fs_table(a, r, FS_SD))[w] = wd;
-        fs_table(a, r, FS_EMIN)[w] = emn;
-    }
-}
-
-__global__ __launch_bounds__(64) void k_fs_int(StreamArgs a) {
-    const int nW = fs_windows(a);
-    const int r = (int)blockIdx.x / nW, w = (int)blockIdx.x - r * nW;
-    if (r >= a.rows) return;
-    const RowPlan P = plan_of(a, r);
-    if (!(P.flags & RF_FPRE)) return;
-    const int lane = (int)threadIdx.x, G = a.full_g, WS = kFWin * G;
-    const float* pv = a.fullp + (size_t)r * a.full_stride;
-    // the window's first step in flight while its binade is found
-    const float4* s0 = reinterpret_cast<const float4*>(pv + (size_t)w * WS + lane * 8);
-    float4 c0 = s0[0], c1 = s0[1];
-    // the window's binade: predicted from the approximate sum before it
-    const uint32_t* wa = fs_table(a, r, FS_A);
-    float pre = 0.0f;
-    for (int k = lane; k < w; k += 64) pre += __uint_as_float(wa[k]);
-    pre = readlane_f(wave_tree_prefix_f(pre), 63);
-    const int E = w == 0 ? -126 : xs_binade(pre);
-    // a window of one step whose approximate end lies in a higher binade (or
-    // within 0.1% below one) keeps its lanes' pairs at E and E + 1
-    const bool lanes_on = G == 1 && w > 0 && xs_binade((pre + __uint_as_float(wa[w])) * 1.001f) != E;
-    XPair wp{0u, 0u};
-    bool nz = false;
-    for (int g = 0; g < G; ++g) {
-        if (g > 0) {
-            const float4* sg = reinterpret_cast<const float4*>(pv + (size_t)w * WS + g * kFWin + lane * 8);
-            c0 = sg[0];
-            c1 = sg[1];
-        }
-        const float v[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-        // increments by float arithmetic; their plain (saturating) sums
-        // while no value is half-way, the parity pairs in order otherwise
+        // the values' increments at E: plain (saturating) sums while no value
+        // is half-way, the parity pairs in order otherwise
         XPair e[8];
         bool tie = false;
         uint32_t ls = 0u;
@@ -4355,20 +4358,32 @@ __global__ __launch_bounds__(64) void k_fs_int(StreamArgs a) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) lp = xcomp(lp, e[j]);
         }
-        if (lanes_on) {
-            XPair l1{0u, 0u};
+        if (G == 1) {
+            // a window whose approximate end lies in a higher binade (or
+            // within 0.1% below one) keeps its lanes' pairs at E and E + 1
+            const float wsum = readlane_f(wave_tree_prefix_f(ws), 63);
+            lanes_on = w > 0 && xs_binade((pre + wsum) * 1.001f) != E;
+            if (lanes_on) {
+                XPair l1{0u, 0u};
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                bool t;
-                l1 = xcomp(l1, xinc2f(v[j], E + 1, t));
+                for (int j = 0; j < 8; ++j) {
+                    bool t;
+                    l1 = xcomp(l1, xinc2f(v[j], E + 1, t));
+                }
+                fs_lanes(a, r)[(size_t)w * 64 + lane] = make_uint4(lp.d0, lp.d1, l1.d0, l1.d1);
             }
-            fs_lanes(a, r)[(size_t)w * 64 + lane] = make_uint4(lp.d0, lp.d1, l1.d0, l1.d1);
         }
         const XPair sp = wave_scan_pair_any(lp);
         wp = xcomp(wp, XPair{(uint32_t)__builtin_amdgcn_readlane((int)sp.d0, 63),
                              (uint32_t)__builtin_amdgcn_readlane((int)sp.d1, 63)});
     }
+    wd = wave_tree_prefix_d(wd);
+    emn = wave_min_u32(emn);
     const bool empty = __ballot(nz) == 0ull;
+    if (lane == 63) {
+        reinterpret_cast<double*>(fs_table(a, r, FS_SD))[w] = wd;
+        fs_table(a, r, FS_EMIN)[w] = emn;
+    }
     if (lane == 0) {
         fs_table(a, r, FS_D0)[w] = wp.d0;
         fs_table(a, r, FS_D1)[w] = wp.d1;
@@ -4627,7 +4642,7 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
         // ---- softmax numerators and their exact index-order sum (sampler.cpp:124-142) ----
         float S;
         if (pre) {
-            // k_fs_exp / k_fs_int left the numerators; their tables went to
+            // k_fs_exp left the numerators; its tables went to
             // LDS at the start (ordered by fblock_max's barriers)
             HSAMP_PHASE(12000 + r, 4);
             S = xs_value(exact_index_compose(pv, nW, G, f, st, fs_lanes(a, r)));
@@ -5458,7 +5473,7 @@ hipError_t launch_merge(const StreamArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
-// The RF_FPRE rows: k_fs_max, k_fs_exp, k_fs_int over B x nW waves, then
+// The RF_FPRE rows: k_fs_max, k_fs_exp over B x nW waves, then
 // k_full's PRE instantiations (no penalty table in their LDS): PLAIN for the
 // rows without top-p and min-p (plain), the other for the rows with them (tp).
 hipError_t launch_full_pre(const StreamArgs& a, bool plain, bool tp, hipStream_t stream) {
@@ -5467,7 +5482,6 @@ hipError_t launch_full_pre(const StreamArgs& a, bool plain, bool tp, hipStream_t
     if (a.dtype == 0) hipLaunchKernelGGL((k_fs_max<0>), g, b, 0, stream, a);
     else hipLaunchKernelGGL((k_fs_max<1>), g, b, 0, stream, a);
     hipLaunchKernelGGL(k_fs_exp, g, b, 0, stream, a);
-    hipLaunchKernelGGL(k_fs_int, g, b, 0, stream, a);
     if (plain) hipLaunchKernelGGL((k_full<false, true, true>), dim3(a.rows), dim3(kFT), (uint32_t)kFullLdsBytes, stream, a);
     if (tp) hipLaunchKernelGGL((k_full<false, true, false>), dim3(a.rows), dim3(kFT), (uint32_t)kFullLdsBytes, stream, a);
     return hipGetLastError();

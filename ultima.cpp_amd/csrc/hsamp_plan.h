@@ -38,8 +38,9 @@ enum : uint32_t {
 };
 
 // k_fs_* per-row tables, nW entries each (nW = full_stride / (512 * full_g)):
-// window maxima, NaN seen, approximate window sums of the numerators, the
-// windows' predicted binades / integer increments for the exact sum, their
+// window maxima m_w, NaN seen, approximate window sums of exp(x - m_w) (the
+// binade predictions' input), the windows' predicted binades / integer
+// increments for the exact sum, their
 // numerators' sums in double (two entries' space: FS_SD and the one after),
 // their counts of ids left in (transformed logit above -inf) and their
 // smallest numerator above 0 (float bits; all ones when none). An even number

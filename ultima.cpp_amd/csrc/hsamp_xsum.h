@@ -629,7 +629,7 @@ constexpr Keep kKeepAll{1.0f, 0u};
 // then one wave composes (replaying the windows where the prediction fails or
 // the sum leaves its binade). With lanes (windows of one step), a window whose
 // approximate end lies in a higher binade (or within 0.1% below one) also
-// leaves each lane's pairs at E and E + 1 there, as k_fs_int does, for the
+// leaves each lane's pairs at E and E + 1 there, as k_fs_exp does, for the
 // compose to resolve it by.
 __device__ __forceinline__ XState exact_index_compose(const float* x, int nW, int G, FullLds f, FullShared& st,
                                                       const uint4* lanes = nullptr, Keep keep = kKeepAll);

@@ -12,7 +12,7 @@ kernel, the commands) and, for the workload's dominant kernel (the one that
 reads the logits, or the lm-head matvec), <out>/<kernel>_<tag>_traffic.json,
 which bench.py reads for roofline.traffic. <tag> is cfg1 .. cfg5, head or
 head_<type>, or cli (bench.py --workload cli: the step's kernels k_fs_max,
-k_fs_exp, k_fs_int and k_full taken together as its traffic).
+k_fs_exp and k_full taken together as its traffic).
 
     python3 ultima.cpp_amd/prof_summary.py --config 2 --stats DIR --fetch DIR --write DIR \
         --bench DIR/stats_bench.json --copy-mib 512 --out profiles --command "..."
@@ -96,7 +96,7 @@ def main() -> None:
     main_row = next((t for t in table if t[0].startswith(sk + "<") and t[5] is not None), None)
     if tag == "cli":
         # the step's four kernels, each launched once per step
-        parts = [t for t in table if t[0].split("<")[0] in ("k_fs_max", "k_fs_exp", "k_fs_int", "k_full")]
+        parts = [t for t in table if t[0].split("<")[0] in ("k_fs_max", "k_fs_exp", "k_full")]
         if parts and all(t[5] is not None for t in parts):
             main_row = ("k_fs_* + k_full", min(t[1] for t in parts), sum(t[2] for t in parts),
                         sum(t[3] for t in parts), sum(t[4] for t in parts), sum(t[5] for t in parts))

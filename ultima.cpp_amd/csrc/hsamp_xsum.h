@@ -253,7 +253,8 @@ __device__ __forceinline__ double wave_sum_d(double x) {
 
 // f(i, x[i]) for every i in [0, n) (n a multiple of 4, x 16-byte aligned),
 // over the block: each thread loads four 16-byte groups of four (sixteen
-// values in flight) before using any of them.
+// values in flight) before using any of them. (Loading the next sixteen while
+// f runs measured slower in k_full's top-p passes.)
 template <class F>
 __device__ __forceinline__ void fpass(const float* __restrict__ x, int n, F&& f) {
     const float4* x4 = reinterpret_cast<const float4*>(x);
@@ -514,8 +515,9 @@ __device__ int xs_replay(XState& s, const float (&v)[8], int start, bool thr_on,
 // value (its order is not known, and a half-way value makes it matter; or
 // too many values for the sums), 2 = empty group, 4 = an index-order window
 // with lane tables (each lane's pair at E and at E + 1; it is predicted to
-// leave its binade once).
-constexpr uint32_t kGCare = 1u, kGEmpty = 2u, kGLanes = 4u;
+// leave its binade once), 8 = a top-p bucket whose increments are summed
+// value by value (the compose reads neither 4 nor 8).
+constexpr uint32_t kGCare = 1u, kGEmpty = 2u, kGLanes = 4u, kGInc = 8u;
 __device__ __forceinline__ uint32_t gpack(int E, uint32_t flags) { return (uint32_t)(E + 256) | (flags << 16); }
 
 // Composes groups 0 .. n-1 in order onto s by one wave: whole groups at once
@@ -532,7 +534,7 @@ __device__ int xs_compose(int n, const uint32_t* EF, const uint32_t* D0, const u
         const bool valid = g < n;
         const uint32_t ef = valid ? EF[g] : 0u;
         const int Eg = (int)(ef & 0xFFFFu) - 256;
-        const uint32_t fl = (ef >> 16) & ~kGLanes;
+        const uint32_t fl = (ef >> 16) & ~(kGLanes | kGInc);
         const bool empty = valid && (fl & kGEmpty) != 0u;
         const bool ok = empty || (valid && fl == 0u && Eg == s.E);
         const XPair d = (ok && !empty) ? XPair{D0[g], D1[g]} : XPair{0u, 0u};
@@ -566,7 +568,8 @@ struct FullLds {
     uint32_t* winEF;    // [kFMaxWin]
     uint32_t* gath;     // [kFGather] top-p: keys of the buckets replayed value by value (the window tables' space)
     uint32_t* bcnt;     // [kFNB + 1] bucket counts, then starts
-    uint32_t* bfill;    // [kFNB] (space only: the index-order compose stages windows over bcnt .. gfill)
+    uint32_t* bfill;    // [kFNB] top-p: the binades where a bucket's values fall half-way (bits; see
+                        // full_top_p); the index-order compose stages windows over bcnt .. gfill
     uint32_t* bD;       // [kFNB]
     uint32_t* bEF;      // [kFNB]
     uint32_t* gst;      // [kFNB] start of the bucket's keys in gath, or kNoGath
@@ -1118,19 +1121,40 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
     int counted = 0;
     uint32_t lo = kmn, hi = kmx;
     for (int level = 0; level < 1024; ++level) {
+        // Buckets aligned to multiples of 2^shift in key space: bucket b holds
+        // the keys k with k >> shift = (hi >> shift) - b, so its values share
+        // their exponent (shift < 23) and their mantissa bits from shift up.
         const uint32_t span = hi - lo;
-        const int shift = span >= (uint32_t)kFNB ? (32 - __clz((int)span)) - 12 : 0;
-        const int nb = (int)(span >> shift) + 1;
-        auto bucket_of = [&](uint32_t key) -> int { return (int)((hi - key) >> shift); };
+        int shift = span >= (uint32_t)kFNB ? (32 - __clz((int)span)) - 12 : 0;
+        if ((int)((hi >> shift) - (lo >> shift)) + 1 > kFNB) ++shift;
+        const int nb = (int)((hi >> shift) - (lo >> shift)) + 1;
+        const uint32_t htop = hi >> shift;
+        auto bucket_of = [&](uint32_t key) -> int { return (int)(htop - (key >> shift)); };
         auto in_range = [&](uint32_t key) -> bool { return key != 0u && key >= lo && key <= hi; };
+        // bucket b's lowest key (below lo for the last bucket) and its values' biased exponent
+        auto bkey = [&](int b) -> uint32_t { return (htop - (uint32_t)b) << shift; };
+        auto bexp = [&](int b) -> int { return (int)(bkey(b) >> 23); };
         for (int b = tid; b < nb; b += kFT) {
             f.bcnt[b] = 0u;
             f.bD[b] = 0u;
+            f.bfill[b] = 0u;
         }
         __syncthreads();
+        // The counts; and where a value falls half-way: X * 2^(ex-23) is
+        // half-way between two multiples of binade E's ulp exactly when
+        // E = ex + tz + 1 (tz: X's trailing zeros). Far from the value's own
+        // binade (tz >= 9) that is rare: such binades are noted per bucket
+        // (bit tz - 9; the bucket's values share ex) for the scan below.
         fpass(pv, Vp, [&](int, float e) {
             const uint32_t key = __float_as_uint(e * inv);
-            if (in_range(key)) atomicAdd(&f.bcnt[bucket_of(key)], 1u);
+            if (in_range(key)) {
+                const int b = bucket_of(key);
+                atomicAdd(&f.bcnt[b], 1u);
+                const uint32_t bx = key >> 23;
+                const uint32_t X = (key & 0x7FFFFFu) | (bx != 0u ? 0x800000u : 0u);
+                const int tz = __builtin_ctz(X | 0x1000000u);
+                if (tz >= 9 && tz <= 23) atomicOr(&f.bfill[b], 1u << (tz - 9));
+            }
         });
         __syncthreads();
         if (level == 0) HSAMP_PHASE(13000 + blockIdx.x, 1);
@@ -1145,8 +1169,8 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
                 const int b = 4 * tid + q;
                 c[q] = b < nb ? f.bcnt[b] : 0u;
                 // count times the bucket's middle value
-                const int64_t mid = (int64_t)hi - ((int64_t)b << shift) - (((int64_t)1 << shift) >> 1);
-                mv[q] = __uint_as_float((uint32_t)max(mid, (int64_t)lo));
+                const int64_t mid = (int64_t)bkey(b) + (((int64_t)1 << shift) >> 1);
+                mv[q] = __uint_as_float((uint32_t)min(max(mid, (int64_t)lo), (int64_t)hi));
                 a4[q] = (float)c[q] * mv[q];
                 cs += c[q];
                 as += a4[q];
@@ -1163,9 +1187,32 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
                 gq[q] = false;
                 if (b < nb) {
                     f.bcnt[b] = cpos;
-                    // more than 255 values: the increment sum could wrap
-                    const uint32_t fl = (c[q] == 0u ? kGEmpty : 0u) | (c[q] > 255u ? kGCare : 0u);
                     const int E = xs_binade(apos);
+                    // a value noted half-way at E (or the binade after, where a
+                    // crossing may take the sum)
+                    const int eb = max(bexp(b), 1) - 127;
+                    const uint32_t tm = f.bfill[b];
+                    const int t0 = E - eb - 10;
+                    const bool tie_e = t0 >= 0 && t0 < 32 && ((tm >> t0) & 1u);
+                    const bool tie_at = tie_e || (t0 + 1 >= 0 && t0 + 1 < 32 && ((tm >> (t0 + 1)) & 1u));
+                    // At d = E - eb >= shift + 1 (and >= 10, where any half-way
+                    // value is noted) every value's increment, (X >> d) rounded
+                    // half up, depends on mantissa bits the bucket's values
+                    // share: the bucket's sum is its count times that of its
+                    // lowest key, exactly, unless a value is half-way at E.
+                    // Otherwise (or more than 255 values: a sum of increments
+                    // could wrap) the increments pass sums them value by value.
+                    const int d = E - eb;
+                    const bool uni = c[q] != 0u && d >= max(shift + 1, 10) && !tie_e;
+                    uint32_t fl = c[q] == 0u ? kGEmpty : 0u;
+                    if (uni) {
+                        const uint32_t k0 = bkey(b);
+                        const uint32_t X0 = (k0 & 0x7FFFFFu) | ((k0 >> 23) != 0u ? 0x800000u : 0u);
+                        const uint32_t inc = d >= 26 ? 0u : ((X0 >> (d - 1)) + 1u) >> 1;
+                        f.bD[b] = (uint32_t)min((uint64_t)c[q] * inc, (uint64_t)1 << 25);
+                    } else if (c[q] != 0u) {
+                        fl |= kGInc | (c[q] > 255u ? kGCare : 0u);
+                    }
                     f.bEF[b] = gpack(E, fl);
                     if (c[q] != 0u && c[q] <= (uint32_t)kFSort) {
                         // (the approximate sums are within about 1e-4 of the true ones)
@@ -1173,7 +1220,7 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
                         const bool tie_prone = E - xs_binade(mv[q]) <= 10;
                         const bool cross = xs_binade(lo_e) != xs_binade(hi_e);
                         const bool at_thr = lo_e <= top_p && top_p <= hi_e;
-                        gq[q] = tie_prone || cross || at_thr;
+                        gq[q] = tie_prone || cross || at_thr || tie_at;
                     }
                     gcnt += gq[q] ? (int)c[q] : 0;
                 }
@@ -1206,10 +1253,12 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
             if (in_range(key)) {
                 const int b = bucket_of(key);
                 const uint32_t ef = f.bEF[b];
-                bool t, bg;
-                const uint32_t inc = xincf(p, (int)(ef & 0xFFFFu) - 256, t, bg);
-                if (inc) atomicAdd(&f.bD[b], inc);
-                if ((t || bg) && !((ef >> 16) & kGCare)) atomicOr(&f.bEF[b], kGCare << 16);
+                if ((ef >> 16) & kGInc) {
+                    bool t, bg;
+                    const uint32_t inc = xincf(p, (int)(ef & 0xFFFFu) - 256, t, bg);
+                    if (inc) atomicAdd(&f.bD[b], inc);
+                    if ((t || bg) && !((ef >> 16) & kGCare)) atomicOr(&f.bEF[b], kGCare << 16);
+                }
                 if (f.gst[b] != kNoGath) f.gath[atomicAdd(&f.gfill[b], 1u)] = key;
             }
         });
@@ -1380,9 +1429,9 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
             // refine: the bucket's key range, from the state before it
             const int b = st.fgroup;
             counted += st.fpos;
-            const uint64_t top = (uint64_t)hi - ((uint64_t)b << shift);
-            const uint64_t w = (uint64_t)1 << shift;
-            const uint64_t bot = top + 1u >= w + lo ? top + 1u - w : (uint64_t)lo;
+            const uint64_t k0 = (uint64_t)bkey(b);
+            const uint64_t top = min(k0 + ((uint64_t)1 << shift) - 1u, (uint64_t)hi);
+            const uint64_t bot = max(k0, (uint64_t)lo);
             hi = (uint32_t)top;
             lo = (uint32_t)bot;
             __syncthreads();

@@ -4160,9 +4160,9 @@ __device__ void full_exp(const float* fv, float* pv, float m, int nW, int G, Ful
 //             it leaves in and its sum of exp(x - m_w) (fast exp; a
 //             prediction only);
 //   k_fs_exp: the row's maximum m, the numerators expf(x - m) into fullp,
-//             each window's sum in double (the draw's window prefixes when
-//             top-p and min-p remove nothing) and its smallest numerator
-//             above 0 (top-p's key range), and its binade -- predicted from
+//             each window's sum in double (rows without top-p and min-p: the
+//             draw's window prefixes) or its smallest numerator above 0
+//             (rows with them: top-p's key range), and its binade -- predicted from
 //             the windows before it, sum over v < w of exp(m_v - m) times
 //             k_fs_max's sums -- with its values' integer increments there
 //             (as exact_index_sum forms them; lane tables when the window's
@@ -4185,14 +4185,18 @@ __device__ __forceinline__ uint4* fs_lanes(const StreamArgs& a, int r) {
     return reinterpret_cast<uint4*>(a.fs_tab + base) + (size_t)r * nW * 64;
 }
 
+// k_fs_* blocks: kFsWaves waves, one window each.
+constexpr int kFsWaves = 4;
+
 template <int DT>
-__global__ __launch_bounds__(64) void k_fs_max(StreamArgs a) {
+__global__ __launch_bounds__(64 * kFsWaves) void k_fs_max(StreamArgs a) {
     const int nW = fs_windows(a);
-    const int r = (int)blockIdx.x / nW, w = (int)blockIdx.x - r * nW;
+    const int gw = (int)blockIdx.x * kFsWaves + wave_id();
+    const int r = gw / nW, w = gw - r * nW;
     if (r >= a.rows) return;
     const RowPlan P = plan_of(a, r);
     if (!(P.flags & RF_FPRE)) return;
-    const int lane = (int)threadIdx.x, V = a.vocab, G = a.full_g, WS = kFWin * G;
+    const int lane = lane_id(), V = a.vocab, G = a.full_g, WS = kFWin * G;
     float* fv = a.fullv + (size_t)r * a.full_stride;
     const char* rowp = static_cast<const char*>(a.logits) + (size_t)r * (size_t)a.logits_stride * (DT == 0 ? 4 : 2);
     const uint32_t* mrow = (P.flags & RF_MASK) ? a.mask + (int64_t)r * a.mask_stride : nullptr;
@@ -4275,15 +4279,17 @@ __global__ __launch_bounds__(64) void k_fs_max(StreamArgs a) {
     }
 }
 
-__global__ __launch_bounds__(64) void k_fs_exp(StreamArgs a) {
+__global__ __launch_bounds__(64 * kFsWaves) void k_fs_exp(StreamArgs a) {
     __shared__ uint64_t expT[32];
+    if (threadIdx.x < 32) expT[threadIdx.x] = kExpT[threadIdx.x];
+    __syncthreads();   // (the block's only barrier: the waves go their own ways below)
     const int nW = fs_windows(a);
-    const int r = (int)blockIdx.x / nW, w = (int)blockIdx.x - r * nW;
+    const int gw = (int)blockIdx.x * kFsWaves + wave_id();
+    const int r = gw / nW, w = gw - r * nW;
     if (r >= a.rows) return;
     const RowPlan P = plan_of(a, r);
     if (!(P.flags & RF_FPRE)) return;
-    const int lane = (int)threadIdx.x, G = a.full_g, WS = kFWin * G;
-    if (lane < 32) expT[lane] = kExpT[lane];
+    const int lane = lane_id(), G = a.full_g, WS = kFWin * G;
     const float* fv = a.fullv + (size_t)r * a.full_stride;
     float* pv = a.fullp + (size_t)r * a.full_stride;
     // the window's first step in flight while the row's maximum is found
@@ -4314,12 +4320,14 @@ __global__ __launch_bounds__(64) void k_fs_exp(StreamArgs a) {
     float pre = (pm == -__builtin_inff()) ? 0.0f : ps * __expf(pm - m);
     pre = readlane_f(wave_tree_prefix_f(pre), 63);
     const int E = w == 0 ? -126 : xs_binade(pre);
-    __syncthreads();
     float ws = 0.0f;
     double wd = 0.0;
     uint32_t emn = 0xFFFFFFFFu;
     XPair wp{0u, 0u};
     bool nz = false, lanes_on = false;
+    // rows with top-p or min-p take the smallest numerator (top-p's key
+    // range) and draw from sums of their own; the others the double sums
+    const bool cut = (P.flags & (RF_TOPP | RF_MINP)) != 0;
     for (int g = 0; g < G; ++g) {
         const int i0 = w * WS + g * kFWin + lane * 8;
         if (g > 0) {
@@ -4332,8 +4340,13 @@ __global__ __launch_bounds__(64) void k_fs_exp(StreamArgs a) {
         for (int j = 0; j < 8; ++j) {
             v[j] = (x[j] == -__builtin_inff() || m == -__builtin_inff()) ? 0.0f : libm_expf_t(x[j] - m, expT);
             ws += v[j];
-            wd += (double)v[j];
-            emn = min(emn, v[j] > 0.0f ? __float_as_uint(v[j]) : 0xFFFFFFFFu);
+        }
+        if (cut) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) emn = min(emn, v[j] > 0.0f ? __float_as_uint(v[j]) : 0xFFFFFFFFu);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) wd += (double)v[j];
         }
         float4* dst = reinterpret_cast<float4*>(pv + i0);
         dst[0] = make_float4(v[0], v[1], v[2], v[3]);
@@ -4377,13 +4390,14 @@ __global__ __launch_bounds__(64) void k_fs_exp(StreamArgs a) {
         wp = xcomp(wp, XPair{(uint32_t)__builtin_amdgcn_readlane((int)sp.d0, 63),
                              (uint32_t)__builtin_amdgcn_readlane((int)sp.d1, 63)});
     }
-    wd = wave_tree_prefix_d(wd);
-    emn = wave_min_u32(emn);
-    const bool empty = __ballot(nz) == 0ull;
-    if (lane == 63) {
-        reinterpret_cast<double*>(fs_table(a, r, FS_SD))[w] = wd;
-        fs_table(a, r, FS_EMIN)[w] = emn;
+    if (cut) {
+        emn = wave_min_u32(emn);
+        if (lane == 63) fs_table(a, r, FS_EMIN)[w] = emn;
+    } else {
+        wd = wave_tree_prefix_d(wd);
+        if (lane == 63) reinterpret_cast<double*>(fs_table(a, r, FS_SD))[w] = wd;
     }
+    const bool empty = __ballot(nz) == 0ull;
     if (lane == 0) {
         fs_table(a, r, FS_D0)[w] = wp.d0;
         fs_table(a, r, FS_D1)[w] = wp.d1;
@@ -5005,7 +5019,7 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
             const float inv = 1.0f / S;
             double* wq = reinterpret_cast<double*>(f.winA);   // [kFMaxWin] window sums of p, then prefixes
             uint32_t* wc = f.winEF;                            // [kFMaxWin] kept counts, then prefixes
-            if (pre && !touched) {
+            if (pre && !touched && !(P.flags & (RF_TOPP | RF_MINP))) {
                 // k_fs_* left each window's numerators summed in double and
                 // its count: the window sums of p are taken as fl(1/S) times
                 // those (within 2^-24 of the sums of fl(e fl(1/S)) relative,
@@ -5478,7 +5492,7 @@ hipError_t launch_merge(const StreamArgs& a, hipStream_t stream) {
 // rows without top-p and min-p (plain), the other for the rows with them (tp).
 hipError_t launch_full_pre(const StreamArgs& a, bool plain, bool tp, hipStream_t stream) {
     const int nW = a.full_stride / (kFWin * a.full_g);
-    const dim3 g((unsigned)((int64_t)a.rows * nW)), b(64);
+    const dim3 g((unsigned)(((int64_t)a.rows * nW + kFsWaves - 1) / kFsWaves)), b(64 * kFsWaves);
     if (a.dtype == 0) hipLaunchKernelGGL((k_fs_max<0>), g, b, 0, stream, a);
     else hipLaunchKernelGGL((k_fs_max<1>), g, b, 0, stream, a);
     hipLaunchKernelGGL(k_fs_exp, g, b, 0, stream, a);

@@ -4649,8 +4649,8 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
     Keep keep = kKeepAll;
     bool listed = false;   // a small kept set's draw and outputs are done (ids in f.gath)
     // an id is left in: its transformed logit is above -inf (and the predicate keeps it)
-    auto inset = [&](float e, float x) -> bool {
-        return keep.key != 0u ? keep(e) > 0.0f : x != -__builtin_inff();
+    auto inset = [&](float e, float x, int i) -> bool {
+        return keep.key != 0u ? keep(e, i) > 0.0f : x != -__builtin_inff();
     };
     if (m != -__builtin_inff()) {
         // ---- softmax numerators and their exact index-order sum (sampler.cpp:124-142) ----
@@ -4698,11 +4698,47 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                 if (cut_key == __float_as_uint(inv) && need < neq) mk_same = false;
                 if (!(P.flags & RF_MINP) && ngt + neq <= kFSort) {
                     // few candidates: the list below keeps the lowest `need` ids with p*
-                    keep = Keep{inv, cut_key};
+                    keep = Keep{inv, cut_key, 0x7FFFFFFF};
                     list_need = need;
                     list_key = cut_key;
                 } else if (need >= neq && !(P.flags & RF_MINP)) {
-                    keep = Keep{inv, cut_key};
+                    keep = Keep{inv, cut_key, 0x7FFFFFFF};
+                } else if (!(P.flags & RF_MINP) && mk_same && neq <= kFSort) {
+                    // the cut splits the ids with p* (not the top ones): the
+                    // lowest `need` of them by id stay; their ids, gathered and
+                    // sorted, give the predicate's id limit
+                    uint32_t* ids = f.gath;
+                    if (tid == 0) st.sel_d = 0;
+                    __syncthreads();
+                    wpass(pv, nW, G, [&](int w, int g, const float (&e)[8]) {
+                        int c = 0;
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) c += __float_as_uint(e[j] * inv) == cut_key;
+                        const int incl = wave_incl_sum_i(c);
+                        const int tot = __builtin_amdgcn_readlane(incl, 63);
+                        if (tot == 0) return;
+                        int base = 0;
+                        if (lane == 0) base = atomicAdd(&st.sel_d, tot);
+                        int pos = __builtin_amdgcn_readfirstlane(base) + incl - c;
+                        const int i0 = w * WS + g * kFWin + lane * 8;
+#pragma unroll
+                        for (int j = 0; j < 8; ++j)
+                            if (__float_as_uint(e[j] * inv) == cut_key) {
+                                if (pos < kFSort) ids[pos] = (uint32_t)(i0 + j);
+                                ++pos;
+                            }
+                    });
+                    __syncthreads();
+                    const int ne = min(st.sel_d, kFSort);
+                    if (wid == 0) {
+                        if (ne <= 64) wave_ids_ascending<1>(ids, ne, pv, f.sortb);
+                        else if (ne <= 128) wave_ids_ascending<2>(ids, ne, pv, f.sortb);
+                        else if (ne <= 256) wave_ids_ascending<4>(ids, ne, pv, f.sortb);
+                        else wave_ids_ascending<8>(ids, ne, pv, f.sortb);
+                        if (lane == 0) st.sel_need = (int)ids[min(need, ne) - 1] + 1;
+                    }
+                    __syncthreads();
+                    keep = Keep{inv, cut_key, st.sel_need};
                 } else if (need >= neq) {
                     fpass(pv, Vp, [&](int i, float e) {
                         if (__float_as_uint(e * inv) < cut_key) {
@@ -4776,18 +4812,18 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
             __syncthreads();
             wpass(pv, nW, G, [&](int w, int g, const float (&e)[8]) {
                 int c = 0;
+                const int i0 = w * WS + g * kFWin + lane * 8;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) c += keep(e[j]) > 0.0f;
+                for (int j = 0; j < 8; ++j) c += keep(e[j], i0 + j) > 0.0f;
                 const int incl = wave_incl_sum_i(c);
                 const int tot = __builtin_amdgcn_readlane(incl, 63);
                 if (tot == 0) return;
                 int base = 0;
                 if (lane == 0) base = atomicAdd(&st.sel_d, tot);
                 int pos = __builtin_amdgcn_readfirstlane(base) + incl - c;
-                const int i0 = w * WS + g * kFWin + lane * 8;
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
-                    if (keep(e[j]) > 0.0f) {
+                    if (keep(e[j], i0 + j) > 0.0f) {
                         if (pos < kFSort) ids[pos] = (uint32_t)(i0 + j);
                         ++pos;
                     }
@@ -4941,9 +4977,10 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                 int wn = 0;
                 wpass(pv, nW, G, [&](int w, int g, const float (&u)[8]) {
                     float v[8];
+                    const int i0 = w * WS + g * kFWin + lane * 8;
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
-                        v[j] = keep(u[j]);
+                        v[j] = keep(u[j], i0 + j);
                         if (pre) {
                             wd += (double)v[j];
                             wn += v[j] > 0.0f;
@@ -5051,8 +5088,9 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                 // sums of p from the numerators alone
                 double ws = 0.0;
                 wpass(pv, nW, G, [&](int w, int g, const float (&e)[8]) {
+                    const int i0 = w * WS + g * kFWin + lane * 8;
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) ws += (double)(keep(e[j]) * inv);
+                    for (int j = 0; j < 8; ++j) ws += (double)(keep(e[j], i0 + j) * inv);
                     if (g == G - 1) {
                         ws = wave_sum_d(ws);
                         if (lane == 0) {
@@ -5066,10 +5104,11 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                 double ws = 0.0;
                 int c = 0;
                 wpass2(pv, fv, nW, G, [&](int w, int g, const float (&e)[8], const float (&x)[8]) {
+                    const int i0 = w * WS + g * kFWin + lane * 8;
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
-                        ws += (double)(keep(e[j]) * inv);
-                        c += inset(e[j], x[j]);
+                        ws += (double)(keep(e[j], i0 + j) * inv);
+                        c += inset(e[j], x[j], i0 + j);
                     }
                     if (g == G - 1) {
                         ws = wave_sum_d(ws);
@@ -5147,8 +5186,9 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                             const int i0 = w * WS + lane * 8;
                             const float4 e0 = reinterpret_cast<const float4*>(pv + i0)[0];
                             const float4 e1 = reinterpret_cast<const float4*>(pv + i0)[1];
-                            const float e[8] = {keep(e0.x), keep(e0.y), keep(e0.z), keep(e0.w),
-                                                keep(e1.x), keep(e1.y), keep(e1.z), keep(e1.w)};
+                            const float e[8] = {keep(e0.x, i0), keep(e0.y, i0 + 1), keep(e0.z, i0 + 2),
+                                                keep(e0.w, i0 + 3), keep(e1.x, i0 + 4), keep(e1.y, i0 + 5),
+                                                keep(e1.z, i0 + 6), keep(e1.w, i0 + 7)};
                             double q[8], ls = 0.0;
 #pragma unroll
                             for (int j = 0; j < 8; ++j) {
@@ -5213,7 +5253,7 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                             double q[8], ls = 0.0;
 #pragma unroll
                             for (int j = 0; j < 8; ++j) {
-                                q[j] = (double)(keep(src[j]) * inv) / Sd;
+                                q[j] = (double)(keep(src[j], i0 + j) * inv) / Sd;
                                 ls += q[j];
                             }
                             const double li = wave_tree_prefix_d(ls);
@@ -5257,14 +5297,14 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                 wpass2(pv, fv, nW, G, [&](int w, int g, const float (&e)[8], const float (&x)[8]) {
                     if (g == 0) pos = (int)wc[w];
                     int c = 0;
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) c += inset(e[j], x[j]);
-                    const int li = wave_incl_sum_i(c);
-                    int p = pos + li - c;
                     const int i0 = w * WS + g * kFWin + lane * 8;
 #pragma unroll
+                    for (int j = 0; j < 8; ++j) c += inset(e[j], x[j], i0 + j);
+                    const int li = wave_incl_sum_i(c);
+                    int p = pos + li - c;
+#pragma unroll
                     for (int j = 0; j < 8; ++j) {
-                        if (inset(e[j], x[j])) {
+                        if (inset(e[j], x[j], i0 + j)) {
                             if (p < a.set_cap) {
                                 a.kept_idx[(int64_t)r * a.set_cap + p] = i0 + j;
                                 a.kept_prob[(int64_t)r * a.set_cap + p] = e[j] * inv;
@@ -5291,7 +5331,7 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
             __syncthreads();
             for (int q = tid; q < nkept; q += kFT) row[f.gath[q]] = fv[f.gath[q]];
         } else if (keep.key != 0u) {
-            for (int i = tid; i < V; i += kFT) row[i] = keep(pv[i]) > 0.0f ? fv[i] : -__builtin_inff();
+            for (int i = tid; i < V; i += kFT) row[i] = keep(pv[i], i) > 0.0f ? fv[i] : -__builtin_inff();
         } else {
             for (int i = tid; i < V; i += kFT) row[i] = fv[i];
         }

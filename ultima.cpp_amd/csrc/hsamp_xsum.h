@@ -615,16 +615,19 @@ __device__ __forceinline__ float fblock_excl_scan_f(float v, float* total, FullS
     return base + incl - v;
 }
 
-// A kept-set predicate over numerators e: e stays when the bits of e * inv
-// (its p) are at least key, else it reads as +0 (key 0 keeps every e >= 0).
+// A kept-set predicate over numerators e (id i): e stays when the bits of
+// e * inv (its p) are above key, or equal to it with i below ilim; else it
+// reads as +0 (key 0 keeps every e >= 0).
 struct Keep {
     float inv;
     uint32_t key;
-    __device__ __forceinline__ float operator()(float e) const {
-        return __float_as_uint(e * inv) >= key ? e : 0.0f;
+    int32_t ilim;
+    __device__ __forceinline__ float operator()(float e, int i) const {
+        const uint32_t k = __float_as_uint(e * inv);
+        return (k > key || (k == key && i < ilim)) ? e : 0.0f;
     }
 };
-constexpr Keep kKeepAll{1.0f, 0u};
+constexpr Keep kKeepAll{1.0f, 0u, 0x7FFFFFFF};
 
 // The exact index-order float sum of keep(x[i]) over [0, nW * 512 * G) (values
 // >= 0, the padding +0), given each window's approximate sum in f.winA:
@@ -660,6 +663,7 @@ __device__ __noinline__ XState exact_index_sum(const float* x, int nW, int G, Fu
         wpass(x, nW, G, [&](int w, int g, const float (&u)[8]) {
             const uint32_t ef = f.winEF[w];
             const int E = (int)(ef & 0xFFFFu) - 256;
+            const int i0 = w * kFWin * G + g * kFWin + lane * 8;
             // increments by float arithmetic; plain (saturating) sums while no
             // value is half-way, the parity pairs in order otherwise
             float v[8];
@@ -669,7 +673,7 @@ __device__ __noinline__ XState exact_index_sum(const float* x, int nW, int G, Fu
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 bool t;
-                v[j] = keep(u[j]);
+                v[j] = keep(u[j], i0 + j);
                 e[j] = xinc2f(v[j], E, t);
                 tie |= t;
                 ls += e[j].d0;
@@ -815,8 +819,11 @@ __device__ __forceinline__ XState exact_index_compose(const float* x, int nW, in
                         const float4* src = reinterpret_cast<const float4*>(x + (size_t)w * WS + lane * 8);
                         const float4 q0 = src[0], q1 = src[1];
                         lds_f32* dst = s_val + q * 512 + lane * 8;
-                        dst[0] = keep(q0.x); dst[1] = keep(q0.y); dst[2] = keep(q0.z); dst[3] = keep(q0.w);
-                        dst[4] = keep(q1.x); dst[5] = keep(q1.y); dst[6] = keep(q1.z); dst[7] = keep(q1.w);
+                        const int i0 = w * WS + lane * 8;
+                        dst[0] = keep(q0.x, i0); dst[1] = keep(q0.y, i0 + 1);
+                        dst[2] = keep(q0.z, i0 + 2); dst[3] = keep(q0.w, i0 + 3);
+                        dst[4] = keep(q1.x, i0 + 4); dst[5] = keep(q1.y, i0 + 5);
+                        dst[6] = keep(q1.z, i0 + 6); dst[7] = keep(q1.w, i0 + 7);
                         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
                         if (lane == 0) s_rdy[q] = (uint32_t)w + 1u;
                     }
@@ -853,15 +860,18 @@ __device__ __forceinline__ XState exact_index_compose(const float* x, int nW, in
                 if (by_lanes) t = lanes[(size_t)w * 64 + lane];
                 const float4* src = reinterpret_cast<const float4*>(x + (size_t)w * WS + lane * 8);
                 const float4 q0 = src[0], q1 = src[1];
-                v[0] = keep(q0.x); v[1] = keep(q0.y); v[2] = keep(q0.z); v[3] = keep(q0.w);
-                v[4] = keep(q1.x); v[5] = keep(q1.y); v[6] = keep(q1.z); v[7] = keep(q1.w);
+                const int i0 = w * WS + lane * 8;
+                v[0] = keep(q0.x, i0); v[1] = keep(q0.y, i0 + 1); v[2] = keep(q0.z, i0 + 2); v[3] = keep(q0.w, i0 + 3);
+                v[4] = keep(q1.x, i0 + 4); v[5] = keep(q1.y, i0 + 5); v[6] = keep(q1.z, i0 + 6); v[7] = keep(q1.w, i0 + 7);
             }
             if (G != 1) {
                 for (int g = 0; g < G; ++g) {
                     const float4* src = reinterpret_cast<const float4*>(x + (size_t)w * WS + g * kFWin + lane * 8);
                     const float4 q0 = src[0], q1 = src[1];
-                    const float u[8] = {keep(q0.x), keep(q0.y), keep(q0.z), keep(q0.w),
-                                        keep(q1.x), keep(q1.y), keep(q1.z), keep(q1.w)};
+                    const int i0 = w * WS + g * kFWin + lane * 8;
+                    const float u[8] = {keep(q0.x, i0), keep(q0.y, i0 + 1), keep(q0.z, i0 + 2), keep(q0.w, i0 + 3),
+                                        keep(q1.x, i0 + 4), keep(q1.y, i0 + 5), keep(q1.z, i0 + 6),
+                                        keep(q1.w, i0 + 7)};
                     xs_replay(s, u, 0, false, 0.0f);
                 }
                 return;

@@ -4279,35 +4279,47 @@ __global__ __launch_bounds__(64 * kFsWaves) void k_fs_max(StreamArgs a) {
     }
 }
 
+// k_fs_exp: each wave takes fs_run consecutive windows of a row (one pass
+// over the row's window tables for all of them; a window's binade is
+// predicted from the approximate sum before the wave's first window plus the
+// approximate sums of the windows it has done): four when the batch has
+// windows enough to keep every CU busy with a quarter of them, else one (a
+// few rows: the latency of a wave's windows one after another would show).
+__host__ __device__ __forceinline__ int fs_run(int rows, int nW) {
+    return (int64_t)rows * nW >= 16384 ? 4 : 1;
+}
+
 __global__ __launch_bounds__(64 * kFsWaves) void k_fs_exp(StreamArgs a) {
     __shared__ uint64_t expT[32];
     if (threadIdx.x < 32) expT[threadIdx.x] = kExpT[threadIdx.x];
     __syncthreads();   // (the block's only barrier: the waves go their own ways below)
     const int nW = fs_windows(a);
+    const int run = fs_run(a.rows, nW);
+    const int nq = (nW + run - 1) / run;
     const int gw = (int)blockIdx.x * kFsWaves + wave_id();
-    const int r = gw / nW, w = gw - r * nW;
+    const int r = gw / nq, q = gw - r * nq;
     if (r >= a.rows) return;
     const RowPlan P = plan_of(a, r);
     if (!(P.flags & RF_FPRE)) return;
     const int lane = lane_id(), G = a.full_g, WS = kFWin * G;
+    const int wb = q * run, we = min(wb + run, nW);
     const float* fv = a.fullv + (size_t)r * a.full_stride;
     float* pv = a.fullp + (size_t)r * a.full_stride;
-    // the window's first step in flight while the row's maximum is found
-    float4 c0 = reinterpret_cast<const float4*>(fv + w * WS + lane * 8)[0];
-    float4 c1 = reinterpret_cast<const float4*>(fv + w * WS + lane * 8)[1];
-    // the row's maximum over the window maxima
+    // the first window's first step in flight while the row's maximum is found
+    float4 c0 = reinterpret_cast<const float4*>(fv + wb * WS + lane * 8)[0];
+    float4 c1 = reinterpret_cast<const float4*>(fv + wb * WS + lane * 8)[1];
+    // the row's maximum over the window maxima and, in the same reads, the
+    // approximate sum before the first window from k_fs_max's window sums
+    // relative to their own maxima (each lane's windows before wb rescaled to
+    // its running maximum pm, then to m)
     const uint32_t* wm = fs_table(a, r, FS_MAX);
     const uint32_t* wa = fs_table(a, r, FS_A);
-    // and, in the same reads, the approximate sum before the window from
-    // k_fs_max's window sums relative to their own maxima (each lane's
-    // windows before w rescaled to its running maximum pm, then to m): its
-    // predicted binade
     float m = -__builtin_inff(), pm = -__builtin_inff(), ps = 0.0f;
     for (int k = lane; k < nW; k += 64) {
         const float mv = __uint_as_float(wm[k]);
         const float av = __uint_as_float(wa[k]);
         m = fmaxf(m, mv);
-        if (k < w && mv != -__builtin_inff()) {
+        if (k < wb && mv != -__builtin_inff()) {
             if (mv > pm) {
                 ps = ps * __expf(pm - mv) + av;
                 pm = mv;
@@ -4319,89 +4331,95 @@ __global__ __launch_bounds__(64 * kFsWaves) void k_fs_exp(StreamArgs a) {
     m = wave_max_f(m);
     float pre = (pm == -__builtin_inff()) ? 0.0f : ps * __expf(pm - m);
     pre = readlane_f(wave_tree_prefix_f(pre), 63);
-    const int E = w == 0 ? -126 : xs_binade(pre);
-    float ws = 0.0f;
-    double wd = 0.0;
-    uint32_t emn = 0xFFFFFFFFu;
-    XPair wp{0u, 0u};
-    bool nz = false, lanes_on = false;
     // rows with top-p or min-p take the smallest numerator (top-p's key
     // range) and draw from sums of their own; the others the double sums
     const bool cut = (P.flags & (RF_TOPP | RF_MINP)) != 0;
-    for (int g = 0; g < G; ++g) {
-        const int i0 = w * WS + g * kFWin + lane * 8;
-        if (g > 0) {
-            c0 = reinterpret_cast<const float4*>(fv + i0)[0];
-            c1 = reinterpret_cast<const float4*>(fv + i0)[1];
-        }
-        const float x[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-        float v[8];
+    for (int w = wb; w < we; ++w) {
+        const int E = w == 0 ? -126 : xs_binade(pre);
+        float ws = 0.0f;
+        double wd = 0.0;
+        uint32_t emn = 0xFFFFFFFFu;
+        XPair wp{0u, 0u};
+        bool nz = false, lanes_on = false;
+        for (int g = 0; g < G; ++g) {
+            const int i0 = w * WS + g * kFWin + lane * 8;
+            // the next step's (or window's) values in flight while these are worked on
+            const bool more = g + 1 < G || w + 1 < we;
+            const int in = more ? (g + 1 < G ? i0 + kFWin : (w + 1) * WS + lane * 8) : i0;
+            const float4 n0 = reinterpret_cast<const float4*>(fv + in)[0];
+            const float4 n1 = reinterpret_cast<const float4*>(fv + in)[1];
+            const float x[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+            float v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            v[j] = (x[j] == -__builtin_inff() || m == -__builtin_inff()) ? 0.0f : libm_expf_t(x[j] - m, expT);
-            ws += v[j];
+            for (int j = 0; j < 8; ++j) {
+                v[j] = (x[j] == -__builtin_inff() || m == -__builtin_inff()) ? 0.0f : libm_expf_t(x[j] - m, expT);
+                ws += v[j];
+            }
+            if (cut) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) emn = min(emn, v[j] > 0.0f ? __float_as_uint(v[j]) : 0xFFFFFFFFu);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) wd += (double)v[j];
+            }
+            float4* dst = reinterpret_cast<float4*>(pv + i0);
+            dst[0] = make_float4(v[0], v[1], v[2], v[3]);
+            dst[1] = make_float4(v[4], v[5], v[6], v[7]);
+            // the values' increments at E: plain (saturating) sums while no
+            // value is half-way, the parity pairs in order otherwise
+            XPair e[8];
+            bool tie = false;
+            uint32_t ls = 0u;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                bool t;
+                e[j] = xinc2f(v[j], E, t);
+                tie |= t;
+                ls += e[j].d0;
+                nz |= v[j] != 0.0f;
+            }
+            ls = min(ls, 1u << 25);
+            XPair lp{ls, ls};
+            if (__ballot(tie) != 0ull) {
+                lp = XPair{0u, 0u};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) lp = xcomp(lp, e[j]);
+            }
+            if (G == 1) {
+                // a window whose approximate end lies in a higher binade (or
+                // within 0.1% below one) keeps its lanes' pairs at E and E + 1
+                const float wsum = readlane_f(wave_tree_prefix_f(ws), 63);
+                lanes_on = w > 0 && xs_binade((pre + wsum) * 1.001f) != E;
+                if (lanes_on) {
+                    XPair l1{0u, 0u};
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        bool t;
+                        l1 = xcomp(l1, xinc2f(v[j], E + 1, t));
+                    }
+                    fs_lanes(a, r)[(size_t)w * 64 + lane] = make_uint4(lp.d0, lp.d1, l1.d0, l1.d1);
+                }
+            }
+            const XPair sp = wave_scan_pair_any(lp);
+            wp = xcomp(wp, XPair{(uint32_t)__builtin_amdgcn_readlane((int)sp.d0, 63),
+                                 (uint32_t)__builtin_amdgcn_readlane((int)sp.d1, 63)});
+            c0 = n0;
+            c1 = n1;
         }
         if (cut) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) emn = min(emn, v[j] > 0.0f ? __float_as_uint(v[j]) : 0xFFFFFFFFu);
+            emn = wave_min_u32(emn);
+            if (lane == 63) fs_table(a, r, FS_EMIN)[w] = emn;
         } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) wd += (double)v[j];
+            wd = wave_tree_prefix_d(wd);
+            if (lane == 63) reinterpret_cast<double*>(fs_table(a, r, FS_SD))[w] = wd;
         }
-        float4* dst = reinterpret_cast<float4*>(pv + i0);
-        dst[0] = make_float4(v[0], v[1], v[2], v[3]);
-        dst[1] = make_float4(v[4], v[5], v[6], v[7]);
-        // the values' increments at E: plain (saturating) sums while no value
-        // is half-way, the parity pairs in order otherwise
-        XPair e[8];
-        bool tie = false;
-        uint32_t ls = 0u;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            bool t;
-            e[j] = xinc2f(v[j], E, t);
-            tie |= t;
-            ls += e[j].d0;
-            nz |= v[j] != 0.0f;
+        const bool empty = __ballot(nz) == 0ull;
+        if (lane == 0) {
+            fs_table(a, r, FS_D0)[w] = wp.d0;
+            fs_table(a, r, FS_D1)[w] = wp.d1;
+            fs_table(a, r, FS_EF)[w] = gpack(E, (empty ? kGEmpty : 0u) | (lanes_on ? kGLanes : 0u));
         }
-        ls = min(ls, 1u << 25);
-        XPair lp{ls, ls};
-        if (__ballot(tie) != 0ull) {
-            lp = XPair{0u, 0u};
-#pragma unroll
-            for (int j = 0; j < 8; ++j) lp = xcomp(lp, e[j]);
-        }
-        if (G == 1) {
-            // a window whose approximate end lies in a higher binade (or
-            // within 0.1% below one) keeps its lanes' pairs at E and E + 1
-            const float wsum = readlane_f(wave_tree_prefix_f(ws), 63);
-            lanes_on = w > 0 && xs_binade((pre + wsum) * 1.001f) != E;
-            if (lanes_on) {
-                XPair l1{0u, 0u};
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    bool t;
-                    l1 = xcomp(l1, xinc2f(v[j], E + 1, t));
-                }
-                fs_lanes(a, r)[(size_t)w * 64 + lane] = make_uint4(lp.d0, lp.d1, l1.d0, l1.d1);
-            }
-        }
-        const XPair sp = wave_scan_pair_any(lp);
-        wp = xcomp(wp, XPair{(uint32_t)__builtin_amdgcn_readlane((int)sp.d0, 63),
-                             (uint32_t)__builtin_amdgcn_readlane((int)sp.d1, 63)});
-    }
-    if (cut) {
-        emn = wave_min_u32(emn);
-        if (lane == 63) fs_table(a, r, FS_EMIN)[w] = emn;
-    } else {
-        wd = wave_tree_prefix_d(wd);
-        if (lane == 63) reinterpret_cast<double*>(fs_table(a, r, FS_SD))[w] = wd;
-    }
-    const bool empty = __ballot(nz) == 0ull;
-    if (lane == 0) {
-        fs_table(a, r, FS_D0)[w] = wp.d0;
-        fs_table(a, r, FS_D1)[w] = wp.d1;
-        fs_table(a, r, FS_EF)[w] = gpack(E, (empty ? kGEmpty : 0u) | (lanes_on ? kGLanes : 0u));
+        pre += readlane_f(wave_tree_prefix_f(ws), 63);
     }
 }
 
@@ -5535,7 +5553,9 @@ hipError_t launch_full_pre(const StreamArgs& a, bool plain, bool tp, hipStream_t
     const dim3 g((unsigned)(((int64_t)a.rows * nW + kFsWaves - 1) / kFsWaves)), b(64 * kFsWaves);
     if (a.dtype == 0) hipLaunchKernelGGL((k_fs_max<0>), g, b, 0, stream, a);
     else hipLaunchKernelGGL((k_fs_max<1>), g, b, 0, stream, a);
-    hipLaunchKernelGGL(k_fs_exp, g, b, 0, stream, a);
+    const int run = fs_run(a.rows, nW), nq = (nW + run - 1) / run;
+    const dim3 ge((unsigned)(((int64_t)a.rows * nq + kFsWaves - 1) / kFsWaves));
+    hipLaunchKernelGGL(k_fs_exp, ge, b, 0, stream, a);
     if (plain) hipLaunchKernelGGL((k_full<false, true, true>), dim3(a.rows), dim3(kFT), (uint32_t)kFullLdsBytes, stream, a);
     if (tp) hipLaunchKernelGGL((k_full<false, true, false>), dim3(a.rows), dim3(kFT), (uint32_t)kFullLdsBytes, stream, a);
     return hipGetLastError();

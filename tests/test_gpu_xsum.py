@@ -75,6 +75,10 @@ def _cases():
     t = np.exp(rng.normal(-30, 0.1, 151936)).astype(np.float32)
     t[5] = np.float32(1e-44)
     c["outlier_range"] = t
+    # nearly equal values: the sum crosses many binades inside buckets of one increment
+    c["narrow"] = np.exp(rng.normal(0, 0.01, 151936)).astype(np.float32)
+    # mantissas ending in 12 or more zero bits: the crossing add and half-way values at every binade
+    c["coarse"] = (rng.integers(2**11, 2**12, 151936) * 2.0**-12).astype(np.float32)
     c["long"] = np.exp(rng.normal(0, 0.5, 1_200_000)).astype(np.float32)     # 2-step windows
     c["tiny"] = np.array([3.0, 0.0, 1e-8], np.float32)
     return c

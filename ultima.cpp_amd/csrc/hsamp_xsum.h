@@ -516,8 +516,9 @@ __device__ int xs_replay(XState& s, const float (&v)[8], int start, bool thr_on,
 // too many values for the sums), 2 = empty group, 4 = an index-order window
 // with lane tables (each lane's pair at E and at E + 1; it is predicted to
 // leave its binade once), 8 = a top-p bucket whose increments are summed
-// value by value (the compose reads neither 4 nor 8).
-constexpr uint32_t kGCare = 1u, kGEmpty = 2u, kGLanes = 4u, kGInc = 8u;
+// value by value, 16 = a top-p bucket whose copied keys are sorted in place
+// (the compose reads none of 4, 8 and 16).
+constexpr uint32_t kGCare = 1u, kGEmpty = 2u, kGLanes = 4u, kGInc = 8u, kGSorted = 16u;
 __device__ __forceinline__ uint32_t gpack(int E, uint32_t flags) { return (uint32_t)(E + 256) | (flags << 16); }
 
 // Composes groups 0 .. n-1 in order onto s by one wave: whole groups at once
@@ -534,7 +535,7 @@ __device__ int xs_compose(int n, const uint32_t* EF, const uint32_t* D0, const u
         const bool valid = g < n;
         const uint32_t ef = valid ? EF[g] : 0u;
         const int Eg = (int)(ef & 0xFFFFu) - 256;
-        const uint32_t fl = (ef >> 16) & ~(kGLanes | kGInc);
+        const uint32_t fl = (ef >> 16) & ~(kGLanes | kGInc | kGSorted);
         const bool empty = valid && (fl & kGEmpty) != 0u;
         const bool ok = empty || (valid && fl == 0u && Eg == s.E);
         const XPair d = (ok && !empty) ? XPair{D0[g], D1[g]} : XPair{0u, 0u};
@@ -1086,6 +1087,45 @@ __device__ int chain_replay(XState& s, const uint32_t* keys, int n, float thr) {
     return -1;
 }
 
+// A top-p bucket of n values (keys k0 .. k0 + 2^shift - 1: one exponent, eb;
+// notes: bit t - 9 set when a value's mantissa has t >= 9 trailing zero
+// bits) added onto sv at its binade E, where d = E - eb >= shift + 1 and
+// >= 10 and no value has d - 1 or more trailing zero bits (none half-way at
+// E or E + 1): every value adds the same increment at E, and the add that
+// takes the sum out of E rounds alike for every value (by the parity of M
+// plus the increment and the side of one half the value's fraction lies on,
+// never on it), as do the increments at E + 1 after it. The order within the
+// bucket then does not matter: the sum after it is arithmetic, across at
+// most one crossing. False (sv unchanged) when this does not hold, the sum
+// would leave E + 1 or it reaches thr.
+__device__ __forceinline__ bool xs_uniform_bucket(XState& sv, uint32_t k0, uint32_t n, uint32_t notes, int shift,
+                                                  float thr) {
+    const int E = sv.E, d = E - ((int)max(k0 >> 23, 1u) - 127);
+    if (sv.M == 0u || d < max(shift + 1, 10)) return false;
+    if (d - 10 < 32 && (notes >> (d - 10)) != 0u) return false;
+    const uint32_t X0 = (k0 & 0x7FFFFFu) | ((k0 >> 23) != 0u ? 0x800000u : 0u);
+    const uint64_t inc = d >= 26 ? 0u : ((X0 >> (d - 1)) + 1u) >> 1;
+    const uint64_t thrM = xs_thr(thr, E);
+    const uint64_t end = (uint64_t)sv.M + (uint64_t)n * inc;
+    if (end < (1u << 24)) {
+        if (end >= thrM) return false;
+        sv.M = (uint32_t)end;
+        return true;
+    }
+    // the jc-th value's add leaves E (k0 | 1, which shares the values' bits
+    // from shift up and has a nonzero fraction at E, gives that add's result)
+    const uint64_t jc = ((1u << 24) - (uint64_t)sv.M + inc - 1u) / inc;
+    const uint64_t Mb = (uint64_t)sv.M + (jc - 1u) * inc;
+    if (Mb >= thrM) return false;
+    const XState s1 = xs_add(XState{E, (uint32_t)Mb}, __uint_as_float(k0 | 1u));
+    if (s1.E != E + 1) return false;
+    const uint64_t inc1 = d + 1 >= 26 ? 0u : ((X0 >> d) + 1u) >> 1;
+    const uint64_t end1 = (uint64_t)s1.M + (uint64_t)(n - jc) * inc1;
+    if (end1 >= (1u << 24) || end1 >= xs_thr(thr, E + 1)) return false;
+    sv = XState{E + 1, (uint32_t)end1};
+    return true;
+}
+
 // The row's top-p cutoff (sampler.cpp:146-164) over the probabilities
 // p = e * inv (e = pv, inv = fl(1 / softmax sum)): the cumulative float sum in
 // (p desc, index asc) order, exactly. Keys (float bits of p > 0) in [lo, hi]
@@ -1097,8 +1137,11 @@ __device__ int chain_replay(XState& s, const uint32_t* keys, int n, float thr) {
 // to be replayed value by value -- those early in the order (half-way
 // values are common while the sum is within 2^10 of them) or where the
 // approximate sum changes binade or reaches top_p. One wave composes the
-// buckets; a bucket that must be replayed is sorted in LDS (or taken as it
-// is when all its keys are equal). Buckets flagged by the pass but not
+// buckets; a bucket of one increment that leaves its binade (or was
+// predicted at another) is added by arithmetic (xs_uniform_bucket), one that
+// must be replayed is sorted in registers (or taken as it is when all its
+// keys are equal) -- the copied ones found to hold half-way values sorted
+// beforehand by all the block's waves. Buckets flagged by the pass but not
 // copied are copied by one more pass, any other bucket on demand; one too
 // large to sort is refined (its key range becomes the next [lo, hi]), and a
 // range that runs out continues below it. A bucket replayed value by value
@@ -1317,6 +1360,38 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
             }
             __syncthreads();
         }
+        // The copied buckets with half-way values (replayed value by value
+        // when the compose gets there) sorted in place now, one per wave in
+        // parallel, rather than each by the composing wave in turn.
+        if (shift != 0) {
+            int scnt = 0;
+            bool sq[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int b = 4 * tid + q;
+                const uint32_t n = b < nb ? f.bcnt[b + 1] - f.bcnt[b] : 0u;
+                sq[q] = n > 1u && f.gst[b] != kNoGath && ((f.bEF[b] >> 16) & kGCare) != 0u;
+                scnt += sq[q] ? 1 : 0;
+            }
+            int stot;
+            int spos = fblock_excl_scan(scnt, &stot, st);
+            if (stot > 0) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    if (sq[q] && spos < kFSort) f.sortb[spos] = (uint32_t)(4 * tid + q);
+                    spos += sq[q] ? 1 : 0;
+                }
+                __syncthreads();
+                const int ns = min(stot, kFSort);
+                for (int k = wid; k < ns; k += kFW) {
+                    const int b = (int)f.sortb[k];
+                    uint32_t* keys = f.gath + f.gst[b];
+                    wave_sort_desc_to(keys, (int)(f.bcnt[b + 1] - f.bcnt[b]), keys);
+                    if (lane == 0) f.bEF[b] |= kGSorted << 16;
+                }
+                __syncthreads();
+            }
+        }
         // compose (wave 0) from bucket c0; st.found: 1 = reached, 2 = refine
         // bucket st.fgroup, 3 = copy bucket st.fgroup first
         int c0 = 0;
@@ -1349,6 +1424,9 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
                         }
                         return false;
                     }
+                    if (!((f.bEF[b] >> 16) & (kGInc | kGCare)) &&
+                        xs_uniform_bucket(sv, bkey(b), n, f.bfill[b], shift, top_p))
+                        return false;
                     if (gs == kNoGath) {
                         if (n > (uint32_t)kFSort) {
                             if (lane == 0) {
@@ -1365,8 +1443,11 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
                         return true;
                     }
                     // the bucket's keys sorted (n <= kFSort), then added as floats in that order
-                    wave_sort_desc_to(f.gath + gs, (int)n, f.sortb);
-                    const uint32_t* keys = f.sortb;
+                    const uint32_t* keys = f.gath + gs;
+                    if (!((f.bEF[b] >> 16) & kGSorted)) {
+                        wave_sort_desc_to(f.gath + gs, (int)n, f.sortb);
+                        keys = f.sortb;
+                    }
                     const int pos = chain_replay(sv, keys, (int)n, top_p);
                     if (pos < 0) return false;
                     // the keys above the cut's and equal to it (all in this bucket)

@@ -249,6 +249,29 @@ __device__ __forceinline__ double wave_sum_d(double x) {
     return readlane_d(x, 63);
 }
 
+// LDS-qualified views of pointers into the block's shared memory: functions
+// that receive them as plain pointers would otherwise access them with flat
+// instructions.
+typedef __attribute__((address_space(3))) uint32_t lds_u32;
+typedef __attribute__((address_space(3))) float lds_f32;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) u32x4 lds_u4;
+__device__ __forceinline__ uint32_t lds_add(lds_u32* p, uint32_t v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lds_or(lds_u32* p, uint32_t v) {
+    __hip_atomic_fetch_or(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+// 16 bytes of a row in global memory (16-byte aligned) by a global load: a
+// plain pointer that reaches a function as an argument is read with flat
+// loads, which the LDS waits then wait on too.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const f32x4 gbl_f32x4;
+__device__ __forceinline__ float4 gload4(const float* p) {
+    const f32x4 v = *(const gbl_f32x4*)p;
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 // ---- passes over a row (latency hidden: loads issued ahead of the work) ----
 
 // f(i, x[i]) for every i in [0, n) (n a multiple of 4, x 16-byte aligned),
@@ -257,12 +280,11 @@ __device__ __forceinline__ double wave_sum_d(double x) {
 // f runs measured slower in k_full's top-p passes.)
 template <class F>
 __device__ __forceinline__ void fpass(const float* __restrict__ x, int n, F&& f) {
-    const float4* x4 = reinterpret_cast<const float4*>(x);
     const int n4 = n >> 2;
     for (int b = (int)threadIdx.x; b < n4; b += 4 * kFT) {
         float4 v[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] = x4[min(b + q * kFT, n4 - 1)];   // (clamped: no branch around a load)
+        for (int q = 0; q < 4; ++q) v[q] = gload4(x + 4 * min(b + q * kFT, n4 - 1));   // (clamped: no branch around a load)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int i = b + q * kFT;
@@ -285,8 +307,8 @@ __device__ __forceinline__ void wpass(const float* __restrict__ x, int nW, int G
     const int WS = kFWin * G;
     int w = wave_id(), g = 0;
     if (w >= nW) return;
-    const float4* p0 = reinterpret_cast<const float4*>(x + (size_t)w * WS + lane * 8);
-    float4 c0 = p0[0], c1 = p0[1];
+    const float* p0 = x + (size_t)w * WS + lane * 8;
+    float4 c0 = gload4(p0), c1 = gload4(p0 + 4);
     for (;;) {
         int nw = w, ng = g + 1;
         if (ng == G) {
@@ -294,8 +316,8 @@ __device__ __forceinline__ void wpass(const float* __restrict__ x, int nW, int G
             nw = w + kFW;
         }
         // (past the last window: the last again, unused; no branch around a load)
-        const float4* pn = reinterpret_cast<const float4*>(x + (size_t)min(nw, nW - 1) * WS + ng * kFWin + lane * 8);
-        const float4 n0 = pn[0], n1 = pn[1];
+        const float* pn = x + (size_t)min(nw, nW - 1) * WS + ng * kFWin + lane * 8;
+        const float4 n0 = gload4(pn), n1 = gload4(pn + 4);
         const float v[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
         f(w, g, v);
         if (nw >= nW) break;
@@ -315,8 +337,8 @@ __device__ __forceinline__ void wpass2(const float* __restrict__ x, const float*
     int w = wave_id(), g = 0;
     if (w >= nW) return;
     const size_t o0 = (size_t)w * WS + lane * 8;
-    float4 c0 = reinterpret_cast<const float4*>(x + o0)[0], c1 = reinterpret_cast<const float4*>(x + o0)[1];
-    float4 d0 = reinterpret_cast<const float4*>(z + o0)[0], d1 = reinterpret_cast<const float4*>(z + o0)[1];
+    float4 c0 = gload4(x + o0), c1 = gload4(x + o0 + 4);
+    float4 d0 = gload4(z + o0), d1 = gload4(z + o0 + 4);
     for (;;) {
         int nw = w, ng = g + 1;
         if (ng == G) {
@@ -325,8 +347,8 @@ __device__ __forceinline__ void wpass2(const float* __restrict__ x, const float*
         }
         // (past the last window: the last again, unused; no branch around a load)
         const size_t on = (size_t)min(nw, nW - 1) * WS + ng * kFWin + lane * 8;
-        const float4 n0 = reinterpret_cast<const float4*>(x + on)[0], n1 = reinterpret_cast<const float4*>(x + on)[1];
-        const float4 m0 = reinterpret_cast<const float4*>(z + on)[0], m1 = reinterpret_cast<const float4*>(z + on)[1];
+        const float4 n0 = gload4(x + on), n1 = gload4(x + on + 4);
+        const float4 m0 = gload4(z + on), m1 = gload4(z + on + 4);
         const float v[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
         const float y[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
         f(w, g, v, y);
@@ -526,8 +548,8 @@ __device__ __forceinline__ uint32_t gpack(int E, uint32_t flags) { return (uint3
 // group goes to slow(g, s), which replays it exactly and returns true when
 // the composition has to stop there (threshold reached, or the caller takes
 // over). Starts at group c. Returns the group it stopped at, or -1.
-template <class Slow>
-__device__ int xs_compose(int n, const uint32_t* EF, const uint32_t* D0, const uint32_t* D1, bool thr_on, float thr,
+template <class P, class Slow>
+__device__ int xs_compose(int n, P EF, P D0, P D1, bool thr_on, float thr,
                           XState& s, Slow&& slow, int c = 0) {
     const int lane = lane_id();
     while (c < n) {
@@ -739,13 +761,6 @@ __device__ __forceinline__ XPair wave_seg_scan_pair(XPair x, bool head) {
     return x;
 }
 
-// LDS-qualified views of pointers into the block's shared memory: functions
-// that receive them as plain pointers would otherwise access them with flat
-// instructions.
-typedef __attribute__((address_space(3))) uint32_t lds_u32;
-typedef __attribute__((address_space(3))) float lds_f32;
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) u32x4 lds_u4;
 
 // The same scans for pairs without half-way values (d0 == d1 in every lane):
 // plain sums, at most 64 x 2^25 < 2^32.
@@ -817,8 +832,8 @@ __device__ __forceinline__ XState exact_index_compose(const float* x, int nW, in
                             const uint4 t = lanes[(size_t)w * 64 + lane];
                             s_lt[q * 64 + lane] = u32x4{t.x, t.y, t.z, t.w};
                         }
-                        const float4* src = reinterpret_cast<const float4*>(x + (size_t)w * WS + lane * 8);
-                        const float4 q0 = src[0], q1 = src[1];
+                        const float* src = x + (size_t)w * WS + lane * 8;
+                        const float4 q0 = gload4(src), q1 = gload4(src + 4);
                         lds_f32* dst = s_val + q * 512 + lane * 8;
                         const int i0 = w * WS + lane * 8;
                         dst[0] = keep(q0.x, i0); dst[1] = keep(q0.y, i0 + 1);
@@ -859,16 +874,16 @@ __device__ __forceinline__ XState exact_index_compose(const float* x, int nW, in
                                   s.E == (int)(ef & 0xFFFFu) - 256;
             if (!have && G == 1) {
                 if (by_lanes) t = lanes[(size_t)w * 64 + lane];
-                const float4* src = reinterpret_cast<const float4*>(x + (size_t)w * WS + lane * 8);
-                const float4 q0 = src[0], q1 = src[1];
+                const float* src = x + (size_t)w * WS + lane * 8;
+                const float4 q0 = gload4(src), q1 = gload4(src + 4);
                 const int i0 = w * WS + lane * 8;
                 v[0] = keep(q0.x, i0); v[1] = keep(q0.y, i0 + 1); v[2] = keep(q0.z, i0 + 2); v[3] = keep(q0.w, i0 + 3);
                 v[4] = keep(q1.x, i0 + 4); v[5] = keep(q1.y, i0 + 5); v[6] = keep(q1.z, i0 + 6); v[7] = keep(q1.w, i0 + 7);
             }
             if (G != 1) {
                 for (int g = 0; g < G; ++g) {
-                    const float4* src = reinterpret_cast<const float4*>(x + (size_t)w * WS + g * kFWin + lane * 8);
-                    const float4 q0 = src[0], q1 = src[1];
+                    const float* src = x + (size_t)w * WS + g * kFWin + lane * 8;
+                    const float4 q0 = gload4(src), q1 = gload4(src + 4);
                     const int i0 = w * WS + g * kFWin + lane * 8;
                     const float u[8] = {keep(q0.x, i0), keep(q0.y, i0 + 1), keep(q0.z, i0 + 2), keep(q0.w, i0 + 3),
                                         keep(q1.x, i0 + 4), keep(q1.y, i0 + 5), keep(q1.z, i0 + 6),
@@ -1017,7 +1032,7 @@ __device__ __forceinline__ void bsort_all(uint32_t (&v)[Q]) {
 // src[0, n) sorted descending into dst[0, n) by one wave (n <= 64 Q), in
 // registers (padding 0, below every key).
 template <int Q>
-__device__ __forceinline__ void wave_bitonic_to(const uint32_t* src, int n, uint32_t* dst) {
+__device__ __forceinline__ void wave_bitonic_to(const lds_u32* src, int n, lds_u32* dst) {
     const int lane = lane_id();
     uint32_t v[Q];
 #pragma unroll
@@ -1028,7 +1043,7 @@ __device__ __forceinline__ void wave_bitonic_to(const uint32_t* src, int n, uint
         if (t * 64 + lane < n) dst[t * 64 + lane] = v[t];
     wave_sync();
 }
-__device__ __forceinline__ void wave_sort_desc_to(const uint32_t* src, int n, uint32_t* dst) {
+__device__ __forceinline__ void wave_sort_desc_to(const lds_u32* src, int n, lds_u32* dst) {
     if (n <= 64) wave_bitonic_to<1>(src, n, dst);
     else if (n <= 128) wave_bitonic_to<2>(src, n, dst);
     else if (n <= 256) wave_bitonic_to<4>(src, n, dst);
@@ -1153,6 +1168,16 @@ __device__ __forceinline__ bool xs_uniform_bucket(XState& sv, uint32_t k0, uint3
 __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_p, FullLds f, FullShared& st,
                            uint32_t range_lo, uint32_t range_hi, uint32_t* cut_key, int* cut_count, int* cut_gt,
                            int* cut_eq) {
+    // the bucket tables as LDS pointers (through FullLds, plain pointers, the
+    // compiler would reach them with flat instructions)
+    lds_u32* const bcnt = (lds_u32*)f.bcnt;
+    lds_u32* const bfill = (lds_u32*)f.bfill;
+    lds_u32* const bD = (lds_u32*)f.bD;
+    lds_u32* const bEF = (lds_u32*)f.bEF;
+    lds_u32* const gst = (lds_u32*)f.gst;
+    lds_u32* const gfill = (lds_u32*)f.gfill;
+    lds_u32* const gath = (lds_u32*)f.gath;
+    lds_u32* const sortb = (lds_u32*)f.sortb;
     const int tid = threadIdx.x, lane = lane_id(), wid = wave_id();
     uint32_t kmx = range_hi, kmn = range_lo;
     if (range_hi == 0u) {
@@ -1188,9 +1213,9 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
         auto bkey = [&](int b) -> uint32_t { return (htop - (uint32_t)b) << shift; };
         auto bexp = [&](int b) -> int { return (int)(bkey(b) >> 23); };
         for (int b = tid; b < nb; b += kFT) {
-            f.bcnt[b] = 0u;
-            f.bD[b] = 0u;
-            f.bfill[b] = 0u;
+            bcnt[b] = 0u;
+            bD[b] = 0u;
+            bfill[b] = 0u;
         }
         __syncthreads();
         // The counts; and where a value falls half-way: X * 2^(ex-23) is
@@ -1202,11 +1227,11 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
             const uint32_t key = __float_as_uint(e * inv);
             if (in_range(key)) {
                 const int b = bucket_of(key);
-                atomicAdd(&f.bcnt[b], 1u);
+                lds_add(bcnt + b, 1u);
                 const uint32_t bx = key >> 23;
                 const uint32_t X = (key & 0x7FFFFFu) | (bx != 0u ? 0x800000u : 0u);
                 const int tz = __builtin_ctz(X | 0x1000000u);
-                if (tz >= 9 && tz <= 23) atomicOr(&f.bfill[b], 1u << (tz - 9));
+                if (tz >= 9 && tz <= 23) lds_or(bfill + b, 1u << (tz - 9));
             }
         });
         __syncthreads();
@@ -1220,7 +1245,7 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int b = 4 * tid + q;
-                c[q] = b < nb ? f.bcnt[b] : 0u;
+                c[q] = b < nb ? bcnt[b] : 0u;
                 // count times the bucket's middle value
                 const int64_t mid = (int64_t)bkey(b) + (((int64_t)1 << shift) >> 1);
                 mv[q] = __uint_as_float((uint32_t)min(max(mid, (int64_t)lo), (int64_t)hi));
@@ -1239,12 +1264,12 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
                 const int b = 4 * tid + q;
                 gq[q] = false;
                 if (b < nb) {
-                    f.bcnt[b] = cpos;
+                    bcnt[b] = cpos;
                     const int E = xs_binade(apos);
                     // a value noted half-way at E (or the binade after, where a
                     // crossing may take the sum)
                     const int eb = max(bexp(b), 1) - 127;
-                    const uint32_t tm = f.bfill[b];
+                    const uint32_t tm = bfill[b];
                     const int t0 = E - eb - 10;
                     const bool tie_e = t0 >= 0 && t0 < 32 && ((tm >> t0) & 1u);
                     const bool tie_at = tie_e || (t0 + 1 >= 0 && t0 + 1 < 32 && ((tm >> (t0 + 1)) & 1u));
@@ -1262,11 +1287,11 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
                         const uint32_t k0 = bkey(b);
                         const uint32_t X0 = (k0 & 0x7FFFFFu) | ((k0 >> 23) != 0u ? 0x800000u : 0u);
                         const uint32_t inc = d >= 26 ? 0u : ((X0 >> (d - 1)) + 1u) >> 1;
-                        f.bD[b] = (uint32_t)min((uint64_t)c[q] * inc, (uint64_t)1 << 25);
+                        bD[b] = (uint32_t)min((uint64_t)c[q] * inc, (uint64_t)1 << 25);
                     } else if (c[q] != 0u) {
                         fl |= kGInc | (c[q] > 255u ? kGCare : 0u);
                     }
-                    f.bEF[b] = gpack(E, fl);
+                    bEF[b] = gpack(E, fl);
                     if (c[q] != 0u && c[q] <= (uint32_t)kFSort) {
                         // (the approximate sums are within about 1e-4 of the true ones)
                         const float lo_e = apos * 0.998f, hi_e = (apos + a4[q]) * 1.002f;
@@ -1288,13 +1313,13 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
                 const int b = 4 * tid + q;
                 if (b < nb) {
                     const bool g = gq[q] && gpos + (int)c[q] <= kFGather;
-                    f.gst[b] = g ? (uint32_t)gpos : kNoGath;
-                    f.gfill[b] = (uint32_t)gpos;
+                    gst[b] = g ? (uint32_t)gpos : kNoGath;
+                    gfill[b] = (uint32_t)gpos;
                     gpos += gq[q] ? (int)c[q] : 0;
                 }
             }
             if (tid == 0) {
-                f.bcnt[nb] = (uint32_t)ctot;
+                bcnt[nb] = (uint32_t)ctot;
                 st.sel_d = min(gtot, kFGather);   // the copy area in use (a bound)
             }
         }
@@ -1305,14 +1330,14 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
             const uint32_t key = __float_as_uint(p);
             if (in_range(key)) {
                 const int b = bucket_of(key);
-                const uint32_t ef = f.bEF[b];
+                const uint32_t ef = bEF[b];
                 if ((ef >> 16) & kGInc) {
                     bool t, bg;
                     const uint32_t inc = xincf(p, (int)(ef & 0xFFFFu) - 256, t, bg);
-                    if (inc) atomicAdd(&f.bD[b], inc);
-                    if ((t || bg) && !((ef >> 16) & kGCare)) atomicOr(&f.bEF[b], kGCare << 16);
+                    if (inc) lds_add(bD + b, inc);
+                    if ((t || bg) && !((ef >> 16) & kGCare)) lds_or(bEF + b, kGCare << 16);
                 }
-                if (f.gst[b] != kNoGath) f.gath[atomicAdd(&f.gfill[b], 1u)] = key;
+                if (gst[b] != kNoGath) gath[lds_add(gfill + b, 1u)] = key;
             }
         });
         __syncthreads();
@@ -1324,9 +1349,9 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int b = 4 * tid + q;
-                const uint32_t n = b < nb ? f.bcnt[b + 1] - f.bcnt[b] : 0u;
-                gq[q] = b < nb && f.gst[b] == kNoGath && n != 0u && n <= (uint32_t)kFSort &&
-                        ((f.bEF[b] >> 16) & kGCare) != 0u;
+                const uint32_t n = b < nb ? bcnt[b + 1] - bcnt[b] : 0u;
+                gq[q] = b < nb && gst[b] == kNoGath && n != 0u && n <= (uint32_t)kFSort &&
+                        ((bEF[b] >> 16) & kGCare) != 0u;
                 gcnt += gq[q] ? (int)n : 0;
             }
             int gtot;
@@ -1337,9 +1362,9 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
                 for (int q = 0; q < 4; ++q) {
                     const int b = 4 * tid + q;
                     if (gq[q]) {
-                        f.gst[b] = kNoGath - 1u;   // being copied: marked, then given its place
-                        f.gfill[b] = (uint32_t)gpos;
-                        gpos += (int)(f.bcnt[b + 1] - f.bcnt[b]);
+                        gst[b] = kNoGath - 1u;   // being copied: marked, then given its place
+                        gfill[b] = (uint32_t)gpos;
+                        gpos += (int)(bcnt[b + 1] - bcnt[b]);
                     }
                 }
                 __syncthreads();
@@ -1347,14 +1372,14 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
                     const uint32_t key = __float_as_uint(e * inv);
                     if (in_range(key)) {
                         const int b = bucket_of(key);
-                        if (f.gst[b] == kNoGath - 1u) f.gath[atomicAdd(&f.gfill[b], 1u)] = key;
+                        if (gst[b] == kNoGath - 1u) gath[lds_add(gfill + b, 1u)] = key;
                     }
                 });
                 __syncthreads();
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int b = 4 * tid + q;
-                    if (gq[q]) f.gst[b] = f.gfill[b] - (f.bcnt[b + 1] - f.bcnt[b]);
+                    if (gq[q]) gst[b] = gfill[b] - (bcnt[b + 1] - bcnt[b]);
                 }
                 if (tid == 0) st.sel_d += gtot;
             }
@@ -1369,8 +1394,8 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int b = 4 * tid + q;
-                const uint32_t n = b < nb ? f.bcnt[b + 1] - f.bcnt[b] : 0u;
-                sq[q] = n > 1u && f.gst[b] != kNoGath && ((f.bEF[b] >> 16) & kGCare) != 0u;
+                const uint32_t n = b < nb ? bcnt[b + 1] - bcnt[b] : 0u;
+                sq[q] = n > 1u && gst[b] != kNoGath && ((bEF[b] >> 16) & kGCare) != 0u;
                 scnt += sq[q] ? 1 : 0;
             }
             int stot;
@@ -1378,16 +1403,16 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
             if (stot > 0) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    if (sq[q] && spos < kFSort) f.sortb[spos] = (uint32_t)(4 * tid + q);
+                    if (sq[q] && spos < kFSort) sortb[spos] = (uint32_t)(4 * tid + q);
                     spos += sq[q] ? 1 : 0;
                 }
                 __syncthreads();
                 const int ns = min(stot, kFSort);
                 for (int k = wid; k < ns; k += kFW) {
-                    const int b = (int)f.sortb[k];
-                    uint32_t* keys = f.gath + f.gst[b];
-                    wave_sort_desc_to(keys, (int)(f.bcnt[b + 1] - f.bcnt[b]), keys);
-                    if (lane == 0) f.bEF[b] |= kGSorted << 16;
+                    const int b = (int)sortb[k];
+                    lds_u32* keys = gath + gst[b];
+                    wave_sort_desc_to(keys, (int)(bcnt[b + 1] - bcnt[b]), keys);
+                    if (lane == 0) bEF[b] |= kGSorted << 16;
                 }
                 __syncthreads();
             }
@@ -1398,10 +1423,10 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
         for (;;) {
             if (wid == 0) {
                 if (lane == 0) st.found = 0;
-                const int g = xs_compose(nb, f.bEF, f.bD, f.bD, true, top_p, s, [&](int b, XState& sv) -> bool {
-                    const uint32_t b0 = f.bcnt[b], n = f.bcnt[b + 1] - b0;
+                const int g = xs_compose(nb, bEF, bD, bD, true, top_p, s, [&](int b, XState& sv) -> bool {
+                    const uint32_t b0 = bcnt[b], n = bcnt[b + 1] - b0;
                     if (n == 0u) return false;
-                    const uint32_t gs = f.gst[b];
+                    const uint32_t gs = gst[b];
                     if (shift == 0) {
                         // a bucket of one key: n equal values, in any order
                         const float val = __uint_as_float(hi - (uint32_t)b);
@@ -1424,8 +1449,8 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
                         }
                         return false;
                     }
-                    if (!((f.bEF[b] >> 16) & (kGInc | kGCare)) &&
-                        xs_uniform_bucket(sv, bkey(b), n, f.bfill[b], shift, top_p))
+                    if (!((bEF[b] >> 16) & (kGInc | kGCare)) &&
+                        xs_uniform_bucket(sv, bkey(b), n, bfill[b], shift, top_p))
                         return false;
                     if (gs == kNoGath) {
                         if (n > (uint32_t)kFSort) {
@@ -1443,18 +1468,18 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
                         return true;
                     }
                     // the bucket's keys sorted (n <= kFSort), then added as floats in that order
-                    const uint32_t* keys = f.gath + gs;
-                    if (!((f.bEF[b] >> 16) & kGSorted)) {
-                        wave_sort_desc_to(f.gath + gs, (int)n, f.sortb);
-                        keys = f.sortb;
+                    const lds_u32* keys = gath + gs;
+                    if (!((bEF[b] >> 16) & kGSorted)) {
+                        wave_sort_desc_to(gath + gs, (int)n, sortb);
+                        keys = sortb;
                     }
-                    const int pos = chain_replay(sv, keys, (int)n, top_p);
+                    const int pos = chain_replay(sv, (const uint32_t*)keys, (int)n, top_p);
                     if (pos < 0) return false;
                     // the keys above the cut's and equal to it (all in this bucket)
-                    const uint32_t ck = ((const lds_u32*)keys)[pos];
+                    const uint32_t ck = keys[pos];
                     int ngt = 0, neq = 0;
                     for (uint32_t e = lane; e < n; e += 64) {
-                        const uint32_t y = ((const lds_u32*)keys)[e];
+                        const uint32_t y = keys[e];
                         ngt += y > ck;
                         neq += y == ck;
                     }
@@ -1478,20 +1503,20 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
             if (fd != 3) break;
             // copy bucket st.fgroup (into LDS when it fits, else refine it)
             const int b = st.fgroup;
-            const uint32_t n = f.bcnt[b + 1] - f.bcnt[b];
+            const uint32_t n = bcnt[b + 1] - bcnt[b];
             if (st.sel_d + (int)n <= kFGather) {
                 if (tid == 0) {
-                    f.gst[b] = kNoGath - 1u;
-                    f.gfill[b] = (uint32_t)st.sel_d;
+                    gst[b] = kNoGath - 1u;
+                    gfill[b] = (uint32_t)st.sel_d;
                 }
                 __syncthreads();
                 fpass(pv, Vp, [&](int, float e) {
                     const uint32_t key = __float_as_uint(e * inv);
-                    if (in_range(key) && bucket_of(key) == b) f.gath[atomicAdd(&f.gfill[b], 1u)] = key;
+                    if (in_range(key) && bucket_of(key) == b) gath[lds_add(gfill + b, 1u)] = key;
                 });
                 __syncthreads();
                 if (tid == 0) {
-                    f.gst[b] = (uint32_t)st.sel_d;
+                    gst[b] = (uint32_t)st.sel_d;
                     st.sel_d += (int)n;
                 }
                 __syncthreads();
@@ -1500,7 +1525,7 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
             }
             if (tid == 0) {
                 st.found = 2;
-                st.fpos = (int)f.bcnt[b];
+                st.fpos = (int)bcnt[b];
             }
             __syncthreads();
             break;
@@ -1529,7 +1554,7 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
             continue;
         }
         // the range ran out: continue below it
-        counted += (int)f.bcnt[nb];
+        counted += (int)bcnt[nb];
         __syncthreads();
         if (lo <= kmn) return false;
         hi = lo - 1u;

@@ -46,6 +46,11 @@
 namespace hsamp {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+// LDS-qualified views (see lds_u32): 64-bit keys and doubles, ids, flags
+typedef __attribute__((address_space(3))) u64 lds_u64;
+typedef __attribute__((address_space(3))) double lds_f64;
+typedef __attribute__((address_space(3))) int32_t lds_i32;
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
 constexpr uint32_t kKeyNegInf = 0x007FFFFFu;        // key32(-inf)
 constexpr uint32_t kEmpty = 0xFFFFFFFFu;
@@ -205,7 +210,8 @@ __device__ __forceinline__ u64 shfl_xor_u64(u64 v, int m) {
 // (n <= 16 * 256); the k-th is found by 8-bit radix passes that start below
 // the bits all entries share, and stop as soon as the digit's bucket is
 // exactly what is still needed.
-__device__ __attribute__((noinline)) void buf_compact(u64* buf, int k, Shared& st) {
+__device__ __attribute__((noinline)) void buf_compact(u64* buf_, int k, Shared& st) {
+    lds_u64* buf = (lds_u64*)buf_;   // (always a block's LDS buffer)
     const int n = st.n;
     if (n <= k) return;
     constexpr int MAXE = 16;
@@ -413,8 +419,8 @@ __device__ void drain_overflow(u64* buf, int cap, int k, const u64* ovf, Shared&
 // J / 4), J = 256, 512 between waves through x[0 .. 1024) in LDS with block
 // barriers. Of each pair the lower entry keeps the minimum when the bitonic
 // run of size K containing it ascends (DESC flips every run).
-template <bool DESC, int K, int J>
-__device__ __forceinline__ void rsort_stage(u64 (&v)[4], u64* x) {
+template <bool DESC, int K, int J, class P>
+__device__ __forceinline__ void rsort_stage(u64 (&v)[4], P x) {
     const int t = threadIdx.x;
     if constexpr (J <= 2) {
 #pragma unroll
@@ -450,13 +456,13 @@ __device__ __forceinline__ void rsort_stage(u64 (&v)[4], u64* x) {
         }
     }
 }
-template <bool DESC, int K, int J>
-__device__ __forceinline__ void rsort_steps(u64 (&v)[4], u64* x) {
+template <bool DESC, int K, int J, class P>
+__device__ __forceinline__ void rsort_steps(u64 (&v)[4], P x) {
     rsort_stage<DESC, K, J>(v, x);
     if constexpr (J > 1) rsort_steps<DESC, K, J / 2>(v, x);
 }
-template <bool DESC, int K = 2>
-__device__ __forceinline__ void rsort1024(u64 (&v)[4], u64* x) {
+template <bool DESC, int K = 2, class P>
+__device__ __forceinline__ void rsort1024(u64 (&v)[4], P x) {
     rsort_steps<DESC, K, K / 2>(v, x);
     if constexpr (K < 1024) rsort1024<DESC, 2 * K>(v, x);
 }
@@ -669,6 +675,22 @@ struct FinLds {
     uint8_t* keep;  // still kept
 };
 
+// FinLds's arrays (and the candidate buffers, all in LDS) as LDS pointers:
+// the noinline functions that receive them as plain pointers would otherwise
+// reach them with flat instructions.
+struct FinView {
+    lds_u64* sortk;
+    lds_i32* fidx;
+    lds_f32* fv;
+    lds_f32* fe;
+    lds_f32* fp;
+    lds_u8* keep;
+};
+__device__ __forceinline__ FinView fin_view(const FinLds& f) {
+    return FinView{(lds_u64*)f.sortk, (lds_i32*)f.fidx, (lds_f32*)f.fv,
+                   (lds_f32*)f.fe,    (lds_f32*)f.fp,   (lds_u8*)f.keep};
+}
+
 // Exclusive block scan of one double per thread (tree association: only for
 // decisions taken with a margin); *total gets the block sum.
 __device__ __forceinline__ double block_excl_scan_d(double v, double* total, Shared& st) {
@@ -737,7 +759,8 @@ __device__ int wave_seq_sum_f(int n, Val v, bool thr_on, float thr, float* sum) 
 // softmax_probs over the kept entries (sampler.cpp:124-142): m, e, float
 // index-order sum (exact, on wave 0), p = e * fl(1/sum). Returns false when
 // nothing is kept.
-__device__ __attribute__((noinline)) bool fin_softmax(FinLds f, int nk, Shared& st) {
+__device__ __attribute__((noinline)) bool fin_softmax(FinLds f_, int nk, Shared& st) {
+    const FinView f = fin_view(f_);
     const int tid = threadIdx.x;
     float m = -__builtin_inff();
     for (int j = tid; j < nk; j += kBlock)
@@ -782,8 +805,10 @@ __device__ __attribute__((noinline)) int32_t uniform_draw(int V, double u) {
 
 // The ladder after top-k for one row whose top-k set is buf[0..nk).
 __device__ __attribute__((noinline)) void finalize_row(const StreamArgs& a, const RowPlan& P, int r,
-                                                       const u64* buf, int nk, FinLds f, Shared& st,
+                                                       const u64* buf_, int nk, FinLds f_, Shared& st,
                                                        uint32_t rflags) {
+    const FinView f = fin_view(f_);
+    const lds_u64* buf = (const lds_u64*)buf_;
     const int tid = threadIdx.x;
     const int V = a.vocab;
     const double u = st.u;
@@ -822,7 +847,7 @@ __device__ __attribute__((noinline)) void finalize_row(const StreamArgs& a, cons
         }
         if (a.topk_count != nullptr && tid == 0) a.topk_count[r] = single ? -1 : nk;
 
-        bool have = fin_softmax(f, nk, st);
+        bool have = fin_softmax(f_, nk, st);
         HSAMP_PHASE(9500 + r, 7);
         bool fresh = true;  // fp matches the current kept set
         if (have && (P.flags & RF_TOPP)) {
@@ -875,7 +900,7 @@ __device__ __attribute__((noinline)) void finalize_row(const StreamArgs& a, cons
         HSAMP_PHASE(9500 + r, 8);
         if (have && (P.flags & RF_MINP)) {
             // sampler.cpp:167-176
-            if (!fresh) have = fin_softmax(f, nk, st);
+            if (!fresh) have = fin_softmax(f_, nk, st);
             fresh = true;
             if (have) {
                 float mp = 0.0f;
@@ -894,7 +919,7 @@ __device__ __attribute__((noinline)) void finalize_row(const StreamArgs& a, cons
                 if (any) fresh = false;
             }
         }
-        if (have && !fresh) have = fin_softmax(f, nk, st);
+        if (have && !fresh) have = fin_softmax(f_, nk, st);
         HSAMP_PHASE(9500 + r, 9);
         if (have) {
             // sampler.cpp:178-182 / discrete_distribution: double sum S, q = p / S,
@@ -958,7 +983,7 @@ __device__ __attribute__((noinline)) void finalize_row(const StreamArgs& a, cons
                 }
             }
             if (!decided) {
-                double* fq = reinterpret_cast<double*>(f.sortk);
+                lds_f64* fq = (lds_f64*)f.sortk;
                 if (tid == 0) {
                     double S = 0.0;
                     for (int j = 0; j < nk; ++j)

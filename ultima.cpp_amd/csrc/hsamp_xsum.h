@@ -538,9 +538,10 @@ __device__ int xs_replay(XState& s, const float (&v)[8], int start, bool thr_on,
 // too many values for the sums), 2 = empty group, 4 = an index-order window
 // with lane tables (each lane's pair at E and at E + 1; it is predicted to
 // leave its binade once), 8 = a top-p bucket whose increments are summed
-// value by value, 16 = a top-p bucket whose copied keys are sorted in place
-// (the compose reads none of 4, 8 and 16).
-constexpr uint32_t kGCare = 1u, kGEmpty = 2u, kGLanes = 4u, kGInc = 8u, kGSorted = 16u;
+// value by value, 16 = a top-p bucket whose copied keys are sorted in place,
+// 32 = a top-p bucket whose keys the increments pass copies (the compose
+// reads none of 4, 8, 16 and 32).
+constexpr uint32_t kGCare = 1u, kGEmpty = 2u, kGLanes = 4u, kGInc = 8u, kGSorted = 16u, kGGath = 32u;
 __device__ __forceinline__ uint32_t gpack(int E, uint32_t flags) { return (uint32_t)(E + 256) | (flags << 16); }
 
 // Composes groups 0 .. n-1 in order onto s by one wave: whole groups at once
@@ -557,7 +558,7 @@ __device__ int xs_compose(int n, P EF, P D0, P D1, bool thr_on, float thr,
         const bool valid = g < n;
         const uint32_t ef = valid ? EF[g] : 0u;
         const int Eg = (int)(ef & 0xFFFFu) - 256;
-        const uint32_t fl = (ef >> 16) & ~(kGLanes | kGInc | kGSorted);
+        const uint32_t fl = (ef >> 16) & ~(kGLanes | kGInc | kGSorted | kGGath);
         const bool empty = valid && (fl & kGEmpty) != 0u;
         const bool ok = empty || (valid && fl == 0u && Eg == s.E);
         const XPair d = (ok && !empty) ? XPair{D0[g], D1[g]} : XPair{0u, 0u};
@@ -1314,6 +1315,7 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
                 if (b < nb) {
                     const bool g = gq[q] && gpos + (int)c[q] <= kFGather;
                     gst[b] = g ? (uint32_t)gpos : kNoGath;
+                    if (g) bEF[b] = bEF[b] | (kGGath << 16);   // (this thread's entry)
                     gfill[b] = (uint32_t)gpos;
                     gpos += gq[q] ? (int)c[q] : 0;
                 }
@@ -1337,7 +1339,7 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
                     if (inc) lds_add(bD + b, inc);
                     if ((t || bg) && !((ef >> 16) & kGCare)) lds_or(bEF + b, kGCare << 16);
                 }
-                if (gst[b] != kNoGath) gath[lds_add(gfill + b, 1u)] = key;
+                if ((ef >> 16) & kGGath) gath[lds_add(gfill + b, 1u)] = key;
             }
         });
         __syncthreads();

@@ -1229,10 +1229,12 @@ __device__ bool full_top_p(const float* pv, int V, int Vp, float inv, float top_
             if (in_range(key)) {
                 const int b = bucket_of(key);
                 lds_add(bcnt + b, 1u);
-                const uint32_t bx = key >> 23;
-                const uint32_t X = (key & 0x7FFFFFu) | (bx != 0u ? 0x800000u : 0u);
-                const int tz = __builtin_ctz(X | 0x1000000u);
-                if (tz >= 9 && tz <= 23) lds_or(bfill + b, 1u << (tz - 9));
+                if ((key & 0x1FFu) == 0u) {   // (X's low nine bits are the key's)
+                    const uint32_t bx = key >> 23;
+                    const uint32_t X = (key & 0x7FFFFFu) | (bx != 0u ? 0x800000u : 0u);
+                    const int tz = __builtin_ctz(X | 0x1000000u);
+                    if (tz <= 23) lds_or(bfill + b, 1u << (tz - 9));
+                }
             }
         });
         __syncthreads();

@@ -4392,15 +4392,13 @@ __global__ __launch_bounds__(64 * kFsWaves) void k_fs_exp(StreamArgs a) {
             dst[1] = make_float4(v[4], v[5], v[6], v[7]);
             // the values' increments at E: plain (saturating) sums while no
             // value is half-way, the parity pairs in order otherwise
-            XPair e[8];
             bool tie = false;
             uint32_t ls = 0u;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 bool t;
-                e[j] = xinc2f(v[j], E, t);
+                ls += xinc1f(v[j], E, t);
                 tie |= t;
-                ls += e[j].d0;
                 nz |= v[j] != 0.0f;
             }
             ls = min(ls, 1u << 25);
@@ -4408,7 +4406,10 @@ __global__ __launch_bounds__(64 * kFsWaves) void k_fs_exp(StreamArgs a) {
             if (__ballot(tie) != 0ull) {
                 lp = XPair{0u, 0u};
 #pragma unroll
-                for (int j = 0; j < 8; ++j) lp = xcomp(lp, e[j]);
+                for (int j = 0; j < 8; ++j) {
+                    bool t;
+                    lp = xcomp(lp, xinc2f(v[j], E, t));
+                }
             }
             if (G == 1) {
                 // a window whose approximate end lies in a higher binade (or

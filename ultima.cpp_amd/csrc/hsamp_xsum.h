@@ -400,6 +400,16 @@ __device__ __forceinline__ XPair xinc2f(float x, int E, bool& tie) {
     return (tie && K < (1u << 25)) ? XPair{lo, hi} : XPair{min(i, 1u << 25), min(i, 1u << 25)};
 }
 
+// xinc2f's increment when x is not half-way (both halves of its pair), and
+// whether x is: the common case, without the pair's parity arithmetic.
+__device__ __forceinline__ uint32_t xinc1f(float x, int E, bool& tie) {
+    const float t = ldexpf(x, 23 - E);
+    const float fl = floorf(t);
+    const float fr = t - fl;
+    tie = fr == 0.5f;
+    return t < 16777216.0f ? (uint32_t)fl + (fr > 0.5f ? 1u : 0u) : (1u << 25);
+}
+
 // a, then b
 __device__ __forceinline__ XPair xcomp(XPair a, XPair b) {
     return XPair{sat_add(a.d0, (a.d0 & 1u) ? b.d1 : b.d0), sat_add(a.d1, (a.d1 & 1u) ? b.d0 : b.d1)};
@@ -691,16 +701,14 @@ __device__ __noinline__ XState exact_index_sum(const float* x, int nW, int G, Fu
             // increments by float arithmetic; plain (saturating) sums while no
             // value is half-way, the parity pairs in order otherwise
             float v[8];
-            XPair e[8];
             bool tie = false;
             uint32_t ls = 0u;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 bool t;
                 v[j] = keep(u[j], i0 + j);
-                e[j] = xinc2f(v[j], E, t);
+                ls += xinc1f(v[j], E, t);
                 tie |= t;
-                ls += e[j].d0;
                 nz |= v[j] != 0.0f;
             }
             ls = min(ls, 1u << 25);
@@ -708,7 +716,10 @@ __device__ __noinline__ XState exact_index_sum(const float* x, int nW, int G, Fu
             if (__ballot(tie) != 0ull) {
                 lp = XPair{0u, 0u};
 #pragma unroll
-                for (int j = 0; j < 8; ++j) lp = xcomp(lp, e[j]);
+                for (int j = 0; j < 8; ++j) {
+                    bool t;
+                    lp = xcomp(lp, xinc2f(v[j], E, t));
+                }
             }
             const bool lon = ((ef >> 16) & kGLanes) != 0u;
             if (lon) {

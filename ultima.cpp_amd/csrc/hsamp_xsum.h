@@ -1086,25 +1086,28 @@ __device__ int chain_replay(XState& s, const uint32_t* keys, int n, float thr) {
             start = lane == l ? acc : start;
             acc = readlane_f(b, l);
         }
-        // the first value whose sum reaches thr: each lane's adds again from its start
-        float c = start, cat = 0.0f;
-        int first = 8;
+        // the first value whose sum reaches thr (the sums only grow: none
+        // when the last does not): each lane's adds again from its start
+        if (acc >= thr) {
+            float c = start, cat = 0.0f;
+            int first = 8;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            c = c + v[j];
-            if (first == 8 && lane < nl && c >= thr) {
-                first = j;
-                cat = c;
+            for (int j = 0; j < 8; ++j) {
+                c = c + v[j];
+                if (first == 8 && lane < nl && c >= thr) {
+                    first = j;
+                    cat = c;
+                }
             }
-        }
-        const u64 hm = __ballot(first < 8);
-        if (hm != 0ull) {
-            const int L = __ffsll((long long)hm) - 1;
-            int ex;
-            uint32_t X;
-            fparts(readlane_f(cat, L), ex, X);
-            s = XState{ex, X};
-            return o + L * 8 + __builtin_amdgcn_readlane(first, L);
+            const u64 hm = __ballot(first < 8);
+            if (hm != 0ull) {
+                const int L = __ffsll((long long)hm) - 1;
+                int ex;
+                uint32_t X;
+                fparts(readlane_f(cat, L), ex, X);
+                s = XState{ex, X};
+                return o + L * 8 + __builtin_amdgcn_readlane(first, L);
+            }
         }
         int ex;
         uint32_t X;

@@ -58,9 +58,10 @@ __global__ void k_xinc(const float* x, int n, int E, uint32_t* out) {
     const XPair b = xinc2f(x[i], E, t);
     // xincf's increment, tie and big flags against xinc's (a mismatch shows as
     // an impossible pair)
-    bool t1, g1, t2, g2;
-    const uint32_t i1 = xinc(x[i], E, t1, g1), i2 = xincf(x[i], E, t2, g2);
-    if (i1 != i2 || t1 != t2 || g1 != g2) {
+    // and xinc1f's: the pair's common increment away from one half, the same tie flag
+    bool t1, g1, t2, g2, t3;
+    const uint32_t i1 = xinc(x[i], E, t1, g1), i2 = xincf(x[i], E, t2, g2), i3 = xinc1f(x[i], E, t3);
+    if (i1 != i2 || t1 != t2 || g1 != g2 || t3 != t || (!t && (i3 != b.d0 || b.d0 != b.d1))) {
         out[4 * i] = 0xFFFFFFFFu;
         out[4 * i + 1] = 0u;
         out[4 * i + 2] = 0u;

@@ -120,7 +120,8 @@ def test_top_p_cutoff(pkg, name, frac, known_range):
 
 @pytest.mark.parametrize("E", [-126, -40, -17, -1, 0, 9, 16, 30])
 def test_float_increments_match_integer_ones(pkg, E):
-    """The increments k_fs_exp takes by float arithmetic (ldexp, floor) are the
+    """The increments k_fs_exp takes by float arithmetic (ldexp, floor; and
+    the plain increment away from one half, by rounding to nearest) are the
     integer ones (xinc2) for every kind of value at binade E: far below the
     sum's ulp, exactly half-way between two multiples of it at every scale,
     just beside half-way, within the binade, at and past its top, zeros and

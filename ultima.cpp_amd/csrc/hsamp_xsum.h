@@ -404,10 +404,9 @@ __device__ __forceinline__ XPair xinc2f(float x, int E, bool& tie) {
 // whether x is: the common case, without the pair's parity arithmetic.
 __device__ __forceinline__ uint32_t xinc1f(float x, int E, bool& tie) {
     const float t = ldexpf(x, 23 - E);
-    const float fl = floorf(t);
-    const float fr = t - fl;
-    tie = fr == 0.5f;
-    return t < 16777216.0f ? (uint32_t)fl + (fr > 0.5f ? 1u : 0u) : (1u << 25);
+    const float r = rintf(t);   // (t - r is exact; away from one half, round half up is this)
+    tie = fabsf(t - r) == 0.5f;
+    return t < 16777216.0f ? (uint32_t)r : (1u << 25);
 }
 
 // a, then b

@@ -4377,7 +4377,8 @@ __global__ __launch_bounds__(64 * kFsWaves) void k_fs_exp(StreamArgs a) {
             float v[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                v[j] = (x[j] == -__builtin_inff() || m == -__builtin_inff()) ? 0.0f : libm_expf_t(x[j] - m, expT);
+                // (x = -inf: libm_expf_t(-inf) is +0; m = -inf, the whole row, decided once)
+                v[j] = m == -__builtin_inff() ? 0.0f : libm_expf_t(x[j] - m, expT);
                 ws += v[j];
             }
             if (cut) {

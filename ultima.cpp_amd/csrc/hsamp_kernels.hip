@@ -5031,17 +5031,20 @@ __global__ __launch_bounds__(kFT) void k_full(StreamArgs a) {
                             wn += v[j] > 0.0f;
                         }
                     }
-                    ws += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+                    if (!pre) ws += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
                     if (g == G - 1) {
-                        ws = wave_tree_prefix_f(ws);
-                        if (lane == 63) f.winA[w] = ws;
                         if (pre) {
+                            // (the double sum, rounded, is the window's approximate sum)
                             wd = wave_tree_prefix_d(wd);
                             wn = wave_incl_sum_i(wn);
                             if (lane == 63) {
                                 reinterpret_cast<double*>(fs_table(a, r, FS_SD))[w] = wd;
                                 fs_table(a, r, FS_CNT)[w] = (uint32_t)wn;
+                                f.winA[w] = (float)wd;
                             }
+                        } else {
+                            ws = wave_tree_prefix_f(ws);
+                            if (lane == 63) f.winA[w] = ws;
                         }
                         ws = 0.0f;
                         wd = 0.0;
